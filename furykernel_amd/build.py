@@ -1,0 +1,72 @@
+"""Builds the native parts of the target in-tree.
+
+* ``libfkrocm.so`` — the C ABI of ``include/fkrocm.h`` over HIP (host code).
+* ``fk_kernels.hsaco`` — the hand-written gfx950 kernels, one code object,
+  which ``fk_module_load_file`` loads.
+
+Kernels are compiled Strict, as ``CompileOptions`` asks of a target
+(src/FuryKernel/Backend.hs:52-73): ``-ffp-contract=off`` and no fast-math, so
+nothing contracts a multiply and an add, nothing reassociates.  Packed FP32
+instructions are disabled (``-packed-fp32-ops``).
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+CSRC = PACKAGE / "csrc"
+ROOT = PACKAGE.parent
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+RUNTIME_SO = PACKAGE / "libfkrocm.so"
+KERNELS_CO = PACKAGE / "fk_kernels.hsaco"
+
+KERNEL_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}")
+
+
+def build_runtime() -> Path:
+    src = CSRC / "fk_runtime.cpp"
+    tmp = RUNTIME_SO.with_suffix(".so.tmp")
+    _run([HIPCC, "-shared", "-fPIC", "-O2", "-std=c++17", "-Wno-unused-value", "-Wno-unused-result",
+          f"-I{ROOT / 'include'}", str(src), "-o", str(tmp)])
+    os.replace(tmp, RUNTIME_SO)
+    return RUNTIME_SO
+
+
+def build_kernels() -> Path:
+    src = CSRC / "kernels" / "fk_kernels.hip"
+    tmp = KERNELS_CO.with_suffix(".hsaco.tmp")
+    _run([HIPCC, "--genco", *KERNEL_FLAGS, str(src), "-o", str(tmp)])
+    os.replace(tmp, KERNELS_CO)
+    return KERNELS_CO
+
+
+def build_all() -> list[Path]:
+    return [build_runtime(), build_kernels()]
+
+
+if __name__ == "__main__":
+    for p in build_all():
+        print(p)

@@ -1,0 +1,144 @@
+// fk_gemv.h — matrix-vector products in the reference GEMV's order
+// (test/Test/FuryKernel/Gemv.hs:5-27,131-191), as wave64 kernels.
+//
+// y = W x for one row x: W is [n, k] row-major (the `out_in` layout,
+// src/FuryKernel/Program/Build.hs:170-176).  A wavefront takes R whole rows:
+// lane l visits packs l, l + 64, ... of P consecutive elements (one 16-byte
+// load of W per pack), the pack's elements four to a chain
+// ((x0 w0 + x1 w1) + (x2 w2 + x3 w3)), each chain its own sum; then the
+// lane's chains in order and the pairwise wavefront sum.
+//
+// That is the reference order at SIMD width 64, split 1.  It is also, bit for
+// bit, the CPU target's order at width 32, split 2 (src/FuryKernel/Cpu.hs:73):
+// there lane v = 32 q + l of split q visits the same packs v, v + 64, ..., each
+// split's 32 lanes sum pairwise, and the combine adds split 0's partial to
+// split 1's (src/FuryKernel/Reduce.hs:112-125) — the last step of the width-64
+// pairwise tree.
+#pragma once
+
+#include "fk_common.h"
+
+namespace fk {
+
+// A pack of P elements of W or x, widened to f32 exactly.
+template <int P>
+__device__ __forceinline__ void load_pack(const float *__restrict__ p, float (&out)[P]) {
+  static_assert(P % 4 == 0, "f32 packs are float4s");
+#pragma unroll
+  for (int i = 0; i < P / 4; i++) {
+    float4 v = *reinterpret_cast<const float4 *>(p + 4 * i);
+    out[4 * i] = v.x;
+    out[4 * i + 1] = v.y;
+    out[4 * i + 2] = v.z;
+    out[4 * i + 3] = v.w;
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void load_pack(const _Float16 *__restrict__ p, float (&out)[P]) {
+  static_assert(P % 8 == 0, "f16 packs are 16-byte loads");
+#pragma unroll
+  for (int i = 0; i < P / 8; i++) {
+    uint4 v = *reinterpret_cast<const uint4 *>(p + 8 * i);
+    uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      out[8 * i + 2 * h] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] & 0xFFFFu));
+      out[8 * i + 2 * h + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] >> 16));
+    }
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void load_pack(const int8_t *__restrict__ p, float (&out)[P]) {
+  static_assert(P % 16 == 0, "i8 packs are 16-byte loads");
+#pragma unroll
+  for (int i = 0; i < P / 16; i++) {
+    uint4 v = *reinterpret_cast<const uint4 *>(p + 16 * i);
+    uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int b = 0; b < 16; b++) out[16 * i + b] = (float)(int8_t)(words[b / 4] >> (8 * (b % 4)));
+  }
+}
+
+// R rows of y = W x (times a per-row scale if given) by one wavefront.
+template <typename WT, typename XT, int P, int R>
+__device__ __forceinline__ void gemv_wave(const WT *__restrict__ w, const XT *__restrict__ x, const float *__restrict__ scale,
+                                         float *__restrict__ y, uint32_t n, uint32_t k, uint32_t row0) {
+  constexpr int C = P / 4;
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+  const uint32_t packs = k / P;
+  float acc[R][C];
+#pragma unroll
+  for (int q = 0; q < R; q++)
+#pragma unroll
+    for (int c = 0; c < C; c++) acc[q][c] = 0.0f;
+  // Rows past n read row n - 1 and store nothing: every lane takes part in
+  // the wavefront sums.
+  const WT *wr[R];
+#pragma unroll
+  for (int q = 0; q < R; q++) wr[q] = w + (size_t)min(row0 + q, n - 1) * k;
+#pragma unroll 4
+  for (uint32_t j = lane; j < packs; j += FK_WAVE) {
+    float xv[P];
+    load_pack<P>(x + (size_t)j * P, xv);
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      float wv[P];
+      load_pack<P>(wr[q] + (size_t)j * P, wv);
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        float p0 = xv[4 * c] * wv[4 * c];
+        float p1 = xv[4 * c + 1] * wv[4 * c + 1];
+        float p2 = xv[4 * c + 2] * wv[4 * c + 2];
+        float p3 = xv[4 * c + 3] * wv[4 * c + 3];
+        acc[q][c] = acc[q][c] + ((p0 + p1) + (p2 + p3));
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < R; q++) {
+    float t = acc[q][0];
+#pragma unroll
+    for (int c = 1; c < C; c++) t = t + acc[q][c];
+    t = wave_sum(t);
+    const uint32_t row = row0 + q;
+    if (lane == 0 && row < n) y[row] = scale ? t * scale[row] : t;
+  }
+}
+
+}  // namespace fk
+
+// Entry points: a threadgroup of W wavefronts takes W * R consecutive rows.
+// Kernargs: the buffers in binding order, then the parameter struct.
+struct fk_gemv_params {
+  uint32_t n;  // rows of W (outputs)
+  uint32_t k;  // columns of W (inputs), a multiple of the pack
+};
+
+#define FK_GEMV_ENTRY(NAME, WT, XT, P, R)                                                                      \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const WT *__restrict__ w, const XT *__restrict__ x, \
+                                                         float *__restrict__ y, fk_gemv_params p) {         \
+    const uint32_t row0 = (blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * (R);             \
+    if (row0 >= p.n) return;                                                                                 \
+    fk::gemv_wave<WT, XT, P, R>(w, x, nullptr, y, p.n, p.k, row0);                                           \
+  }
+
+#define FK_GEMV_SCALED_ENTRY(NAME, WT, XT, P, R)                                                           \
+  extern "C" __global__ void __launch_bounds__(256)                                                        \
+      NAME(const WT *__restrict__ w, const float *__restrict__ scale, const XT *__restrict__ x,            \
+           float *__restrict__ y, fk_gemv_params p) {                                                      \
+    const uint32_t row0 = (blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * (R);           \
+    if (row0 >= p.n) return;                                                                               \
+    fk::gemv_wave<WT, XT, P, R>(w, x, scale, y, p.n, p.k, row0);                                           \
+  }
+
+FK_GEMV_ENTRY(fk_gemv_f32_f32_r1, float, float, 4, 1)
+FK_GEMV_ENTRY(fk_gemv_f32_f32_r2, float, float, 4, 2)
+FK_GEMV_ENTRY(fk_gemv_f32_f32_r4, float, float, 4, 4)
+FK_GEMV_ENTRY(fk_gemv_f16_f32_r1, _Float16, float, 8, 1)
+FK_GEMV_ENTRY(fk_gemv_f16_f32_r2, _Float16, float, 8, 2)
+FK_GEMV_ENTRY(fk_gemv_f16_f32_r4, _Float16, float, 8, 4)
+FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r1, int8_t, _Float16, 16, 1)
+FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r2, int8_t, _Float16, 16, 2)
+FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r4, int8_t, _Float16, 16, 4)

@@ -1,0 +1,167 @@
+"""The launch table of the hand-written gfx950 kernels.
+
+What a ``Lowered``'s ``loweredKernels`` carries for a runtime
+(src/FuryKernel/Backend.hs:76-101): each kernel's entry, its buffers in
+binding order, its parameter struct in C layout (src/FuryKernel/Abi.hs:
+113-133) and its threads.  Kernargs are the buffers' device addresses in that
+order, then the struct.
+
+Every launcher checks the shapes it is given against what its kernel assumes
+(packs dividing rows, buffers large enough for every access) before it
+launches, and raises ``LaunchError`` otherwise: a kernel is never launched on
+a shape it would read or write past.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import struct
+from dataclasses import dataclass
+from pathlib import Path
+
+from . import runtime
+
+PACKAGE = Path(__file__).resolve().parent
+CODE_OBJECT = PACKAGE / "fk_kernels.hsaco"
+WAVE = 64
+
+
+class LaunchError(ValueError):
+    """A launch whose shapes or buffers don't fit its kernel."""
+
+
+class GemvParams(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_uint32), ("k", ctypes.c_uint32)]
+
+
+class RmsNormParams(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_uint32),
+        ("width", ctypes.c_uint32),
+        ("seg", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+        ("factor", ctypes.c_float),
+        ("has_gamma", ctypes.c_uint32),
+    ]
+
+
+class SoftmaxParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("n", ctypes.c_uint32)]
+
+
+@dataclass(frozen=True)
+class KernelAbi:
+    """A kernel's binary interface: buffers in binding order, then the params struct."""
+
+    entry: str
+    buffers: tuple[str, ...]
+    params: type
+
+    def kernarg(self, bound: dict[str, int], params: ctypes.Structure) -> bytes:
+        missing = [b for b in self.buffers if b not in bound]
+        if missing:
+            raise LaunchError(f"{self.entry}: buffers {missing} not bound")
+        ptrs = struct.pack(f"<{len(self.buffers)}Q", *[int(bound[b]) for b in self.buffers])
+        return ptrs + bytes(params)
+
+
+def _gemv_abis() -> dict[str, KernelAbi]:
+    out = {}
+    for wt, xt in (("f32", "f32"), ("f16", "f32")):
+        for r in (1, 2, 4):
+            e = f"fk_gemv_{wt}_{xt}_r{r}"
+            out[e] = KernelAbi(e, ("w", "x", "y"), GemvParams)
+    for r in (1, 2, 4):
+        e = f"fk_gemv_i8_f16_r{r}"
+        out[e] = KernelAbi(e, ("w", "scale", "x", "y"), GemvParams)
+    return out
+
+
+ABIS: dict[str, KernelAbi] = {
+    **_gemv_abis(),
+    "fk_rmsnorm_f32": KernelAbi("fk_rmsnorm_f32", ("x", "gamma", "y"), RmsNormParams),
+    "fk_softmax_f32": KernelAbi("fk_softmax_f32", ("x", "y"), SoftmaxParams),
+}
+
+# Elements a lane loads at once, by weight type: one 16-byte load of W.
+GEMV_PACK = {"f32": 4, "f16": 8, "i8": 16}
+ELEM_BYTES = {"f32": 4, "f16": 2, "i8": 1}
+
+
+def _need(buf: runtime.Buffer, nbytes: int, what: str, entry: str) -> None:
+    if buf.size < nbytes:
+        raise LaunchError(f"{entry}: {what} holds {buf.size} bytes, the launch reads or writes {nbytes}")
+    if buf.ptr % 16:
+        raise LaunchError(f"{entry}: {what} is not 16-byte aligned")
+
+
+class Kernels:
+    """The code object loaded on a device, and a launcher per kernel family."""
+
+    def __init__(self, device: runtime.Device, path: Path = CODE_OBJECT):
+        if not Path(path).exists():
+            raise runtime.NativeMissing(f"{path} is not built; run __graft_entry__.build()")
+        self.device = device
+        self.module = device.load_module(path)
+
+    def fn(self, entry: str) -> runtime.Function:
+        return self.module.function(entry)
+
+    def launch(self, entry: str, groups: int, threads: int, bound: dict[str, int], params: ctypes.Structure,
+               stream: runtime.Stream | None = None, lds_bytes: int = 0) -> None:
+        abi = ABIS[entry]
+        self.fn(entry).launch(groups, threads, abi.kernarg(bound, params), lds_bytes, stream)
+
+    # y = W x: the GEMV family (test/Test/FuryKernel/Gemv.hs:131-191) at split 1.
+    def gemv(self, w: runtime.Buffer, x: runtime.Buffer, y: runtime.Buffer, n: int, k: int, wtype: str = "f32",
+             rows_per_wave: int = 1, threads: int = 256, scale: runtime.Buffer | None = None,
+             stream: runtime.Stream | None = None) -> None:
+        xtype = "f16" if wtype == "i8" else "f32"
+        entry = f"fk_gemv_{wtype}_{xtype}_r{rows_per_wave}"
+        if entry not in ABIS:
+            raise LaunchError(f"no GEMV kernel {entry}")
+        pack = GEMV_PACK[wtype]
+        if n <= 0 or k <= 0 or k % pack:
+            raise LaunchError(f"{entry}: k = {k} is not a positive multiple of the pack width {pack}")
+        if threads % WAVE or not 0 < threads <= 256:
+            raise LaunchError(f"{entry}: {threads} threads is not 1 to 4 wavefronts")
+        _need(w, n * k * ELEM_BYTES[wtype], "W", entry)
+        _need(x, k * ELEM_BYTES[xtype], "x", entry)
+        _need(y, n * 4, "y", entry)
+        bound = {"w": w.ptr, "x": x.ptr, "y": y.ptr}
+        if wtype == "i8":
+            if scale is None:
+                raise LaunchError(f"{entry}: the int8 layer needs its per-row scales")
+            _need(scale, n * 4, "scale", entry)
+            bound["scale"] = scale.ptr
+        rows_per_group = threads // WAVE * rows_per_wave
+        groups = (n + rows_per_group - 1) // rows_per_group
+        self.launch(entry, groups, threads, bound, GemvParams(n, k), stream)
+
+    def rmsnorm(self, x: runtime.Buffer, gamma: runtime.Buffer | None, y: runtime.Buffer, rows: int, width: int,
+                seg: int | None = None, eps: float = 1e-6, factor: float = 1.0, threads: int = 256,
+                stream: runtime.Stream | None = None) -> None:
+        entry = "fk_rmsnorm_f32"
+        seg = width if seg is None else seg
+        if rows <= 0 or seg <= 0 or width % seg or seg % 4:
+            raise LaunchError(f"{entry}: segments of {seg} don't divide rows of {width} into packs of 4")
+        if threads % WAVE or not 0 < threads <= 1024:
+            raise LaunchError(f"{entry}: {threads} threads is not 1 to 16 wavefronts")
+        _need(x, rows * width * 4, "x", entry)
+        _need(y, rows * width * 4, "y", entry)
+        if gamma is not None:
+            _need(gamma, seg * 4, "gamma", entry)
+        bound = {"x": x.ptr, "gamma": gamma.ptr if gamma is not None else 0, "y": y.ptr}
+        params = RmsNormParams(rows, width, seg, eps, factor, 1 if gamma is not None else 0)
+        self.launch(entry, rows * (width // seg), threads, bound, params, stream)
+
+    def softmax(self, x: runtime.Buffer, y: runtime.Buffer, rows: int, n: int, threads: int = 256,
+                stream: runtime.Stream | None = None) -> None:
+        entry = "fk_softmax_f32"
+        if rows <= 0 or n <= 0 or n % 4:
+            raise LaunchError(f"{entry}: rows of {n} are not packs of 4")
+        if threads % WAVE or not 0 < threads <= 1024:
+            raise LaunchError(f"{entry}: {threads} threads is not 1 to 16 wavefronts")
+        _need(x, rows * n * 4, "x", entry)
+        _need(y, rows * n * 4, "y", entry)
+        self.launch(entry, rows, threads, {"x": x.ptr, "y": y.ptr}, SoftmaxParams(rows, n), stream)

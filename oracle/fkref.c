@@ -1,0 +1,332 @@
+/*
+ * fkref.c — the oracle's C restatement (see fkref.h).
+ *
+ * TEST INFRASTRUCTURE: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load this, as the checker and the CPU baseline.
+ *
+ * Built with -O2 -ffp-contract=off and no fast-math, so each C operation on
+ * floats is one IEEE 754 operation rounded once, as the CPU target's Rust is
+ * (src/FuryKernel/Backend.hs:52-73: Strict, no contraction).
+ */
+#include "fkref.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* Numerics: src/FuryKernel/Numerics.hs                                      */
+
+static uint32_t bits_of(float x) {
+  uint32_t w;
+  memcpy(&w, &x, 4);
+  return w;
+}
+
+static float float_of(uint32_t w) {
+  float x;
+  memcpy(&x, &w, 4);
+  return x;
+}
+
+/* widenBF16 (Numerics.hs:33-39): the upper half of a binary32; NaN quiet. */
+float fkref_widen_bf16(uint16_t b) {
+  uint32_t w = (uint32_t)b << 16;
+  if ((w & 0x7F800000u) == 0x7F800000u && (w & 0x007FFFFFu) != 0) w |= 0x00400000u;
+  return float_of(w);
+}
+
+/* narrowBF16 (Numerics.hs:41-49): RNE by adding 0x7FFF plus the kept lsb. */
+uint16_t fkref_narrow_bf16(float x) {
+  uint32_t w = bits_of(x);
+  if (isnan(x)) return (uint16_t)((w >> 16) | 0x0040);
+  uint32_t lsb = (w >> 16) & 1u;
+  return (uint16_t)((w + 0x7FFFu + lsb) >> 16);
+}
+
+/* widenF16 (Numerics.hs:51-71): exact, subnormals normalised, NaN quiet. */
+float fkref_widen_f16(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1Fu;
+  uint32_t m = h & 0x3FFu;
+  uint32_t mag;
+  if (e == 0x1F && m != 0) {
+    mag = 0x7FC00000u | (m << 13);
+  } else if (e == 0x1F) {
+    mag = 0x7F800000u;
+  } else if (e != 0) {
+    mag = ((e + 112u) << 23) | (m << 13);
+  } else if (m == 0) {
+    mag = 0;
+  } else {
+    int shift = 0; /* leading zeros of the 10-bit mantissa */
+    while (!(m & (0x200u >> shift))) shift++;
+    uint32_t m2 = (m << (shift + 1)) & 0x3FFu;
+    mag = ((uint32_t)(113 - shift - 1) << 23) | (m2 << 13);
+  }
+  return float_of(sign | mag);
+}
+
+/* roundShifted (Numerics.hs:159-167). */
+static uint64_t round_shifted(uint64_t kept, uint64_t dropped, int width) {
+  uint64_t half = (uint64_t)1 << (width - 1);
+  if (dropped > half || (dropped == half && (kept & 1u))) return kept + 1;
+  return kept;
+}
+
+/* narrowF16 (Numerics.hs:100-130): RNE with gradual underflow. */
+uint16_t fkref_narrow_f16(float x) {
+  uint32_t w = bits_of(x);
+  uint16_t sign = (uint16_t)((w >> 16) & 0x8000u);
+  int e = (int)((w >> 23) & 0xFFu);
+  uint32_t m = w & 0x7FFFFFu;
+  int unbiased = e - 127;
+  uint16_t mag;
+  if (e == 0xFF && m != 0) {
+    mag = (uint16_t)(0x7E00u | (m >> 13));
+  } else if (e == 0xFF) {
+    mag = 0x7C00;
+  } else if (unbiased >= 16) {
+    mag = 0x7C00;
+  } else if (unbiased >= -14) {
+    uint32_t r = ((uint32_t)(unbiased + 15) << 10) | (m >> 13);
+    mag = (uint16_t)round_shifted(r, m & 0x1FFFu, 13);
+  } else {
+    int shift = -(unbiased + 1);
+    uint32_t full = m | 0x800000u;
+    if (shift > 24) {
+      mag = 0;
+    } else {
+      mag = (uint16_t)round_shifted(full >> shift, full & ((1u << shift) - 1u), shift);
+    }
+  }
+  return (uint16_t)(sign | mag);
+}
+
+/* narrowF16Double (Numerics.hs:132-157): binary64 to binary16 in one rounding. */
+uint16_t fkref_narrow_f16_f64(double x) {
+  uint64_t w;
+  memcpy(&w, &x, 8);
+  uint16_t sign = (uint16_t)((w >> 48) & 0x8000u);
+  int e = (int)((w >> 52) & 0x7FFu);
+  uint64_t m = w & 0xFFFFFFFFFFFFFull;
+  int unbiased = e - 1023;
+  uint16_t mag;
+  if (e == 0x7FF && m != 0) {
+    mag = (uint16_t)(0x7E00u | (uint16_t)(m >> 42));
+  } else if (e == 0x7FF) {
+    mag = 0x7C00;
+  } else if (unbiased >= 16) {
+    mag = 0x7C00;
+  } else if (unbiased >= -14) {
+    uint64_t r = ((uint64_t)(unbiased + 15) << 10) | (m >> 42);
+    mag = (uint16_t)round_shifted(r, m & ((1ull << 42) - 1), 42);
+  } else {
+    int shift = 28 - unbiased;
+    uint64_t full = m | (1ull << 52);
+    if (shift > 53) {
+      mag = 0;
+    } else {
+      mag = (uint16_t)round_shifted(full >> shift, full & ((1ull << shift) - 1), shift);
+    }
+  }
+  return (uint16_t)(sign | mag);
+}
+
+/* minimumNumber / maximumNumber (Interp.hs:940-956). */
+float fkref_min(float x, float y) {
+  if (isnan(x)) return isnan(y) ? float_of(0x7FC00000u) : y;
+  if (isnan(y) || x < y) return x;
+  if (y < x) return y;
+  return float_of(bits_of(x) | bits_of(y));
+}
+
+float fkref_max(float x, float y) {
+  if (isnan(x)) return isnan(y) ? float_of(0x7FC00000u) : y;
+  if (isnan(y) || x > y) return x;
+  if (y > x) return y;
+  return float_of(bits_of(x) & bits_of(y));
+}
+
+/* Transcendentals in binary64, rounded once (Interp.hs:828-854). */
+float fkref_rsqrt(float x) { return (float)(1.0 / sqrt((double)x)); }
+
+float fkref_exp(float x) { return (float)exp((double)x); }
+
+/* ------------------------------------------------------------------------ */
+/* Reductions: Interp.hs:733-745, Reduce.hs                                  */
+
+/* Pairwise, neighbours first: ((x0+x1)+(x2+x3))+...; an odd lane out goes on
+ * as it is (Interp.hs:733-745).  width <= 1024. */
+static float simd_reduce(const float *lanes, int width, int is_max) {
+  float buf[1024];
+  int n = width;
+  if (n <= 0) return is_max ? -INFINITY : -0.0f;
+  memcpy(buf, lanes, sizeof(float) * (size_t)n);
+  while (n > 1) {
+    int out = 0;
+    int i = 0;
+    for (; i + 1 < n; i += 2) buf[out++] = is_max ? fkref_max(buf[i], buf[i + 1]) : buf[i] + buf[i + 1];
+    if (i < n) buf[out++] = buf[i];
+    n = out;
+  }
+  return buf[0];
+}
+
+float fkref_simd_sum(const float *lanes, int width) { return simd_reduce(lanes, width, 0); }
+
+float fkref_simd_max(const float *lanes, int width) { return simd_reduce(lanes, width, 1); }
+
+/* tgReduce (Reduce.hs:55-85): each SIMD group's reduction in its slot; the
+ * first group's lane l folds slots l, l + width, ... from the neutral value;
+ * then one more SIMD reduction. */
+static float tg_reduce(const float *v, int threads, int width, int is_max) {
+  int groups = threads / width;
+  float slots[1024];
+  float lanes[1024];
+  for (int g = 0; g < groups; g++) slots[g] = simd_reduce(v + (size_t)g * width, width, is_max);
+  for (int l = 0; l < width; l++) {
+    float acc = is_max ? -INFINITY : -0.0f;
+    for (int k = l; k < groups; k += width) acc = is_max ? fkref_max(acc, slots[k]) : acc + slots[k];
+    lanes[l] = acc;
+  }
+  return simd_reduce(lanes, width, is_max);
+}
+
+float fkref_tg_reduce_sum(const float *v, int threads, int width) { return tg_reduce(v, threads, width, 0); }
+
+float fkref_tg_reduce_max(const float *v, int threads, int width) { return tg_reduce(v, threads, width, 1); }
+
+/* combineSplits (Reduce.hs:112-125): ((p0 + p1) + p2) + ... */
+float fkref_combine_splits(const float *p, int splits) {
+  float acc = p[0];
+  for (int q = 1; q < splits; q++) acc = acc + p[q];
+  return acc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMV: test/Test/FuryKernel/Gemv.hs:131-191                                */
+
+static float element(const void *base, int type, size_t i) {
+  switch (type) {
+    case FKREF_F32: return ((const float *)base)[i];
+    case FKREF_F16: return fkref_widen_f16(((const uint16_t *)base)[i]);
+    case FKREF_BF16: return fkref_widen_bf16(((const uint16_t *)base)[i]);
+    case FKREF_I8: return (float)((const int8_t *)base)[i];
+    default: return NAN;
+  }
+}
+
+int fkref_gemv(const void *w, int wtype, const void *x, int xtype, float *y, const float *row_scale, int n, int k,
+               int m, int width, int pack, int split) {
+  if (n < 0 || k <= 0 || m <= 0 || width <= 0 || width > 1024 || pack < 4 || pack % 4 || k % pack || split <= 0 ||
+      split > 64)
+    return -1;
+  const int packs = k / pack;
+  const int vlanes = split * width;
+  const int chains = pack / 4;
+  float *lane_total = (float *)malloc(sizeof(float) * (size_t)vlanes);
+  float *acc = (float *)malloc(sizeof(float) * (size_t)chains);
+  float partial[64];
+  if (!lane_total || !acc) {
+    free(lane_total);
+    free(acc);
+    return -2;
+  }
+  for (int i = 0; i < m; i++) {
+    for (int j = 0; j < n; j++) {
+      for (int v = 0; v < vlanes; v++) {
+        /* Lane v of the virtual lanes (split q = v / width) visits packs
+         * v, v + split * width, ...; each pack's elements go four to a chain,
+         * ((x0 w0 + x1 w1) + (x2 w2 + x3 w3)), each chain its own sum. */
+        for (int c = 0; c < chains; c++) acc[c] = 0.0f;
+        for (int jp = v; jp < packs; jp += vlanes) {
+          for (int c = 0; c < chains; c++) {
+            size_t at = (size_t)jp * pack + 4 * c;
+            float p0 = element(x, xtype, (size_t)i * k + at) * element(w, wtype, (size_t)j * k + at);
+            float p1 = element(x, xtype, (size_t)i * k + at + 1) * element(w, wtype, (size_t)j * k + at + 1);
+            float p2 = element(x, xtype, (size_t)i * k + at + 2) * element(w, wtype, (size_t)j * k + at + 2);
+            float p3 = element(x, xtype, (size_t)i * k + at + 3) * element(w, wtype, (size_t)j * k + at + 3);
+            acc[c] = acc[c] + ((p0 + p1) + (p2 + p3));
+          }
+        }
+        /* The lane's chains in order (Gemv.hs:216-220, inOrder). */
+        float t = acc[0];
+        for (int c = 1; c < chains; c++) t = t + acc[c];
+        lane_total[v] = t;
+      }
+      for (int q = 0; q < split; q++) partial[q] = fkref_simd_sum(lane_total + (size_t)q * width, width);
+      float total = fkref_combine_splits(partial, split);
+      if (row_scale) total = total * row_scale[j];
+      y[(size_t)i * n + j] = total;
+    }
+  }
+  free(lane_total);
+  free(acc);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm: test/Test/FuryKernel/Kernels.hs:53-74                            */
+
+int fkref_rmsnorm(const float *x, const float *gamma, float *y, int rows, int width_elems, int seg, float eps,
+                  float factor, int threads, int width, int pack) {
+  if (rows < 0 || seg <= 0 || width_elems % seg || seg % pack || threads % width || threads > 1024) return -1;
+  float acc[1024];
+  const int segs = width_elems / seg;
+  const int packs = seg / pack;
+  for (int r = 0; r < rows; r++) {
+    for (int s = 0; s < segs; s++) {
+      const float *xs = x + (size_t)r * width_elems + (size_t)s * seg;
+      float *ys = y + (size_t)r * width_elems + (size_t)s * seg;
+      for (int t = 0; t < threads; t++) {
+        float a = 0.0f;
+        for (int j = t; j < packs; j += threads) {
+          for (int e = 0; e < pack; e++) {
+            float v = xs[(size_t)j * pack + e];
+            a = a + v * v;
+          }
+        }
+        acc[t] = a;
+      }
+      float total = fkref_tg_reduce_sum(acc, threads, width);
+      float scale = fkref_rsqrt(total / (float)seg + eps);
+      for (int i = 0; i < seg; i++) {
+        float v = xs[i] * scale;
+        if (gamma) v = v * gamma[i];
+        if (factor != 1.0f) v = v * factor;
+        ys[i] = v;
+      }
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Row softmax (the reductions of src/FuryKernel/Reduce.hs:29-85)            */
+
+int fkref_softmax(const float *x, float *y, int rows, int n, int threads, int width, int pack) {
+  if (rows < 0 || n <= 0 || n % pack || threads % width || threads > 1024) return -1;
+  float acc[1024];
+  const int packs = n / pack;
+  for (int r = 0; r < rows; r++) {
+    const float *xs = x + (size_t)r * n;
+    float *ys = y + (size_t)r * n;
+    for (int t = 0; t < threads; t++) {
+      float a = -INFINITY;
+      for (int j = t; j < packs; j += threads)
+        for (int e = 0; e < pack; e++) a = fkref_max(a, xs[(size_t)j * pack + e]);
+      acc[t] = a;
+    }
+    float top = fkref_tg_reduce_max(acc, threads, width);
+    for (int t = 0; t < threads; t++) {
+      float a = -0.0f;
+      for (int j = t; j < packs; j += threads)
+        for (int e = 0; e < pack; e++) a = a + fkref_exp(xs[(size_t)j * pack + e] - top);
+      acc[t] = a;
+    }
+    float total = fkref_tg_reduce_sum(acc, threads, width);
+    for (int i = 0; i < n; i++) ys[i] = fkref_exp(xs[i] - top) / total;
+  }
+  return 0;
+}

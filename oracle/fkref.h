@@ -1,0 +1,81 @@
+/*
+ * fkref.h — the oracle: a CPU restatement of FuryKernel's interpreter and CPU
+ * target arithmetic (src/FuryKernel/Interp.hs, src/FuryKernel/Cpu.hs), of the
+ * reference's reduction orders (src/FuryKernel/Reduce.hs, test/Test/FuryKernel/
+ * Gemv.hs, test/Test/FuryKernel/Kernels.hs) and of the kernels of a planned
+ * step, in plain C: lanes in lock-step, one thread, threadgroups in sequence
+ * (src/FuryKernel/Cpu.hs:4-14,259-263).
+ *
+ * TEST INFRASTRUCTURE.  Only the tests, the smoke check and the benchmark's
+ * CPU-baseline leg load this library, as the checker of the HIP kernels and
+ * as the CPU baseline.  Nothing of the product links or calls it.
+ *
+ * Every reduction takes the SIMD width `width` as a parameter: 32 is the CPU
+ * target's (src/FuryKernel/Cpu.hs:73), 64 is gfx950's wavefront.
+ */
+#ifndef FKREF_H
+#define FKREF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types, as the kernels' buffers hold them. */
+enum { FKREF_F32 = 0, FKREF_F16 = 1, FKREF_BF16 = 2, FKREF_I8 = 3, FKREF_U32 = 4 };
+
+/* Numerics (src/FuryKernel/Numerics.hs). */
+float fkref_widen_bf16(uint16_t b);
+uint16_t fkref_narrow_bf16(float x);
+float fkref_widen_f16(uint16_t h);
+uint16_t fkref_narrow_f16(float x);
+uint16_t fkref_narrow_f16_f64(double x);
+/* IEEE 754-2019 minimumNumber / maximumNumber as the interpreter has them
+ * (src/FuryKernel/Interp.hs:940-956). */
+float fkref_min(float a, float b);
+float fkref_max(float a, float b);
+/* rsqrt, exp, log, tanh: binary64's, rounded once to binary32
+ * (src/FuryKernel/Interp.hs:828-854). */
+float fkref_rsqrt(float x);
+float fkref_exp(float x);
+
+/* SIMD-group reductions: pairwise, neighbours first (src/FuryKernel/IR.hs:
+ * 269-283, src/FuryKernel/Interp.hs:733-745). */
+float fkref_simd_sum(const float *lanes, int width);
+float fkref_simd_max(const float *lanes, int width);
+/* Threadgroup reductions of one value per thread (src/FuryKernel/Reduce.hs:
+ * 29-85): `threads` a multiple of `width`. */
+float fkref_tg_reduce_sum(const float *per_thread, int threads, int width);
+float fkref_tg_reduce_max(const float *per_thread, int threads, int width);
+/* Split-K's combine: partials added in split order (src/FuryKernel/Reduce.hs:
+ * 87-125). */
+float fkref_combine_splits(const float *partials, int splits);
+
+/* The GEMV of test/Test/FuryKernel/Gemv.hs:131-191, in its order.
+ * W is [n, k] (out_in) of `wtype`, x is [m, k] of `xtype`, y is [m, n] f32.
+ * pack: elements a lane loads at once (a multiple of 4); split: SIMD groups
+ * sharing a row.  `row_scale` (n f32, or NULL) multiplies each output row's
+ * sum: y = total * scale (the int8 weight-only layer). */
+int fkref_gemv(const void *w, int wtype, const void *x, int xtype, float *y, const float *row_scale, int n, int k,
+               int m, int width, int pack, int split);
+
+/* RMSNorm in the order of test/Test/FuryKernel/Kernels.hs:53-74, generalised
+ * to packs and segments: one threadgroup of `threads` threads per segment;
+ * thread t visits packs t, t + threads, ...; its sum of squares, then
+ * tgReduceSum; scale = rsqrt(total / seg + eps); y = ((x * scale) * gamma) *
+ * factor, gamma (seg f32) optional, factor skipped when 1. */
+int fkref_rmsnorm(const float *x, const float *gamma, float *y, int rows, int width_elems, int seg, float eps,
+                  float factor, int threads, int width, int pack);
+
+/* A row softmax: tgReduceMax of the elements (from -inf), exp(x - max) in
+ * binary64 rounded once, tgReduceSum of those (from -0), and each over the
+ * sum (src/FuryKernel/Reduce.hs:39-47 for the reductions). */
+int fkref_softmax(const float *x, float *y, int rows, int n, int threads, int width, int pack);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FKREF_H */

@@ -1,0 +1,142 @@
+"""The standalone kernels on the GPU, through the C ABI, against the oracle.
+
+Bars (the reference's CPU target is SIMD width 32, gfx950's wavefront 64):
+* bit for bit against the oracle in the kernel's own order (width 64), which
+  for the GEMVs is also the CPU target's width-32 split-2 order;
+* within 1e-5 relative (to the row's magnitude) of the CPU target's default
+  width-32 split-1 order, and of f64;
+* exps are binary64's rounded once: the oracle's libm and the GPU's may round
+  a value within their error of a binary32 midpoint differently, so those
+  outputs are held to 1 ulp (src/FuryKernel/IR.hs:119-127 states the same
+  leeway between platforms), and to being rare.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import fkref
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(2027)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def ulps(a, b):
+    ia = bits(a).astype(np.int64)
+    ib = bits(b).astype(np.int64)
+    ia = np.where(ia & 0x80000000, 0x80000000 - ia, ia)
+    ib = np.where(ib & 0x80000000, 0x80000000 - ib, ib)
+    return np.abs(ia - ib)
+
+
+def run_gemv(device, kernels, w, x, wtype, r=1, scale=None):
+    n, k = w.shape
+    bw, bx, by = device.upload(w), device.upload(x), device.alloc(n * 4)
+    bs = device.upload(scale) if scale is not None else None
+    print(f"gemv {wtype} {n}x{k} r{r}", flush=True)
+    kernels.gemv(bw, bx, by, n, k, wtype=wtype, rows_per_wave=r, scale=bs)
+    device.sync()
+    out = by.read(np.float32, n)
+    for b in (bw, bx, by, bs):
+        if b is not None:
+            b.free()
+    return out
+
+
+@pytest.mark.parametrize("r", [1, 2, 4])
+def test_gemv_f32_4096(device, kernels, r):
+    n = k = 4096
+    w = RNG.uniform(-1, 1, (n, k)).astype(np.float32)
+    x = RNG.uniform(-1, 1, k).astype(np.float32)
+    got = run_gemv(device, kernels, w, x, "f32", r)
+    assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 64, 4, 1)))
+    assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 32, 4, 2)))
+    mag = np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    cpu32 = fkref.gemv(w, x, 32, 4, 1)
+    assert np.max(np.abs(got - cpu32) / mag) < 1e-5
+    exact = w.astype(np.float64) @ x.astype(np.float64)
+    assert np.max(np.abs(got - exact) / mag) < 1e-5
+
+
+@pytest.mark.parametrize("n,k,r", [(3072, 2048, 1), (2048, 2048, 2), (8192, 2048, 4), (2048, 8192, 1),
+                                   (37, 8, 1), (65, 136, 2), (1, 2048, 4)])
+def test_gemv_f16_decode_shapes_and_ragged(device, kernels, n, k, r):
+    w = RNG.normal(0, 0.02, (n, k)).astype(np.float16)
+    x = RNG.normal(0, 1, k).astype(np.float32)
+    got = run_gemv(device, kernels, w, x, "f16", r)
+    assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 64, 8, 1)))
+
+
+def test_gemv_i8_8192(device, kernels):
+    n = k = 8192
+    w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
+    x = RNG.normal(0, 1, k).astype(np.float16)
+    s = RNG.uniform(0.001, 0.01, n).astype(np.float32)
+    got = run_gemv(device, kernels, w, x, "i8", 2, scale=s)
+    assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 64, 16, 1, row_scale=s)))
+    assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 32, 16, 2, row_scale=s)))
+
+
+def test_gemv_i8_integer_closed_form(device, kernels):
+    n, k = 256, 8192
+    w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
+    x = RNG.integers(-8, 9, k).astype(np.float16)
+    s = RNG.uniform(0.001, 0.01, n).astype(np.float32)
+    got = run_gemv(device, kernels, w, x, "i8", 1, scale=s)
+    exact = w.astype(np.int64) @ x.astype(np.int64)
+    assert np.array_equal(got, (exact.astype(np.float32) * s).astype(np.float32))
+
+
+@pytest.mark.parametrize("threads", [256, 1024])
+def test_rmsnorm_64x4096(device, kernels, threads):
+    rows, h = 64, 4096
+    x = RNG.uniform(-1, 1, (rows, h)).astype(np.float32)
+    g = RNG.uniform(-1, 1, h).astype(np.float32)
+    bx, bg, by = device.upload(x), device.upload(g), device.alloc(x.nbytes)
+    print(f"rmsnorm {rows}x{h} t{threads}", flush=True)
+    kernels.rmsnorm(bx, bg, by, rows, h, eps=1e-6, threads=threads)
+    device.sync()
+    got = by.read(np.float32).reshape(rows, h)
+    want = fkref.rmsnorm(x, g, 1e-6, threads=threads, width=64, pack=4)
+    # rsqrt is binary64's rounded once: one value a row, held to 1 ulp.
+    u = ulps(got, want)
+    assert u.max() <= 1
+    assert np.mean(u > 0) < 1e-3
+    cpu32 = fkref.rmsnorm(x, g, 1e-6, threads=256, width=32, pack=1)
+    assert np.max(np.abs(got - cpu32) / (np.abs(cpu32) + 1e-30)) < 1e-5
+    for b in (bx, bg, by):
+        b.free()
+
+
+def test_rmsnorm_segments_factor_no_gamma(device, kernels):
+    rows, h, seg = 3, 512, 64
+    x = RNG.uniform(-4, 4, (rows, h)).astype(np.float32)
+    bx, by = device.upload(x), device.alloc(x.nbytes)
+    print("rmsnorm segments", flush=True)
+    kernels.rmsnorm(bx, None, by, rows, h, seg=seg, eps=1e-5, factor=0.5, threads=64)
+    device.sync()
+    got = by.read(np.float32).reshape(rows, h)
+    want = fkref.rmsnorm(x, None, 1e-5, threads=64, width=64, pack=4, seg=seg, factor=0.5)
+    assert ulps(got, want).max() <= 1
+
+
+@pytest.mark.parametrize("threads", [256, 1024])
+def test_softmax_64x4096(device, kernels, threads):
+    rows, n = 64, 4096
+    x = RNG.uniform(-1, 1, (rows, n)).astype(np.float32)
+    bx, by = device.upload(x), device.alloc(x.nbytes)
+    print(f"softmax {rows}x{n} t{threads}", flush=True)
+    kernels.softmax(bx, by, rows, n, threads=threads)
+    device.sync()
+    got = by.read(np.float32).reshape(rows, n)
+    want = fkref.softmax(x, threads=threads, width=64, pack=4)
+    u = ulps(got, want)
+    assert u.max() <= 2
+    assert np.mean(u > 0) < 1e-3
+    xd = x.astype(np.float64)
+    e = np.exp(xd - xd.max(axis=1, keepdims=True))
+    spec = e / e.sum(axis=1, keepdims=True)
+    assert np.max(np.abs(got - spec) / spec) < 1e-5
