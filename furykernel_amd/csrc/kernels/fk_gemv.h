@@ -61,6 +61,31 @@ __device__ __forceinline__ void load_pack(const int8_t *__restrict__ p, float (&
   }
 }
 
+// A pack held in registers as 16-byte words, widened to f32 exactly.
+template <int P>
+__device__ __forceinline__ void unpack(const uint4 (&u)[P / 4], float (&out)[P], float) {
+#pragma unroll
+  for (int i = 0; i < P / 4; i++) {
+    out[4 * i] = __uint_as_float(u[i].x);
+    out[4 * i + 1] = __uint_as_float(u[i].y);
+    out[4 * i + 2] = __uint_as_float(u[i].z);
+    out[4 * i + 3] = __uint_as_float(u[i].w);
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void unpack(const uint4 (&u)[P / 8], float (&out)[P], _Float16) {
+#pragma unroll
+  for (int i = 0; i < P / 8; i++) {
+    const uint32_t words[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      out[8 * i + 2 * h] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] & 0xFFFFu));
+      out[8 * i + 2 * h + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] >> 16));
+    }
+  }
+}
+
 // R rows of y = W x (times a per-row scale if given) by one wavefront.
 template <typename WT, typename XT, int P, int R>
 __device__ __forceinline__ void gemv_wave(const WT *__restrict__ w, const XT *__restrict__ x, const float *__restrict__ scale,

@@ -3,3 +3,5 @@
 // runtime loads (include/fkrocm.h: fk_module_load).
 #include "fk_gemv.h"
 #include "fk_rows.h"
+#include "fk_misc.h"
+#include "fk_step.h"

@@ -1,0 +1,131 @@
+"""Runs a lowered plan on the GPU: the executor of a planned step.
+
+Everything a step reads or writes lives in one arena of HBM, allocated once
+and resident across steps: the weights, the KV caches, the values steps store
+for later steps, the attention partials, the row integers.  Each launch's
+kernarg bytes are built once (the buffers never move), so a step is a list of
+``fk_launch`` calls, which ``capture`` records into a HIP graph and
+``Graph.replay`` runs as one.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+
+from . import kernels as K
+from . import runtime
+from .lower import Launch, Lowered
+
+_NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16}
+_STRUCTS = {
+    "fk_step_store": K.StepStoreParams,
+    "fk_step_attend": K.StepAttendParams,
+    "fk_step_combine": K.StepCombineParams,
+    "fk_step_argmax": K.CountParams,
+    "fk_step_silu_mul": K.CountParams,
+}
+
+
+def params_struct(launch: Launch) -> ctypes.Structure:
+    cls = K.StepGemvParams if launch.entry.startswith("fk_step_gemv") else _STRUCTS[launch.entry]
+    s = cls()
+    for name, value in launch.params.items():
+        field = getattr(cls, name, None)
+        if field is None:
+            raise K.LaunchError(f"{launch.entry}: no parameter {name}")
+        if isinstance(value, (list, tuple)):
+            arr = getattr(s, name)
+            for i, v in enumerate(value):
+                arr[i] = v
+        else:
+            setattr(s, name, value)
+    return s
+
+
+class Engine:
+    def __init__(self, device: runtime.Device, ks: K.Kernels, lowered: Lowered, extra_bytes: int = 0):
+        self.device = device
+        self.kernels = ks
+        self.lowered = lowered
+        specs = lowered.buffers
+        total = sum((spec.nbytes + 255) // 256 * 256 for spec in specs.values()) + 4096 + extra_bytes
+        self.arena = device.arena(total)
+        self.buffers: dict[str, runtime.Buffer] = {}
+        for name, spec in specs.items():
+            self.buffers[name] = self.arena.alloc(spec.nbytes, 256)
+        self._kernargs = [self._kernarg(launch) for launch in lowered.launches]
+        self._fns = [ks.fn(launch.entry) for launch in lowered.launches]
+
+    def _kernarg(self, launch: Launch) -> bytes:
+        abi = K.ABIS[launch.entry]
+        bound = {}
+        for b in abi.buffers:
+            name = launch.bind.get(b)
+            bound[b] = 0 if name is None else self.buffers[name].ptr
+        return abi.kernarg(bound, params_struct(launch))
+
+    # State -------------------------------------------------------------------
+
+    def spec(self, name: str):
+        return self.lowered.buffers[name]
+
+    def write(self, name: str, values: np.ndarray) -> None:
+        spec = self.spec(name)
+        a = np.ascontiguousarray(values, dtype=_NP[spec.dtype]).reshape(-1)
+        if a.size != spec.count:
+            raise ValueError(f"{name}: {a.size} elements for a buffer of {spec.count}")
+        self.buffers[name].write(a)
+
+    def read(self, name: str) -> np.ndarray:
+        spec = self.spec(name)
+        return self.buffers[name].read(_NP[spec.dtype], spec.count)
+
+    def set_ints(self, source: str, values, bound: Optional[int] = None) -> None:
+        a = np.asarray(values, dtype=np.uint32).reshape(-1)
+        if bound is not None and np.any(a >= bound):
+            raise ValueError(f"{source}: {a.tolist()} not below its bound {bound}")
+        self.write(f"ints:{source}", a)
+
+    def init_normal(self, name: str, seed: int, std: float) -> None:
+        """Synthetic values on the device: std * N(0, 1), SplitMix64 + Box-Muller."""
+        spec = self.spec(name)
+        if spec.dtype not in ("f16", "f32"):
+            raise ValueError(f"{name}: normals of {spec.dtype}")
+        buf = self.buffers[name]
+        groups = min(max(spec.count // 256, 1), 65536)
+        self.kernels.launch("fk_init_normal", groups, 256, {"dst": buf.ptr},
+                            K.InitNormalParams(spec.count, seed & 0xFFFFFFFFFFFFFFFF, std,
+                                               1 if spec.dtype == "f16" else 0))
+
+    def zero(self, name: str) -> None:
+        self.kernels.fill_u32(self.buffers[name], 0, (self.spec(name).nbytes + 3) // 4)
+
+    # Running -----------------------------------------------------------------
+
+    def enqueue(self, stream: runtime.Stream | None = None) -> None:
+        """Queues every launch of the step, in plan order."""
+        for launch, fn, arg in zip(self.lowered.launches, self._fns, self._kernargs):
+            fn.launch(launch.groups, launch.threads, arg, launch.lds_bytes, stream)
+
+    def enqueue_advance(self, token_out: str, token_in: str, position: str, context: int, step: int = 1,
+                        stream: runtime.Stream | None = None) -> None:
+        """The next decode step's inputs on the device: the greedy token in,
+        the position `step` on."""
+        self.kernels.launch("fk_step_advance", 1, 64,
+                            {"next_token": self.buffers[token_out].ptr, "token": self.buffers[token_in].ptr,
+                             "position": self.buffers[position].ptr},
+                            K.AdvanceParams(context, step), stream)
+
+    def capture(self, advance: Optional[dict] = None, stream: runtime.Stream | None = None) -> runtime.Graph:
+        """A graph of the step's launches (and the advance, if given), to replay."""
+        with self.device.capture(stream) as out:
+            self.enqueue(stream)
+            if advance is not None:
+                self.enqueue_advance(stream=stream, **advance)
+        return out[0]
+
+    def close(self) -> None:
+        self.arena.destroy()

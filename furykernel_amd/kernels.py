@@ -49,6 +49,80 @@ class SoftmaxParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("n", ctypes.c_uint32)]
 
 
+class FillParams(ctypes.Structure):
+    _fields_ = [("count", ctypes.c_uint32), ("value", ctypes.c_uint32)]
+
+
+class NoopParams(ctypes.Structure):
+    _fields_ = [("unused", ctypes.c_uint32)]
+
+
+class StepGemvParams(ctypes.Structure):
+    _fields_ = [
+        ("n_anchors", ctypes.c_uint32),
+        ("rows", ctypes.c_uint32 * 3),
+        ("first_group", ctypes.c_uint32 * 4),
+        ("k", ctypes.c_uint32),
+        ("pro_mode", ctypes.c_uint32),
+        ("seg", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+        ("factor", ctypes.c_float),
+        ("gfactor", ctypes.c_float),
+        ("has_gamma", ctypes.c_uint32),
+        ("epi_mode", ctypes.c_uint32),
+        ("store_tile", ctypes.c_uint32),
+        ("table_rows", ctypes.c_uint32),
+    ]
+
+
+class StepStoreParams(ctypes.Structure):
+    _fields_ = [
+        ("n_stores", ctypes.c_uint32),
+        ("rope", ctypes.c_uint32 * 2),
+        ("kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("length", ctypes.c_uint32),
+        ("slots", ctypes.c_uint32),
+        ("rotated", ctypes.c_uint32),
+        ("theta", ctypes.c_float),
+        ("cache_bf16", ctypes.c_uint32),
+    ]
+
+
+class StepAttendParams(ctypes.Structure):
+    _fields_ = [
+        ("heads", ctypes.c_uint32),
+        ("kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("length", ctypes.c_uint32),
+        ("slots", ctypes.c_uint32),
+        ("splits", ctypes.c_uint32),
+        ("rope", ctypes.c_uint32),
+        ("rotated", ctypes.c_uint32),
+        ("theta", ctypes.c_float),
+        ("scale", ctypes.c_float),
+        ("window", ctypes.c_uint32),
+        ("cache_bf16", ctypes.c_uint32),
+    ]
+
+
+class StepCombineParams(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32), ("splits", ctypes.c_uint32)]
+
+
+class CountParams(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_uint32)]
+
+
+class AdvanceParams(ctypes.Structure):
+    _fields_ = [("context", ctypes.c_uint32), ("step", ctypes.c_uint32)]
+
+
+class InitNormalParams(ctypes.Structure):
+    _fields_ = [("count", ctypes.c_uint64), ("seed", ctypes.c_uint64), ("std", ctypes.c_float),
+                ("f16", ctypes.c_uint32)]
+
+
 @dataclass(frozen=True)
 class KernelAbi:
     """A kernel's binary interface: buffers in binding order, then the params struct."""
@@ -81,6 +155,19 @@ ABIS: dict[str, KernelAbi] = {
     **_gemv_abis(),
     "fk_rmsnorm_f32": KernelAbi("fk_rmsnorm_f32", ("x", "gamma", "y"), RmsNormParams),
     "fk_softmax_f32": KernelAbi("fk_softmax_f32", ("x", "y"), SoftmaxParams),
+    "fk_fill_u32": KernelAbi("fk_fill_u32", ("dst",), FillParams),
+    **{f"fk_step_gemv_{t}_r{r}": KernelAbi(f"fk_step_gemv_{t}_r{r}", (
+        "w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
+        "res_token", "epi_out"), StepGemvParams) for t, r in (("f16", 1), ("f16", 2), ("f32", 1))},
+    "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot"), StepStoreParams),
+    "fk_step_attend": KernelAbi("fk_step_attend", ("q", "kc", "vc", "position", "slot", "partials"),
+                                StepAttendParams),
+    "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams),
+    "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
+    "fk_step_silu_mul": KernelAbi("fk_step_silu_mul", ("a", "b", "y"), CountParams),
+    "fk_step_advance": KernelAbi("fk_step_advance", ("next_token", "token", "position"), AdvanceParams),
+    "fk_init_normal": KernelAbi("fk_init_normal", ("dst",), InitNormalParams),
+    "fk_noop": KernelAbi("fk_noop", (), NoopParams),
 }
 
 # Elements a lane loads at once, by weight type: one 16-byte load of W.
@@ -154,6 +241,15 @@ class Kernels:
         bound = {"x": x.ptr, "gamma": gamma.ptr if gamma is not None else 0, "y": y.ptr}
         params = RmsNormParams(rows, width, seg, eps, factor, 1 if gamma is not None else 0)
         self.launch(entry, rows * (width // seg), threads, bound, params, stream)
+
+    def fill_u32(self, dst: runtime.Buffer, value: int = 0, count: int | None = None,
+                 stream: runtime.Stream | None = None) -> None:
+        """Sets 32-bit words of a buffer: what a graph clears memory with."""
+        count = dst.size // 4 if count is None else count
+        if count * 4 > dst.size:
+            raise LaunchError(f"fk_fill_u32: {count} words past a buffer of {dst.size} bytes")
+        groups = min(max((count + 255) // 256, 1), 4096)
+        self.launch("fk_fill_u32", groups, 256, {"dst": dst.ptr}, FillParams(count, value & 0xFFFFFFFF), stream)
 
     def softmax(self, x: runtime.Buffer, y: runtime.Buffer, rows: int, n: int, threads: int = 256,
                 stream: runtime.Stream | None = None) -> None:

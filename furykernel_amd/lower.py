@@ -1,0 +1,429 @@
+"""A plan's steps as launches of the hand-written gfx950 kernels.
+
+Each step of a plan (src/FuryKernel/Program/Plan.hs) is one launch.  A step's
+shape — its anchors, the chains it recomputes, its epilogues, effects and
+stores — picks the kernel and fills its parameters; buffers are named
+logically (``value:``, ``weight:``, ``cache:``, ``ints:``, ``partials:``) and
+the engine binds them to device memory.  A step of a shape no kernel here
+takes is refused with ``LoweringError``: it is never run some other way.
+
+This is pure host logic, the lowering a ``Backend Rocm`` does for the planned
+step's kernels (src/FuryKernel/Backend.hs:29-101).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+from .program.check import CheckedProgram
+from .program.graph import (
+    BF16, CACHE_BF16, F16, F32, SILU, U32, Add, ArgMax, Attend, Gather, GeluMul, Input, KvStore, Linear, Ring, RmsNorm,
+    Rope, ROPE_HALVES, SCache, SInput, SRowInts, SWeight)
+from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
+
+THREADS = 256
+ATTN_SPLIT = 128
+MAX_K = 8192
+
+# GEMV step prologue and epilogue modes (fk_step.h).
+PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = 0, 1, 2, 3, 4
+EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER = 0, 1, 2
+
+
+class LoweringError(ValueError):
+    """A step no kernel of this target takes."""
+
+
+@dataclass(frozen=True)
+class BufferSpec:
+    name: str
+    dtype: str   # "f32", "f16", "bf16", "u32", "u16"
+    count: int   # elements
+
+    @property
+    def nbytes(self) -> int:
+        return self.count * {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2}[self.dtype]
+
+
+@dataclass
+class Launch:
+    step: str
+    entry: str
+    groups: int
+    threads: int
+    bind: dict      # binding name -> logical buffer name (None: unbound)
+    params: dict    # parameter struct field -> value
+    lds_bytes: int = 0
+
+
+@dataclass
+class Lowered:
+    program: object
+    plan: Plan
+    rows: int
+    buffers: dict = field(default_factory=dict)  # name -> BufferSpec
+    launches: list = field(default_factory=list)
+
+    def buffer(self, name: str, dtype: str, count: int) -> str:
+        spec = BufferSpec(name, dtype, count)
+        old = self.buffers.get(name)
+        if old is not None and old != spec:
+            raise LoweringError(f"buffer {name} wanted as {spec} and {old}")
+        self.buffers[name] = spec
+        return name
+
+
+def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1) -> Lowered:
+    """The launches of every step of the plan, in order, for steps of `rows`
+    rows (one, a decode step's)."""
+    if rows != 1:
+        raise LoweringError(f"steps of {rows} rows: the decode kernels take one row a step")
+    out = Lowered(checked.program, plan, rows)
+    low = _StepLowering(out)
+    for step in plan.steps:
+        out.launches.append(low.step(step))
+    return out
+
+
+class _StepLowering:
+    def __init__(self, out: Lowered):
+        self.out = out
+        self.p = out.program
+        self.producer = {v: n for n in self.p.nodes for v in n.outputs}
+
+    # Buffers -------------------------------------------------------------------
+
+    def value(self, v: int) -> str:
+        val = self.p.value(v)
+        prod = self.producer.get(v)
+        if prod is not None and isinstance(prod.op, Input):
+            src = self.p.source(prod.op.source)
+            if isinstance(src.kind, SInput) and src.kind.type not in (F32,):
+                raise LoweringError(f"input {src.name} of {src.kind.type}: the kernels read f32 rows")
+        dtype = "u32" if val.type == U32 else "f32"
+        return self.out.buffer(f"value:{val.name}", dtype, val.shape.width * self.out.rows)
+
+    def weight(self, s: int) -> tuple[str, str]:
+        src = self.p.source(s)
+        if not isinstance(src.kind, SWeight):
+            raise LoweringError(f"{src.name} is not a weight")
+        t = src.kind.type
+        if t not in (F16, F32):
+            raise LoweringError(f"weight {src.name} of {t}: the GEMV steps take f16 and f32 weights")
+        return self.out.buffer(f"weight:{src.name}", t, int(np.prod(src.kind.dims))), t
+
+    def ints(self, s: int) -> str:
+        src = self.p.source(s)
+        if not isinstance(src.kind, SRowInts):
+            raise LoweringError(f"{src.name} is not a row of integers")
+        return self.out.buffer(f"ints:{src.name}", "u32", src.kind.count * self.out.rows)
+
+    def cache(self, s: int) -> tuple[str, Ring, bool]:
+        src = self.p.source(s)
+        if not isinstance(src.kind, SCache):
+            raise LoweringError(f"{src.name} is not a cache")
+        lay = src.kind.layout
+        if not isinstance(lay, Ring):
+            raise LoweringError(f"cache {src.name}: paged caches are not lowered yet")
+        count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
+        bf16 = src.kind.elem == CACHE_BF16
+        return self.out.buffer(f"cache:{src.name}", "bf16" if bf16 else "f16", count), lay, bf16
+
+    def stored_before(self, step: Step, v: int) -> bool:
+        prod = self.producer.get(v)
+        if prod is not None and isinstance(prod.op, Input):
+            return True
+        return any(st.value == v and st.form[0] == "elements" for st in step.reads)
+
+    # Steps -----------------------------------------------------------------------
+
+    def step(self, step: Step) -> Launch:
+        kinds = {w.kind for w in step.work}
+        if STAGE in kinds or LAND in kinds:
+            raise LoweringError(f"{step.name}: staged stores are not lowered yet")
+        anchors = [self.p.node(w.node) for w in step.work if w.kind == ANCHOR]
+        if anchors and all(isinstance(a.op, Linear) for a in anchors):
+            return self.gemv_step(step, anchors)
+        if len(anchors) == 1 and isinstance(anchors[0].op, Attend):
+            return self.attend_step(step, anchors[0])
+        if anchors:
+            raise LoweringError(f"{step.name}: anchors of mixed or unknown kinds")
+        if EFFECT in kinds:
+            return self.store_step(step)
+        if COMBINE in kinds:
+            return self.combine_step(step)
+        return self.light_step(step)
+
+    def recomputes(self, step: Step) -> dict:
+        return {self.p.node(w.node).outputs[0]: self.p.node(w.node) for w in step.work if w.kind == RECOMPUTE}
+
+    def gemv_step(self, step: Step, anchors: list) -> Launch:
+        if len(anchors) > 3:
+            raise LoweringError(f"{step.name}: {len(anchors)} anchors; a GEMV step takes up to 3")
+        xs = {a.op.x for a in anchors}
+        if len(xs) != 1:
+            raise LoweringError(f"{step.name}: anchors of different inputs")
+        x = xs.pop()
+        rec = self.recomputes(step)
+        used: set = set()
+        bind: dict = {k: None for k in ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token",
+                                        "res", "res_table", "res_token", "epi_out")}
+        params: dict = {"eps": 0.0, "factor": 1.0, "gfactor": 1.0, "has_gamma": 0, "table_rows": 1}
+        wtypes = set()
+        k = self.p.value(x).shape.width
+        if k > MAX_K or k % 8:
+            raise LoweringError(f"{step.name}: an input row of {k}, not a multiple of 8 up to {MAX_K}")
+
+        def gather_of(v: int):
+            n = rec.get(v)
+            if n is None or not isinstance(n.op, Gather):
+                return None
+            tsrc = self.p.source(n.op.tokens)
+            if not isinstance(tsrc.kind, SRowInts) or tsrc.kind.count != 1:
+                raise LoweringError(f"{step.name}: a gather of several rows is not lowered yet")
+            used.add(v)
+            tname, ttype = self.weight(n.op.table)
+            params["table_rows"] = self.p.source(n.op.table).kind.dims[0]
+            params["gfactor"] = float(np.float32(n.op.factor))
+            return tname, self.ints(n.op.tokens), ttype
+
+        # Prologue: how the anchors' input row is made.
+        if x not in rec:
+            if not self.stored_before(step, x):
+                raise LoweringError(f"{step.name}: the anchors' input is neither stored nor recomputed")
+            pro = PRO_STORED
+            bind["src"] = self.value(x)
+        else:
+            node = rec[x]
+            used.add(x)
+            op = node.op
+            if isinstance(op, RmsNorm):
+                params["eps"] = float(np.float32(op.eps))
+                params["factor"] = float(np.float32(op.factor))
+                params["seg"] = self.p.value(op.x).shape.segment
+                if op.gamma is not None:
+                    params["has_gamma"] = 1
+                    gname, gt = self.weight(op.gamma)
+                    if gt != F32:
+                        raise LoweringError(f"{step.name}: a gamma of {gt}; the kernels read f32 gammas")
+                    bind["gamma"] = gname
+                g = gather_of(op.x)
+                if g is not None:
+                    pro = PRO_GATHER_RMSNORM
+                    bind["table"], bind["token"], gtype = g
+                    wtypes.add(gtype)
+                elif self.stored_before(step, op.x):
+                    pro = PRO_RMSNORM
+                    bind["src"] = self.value(op.x)
+                else:
+                    raise LoweringError(f"{step.name}: an RMSNorm of a value neither stored nor gathered")
+            elif isinstance(op, Gather):
+                pro = PRO_GATHER
+                bind["table"], bind["token"], gtype = gather_of(x)
+                wtypes.add(gtype)
+            elif isinstance(op, GeluMul) and op.form == SILU:
+                if not (self.stored_before(step, op.a) and self.stored_before(step, op.b)):
+                    raise LoweringError(f"{step.name}: a SiLU·mul of values not stored")
+                pro = PRO_SILU_MUL
+                bind["src"], bind["src2"] = self.value(op.a), self.value(op.b)
+            else:
+                raise LoweringError(f"{step.name}: no prologue computes {type(op).__name__}")
+        params["pro_mode"] = pro
+        params.setdefault("seg", k)
+        if params["seg"] % 4 or k % params["seg"]:
+            raise LoweringError(f"{step.name}: RMSNorm segments of {params['seg']} don't divide {k} in packs of 4")
+
+        # Anchors.
+        rows, first, g = [], [0], 0
+        anchor_outs = {}
+        for j, a in enumerate(anchors):
+            wname, wt = self.weight(a.op.weight)
+            wtypes.add(wt)
+            bind[f"w{j}"] = wname
+            n = self.p.value(a.outputs[0]).shape.width
+            rows.append(n)
+            g += -(-n // (THREADS // 64))
+            first.append(g)
+            anchor_outs[a.outputs[0]] = j
+        if len(wtypes) != 1:
+            raise LoweringError(f"{step.name}: weights of several types {wtypes}")
+        wt = wtypes.pop()
+
+        # Epilogues: one residual add on a single anchor's tile.
+        epis = [self.p.node(w.node) for w in step.work if w.kind == EPILOGUE]
+        epi, epi_value = EPI_NONE, None
+        if epis:
+            if len(epis) != 1 or len(anchors) != 1 or not isinstance(epis[0].op, Add):
+                raise LoweringError(f"{step.name}: epilogues other than one residual add on one anchor")
+            op = epis[0].op
+            tile = anchors[0].outputs[0]
+            if tile not in (op.a, op.b):
+                raise LoweringError(f"{step.name}: an epilogue off its anchor's tile")
+            other = op.b if op.a == tile else op.a
+            g2 = gather_of(other)
+            if g2 is not None:
+                epi = EPI_ADD_GATHER
+                bind["res_table"], bind["res_token"], _ = g2
+            elif self.stored_before(step, other):
+                epi = EPI_ADD_STORED
+                bind["res"] = self.value(other)
+            else:
+                raise LoweringError(f"{step.name}: a residual neither stored nor gathered")
+            epi_value = epis[0].outputs[0]
+        params["epi_mode"] = epi
+        leftover = set(rec) - used
+        if leftover:
+            raise LoweringError(f"{step.name}: recomputes {[self.p.value(v).name for v in leftover]} no kernel takes")
+
+        # Stores: the anchors' tiles, or the epilogue's value.
+        store_tile = 0
+        for st in step.stores:
+            if st.form[0] != "elements":
+                raise LoweringError(f"{step.name}: stores of {st.form}")
+            if st.value in anchor_outs:
+                store_tile = 1
+                bind[f"y{anchor_outs[st.value]}"] = self.value(st.value)
+            elif st.value == epi_value:
+                bind["epi_out"] = self.value(st.value)
+            else:
+                raise LoweringError(f"{step.name}: stores {self.p.value(st.value).name}, which no kernel output holds")
+        if store_tile and len([st for st in step.stores if st.value in anchor_outs]) != len(anchors):
+            raise LoweringError(f"{step.name}: some anchors' tiles stored and some not")
+        if epi != EPI_NONE and bind["epi_out"] is None:
+            raise LoweringError(f"{step.name}: an epilogue whose value isn't stored")
+        params.update(n_anchors=len(anchors), rows=rows + [0] * (3 - len(rows)),
+                      first_group=first + [g] * (4 - len(first)), k=k, store_tile=store_tile)
+        entry = f"fk_step_gemv_{wt}_r1"
+        return Launch(step.name, entry, g, THREADS, bind, params)
+
+    def rope_of(self, step: Step, node, rec: dict) -> Optional[int]:
+        if not isinstance(node.op, Rope):
+            return None
+        spec = node.op.spec
+        if spec.axes != 1 or spec.pairs != ROPE_HALVES:
+            raise LoweringError(f"{step.name}: RoPE of {spec.axes} axes is not lowered yet")
+        return node.op.x
+
+    def store_step(self, step: Step) -> Launch:
+        rec = self.recomputes(step)
+        effects = [self.p.node(w.node) for w in step.work if w.kind == EFFECT]
+        if not 1 <= len(effects) <= 2 or not all(isinstance(e.op, KvStore) for e in effects):
+            raise LoweringError(f"{step.name}: effects other than one or two KV stores")
+        bind = {"x0": None, "x1": None, "c0": None, "c1": None, "position": None, "slot": None}
+        params: dict = {"n_stores": len(effects), "rope": [0, 0], "rotated": 0, "theta": 1.0}
+        layouts, used = set(), set()
+        for j, e in enumerate(effects):
+            at = e.op.at
+            cname, lay, bf16 = self.cache(at.cache)
+            layouts.add((lay.kv_heads, lay.head_dim, lay.length, lay.slots, bf16))
+            bind[f"c{j}"] = cname
+            pos, slot = self.ints(at.positions), self.ints(at.sequences)
+            if bind["position"] not in (None, pos) or bind["slot"] not in (None, slot):
+                raise LoweringError(f"{step.name}: stores at different positions or sequences")
+            bind["position"], bind["slot"] = pos, slot
+            v = e.op.x
+            if v in rec:
+                inner = self.rope_of(step, rec[v], rec)
+                if inner is None or not self.stored_before(step, inner):
+                    raise LoweringError(f"{step.name}: a stored value recomputed by other than RoPE of a stored row")
+                used.add(v)
+                spec = rec[v].op.spec
+                if params["rope"] != [0, 0] and (params["rotated"], params["theta"]) != (
+                        spec.rotated, float(np.float32(spec.theta))):
+                    raise LoweringError(f"{step.name}: two RoPEs of different specs")
+                params["rope"][j] = 1
+                params["rotated"] = spec.rotated
+                params["theta"] = float(np.float32(spec.theta))
+                bind[f"x{j}"] = self.value(inner)
+            elif self.stored_before(step, v):
+                bind[f"x{j}"] = self.value(v)
+            else:
+                raise LoweringError(f"{step.name}: a store of a value neither stored nor recomputed")
+        if len(layouts) != 1:
+            raise LoweringError(f"{step.name}: stores into caches of different layouts")
+        if set(rec) - used:
+            raise LoweringError(f"{step.name}: recomputes no store kernel takes")
+        if step.stores:
+            raise LoweringError(f"{step.name}: a store step that also stores values")
+        kv, d, length, slots, bf16 = layouts.pop()
+        params.update(kv_heads=kv, head_dim=d, length=length, slots=slots, cache_bf16=int(bf16))
+        return Launch(step.name, "fk_step_store", 1, THREADS, bind, params)
+
+    def attend_step(self, step: Step, anchor) -> Launch:
+        op = anchor.op
+        spec = op.spec
+        rec = self.recomputes(step)
+        if spec.reach is not None:
+            raise LoweringError(f"{step.name}: attention with a reach is not lowered yet")
+        if spec.head_dim > 64 or spec.heads // spec.kv_heads > 8:
+            raise LoweringError(f"{step.name}: heads of {spec.head_dim} or groups of {spec.heads // spec.kv_heads}")
+        kname, lay, bf16 = self.cache(op.to.keys)
+        vname, vlay, _ = self.cache(op.to.values)
+        params = {"heads": spec.heads, "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "length": lay.length,
+                  "slots": lay.slots, "rope": 0, "rotated": 0, "theta": 1.0,
+                  "scale": float(np.float32(spec.scale)), "window": spec.window or 0, "cache_bf16": int(bf16)}
+        q = op.q
+        if q in rec:
+            inner = self.rope_of(step, rec[q], rec)
+            if inner is None or not self.stored_before(step, inner):
+                raise LoweringError(f"{step.name}: queries recomputed by other than RoPE of a stored row")
+            params.update(rope=1, rotated=rec[q].op.spec.rotated, theta=float(np.float32(rec[q].op.spec.theta)))
+            qbuf = self.value(inner)
+            if set(rec) - {q}:
+                raise LoweringError(f"{step.name}: recomputes the attention kernel doesn't take")
+        elif self.stored_before(step, q):
+            qbuf = self.value(q)
+        else:
+            raise LoweringError(f"{step.name}: queries neither stored nor recomputed")
+        bound = self.p.source(op.to.positions).kind.bound
+        splits = -(-min(bound, lay.length if spec.window is None else bound) // ATTN_SPLIT)
+        if splits > 4096:
+            raise LoweringError(f"{step.name}: {splits} splits")
+        params["splits"] = splits
+        out = anchor.outputs[0]
+        pname = self.out.buffer(f"partials:{self.p.value(out).name}", "f32",
+                                spec.heads * splits * (spec.head_dim + 2))
+        bind = {"q": qbuf, "kc": kname, "vc": vname, "position": self.ints(op.to.positions),
+                "slot": self.ints(op.to.sequences), "partials": pname}
+        return Launch(step.name, "fk_step_attend", spec.kv_heads * splits, THREADS, bind, params)
+
+    def combine_step(self, step: Step) -> Launch:
+        combines = [self.p.node(w.node) for w in step.work if w.kind == COMBINE]
+        others = [w for w in step.work if w.kind != COMBINE]
+        if len(combines) != 1 or others:
+            raise LoweringError(f"{step.name}: a combine step with other work")
+        node = combines[0]
+        spec = node.op.spec
+        out = node.outputs[0]
+        if [st.value for st in step.stores] != [out]:
+            raise LoweringError(f"{step.name}: a combine that doesn't store its output alone")
+        pname = f"partials:{self.p.value(out).name}"
+        if pname not in self.out.buffers:
+            raise LoweringError(f"{step.name}: combines partials no step stored")
+        splits = self.out.buffers[pname].count // (spec.heads * (spec.head_dim + 2))
+        params = {"heads": spec.heads, "head_dim": spec.head_dim, "splits": splits}
+        total = spec.heads * spec.head_dim
+        return Launch(step.name, "fk_step_combine", -(-total // THREADS), THREADS,
+                      {"partials": pname, "out": self.value(out)}, params)
+
+    def light_step(self, step: Step) -> Launch:
+        rec = [self.p.node(w.node) for w in step.work if w.kind == RECOMPUTE]
+        if len(rec) != 1 or len(step.stores) != 1 or step.stores[0].value != rec[0].outputs[0]:
+            raise LoweringError(f"{step.name}: a light step other than one stored recompute")
+        node = rec[0]
+        op = node.op
+        if isinstance(op, ArgMax) and self.stored_before(step, op.x):
+            n = self.p.value(op.x).shape.width
+            return Launch(step.name, "fk_step_argmax", 1, 1024,
+                          {"x": self.value(op.x), "out": self.value(node.outputs[0])}, {"n": n})
+        if isinstance(op, GeluMul) and op.form == SILU and self.stored_before(step, op.a) and \
+                self.stored_before(step, op.b):
+            n = self.p.value(op.a).shape.width
+            return Launch(step.name, "fk_step_silu_mul", -(-n // THREADS), THREADS,
+                          {"a": self.value(op.a), "b": self.value(op.b), "y": self.value(node.outputs[0])},
+                          {"n": n})
+        raise LoweringError(f"{step.name}: no light kernel recomputes {type(op).__name__}")

@@ -1,0 +1,114 @@
+"""The step programs of a decoder-only transformer, as an engine writes them
+with the program builder: token embedding, per layer RMSNorm → q/k/v →
+RoPE → KV stores into ring caches → attention (GQA) → output projection →
+residual, RMSNorm → gate/up → SiLU·up → down → residual, then the final norm,
+the unembedding and the greedy token.
+
+Sources are named per layer (``l{i}_q_proj``, ``l{i}_k_cache``, ...); the
+engine binds them by name.  Weights are ``out_in`` ([outputs, inputs]).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+from .build import ProgramBuilder, program
+from .graph import CACHE_F16, F16, F32, SILU, AttnSpec, Program, Ring, RopeSpec, whole_row
+
+
+@dataclass(frozen=True)
+class DecoderDims:
+    d_model: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    context: int          # positions a ring cache holds (a sequence's length bound)
+    rope_theta: float = 10000.0
+    eps: float = 1e-5
+    weight_type: str = F16
+    cache_elem: str = CACHE_F16
+    slots: int = 1        # sequences the caches hold
+
+    @property
+    def q_width(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_width(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    def layer_params(self) -> int:
+        d, f = self.d_model, self.ffn
+        return d * self.q_width + 2 * d * self.kv_width + self.q_width * d + 3 * d * f + 2 * d
+
+    def params(self) -> int:
+        return self.layers * self.layer_params() + 2 * self.vocab * self.d_model + self.d_model
+
+
+# The configurations: the tiny f32 decode and the 1B-class f16 decode.
+TINY = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=4, head_dim=16, ffn=256, vocab=256, context=16,
+                   weight_type=F32)
+ONE_B = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000, context=4096)
+
+
+def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
+                 layers: Optional[int] = None) -> Program:
+    """One decode step: ``embed`` gathers the token's row of ``embed`` (else the
+    row ``x`` is an input); outputs ``logits`` and the greedy ``token``."""
+    L = dims.layers if layers is None else layers
+    wt = dims.weight_type
+
+    def body(b: ProgramBuilder):
+        pos = b.row_ints("position", 1, dims.context)
+        slot = b.row_ints("slot", 1, dims.slots)
+        if embed:
+            tokens = b.row_ints("tokens", 1, dims.vocab)
+            table = b.weight("embed", [dims.vocab, dims.d_model], wt)
+            x = b.gather("x0", table, tokens, 1.0)
+        else:
+            x = b.input("x", whole_row(dims.d_model), F32)
+        rope = RopeSpec(dims.rope_theta, dims.head_dim // 2)
+        attn = AttnSpec(dims.heads, dims.kv_heads, dims.head_dim, None, 1.0 / math.sqrt(dims.head_dim))
+        for i in range(L):
+            p = f"l{i}_"
+            g_attn = b.weight(p + "attn_norm", [dims.d_model], F32)
+            wq = b.weight(p + "q_proj", [dims.q_width, dims.d_model], wt)
+            wk = b.weight(p + "k_proj", [dims.kv_width, dims.d_model], wt)
+            wv = b.weight(p + "v_proj", [dims.kv_width, dims.d_model], wt)
+            wo = b.weight(p + "o_proj", [dims.d_model, dims.q_width], wt)
+            g_mlp = b.weight(p + "mlp_norm", [dims.d_model], F32)
+            wg = b.weight(p + "gate_proj", [dims.ffn, dims.d_model], wt)
+            wu = b.weight(p + "up_proj", [dims.ffn, dims.d_model], wt)
+            wd = b.weight(p + "down_proj", [dims.d_model, dims.ffn], wt)
+            kc = b.cache(p + "k_cache", Ring(dims.slots, dims.kv_heads, dims.context, dims.head_dim), dims.cache_elem)
+            vc = b.cache(p + "v_cache", Ring(dims.slots, dims.kv_heads, dims.context, dims.head_dim), dims.cache_elem)
+            a = b.rmsnorm(p + "attn_in", dims.eps, g_attn, 1.0, x)
+            q = b.linear(p + "q", wq, dims.head_dim, a)
+            k = b.linear(p + "k", wk, dims.head_dim, a)
+            v = b.linear(p + "v", wv, dims.head_dim, a)
+            qr = b.rope(p + "q_rot", rope, pos, q)
+            kr = b.rope(p + "k_rot", rope, pos, k)
+            b.kv_store(p + "store_k", kc, pos, slot, kr)
+            b.kv_store(p + "store_v", vc, pos, slot, v)
+            o = b.attend(p + "attn", attn, qr, kc, vc, pos, slot)
+            out = b.linear(p + "o", wo, 0, o)
+            x1 = b.add(p + "x1", x, out)
+            m = b.rmsnorm(p + "mlp_in", dims.eps, g_mlp, 1.0, x1)
+            gate = b.linear(p + "gate", wg, 0, m)
+            up = b.linear(p + "up", wu, 0, m)
+            act = b.gelu_mul(p + "act", gate, up, SILU)
+            down = b.linear(p + "down", wd, 0, act)
+            x = b.add(p + "x2", x1, down)
+        g_final = b.weight("final_norm", [dims.d_model], F32)
+        head = b.weight("lm_head", [dims.vocab, dims.d_model], wt)
+        n = b.rmsnorm("final_normed", dims.eps, g_final, 1.0, x)
+        logits = b.linear("logits", head, 0, n)
+        b.output("logits", logits)
+        b.output("token", b.argmax("token", logits))
+
+    return program(name, body)

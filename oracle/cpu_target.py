@@ -1,0 +1,87 @@
+"""The CPU target of the oracle: a lowered plan's launches run by the C
+restatement, each kernel's loops in the order its gfx950 kernel computes, its
+buffers numpy arrays named as the engine names its device buffers.
+
+TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker of the GPU engine (same launch
+list, same arithmetic, compared bit for bit) and as the CPU baseline.
+
+``width`` is the SIMD width of the reductions: 64 for the gfx950 kernels'
+bits, 32 for the reference CPU target's.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import fkref
+
+NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16}
+TYPE = {"f16": fkref.F16, "f32": fkref.F32}
+
+
+class CpuTarget:
+    def __init__(self, lowered, width: int = 64):
+        self.lowered = lowered
+        self.width = width
+        self.buffers = {name: np.zeros(spec.count, NP[spec.dtype]) for name, spec in lowered.buffers.items()}
+
+    def write(self, name: str, values) -> None:
+        a = np.asarray(values, dtype=self.buffers[name].dtype).reshape(-1)
+        if a.size != self.buffers[name].size:
+            raise ValueError(f"{name}: {a.size} elements for {self.buffers[name].size}")
+        self.buffers[name][:] = a
+
+    def read(self, name: str) -> np.ndarray:
+        return self.buffers[name].copy()
+
+    def _p(self, name):
+        return None if name is None else self.buffers[name].ctypes.data
+
+    def run(self) -> None:
+        for launch in self.lowered.launches:
+            self.run_launch(launch)
+
+    def run_launch(self, launch) -> None:
+        L = fkref.lib()
+        b, p = launch.bind, launch.params
+        e = launch.entry
+        if e.startswith("fk_step_gemv"):
+            wt = "f16" if "_f16_" in e else "f32"
+            n = p["n_anchors"]
+            ws = (ctypes.c_void_p * 3)(*[self._p(b[f"w{j}"]) for j in range(3)])
+            ys = (ctypes.c_void_p * 3)(*[self._p(b[f"y{j}"]) for j in range(3)])
+            rows = (ctypes.c_int * 3)(*p["rows"])
+            tok = int(self.buffers[b["token"]][0]) if b["token"] else 0
+            rtok = int(self.buffers[b["res_token"]][0]) if b["res_token"] else 0
+            st = L.fkref_step_gemv(ws, TYPE[wt], ys, rows, n, p["k"], p["pro_mode"], self._p(b["src"]),
+                                   self._p(b["src2"]), self._p(b["gamma"]) if p["has_gamma"] else None,
+                                   self._p(b["table"] or b["res_table"]), tok, p["table_rows"], p["seg"], p["eps"],
+                                   p["factor"], p["gfactor"], p["epi_mode"], self._p(b["res"]),
+                                   self._p(b["res_table"]), rtok, self._p(b["epi_out"]), launch.threads, self.width)
+        elif e == "fk_step_store":
+            st = L.fkref_step_store(self._p(b["x0"]), self._p(b["x1"]), self._p(b["c0"]), self._p(b["c1"]),
+                                    p["n_stores"], p["rope"][0], p["rope"][1], p["kv_heads"], p["head_dim"],
+                                    p["length"], p["slots"], p["rotated"], p["theta"],
+                                    int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0]),
+                                    p["cache_bf16"])
+        elif e == "fk_step_attend":
+            st = L.fkref_step_attend(self._p(b["q"]), self._p(b["kc"]), self._p(b["vc"]), self._p(b["partials"]),
+                                     p["heads"], p["kv_heads"], p["head_dim"], p["length"], p["slots"],
+                                     p["splits"], p["rope"], p["rotated"], p["theta"], p["scale"], p["window"],
+                                     int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0]),
+                                     p["cache_bf16"])
+        elif e == "fk_step_combine":
+            st = L.fkref_step_combine(self._p(b["partials"]), self._p(b["out"]), p["heads"], p["head_dim"],
+                                      p["splits"])
+        elif e == "fk_step_argmax":
+            self.buffers[b["out"]][0] = L.fkref_argmax(self._p(b["x"]), p["n"])
+            st = 0
+        elif e == "fk_step_silu_mul":
+            st = L.fkref_silu_mul(self._p(b["a"]), self._p(b["b"]), self._p(b["y"]), p["n"])
+        else:
+            raise ValueError(f"the CPU target has no kernel {e}")
+        if st:
+            raise ValueError(f"{launch.step} ({e}): the oracle refused it (status {st})")

@@ -330,3 +330,200 @@ int fkref_softmax(const float *x, float *y, int rows, int n, int threads, int wi
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* The kernels of a planned step                                             */
+
+static float silu_mul_1(float a, float b) {
+  float e = fkref_exp(-a);
+  float d = 1.0f + e;
+  return (a / d) * b;
+}
+
+int fkref_silu_mul(const float *a, const float *b, float *y, int n) {
+  for (int i = 0; i < n; i++) y[i] = silu_mul_1(a[i], b[i]);
+  return 0;
+}
+
+static size_t elem_bytes(int type) {
+  switch (type) {
+    case FKREF_F32: return 4;
+    case FKREF_F16:
+    case FKREF_BF16: return 2;
+    case FKREF_I8: return 1;
+    default: return 0;
+  }
+}
+
+int fkref_step_gemv(const void *const *w, int wtype, float *const *y, const int *rows, int n_anchors, int k,
+                    int pro_mode, const float *src, const float *src2, const float *gamma, const void *table,
+                    uint32_t token, int table_rows, int seg, float eps, float factor, float gfactor, int epi_mode,
+                    const float *res, const void *res_table, uint32_t res_token, float *epi_out, int threads,
+                    int width) {
+  if (n_anchors < 1 || n_anchors > 3 || k <= 0) return -1;
+  float *x = (float *)malloc(sizeof(float) * (size_t)k);
+  if (!x) return -2;
+  uint32_t tok = token < (uint32_t)table_rows ? token : (uint32_t)(table_rows - 1);
+  for (int i = 0; i < k; i++) {
+    switch (pro_mode) {
+      case FKREF_PRO_GATHER:
+      case FKREF_PRO_GATHER_RMSNORM: x[i] = element(table, wtype, (size_t)tok * k + i) * gfactor; break;
+      case FKREF_PRO_SILU_MUL: x[i] = silu_mul_1(src[i], src2[i]); break;
+      default: x[i] = src[i]; break;
+    }
+  }
+  if (pro_mode == FKREF_PRO_RMSNORM || pro_mode == FKREF_PRO_GATHER_RMSNORM) {
+    int st = fkref_rmsnorm(x, gamma, x, 1, k, seg, eps, factor, threads, width, 4);
+    if (st) {
+      free(x);
+      return st;
+    }
+  }
+  const int pack = (int)(16 / elem_bytes(wtype));
+  uint32_t rtok = res_token < (uint32_t)table_rows ? res_token : (uint32_t)(table_rows - 1);
+  for (int a = 0; a < n_anchors; a++) {
+    const int n = rows[a];
+    float *t = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    if (!t) {
+      free(x);
+      return -2;
+    }
+    int st = fkref_gemv(w[a], wtype, x, FKREF_F32, t, NULL, n, k, 1, width, pack, 1);
+    if (st) {
+      free(t);
+      free(x);
+      return st;
+    }
+    for (int r = 0; r < n; r++) {
+      if (y[a]) y[a][r] = t[r];
+      if (epi_mode == FKREF_EPI_ADD_STORED) epi_out[r] = res[r] + t[r];
+      if (epi_mode == FKREF_EPI_ADD_GATHER) epi_out[r] = element(res_table, wtype, (size_t)rtok * n + r) * gfactor + t[r];
+    }
+    free(t);
+  }
+  free(x);
+  return 0;
+}
+
+float fkref_rope_elem(const float *head, int j, int d, int rotated, uint32_t position, float theta) {
+  int half = d / 2;
+  int i = j < half ? j : j - half;
+  if (i >= rotated) return head[j];
+  float freq = (float)pow((double)theta, -(double)(2 * i) / (double)d);
+  float angle = (float)position * freq;
+  float c = (float)cos((double)angle);
+  float s = (float)sin((double)angle);
+  return j < half ? head[j] * c - head[j + half] * s : head[j] * c + head[j - half] * s;
+}
+
+static uint16_t narrow_cache(float v, int bf16) { return bf16 ? fkref_narrow_bf16(v) : fkref_narrow_f16(v); }
+
+static float widen_cache(uint16_t h, int bf16) { return bf16 ? fkref_widen_bf16(h) : fkref_widen_f16(h); }
+
+int fkref_step_store(const float *x0, const float *x1, uint16_t *c0, uint16_t *c1, int n_stores, int rope0,
+                     int rope1, int kv_heads, int head_dim, int length, int slots, int rotated, float theta,
+                     uint32_t position, uint32_t slot, int cache_bf16) {
+  if (slot >= (uint32_t)slots) return 0;
+  const int width = kv_heads * head_dim;
+  for (int st = 0; st < n_stores; st++) {
+    const float *x = st == 0 ? x0 : x1;
+    uint16_t *c = st == 0 ? c0 : c1;
+    int rope = st == 0 ? rope0 : rope1;
+    for (int e = 0; e < width; e++) {
+      int h = e / head_dim;
+      int i = e % head_dim;
+      float v = rope ? fkref_rope_elem(x + (size_t)h * head_dim, i, head_dim, rotated, position, theta) : x[e];
+      size_t at = (((size_t)slot * kv_heads + h) * length + position % (uint32_t)length) * head_dim + i;
+      c[at] = narrow_cache(v, cache_bf16);
+    }
+  }
+  return 0;
+}
+
+#define SPLIT 128
+
+int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
+                      int kv_heads, int head_dim, int length, int slots, int splits, int rope, int rotated,
+                      float theta, float scale, int window, uint32_t position, uint32_t slot, int cache_bf16) {
+  const int group = heads / kv_heads;
+  const int d = head_dim;
+  if (group > 8 || d > 64) return -1;
+  uint32_t s = slot < (uint32_t)slots ? slot : 0;
+  float qs[8 * 64];
+  float wt[8 * SPLIT];
+  float mx[8];
+  uint32_t first = (window && position + 1 > (uint32_t)window) ? position + 1 - (uint32_t)window : 0;
+  for (int g = 0; g < kv_heads; g++) {
+    for (int t = 0; t < splits; t++) {
+      uint32_t lo = (uint32_t)t * SPLIT > first ? (uint32_t)t * SPLIT : first;
+      uint32_t hi = position + 1 < (uint32_t)(t + 1) * SPLIT ? position + 1 : (uint32_t)(t + 1) * SPLIT;
+      int count = hi > lo ? (int)(hi - lo) : 0;
+      for (int e = 0; e < group * d; e++) {
+        const float *head = q + (size_t)(g * group + e / d) * d;
+        qs[e] = rope ? fkref_rope_elem(head, e % d, d, rotated, position, theta) : head[e % d];
+      }
+      size_t base = ((size_t)s * kv_heads + g) * length;
+      for (int h = 0; h < group; h++) {
+        for (int r = 0; r < count; r++) {
+          size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
+          float dot = 0.0f;
+          for (int i = 0; i < d; i++) dot = dot + qs[h * d + i] * widen_cache(kc[at + i], cache_bf16);
+          wt[h * SPLIT + r] = dot * scale;
+        }
+      }
+      for (int h = 0; h < group; h++) {
+        float m = -INFINITY;
+        for (int r = 0; r < count; r++) m = fkref_max(m, wt[h * SPLIT + r]);
+        mx[h] = m;
+      }
+      for (int h = 0; h < group; h++)
+        for (int r = 0; r < count; r++) wt[h * SPLIT + r] = fkref_exp(wt[h * SPLIT + r] - mx[h]);
+      for (int h = 0; h < group; h++) {
+        float *out = partials + ((size_t)(g * group + h) * splits + t) * (d + 2);
+        for (int i = 0; i < d; i++) {
+          float l = 0.0f;
+          float acc = 0.0f;
+          for (int r = 0; r < count; r++) {
+            size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
+            float w = wt[h * SPLIT + r];
+            l = l + w;
+            acc = acc + w * widen_cache(vc[at + i], cache_bf16);
+          }
+          if (i == 0) {
+            out[0] = mx[h];
+            out[1] = l;
+          }
+          out[2 + i] = acc;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+int fkref_step_combine(const float *partials, float *out, int heads, int head_dim, int splits) {
+  const int stride = head_dim + 2;
+  for (int h = 0; h < heads; h++) {
+    const float *ph = partials + (size_t)h * splits * stride;
+    float m = -INFINITY;
+    for (int t = 0; t < splits; t++) m = fkref_max(m, ph[(size_t)t * stride]);
+    for (int i = 0; i < head_dim; i++) {
+      float l = 0.0f;
+      float acc = 0.0f;
+      for (int t = 0; t < splits; t++) {
+        float w = fkref_exp(ph[(size_t)t * stride] - m);
+        l = l + ph[(size_t)t * stride + 1] * w;
+        acc = acc + ph[(size_t)t * stride + 2 + i] * w;
+      }
+      out[(size_t)h * head_dim + i] = acc / l;
+    }
+  }
+  return 0;
+}
+
+uint32_t fkref_argmax(const float *x, int n) {
+  uint32_t best = 0;
+  for (int i = 1; i < n; i++)
+    if (x[i] > x[best]) best = (uint32_t)i;
+  return best;
+}

@@ -74,6 +74,51 @@ int fkref_rmsnorm(const float *x, const float *gamma, float *y, int rows, int wi
  * sum (src/FuryKernel/Reduce.hs:39-47 for the reductions). */
 int fkref_softmax(const float *x, float *y, int rows, int n, int threads, int width, int pack);
 
+/* ------------------------------------------------------------------------ */
+/* The kernels of a planned step, in the orders the gfx950 kernels compute
+ * them (furykernel_amd/csrc/kernels/fk_step.h), their arithmetic the
+ * evaluator's contract (src/FuryKernel/Program/Eval.hs:26-86).               */
+
+/* Prologue and epilogue modes of a GEMV step. */
+enum { FKREF_PRO_STORED = 0, FKREF_PRO_RMSNORM = 1, FKREF_PRO_GATHER = 2, FKREF_PRO_GATHER_RMSNORM = 3,
+       FKREF_PRO_SILU_MUL = 4 };
+enum { FKREF_EPI_NONE = 0, FKREF_EPI_ADD_STORED = 1, FKREF_EPI_ADD_GATHER = 2 };
+
+/* A GEMV step: the anchors' input row made by the prologue (`threads`
+ * threads for the RMSNorm's reduction), then each anchor's rows in the
+ * reference GEMV's order at `width` (split 1, packs of 16 bytes), then the
+ * epilogue.  `w[j]`/`y[j]` per anchor (y[j] NULL: not stored). */
+int fkref_step_gemv(const void *const *w, int wtype, float *const *y, const int *rows, int n_anchors, int k,
+                    int pro_mode, const float *src, const float *src2, const float *gamma, const void *table,
+                    uint32_t token, int table_rows, int seg, float eps, float factor, float gfactor, int epi_mode,
+                    const float *res, const void *res_table, uint32_t res_token, float *epi_out, int threads,
+                    int width);
+
+/* RoPE (NeoX halves) of element j of a head of width d turned by `position`:
+ * freq = theta^(-2i/d) and cos/sin in binary64 rounded once, the angle the
+ * binary32 product position * freq. */
+float fkref_rope_elem(const float *head, int j, int d, int rotated, uint32_t position, float theta);
+
+/* KV stores of one row into ring caches (uint16 elements, f16 or bf16). */
+int fkref_step_store(const float *x0, const float *x1, uint16_t *c0, uint16_t *c1, int n_stores, int rope0,
+                     int rope1, int kv_heads, int head_dim, int length, int slots, int rotated, float theta,
+                     uint32_t position, uint32_t slot, int cache_bf16);
+
+/* Attention partials over splits of 128 positions per KV head:
+ * partials[((h * splits + t) * (d + 2))] = [max, sum, acc[d]]. */
+int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
+                      int kv_heads, int head_dim, int length, int slots, int splits, int rope, int rotated,
+                      float theta, float scale, int window, uint32_t position, uint32_t slot, int cache_bf16);
+
+/* The splits combined once, in split order. */
+int fkref_step_combine(const float *partials, float *out, int heads, int head_dim, int splits);
+
+/* The index of the largest element, ties to the lowest (Eval.hs:681-685). */
+uint32_t fkref_argmax(const float *x, int n);
+
+/* SiLU(a) * b elementwise: a / (1 + exp(-a)) * b, exp binary64's rounded once. */
+int fkref_silu_mul(const float *a, const float *b, float *y, int n);
+
 #ifdef __cplusplus
 }
 #endif

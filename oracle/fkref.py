@@ -47,6 +47,17 @@ def lib() -> ctypes.CDLL:
             "fkref_gemv": (_i, [_vp, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i]),
             "fkref_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, ctypes.c_float, _i, _i, _i]),
             "fkref_softmax": (_i, [_vp, _vp, _i, _i, _i, _i, _i]),
+            "fkref_step_gemv": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, ctypes.c_uint32, _i, _i,
+                                     ctypes.c_float, ctypes.c_float, ctypes.c_float, _i, _vp, _vp, ctypes.c_uint32,
+                                     _vp, _i, _i]),
+            "fkref_rope_elem": (ctypes.c_float, [_vp, _i, _i, _i, ctypes.c_uint32, ctypes.c_float]),
+            "fkref_step_store": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
+                                      ctypes.c_uint32, ctypes.c_uint32, _i]),
+            "fkref_step_attend": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
+                                       ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32, _i]),
+            "fkref_step_combine": (_i, [_vp, _vp, _i, _i, _i]),
+            "fkref_argmax": (ctypes.c_uint32, [_vp, _i]),
+            "fkref_silu_mul": (_i, [_vp, _vp, _vp, _i]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)

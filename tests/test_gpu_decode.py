@@ -1,0 +1,121 @@
+"""A planned decode step on the GPU against the oracle's CPU target running the
+same launch list, bit for bit; and the device state it leaves (KV caches,
+every stored value).  Configurations: the tiny f32 decode and the 1B-class f16
+decode (d_model 2048, 16 layers, 32/8 heads of 64, FFN 8192, vocab 32000,
+context 4096)."""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+from furykernel_amd.decode import DecodeSession
+from furykernel_amd.program.decoder import ONE_B, TINY
+from furykernel_amd.program.plan import PlanOptions
+from oracle.cpu_target import CpuTarget
+
+pytestmark = pytest.mark.gpu
+
+TINY32 = dataclasses.replace(TINY, context=32)
+
+
+def mirror(session: DecodeSession, width: int = 64, cpu: CpuTarget | None = None) -> CpuTarget:
+    """The CPU target with every buffer the device holds (given a CPU target
+    that has the weights already, every other buffer)."""
+    fresh = cpu is None
+    cpu = CpuTarget(session.lowered, width) if fresh else cpu
+    for name in session.lowered.buffers:
+        if fresh or not name.startswith("weight:"):
+            cpu.write(name, session.engine.read(name))
+    return cpu
+
+
+def bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def compare_all(session, cpu, names=None):
+    bad = []
+    for name in names or session.lowered.buffers:
+        g, c = session.engine.read(name), cpu.read(name)
+        if not np.array_equal(bits(g), bits(c)):
+            bad.append((name, int(np.sum(bits(g) != bits(c))), g.size))
+    return bad
+
+
+@pytest.mark.parametrize("position", [0, 16, 31])
+def test_tiny_decode_step_bit_exact(device, kernels, position):
+    s = DecodeSession(device, kernels, TINY32, PlanOptions(), embed=False)
+    try:
+        s.init_synthetic()
+        s.set_position(position)
+        cpu = mirror(s)
+        print(f"tiny decode at position {position}: {len(s.lowered.launches)} launches", flush=True)
+        s.step()
+        device.sync()
+        cpu.run()
+        assert compare_all(s, cpu) == []
+    finally:
+        s.close()
+
+
+def test_tiny_decode_graph_replays_agree_with_eager(device, kernels):
+    s = DecodeSession(device, kernels, TINY32, PlanOptions(store_gelus=True), embed=False)
+    try:
+        s.init_synthetic()
+        s.set_position(5)
+        s.step()
+        device.sync()
+        eager = s.logits()
+        g = s.graph()
+        for _ in range(3):
+            g.replay()
+            device.sync()
+            assert np.array_equal(bits(s.logits()), bits(eager))
+        g.destroy()
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("layers", [2])
+def test_1b_decode_step_bit_exact(device, kernels, layers):
+    """The 1B-class step's real shapes (2 of its 16 layers, and the head) at the
+    full context: position 4095 reads all 4096 positions of every cache."""
+    s = DecodeSession(device, kernels, ONE_B, PlanOptions(), embed=True, layers=layers)
+    try:
+        s.init_synthetic()
+        s.set_position(4095, token=31999)
+        cpu = mirror(s)
+        print(f"1B decode ({layers} layers) at position 4095: {len(s.lowered.launches)} launches", flush=True)
+        s.step()
+        device.sync()
+        cpu.run()
+        skip = {n for n in s.lowered.buffers if n.startswith("weight:")}
+        assert compare_all(s, cpu, [n for n in s.lowered.buffers if n not in skip]) == []
+    finally:
+        s.close()
+
+
+def test_1b_full_decode_greedy_tokens_via_graph(device, kernels):
+    """All 16 layers: three greedy tokens by graph replay, each step's token the
+    CPU target's for the same state."""
+    s = DecodeSession(device, kernels, ONE_B, PlanOptions(), embed=True)
+    try:
+        s.init_synthetic()
+        s.set_position(4000, token=7)
+        g = s.graph()
+        cpu = None
+        for i in range(3):
+            cpu = mirror(s, cpu=cpu)
+            print(f"1B decode token {i}", flush=True)
+            g.replay()
+            device.sync()
+            cpu.run()
+            assert s.token() == int(cpu.read("value:token")[0])
+            assert np.array_equal(bits(s.logits()), bits(cpu.read("value:logits")))
+            assert int(s.engine.read("ints:tokens")[0]) == s.token()
+            assert int(s.engine.read("ints:position")[0]) == 4001 + i
+        g.destroy()
+    finally:
+        s.close()
