@@ -17,7 +17,8 @@
 // Arithmetic follows the evaluator's contract (src/FuryKernel/Program/Eval.hs:
 // 26-86) in fixed orders, which the oracle restates in C operation for
 // operation: GEMV rows in the reference GEMV's order, RMSNorm in tgReduceSum's,
-// exp/sin/cos/pow in binary64 rounded once.
+// exp and rsqrt in binary64 rounded once, RoPE's cosines and sines from a
+// table of binary64 values rounded once.
 #pragma once
 
 #include "fk_common.h"
@@ -45,7 +46,7 @@ enum : uint32_t {
 struct fk_step_gemv_params {
   uint32_t n_anchors;  // 1 to 3
   uint32_t rows[3];    // each anchor's outputs
-  uint32_t first_group[4];  // anchor j's threadgroups are [first_group[j], first_group[j+1])
+  uint32_t first_group[4];  // anchor j's row blocks are [first_group[j], first_group[j+1])
   uint32_t k;          // the input row's width
   uint32_t pro_mode;
   uint32_t seg;        // RMSNorm's segment (k, one segment)
@@ -103,13 +104,122 @@ __device__ __forceinline__ float silu_mul(float a, float b) {
   return (a / d) * b;
 }
 
+// An anchor's pointer or count by index, without indexing an array: a
+// dynamically indexed array of kernel pointers would lose their address space
+// (its loads would become flat loads, which wait with LDS traffic).
+template <typename T>
+__device__ __forceinline__ T pick3(uint32_t a, T x0, T x1, T x2) {
+  return a == 0 ? x0 : (a == 1 ? x1 : x2);
+}
+
+// Which anchor row r of the numbered rows belongs to.
+__device__ __forceinline__ uint32_t anchor_of(uint32_t r, const fk_step_gemv_params &p) {
+  return (p.n_anchors > 1 && r >= p.first_group[1] ? 1u : 0u) + (p.n_anchors > 2 && r >= p.first_group[2] ? 1u : 0u);
+}
+
 }  // namespace fk
 
-// One wavefront's rows of a GEMV step: R rows of one anchor, x in LDS.  The
-// first PF packs of every row are loaded before the prologue runs (weights
-// don't depend on it), so the prologue hides their latency.
+// The prologue of a GEMV step in two halves, so that its loads are issued
+// before the weights' and its arithmetic runs while the weights stream in
+// (the wave waits for loads in the order it issued them).  Thread t holds
+// packs t, t + T, ... of the row (NPK of them at most, 4 elements each), the
+// order RMSNorm's sum of squares takes them in.
+template <typename WT, int NPK>
+struct Prologue {
+  float4 x[NPK];
+  float4 x2[NPK];
+  float4 g[NPK];
+
+  __device__ __forceinline__ void load(const float *__restrict__ src, const float *__restrict__ src2,
+                                       const float *__restrict__ gamma, const WT *__restrict__ table,
+                                       const uint32_t *__restrict__ token, const fk_step_gemv_params &p) {
+    const uint32_t packs = p.k / 4;
+    const bool gather = p.pro_mode == FK_PRO_GATHER || p.pro_mode == FK_PRO_GATHER_RMSNORM;
+    const uint32_t tok = gather ? min(token[0], p.table_rows - 1) : 0;
+#pragma unroll
+    for (int m = 0; m < NPK; m++) {
+      const uint32_t j = threadIdx.x + m * blockDim.x;
+      const bool in = j < packs;
+      if (gather) {
+        const WT *row = table + (size_t)tok * p.k + 4 * j;
+        x[m] = in ? make_float4((float)row[0], (float)row[1], (float)row[2], (float)row[3]) : make_float4(0, 0, 0, 0);
+      } else {
+        x[m] = in ? reinterpret_cast<const float4 *>(src)[j] : make_float4(0, 0, 0, 0);
+      }
+      x2[m] = (in && p.pro_mode == FK_PRO_SILU_MUL) ? reinterpret_cast<const float4 *>(src2)[j]
+                                                     : make_float4(0, 0, 0, 0);
+      g[m] = (in && p.has_gamma && (p.pro_mode == FK_PRO_RMSNORM || p.pro_mode == FK_PRO_GATHER_RMSNORM))
+                 ? reinterpret_cast<const float4 *>(gamma)[j % (p.seg / 4)]
+                 : make_float4(1, 1, 1, 1);
+    }
+  }
+
+  // The anchors' input row into `xs`: gathered rows times the factor, SiLU·mul,
+  // or RMSNorm (one segment, the row) of them; a barrier after.
+  __device__ __forceinline__ void finish(float *xs, float *slots, const fk_step_gemv_params &p) {
+    const uint32_t packs = p.k / 4;
+    const bool gather = p.pro_mode == FK_PRO_GATHER || p.pro_mode == FK_PRO_GATHER_RMSNORM;
+#pragma unroll
+    for (int m = 0; m < NPK; m++) {
+      if (gather) {
+        x[m].x = x[m].x * p.gfactor;
+        x[m].y = x[m].y * p.gfactor;
+        x[m].z = x[m].z * p.gfactor;
+        x[m].w = x[m].w * p.gfactor;
+      } else if (p.pro_mode == FK_PRO_SILU_MUL) {
+        x[m] = make_float4(fk::silu_mul(x[m].x, x2[m].x), fk::silu_mul(x[m].y, x2[m].y),
+                           fk::silu_mul(x[m].z, x2[m].z), fk::silu_mul(x[m].w, x2[m].w));
+      }
+    }
+    if (p.pro_mode == FK_PRO_RMSNORM || p.pro_mode == FK_PRO_GATHER_RMSNORM) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int m = 0; m < NPK; m++) {
+        if (threadIdx.x + m * blockDim.x < packs) {
+          acc = acc + x[m].x * x[m].x;
+          acc = acc + x[m].y * x[m].y;
+          acc = acc + x[m].z * x[m].z;
+          acc = acc + x[m].w * x[m].w;
+        }
+      }
+      const float total = fk::block_reduce<false>(acc, slots);
+      const float scale = fk::rsqrt_once(total / (float)p.seg + p.eps);
+#pragma unroll
+      for (int m = 0; m < NPK; m++) {
+        float o[4] = {x[m].x * scale, x[m].y * scale, x[m].z * scale, x[m].w * scale};
+        if (p.has_gamma) {
+          o[0] = o[0] * g[m].x;
+          o[1] = o[1] * g[m].y;
+          o[2] = o[2] * g[m].z;
+          o[3] = o[3] * g[m].w;
+        }
+        if (p.factor != 1.0f) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) o[e] = o[e] * p.factor;
+        }
+        x[m] = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NPK; m++) {
+      const uint32_t j = threadIdx.x + m * blockDim.x;
+      if (j < packs) reinterpret_cast<float4 *>(xs)[j] = x[m];
+    }
+    __syncthreads();
+  }
+};
+
+// A GEMV step's threadgroups are persistent: the grid is what fits on the
+// device at once, each threadgroup makes the anchors' input row once (its
+// prologue) and its wavefronts then take row blocks of R rows in turn, block
+// b, b + (all wavefronts), ...  The anchors' rows are numbered one after
+// another.  While a wavefront computes a block, the first PF packs of its next
+// block are already loading; its first block's packs load before the prologue
+// runs, since weights don't depend on it.
 template <typename WT, int P, int R, int PF>
-__device__ __forceinline__ void step_gemv_body(const WT *const *__restrict__ ws, float *const *__restrict__ ys,
+__device__ __forceinline__ void step_gemv_body(const WT *__restrict__ w0, const WT *__restrict__ w1,
+                                               const WT *__restrict__ w2, float *__restrict__ y0,
+                                               float *__restrict__ y1, float *__restrict__ y2,
                                                const float *__restrict__ src, const float *__restrict__ src2,
                                                const float *__restrict__ gamma, const WT *__restrict__ table,
                                                const uint32_t *__restrict__ token, const float *__restrict__ res,
@@ -118,187 +228,338 @@ __device__ __forceinline__ void step_gemv_body(const WT *const *__restrict__ ws,
   __shared__ float xs[FK_STEP_MAX_K];
   __shared__ float slots[16];
   constexpr int C = P / 4;
-  // Which anchor and rows this threadgroup takes.
-  uint32_t a = 0;
-  while (a + 1 < p.n_anchors && blockIdx.x >= p.first_group[a + 1]) a++;
-  const uint32_t n = p.rows[a];
+  constexpr int U = P * sizeof(WT) / 16;
   const uint32_t k = p.k;
   const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
-  const uint32_t wave = threadIdx.x / FK_WAVE;
   const uint32_t waves = blockDim.x / FK_WAVE;
-  const uint32_t row0 = ((blockIdx.x - p.first_group[a]) * waves + wave) * R;
-  const bool active = row0 < n;
-  const WT *w = ws[a];
+  const uint32_t total_waves = gridDim.x * waves;
   const uint32_t packs = k / P;
-  const WT *wr[R];
-#pragma unroll
-  for (int q = 0; q < R; q++) wr[q] = w + (size_t)min(row0 + q, n - 1) * k;
+  // Row blocks: anchor a's rows are blocks [first_group[a], first_group[a + 1]).
+  const uint32_t blocks = p.first_group[p.n_anchors];
 
-  // Prefetch: the first PF packs of each row, as 16-byte words.
-  constexpr int U = P * sizeof(WT) / 16;
-  uint4 pre[PF][R][U];
+  // Where block b's rows are: its anchor, and the W rows of its R rows.
+  auto locate = [&](uint32_t b, uint32_t &a, uint32_t &row0, const WT *(&wr)[R]) {
+    a = fk::anchor_of(b, p);
+    row0 = (b - fk::pick3(a, p.first_group[0], p.first_group[1], p.first_group[2])) * R;
+    const uint32_t n = fk::pick3(a, p.rows[0], p.rows[1], p.rows[2]);
+    const WT *wa = fk::pick3(a, w0, w1, w2);
 #pragma unroll
-  for (int it = 0; it < PF; it++) {
-    const uint32_t j = lane + it * FK_WAVE;
+    for (int q = 0; q < R; q++) wr[q] = wa + (size_t)min(row0 + q, n - 1) * k;
+  };
+  auto prefetch = [&](const WT *(&wr)[R], uint4 (&pre)[PF][R][U], bool live) {
+#pragma unroll
+    for (int it = 0; it < PF; it++) {
+      const uint32_t j = lane + it * FK_WAVE;
+#pragma unroll
+      for (int q = 0; q < R; q++)
+#pragma unroll
+        for (int u = 0; u < U; u++)
+          pre[it][q][u] = (live && j < packs) ? reinterpret_cast<const uint4 *>(wr[q] + (size_t)j * P)[u]
+                                              : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  uint32_t b = blockIdx.x * waves + threadIdx.x / FK_WAVE;
+  uint32_t a, row0;
+  const WT *wr[R];
+  uint4 cur[PF][R][U];
+  Prologue<WT, FK_STEP_MAX_K / (4 * 512)> pro;
+  pro.load(src, src2, gamma, table, token, p);
+  locate(b < blocks ? b : 0, a, row0, wr);
+  prefetch(wr, cur, b < blocks);
+  pro.finish(xs, slots, p);
+  const uint32_t rtok = (p.epi_mode == FK_EPI_ADD_GATHER) ? min(res_token[0], p.table_rows - 1) : 0;
+
+  for (; b < blocks; b += total_waves) {
+    const uint32_t nb = b + total_waves;
+    uint32_t na = 0, nrow0 = 0;
+    const WT *nwr[R];
+    uint4 nxt[PF][R][U];
+    locate(nb < blocks ? nb : b, na, nrow0, nwr);
+    prefetch(nwr, nxt, nb < blocks);
+
+    // The block's rows, in the reference GEMV's order.
+    float acc[R][C];
 #pragma unroll
     for (int q = 0; q < R; q++)
 #pragma unroll
-      for (int u = 0; u < U; u++)
-        pre[it][q][u] = (active && j < packs) ? reinterpret_cast<const uint4 *>(wr[q] + (size_t)j * P)[u]
-                                              : make_uint4(0, 0, 0, 0);
-  }
-
-  // Prologue: the anchors' input row, into LDS.
-  const uint32_t tok =
-      (p.pro_mode == FK_PRO_GATHER || p.pro_mode == FK_PRO_GATHER_RMSNORM) ? min(token[0], p.table_rows - 1) : 0;
-  for (uint32_t i = threadIdx.x; i < k; i += blockDim.x) {
-    float v;
-    switch (p.pro_mode) {
-      case FK_PRO_GATHER:
-      case FK_PRO_GATHER_RMSNORM: v = fk::gathered(table, tok, k, i, p.gfactor); break;
-      case FK_PRO_SILU_MUL: v = fk::silu_mul(src[i], src2[i]); break;
-      default: v = src[i]; break;
+      for (int c = 0; c < C; c++) acc[q][c] = 0.0f;
+    auto consume = [&](uint32_t j, const uint4 (&wv4)[R][U]) {
+      float xv[P];
+#pragma unroll
+      for (int e = 0; e < P; e++) xv[e] = xs[j * P + e];
+#pragma unroll
+      for (int q = 0; q < R; q++) {
+        float wv[P];
+        fk::unpack<P>(wv4[q], wv, WT{});
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+          float p0 = xv[4 * c] * wv[4 * c];
+          float p1 = xv[4 * c + 1] * wv[4 * c + 1];
+          float p2 = xv[4 * c + 2] * wv[4 * c + 2];
+          float p3 = xv[4 * c + 3] * wv[4 * c + 3];
+          acc[q][c] = acc[q][c] + ((p0 + p1) + (p2 + p3));
+        }
+      }
+    };
+#pragma unroll
+    for (int it = 0; it < PF; it++) {
+      const uint32_t j = lane + it * FK_WAVE;
+      if (j < packs) consume(j, cur[it]);
     }
-    xs[i] = v;
-  }
-  __syncthreads();
-  if (p.pro_mode == FK_PRO_RMSNORM || p.pro_mode == FK_PRO_GATHER_RMSNORM)
-    fk::rmsnorm_lds(xs, k, p.seg, p.eps, p.factor, p.has_gamma ? gamma : nullptr, slots);
-  if (!active) return;
-
-  // The rows, in the reference GEMV's order.
-  float acc[R][C];
+#pragma unroll 4
+    for (uint32_t j = lane + PF * FK_WAVE; j < packs; j += FK_WAVE) {
+      uint4 wv4[R][U];
 #pragma unroll
-  for (int q = 0; q < R; q++)
+      for (int q = 0; q < R; q++)
 #pragma unroll
-    for (int c = 0; c < C; c++) acc[q][c] = 0.0f;
-  auto consume = [&](uint32_t j, const uint4 (&wv4)[R][U]) {
-    float xv[P];
-#pragma unroll
-    for (int e = 0; e < P; e++) xv[e] = xs[j * P + e];
+        for (int u = 0; u < U; u++) wv4[q][u] = reinterpret_cast<const uint4 *>(wr[q] + (size_t)j * P)[u];
+      consume(j, wv4);
+    }
+    const uint32_t n = fk::pick3(a, p.rows[0], p.rows[1], p.rows[2]);
+    float *ya = fk::pick3(a, y0, y1, y2);
 #pragma unroll
     for (int q = 0; q < R; q++) {
+      float t = acc[q][0];
+#pragma unroll
+      for (int c = 1; c < C; c++) t = t + acc[q][c];
+      t = fk::wave_sum(t);
+      const uint32_t row = row0 + q;
+      if (lane == 0 && row < n) {
+        if (p.store_tile) ya[row] = t;
+        if (p.epi_mode == FK_EPI_ADD_STORED) {
+          epi_out[row] = res[row] + t;
+        } else if (p.epi_mode == FK_EPI_ADD_GATHER) {
+          epi_out[row] = fk::gathered(res_table, rtok, n, row, p.gfactor) + t;
+        }
+      }
+    }
+    a = na;
+    row0 = nrow0;
+#pragma unroll
+    for (int q = 0; q < R; q++) wr[q] = nwr[q];
+#pragma unroll
+    for (int it = 0; it < PF; it++)
+#pragma unroll
+      for (int q = 0; q < R; q++)
+#pragma unroll
+        for (int u = 0; u < U; u++) cur[it][q][u] = nxt[it][q][u];
+  }
+}
+
+// Buffers in binding order, then the parameter struct.
+#define FK_STEP_GEMV_ENTRY(NAME, WT, P, R, PF)                                                                      \
+  extern "C" __global__ void __launch_bounds__(512)                                                                 \
+      NAME(const WT *__restrict__ w0, const WT *__restrict__ w1, const WT *__restrict__ w2, float *__restrict__ y0, \
+           float *__restrict__ y1, float *__restrict__ y2, const float *__restrict__ src,                          \
+           const float *__restrict__ src2, const float *__restrict__ gamma, const WT *__restrict__ table,           \
+           const uint32_t *__restrict__ token, const float *__restrict__ res, const WT *__restrict__ res_table,     \
+           const uint32_t *__restrict__ res_token, float *__restrict__ epi_out, fk_step_gemv_params p) {           \
+    step_gemv_body<WT, P, R, PF>(w0, w1, w2, y0, y1, y2, src, src2, gamma, table, token, res, res_table, res_token, \
+                                 epi_out, p);                                                                       \
+  }
+
+FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r1, _Float16, 8, 1, 4)
+FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r2, _Float16, 8, 2, 4)
+FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r4, _Float16, 8, 4, 2)
+FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r1p8, _Float16, 8, 1, 8)
+FK_STEP_GEMV_ENTRY(fk_step_gemv_f32_r1, float, 4, 1, 4)
+
+// GEMV steps of a known input width: every row's weights in registers.
+//
+// A wavefront takes ROWS consecutive rows (numbered across the anchors) and
+// the input width is 64 * P * PPL, so lane l's packs are l, l + 64, ... (PPL
+// of them) of each row.  The wavefront issues all ROWS * PPL of its 16-byte
+// weight loads when it starts, before the prologue: the whole matrix is
+// requested at once and the prologue runs under the loads.  The input row
+// lives in dynamic LDS (k floats); with PPL <= 4 each lane keeps its x packs
+// in registers for all its rows.  Each row's lane totals are reduced across
+// the wavefront together at the end, ROWS independent pairwise trees.
+// Same order, same bits as step_gemv_body.
+template <typename WT, int P, int ROWS, int PPL>
+__device__ __forceinline__ void step_gemv_resident(const WT *__restrict__ w0, const WT *__restrict__ w1,
+                                                   const WT *__restrict__ w2, float *__restrict__ y0,
+                                                   float *__restrict__ y1, float *__restrict__ y2,
+                                                   const float *__restrict__ src, const float *__restrict__ src2,
+                                                   const float *__restrict__ gamma, const WT *__restrict__ table,
+                                                   const uint32_t *__restrict__ token, const float *__restrict__ res,
+                                                   const WT *__restrict__ res_table,
+                                                   const uint32_t *__restrict__ res_token, float *__restrict__ epi_out,
+                                                   const fk_step_gemv_params &p) {
+  extern __shared__ float xs[];
+  __shared__ float slots[16];
+  constexpr int C = P / 4;
+  constexpr int U = P * sizeof(WT) / 16;
+  constexpr bool XREG = PPL <= 4;
+  const uint32_t k = p.k;
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+  const uint32_t total = p.first_group[p.n_anchors];  // rows, all anchors
+  const uint32_t row_first = (blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * ROWS;
+
+  Prologue<WT, FK_STEP_MAX_K / (4 * 512)> pro;
+  pro.load(src, src2, gamma, table, token, p);
+  uint32_t anc[ROWS], lrow[ROWS];
+  uint4 w[ROWS][PPL][U];
+#pragma unroll
+  for (int q = 0; q < ROWS; q++) {
+    const uint32_t r = row_first + q;
+    const uint32_t a = fk::anchor_of(r, p);
+    anc[q] = a;
+    lrow[q] = r - fk::pick3(a, p.first_group[0], p.first_group[1], p.first_group[2]);
+    const bool live = r < total;
+    const WT *wr = fk::pick3(a, w0, w1, w2) + (size_t)(live ? lrow[q] : 0) * k;
+#pragma unroll
+    for (int it = 0; it < PPL; it++)
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        w[q][it][u] = live ? reinterpret_cast<const uint4 *>(wr + (size_t)(lane + it * FK_WAVE) * P)[u]
+                           : make_uint4(0, 0, 0, 0);
+  }
+
+  pro.finish(xs, slots, p);
+  if (row_first >= total) return;
+
+  float xr[XREG ? PPL : 1][XREG ? P : 1];
+  if (XREG) {
+#pragma unroll
+    for (int it = 0; it < PPL; it++)
+#pragma unroll
+      for (int e = 0; e < P; e++) xr[XREG ? it : 0][XREG ? e : 0] = xs[(lane + it * FK_WAVE) * P + e];
+  }
+  float t[ROWS];
+#pragma unroll
+  for (int q = 0; q < ROWS; q++) {
+    float acc[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) acc[c] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < PPL; it++) {
+      float xv[P];
+      if (XREG) {
+#pragma unroll
+        for (int e = 0; e < P; e++) xv[e] = xr[XREG ? it : 0][XREG ? e : 0];
+      } else {
+#pragma unroll
+        for (int e = 0; e < P; e++) xv[e] = xs[(lane + it * FK_WAVE) * P + e];
+      }
       float wv[P];
-      fk::unpack<P>(wv4[q], wv, WT{});
+      fk::unpack<P>(w[q][it], wv, WT{});
 #pragma unroll
       for (int c = 0; c < C; c++) {
         float p0 = xv[4 * c] * wv[4 * c];
         float p1 = xv[4 * c + 1] * wv[4 * c + 1];
         float p2 = xv[4 * c + 2] * wv[4 * c + 2];
         float p3 = xv[4 * c + 3] * wv[4 * c + 3];
-        acc[q][c] = acc[q][c] + ((p0 + p1) + (p2 + p3));
+        acc[c] = acc[c] + ((p0 + p1) + (p2 + p3));
       }
     }
-  };
+    float tq = acc[0];
 #pragma unroll
-  for (int it = 0; it < PF; it++) {
-    const uint32_t j = lane + it * FK_WAVE;
-    if (j < packs) consume(j, pre[it]);
+    for (int c = 1; c < C; c++) tq = tq + acc[c];
+    t[q] = tq;
   }
-#pragma unroll 4
-  for (uint32_t j = lane + PF * FK_WAVE; j < packs; j += FK_WAVE) {
-    uint4 wv4[R][U];
+  // The wavefront sums of all ROWS rows, level by level.
 #pragma unroll
-    for (int q = 0; q < R; q++)
+  for (int m = 1; m < FK_WAVE; m <<= 1) {
+    float o[ROWS];
 #pragma unroll
-      for (int u = 0; u < U; u++)
-        wv4[q][u] = reinterpret_cast<const uint4 *>(wr[q] + (size_t)j * P)[u];
-    consume(j, wv4);
+    for (int q = 0; q < ROWS; q++) o[q] = __shfl_xor(t[q], m);
+#pragma unroll
+    for (int q = 0; q < ROWS; q++) t[q] = t[q] + o[q];
   }
-
-  const uint32_t rtok = (p.epi_mode == FK_EPI_ADD_GATHER) ? min(res_token[0], p.table_rows - 1) : 0;
+  if (lane == 0) {
+    const uint32_t rtok = (p.epi_mode == FK_EPI_ADD_GATHER) ? min(res_token[0], p.table_rows - 1) : 0;
 #pragma unroll
-  for (int q = 0; q < R; q++) {
-    float t = acc[q][0];
-#pragma unroll
-    for (int c = 1; c < C; c++) t = t + acc[q][c];
-    t = fk::wave_sum(t);
-    const uint32_t row = row0 + q;
-    if (lane == 0 && row < n) {
-      if (p.store_tile) ys[a][row] = t;
+    for (int q = 0; q < ROWS; q++) {
+      if (row_first + q >= total) break;
+      const uint32_t a = anc[q];
+      const uint32_t row = lrow[q];
+      if (p.store_tile) fk::pick3(a, y0, y1, y2)[row] = t[q];
       if (p.epi_mode == FK_EPI_ADD_STORED) {
-        epi_out[row] = res[row] + t;
+        epi_out[row] = res[row] + t[q];
       } else if (p.epi_mode == FK_EPI_ADD_GATHER) {
-        epi_out[row] = fk::gathered(res_table, rtok, n, row, p.gfactor) + t;
+        epi_out[row] = fk::gathered(res_table, rtok, fk::pick3(a, p.rows[0], p.rows[1], p.rows[2]), row, p.gfactor) + t[q];
       }
     }
   }
 }
 
-// Buffers in binding order, then the parameter struct.
-#define FK_STEP_GEMV_ENTRY(NAME, WT, P, R, PF)                                                                      \
-  extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)                                                     \
+#define FK_STEP_GEMV_RESIDENT(NAME, WT, P, ROWS, PPL)                                                             \
+  extern "C" __global__ void __launch_bounds__(512)                                                                 \
       NAME(const WT *__restrict__ w0, const WT *__restrict__ w1, const WT *__restrict__ w2, float *__restrict__ y0, \
            float *__restrict__ y1, float *__restrict__ y2, const float *__restrict__ src,                          \
            const float *__restrict__ src2, const float *__restrict__ gamma, const WT *__restrict__ table,           \
            const uint32_t *__restrict__ token, const float *__restrict__ res, const WT *__restrict__ res_table,     \
            const uint32_t *__restrict__ res_token, float *__restrict__ epi_out, fk_step_gemv_params p) {           \
-    const WT *ws[3] = {w0, w1, w2};                                                                                 \
-    float *ys[3] = {y0, y1, y2};                                                                                    \
-    step_gemv_body<WT, P, R, PF>(ws, ys, src, src2, gamma, table, token, res, res_table, res_token, epi_out, p);   \
+    step_gemv_resident<WT, P, ROWS, PPL>(w0, w1, w2, y0, y1, y2, src, src2, gamma, table, token, res, res_table,   \
+                                         res_token, epi_out, p);                                                    \
   }
 
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r1, _Float16, 8, 1, 4)
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r2, _Float16, 8, 2, 4)
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f32_r1, float, 4, 1, 4)
+// f16 weights, k = 2048 (PPL 4) and k = 8192 (PPL 16).
+FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r1, _Float16, 8, 1, 4)
+FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r2, _Float16, 8, 2, 4)
+FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r4, _Float16, 8, 4, 4)
+FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r8, _Float16, 8, 8, 4)
+FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k8192_r1, _Float16, 8, 1, 16)
+FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k8192_r2, _Float16, 8, 2, 16)
 
 // KV stores ----------------------------------------------------------------
 
-struct fk_step_store_params {
-  uint32_t n_stores;    // 1 or 2
-  uint32_t rope[2];     // store j's value is RoPE'd first (its source is k)
-  uint32_t kv_heads;
-  uint32_t head_dim;
-  uint32_t length;      // the ring's positions
-  uint32_t slots;       // the ring's sequences
-  uint32_t rotated;     // pairs turned
-  float theta;
-  uint32_t cache_bf16;  // the caches round to bf16 (else f16)
-};
-
 namespace fk {
 
-// The frequency of pair i of a head of width d: theta^(-2i/d) in binary64,
-// rounded once.
-__device__ __forceinline__ float rope_freq(float theta, uint32_t i, uint32_t d) {
-  return (float)::pow((double)theta, -(double)(2 * i) / (double)d);
-}
-
-// Element j of a head turned by `position` (NeoX halves, Graph.hs:209-221):
-// angle = position * freq in binary32, its cosine and sine binary64's rounded
-// once; (x_j c - x_{j+d/2} s) below the half, (x_j c + x_{j-d/2} s) above.
+// Element j of a head of width d turned by RoPE (NeoX halves, Graph.hs:209-221),
+// pair i's cosine and sine from `cs` (the position's row of the RoPE table:
+// cos, sin of the binary32 angle position * theta^(-2i/d), each binary64's
+// rounded once): (x_j c - x_{j+d/2} s) below the half, (x_j c + x_{j-d/2} s)
+// above; pairs past `rotated` stay.
 __device__ __forceinline__ float rope_elem(const float *head, uint32_t j, uint32_t d, uint32_t rotated,
-                                           uint32_t position, float theta) {
+                                           const float *__restrict__ cs) {
   const uint32_t half = d / 2;
   const uint32_t i = j < half ? j : j - half;
   if (i >= rotated) return head[j];
-  const float angle = (float)position * rope_freq(theta, i, d);
-  const float c = (float)::cos((double)angle);
-  const float s = (float)::sin((double)angle);
+  const float c = cs[2 * i];
+  const float s = cs[2 * i + 1];
   return j < half ? head[j] * c - head[j + half] * s : head[j] * c + head[j - half] * s;
 }
 
 __device__ __forceinline__ uint16_t narrow_cache(float v, bool bf16) { return bf16 ? narrow_bf16(v) : narrow_f16(v); }
 
+__device__ __forceinline__ float widen_cache(uint16_t h, bool bf16) {
+  return bf16 ? __uint_as_float((uint32_t)h << 16) : widen_f16(h);
+}
+
 }  // namespace fk
 
-// One threadgroup: every element of one row's kv heads, for each store.
+struct fk_step_store_params {
+  uint32_t n_stores;    // 1 or 2
+  uint32_t rope[2];     // store j's value is RoPE'd first
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t length;      // the ring's positions
+  uint32_t slots;       // the ring's sequences
+  uint32_t rotated;     // pairs turned
+  uint32_t rope_rows;   // positions the RoPE table holds
+  uint32_t cache_bf16;  // the caches round to bf16 (else f16)
+};
+
+// One threadgroup: every element of one row's kv heads, for each store, at
+// ((s * kvHeads + h) * length + pos mod length) * headDim (Graph.hs:138-143).
 extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
     fk_step_store(const float *__restrict__ x0, const float *__restrict__ x1, uint16_t *__restrict__ c0,
                   uint16_t *__restrict__ c1, const uint32_t *__restrict__ position,
-                  const uint32_t *__restrict__ slot, fk_step_store_params p) {
+                  const uint32_t *__restrict__ slot, const float *__restrict__ rope, fk_step_store_params p) {
   const uint32_t pos = position[0];
   const uint32_t s = slot[0];
   const uint32_t width = p.kv_heads * p.head_dim;
-  if (s >= p.slots) return;  // the gate bounds slots; a bad one stores nothing
+  if (s >= p.slots) return;  // the gate bounds slots: a bad one stores nothing
+  const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
   for (uint32_t st = 0; st < p.n_stores; st++) {
     const float *x = st == 0 ? x0 : x1;
     uint16_t *c = st == 0 ? c0 : c1;
     for (uint32_t e = threadIdx.x; e < width; e += blockDim.x) {
       const uint32_t h = e / p.head_dim;
       const uint32_t i = e % p.head_dim;
-      const float v = p.rope[st] ? fk::rope_elem(x + h * p.head_dim, i, p.head_dim, p.rotated, pos, p.theta) : x[e];
-      // Ring: ((s * kvHeads + h) * length + pos mod length) * headDim (Graph.hs:138-143).
+      const float v = p.rope[st] ? fk::rope_elem(x + h * p.head_dim, i, p.head_dim, p.rotated, cs) : x[e];
       const size_t at = (((size_t)s * p.kv_heads + h) * p.length + pos % p.length) * p.head_dim + i;
       c[at] = fk::narrow_cache(v, p.cache_bf16);
     }
@@ -314,42 +575,40 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
 struct fk_step_attend_params {
   uint32_t heads;
   uint32_t kv_heads;
-  uint32_t head_dim;  // at most 64
+  uint32_t head_dim;  // a multiple of 8, at most 64
   uint32_t length;    // the ring's positions
   uint32_t slots;
   uint32_t splits;    // threadgroups per kv head; split t covers positions [128 t, 128 t + 128)
   uint32_t rope;      // q is RoPE'd first
   uint32_t rotated;
-  float theta;
+  uint32_t rope_rows;
   float scale;        // the attention's scale, rounded once to binary32
   uint32_t window;    // 0: none
   uint32_t cache_bf16;
 };
 
-namespace fk {
-__device__ __forceinline__ float widen_cache(uint16_t h, bool bf16) {
-  return bf16 ? __uint_as_float((uint32_t)h << 16) : widen_f16(h);
-}
-}  // namespace fk
-
-// Threadgroup (kv head g, split t): the scores of the group's query heads over
-// the split's positions, each head's maximum over the split, the weights
-// exp(score - max), their sum and the weighted sum of the values, stored as
+// Threadgroup (kv head g, split t): for each query head h of the group and
+// each position r of the split, score = (sum over i in order of q_i k_i) *
+// scale; the head's maximum over the split (exact whatever the order); the
+// weights exp(score - max), binary64's rounded once; the weights' sum and the
+// weighted sum of the values, each in order of position.  Stored as
 // partials: per (head, split) [max, sum, acc[head_dim]].
 extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
     fk_step_attend(const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
                    const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot,
-                   float *__restrict__ partials, fk_step_attend_params p) {
-  constexpr uint32_t KS = FK_ATTN_MAX_DIM + 2;  // a key row's stride in LDS, past the banks' period
+                   const float *__restrict__ rope, float *__restrict__ partials, fk_step_attend_params p) {
   __shared__ float qs[FK_ATTN_MAX_GROUP * FK_ATTN_MAX_DIM];
-  __shared__ uint16_t ks[FK_ATTN_SPLIT * KS];
-  __shared__ uint16_t vs[FK_ATTN_SPLIT * FK_ATTN_MAX_DIM];
+  __shared__ uint16_t kt[FK_ATTN_MAX_DIM * FK_ATTN_SPLIT];  // keys transposed: kt[i][r]
+  __shared__ uint4 vsv[FK_ATTN_SPLIT * FK_ATTN_MAX_DIM / 8];
   __shared__ float wt[FK_ATTN_MAX_GROUP * FK_ATTN_SPLIT];
   __shared__ float mx[FK_ATTN_MAX_GROUP];
+  const uint16_t *vs = reinterpret_cast<const uint16_t *>(vsv);
   const uint32_t g = blockIdx.x / p.splits;
   const uint32_t t = blockIdx.x % p.splits;
   const uint32_t group = p.heads / p.kv_heads;
   const uint32_t d = p.head_dim;
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+  const uint32_t wave = threadIdx.x / FK_WAVE;
   const uint32_t pos = position[0];
   const uint32_t s = slot[0] < p.slots ? slot[0] : 0;
   const bool bf16 = p.cache_bf16 != 0;
@@ -358,31 +617,43 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
   const uint32_t lo = max(first, t * FK_ATTN_SPLIT);
   const uint32_t hi = min(pos + 1, (t + 1) * FK_ATTN_SPLIT);
   const uint32_t count = hi > lo ? hi - lo : 0;
+  const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
   for (uint32_t e = threadIdx.x; e < group * d; e += blockDim.x) {
     const float *head = q + (size_t)(g * group + e / d) * d;
-    qs[e] = p.rope ? fk::rope_elem(head, e % d, d, p.rotated, pos, p.theta) : head[e % d];
+    qs[e] = p.rope ? fk::rope_elem(head, e % d, d, p.rotated, cs) : head[e % d];
   }
+  // The split's keys and values, 16 bytes a load.
   const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
-  for (uint32_t e = threadIdx.x; e < count * d; e += blockDim.x) {
-    const uint32_t r = e / d;
-    const size_t at = (base + (lo + r) % p.length) * d + e % d;
-    ks[r * KS + e % d] = kc[at];
-    vs[e] = vc[at];
+  const uint32_t per_row = d / 8;
+  for (uint32_t e = threadIdx.x; e < count * per_row; e += blockDim.x) {
+    const uint32_t r = e / per_row;
+    const uint32_t c8 = e % per_row;
+    const size_t at = (base + (lo + r) % p.length) * d + 8 * c8;
+    const uint4 kv = *reinterpret_cast<const uint4 *>(kc + at);
+    const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+    for (int h2 = 0; h2 < 4; h2++) {
+      kt[(8 * c8 + 2 * h2) * FK_ATTN_SPLIT + r] = (uint16_t)(kw[h2] & 0xFFFFu);
+      kt[(8 * c8 + 2 * h2 + 1) * FK_ATTN_SPLIT + r] = (uint16_t)(kw[h2] >> 16);
+    }
+    vsv[r * per_row + c8] = *reinterpret_cast<const uint4 *>(vc + at);
   }
   __syncthreads();
-  // Scores: (sum over i in order of q_i k_i) * scale.
+  // Scores.
   for (uint32_t e = threadIdx.x; e < group * count; e += blockDim.x) {
     const uint32_t h = e / count;
     const uint32_t r = e % count;
     float dot = 0.0f;
-    for (uint32_t i = 0; i < d; i++) dot = dot + qs[h * d + i] * fk::widen_cache(ks[r * KS + i], bf16);
+    for (uint32_t i = 0; i < d; i++) dot = dot + qs[h * d + i] * fk::widen_cache(kt[i * FK_ATTN_SPLIT + r], bf16);
     wt[h * FK_ATTN_SPLIT + r] = dot * p.scale;
   }
   __syncthreads();
-  if (threadIdx.x < group) {
+  // Each head's maximum: wavefront h's lanes over the positions.
+  for (uint32_t h = wave; h < group; h += blockDim.x / FK_WAVE) {
     float m = -__builtin_inff();
-    for (uint32_t r = 0; r < count; r++) m = fk::max_number(m, wt[threadIdx.x * FK_ATTN_SPLIT + r]);
-    mx[threadIdx.x] = m;
+    for (uint32_t r = lane; r < count; r += FK_WAVE) m = fk::max_number(m, wt[h * FK_ATTN_SPLIT + r]);
+    m = fk::wave_max(m);
+    if (lane == 0) mx[h] = m;
   }
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < group * count; e += blockDim.x) {
@@ -414,29 +685,38 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
 struct fk_step_combine_params {
   uint32_t heads;
   uint32_t head_dim;
-  uint32_t splits;
+  uint32_t splits;  // at most 256
 };
 
-// Thread (h, i): the splits combined once, in split order: M the largest
-// maximum, w_t = exp(max_t - M), out = (sum_t acc_t w_t) / (sum_t l_t w_t).
+// Threadgroup per head: M the largest of the splits' maxima (exact whatever
+// the order), the splits' weights w_t = exp(max_t - M) binary64's rounded
+// once, then thread i: out = (sum_t acc_t[i] w_t) / (sum_t l_t w_t), both sums
+// in split order.
 extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
     fk_step_combine(const float *__restrict__ partials, float *__restrict__ out, fk_step_combine_params p) {
-  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= p.heads * p.head_dim) return;
-  const uint32_t h = e / p.head_dim;
-  const uint32_t i = e % p.head_dim;
+  __shared__ float w[256];
+  __shared__ float top;
+  const uint32_t h = blockIdx.x;
   const uint32_t stride = p.head_dim + 2;
   const float *ph = partials + (size_t)h * p.splits * stride;
-  float m = -__builtin_inff();
-  for (uint32_t t = 0; t < p.splits; t++) m = fk::max_number(m, ph[t * stride]);
-  float l = 0.0f;
-  float acc = 0.0f;
-  for (uint32_t t = 0; t < p.splits; t++) {
-    const float w = fk::exp_once(ph[t * stride] - m);
-    l = l + ph[t * stride + 1] * w;
-    acc = acc + ph[t * stride + 2 + i] * w;
+  if (threadIdx.x < FK_WAVE) {
+    float m = -__builtin_inff();
+    for (uint32_t t = threadIdx.x; t < p.splits; t += FK_WAVE) m = fk::max_number(m, ph[t * stride]);
+    m = fk::wave_max(m);
+    if (threadIdx.x == 0) top = m;
   }
-  out[e] = acc / l;
+  __syncthreads();
+  for (uint32_t t = threadIdx.x; t < p.splits; t += blockDim.x) w[t] = fk::exp_once(ph[t * stride] - top);
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < p.head_dim; i += blockDim.x) {
+    float l = 0.0f;
+    float acc = 0.0f;
+    for (uint32_t t = 0; t < p.splits; t++) {
+      l = l + ph[t * stride + 1] * w[t];
+      acc = acc + ph[t * stride + 2 + i] * w[t];
+    }
+    out[(size_t)h * p.head_dim + i] = acc / l;
+  }
 }
 
 // Greedy token ------------------------------------------------------------
@@ -445,42 +725,50 @@ struct fk_step_argmax_params {
   uint32_t n;
 };
 
-// The index of the row's largest element, ties to the lowest
-// (src/FuryKernel/Program/Eval.hs:681-685): thread t scans t, t + T, ...; then
-// pairs combine, the later winning only if strictly larger.
+namespace fk {
+// Of two (value, index) candidates, the larger value; of equal values (or
+// values neither larger), the lower index: the fold of Eval.hs:681-685 where
+// a later element wins only if strictly larger.
+__device__ __forceinline__ void argmax_merge(float &v, uint32_t &i, float ov, uint32_t oi) {
+  if (oi == 0xFFFFFFFFu) return;
+  if (i == 0xFFFFFFFFu) {
+    v = ov;
+    i = oi;
+    return;
+  }
+  const bool take = oi < i ? !(v > ov) : ov > v;
+  if (take) {
+    v = ov;
+    i = oi;
+  }
+}
+}  // namespace fk
+
 extern "C" __global__ void __launch_bounds__(1024)
     fk_step_argmax(const float *__restrict__ x, uint32_t *__restrict__ out, fk_step_argmax_params p) {
-  __shared__ float bv[1024];
-  __shared__ uint32_t bi[1024];
+  __shared__ float bv[16];
+  __shared__ uint32_t bi[16];
   float v = -__builtin_inff();
   uint32_t idx = 0xFFFFFFFFu;
-  for (uint32_t i = threadIdx.x; i < p.n; i += blockDim.x) {
-    const float c = x[i];
-    if (idx == 0xFFFFFFFFu || c > v) {
-      v = c;
-      idx = i;
-    }
+  for (uint32_t i = threadIdx.x; i < p.n; i += blockDim.x) fk::argmax_merge(v, idx, x[i], i);
+  for (int m = 1; m < FK_WAVE; m <<= 1) {
+    const float ov = __shfl_xor(v, m);
+    const uint32_t oi = __shfl_xor(idx, m);
+    fk::argmax_merge(v, idx, ov, oi);
   }
-  bv[threadIdx.x] = v;
-  bi[threadIdx.x] = idx;
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+  const uint32_t wave = threadIdx.x / FK_WAVE;
+  if (lane == 0) {
+    bv[wave] = v;
+    bi[wave] = idx;
+  }
   __syncthreads();
-  for (uint32_t w = blockDim.x / 2; w > 0; w /= 2) {
-    if (threadIdx.x < w) {
-      const float ov = bv[threadIdx.x + w];
-      const uint32_t oi = bi[threadIdx.x + w];
-      const uint32_t mi = bi[threadIdx.x];
-      // The element of the lower index wins unless the other is strictly larger.
-      const bool other_lower = oi < mi;
-      const bool take = oi != 0xFFFFFFFFu &&
-                        (mi == 0xFFFFFFFFu || (other_lower ? !(bv[threadIdx.x] > ov) : ov > bv[threadIdx.x]));
-      if (take) {
-        bv[threadIdx.x] = ov;
-        bi[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    float fv = bv[0];
+    uint32_t fi = bi[0];
+    for (uint32_t w2 = 1; w2 < blockDim.x / FK_WAVE; w2++) fk::argmax_merge(fv, fi, bv[w2], bi[w2]);
+    out[0] = fi;
   }
-  if (threadIdx.x == 0) out[0] = bi[0];
 }
 
 struct fk_step_silu_mul_params {

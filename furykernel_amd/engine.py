@@ -17,7 +17,7 @@ import numpy as np
 
 from . import kernels as K
 from . import runtime
-from .lower import Launch, Lowered
+from .lower import Launch, Lowered, rope_table
 
 _NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16}
 _STRUCTS = {
@@ -56,6 +56,11 @@ class Engine:
         self.buffers: dict[str, runtime.Buffer] = {}
         for name, spec in specs.items():
             self.buffers[name] = self.arena.alloc(spec.nbytes, 256)
+        for name, what in lowered.constants.items():
+            if what[0] == "rope":
+                self.write(name, rope_table(*what[1:]))
+            else:
+                raise ValueError(f"{name}: no constant {what[0]}")
         self._kernargs = [self._kernarg(launch) for launch in lowered.launches]
         self._fns = [ks.fn(launch.entry) for launch in lowered.launches]
 

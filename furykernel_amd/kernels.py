@@ -53,6 +53,10 @@ class FillParams(ctypes.Structure):
     _fields_ = [("count", ctypes.c_uint32), ("value", ctypes.c_uint32)]
 
 
+class StreamReadParams(ctypes.Structure):
+    _fields_ = [("words", ctypes.c_uint64)]
+
+
 class NoopParams(ctypes.Structure):
     _fields_ = [("unused", ctypes.c_uint32)]
 
@@ -84,7 +88,7 @@ class StepStoreParams(ctypes.Structure):
         ("length", ctypes.c_uint32),
         ("slots", ctypes.c_uint32),
         ("rotated", ctypes.c_uint32),
-        ("theta", ctypes.c_float),
+        ("rope_rows", ctypes.c_uint32),
         ("cache_bf16", ctypes.c_uint32),
     ]
 
@@ -99,7 +103,7 @@ class StepAttendParams(ctypes.Structure):
         ("splits", ctypes.c_uint32),
         ("rope", ctypes.c_uint32),
         ("rotated", ctypes.c_uint32),
-        ("theta", ctypes.c_float),
+        ("rope_rows", ctypes.c_uint32),
         ("scale", ctypes.c_float),
         ("window", ctypes.c_uint32),
         ("cache_bf16", ctypes.c_uint32),
@@ -158,9 +162,15 @@ ABIS: dict[str, KernelAbi] = {
     "fk_fill_u32": KernelAbi("fk_fill_u32", ("dst",), FillParams),
     **{f"fk_step_gemv_{t}_r{r}": KernelAbi(f"fk_step_gemv_{t}_r{r}", (
         "w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
-        "res_token", "epi_out"), StepGemvParams) for t, r in (("f16", 1), ("f16", 2), ("f32", 1))},
-    "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot"), StepStoreParams),
-    "fk_step_attend": KernelAbi("fk_step_attend", ("q", "kc", "vc", "position", "slot", "partials"),
+        "res_token", "epi_out"), StepGemvParams) for t, r in (("f16", 1), ("f16", 2), ("f16", 4), ("f16", "1p8"),
+                                                          ("f32", 1))},
+    **{f"fk_step_gemv_f16_k{k}_r{r}": KernelAbi(f"fk_step_gemv_f16_k{k}_r{r}", (
+        "w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
+        "res_token", "epi_out"), StepGemvParams) for k, r in ((2048, 1), (2048, 2), (2048, 4), (2048, 8), (8192, 1),
+                                                              (8192, 2))},
+    "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
+                               StepStoreParams),
+    "fk_step_attend": KernelAbi("fk_step_attend", ("q", "kc", "vc", "position", "slot", "rope", "partials"),
                                 StepAttendParams),
     "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams),
     "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
@@ -168,6 +178,7 @@ ABIS: dict[str, KernelAbi] = {
     "fk_step_advance": KernelAbi("fk_step_advance", ("next_token", "token", "position"), AdvanceParams),
     "fk_init_normal": KernelAbi("fk_init_normal", ("dst",), InitNormalParams),
     "fk_noop": KernelAbi("fk_noop", (), NoopParams),
+    "fk_stream_read": KernelAbi("fk_stream_read", ("src", "out"), StreamReadParams),
 }
 
 # Elements a lane loads at once, by weight type: one 16-byte load of W.
@@ -250,6 +261,17 @@ class Kernels:
             raise LaunchError(f"fk_fill_u32: {count} words past a buffer of {dst.size} bytes")
         groups = min(max((count + 255) // 256, 1), 4096)
         self.launch("fk_fill_u32", groups, 256, {"dst": dst.ptr}, FillParams(count, value & 0xFFFFFFFF), stream)
+
+    def stream_read(self, src: runtime.Buffer, out: runtime.Buffer, groups: int, nbytes: int | None = None,
+                    stream: runtime.Stream | None = None) -> None:
+        """Reads `nbytes` of a buffer once (the attainable read bandwidth)."""
+        nbytes = src.size if nbytes is None else nbytes
+        if nbytes > src.size or nbytes % 16 or src.ptr % 16:
+            raise LaunchError("fk_stream_read: a read past the buffer or not in 16-byte words")
+        if out.size < groups * 4 * 4:
+            raise LaunchError("fk_stream_read: the output holds a word per wavefront")
+        self.launch("fk_stream_read", groups, 256, {"src": src.ptr, "out": out.ptr}, StreamReadParams(nbytes // 16),
+                    stream)
 
     def softmax(self, x: runtime.Buffer, y: runtime.Buffer, rows: int, n: int, threads: int = 256,
                 stream: runtime.Stream | None = None) -> None:

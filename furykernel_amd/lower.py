@@ -57,6 +57,7 @@ class Launch:
     threads: int
     bind: dict      # binding name -> logical buffer name (None: unbound)
     params: dict    # parameter struct field -> value
+    meta: dict = field(default_factory=dict)  # what the kernel's table buffers were made from
     lds_bytes: int = 0
 
 
@@ -67,6 +68,7 @@ class Lowered:
     rows: int
     buffers: dict = field(default_factory=dict)  # name -> BufferSpec
     launches: list = field(default_factory=list)
+    constants: dict = field(default_factory=dict)  # name -> what fills it: ("rope", theta, d, rotated, rows)
 
     def buffer(self, name: str, dtype: str, count: int) -> str:
         spec = BufferSpec(name, dtype, count)
@@ -77,21 +79,39 @@ class Lowered:
         return name
 
 
-def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1) -> Lowered:
+def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units: int = 256) -> Lowered:
     """The launches of every step of the plan, in order, for steps of `rows`
-    rows (one, a decode step's)."""
+    rows (one, a decode step's), on a device of `compute_units` CUs."""
     if rows != 1:
         raise LoweringError(f"steps of {rows} rows: the decode kernels take one row a step")
     out = Lowered(checked.program, plan, rows)
-    low = _StepLowering(out)
+    low = _StepLowering(out, compute_units)
     for step in plan.steps:
         out.launches.append(low.step(step))
     return out
 
 
+def rope_table(theta: float, d: int, rotated: int, rows: int) -> np.ndarray:
+    """RoPE's cosines and sines by position: row p holds (cos, sin) of pair i's
+    angle, the binary32 product p * theta^(-2i/d), the frequency and the
+    cosine and sine each binary64's rounded once to binary32 (the contract of
+    src/FuryKernel/Program/Eval.hs:819-829 with tables)."""
+    t32 = float(np.float32(theta))
+    freqs = np.array([math.pow(t32, -(2.0 * i) / d) for i in range(rotated)], np.float32)
+    angles = (np.arange(rows, dtype=np.float32)[:, None] * freqs[None, :]).astype(np.float32).ravel().tolist()
+    out = np.empty((rows * rotated, 2), np.float32)
+    out[:, 0] = [math.cos(a) for a in angles]
+    out[:, 1] = [math.sin(a) for a in angles]
+    return out.reshape(rows, rotated, 2)
+
+
+GEMV_THREADS = 512
+
+
 class _StepLowering:
-    def __init__(self, out: Lowered):
+    def __init__(self, out: Lowered, compute_units: int = 256):
         self.out = out
+        self.compute_units = compute_units
         self.p = out.program
         self.producer = {v: n for n in self.p.nodes for v in n.outputs}
 
@@ -132,6 +152,12 @@ class _StepLowering:
         count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
         bf16 = src.kind.elem == CACHE_BF16
         return self.out.buffer(f"cache:{src.name}", "bf16" if bf16 else "f16", count), lay, bf16
+
+    def rope(self, spec, d: int, rows: int) -> str:
+        name = f"rope:{spec.theta!r}:{d}:{spec.rotated}:{rows}"
+        self.out.buffer(name, "f32", rows * spec.rotated * 2)
+        self.out.constants[name] = ("rope", float(spec.theta), d, spec.rotated, rows)
+        return name
 
     def stored_before(self, step: Step, v: int) -> bool:
         prod = self.producer.get(v)
@@ -234,10 +260,12 @@ class _StepLowering:
                 raise LoweringError(f"{step.name}: no prologue computes {type(op).__name__}")
         params["pro_mode"] = pro
         params.setdefault("seg", k)
-        if params["seg"] % 4 or k % params["seg"]:
-            raise LoweringError(f"{step.name}: RMSNorm segments of {params['seg']} don't divide {k} in packs of 4")
+        if params["seg"] != k or k % 4:
+            raise LoweringError(f"{step.name}: RMSNorm in segments of {params['seg']} of a row of {k}; the GEMV "
+                                f"prologue norms the whole row")
 
-        # Anchors.
+        # Anchors: their rows one after another, in blocks of R rows.
+        R = 1
         rows, first, g = [], [0], 0
         anchor_outs = {}
         for j, a in enumerate(anchors):
@@ -246,7 +274,7 @@ class _StepLowering:
             bind[f"w{j}"] = wname
             n = self.p.value(a.outputs[0]).shape.width
             rows.append(n)
-            g += -(-n // (THREADS // 64))
+            g += -(-n // R)
             first.append(g)
             anchor_outs[a.outputs[0]] = j
         if len(wtypes) != 1:
@@ -297,8 +325,10 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: an epilogue whose value isn't stored")
         params.update(n_anchors=len(anchors), rows=rows + [0] * (3 - len(rows)),
                       first_group=first + [g] * (4 - len(first)), k=k, store_tile=store_tile)
-        entry = f"fk_step_gemv_{wt}_r1"
-        return Launch(step.name, entry, g, THREADS, bind, params)
+        entry = f"fk_step_gemv_{wt}_r{R}"
+        waves = GEMV_THREADS // 64
+        groups = min(-(-g // waves), 2 * self.compute_units)
+        return Launch(step.name, entry, groups, GEMV_THREADS, bind, params)
 
     def rope_of(self, step: Step, node, rec: dict) -> Optional[int]:
         if not isinstance(node.op, Rope):
@@ -313,8 +343,9 @@ class _StepLowering:
         effects = [self.p.node(w.node) for w in step.work if w.kind == EFFECT]
         if not 1 <= len(effects) <= 2 or not all(isinstance(e.op, KvStore) for e in effects):
             raise LoweringError(f"{step.name}: effects other than one or two KV stores")
-        bind = {"x0": None, "x1": None, "c0": None, "c1": None, "position": None, "slot": None}
-        params: dict = {"n_stores": len(effects), "rope": [0, 0], "rotated": 0, "theta": 1.0}
+        bind = {"x0": None, "x1": None, "c0": None, "c1": None, "position": None, "slot": None, "rope": None}
+        params: dict = {"n_stores": len(effects), "rope": [0, 0], "rotated": 0, "rope_rows": 1}
+        meta: dict = {"theta": 1.0}
         layouts, used = set(), set()
         for j, e in enumerate(effects):
             at = e.op.at
@@ -332,12 +363,15 @@ class _StepLowering:
                     raise LoweringError(f"{step.name}: a stored value recomputed by other than RoPE of a stored row")
                 used.add(v)
                 spec = rec[v].op.spec
-                if params["rope"] != [0, 0] and (params["rotated"], params["theta"]) != (
+                if params["rope"] != [0, 0] and (params["rotated"], meta["theta"]) != (
                         spec.rotated, float(np.float32(spec.theta))):
                     raise LoweringError(f"{step.name}: two RoPEs of different specs")
                 params["rope"][j] = 1
                 params["rotated"] = spec.rotated
-                params["theta"] = float(np.float32(spec.theta))
+                meta["theta"] = float(np.float32(spec.theta))
+                rope_rows = self.p.source(at.positions).kind.bound
+                params["rope_rows"] = rope_rows
+                bind["rope"] = self.rope(spec, self.p.value(inner).shape.segment, rope_rows)
                 bind[f"x{j}"] = self.value(inner)
             elif self.stored_before(step, v):
                 bind[f"x{j}"] = self.value(v)
@@ -351,7 +385,9 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: a store step that also stores values")
         kv, d, length, slots, bf16 = layouts.pop()
         params.update(kv_heads=kv, head_dim=d, length=length, slots=slots, cache_bf16=int(bf16))
-        return Launch(step.name, "fk_step_store", 1, THREADS, bind, params)
+        if bind["rope"] is None:
+            bind["rope"] = bind["position"]  # bound but never read
+        return Launch(step.name, "fk_step_store", 1, THREADS, bind, params, meta)
 
     def attend_step(self, step: Step, anchor) -> Launch:
         op = anchor.op
@@ -363,15 +399,23 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: heads of {spec.head_dim} or groups of {spec.heads // spec.kv_heads}")
         kname, lay, bf16 = self.cache(op.to.keys)
         vname, vlay, _ = self.cache(op.to.values)
+        if spec.head_dim % 8:
+            raise LoweringError(f"{step.name}: heads of {spec.head_dim}, not a multiple of 8")
         params = {"heads": spec.heads, "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "length": lay.length,
-                  "slots": lay.slots, "rope": 0, "rotated": 0, "theta": 1.0,
+                  "slots": lay.slots, "rope": 0, "rotated": 0, "rope_rows": 1,
                   "scale": float(np.float32(spec.scale)), "window": spec.window or 0, "cache_bf16": int(bf16)}
+        meta = {"theta": 1.0}
+        rope_buf = None
         q = op.q
         if q in rec:
             inner = self.rope_of(step, rec[q], rec)
             if inner is None or not self.stored_before(step, inner):
                 raise LoweringError(f"{step.name}: queries recomputed by other than RoPE of a stored row")
-            params.update(rope=1, rotated=rec[q].op.spec.rotated, theta=float(np.float32(rec[q].op.spec.theta)))
+            rspec = rec[q].op.spec
+            rope_rows = self.p.source(op.to.positions).kind.bound
+            params.update(rope=1, rotated=rspec.rotated, rope_rows=rope_rows)
+            meta["theta"] = float(np.float32(rspec.theta))
+            rope_buf = self.rope(rspec, spec.head_dim, rope_rows)
             qbuf = self.value(inner)
             if set(rec) - {q}:
                 raise LoweringError(f"{step.name}: recomputes the attention kernel doesn't take")
@@ -387,9 +431,10 @@ class _StepLowering:
         out = anchor.outputs[0]
         pname = self.out.buffer(f"partials:{self.p.value(out).name}", "f32",
                                 spec.heads * splits * (spec.head_dim + 2))
-        bind = {"q": qbuf, "kc": kname, "vc": vname, "position": self.ints(op.to.positions),
-                "slot": self.ints(op.to.sequences), "partials": pname}
-        return Launch(step.name, "fk_step_attend", spec.kv_heads * splits, THREADS, bind, params)
+        pos_buf = self.ints(op.to.positions)
+        bind = {"q": qbuf, "kc": kname, "vc": vname, "position": pos_buf, "slot": self.ints(op.to.sequences),
+                "rope": rope_buf or pos_buf, "partials": pname}
+        return Launch(step.name, "fk_step_attend", spec.kv_heads * splits, THREADS, bind, params, meta)
 
     def combine_step(self, step: Step) -> Launch:
         combines = [self.p.node(w.node) for w in step.work if w.kind == COMBINE]
@@ -405,9 +450,10 @@ class _StepLowering:
         if pname not in self.out.buffers:
             raise LoweringError(f"{step.name}: combines partials no step stored")
         splits = self.out.buffers[pname].count // (spec.heads * (spec.head_dim + 2))
+        if splits > 256:
+            raise LoweringError(f"{step.name}: {splits} splits; the combine takes up to 256")
         params = {"heads": spec.heads, "head_dim": spec.head_dim, "splits": splits}
-        total = spec.heads * spec.head_dim
-        return Launch(step.name, "fk_step_combine", -(-total // THREADS), THREADS,
+        return Launch(step.name, "fk_step_combine", spec.heads, 64 if spec.head_dim <= 64 else THREADS,
                       {"partials": pname, "out": self.value(out)}, params)
 
     def light_step(self, step: Step) -> Launch:

@@ -64,13 +64,14 @@ class CpuTarget:
         elif e == "fk_step_store":
             st = L.fkref_step_store(self._p(b["x0"]), self._p(b["x1"]), self._p(b["c0"]), self._p(b["c1"]),
                                     p["n_stores"], p["rope"][0], p["rope"][1], p["kv_heads"], p["head_dim"],
-                                    p["length"], p["slots"], p["rotated"], p["theta"],
+                                    p["length"], p["slots"], p["rotated"], launch.meta["theta"],
                                     int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0]),
                                     p["cache_bf16"])
         elif e == "fk_step_attend":
             st = L.fkref_step_attend(self._p(b["q"]), self._p(b["kc"]), self._p(b["vc"]), self._p(b["partials"]),
                                      p["heads"], p["kv_heads"], p["head_dim"], p["length"], p["slots"],
-                                     p["splits"], p["rope"], p["rotated"], p["theta"], p["scale"], p["window"],
+                                     p["splits"], p["rope"], p["rotated"], launch.meta["theta"], p["scale"],
+                                     p["window"],
                                      int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0]),
                                      p["cache_bf16"])
         elif e == "fk_step_combine":
