@@ -110,10 +110,13 @@ class Engine:
 
     # Running -----------------------------------------------------------------
 
-    def enqueue(self, stream: runtime.Stream | None = None) -> None:
-        """Queues every launch of the step, in plan order."""
-        for launch, fn, arg in zip(self.lowered.launches, self._fns, self._kernargs):
-            fn.launch(launch.groups, launch.threads, arg, launch.lds_bytes, stream)
+    def enqueue(self, stream: runtime.Stream | None = None, only: Optional[list] = None) -> None:
+        """Queues every launch of the step (or those at the indices `only`),
+        in plan order."""
+        picks = range(len(self.lowered.launches)) if only is None else only
+        for i in picks:
+            launch = self.lowered.launches[i]
+            self._fns[i].launch(launch.groups, launch.threads, self._kernargs[i], launch.lds_bytes, stream)
 
     def enqueue_advance(self, token_out: str, token_in: str, position: str, context: int, step: int = 1,
                         stream: runtime.Stream | None = None) -> None:
@@ -124,10 +127,12 @@ class Engine:
                              "position": self.buffers[position].ptr},
                             K.AdvanceParams(context, step), stream)
 
-    def capture(self, advance: Optional[dict] = None, stream: runtime.Stream | None = None) -> runtime.Graph:
-        """A graph of the step's launches (and the advance, if given), to replay."""
+    def capture(self, advance: Optional[dict] = None, stream: runtime.Stream | None = None,
+                only: Optional[list] = None) -> runtime.Graph:
+        """A graph of the step's launches (or those at the indices `only`; and
+        the advance, if given), to replay."""
         with self.device.capture(stream) as out:
-            self.enqueue(stream)
+            self.enqueue(stream, only)
             if advance is not None:
                 self.enqueue_advance(stream=stream, **advance)
         return out[0]

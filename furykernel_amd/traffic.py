@@ -1,0 +1,85 @@
+"""Algorithmic HBM bytes of a lowered launch: what it must read and write, once
+each, at a given decode position — the figure a kernel's achieved GB/s is
+quoted against.
+
+Counted per launch, from its parameters and the buffer types it binds:
+
+- GEMV step: every weight row of its anchors, the input row (the stored
+  f32 row, both rows of a SiLU·mul, or the gathered table row and its
+  token), the norm gains, the stored tiles, the residual row read and the
+  epilogue row written;
+- KV store: each stored row read (f32) and written to the cache (f16/bf16),
+  and the RoPE table row;
+- attention: K and V of every position the query reads (the ring up to the
+  position, or the window), the query rows, the RoPE row and the partials
+  written;
+- combine: the partials read and the combined rows written;
+- argmax, SiLU·mul: their rows.
+"""
+
+from __future__ import annotations
+
+from .lower import ATTN_SPLIT, EPI_ADD_GATHER, EPI_ADD_STORED, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, \
+    Launch, Lowered
+
+_ELT = {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2}
+
+
+def _elt(lowered: Lowered, name: str) -> int:
+    return _ELT[lowered.buffers[name].dtype]
+
+
+def positions_read(length: int, window: int, position: int) -> int:
+    """Cache positions an attention at `position` reads: up to the ring's
+    length, or the window's."""
+    n = min(position + 1, length)
+    return min(n, window) if window else n
+
+
+def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
+    b, p, e = launch.bind, launch.params, launch.entry
+    if e.startswith("fk_step_gemv"):
+        k = p["k"]
+        rows = p["rows"][:p["n_anchors"]]
+        total = sum(r * k * _elt(lowered, b[f"w{j}"]) for j, r in enumerate(rows))
+        if p["pro_mode"] in (PRO_GATHER, PRO_GATHER_RMSNORM):
+            total += k * _elt(lowered, b["table"]) + 4
+        else:
+            total += k * 4 * (2 if p["pro_mode"] == PRO_SILU_MUL else 1)
+        if p["has_gamma"]:
+            total += k * 4
+        if p["store_tile"]:
+            total += sum(rows) * 4
+        if p["epi_mode"] == EPI_ADD_STORED:
+            total += rows[0] * 4 * 2
+        elif p["epi_mode"] == EPI_ADD_GATHER:
+            total += rows[0] * _elt(lowered, b["res_table"]) + 4 + rows[0] * 4
+        return total
+    if e == "fk_step_store":
+        row = p["kv_heads"] * p["head_dim"]
+        cache = 2 if p["cache_bf16"] or lowered.buffers[b["c0"]].dtype == "f16" else 4
+        total = p["n_stores"] * row * (4 + cache) + 8
+        if p["rope"] != [0, 0]:
+            total += p["rotated"] * 8
+        return total
+    if e == "fk_step_attend":
+        n = positions_read(p["length"], p["window"], position)
+        elt = _elt(lowered, b["kc"])
+        d = p["head_dim"]
+        total = 2 * p["kv_heads"] * n * d * elt + p["heads"] * d * 4 + 8
+        total += p["heads"] * -(-n // ATTN_SPLIT) * (d + 2) * 4
+        if p["rope"]:
+            total += p["rotated"] * 8
+        return total
+    if e == "fk_step_combine":
+        d = p["head_dim"]
+        return p["heads"] * p["splits"] * (d + 2) * 4 + p["heads"] * d * 4
+    if e == "fk_step_argmax":
+        return p["n"] * 4 + 4
+    if e == "fk_step_silu_mul":
+        return p["n"] * 4 * 3
+    raise ValueError(f"no byte count for {e}")
+
+
+def step_bytes(lowered: Lowered, position: int) -> int:
+    return sum(launch_bytes(lowered, launch, position) for launch in lowered.launches)
