@@ -120,7 +120,8 @@ def cpu_baseline(dims, seconds: float) -> dict:
         elif name.startswith("cache:"):
             buf[:] = np.resize(block, spec.count)
     for name, what in one.constants.items():
-        cpu.write(name, rope_table(*what[1:]))
+        if what[0] == "rope":
+            cpu.write(name, rope_table(*what[1:]))
     cpu.write("ints:position", [POSITION])
     cpu.write("ints:tokens", [7])
     layer, head = one.launches[:per_layer], one.launches[per_layer:]
@@ -195,7 +196,8 @@ def main() -> int:
     tok_s = args.steps / elapsed
     nbytes = step_bytes(session.lowered, POSITION)
     table = kernel_table(session, args.kernel_reps, args.eager)
-    log(f"kernel table: {len(table)} kernels timed")
+    for entry, row in table.items():
+        log(f"{entry}: {row['launches']} launches a step, {row['avg_us']} us a launch, {row['gbps']} GB/s")
     dominant = max(table, key=lambda e: table[e]["us_per_step"])
     dom = table[dominant]
     achieved = dom["gbps"]

@@ -14,6 +14,10 @@
 
 namespace fk {
 
+// Four 32-bit words in registers: a 16-byte load or store.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+
 // The sum of a value over the wavefront's 64 lanes, in every lane, pairwise,
 // neighbours first: ((x0 + x1) + (x2 + x3)) + ... (src/FuryKernel/IR.hs:269-283).
 // Step m adds the value of lane l ^ m, which holds the sum of the sibling
@@ -35,6 +39,19 @@ __device__ __forceinline__ float max_number(float x, float y) {
   if (__builtin_isnan(y) || x > y) return x;
   if (y > x) return y;
   return __uint_as_float(__float_as_uint(x) & __float_as_uint(y));
+}
+
+// maximumNumber as an integer maximum: a float's key orders as the float
+// does, -0 below +0, NaN below everything (so a maximum ignores it unless
+// every operand is NaN, which gives the quiet NaN back).
+__device__ __forceinline__ int max_key(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return __builtin_isnan(x) ? INT32_MIN : (int)((b & 0x80000000u) ? b ^ 0x7FFFFFFFu : b);
+}
+
+__device__ __forceinline__ float from_max_key(int k) {
+  if (k == INT32_MIN) return __uint_as_float(0x7FC00000u);
+  return __uint_as_float(k < 0 ? (uint32_t)k ^ 0x7FFFFFFFu : (uint32_t)k);
 }
 
 // The maximum over the wavefront, pairwise as the sum.

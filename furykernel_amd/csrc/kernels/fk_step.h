@@ -568,9 +568,14 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
 
 // Attention ----------------------------------------------------------------
 
-#define FK_ATTN_SPLIT 128
+#define FK_ATTN_MAX_SPLIT 128
 #define FK_ATTN_MAX_GROUP 8
 #define FK_ATTN_MAX_DIM 64
+#define FK_ATTN_THREADS 512
+#define FK_ATTN_WAVES (FK_ATTN_THREADS / FK_WAVE)
+// A key row in LDS: 64 halves and 8 of padding (144 bytes), so that lanes
+// reading 16 bytes of consecutive rows hit distinct banks.
+#define FK_ATTN_KROW (FK_ATTN_MAX_DIM + 8)
 
 struct fk_step_attend_params {
   uint32_t heads;
@@ -578,108 +583,316 @@ struct fk_step_attend_params {
   uint32_t head_dim;  // a multiple of 8, at most 64
   uint32_t length;    // the ring's positions
   uint32_t slots;
-  uint32_t splits;    // threadgroups per kv head; split t covers positions [128 t, 128 t + 128)
+  uint32_t splits;    // threadgroups per kv head
+  uint32_t split;     // positions a split covers: split t is [t split, (t + 1) split); 64 or 128
   uint32_t rope;      // q is RoPE'd first
   uint32_t rotated;
   uint32_t rope_rows;
   float scale;        // the attention's scale, rounded once to binary32
   uint32_t window;    // 0: none
   uint32_t cache_bf16;
+  uint32_t store;     // the new key and value rows are stored into the caches first
+  uint32_t krope;     // the stored key row is RoPE'd first (q's table)
 };
 
-// Threadgroup (kv head g, split t): for each query head h of the group and
-// each position r of the split, score = (sum over i in order of q_i k_i) *
-// scale; the head's maximum over the split (exact whatever the order); the
-// weights exp(score - max), binary64's rounded once; the weights' sum and the
-// weighted sum of the values, each in order of position.  Stored as
+namespace fk {
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+
+// The wavefront's maximumNumber, every lane, on max_key's integers: within
+// rows of 16 lanes by DPP (pairs, quads, halves, rows), then across the four
+// rows.  Exact whatever the order.
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  int v = max_key(x);
+  v = max(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = max(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = max(v, dpp<0x141>(v));  // row_half_mirror
+  v = max(v, dpp<0x140>(v));  // row_mirror
+  const int a = __builtin_amdgcn_readlane(v, 0);
+  const int b = __builtin_amdgcn_readlane(v, 16);
+  const int c = __builtin_amdgcn_readlane(v, 32);
+  const int d = __builtin_amdgcn_readlane(v, 48);
+  return from_max_key(max(max(a, b), max(c, d)));
+}
+
+// LDS of one attention threadgroup.
+struct AttendLds {
+  alignas(16) float qs[FK_ATTN_MAX_GROUP * FK_ATTN_MAX_DIM];
+  alignas(16) u32x4 ks[FK_ATTN_MAX_SPLIT * FK_ATTN_KROW / 8];   // later: the runs' weighted values
+  alignas(16) u32x4 vs[FK_ATTN_MAX_SPLIT * FK_ATTN_MAX_DIM / 8];
+  alignas(16) float wt[FK_ATTN_MAX_SPLIT * FK_ATTN_MAX_GROUP];  // [position][head]
+  alignas(16) float pm[FK_ATTN_MAX_GROUP * 2];  // per head, the maxima of the split's 64-position halves
+  alignas(16) float pl[FK_ATTN_WAVES * FK_ATTN_MAX_GROUP];     // the runs' weight sums
+};
+
+// Threadgroup (kv head g, split t) of 512 threads.  G, D, S, CB: the
+// group's query heads, the head dimension, the split's positions and the
+// caches' bf16-ness when known at compile time (0, 0, 0, -1: read from the
+// parameters).
+//
+// Store (if asked): the threadgroup whose split holds the position stores kv
+// head g's new key row (RoPE'd if asked) and value row at the ring index
+// ((s * kvHeads + g) * length + pos mod length) * headDim, rounded to the
+// cache's type (Graph.hs:138-143) — what the plan's store step does for that
+// head — and takes the rounded rows as that position's key and value.  No
+// other position of the ring maps to that index (the gate holds attention to
+// what the ring holds), so no other threadgroup reads it.
+//
+// Attend: for each query head h of the group and each position r of the
+// split, score = (sum over i in order of q_i k_i) * scale; the head's maximum
+// over the split (exact whatever the order); the weights exp(score - max),
+// binary64's rounded once.  The weights' sum and the weighted sum of the
+// values over 8 runs of split/8 positions (wavefront w's run w), each in
+// order of position from +0, then the runs' sums in order.  Stored as
 // partials: per (head, split) [max, sum, acc[head_dim]].
-extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
-    fk_step_attend(const float *__restrict__ q, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-                   const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot,
-                   const float *__restrict__ rope, float *__restrict__ partials, fk_step_attend_params p) {
-  __shared__ float qs[FK_ATTN_MAX_GROUP * FK_ATTN_MAX_DIM];
-  __shared__ uint16_t kt[FK_ATTN_MAX_DIM * FK_ATTN_SPLIT];  // keys transposed: kt[i][r]
-  __shared__ uint4 vsv[FK_ATTN_SPLIT * FK_ATTN_MAX_DIM / 8];
-  __shared__ float wt[FK_ATTN_MAX_GROUP * FK_ATTN_SPLIT];
-  __shared__ float mx[FK_ATTN_MAX_GROUP];
-  const uint16_t *vs = reinterpret_cast<const uint16_t *>(vsv);
+template <uint32_t G, uint32_t D, uint32_t S, int CB>
+__device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restrict__ q,
+                                             const float *__restrict__ knew, const float *__restrict__ vnew,
+                                             uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+                                             const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot,
+                                             const float *__restrict__ rope, float *__restrict__ partials,
+                                             const fk_step_attend_params &p) {
+  constexpr uint32_t T = FK_ATTN_THREADS;
+  constexpr uint32_t HPT = FK_ATTN_MAX_GROUP * FK_ATTN_MAX_SPLIT / T;  // heads a thread scores, at most
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (FK_WAVE - 1);
+  const uint32_t wave = tid / FK_WAVE;
   const uint32_t g = blockIdx.x / p.splits;
   const uint32_t t = blockIdx.x % p.splits;
-  const uint32_t group = p.heads / p.kv_heads;
-  const uint32_t d = p.head_dim;
-  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
-  const uint32_t wave = threadIdx.x / FK_WAVE;
+  const uint32_t group = G ? G : p.heads / p.kv_heads;
+  const uint32_t d = D ? D : p.head_dim;
+  const uint32_t split = S ? S : p.split;
+  const uint32_t half = d / 2;
   const uint32_t pos = position[0];
-  const uint32_t s = slot[0] < p.slots ? slot[0] : 0;
-  const bool bf16 = p.cache_bf16 != 0;
+  const uint32_t sraw = slot[0];
+  const uint32_t s = sraw < p.slots ? sraw : 0;
+  const bool bf16 = CB >= 0 ? CB != 0 : p.cache_bf16 != 0;
   // Positions [first, pos], this split's part of them.
   const uint32_t first = (p.window && pos + 1 > p.window) ? pos + 1 - p.window : 0;
-  const uint32_t lo = max(first, t * FK_ATTN_SPLIT);
-  const uint32_t hi = min(pos + 1, (t + 1) * FK_ATTN_SPLIT);
-  const uint32_t count = hi > lo ? hi - lo : 0;
+  const uint32_t lo = max(first, t * split);
+  const uint32_t hi = min(pos + 1, (t + 1) * split);
+  const uint32_t n = hi > lo ? hi - lo : 0;
   const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
-  for (uint32_t e = threadIdx.x; e < group * d; e += blockDim.x) {
-    const float *head = q + (size_t)(g * group + e / d) * d;
-    qs[e] = p.rope ? fk::rope_elem(head, e % d, d, p.rotated, cs) : head[e % d];
+  const bool stores = p.store && sraw < p.slots && lo <= pos && pos < hi;
+  uint16_t *ksh = reinterpret_cast<uint16_t *>(sh.ks);
+  const uint16_t *vsh = reinterpret_cast<const uint16_t *>(sh.vs);
+
+  // Loads, in the order their results are needed (a wavefront's loads
+  // complete in order): the query rows with their RoPE partners and
+  // cosines, the new rows, then the split's keys and values, 16 bytes a load.
+  float qx = 0.0f, qp = 0.0f, qc = 1.0f, qn = 0.0f;
+  if (tid < group * d) {
+    const float *head = q + (size_t)(g * group + tid / d) * d;
+    const uint32_t j = tid % d;
+    const uint32_t i = j < half ? j : j - half;
+    qx = head[j];
+    if (p.rope && i < p.rotated) {
+      qp = head[j < half ? j + half : j - half];
+      qc = cs[2 * i];
+      qn = cs[2 * i + 1];
+    }
   }
-  // The split's keys and values, 16 bytes a load.
-  const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
+  float kx = 0.0f, kp = 0.0f, kcs = 1.0f, ksn = 0.0f, vx = 0.0f;
+  if (stores && tid < d) {
+    const float *head = knew + (size_t)g * d;
+    const uint32_t j = tid;
+    const uint32_t i = j < half ? j : j - half;
+    kx = head[j];
+    if (p.krope && i < p.rotated) {
+      kp = head[j < half ? j + half : j - half];
+      kcs = cs[2 * i];
+      ksn = cs[2 * i + 1];
+    }
+    vx = vnew[(size_t)g * d + j];
+  }
   const uint32_t per_row = d / 8;
-  for (uint32_t e = threadIdx.x; e < count * per_row; e += blockDim.x) {
-    const uint32_t r = e / per_row;
-    const uint32_t c8 = e % per_row;
-    const size_t at = (base + (lo + r) % p.length) * d + 8 * c8;
-    const uint4 kv = *reinterpret_cast<const uint4 *>(kc + at);
-    const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+  const uint32_t chunks = n * per_row;
+  const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
+  // Ring index of row r: (lo + r) mod length, where r < n <= length.
+  const uint32_t ring0 = lo % p.length;
+  u32x4 kr[2], vr[2];
 #pragma unroll
-    for (int h2 = 0; h2 < 4; h2++) {
-      kt[(8 * c8 + 2 * h2) * FK_ATTN_SPLIT + r] = (uint16_t)(kw[h2] & 0xFFFFu);
-      kt[(8 * c8 + 2 * h2 + 1) * FK_ATTN_SPLIT + r] = (uint16_t)(kw[h2] >> 16);
+  for (int m = 0; m < 2; m++) {
+    const uint32_t e = tid + m * T;
+    kr[m] = vr[m] = u32x4{0u, 0u, 0u, 0u};
+    if (e < chunks) {
+      uint32_t ring = ring0 + e / per_row;
+      ring = ring >= p.length ? ring - p.length : ring;
+      const size_t at = (base + ring) * d + 8 * (e % per_row);
+      kr[m] = *reinterpret_cast<const u32x4 *>(kc + at);
+      vr[m] = *reinterpret_cast<const u32x4 *>(vc + at);
     }
-    vsv[r * per_row + c8] = *reinterpret_cast<const uint4 *>(vc + at);
   }
-  __syncthreads();
-  // Scores.
-  for (uint32_t e = threadIdx.x; e < group * count; e += blockDim.x) {
-    const uint32_t h = e / count;
-    const uint32_t r = e % count;
-    float dot = 0.0f;
-    for (uint32_t i = 0; i < d; i++) dot = dot + qs[h * d + i] * fk::widen_cache(kt[i * FK_ATTN_SPLIT + r], bf16);
-    wt[h * FK_ATTN_SPLIT + r] = dot * p.scale;
+
+  // The query rows, RoPE'd as rope_elem does, and the tile into LDS.
+  if (tid < group * d) {
+    const uint32_t j = tid % d;
+    const uint32_t i = j < half ? j : j - half;
+    float v = qx;
+    if (p.rope && i < p.rotated) v = j < half ? qx * qc - qp * qn : qx * qc + qp * qn;
+    sh.qs[tid] = v;
   }
-  __syncthreads();
-  // Each head's maximum: wavefront h's lanes over the positions.
-  for (uint32_t h = wave; h < group; h += blockDim.x / FK_WAVE) {
-    float m = -__builtin_inff();
-    for (uint32_t r = lane; r < count; r += FK_WAVE) m = fk::max_number(m, wt[h * FK_ATTN_SPLIT + r]);
-    m = fk::wave_max(m);
-    if (lane == 0) mx[h] = m;
-  }
-  __syncthreads();
-  for (uint32_t e = threadIdx.x; e < group * count; e += blockDim.x) {
-    const uint32_t h = e / count;
-    const uint32_t r = e % count;
-    wt[h * FK_ATTN_SPLIT + r] = fk::exp_once(wt[h * FK_ATTN_SPLIT + r] - mx[h]);
-  }
-  __syncthreads();
-  // Thread (h, i): the weights' sum and the weighted values, in order of position.
-  for (uint32_t e = threadIdx.x; e < group * d; e += blockDim.x) {
-    const uint32_t h = e / d;
-    const uint32_t i = e % d;
-    float l = 0.0f;
-    float acc = 0.0f;
-    for (uint32_t r = 0; r < count; r++) {
-      const float w = wt[h * FK_ATTN_SPLIT + r];
-      l = l + w;
-      acc = acc + w * fk::widen_cache(vs[r * d + i], bf16);
+#pragma unroll
+  for (int m = 0; m < 2; m++) {
+    const uint32_t e = tid + m * T;
+    if (e < chunks) {
+      const uint32_t r = e / per_row;
+      const uint32_t c8 = e % per_row;
+      sh.ks[r * (FK_ATTN_KROW / 8) + c8] = kr[m];
+      sh.vs[r * per_row + c8] = vr[m];
     }
-    float *out = partials + ((size_t)(g * group + h) * p.splits + t) * (d + 2);
-    if (i == 0) {
-      out[0] = mx[h];
-      out[1] = l;
-    }
-    out[2 + i] = acc;
   }
+  __syncthreads();
+  if (stores && tid < d) {
+    const uint32_t j = tid;
+    const uint32_t i = j < half ? j : j - half;
+    float k = kx;
+    if (p.krope && i < p.rotated) k = j < half ? kx * kcs - kp * ksn : kx * kcs + kp * ksn;
+    const uint16_t kh = narrow_cache(k, bf16);
+    const uint16_t vh = narrow_cache(vx, bf16);
+    const size_t at = (base + pos % p.length) * d + j;
+    kc[at] = kh;
+    vc[at] = vh;
+    ksh[(pos - lo) * FK_ATTN_KROW + j] = kh;
+    reinterpret_cast<uint16_t *>(sh.vs)[(pos - lo) * d + j] = vh;
+  }
+  __syncthreads();
+
+  // Scores: thread (r, hs) takes position r of the split for the heads hs,
+  // hs + 512/split: its key row read once, 16 bytes at a time.  Each
+  // wavefront holds 64 positions of its heads: their maximum by DPP.
+  const uint32_t nh = T / split;
+  const uint32_t r = tid % split;
+  const uint32_t hs = tid / split;
+  const uint32_t halfk = r / FK_WAVE;
+  float sc[HPT];
+  {
+    float kf[FK_ATTN_MAX_DIM];
+#pragma unroll
+    for (uint32_t c8 = 0; c8 < FK_ATTN_MAX_DIM / 8; c8++) {
+      u32x4 kk = u32x4{0u, 0u, 0u, 0u};
+      if (c8 < per_row && r < n) kk = sh.ks[r * (FK_ATTN_KROW / 8) + c8];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        kf[8 * c8 + 2 * j] = widen_cache((uint16_t)(kk[j] & 0xFFFFu), bf16);
+        kf[8 * c8 + 2 * j + 1] = widen_cache((uint16_t)(kk[j] >> 16), bf16);
+      }
+    }
+#pragma unroll
+    for (uint32_t a = 0; a < HPT; a++) {
+      const uint32_t h = hs + a * nh;
+      sc[a] = -__builtin_inff();
+      if (h < group && r < n) {
+        const float4 *qh = reinterpret_cast<const float4 *>(sh.qs + h * d);
+        float dot = 0.0f;
+#pragma unroll
+        for (uint32_t c4 = 0; c4 < FK_ATTN_MAX_DIM / 4; c4++) {
+          if (c4 < d / 4) {
+            const float4 qq = qh[c4];
+            dot = dot + qq.x * kf[4 * c4];
+            dot = dot + qq.y * kf[4 * c4 + 1];
+            dot = dot + qq.z * kf[4 * c4 + 2];
+            dot = dot + qq.w * kf[4 * c4 + 3];
+          }
+        }
+        sc[a] = dot * p.scale;
+      }
+    }
+#pragma unroll
+    for (uint32_t a = 0; a < HPT; a++) {
+      const uint32_t h = hs + a * nh;
+      if (h < group) {
+        const float m = wave_max_dpp(sc[a]);
+        if (lane == 0) sh.pm[h * 2 + halfk] = m;
+      }
+    }
+  }
+  __syncthreads();
+  // The weights exp(score - max), the head's maximum the larger of its halves'.
+#pragma unroll
+  for (uint32_t a = 0; a < HPT; a++) {
+    const uint32_t h = hs + a * nh;
+    if (h < group && r < n) {
+      const float m = split > FK_WAVE ? max_number(sh.pm[h * 2], sh.pm[h * 2 + 1]) : sh.pm[h * 2];
+      sh.wt[r * FK_ATTN_MAX_GROUP + h] = exp_once(sc[a] - m);
+    }
+  }
+  __syncthreads();
+  // Wavefront w's run of positions, lane i's dimension, every head at once.
+  {
+    const uint32_t run = split / FK_ATTN_WAVES;
+    const uint32_t u0 = wave * run;
+    const uint32_t u1 = min(u0 + run, n);
+    float l[FK_ATTN_MAX_GROUP], acc[FK_ATTN_MAX_GROUP];
+#pragma unroll
+    for (int h = 0; h < FK_ATTN_MAX_GROUP; h++) l[h] = acc[h] = 0.0f;
+    if (lane < d) {
+      for (uint32_t u = u0; u < u1; u++) {
+        const float v = widen_cache(vsh[u * d + lane], bf16);
+        const float4 w0 = *reinterpret_cast<const float4 *>(sh.wt + u * FK_ATTN_MAX_GROUP);
+        const float4 w1 = group > 4 ? *reinterpret_cast<const float4 *>(sh.wt + u * FK_ATTN_MAX_GROUP + 4)
+                                    : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float w[FK_ATTN_MAX_GROUP] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int h = 0; h < FK_ATTN_MAX_GROUP; h++) {
+          if ((uint32_t)h < group) {
+            l[h] = l[h] + w[h];
+            acc[h] = acc[h] + w[h] * v;
+          }
+        }
+      }
+    }
+    __syncthreads();  // the keys are no longer read: their LDS holds the runs' sums
+    float *pacc = reinterpret_cast<float *>(sh.ks);  // [wave][head][dim]
+    if (lane < d) {
+#pragma unroll
+      for (int h = 0; h < FK_ATTN_MAX_GROUP; h++)
+        if ((uint32_t)h < group) pacc[(wave * FK_ATTN_MAX_GROUP + h) * FK_ATTN_MAX_DIM + lane] = acc[h];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < FK_ATTN_MAX_GROUP; h++)
+        if ((uint32_t)h < group) sh.pl[wave * FK_ATTN_MAX_GROUP + h] = l[h];
+    }
+    __syncthreads();
+    if (tid < group * d) {
+      const uint32_t h = tid / d;
+      const uint32_t i = tid % d;
+      float lt = 0.0f;
+      float at = 0.0f;
+#pragma unroll
+      for (int w = 0; w < FK_ATTN_WAVES; w++) {
+        lt = lt + sh.pl[w * FK_ATTN_MAX_GROUP + h];
+        at = at + pacc[(w * FK_ATTN_MAX_GROUP + h) * FK_ATTN_MAX_DIM + i];
+      }
+      float *o = partials + ((size_t)(g * group + h) * p.splits + t) * (d + 2);
+      if (i == 0) {
+        o[0] = split > FK_WAVE ? max_number(sh.pm[h * 2], sh.pm[h * 2 + 1]) : sh.pm[h * 2];
+        o[1] = lt;
+      }
+      o[2 + i] = at;
+    }
+  }
+}
+
+}  // namespace fk
+
+extern "C" __global__ void __launch_bounds__(FK_ATTN_THREADS)
+    fk_step_attend(const float *__restrict__ q, const float *__restrict__ knew, const float *__restrict__ vnew,
+                   uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
+                   const uint32_t *__restrict__ slot, const float *__restrict__ rope, float *__restrict__ partials,
+                   fk_step_attend_params p) {
+  __shared__ fk::AttendLds sh;
+  const uint32_t group = p.heads / p.kv_heads;
+  if (group == 4 && p.head_dim == 64 && p.split == 128 && !p.cache_bf16)
+    fk::attend_split<4, 64, 128, 0>(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+  else if (group == 4 && p.head_dim == 64 && p.split == 64 && !p.cache_bf16)
+    fk::attend_split<4, 64, 64, 0>(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+  else
+    fk::attend_split<0, 0, 0, -1>(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, p);
 }
 
 struct fk_step_combine_params {
@@ -691,7 +904,7 @@ struct fk_step_combine_params {
 // Threadgroup per head: M the largest of the splits' maxima (exact whatever
 // the order), the splits' weights w_t = exp(max_t - M) binary64's rounded
 // once, then thread i: out = (sum_t acc_t[i] w_t) / (sum_t l_t w_t), both sums
-// in split order.
+// in split order, sixteen splits' loads in flight at a time.
 extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
     fk_step_combine(const float *__restrict__ partials, float *__restrict__ out, fk_step_combine_params p) {
   __shared__ float w[256];
@@ -711,15 +924,27 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
   for (uint32_t i = threadIdx.x; i < p.head_dim; i += blockDim.x) {
     float l = 0.0f;
     float acc = 0.0f;
-    for (uint32_t t = 0; t < p.splits; t++) {
-      l = l + ph[t * stride + 1] * w[t];
-      acc = acc + ph[t * stride + 2 + i] * w[t];
+    for (uint32_t t0 = 0; t0 < p.splits; t0 += 16) {
+      float lv[16], av[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        lv[j] = av[j] = 0.0f;
+        if (t0 + j < p.splits) {
+          lv[j] = ph[(t0 + j) * stride + 1];
+          av[j] = ph[(t0 + j) * stride + 2 + i];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        if (t0 + j < p.splits) {
+          l = l + lv[j] * w[t0 + j];
+          acc = acc + av[j] * w[t0 + j];
+        }
+      }
     }
     out[(size_t)h * p.head_dim + i] = acc / l;
   }
 }
-
-// Greedy token ------------------------------------------------------------
 
 struct fk_step_argmax_params {
   uint32_t n;

@@ -33,12 +33,13 @@ class DecodeSession:
     options: PlanOptions
     embed: bool = True
     layers: Optional[int] = None
+    fuse: bool = True
 
     def __post_init__(self):
         self.program = decoder_step(self.dims, embed=self.embed, layers=self.layers)
         self.checked = check_program(self.program)
         self.plan = plan(self.options, self.checked)
-        self.lowered = lower_plan(self.checked, self.plan)
+        self.lowered = lower_plan(self.checked, self.plan, fuse=self.fuse)
         self.engine = Engine(self.device, self.kernels, self.lowered)
 
     # Synthetic state ------------------------------------------------------------

@@ -59,6 +59,8 @@ class Engine:
         for name, what in lowered.constants.items():
             if what[0] == "rope":
                 self.write(name, rope_table(*what[1:]))
+            elif what[0] == "zero":
+                self.zero(name)
             else:
                 raise ValueError(f"{name}: no constant {what[0]}")
         self._kernargs = [self._kernarg(launch) for launch in lowered.launches]

@@ -101,12 +101,15 @@ class StepAttendParams(ctypes.Structure):
         ("length", ctypes.c_uint32),
         ("slots", ctypes.c_uint32),
         ("splits", ctypes.c_uint32),
+        ("split", ctypes.c_uint32),
         ("rope", ctypes.c_uint32),
         ("rotated", ctypes.c_uint32),
         ("rope_rows", ctypes.c_uint32),
         ("scale", ctypes.c_float),
         ("window", ctypes.c_uint32),
         ("cache_bf16", ctypes.c_uint32),
+        ("store", ctypes.c_uint32),
+        ("krope", ctypes.c_uint32),
     ]
 
 
@@ -170,8 +173,8 @@ ABIS: dict[str, KernelAbi] = {
                                                               (8192, 2))},
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
-    "fk_step_attend": KernelAbi("fk_step_attend", ("q", "kc", "vc", "position", "slot", "rope", "partials"),
-                                StepAttendParams),
+    "fk_step_attend": KernelAbi("fk_step_attend", ("q", "knew", "vnew", "kc", "vc", "position", "slot", "rope",
+                                                   "partials"), StepAttendParams),
     "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams),
     "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
     "fk_step_silu_mul": KernelAbi("fk_step_silu_mul", ("a", "b", "y"), CountParams),

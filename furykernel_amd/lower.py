@@ -26,7 +26,8 @@ from .program.graph import (
 from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
 
 THREADS = 256
-ATTN_SPLIT = 128
+ATTN_SPLIT = 128      # positions a split of the attention covers (64 or 128)
+ATTN_THREADS = 512
 MAX_K = 8192
 
 # GEMV step prologue and epilogue modes (fk_step.h).
@@ -79,16 +80,71 @@ class Lowered:
         return name
 
 
-def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units: int = 256) -> Lowered:
+def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units: int = 256,
+               fuse: bool = True) -> Lowered:
     """The launches of every step of the plan, in order, for steps of `rows`
-    rows (one, a decode step's), on a device of `compute_units` CUs."""
+    rows (one, a decode step's), on a device of `compute_units` CUs; with
+    `fuse`, a KV store folded into the attention right after it."""
     if rows != 1:
         raise LoweringError(f"steps of {rows} rows: the decode kernels take one row a step")
     out = Lowered(checked.program, plan, rows)
     low = _StepLowering(out, compute_units)
     for step in plan.steps:
         out.launches.append(low.step(step))
+    if fuse:
+        _fuse_attention(out)
     return out
+
+
+def _fuse_attention(out: Lowered) -> None:
+    """Folds a KV store step into the attention step right after it that
+    reads those caches at the same position and sequence: one launch, whose
+    threadgroup holding the position stores each kv head's new rows and
+    takes them as that position's key and value, with the same arithmetic.
+    (The combine stays a launch of its own: folding it in needs every split
+    of a kv head to see the others' partials, a device-wide release and
+    acquire that costs more on this GPU than the launch it saves.)"""
+    fused: list = []
+    for launch in out.launches:
+        prev = fused[-1] if fused else None
+        merged = None
+        if prev is not None and launch.entry == "fk_step_attend" and prev.entry == "fk_step_store":
+            merged = _store_into_attend(prev, launch)
+        if merged is not None:
+            fused[-1] = merged
+        else:
+            fused.append(launch)
+    out.launches = fused
+
+
+def _store_into_attend(st: Launch, at: Launch) -> Optional[Launch]:
+    sp, ap, sb, ab = st.params, at.params, st.bind, at.bind
+    if sp["n_stores"] != 2 or ap["store"] or sb["position"] != ab["position"] or sb["slot"] != ab["slot"]:
+        return None
+    if (sp["kv_heads"], sp["head_dim"], sp["length"], sp["slots"], sp["cache_bf16"]) != (
+            ap["kv_heads"], ap["head_dim"], ap["length"], ap["slots"], ap["cache_bf16"]):
+        return None
+    if (sb["c0"], sb["c1"]) == (ab["kc"], ab["vc"]):
+        kj, vj = 0, 1
+    elif (sb["c1"], sb["c0"]) == (ab["kc"], ab["vc"]):
+        kj, vj = 1, 0
+    else:
+        return None
+    krope = sp["rope"][kj]
+    if sp["rope"][vj]:
+        return None
+    params, bind, meta = dict(ap), dict(ab), dict(at.meta)
+    if krope:
+        if ap["rope"]:
+            if sb["rope"] != ab["rope"]:
+                return None  # the key's RoPE and the query's differ: keep the store apart
+        else:
+            params.update(rotated=sp["rotated"], rope_rows=sp["rope_rows"])
+            bind["rope"] = sb["rope"]
+    meta["store_theta"] = st.meta["theta"]
+    params.update(store=1, krope=krope)
+    bind.update(knew=sb[f"x{kj}"], vnew=sb[f"x{vj}"])
+    return Launch(f"{st.step}+{at.step}", at.entry, at.groups, at.threads, bind, params, meta, at.lds_bytes)
 
 
 def rope_table(theta: float, d: int, rotated: int, rows: int) -> np.ndarray:
@@ -402,8 +458,9 @@ class _StepLowering:
         if spec.head_dim % 8:
             raise LoweringError(f"{step.name}: heads of {spec.head_dim}, not a multiple of 8")
         params = {"heads": spec.heads, "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "length": lay.length,
-                  "slots": lay.slots, "rope": 0, "rotated": 0, "rope_rows": 1,
-                  "scale": float(np.float32(spec.scale)), "window": spec.window or 0, "cache_bf16": int(bf16)}
+                  "slots": lay.slots, "split": ATTN_SPLIT, "rope": 0, "rotated": 0, "rope_rows": 1,
+                  "scale": float(np.float32(spec.scale)), "window": spec.window or 0, "cache_bf16": int(bf16),
+                  "store": 0, "krope": 0}
         meta = {"theta": 1.0}
         rope_buf = None
         q = op.q
@@ -423,6 +480,8 @@ class _StepLowering:
             qbuf = self.value(q)
         else:
             raise LoweringError(f"{step.name}: queries neither stored nor recomputed")
+        if ATTN_SPLIT not in (64, 128):
+            raise LoweringError(f"{step.name}: attention splits of {ATTN_SPLIT} positions; the kernel takes 64 or 128")
         bound = self.p.source(op.to.positions).kind.bound
         splits = -(-min(bound, lay.length if spec.window is None else bound) // ATTN_SPLIT)
         if splits > 4096:
@@ -432,9 +491,9 @@ class _StepLowering:
         pname = self.out.buffer(f"partials:{self.p.value(out).name}", "f32",
                                 spec.heads * splits * (spec.head_dim + 2))
         pos_buf = self.ints(op.to.positions)
-        bind = {"q": qbuf, "kc": kname, "vc": vname, "position": pos_buf, "slot": self.ints(op.to.sequences),
-                "rope": rope_buf or pos_buf, "partials": pname}
-        return Launch(step.name, "fk_step_attend", spec.kv_heads * splits, THREADS, bind, params, meta)
+        bind = {"q": qbuf, "knew": None, "vnew": None, "kc": kname, "vc": vname, "position": pos_buf,
+                "slot": self.ints(op.to.sequences), "rope": rope_buf or pos_buf, "partials": pname}
+        return Launch(step.name, "fk_step_attend", spec.kv_heads * splits, ATTN_THREADS, bind, params, meta)
 
     def combine_step(self, step: Step) -> Launch:
         combines = [self.p.node(w.node) for w in step.work if w.kind == COMBINE]

@@ -12,14 +12,14 @@ Counted per launch, from its parameters and the buffer types it binds:
   and the RoPE table row;
 - attention: K and V of every position the query reads (the ring up to the
   position, or the window), the query rows, the RoPE row and the partials
-  written;
+  written; with the store folded in, the new rows read and stored;
 - combine: the partials read and the combined rows written;
 - argmax, SiLU·mul: their rows.
 """
 
 from __future__ import annotations
 
-from .lower import ATTN_SPLIT, EPI_ADD_GATHER, EPI_ADD_STORED, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, \
+from .lower import EPI_ADD_GATHER, EPI_ADD_STORED, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, \
     Launch, Lowered
 
 _ELT = {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2}
@@ -67,9 +67,12 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
         elt = _elt(lowered, b["kc"])
         d = p["head_dim"]
         total = 2 * p["kv_heads"] * n * d * elt + p["heads"] * d * 4 + 8
-        total += p["heads"] * -(-n // ATTN_SPLIT) * (d + 2) * 4
-        if p["rope"]:
+        partials = p["heads"] * -(-n // p["split"]) * (d + 2) * 4
+        total += partials
+        if p["rope"] or p["krope"]:
             total += p["rotated"] * 8
+        if p["store"]:
+            total += 2 * p["kv_heads"] * d * (4 + elt)
         return total
     if e == "fk_step_combine":
         d = p["head_dim"]

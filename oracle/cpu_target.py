@@ -68,12 +68,17 @@ class CpuTarget:
                                     int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0]),
                                     p["cache_bf16"])
         elif e == "fk_step_attend":
-            st = L.fkref_step_attend(self._p(b["q"]), self._p(b["kc"]), self._p(b["vc"]), self._p(b["partials"]),
-                                     p["heads"], p["kv_heads"], p["head_dim"], p["length"], p["slots"],
-                                     p["splits"], p["rope"], p["rotated"], launch.meta["theta"], p["scale"],
-                                     p["window"],
-                                     int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0]),
-                                     p["cache_bf16"])
+            # The store the launch may do first, then the attention.
+            pos, slot = int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0])
+            st = 0
+            if p["store"]:
+                st = L.fkref_step_store(self._p(b["knew"]), self._p(b["vnew"]), self._p(b["kc"]), self._p(b["vc"]),
+                                        2, p["krope"], 0, p["kv_heads"], p["head_dim"], p["length"], p["slots"],
+                                        p["rotated"], launch.meta["store_theta"], pos, slot, p["cache_bf16"])
+            st = st or L.fkref_step_attend(self._p(b["q"]), self._p(b["kc"]), self._p(b["vc"]),
+                                           self._p(b["partials"]), p["heads"], p["kv_heads"], p["head_dim"],
+                                           p["length"], p["slots"], p["splits"], p["split"], p["rope"], p["rotated"],
+                                           launch.meta["theta"], p["scale"], p["window"], pos, slot, p["cache_bf16"])
         elif e == "fk_step_combine":
             st = L.fkref_step_combine(self._p(b["partials"]), self._p(b["out"]), p["heads"], p["head_dim"],
                                       p["splits"])

@@ -440,17 +440,20 @@ int fkref_step_store(const float *x0, const float *x1, uint16_t *c0, uint16_t *c
   return 0;
 }
 
-#define SPLIT 128
+#define SPLIT_MAX 128
+#define ATTEND_CHUNKS 8
 
 int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
-                      int kv_heads, int head_dim, int length, int slots, int splits, int rope, int rotated,
-                      float theta, float scale, int window, uint32_t position, uint32_t slot, int cache_bf16) {
+                      int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
+                      int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
+                      int cache_bf16) {
   const int group = heads / kv_heads;
   const int d = head_dim;
-  if (group > 8 || d > 64) return -1;
+  const uint32_t SPLIT = (uint32_t)split;
+  if (group > 8 || d > 64 || split < ATTEND_CHUNKS || split > SPLIT_MAX || split % ATTEND_CHUNKS) return -1;
   uint32_t s = slot < (uint32_t)slots ? slot : 0;
   float qs[8 * 64];
-  float wt[8 * SPLIT];
+  float wt[8 * SPLIT_MAX];
   float mx[8];
   uint32_t first = (window && position + 1 > (uint32_t)window) ? position + 1 - (uint32_t)window : 0;
   for (int g = 0; g < kv_heads; g++) {
@@ -478,16 +481,26 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
       }
       for (int h = 0; h < group; h++)
         for (int r = 0; r < count; r++) wt[h * SPLIT + r] = fkref_exp(wt[h * SPLIT + r] - mx[h]);
+      /* The weights' sum and the weighted values: the split's positions in
+       * ATTEND_CHUNKS runs of split / ATTEND_CHUNKS, each summed in order of
+       * position from +0, then the runs' sums added in order. */
+      const int run = split / ATTEND_CHUNKS;
       for (int h = 0; h < group; h++) {
         float *out = partials + ((size_t)(g * group + h) * splits + t) * (d + 2);
         for (int i = 0; i < d; i++) {
           float l = 0.0f;
           float acc = 0.0f;
-          for (int r = 0; r < count; r++) {
-            size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
-            float w = wt[h * SPLIT + r];
-            l = l + w;
-            acc = acc + w * widen_cache(vc[at + i], cache_bf16);
+          for (int c = 0; c < ATTEND_CHUNKS; c++) {
+            float lc = 0.0f;
+            float ac = 0.0f;
+            for (int r = c * run; r < (c + 1) * run && r < count; r++) {
+              size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
+              float w = wt[h * SPLIT + r];
+              lc = lc + w;
+              ac = ac + w * widen_cache(vc[at + i], cache_bf16);
+            }
+            l = l + lc;
+            acc = acc + ac;
           }
           if (i == 0) {
             out[0] = mx[h];

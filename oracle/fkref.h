@@ -104,11 +104,14 @@ int fkref_step_store(const float *x0, const float *x1, uint16_t *c0, uint16_t *c
                      int rope1, int kv_heads, int head_dim, int length, int slots, int rotated, float theta,
                      uint32_t position, uint32_t slot, int cache_bf16);
 
-/* Attention partials over splits of 128 positions per KV head:
- * partials[((h * splits + t) * (d + 2))] = [max, sum, acc[d]]. */
+/* Attention partials over splits of `split` (at most 128, a multiple of 8)
+ * positions per KV head: partials[((h * splits + t) * (d + 2))] =
+ * [max, sum, acc[d]]; the sums over 8 runs of split / 8 positions, each in
+ * order of position, then the runs in order. */
 int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
-                      int kv_heads, int head_dim, int length, int slots, int splits, int rope, int rotated,
-                      float theta, float scale, int window, uint32_t position, uint32_t slot, int cache_bf16);
+                      int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
+                      int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
+                      int cache_bf16);
 
 /* The splits combined once, in split order. */
 int fkref_step_combine(const float *partials, float *out, int heads, int head_dim, int splits);

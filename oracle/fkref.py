@@ -53,7 +53,7 @@ def lib() -> ctypes.CDLL:
             "fkref_rope_elem": (ctypes.c_float, [_vp, _i, _i, _i, ctypes.c_uint32, ctypes.c_float]),
             "fkref_step_store": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
                                       ctypes.c_uint32, ctypes.c_uint32, _i]),
-            "fkref_step_attend": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
+            "fkref_step_attend": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
                                        ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32, _i]),
             "fkref_step_combine": (_i, [_vp, _vp, _i, _i, _i]),
             "fkref_argmax": (ctypes.c_uint32, [_vp, _i]),

@@ -44,14 +44,16 @@ def compare_all(session, cpu, names=None):
     return bad
 
 
-@pytest.mark.parametrize("position", [0, 16, 31])
-def test_tiny_decode_step_bit_exact(device, kernels, position):
-    s = DecodeSession(device, kernels, TINY32, PlanOptions(), embed=False)
+@pytest.mark.parametrize("position,fuse", [(0, True), (16, True), (31, True), (0, False), (31, False)])
+def test_tiny_decode_step_bit_exact(device, kernels, position, fuse):
+    """With the KV store and the combine folded into the attention launch
+    (fuse), and as the plan's separate store, attention and combine steps."""
+    s = DecodeSession(device, kernels, TINY32, PlanOptions(), embed=False, fuse=fuse)
     try:
         s.init_synthetic()
         s.set_position(position)
         cpu = mirror(s)
-        print(f"tiny decode at position {position}: {len(s.lowered.launches)} launches", flush=True)
+        print(f"tiny decode at position {position} (fuse {fuse}): {len(s.lowered.launches)} launches", flush=True)
         s.step()
         device.sync()
         cpu.run()

@@ -1,0 +1,89 @@
+"""The lowering of planned steps to launches, on the CPU: which launches a
+decoder step becomes, and that the attention launch which folds in the KV
+store before it computes, in the oracle's CPU target, exactly what the
+plan's separate store and attention steps compute."""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+from furykernel_amd.lower import LoweringError, lower_plan, rope_table
+from furykernel_amd.program.check import check_program
+from furykernel_amd.program.decoder import ONE_B, TINY, decoder_step
+from furykernel_amd.program.plan import PlanOptions, plan
+from oracle.cpu_target import CpuTarget
+
+TINY32 = dataclasses.replace(TINY, context=32)
+
+
+def lowered(dims, options=PlanOptions(), fuse=True, embed=False, layers=None):
+    checked = check_program(decoder_step(dims, embed=embed, layers=layers))
+    return lower_plan(checked, plan(options, checked), fuse=fuse)
+
+
+def seeded(low, seed, position, width=64):
+    """A CPU target with every buffer the step reads drawn from a seeded
+    stream: weights 0.02 N(0, 1) (norm gains 1), caches N(0, 1), inputs
+    0.02 N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    cpu = CpuTarget(low, width)
+    for name, spec in sorted(low.buffers.items()):
+        buf = cpu.buffers[name]
+        if name.startswith("weight:"):
+            if "norm" in name:
+                buf[:] = 1
+            else:
+                buf[:] = (rng.standard_normal(spec.count) * 0.02).astype(buf.dtype)
+        elif name.startswith("cache:"):
+            buf[:] = rng.standard_normal(spec.count).astype(np.float16).view(buf.dtype)
+        elif name.startswith("value:"):
+            buf[:] = (rng.standard_normal(spec.count) * 0.02).astype(buf.dtype)
+    for name, what in low.constants.items():
+        if what[0] == "rope":
+            cpu.write(name, rope_table(*what[1:]))
+    cpu.write("ints:position", [position])
+    return cpu
+
+
+def test_a_1b_layer_is_six_launches():
+    low = lowered(ONE_B, embed=True)
+    entries = [launch.entry for launch in low.launches]
+    assert len(entries) == 16 * 6 + 2
+    assert entries[:6] == ["fk_step_gemv_f16_r1", "fk_step_attend", "fk_step_combine"] + \
+        ["fk_step_gemv_f16_r1"] * 3
+    attend = low.launches[1]
+    assert attend.step == "s1_store+s2_attend"
+    assert (attend.params["store"], attend.params["krope"]) == (1, 1)
+    assert attend.groups == ONE_B.kv_heads * attend.params["splits"]
+
+
+def test_unfused_lowering_keeps_the_plans_steps():
+    low = lowered(ONE_B, embed=True, fuse=False)
+    assert [launch.entry for launch in low.launches[:7]] == [
+        "fk_step_gemv_f16_r1", "fk_step_store", "fk_step_attend", "fk_step_combine"] + ["fk_step_gemv_f16_r1"] * 3
+
+
+@pytest.mark.parametrize("position", [0, 5, 31])
+@pytest.mark.parametrize("options", [PlanOptions(), PlanOptions(store_gelus=True)])
+def test_fused_attention_computes_the_two_steps(position, options):
+    fused, apart = lowered(TINY32, options), lowered(TINY32, options, fuse=False)
+    assert len(apart.launches) - len(fused.launches) == TINY32.layers
+    a, b = seeded(fused, 7, position), seeded(apart, 7, position)
+    a.run()
+    b.run()
+    for name in apart.buffers:
+        assert np.array_equal(a.read(name).view(np.uint8), b.read(name).view(np.uint8)), name
+
+
+def test_bf16_caches_fuse_the_same_way():
+    dims = dataclasses.replace(TINY32, cache_elem="bf16")
+    try:
+        fused, apart = lowered(dims), lowered(dims, fuse=False)
+    except (LoweringError, ValueError) as e:  # a program the gate refuses needs no lowering test
+        pytest.skip(f"bf16 caches: {e}")
+    a, b = seeded(fused, 9, 17), seeded(apart, 9, 17)
+    a.run()
+    b.run()
+    for name in apart.buffers:
+        assert np.array_equal(a.read(name).view(np.uint8), b.read(name).view(np.uint8)), name
