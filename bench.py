@@ -36,6 +36,17 @@ HBM_PEAK_GBPS = 8000.0
 POSITION = 4095
 
 
+def _plan_options():
+    from furykernel_amd.program.plan import PlanOptions
+
+    # The SiLU·mul stored once (folded into the gate/up step) rather than
+    # recomputed by every threadgroup of the down projection.
+    return PlanOptions(store_gelus=True)
+
+
+PLAN = None
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -57,10 +68,10 @@ def lowered_for(dims, layers=None):
     from furykernel_amd.lower import lower_plan
     from furykernel_amd.program.check import check_program
     from furykernel_amd.program.decoder import decoder_step
-    from furykernel_amd.program.plan import PlanOptions, plan
+    from furykernel_amd.program.plan import plan
 
     checked = check_program(decoder_step(dims, embed=True, layers=layers))
-    return lower_plan(checked, plan(PlanOptions(), checked))
+    return lower_plan(checked, plan(_plan_options(), checked))
 
 
 def kernel_table(session, reps: int, eager: bool) -> dict:
@@ -156,12 +167,14 @@ def main() -> int:
     from furykernel_amd import kernels, runtime
     from furykernel_amd.decode import DecodeSession
     from furykernel_amd.program.decoder import ONE_B
-    from furykernel_amd.program.plan import PlanOptions
     from furykernel_amd.traffic import step_bytes
+
+    global PLAN
+    PLAN = _plan_options()
 
     dev = runtime.Device(0)
     ks = kernels.Kernels(dev)
-    session = DecodeSession(dev, ks, ONE_B, PlanOptions(), embed=True)
+    session = DecodeSession(dev, ks, ONE_B, PLAN, embed=True)
     session.init_synthetic()
     session.set_position(POSITION, token=7)
     log(f"{len(session.lowered.launches)} launches a step resident in HBM; "
@@ -171,8 +184,7 @@ def main() -> int:
                        context=ONE_B.context, step=0)
 
         def run():
-            session.engine.enqueue()
-            session.engine.enqueue_advance(**advance)
+            session.engine.enqueue(advance=advance)
     else:
         graph = session.graph(advance_position=False)
         run = graph.replay

@@ -518,6 +518,12 @@ int fk_event_sync(fk_event *e) {
   return FK_OK;
 }
 
+int fk_stream_wait_event(fk_stream *s, fk_event *e) {
+  if (!e) return fail(nullptr, FK_ERR_ARG, "fk_stream_wait_event: null event");
+  FK_HIP(e->ctx, hipStreamWaitEvent(stream_of(e->ctx, s), e->event, 0));
+  return FK_OK;
+}
+
 int fk_event_elapsed_ms(fk_event *a, fk_event *b, float *ms) {
   if (!a || !b || !ms) return fail(a ? a->ctx : nullptr, FK_ERR_ARG, "fk_event_elapsed_ms: null argument");
   FK_HIP(a->ctx, hipEventElapsedTime(ms, a->event, b->event));

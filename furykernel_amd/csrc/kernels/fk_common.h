@@ -18,19 +18,50 @@ namespace fk {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 
-// The sum of a value over the wavefront's 64 lanes, in every lane, pairwise,
-// neighbours first: ((x0 + x1) + (x2 + x3)) + ... (src/FuryKernel/IR.hs:269-283).
-// Step m adds the value of lane l ^ m, which holds the sum of the sibling
-// block of m lanes; IEEE addition commutes, so both lanes of a pair hold the
-// same bits and every lane ends with the pairwise tree's root.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// The sum of a value over the wavefront's 64 lanes, pairwise, neighbours
+// first: ((x0 + x1) + (x2 + x3)) + ... (src/FuryKernel/IR.hs:269-283), the same
+// value in every lane.  Within each row of 16 lanes by DPP: lane l adds the
+// value of lane l ^ 1, then l ^ 2 (quad permutes); after those, the four lanes
+// of a quad hold the same bits (IEEE addition commutes), so the half-row
+// mirror adds the other quad's sum and the row mirror the other half's.  The
+// four rows' sums (lanes 0, 16, 32, 48) are then added as (r0 + r1) + (r2 + r3).
 __device__ __forceinline__ float wave_sum(float v) {
-  v = v + __shfl_xor(v, 1);
-  v = v + __shfl_xor(v, 2);
-  v = v + __shfl_xor(v, 4);
-  v = v + __shfl_xor(v, 8);
-  v = v + __shfl_xor(v, 16);
-  v = v + __shfl_xor(v, 32);
-  return v;
+  v = v + dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = v + dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = v + dpp_f<0x141>(v);  // row_half_mirror
+  v = v + dpp_f<0x140>(v);  // row_mirror
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+// R sums at once, each wave_sum's tree: the DPP steps of the R values
+// interleaved so their latencies overlap.
+template <int R>
+__device__ __forceinline__ void wave_sums(float (&v)[R]) {
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = v[q] + dpp_f<0xB1>(v[q]);
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = v[q] + dpp_f<0x4E>(v[q]);
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = v[q] + dpp_f<0x141>(v[q]);
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = v[q] + dpp_f<0x140>(v[q]);
+#pragma unroll
+  for (int q = 0; q < R; q++)
+    v[q] = (readlane_f(v[q], 0) + readlane_f(v[q], 16)) + (readlane_f(v[q], 32) + readlane_f(v[q], 48));
 }
 
 // IEEE 754-2019 maximumNumber with +0 above -0 (src/FuryKernel/Interp.hs:952-956).
@@ -54,15 +85,20 @@ __device__ __forceinline__ float from_max_key(int k) {
   return __uint_as_float(k < 0 ? (uint32_t)k ^ 0x7FFFFFFFu : (uint32_t)k);
 }
 
-// The maximum over the wavefront, pairwise as the sum.
-__device__ __forceinline__ float wave_max(float v) {
-  v = max_number(v, __shfl_xor(v, 1));
-  v = max_number(v, __shfl_xor(v, 2));
-  v = max_number(v, __shfl_xor(v, 4));
-  v = max_number(v, __shfl_xor(v, 8));
-  v = max_number(v, __shfl_xor(v, 16));
-  v = max_number(v, __shfl_xor(v, 32));
-  return v;
+// The wavefront's maximumNumber, every lane, on max_key's integers: within
+// rows of 16 lanes by DPP (pairs, quads, halves, rows), then across the four
+// rows.  Exact whatever the order.
+__device__ __forceinline__ float wave_max(float x) {
+  int v = max_key(x);
+  v = max(v, dpp_i<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = max(v, dpp_i<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = max(v, dpp_i<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_i<0x140>(v));  // row_mirror
+  const int a = __builtin_amdgcn_readlane(v, 0);
+  const int b = __builtin_amdgcn_readlane(v, 16);
+  const int c = __builtin_amdgcn_readlane(v, 32);
+  const int d = __builtin_amdgcn_readlane(v, 48);
+  return from_max_key(max(max(a, b), max(c, d)));
 }
 
 // tgReduceSum / tgReduceMax (src/FuryKernel/Reduce.hs:55-85): each wave's

@@ -3,9 +3,7 @@
 // set the grid, its recomputed values run in every threadgroup before them,
 // its epilogues run on a linear layer's tile.
 //
-//   fk_step_gemv_*   recompute (RMSNorm of a stored row or a gathered
-//                    embedding row, SiLU·mul of two stored rows) → anchors
-//                    (linear layers sharing the input) → epilogue (residual add)
+//   fk_step_gemv_*   (fk_step_gemv.h) recompute → anchors → epilogue
 //   fk_step_store    recompute RoPE of k → effects: KV stores into ring caches
 //   fk_step_attend   recompute RoPE of q → anchor: attention over a split of
 //                    positions for one KV head, stored as partials
@@ -22,486 +20,9 @@
 #pragma once
 
 #include "fk_common.h"
-#include "fk_gemv.h"
+#include "fk_step_gemv.h"
 
-#define FK_STEP_MAX_K 8192
 #define FK_STEP_THREADS 256
-
-// Prologue modes: how a GEMV step's threadgroups make the anchors' input row.
-enum : uint32_t {
-  FK_PRO_STORED = 0,          // x = src
-  FK_PRO_RMSNORM = 1,         // x = rmsnorm(src) * gamma * factor
-  FK_PRO_GATHER = 2,          // x = table[token] * gfactor
-  FK_PRO_GATHER_RMSNORM = 3,  // x = rmsnorm(table[token] * gfactor) * gamma * factor
-  FK_PRO_SILU_MUL = 4,        // x = silu(src) * src2
-};
-
-// Epilogue modes: elementwise work on the anchor's tile.
-enum : uint32_t {
-  FK_EPI_NONE = 0,
-  FK_EPI_ADD_STORED = 1,  // out = res + tile
-  FK_EPI_ADD_GATHER = 2,  // out = table[token] * gfactor + tile
-};
-
-struct fk_step_gemv_params {
-  uint32_t n_anchors;  // 1 to 3
-  uint32_t rows[3];    // each anchor's outputs
-  uint32_t first_group[4];  // anchor j's row blocks are [first_group[j], first_group[j+1])
-  uint32_t k;          // the input row's width
-  uint32_t pro_mode;
-  uint32_t seg;        // RMSNorm's segment (k, one segment)
-  float eps;
-  float factor;        // RMSNorm's factor
-  float gfactor;       // the gather's factor
-  uint32_t has_gamma;
-  uint32_t epi_mode;
-  uint32_t store_tile;  // the anchors' own values are stored (into y[j])
-  uint32_t table_rows;  // the gathered table's rows: a token past them reads its last (the engine refuses one)
-};
-
-namespace fk {
-
-// The row of `table` a token names, times the factor: a gather of one row
-// (src/FuryKernel/Program/Eval.hs:528-535).
-template <typename TT>
-__device__ __forceinline__ float gathered(const TT *__restrict__ table, uint32_t token, uint32_t k, uint32_t i,
-                                          float f) {
-  return (float)table[(size_t)token * k + i] * f;
-}
-
-// RMSNorm of a row held in LDS `xs` (k elements, segments of `seg`), in place:
-// per segment the threads' sums of squares over packs of 4 in tgReduceSum's
-// order, scale = rsqrt(sum / seg + eps) in binary64 rounded once, then
-// ((x * scale) * gamma) * factor.
-__device__ __forceinline__ void rmsnorm_lds(float *xs, uint32_t k, uint32_t seg, float eps, float factor,
-                                            const float *__restrict__ gamma, float *slots) {
-  for (uint32_t s0 = 0; s0 < k; s0 += seg) {
-    const uint32_t packs = seg / 4;
-    float acc = 0.0f;
-    for (uint32_t j = threadIdx.x; j < packs; j += blockDim.x) {
-      const float *v = xs + s0 + 4 * j;
-      acc = acc + v[0] * v[0];
-      acc = acc + v[1] * v[1];
-      acc = acc + v[2] * v[2];
-      acc = acc + v[3] * v[3];
-    }
-    const float total = block_reduce<false>(acc, slots);
-    const float scale = rsqrt_once(total / (float)seg + eps);
-    for (uint32_t i = threadIdx.x; i < seg; i += blockDim.x) {
-      float v = xs[s0 + i] * scale;
-      if (gamma) v = v * gamma[i];
-      if (factor != 1.0f) v = v * factor;
-      xs[s0 + i] = v;
-    }
-    __syncthreads();
-  }
-}
-
-// SiLU(a) · b: a / (1 + e^-a), e^-a binary64's rounded once, then times b.
-__device__ __forceinline__ float silu_mul(float a, float b) {
-  const float e = exp_once(-a);
-  const float d = 1.0f + e;
-  return (a / d) * b;
-}
-
-// An anchor's pointer or count by index, without indexing an array: a
-// dynamically indexed array of kernel pointers would lose their address space
-// (its loads would become flat loads, which wait with LDS traffic).
-template <typename T>
-__device__ __forceinline__ T pick3(uint32_t a, T x0, T x1, T x2) {
-  return a == 0 ? x0 : (a == 1 ? x1 : x2);
-}
-
-// Which anchor row r of the numbered rows belongs to.
-__device__ __forceinline__ uint32_t anchor_of(uint32_t r, const fk_step_gemv_params &p) {
-  return (p.n_anchors > 1 && r >= p.first_group[1] ? 1u : 0u) + (p.n_anchors > 2 && r >= p.first_group[2] ? 1u : 0u);
-}
-
-}  // namespace fk
-
-// The prologue of a GEMV step in two halves, so that its loads are issued
-// before the weights' and its arithmetic runs while the weights stream in
-// (the wave waits for loads in the order it issued them).  Thread t holds
-// packs t, t + T, ... of the row (NPK of them at most, 4 elements each), the
-// order RMSNorm's sum of squares takes them in.
-template <typename WT, int NPK>
-struct Prologue {
-  float4 x[NPK];
-  float4 x2[NPK];
-  float4 g[NPK];
-
-  __device__ __forceinline__ void load(const float *__restrict__ src, const float *__restrict__ src2,
-                                       const float *__restrict__ gamma, const WT *__restrict__ table,
-                                       const uint32_t *__restrict__ token, const fk_step_gemv_params &p) {
-    const uint32_t packs = p.k / 4;
-    const bool gather = p.pro_mode == FK_PRO_GATHER || p.pro_mode == FK_PRO_GATHER_RMSNORM;
-    const uint32_t tok = gather ? min(token[0], p.table_rows - 1) : 0;
-#pragma unroll
-    for (int m = 0; m < NPK; m++) {
-      const uint32_t j = threadIdx.x + m * blockDim.x;
-      const bool in = j < packs;
-      if (gather) {
-        const WT *row = table + (size_t)tok * p.k + 4 * j;
-        x[m] = in ? make_float4((float)row[0], (float)row[1], (float)row[2], (float)row[3]) : make_float4(0, 0, 0, 0);
-      } else {
-        x[m] = in ? reinterpret_cast<const float4 *>(src)[j] : make_float4(0, 0, 0, 0);
-      }
-      x2[m] = (in && p.pro_mode == FK_PRO_SILU_MUL) ? reinterpret_cast<const float4 *>(src2)[j]
-                                                     : make_float4(0, 0, 0, 0);
-      g[m] = (in && p.has_gamma && (p.pro_mode == FK_PRO_RMSNORM || p.pro_mode == FK_PRO_GATHER_RMSNORM))
-                 ? reinterpret_cast<const float4 *>(gamma)[j % (p.seg / 4)]
-                 : make_float4(1, 1, 1, 1);
-    }
-  }
-
-  // The anchors' input row into `xs`: gathered rows times the factor, SiLU·mul,
-  // or RMSNorm (one segment, the row) of them; a barrier after.
-  __device__ __forceinline__ void finish(float *xs, float *slots, const fk_step_gemv_params &p) {
-    const uint32_t packs = p.k / 4;
-    const bool gather = p.pro_mode == FK_PRO_GATHER || p.pro_mode == FK_PRO_GATHER_RMSNORM;
-#pragma unroll
-    for (int m = 0; m < NPK; m++) {
-      if (gather) {
-        x[m].x = x[m].x * p.gfactor;
-        x[m].y = x[m].y * p.gfactor;
-        x[m].z = x[m].z * p.gfactor;
-        x[m].w = x[m].w * p.gfactor;
-      } else if (p.pro_mode == FK_PRO_SILU_MUL) {
-        x[m] = make_float4(fk::silu_mul(x[m].x, x2[m].x), fk::silu_mul(x[m].y, x2[m].y),
-                           fk::silu_mul(x[m].z, x2[m].z), fk::silu_mul(x[m].w, x2[m].w));
-      }
-    }
-    if (p.pro_mode == FK_PRO_RMSNORM || p.pro_mode == FK_PRO_GATHER_RMSNORM) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int m = 0; m < NPK; m++) {
-        if (threadIdx.x + m * blockDim.x < packs) {
-          acc = acc + x[m].x * x[m].x;
-          acc = acc + x[m].y * x[m].y;
-          acc = acc + x[m].z * x[m].z;
-          acc = acc + x[m].w * x[m].w;
-        }
-      }
-      const float total = fk::block_reduce<false>(acc, slots);
-      const float scale = fk::rsqrt_once(total / (float)p.seg + p.eps);
-#pragma unroll
-      for (int m = 0; m < NPK; m++) {
-        float o[4] = {x[m].x * scale, x[m].y * scale, x[m].z * scale, x[m].w * scale};
-        if (p.has_gamma) {
-          o[0] = o[0] * g[m].x;
-          o[1] = o[1] * g[m].y;
-          o[2] = o[2] * g[m].z;
-          o[3] = o[3] * g[m].w;
-        }
-        if (p.factor != 1.0f) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) o[e] = o[e] * p.factor;
-        }
-        x[m] = make_float4(o[0], o[1], o[2], o[3]);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < NPK; m++) {
-      const uint32_t j = threadIdx.x + m * blockDim.x;
-      if (j < packs) reinterpret_cast<float4 *>(xs)[j] = x[m];
-    }
-    __syncthreads();
-  }
-};
-
-// A GEMV step's threadgroups are persistent: the grid is what fits on the
-// device at once, each threadgroup makes the anchors' input row once (its
-// prologue) and its wavefronts then take row blocks of R rows in turn, block
-// b, b + (all wavefronts), ...  The anchors' rows are numbered one after
-// another.  While a wavefront computes a block, the first PF packs of its next
-// block are already loading; its first block's packs load before the prologue
-// runs, since weights don't depend on it.
-template <typename WT, int P, int R, int PF>
-__device__ __forceinline__ void step_gemv_body(const WT *__restrict__ w0, const WT *__restrict__ w1,
-                                               const WT *__restrict__ w2, float *__restrict__ y0,
-                                               float *__restrict__ y1, float *__restrict__ y2,
-                                               const float *__restrict__ src, const float *__restrict__ src2,
-                                               const float *__restrict__ gamma, const WT *__restrict__ table,
-                                               const uint32_t *__restrict__ token, const float *__restrict__ res,
-                                               const WT *__restrict__ res_table, const uint32_t *__restrict__ res_token,
-                                               float *__restrict__ epi_out, const fk_step_gemv_params &p) {
-  __shared__ float xs[FK_STEP_MAX_K];
-  __shared__ float slots[16];
-  constexpr int C = P / 4;
-  constexpr int U = P * sizeof(WT) / 16;
-  const uint32_t k = p.k;
-  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
-  const uint32_t waves = blockDim.x / FK_WAVE;
-  const uint32_t total_waves = gridDim.x * waves;
-  const uint32_t packs = k / P;
-  // Row blocks: anchor a's rows are blocks [first_group[a], first_group[a + 1]).
-  const uint32_t blocks = p.first_group[p.n_anchors];
-
-  // Where block b's rows are: its anchor, and the W rows of its R rows.
-  auto locate = [&](uint32_t b, uint32_t &a, uint32_t &row0, const WT *(&wr)[R]) {
-    a = fk::anchor_of(b, p);
-    row0 = (b - fk::pick3(a, p.first_group[0], p.first_group[1], p.first_group[2])) * R;
-    const uint32_t n = fk::pick3(a, p.rows[0], p.rows[1], p.rows[2]);
-    const WT *wa = fk::pick3(a, w0, w1, w2);
-#pragma unroll
-    for (int q = 0; q < R; q++) wr[q] = wa + (size_t)min(row0 + q, n - 1) * k;
-  };
-  auto prefetch = [&](const WT *(&wr)[R], uint4 (&pre)[PF][R][U], bool live) {
-#pragma unroll
-    for (int it = 0; it < PF; it++) {
-      const uint32_t j = lane + it * FK_WAVE;
-#pragma unroll
-      for (int q = 0; q < R; q++)
-#pragma unroll
-        for (int u = 0; u < U; u++)
-          pre[it][q][u] = (live && j < packs) ? reinterpret_cast<const uint4 *>(wr[q] + (size_t)j * P)[u]
-                                              : make_uint4(0, 0, 0, 0);
-    }
-  };
-
-  uint32_t b = blockIdx.x * waves + threadIdx.x / FK_WAVE;
-  uint32_t a, row0;
-  const WT *wr[R];
-  uint4 cur[PF][R][U];
-  Prologue<WT, FK_STEP_MAX_K / (4 * 512)> pro;
-  pro.load(src, src2, gamma, table, token, p);
-  locate(b < blocks ? b : 0, a, row0, wr);
-  prefetch(wr, cur, b < blocks);
-  pro.finish(xs, slots, p);
-  const uint32_t rtok = (p.epi_mode == FK_EPI_ADD_GATHER) ? min(res_token[0], p.table_rows - 1) : 0;
-
-  for (; b < blocks; b += total_waves) {
-    const uint32_t nb = b + total_waves;
-    uint32_t na = 0, nrow0 = 0;
-    const WT *nwr[R];
-    uint4 nxt[PF][R][U];
-    locate(nb < blocks ? nb : b, na, nrow0, nwr);
-    prefetch(nwr, nxt, nb < blocks);
-
-    // The block's rows, in the reference GEMV's order.
-    float acc[R][C];
-#pragma unroll
-    for (int q = 0; q < R; q++)
-#pragma unroll
-      for (int c = 0; c < C; c++) acc[q][c] = 0.0f;
-    auto consume = [&](uint32_t j, const uint4 (&wv4)[R][U]) {
-      float xv[P];
-#pragma unroll
-      for (int e = 0; e < P; e++) xv[e] = xs[j * P + e];
-#pragma unroll
-      for (int q = 0; q < R; q++) {
-        float wv[P];
-        fk::unpack<P>(wv4[q], wv, WT{});
-#pragma unroll
-        for (int c = 0; c < C; c++) {
-          float p0 = xv[4 * c] * wv[4 * c];
-          float p1 = xv[4 * c + 1] * wv[4 * c + 1];
-          float p2 = xv[4 * c + 2] * wv[4 * c + 2];
-          float p3 = xv[4 * c + 3] * wv[4 * c + 3];
-          acc[q][c] = acc[q][c] + ((p0 + p1) + (p2 + p3));
-        }
-      }
-    };
-#pragma unroll
-    for (int it = 0; it < PF; it++) {
-      const uint32_t j = lane + it * FK_WAVE;
-      if (j < packs) consume(j, cur[it]);
-    }
-#pragma unroll 4
-    for (uint32_t j = lane + PF * FK_WAVE; j < packs; j += FK_WAVE) {
-      uint4 wv4[R][U];
-#pragma unroll
-      for (int q = 0; q < R; q++)
-#pragma unroll
-        for (int u = 0; u < U; u++) wv4[q][u] = reinterpret_cast<const uint4 *>(wr[q] + (size_t)j * P)[u];
-      consume(j, wv4);
-    }
-    const uint32_t n = fk::pick3(a, p.rows[0], p.rows[1], p.rows[2]);
-    float *ya = fk::pick3(a, y0, y1, y2);
-#pragma unroll
-    for (int q = 0; q < R; q++) {
-      float t = acc[q][0];
-#pragma unroll
-      for (int c = 1; c < C; c++) t = t + acc[q][c];
-      t = fk::wave_sum(t);
-      const uint32_t row = row0 + q;
-      if (lane == 0 && row < n) {
-        if (p.store_tile) ya[row] = t;
-        if (p.epi_mode == FK_EPI_ADD_STORED) {
-          epi_out[row] = res[row] + t;
-        } else if (p.epi_mode == FK_EPI_ADD_GATHER) {
-          epi_out[row] = fk::gathered(res_table, rtok, n, row, p.gfactor) + t;
-        }
-      }
-    }
-    a = na;
-    row0 = nrow0;
-#pragma unroll
-    for (int q = 0; q < R; q++) wr[q] = nwr[q];
-#pragma unroll
-    for (int it = 0; it < PF; it++)
-#pragma unroll
-      for (int q = 0; q < R; q++)
-#pragma unroll
-        for (int u = 0; u < U; u++) cur[it][q][u] = nxt[it][q][u];
-  }
-}
-
-// Buffers in binding order, then the parameter struct.
-#define FK_STEP_GEMV_ENTRY(NAME, WT, P, R, PF)                                                                      \
-  extern "C" __global__ void __launch_bounds__(512)                                                                 \
-      NAME(const WT *__restrict__ w0, const WT *__restrict__ w1, const WT *__restrict__ w2, float *__restrict__ y0, \
-           float *__restrict__ y1, float *__restrict__ y2, const float *__restrict__ src,                          \
-           const float *__restrict__ src2, const float *__restrict__ gamma, const WT *__restrict__ table,           \
-           const uint32_t *__restrict__ token, const float *__restrict__ res, const WT *__restrict__ res_table,     \
-           const uint32_t *__restrict__ res_token, float *__restrict__ epi_out, fk_step_gemv_params p) {           \
-    step_gemv_body<WT, P, R, PF>(w0, w1, w2, y0, y1, y2, src, src2, gamma, table, token, res, res_table, res_token, \
-                                 epi_out, p);                                                                       \
-  }
-
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r1, _Float16, 8, 1, 4)
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r2, _Float16, 8, 2, 4)
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r4, _Float16, 8, 4, 2)
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f16_r1p8, _Float16, 8, 1, 8)
-FK_STEP_GEMV_ENTRY(fk_step_gemv_f32_r1, float, 4, 1, 4)
-
-// GEMV steps of a known input width: every row's weights in registers.
-//
-// A wavefront takes ROWS consecutive rows (numbered across the anchors) and
-// the input width is 64 * P * PPL, so lane l's packs are l, l + 64, ... (PPL
-// of them) of each row.  The wavefront issues all ROWS * PPL of its 16-byte
-// weight loads when it starts, before the prologue: the whole matrix is
-// requested at once and the prologue runs under the loads.  The input row
-// lives in dynamic LDS (k floats); with PPL <= 4 each lane keeps its x packs
-// in registers for all its rows.  Each row's lane totals are reduced across
-// the wavefront together at the end, ROWS independent pairwise trees.
-// Same order, same bits as step_gemv_body.
-template <typename WT, int P, int ROWS, int PPL>
-__device__ __forceinline__ void step_gemv_resident(const WT *__restrict__ w0, const WT *__restrict__ w1,
-                                                   const WT *__restrict__ w2, float *__restrict__ y0,
-                                                   float *__restrict__ y1, float *__restrict__ y2,
-                                                   const float *__restrict__ src, const float *__restrict__ src2,
-                                                   const float *__restrict__ gamma, const WT *__restrict__ table,
-                                                   const uint32_t *__restrict__ token, const float *__restrict__ res,
-                                                   const WT *__restrict__ res_table,
-                                                   const uint32_t *__restrict__ res_token, float *__restrict__ epi_out,
-                                                   const fk_step_gemv_params &p) {
-  extern __shared__ float xs[];
-  __shared__ float slots[16];
-  constexpr int C = P / 4;
-  constexpr int U = P * sizeof(WT) / 16;
-  constexpr bool XREG = PPL <= 4;
-  const uint32_t k = p.k;
-  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
-  const uint32_t total = p.first_group[p.n_anchors];  // rows, all anchors
-  const uint32_t row_first = (blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * ROWS;
-
-  Prologue<WT, FK_STEP_MAX_K / (4 * 512)> pro;
-  pro.load(src, src2, gamma, table, token, p);
-  uint32_t anc[ROWS], lrow[ROWS];
-  uint4 w[ROWS][PPL][U];
-#pragma unroll
-  for (int q = 0; q < ROWS; q++) {
-    const uint32_t r = row_first + q;
-    const uint32_t a = fk::anchor_of(r, p);
-    anc[q] = a;
-    lrow[q] = r - fk::pick3(a, p.first_group[0], p.first_group[1], p.first_group[2]);
-    const bool live = r < total;
-    const WT *wr = fk::pick3(a, w0, w1, w2) + (size_t)(live ? lrow[q] : 0) * k;
-#pragma unroll
-    for (int it = 0; it < PPL; it++)
-#pragma unroll
-      for (int u = 0; u < U; u++)
-        w[q][it][u] = live ? reinterpret_cast<const uint4 *>(wr + (size_t)(lane + it * FK_WAVE) * P)[u]
-                           : make_uint4(0, 0, 0, 0);
-  }
-
-  pro.finish(xs, slots, p);
-  if (row_first >= total) return;
-
-  float xr[XREG ? PPL : 1][XREG ? P : 1];
-  if (XREG) {
-#pragma unroll
-    for (int it = 0; it < PPL; it++)
-#pragma unroll
-      for (int e = 0; e < P; e++) xr[XREG ? it : 0][XREG ? e : 0] = xs[(lane + it * FK_WAVE) * P + e];
-  }
-  float t[ROWS];
-#pragma unroll
-  for (int q = 0; q < ROWS; q++) {
-    float acc[C];
-#pragma unroll
-    for (int c = 0; c < C; c++) acc[c] = 0.0f;
-#pragma unroll
-    for (int it = 0; it < PPL; it++) {
-      float xv[P];
-      if (XREG) {
-#pragma unroll
-        for (int e = 0; e < P; e++) xv[e] = xr[XREG ? it : 0][XREG ? e : 0];
-      } else {
-#pragma unroll
-        for (int e = 0; e < P; e++) xv[e] = xs[(lane + it * FK_WAVE) * P + e];
-      }
-      float wv[P];
-      fk::unpack<P>(w[q][it], wv, WT{});
-#pragma unroll
-      for (int c = 0; c < C; c++) {
-        float p0 = xv[4 * c] * wv[4 * c];
-        float p1 = xv[4 * c + 1] * wv[4 * c + 1];
-        float p2 = xv[4 * c + 2] * wv[4 * c + 2];
-        float p3 = xv[4 * c + 3] * wv[4 * c + 3];
-        acc[c] = acc[c] + ((p0 + p1) + (p2 + p3));
-      }
-    }
-    float tq = acc[0];
-#pragma unroll
-    for (int c = 1; c < C; c++) tq = tq + acc[c];
-    t[q] = tq;
-  }
-  // The wavefront sums of all ROWS rows, level by level.
-#pragma unroll
-  for (int m = 1; m < FK_WAVE; m <<= 1) {
-    float o[ROWS];
-#pragma unroll
-    for (int q = 0; q < ROWS; q++) o[q] = __shfl_xor(t[q], m);
-#pragma unroll
-    for (int q = 0; q < ROWS; q++) t[q] = t[q] + o[q];
-  }
-  if (lane == 0) {
-    const uint32_t rtok = (p.epi_mode == FK_EPI_ADD_GATHER) ? min(res_token[0], p.table_rows - 1) : 0;
-#pragma unroll
-    for (int q = 0; q < ROWS; q++) {
-      if (row_first + q >= total) break;
-      const uint32_t a = anc[q];
-      const uint32_t row = lrow[q];
-      if (p.store_tile) fk::pick3(a, y0, y1, y2)[row] = t[q];
-      if (p.epi_mode == FK_EPI_ADD_STORED) {
-        epi_out[row] = res[row] + t[q];
-      } else if (p.epi_mode == FK_EPI_ADD_GATHER) {
-        epi_out[row] = fk::gathered(res_table, rtok, fk::pick3(a, p.rows[0], p.rows[1], p.rows[2]), row, p.gfactor) + t[q];
-      }
-    }
-  }
-}
-
-#define FK_STEP_GEMV_RESIDENT(NAME, WT, P, ROWS, PPL)                                                             \
-  extern "C" __global__ void __launch_bounds__(512)                                                                 \
-      NAME(const WT *__restrict__ w0, const WT *__restrict__ w1, const WT *__restrict__ w2, float *__restrict__ y0, \
-           float *__restrict__ y1, float *__restrict__ y2, const float *__restrict__ src,                          \
-           const float *__restrict__ src2, const float *__restrict__ gamma, const WT *__restrict__ table,           \
-           const uint32_t *__restrict__ token, const float *__restrict__ res, const WT *__restrict__ res_table,     \
-           const uint32_t *__restrict__ res_token, float *__restrict__ epi_out, fk_step_gemv_params p) {           \
-    step_gemv_resident<WT, P, ROWS, PPL>(w0, w1, w2, y0, y1, y2, src, src2, gamma, table, token, res, res_table,   \
-                                         res_token, epi_out, p);                                                    \
-  }
-
-// f16 weights, k = 2048 (PPL 4) and k = 8192 (PPL 16).
-FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r1, _Float16, 8, 1, 4)
-FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r2, _Float16, 8, 2, 4)
-FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r4, _Float16, 8, 4, 4)
-FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k2048_r8, _Float16, 8, 8, 4)
-FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k8192_r1, _Float16, 8, 1, 16)
-FK_STEP_GEMV_RESIDENT(fk_step_gemv_f16_k8192_r2, _Float16, 8, 2, 16)
 
 // KV stores ----------------------------------------------------------------
 
@@ -596,27 +117,6 @@ struct fk_step_attend_params {
 };
 
 namespace fk {
-
-template <int CTRL>
-__device__ __forceinline__ int dpp(int v) {
-  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
-}
-
-// The wavefront's maximumNumber, every lane, on max_key's integers: within
-// rows of 16 lanes by DPP (pairs, quads, halves, rows), then across the four
-// rows.  Exact whatever the order.
-__device__ __forceinline__ float wave_max_dpp(float x) {
-  int v = max_key(x);
-  v = max(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-  v = max(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-  v = max(v, dpp<0x141>(v));  // row_half_mirror
-  v = max(v, dpp<0x140>(v));  // row_mirror
-  const int a = __builtin_amdgcn_readlane(v, 0);
-  const int b = __builtin_amdgcn_readlane(v, 16);
-  const int c = __builtin_amdgcn_readlane(v, 32);
-  const int d = __builtin_amdgcn_readlane(v, 48);
-  return from_max_key(max(max(a, b), max(c, d)));
-}
 
 // LDS of one attention threadgroup.
 struct AttendLds {
@@ -805,7 +305,7 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
     for (uint32_t a = 0; a < HPT; a++) {
       const uint32_t h = hs + a * nh;
       if (h < group) {
-        const float m = wave_max_dpp(sc[a]);
+        const float m = wave_max(sc[a]);
         if (lane == 0) sh.pm[h * 2 + halfk] = m;
       }
     }
@@ -898,51 +398,86 @@ extern "C" __global__ void __launch_bounds__(FK_ATTN_THREADS)
 struct fk_step_combine_params {
   uint32_t heads;
   uint32_t head_dim;
-  uint32_t splits;  // at most 256
+  uint32_t splits;
 };
 
-// Threadgroup per head: M the largest of the splits' maxima (exact whatever
-// the order), the splits' weights w_t = exp(max_t - M) binary64's rounded
-// once, then thread i: out = (sum_t acc_t[i] w_t) / (sum_t l_t w_t), both sums
-// in split order, sixteen splits' loads in flight at a time.
-extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
+// Threadgroup (one wavefront) per head: M the largest of the splits' maxima
+// (exact whatever the order), the splits' weights w_t = exp(max_t - M),
+// binary64's rounded once, then lane i: out_i = (sum_t acc_t[i] w_t) /
+// (sum_t l_t w_t), both sums in split order from +0.  Every load of a chunk of
+// 64 splits is issued before any is used — the maxima and weight sums by lane
+// t, the values acc_t[i] by lane i — so a chunk costs one round trip to memory;
+// lane t makes split t's weight and l_t w_t, which the sums read by lane.
+#define FK_COMBINE_CHUNK 64
+extern "C" __global__ void __launch_bounds__(FK_WAVE)
     fk_step_combine(const float *__restrict__ partials, float *__restrict__ out, fk_step_combine_params p) {
-  __shared__ float w[256];
-  __shared__ float top;
   const uint32_t h = blockIdx.x;
+  const uint32_t lane = threadIdx.x;
   const uint32_t stride = p.head_dim + 2;
   const float *ph = partials + (size_t)h * p.splits * stride;
-  if (threadIdx.x < FK_WAVE) {
-    float m = -__builtin_inff();
-    for (uint32_t t = threadIdx.x; t < p.splits; t += FK_WAVE) m = fk::max_number(m, ph[t * stride]);
-    m = fk::wave_max(m);
-    if (threadIdx.x == 0) top = m;
-  }
-  __syncthreads();
-  for (uint32_t t = threadIdx.x; t < p.splits; t += blockDim.x) w[t] = fk::exp_once(ph[t * stride] - top);
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < p.head_dim; i += blockDim.x) {
+  if (p.splits <= FK_COMBINE_CHUNK && p.head_dim <= FK_WAVE) {
+    // One chunk: every load first.
+    // Every load unconditional, its index clamped into the partials, so the
+    // compiler keeps them all in flight together.
+    const uint32_t i = lane;
+    const uint32_t ic = min(i, p.head_dim - 1);
+    const uint32_t tc = min(lane, p.splits - 1);
+    float mt = ph[(size_t)tc * stride];
+    const float lt = ph[(size_t)tc * stride + 1];
+    float av[FK_COMBINE_CHUNK];
+#pragma unroll
+    for (int j = 0; j < FK_COMBINE_CHUNK; j++) av[j] = ph[(size_t)min((uint32_t)j, p.splits - 1) * stride + 2 + ic];
+    if (lane >= p.splits) mt = -__builtin_inff();
+    const float top = fk::wave_max(mt);
+    float wt = 0.0f, lw = 0.0f;
+    if (lane < p.splits) {
+      wt = fk::exp_once(mt - top);
+      lw = lt * wt;
+    }
     float l = 0.0f;
     float acc = 0.0f;
-    for (uint32_t t0 = 0; t0 < p.splits; t0 += 16) {
-      float lv[16], av[16];
 #pragma unroll
-      for (int j = 0; j < 16; j++) {
-        lv[j] = av[j] = 0.0f;
-        if (t0 + j < p.splits) {
-          lv[j] = ph[(t0 + j) * stride + 1];
-          av[j] = ph[(t0 + j) * stride + 2 + i];
-        }
+    for (int j = 0; j < FK_COMBINE_CHUNK; j++) {
+      if ((uint32_t)j < p.splits) {
+        l = l + fk::readlane_f(lw, j);
+        acc = acc + av[j] * fk::readlane_f(wt, j);
+      }
+    }
+    if (i < p.head_dim) out[(size_t)h * p.head_dim + i] = acc / l;
+    return;
+  }
+  float m = -__builtin_inff();
+  for (uint32_t t = lane; t < p.splits; t += FK_WAVE) m = fk::max_number(m, ph[(size_t)t * stride]);
+  const float top = fk::wave_max(m);
+  for (uint32_t i0 = 0; i0 < p.head_dim; i0 += FK_WAVE) {
+    const uint32_t i = i0 + lane;
+    float l = 0.0f;
+    float acc = 0.0f;
+    for (uint32_t t0 = 0; t0 < p.splits; t0 += FK_COMBINE_CHUNK) {
+      const uint32_t t = t0 + lane;
+      float mt = 0.0f, lt = 0.0f;
+      if (t < p.splits) {
+        mt = ph[(size_t)t * stride];
+        lt = ph[(size_t)t * stride + 1];
+      }
+      float av[FK_COMBINE_CHUNK];
+#pragma unroll
+      for (int j = 0; j < FK_COMBINE_CHUNK; j++)
+        av[j] = (t0 + j < p.splits && i < p.head_dim) ? ph[(size_t)(t0 + j) * stride + 2 + i] : 0.0f;
+      float wt = 0.0f, lw = 0.0f;
+      if (t < p.splits) {
+        wt = fk::exp_once(mt - top);
+        lw = lt * wt;
       }
 #pragma unroll
-      for (int j = 0; j < 16; j++) {
+      for (int j = 0; j < FK_COMBINE_CHUNK; j++) {
         if (t0 + j < p.splits) {
-          l = l + lv[j] * w[t0 + j];
-          acc = acc + av[j] * w[t0 + j];
+          l = l + fk::readlane_f(lw, j);
+          acc = acc + av[j] * fk::readlane_f(wt, j);
         }
       }
     }
-    out[(size_t)h * p.head_dim + i] = acc / l;
+    if (i < p.head_dim) out[(size_t)h * p.head_dim + i] = acc / l;
   }
 }
 

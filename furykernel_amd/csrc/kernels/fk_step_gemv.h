@@ -1,0 +1,515 @@
+// fk_step_gemv.h — the GEMV step of a planned decode step
+// (src/FuryKernel/Program/Plan.hs:17-31): one launch whose threadgroups make
+// the anchors' input row (the recomputed chain: RMSNorm of a stored or gathered
+// row, a gathered row, SiLU·mul of two stored rows, or a stored row), then take
+// blocks of the anchors' output rows — each row y_j = sum_i W[j, i] x_i in the
+// reference GEMV's order at SIMD width 64, split 1 — and run the step's
+// epilogue on the tile.
+//
+// Layout in HBM: each anchor's W is [rows, k] row-major (`out_in`,
+// src/FuryKernel/Program/Build.hs:175-176), f16 or f32; x, y and the epilogue
+// rows are f32.
+//
+// Work split: the anchors' rows are numbered one after another; a block is R
+// consecutive rows (or, for the SiLU·mul epilogue, rows j .. j + R/2 - 1 of
+// both anchors, so a wavefront holds gate_j and up_j together).  A wavefront
+// takes blocks b, b + (all wavefronts), ...; lane l holds packs l, l + 64, ...
+// (KPL of them at most, 16 bytes each) of each of its rows.  A block's weight
+// loads are all issued at once, and with DB the next block's are issued
+// before the current block is computed, so a wavefront keeps two blocks in
+// flight.  The prologue's loads go out first, the first block's weights right
+// after them: the prologue's arithmetic and its one barrier run while the
+// weights stream in.
+//
+// Order (the bits): per row, lane l's pack elements four to a chain
+// ((x0 w0 + x1 w1) + (x2 w2 + x3 w3)), each chain summed over the lane's packs
+// in order, the lane's chains added in order, then the pairwise wavefront sum
+// (test/Test/FuryKernel/Gemv.hs:16-23,131-191).  RMSNorm's sum of squares in
+// tgReduceSum's order with the launch's threads (src/FuryKernel/Reduce.hs:55-85).
+#pragma once
+
+#include "fk_common.h"
+#include "fk_gemv.h"
+
+#define FK_GEMV_MAX_K 8192
+// Threads of every GEMV step launch: a compile-time constant, since reading
+// the launch's size costs the kernel a load from the dispatch packet.
+#define FK_GEMV_THREADS 512
+
+// Prologue modes: how a GEMV step's threadgroups make the anchors' input row.
+enum : uint32_t {
+  FK_PRO_STORED = 0,          // x = src
+  FK_PRO_RMSNORM = 1,         // x = rmsnorm(src) * gamma * factor
+  FK_PRO_GATHER = 2,          // x = table[token] * gfactor
+  FK_PRO_GATHER_RMSNORM = 3,  // x = rmsnorm(table[token] * gfactor) * gamma * factor
+  FK_PRO_SILU_MUL = 4,        // x = silu(src) * src2
+};
+
+// Epilogue modes: work on the anchors' tile.
+enum : uint32_t {
+  FK_EPI_NONE = 0,
+  FK_EPI_ADD_STORED = 1,  // out = res + tile
+  FK_EPI_ADD_GATHER = 2,  // out = table[token] * gfactor + tile
+  FK_EPI_SILU_MUL = 3,    // out = silu(tile of anchor 0) * tile of anchor 1 (a stored SiLU·mul, folded in)
+  FK_EPI_ARGMAX = 4,      // arg = max(arg, argmax key of each row) (the greedy token, folded in)
+};
+
+struct fk_step_gemv_params {
+  uint32_t n_anchors;     // 1 to 3
+  uint32_t rows[3];       // each anchor's outputs
+  uint32_t first_row[4];  // anchor j's rows are [first_row[j], first_row[j + 1]) of the numbered rows
+  uint32_t k;             // the input row's width
+  uint32_t pro_mode;
+  uint32_t seg;           // RMSNorm's segment: the row (k)
+  float eps;
+  float factor;           // RMSNorm's factor
+  float gfactor;          // the gather's factor
+  uint32_t has_gamma;
+  uint32_t epi_mode;
+  uint32_t store_tile;    // the anchors' own values are stored (into y[j])
+  uint32_t table_rows;    // the gathered table's rows: a token past them reads its last (the engine refuses one)
+  uint32_t blocks;        // row blocks
+  uint32_t arg_slots;     // the argmax epilogue's slots (one a threadgroup); a threadgroup past them stores none
+};
+
+namespace fk {
+
+// SiLU(a) · b: a / (1 + e^-a), e^-a binary64's rounded once, then times b.
+__device__ __forceinline__ float silu_mul(float a, float b) {
+  const float e = exp_once(-a);
+  const float d = 1.0f + e;
+  return (a / d) * b;
+}
+
+// An anchor's pointer or count by index, without indexing an array: a
+// dynamically indexed array of kernel pointers would lose their address space
+// (its loads would become flat loads, which wait with LDS traffic).
+template <typename T>
+__device__ __forceinline__ T pick3(uint32_t a, T x0, T x1, T x2) {
+  return a == 0 ? x0 : (a == 1 ? x1 : x2);
+}
+
+// The greedy token's fold (src/FuryKernel/Program/Eval.hs:681-685: a later
+// element wins only if strictly larger) as the maximum of one 64-bit key per
+// element: the value's order in the high word (+0 and -0 equal; a NaN at
+// index 0 above everything, since nothing is larger than it and it is never
+// replaced; a NaN elsewhere below everything, since it never wins), and the
+// complement of the index in the low word, so equal values go to the lowest.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
+  uint32_t hi;
+  if (__builtin_isnan(v)) {
+    hi = index == 0 ? 0xFFFFFFFFu : 0u;
+  } else {
+    const uint32_t b = v == 0.0f ? 0u : __float_as_uint(v);
+    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - index);
+}
+
+// Where slot q of block b is: its anchor, its row in the anchor, and whether
+// it exists.
+template <int R>
+struct Block {
+  uint32_t anchor[R];
+  uint32_t row[R];
+  bool live[R];
+
+  __device__ __forceinline__ void locate(uint32_t b, const fk_step_gemv_params &p) {
+    const bool paired = p.epi_mode == FK_EPI_SILU_MUL;
+    const uint32_t total = p.first_row[p.n_anchors];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      if (paired) {
+        constexpr uint32_t H = R / 2 > 0 ? R / 2 : 1;
+        anchor[q] = (uint32_t)q < H ? 0u : 1u;
+        row[q] = b * H + ((uint32_t)q % H);
+        live[q] = b < p.blocks && row[q] < p.rows[0];
+      } else {
+        const uint32_t g = b * R + q;
+        const uint32_t a = (p.n_anchors > 1 && g >= p.first_row[1] ? 1u : 0u) +
+                           (p.n_anchors > 2 && g >= p.first_row[2] ? 1u : 0u);
+        anchor[q] = a;
+        row[q] = g - pick3(a, p.first_row[0], p.first_row[1], p.first_row[2]);
+        live[q] = b < p.blocks && g < total;
+      }
+    }
+  }
+};
+
+}  // namespace fk
+
+// Loads a wavefront issues are waited for in the order it issued them, and
+// the compiler counts them only through straight-line code: so every load here
+// is unconditional (its address clamped into the buffer, its value replaced
+// by zero where it lies outside the row), the prologue and epilogue modes are
+// template parameters, and the block loop alternates between two named
+// buffers rather than copying one into the other.  Each use then waits for its
+// own loads only, never for the ones issued after them.
+
+namespace fk {
+
+// A block's weights: R rows of KPL 16-byte packs a lane.
+template <typename WT, int P, int R, int KPL>
+__device__ __forceinline__ void issue_block(uint4 (&dst)[R][KPL], const Block<R> &blk, const WT *__restrict__ w0,
+                                            const WT *__restrict__ w1, const WT *__restrict__ w2, uint32_t k,
+                                            uint32_t packs, uint32_t lane, const fk_step_gemv_params &p) {
+#pragma unroll
+  for (int q = 0; q < R; q++) {
+    const uint32_t a = blk.anchor[q];
+    const uint32_t n = pick3(a, p.rows[0], p.rows[1], p.rows[2]);
+    const WT *wr = pick3(a, w0, w1, w2) + (size_t)min(blk.row[q], n - 1) * k;
+#pragma unroll
+    for (int it = 0; it < KPL; it++) {
+      const uint32_t j = lane + it * FK_WAVE;
+      dst[q][it] = *reinterpret_cast<const uint4 *>(wr + (size_t)min(j, packs - 1) * P);
+    }
+  }
+}
+
+}  // namespace fk
+
+// One wavefront's block loop.  WT: weight element; P: elements a 16-byte pack
+// holds; R: rows a block; KPL: packs a lane holds of a row (k <= 64 P KPL);
+// DB: the next block's weights in flight while a block is computed (else
+// issued after it); PRO, EPI: the prologue and epilogue modes.
+template <typename WT, int P, int R, int KPL, bool DB, uint32_t PRO, uint32_t EPI>
+__device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *__restrict__ w1, const WT *__restrict__ w2,
+                                          float *__restrict__ y0, float *__restrict__ y1, float *__restrict__ y2,
+                                          const float *__restrict__ src, const float *__restrict__ src2,
+                                          const float *__restrict__ gamma, const WT *__restrict__ table,
+                                          const uint32_t *__restrict__ token, const float *__restrict__ res,
+                                          const WT *__restrict__ res_table, const uint32_t *__restrict__ res_token,
+                                          float *__restrict__ epi_out, unsigned long long *__restrict__ arg,
+                                          const fk_step_gemv_params &p) {
+  static_assert(P * sizeof(WT) == 16, "a pack is one 16-byte load");
+  static_assert(EPI != FK_EPI_SILU_MUL || R % 2 == 0, "the SiLU·mul epilogue pairs rows");
+  constexpr int C = P / 4;
+  // The prologue's packs of 4 a thread holds, at most, with the 512 threads
+  // every launch of these kernels has.
+  constexpr int NPK = KPL * P / 32 > 0 ? KPL * P / 32 : 1;
+  constexpr bool GATHER = PRO == FK_PRO_GATHER || PRO == FK_PRO_GATHER_RMSNORM;
+  constexpr bool NORM = PRO == FK_PRO_RMSNORM || PRO == FK_PRO_GATHER_RMSNORM;
+  constexpr bool SILU = PRO == FK_PRO_SILU_MUL;
+  constexpr bool RESIDUAL = EPI == FK_EPI_ADD_STORED || EPI == FK_EPI_ADD_GATHER;
+  // The input row (and the norm's gains) in LDS transposed to the lanes'
+  // packs: chunk c (4 elements) of lane l's pack it is float4 (it C + c) 64 + l,
+  // so a wavefront reads a chunk of all its lanes' packs with one conflict-free
+  // 16-byte load a lane.  XT float4s: 64 P KPL / 4 a row.
+  constexpr uint32_t XT = 64 * P * KPL / 4;
+  extern __shared__ float4 lds4[];  // xt[XT], then gt[XT]
+  __shared__ float slots[16];
+  __shared__ unsigned long long bests[16];
+  float4 *xt = lds4;
+  float4 *gt = lds4 + XT;
+  const uint32_t k = p.k;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (FK_WAVE - 1);
+  const uint32_t wave = tid / FK_WAVE;
+  constexpr uint32_t waves = FK_GEMV_THREADS / FK_WAVE;
+  const uint32_t total_waves = gridDim.x * waves;
+  const uint32_t packs = k / P;
+  const uint32_t packs4 = k / 4;
+  const bool has_gamma = NORM && p.has_gamma;
+  const float gfactor = p.gfactor;
+  const float eps = p.eps;
+  const float factor = p.factor;
+  const uint32_t blocks = p.blocks;
+  // Where pack-of-4 j of the row (elements 4j .. 4j + 3) lives in xt.
+  auto xt_at = [](uint32_t j) -> uint32_t {
+    const uint32_t pk = j / C;
+    return ((pk / FK_WAVE) * C + j % C) * FK_WAVE + pk % FK_WAVE;
+  };
+
+  // Prologue loads: thread t's packs of 4, t, t + T, ... (tgReduceSum's order).
+  const uint32_t tok = GATHER ? min(token[0], p.table_rows - 1) : 0u;
+  float4 xa[NPK], xb[NPK], ga[NPK];
+#pragma unroll
+  for (int m = 0; m < NPK; m++) {
+    const uint32_t j = min(tid + m * FK_GEMV_THREADS, packs4 - 1);
+    if constexpr (GATHER) {
+      const WT *row = table + (size_t)tok * k + 4 * j;
+      if constexpr (sizeof(WT) == 2) {
+        const uint2 h = *reinterpret_cast<const uint2 *>(row);
+        xa[m] = make_float4(fk::widen_f16((uint16_t)(h.x & 0xFFFFu)), fk::widen_f16((uint16_t)(h.x >> 16)),
+                            fk::widen_f16((uint16_t)(h.y & 0xFFFFu)), fk::widen_f16((uint16_t)(h.y >> 16)));
+      } else {
+        const float4 v = *reinterpret_cast<const float4 *>(row);
+        xa[m] = v;
+      }
+    } else {
+      xa[m] = reinterpret_cast<const float4 *>(src)[j];
+    }
+    if constexpr (SILU) xb[m] = reinterpret_cast<const float4 *>(src2)[j];
+    // A norm without gains has a row of ones bound here (the product is then
+    // not taken), so the load is unconditional.
+    if constexpr (NORM) ga[m] = reinterpret_cast<const float4 *>(gamma)[j];
+  }
+  const uint32_t rtok = EPI == FK_EPI_ADD_GATHER ? min(res_token[0], p.table_rows - 1) : 0u;
+
+  // The first block's weights.
+  uint32_t b = blockIdx.x * waves + wave;
+  fk::Block<R> ba, bb;
+  uint4 wa[R][KPL], wb[DB ? R : 1][DB ? KPL : 1];
+  ba.locate(b, p);
+  fk::issue_block<WT, P, R, KPL>(wa, ba, w0, w1, w2, k, packs, lane, p);
+
+  // The prologue's arithmetic: the row (and the gains) into LDS, each wave's
+  // sum of squares into its slot; one barrier.  Slots of xt past the row hold
+  // zeros.
+  float acc = 0.0f;
+#pragma unroll
+  for (int m = 0; m < NPK; m++) {
+    const uint32_t j = tid + m * FK_GEMV_THREADS;
+    float4 v = xa[m];
+    if constexpr (GATHER) {
+      v.x = v.x * gfactor;
+      v.y = v.y * gfactor;
+      v.z = v.z * gfactor;
+      v.w = v.w * gfactor;
+    }
+    if constexpr (SILU) {
+      v = make_float4(fk::silu_mul(v.x, xb[m].x), fk::silu_mul(v.y, xb[m].y), fk::silu_mul(v.z, xb[m].z),
+                      fk::silu_mul(v.w, xb[m].w));
+    }
+    if (j < packs4) {
+      if constexpr (NORM) {
+        acc = acc + v.x * v.x;
+        acc = acc + v.y * v.y;
+        acc = acc + v.z * v.z;
+        acc = acc + v.w * v.w;
+        gt[xt_at(j)] = ga[m];
+      }
+      xt[xt_at(j)] = v;
+    } else if (j < XT) {
+      xt[xt_at(j)] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (NORM) gt[xt_at(j)] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
+  if constexpr (NORM) {
+    const float s = fk::wave_sum(acc);
+    if (lane == 0) slots[wave] = s;
+  }
+  __syncthreads();
+  // tgReduceSum's last steps, in every wavefront: lane l folds slots l, l + 64,
+  // ... from -0, then the wavefront sum.
+  float scale = 1.0f;
+  if constexpr (NORM) {
+    const float sl = slots[min(lane, waves - 1)];
+    const float t = -0.0f + (lane < waves ? sl : -0.0f);
+    scale = fk::rsqrt_once(fk::wave_sum(t) / (float)p.seg + eps);
+  }
+  // Chunk c of lane l's pack it of the anchors' input row: ((x scale) gamma)
+  // factor for the norm, x otherwise; both products made, one kept (a select,
+  // not a branch, so the chunk's loads are issued together).
+  auto xin4 = [&](int it, int c) -> float4 {
+    float4 v = xt[(it * C + c) * FK_WAVE + lane];
+    if constexpr (NORM) {
+      const float4 g = gt[(it * C + c) * FK_WAVE + lane];
+      float e[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+      const float gg[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float eg = e[q] * gg[q];
+        e[q] = has_gamma ? eg : e[q];
+        const float ef = e[q] * factor;
+        e[q] = factor != 1.0f ? ef : e[q];
+      }
+      v = make_float4(e[0], e[1], e[2], e[3]);
+    }
+    return v;
+  };
+  uint64_t best = 0;
+  // Block `blk`'s rows from the weights `w`: the residuals loaded first (lane q
+  // holds slot q's), then (with DB) the next block's weights issued into `wn`,
+  // then the block computed, reduced and its epilogue run.
+  auto run = [&](const fk::Block<R> &blk, const uint4 (&w)[R][KPL], fk::Block<R> &bn, uint4 (&wn)[R][KPL],
+                 uint32_t nb) {
+    float resv = 0.0f;
+    if constexpr (RESIDUAL) {
+      uint32_t a = blk.anchor[0], r = blk.row[0];
+#pragma unroll
+      for (int q = 1; q < R; q++)
+        if (lane == (uint32_t)q) a = blk.anchor[q], r = blk.row[q];
+      const uint32_t n = fk::pick3(a, p.rows[0], p.rows[1], p.rows[2]);
+      if constexpr (EPI == FK_EPI_ADD_STORED) {
+        resv = res[min(r, n - 1)];
+      } else {
+        resv = (float)res_table[(size_t)rtok * n + min(r, n - 1)] * gfactor;
+      }
+    }
+    if constexpr (DB) {
+      bn.locate(nb, p);
+      fk::issue_block<WT, P, R, KPL>(wn, bn, w0, w1, w2, k, packs, lane, p);
+    }
+
+    float t[R];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      float a[C];
+#pragma unroll
+      for (int c = 0; c < C; c++) a[c] = 0.0f;
+#pragma unroll
+      for (int it = 0; it < KPL; it++) {
+        const uint32_t j = lane + it * FK_WAVE;
+        float wv[P];
+        const uint4 u[1] = {w[q][it]};
+        fk::unpack<P>(u, wv, WT{});
+        float xv[P];
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+          const float4 x4 = xin4(it, c);
+          xv[4 * c] = x4.x;
+          xv[4 * c + 1] = x4.y;
+          xv[4 * c + 2] = x4.z;
+          xv[4 * c + 3] = x4.w;
+        }
+        // A pack past the row adds +0 in place of its products (the lane never
+        // visits it): exact, since a chain that starts at +0 is never -0.
+        const bool in = j < packs;
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+          const float p0 = xv[4 * c] * wv[4 * c];
+          const float p1 = xv[4 * c + 1] * wv[4 * c + 1];
+          const float p2 = xv[4 * c + 2] * wv[4 * c + 2];
+          const float p3 = xv[4 * c + 3] * wv[4 * c + 3];
+          const float ps = (p0 + p1) + (p2 + p3);
+          a[c] = a[c] + (in ? ps : 0.0f);
+        }
+      }
+      float s = a[0];
+#pragma unroll
+      for (int c = 1; c < C; c++) s = s + a[c];
+      t[q] = s;
+    }
+    fk::wave_sums<R>(t);
+
+    // Epilogue: slot q's stores by lane q.
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      if (blk.live[q]) {
+        if constexpr (EPI == FK_EPI_ARGMAX) {
+          const uint64_t key = fk::argmax_key(t[q], blk.row[q]);
+          best = key > best ? key : best;
+        }
+        if (lane == (uint32_t)q) {
+          const uint32_t a = blk.anchor[q];
+          const uint32_t r = blk.row[q];
+          if (p.store_tile) fk::pick3(a, y0, y1, y2)[r] = t[q];
+          if constexpr (RESIDUAL) epi_out[r] = resv + t[q];
+          if constexpr (EPI == FK_EPI_SILU_MUL) {
+            if (q < R / 2) epi_out[r] = fk::silu_mul(t[q], t[(q + R / 2) % R]);
+          }
+        }
+      }
+    }
+  };
+
+  if constexpr (DB) {
+    while (b < blocks) {
+      run(ba, wa, bb, wb, b + total_waves);
+      b += total_waves;
+      if (b >= blocks) break;
+      run(bb, wb, ba, wa, b + total_waves);
+      b += total_waves;
+    }
+  } else {
+    while (b < blocks) {
+      run(ba, wa, bb, wa, 0);
+      b += total_waves;
+      if (b >= blocks) break;
+      ba.locate(b, p);
+      fk::issue_block<WT, P, R, KPL>(wa, ba, w0, w1, w2, k, packs, lane, p);
+    }
+  }
+  if constexpr (EPI == FK_EPI_ARGMAX) {
+    // The threadgroup's largest key into its own slot of `arg`; the token
+    // launch takes the largest of the slots.
+    if (lane == 0) bests[wave] = best;
+    __syncthreads();
+    if (tid == 0 && blockIdx.x < p.arg_slots) {
+      unsigned long long m = 0;
+      for (uint32_t w = 0; w < waves; w++) m = bests[w] > m ? bests[w] : m;
+      arg[blockIdx.x] = m;
+    }
+  }
+}
+
+// Buffers in binding order, then the parameter struct.
+#define FK_STEP_GEMV(NAME, WT, P, R, KPL, DB, PRO, EPI)                                                                \
+  extern "C" __global__ void __launch_bounds__(FK_GEMV_THREADS)                                                     \
+      NAME(const WT *__restrict__ w0, const WT *__restrict__ w1, const WT *__restrict__ w2, float *__restrict__ y0, \
+           float *__restrict__ y1, float *__restrict__ y2, const float *__restrict__ src,                          \
+           const float *__restrict__ src2, const float *__restrict__ gamma, const WT *__restrict__ table,           \
+           const uint32_t *__restrict__ token, const float *__restrict__ res, const WT *__restrict__ res_table,     \
+           const uint32_t *__restrict__ res_token, float *__restrict__ epi_out,                                    \
+           unsigned long long *__restrict__ arg, fk_step_gemv_params p) {                                           \
+    step_gemv<WT, P, R, KPL, DB, PRO, EPI>(w0, w1, w2, y0, y1, y2, src, src2, gamma, table, token, res,          \
+                                           res_table, res_token, epi_out, arg, p);                                  \
+  }
+
+// Every prologue with the epilogues a shape takes: entries named
+// <shape>_p<prologue>_e<epilogue>.
+#define FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, PRO)    \
+  FK_STEP_GEMV(NAME##_p##PRO##_e0, WT, P, R, KPL, DB, PRO, 0) \
+  FK_STEP_GEMV(NAME##_p##PRO##_e1, WT, P, R, KPL, DB, PRO, 1) \
+  FK_STEP_GEMV(NAME##_p##PRO##_e2, WT, P, R, KPL, DB, PRO, 2) \
+  FK_STEP_GEMV(NAME##_p##PRO##_e4, WT, P, R, KPL, DB, PRO, 4)
+#define FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, PRO) \
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, PRO)         \
+  FK_STEP_GEMV(NAME##_p##PRO##_e3, WT, P, R, KPL, DB, PRO, 3)
+#define FK_STEP_GEMV_SHAPE(NAME, WT, P, R, KPL, DB) \
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 0)      \
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 1)      \
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 2)      \
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 3)      \
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 4)
+#define FK_STEP_GEMV_SHAPE_PAIRS(NAME, WT, P, R, KPL, DB) \
+  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 0)          \
+  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 1)          \
+  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 2)          \
+  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 3)          \
+  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 4)
+
+// f16 weights: k up to 2048 (4 packs a lane) in blocks of 1 or 2 rows; k up to
+// 8192 (16 packs a lane), one row a block.  A block's loads are issued when the
+// block before it is done: the memory's parallelism comes from the resident
+// wavefronts, each with one block in flight.
+FK_STEP_GEMV_SHAPE(fk_step_gemv_f16_k2048_r1, _Float16, 8, 1, 4, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f16_k2048_r2, _Float16, 8, 2, 4, false)
+FK_STEP_GEMV_SHAPE(fk_step_gemv_f16_k8192_r1, _Float16, 8, 1, 16, false)
+// f32 weights: k up to 256 and 1024.
+FK_STEP_GEMV_SHAPE(fk_step_gemv_f32_k256_r1, float, 4, 1, 1, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k256_r2, float, 4, 2, 1, false)
+FK_STEP_GEMV_SHAPE(fk_step_gemv_f32_k1024_r1, float, 4, 1, 4, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k1024_r2, float, 4, 2, 4, false)
+
+struct fk_step_token_params {
+  uint32_t slots;    // the folded argmax's slots: one a threadgroup of the logits' step
+  uint32_t context;  // positions wrap below this
+  uint32_t step;     // positions advance by this (0 holds the position)
+  uint32_t advance;  // also set the next step's token and position
+};
+
+// The greedy token from the folded argmax: the largest of the threadgroups'
+// keys (exact whatever the order), its index the complement of the key's low
+// word; with `advance`, the next decode step's token is this one and its
+// position `step` on.  One wavefront.
+extern "C" __global__ void __launch_bounds__(FK_WAVE)
+    fk_step_token(const unsigned long long *__restrict__ arg, uint32_t *__restrict__ out,
+                  uint32_t *__restrict__ token, uint32_t *__restrict__ position, fk_step_token_params p) {
+  const uint32_t lane = threadIdx.x;
+  unsigned long long m = 0;
+  for (uint32_t i = lane; i < p.slots; i += FK_WAVE) m = arg[i] > m ? arg[i] : m;
+  for (int s = 1; s < FK_WAVE; s <<= 1) {
+    const unsigned long long o = __shfl_xor(m, s);
+    m = o > m ? o : m;
+  }
+  if (lane == 0) {
+    const uint32_t t = 0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull);
+    out[0] = t;
+    if (p.advance) {
+      token[0] = t;
+      position[0] = (position[0] + p.step) % p.context;
+    }
+  }
+}

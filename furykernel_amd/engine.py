@@ -19,13 +19,15 @@ from . import kernels as K
 from . import runtime
 from .lower import Launch, Lowered, rope_table
 
-_NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16}
+_NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16,
+       "u64": np.uint64}
 _STRUCTS = {
     "fk_step_store": K.StepStoreParams,
     "fk_step_attend": K.StepAttendParams,
     "fk_step_combine": K.StepCombineParams,
     "fk_step_argmax": K.CountParams,
     "fk_step_silu_mul": K.CountParams,
+    "fk_step_token": K.StepTokenParams,
 }
 
 
@@ -61,6 +63,8 @@ class Engine:
                 self.write(name, rope_table(*what[1:]))
             elif what[0] == "zero":
                 self.zero(name)
+            elif what[0] == "ones":
+                self.write(name, np.ones(specs[name].count, np.float32))
             else:
                 raise ValueError(f"{name}: no constant {what[0]}")
         self._kernargs = [self._kernarg(launch) for launch in lowered.launches]
@@ -68,6 +72,12 @@ class Engine:
 
     def _kernarg(self, launch: Launch) -> bytes:
         abi = K.ABIS[launch.entry]
+        if abi.threads and launch.threads != abi.threads:
+            raise K.LaunchError(f"{launch.entry} is compiled for {abi.threads} threads, not {launch.threads}")
+        arg = launch.bind.get("arg")
+        if arg is not None and launch.params.get("arg_slots", 0) > self.lowered.buffers[arg].count:
+            raise K.LaunchError(f"{launch.entry}: {launch.params['arg_slots']} argmax slots in a buffer of "
+                                f"{self.lowered.buffers[arg].count}")
         bound = {}
         for b in abi.buffers:
             name = launch.bind.get(b)
@@ -112,13 +122,31 @@ class Engine:
 
     # Running -----------------------------------------------------------------
 
-    def enqueue(self, stream: runtime.Stream | None = None, only: Optional[list] = None) -> None:
+    def enqueue(self, stream: runtime.Stream | None = None, only: Optional[list] = None,
+                advance: Optional[dict] = None) -> None:
         """Queues every launch of the step (or those at the indices `only`),
-        in plan order."""
-        picks = range(len(self.lowered.launches)) if only is None else only
+        in plan order; with `advance`, then the next step's token and
+        position (see ``enqueue_advance``)."""
+        picks = list(range(len(self.lowered.launches))) if only is None else list(only)
+        last = len(self.lowered.launches) - 1
+        folded = advance is not None and self.lowered.launches[last].entry == "fk_step_token" and \
+            (not picks or picks[-1] == last)
         for i in picks:
             launch = self.lowered.launches[i]
-            self._fns[i].launch(launch.groups, launch.threads, self._kernargs[i], launch.lds_bytes, stream)
+            kernarg = self._advance_kernarg(launch, **advance) if folded and i == last else self._kernargs[i]
+            self._fns[i].launch(launch.groups, launch.threads, kernarg, launch.lds_bytes, stream)
+        if advance is not None and not folded:
+            self.enqueue_advance(stream=stream, **advance)
+
+    def _advance_kernarg(self, launch: Launch, token_out: str, token_in: str, position: str, context: int,
+                         step: int = 1) -> bytes:
+        """The token launch that also advances: the greedy token it makes is
+        the next step's token, the position `step` on."""
+        if launch.bind["out"] != token_out:
+            raise ValueError(f"the step's token is {launch.bind['out']}, not {token_out}")
+        bind = dict(launch.bind, token=token_in, position=position)
+        params = dict(launch.params, context=context, step=step, advance=1)
+        return self._kernarg(Launch(launch.step, launch.entry, launch.groups, launch.threads, bind, params))
 
     def enqueue_advance(self, token_out: str, token_in: str, position: str, context: int, step: int = 1,
                         stream: runtime.Stream | None = None) -> None:
@@ -134,9 +162,7 @@ class Engine:
         """A graph of the step's launches (or those at the indices `only`; and
         the advance, if given), to replay."""
         with self.device.capture(stream) as out:
-            self.enqueue(stream, only)
-            if advance is not None:
-                self.enqueue_advance(stream=stream, **advance)
+            self.enqueue(stream, only, advance)
         return out[0]
 
     def close(self) -> None:

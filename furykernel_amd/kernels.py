@@ -65,7 +65,7 @@ class StepGemvParams(ctypes.Structure):
     _fields_ = [
         ("n_anchors", ctypes.c_uint32),
         ("rows", ctypes.c_uint32 * 3),
-        ("first_group", ctypes.c_uint32 * 4),
+        ("first_row", ctypes.c_uint32 * 4),
         ("k", ctypes.c_uint32),
         ("pro_mode", ctypes.c_uint32),
         ("seg", ctypes.c_uint32),
@@ -76,7 +76,14 @@ class StepGemvParams(ctypes.Structure):
         ("epi_mode", ctypes.c_uint32),
         ("store_tile", ctypes.c_uint32),
         ("table_rows", ctypes.c_uint32),
+        ("blocks", ctypes.c_uint32),
+        ("arg_slots", ctypes.c_uint32),
     ]
+
+
+class StepTokenParams(ctypes.Structure):
+    _fields_ = [("slots", ctypes.c_uint32), ("context", ctypes.c_uint32), ("step", ctypes.c_uint32),
+                ("advance", ctypes.c_uint32)]
 
 
 class StepStoreParams(ctypes.Structure):
@@ -137,6 +144,7 @@ class KernelAbi:
     entry: str
     buffers: tuple[str, ...]
     params: type
+    threads: int = 0  # the threads a launch must have, when the kernel is compiled for one count
 
     def kernarg(self, bound: dict[str, int], params: ctypes.Structure) -> bytes:
         missing = [b for b in self.buffers if b not in bound]
@@ -158,24 +166,30 @@ def _gemv_abis() -> dict[str, KernelAbi]:
     return out
 
 
+# The GEMV step kernels (fk_step_gemv.h): <shape>_p<prologue>_e<epilogue>, a
+# shape being the weight type, the largest input width it takes and its rows a
+# block; the SiLU·mul epilogue (3) only on shapes of row pairs.
+STEP_GEMV_SHAPES = {"fk_step_gemv_f16_k2048_r1": False, "fk_step_gemv_f16_k2048_r2": True,
+                    "fk_step_gemv_f16_k8192_r1": False, "fk_step_gemv_f32_k256_r1": False,
+                    "fk_step_gemv_f32_k256_r2": True, "fk_step_gemv_f32_k1024_r1": False,
+                    "fk_step_gemv_f32_k1024_r2": True}
+STEP_GEMV_ENTRIES = tuple(f"{shape}_p{pro}_e{epi}" for shape, pairs in STEP_GEMV_SHAPES.items() for pro in range(5)
+                          for epi in ((0, 1, 2, 3, 4) if pairs else (0, 1, 2, 4)))
+STEP_GEMV_BUFFERS = ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
+                     "res_token", "epi_out", "arg")
+
 ABIS: dict[str, KernelAbi] = {
     **_gemv_abis(),
     "fk_rmsnorm_f32": KernelAbi("fk_rmsnorm_f32", ("x", "gamma", "y"), RmsNormParams),
     "fk_softmax_f32": KernelAbi("fk_softmax_f32", ("x", "y"), SoftmaxParams),
     "fk_fill_u32": KernelAbi("fk_fill_u32", ("dst",), FillParams),
-    **{f"fk_step_gemv_{t}_r{r}": KernelAbi(f"fk_step_gemv_{t}_r{r}", (
-        "w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
-        "res_token", "epi_out"), StepGemvParams) for t, r in (("f16", 1), ("f16", 2), ("f16", 4), ("f16", "1p8"),
-                                                          ("f32", 1))},
-    **{f"fk_step_gemv_f16_k{k}_r{r}": KernelAbi(f"fk_step_gemv_f16_k{k}_r{r}", (
-        "w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
-        "res_token", "epi_out"), StepGemvParams) for k, r in ((2048, 1), (2048, 2), (2048, 4), (2048, 8), (8192, 1),
-                                                              (8192, 2))},
+    **{e: KernelAbi(e, STEP_GEMV_BUFFERS, StepGemvParams, 512) for e in STEP_GEMV_ENTRIES},
+    "fk_step_token": KernelAbi("fk_step_token", ("arg", "out", "token", "position"), StepTokenParams, 64),
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
     "fk_step_attend": KernelAbi("fk_step_attend", ("q", "knew", "vnew", "kc", "vc", "position", "slot", "rope",
                                                    "partials"), StepAttendParams),
-    "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams),
+    "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams, 64),
     "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
     "fk_step_silu_mul": KernelAbi("fk_step_silu_mul", ("a", "b", "y"), CountParams),
     "fk_step_advance": KernelAbi("fk_step_advance", ("next_token", "token", "position"), AdvanceParams),

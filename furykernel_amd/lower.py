@@ -30,9 +30,9 @@ ATTN_SPLIT = 128      # positions a split of the attention covers (64 or 128)
 ATTN_THREADS = 512
 MAX_K = 8192
 
-# GEMV step prologue and epilogue modes (fk_step.h).
+# GEMV step prologue and epilogue modes (fk_step_gemv.h).
 PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = 0, 1, 2, 3, 4
-EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER = 0, 1, 2
+EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX = 0, 1, 2, 3, 4
 
 
 class LoweringError(ValueError):
@@ -42,12 +42,12 @@ class LoweringError(ValueError):
 @dataclass(frozen=True)
 class BufferSpec:
     name: str
-    dtype: str   # "f32", "f16", "bf16", "u32", "u16"
+    dtype: str   # "f32", "f16", "bf16", "u32", "u16", "u64"
     count: int   # elements
 
     @property
     def nbytes(self) -> int:
-        return self.count * {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2}[self.dtype]
+        return self.count * {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2, "u64": 8}[self.dtype]
 
 
 @dataclass
@@ -83,8 +83,10 @@ class Lowered:
 def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units: int = 256,
                fuse: bool = True) -> Lowered:
     """The launches of every step of the plan, in order, for steps of `rows`
-    rows (one, a decode step's), on a device of `compute_units` CUs; with
-    `fuse`, a KV store folded into the attention right after it."""
+    rows (one, a decode step's), on a device of `compute_units` CUs.  With
+    `fuse`, light steps fold into the launch before them: a KV store into the
+    attention right after it, a stored SiLU·mul into the GEMV step of its two
+    anchors, the greedy token into the GEMV step of its logits."""
     if rows != 1:
         raise LoweringError(f"steps of {rows} rows: the decode kernels take one row a step")
     out = Lowered(checked.program, plan, rows)
@@ -93,6 +95,7 @@ def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units
         out.launches.append(low.step(step))
     if fuse:
         _fuse_attention(out)
+        _fuse_light(out, compute_units)
     return out
 
 
@@ -147,6 +150,90 @@ def _store_into_attend(st: Launch, at: Launch) -> Optional[Launch]:
     return Launch(f"{st.step}+{at.step}", at.entry, at.groups, at.threads, bind, params, meta, at.lds_bytes)
 
 
+def _fuse_light(out: Lowered, compute_units: int) -> None:
+    """A light step of one stored SiLU·mul of the two anchors of the GEMV
+    step right before it becomes that step's epilogue: its wavefronts hold row
+    j of both anchors and store silu(gate_j) * up_j — the light kernel's
+    arithmetic.  A light step of the greedy token of the row the GEMV step
+    before it stores becomes that step's epilogue (each row's argmax key into
+    a 64-bit maximum) and a one-thread launch that turns the key into the
+    token and clears it for the next step."""
+    fused: list = []
+    for launch in out.launches:
+        prev = fused[-1] if fused else None
+        if prev is not None and prev.entry.startswith("fk_step_gemv") and prev.params["epi_mode"] == EPI_NONE:
+            pp, pb = prev.params, prev.bind
+            if (launch.entry == "fk_step_silu_mul" and pp["n_anchors"] == 2 and pp["rows"][0] == pp["rows"][1]
+                    and pb["y0"] == launch.bind["a"] and pb["y1"] == launch.bind["b"]):
+                pp["epi_mode"] = EPI_SILU_MUL
+                pb["epi_out"] = launch.bind["y"]
+                prev.step = f"{prev.step}+{launch.step}"
+                _shape_gemv(prev, compute_units)
+                continue
+            if (launch.entry == "fk_step_argmax" and pp["n_anchors"] == 1 and pb["y0"] == launch.bind["x"]
+                    and pp["store_tile"]):
+                pp["epi_mode"] = EPI_ARGMAX
+                prev.step = f"{prev.step}+{launch.step}"
+                _shape_gemv(prev, compute_units)
+                arg = out.buffer(f"argmax:{launch.bind['out'].split(':', 1)[1]}", "u64", prev.groups)
+                pb["arg"] = arg
+                pp["arg_slots"] = prev.groups
+                fused.append(Launch(launch.step, "fk_step_token", 1, 64,
+                                    {"arg": arg, "out": launch.bind["out"], "token": None, "position": None},
+                                    {"slots": prev.groups, "context": 1, "step": 0, "advance": 0}))
+                continue
+        fused.append(launch)
+    out.launches = fused
+
+
+GEMV_THREADS = 512
+
+
+def _shape_gemv(launch: Launch, compute_units: int) -> None:
+    """The GEMV step variant for the launch's weights, input width, rows and
+    epilogue — rows a block, packs a lane — and its grid: blocks of rows, and
+    threadgroups of 8 wavefronts up to two a CU, each wavefront taking blocks
+    in turn."""
+    p = launch.params
+    k, wt = p["k"], launch.meta["wtype"]
+    total = p["first_row"][p["n_anchors"]]
+    pairs = p["epi_mode"] == EPI_SILU_MUL
+    if wt == F16:
+        if k <= 2048:
+            r = 2 if pairs or total > 4096 else 1
+            entry, kmax = f"fk_step_gemv_f16_k2048_r{r}", 2048
+        elif k <= MAX_K:
+            r, entry, kmax = 1, "fk_step_gemv_f16_k8192_r1", 8192
+        else:
+            raise LoweringError(f"{launch.step}: an input row of {k}; the f16 GEMV steps take up to {MAX_K}")
+    elif wt == F32:
+        r = 2 if pairs else 1
+        if k <= 256:
+            entry, kmax = f"fk_step_gemv_f32_k256_r{r}", 256
+        elif k <= 1024:
+            entry, kmax = f"fk_step_gemv_f32_k1024_r{r}", 1024
+        else:
+            raise LoweringError(f"{launch.step}: an input row of {k}; the f32 GEMV steps take up to 1024")
+    else:
+        raise LoweringError(f"{launch.step}: weights of {wt}")
+    entry = f"{entry}_p{p['pro_mode']}_e{p['epi_mode']}"
+    if p["epi_mode"] == EPI_SILU_MUL:
+        if r < 2:
+            raise LoweringError(f"{launch.step}: the SiLU·mul epilogue needs blocks of row pairs")
+        blocks = -(-p["rows"][0] // (r // 2))
+    else:
+        blocks = -(-total // r)
+    p["blocks"] = blocks
+    launch.entry = entry
+    launch.threads = GEMV_THREADS
+    waves = GEMV_THREADS // 64
+    launch.groups = max(1, min(-(-blocks // waves), 2 * compute_units))
+    # The input row transposed in LDS, padded to the variant's widest row, and
+    # the norm's gains beside it.
+    norm = p["pro_mode"] in (PRO_RMSNORM, PRO_GATHER_RMSNORM)
+    launch.lds_bytes = kmax * 4 * (2 if norm else 1)
+
+
 def rope_table(theta: float, d: int, rotated: int, rows: int) -> np.ndarray:
     """RoPE's cosines and sines by position: row p holds (cos, sin) of pair i's
     angle, the binary32 product p * theta^(-2i/d), the frequency and the
@@ -159,9 +246,6 @@ def rope_table(theta: float, d: int, rotated: int, rows: int) -> np.ndarray:
     out[:, 0] = [math.cos(a) for a in angles]
     out[:, 1] = [math.sin(a) for a in angles]
     return out.reshape(rows, rotated, 2)
-
-
-GEMV_THREADS = 512
 
 
 class _StepLowering:
@@ -253,8 +337,8 @@ class _StepLowering:
         rec = self.recomputes(step)
         used: set = set()
         bind: dict = {k: None for k in ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token",
-                                        "res", "res_table", "res_token", "epi_out")}
-        params: dict = {"eps": 0.0, "factor": 1.0, "gfactor": 1.0, "has_gamma": 0, "table_rows": 1}
+                                        "res", "res_table", "res_token", "epi_out", "arg")}
+        params: dict = {"eps": 0.0, "factor": 1.0, "gfactor": 1.0, "has_gamma": 0, "table_rows": 1, "arg_slots": 0}
         wtypes = set()
         k = self.p.value(x).shape.width
         if k > MAX_K or k % 8:
@@ -293,6 +377,12 @@ class _StepLowering:
                     if gt != F32:
                         raise LoweringError(f"{step.name}: a gamma of {gt}; the kernels read f32 gammas")
                     bind["gamma"] = gname
+                else:
+                    # The kernel loads gains whatever the norm: a row of ones
+                    # it never multiplies by.
+                    width = self.p.value(op.x).shape.width
+                    bind["gamma"] = self.out.buffer(f"ones:{width}", "f32", width)
+                    self.out.constants[bind["gamma"]] = ("ones",)
                 g = gather_of(op.x)
                 if g is not None:
                     pro = PRO_GATHER_RMSNORM
@@ -320,8 +410,7 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: RMSNorm in segments of {params['seg']} of a row of {k}; the GEMV "
                                 f"prologue norms the whole row")
 
-        # Anchors: their rows one after another, in blocks of R rows.
-        R = 1
+        # Anchors: their rows one after another.
         rows, first, g = [], [0], 0
         anchor_outs = {}
         for j, a in enumerate(anchors):
@@ -330,7 +419,7 @@ class _StepLowering:
             bind[f"w{j}"] = wname
             n = self.p.value(a.outputs[0]).shape.width
             rows.append(n)
-            g += -(-n // R)
+            g += n
             first.append(g)
             anchor_outs[a.outputs[0]] = j
         if len(wtypes) != 1:
@@ -380,11 +469,10 @@ class _StepLowering:
         if epi != EPI_NONE and bind["epi_out"] is None:
             raise LoweringError(f"{step.name}: an epilogue whose value isn't stored")
         params.update(n_anchors=len(anchors), rows=rows + [0] * (3 - len(rows)),
-                      first_group=first + [g] * (4 - len(first)), k=k, store_tile=store_tile)
-        entry = f"fk_step_gemv_{wt}_r{R}"
-        waves = GEMV_THREADS // 64
-        groups = min(-(-g // waves), 2 * self.compute_units)
-        return Launch(step.name, entry, groups, GEMV_THREADS, bind, params)
+                      first_row=first + [g] * (4 - len(first)), k=k, store_tile=store_tile)
+        launch = Launch(step.name, "", 0, GEMV_THREADS, bind, params, {"wtype": wt})
+        _shape_gemv(launch, self.compute_units)
+        return launch
 
     def rope_of(self, step: Step, node, rec: dict) -> Optional[int]:
         if not isinstance(node.op, Rope):
@@ -512,7 +600,7 @@ class _StepLowering:
         if splits > 256:
             raise LoweringError(f"{step.name}: {splits} splits; the combine takes up to 256")
         params = {"heads": spec.heads, "head_dim": spec.head_dim, "splits": splits}
-        return Launch(step.name, "fk_step_combine", spec.heads, 64 if spec.head_dim <= 64 else THREADS,
+        return Launch(step.name, "fk_step_combine", spec.heads, 64,
                       {"partials": pname, "out": self.value(out)}, params)
 
     def light_step(self, step: Step) -> Launch:

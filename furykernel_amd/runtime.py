@@ -88,6 +88,7 @@ ENTRY_POINTS: list[tuple[str, object, list]] = [
     ("fk_event_destroy", _int, [_vp]),
     ("fk_event_record", _int, [_vp, _vp]),
     ("fk_event_sync", _int, [_vp]),
+    ("fk_stream_wait_event", _int, [_vp, _vp]),
     ("fk_event_elapsed_ms", _int, [_vp, _vp, ctypes.POINTER(ctypes.c_float)]),
     ("fk_graph_begin", _int, [_vp, _vp]),
     ("fk_graph_end", _int, [_vp, _vp, _PP]),
@@ -202,6 +203,10 @@ class Stream:
     def __init__(self, device: "Device", handle: int | None):
         self.device = device
         self.handle = handle
+
+    def wait(self, event: "Event") -> None:
+        """Work queued on this stream from now on waits for the event."""
+        _check(self.device.ctx, library().fk_stream_wait_event(self.handle, event.handle))
 
 
 def _sh(stream: Stream | None):

@@ -14,15 +14,17 @@ Counted per launch, from its parameters and the buffer types it binds:
   position, or the window), the query rows, the RoPE row and the partials
   written; with the store folded in, the new rows read and stored;
 - combine: the partials read and the combined rows written;
-- argmax, SiLU·mul: their rows.
+- argmax, SiLU·mul: their rows; a folded SiLU·mul its stored row, a folded
+  argmax its threadgroups' 64-bit keys, the token launch those keys read and
+  the token written.
 """
 
 from __future__ import annotations
 
-from .lower import EPI_ADD_GATHER, EPI_ADD_STORED, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, \
-    Launch, Lowered
+from .lower import EPI_ADD_GATHER, EPI_ADD_STORED, EPI_ARGMAX, EPI_SILU_MUL, PRO_GATHER, PRO_GATHER_RMSNORM, \
+    PRO_SILU_MUL, Launch, Lowered
 
-_ELT = {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2}
+_ELT = {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2, "u64": 8}
 
 
 def _elt(lowered: Lowered, name: str) -> int:
@@ -54,7 +56,13 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
             total += rows[0] * 4 * 2
         elif p["epi_mode"] == EPI_ADD_GATHER:
             total += rows[0] * _elt(lowered, b["res_table"]) + 4 + rows[0] * 4
+        elif p["epi_mode"] == EPI_SILU_MUL:
+            total += rows[0] * 4
+        elif p["epi_mode"] == EPI_ARGMAX:
+            total += 8 * launch.groups
         return total
+    if e == "fk_step_token":
+        return 8 * p["slots"] + 4
     if e == "fk_step_store":
         row = p["kv_heads"] * p["head_dim"]
         cache = 2 if p["cache_bf16"] or lowered.buffers[b["c0"]].dtype == "f16" else 4

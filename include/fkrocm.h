@@ -152,6 +152,9 @@ int fk_event_create(fk_ctx *ctx, fk_event **out);
 int fk_event_destroy(fk_event *event);
 int fk_event_record(fk_event *event, fk_stream *stream);
 int fk_event_sync(fk_event *event);
+/* Work queued on `stream` after this call waits for the event's last record
+ * (cross-stream ordering; under graph capture, an edge of the graph). */
+int fk_stream_wait_event(fk_stream *stream, fk_event *event);
 /* Milliseconds from `start` to `end`, both recorded and complete. */
 int fk_event_elapsed_ms(fk_event *start, fk_event *end, float *ms);
 

@@ -18,7 +18,9 @@ import numpy as np
 
 from . import fkref
 
-NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16}
+NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16,
+      "u64": np.uint64}
+EPI_SILU_MUL, EPI_ARGMAX = 3, 4
 TYPE = {"f16": fkref.F16, "f32": fkref.F32}
 
 
@@ -51,16 +53,49 @@ class CpuTarget:
         if e.startswith("fk_step_gemv"):
             wt = "f16" if "_f16_" in e else "f32"
             n = p["n_anchors"]
+            epi = p["epi_mode"]
+            folded = epi in (EPI_SILU_MUL, EPI_ARGMAX)
+            # A folded epilogue reads the anchors' tiles: kept here whether or not
+            # the step stores them.
+            tiles = [self.buffers[b[f"y{j}"]] if b[f"y{j}"] else np.zeros(p["rows"][j], np.float32)
+                     for j in range(n)]
             ws = (ctypes.c_void_p * 3)(*[self._p(b[f"w{j}"]) for j in range(3)])
-            ys = (ctypes.c_void_p * 3)(*[self._p(b[f"y{j}"]) for j in range(3)])
+            ys = (ctypes.c_void_p * 3)(*([t.ctypes.data for t in tiles] + [None] * (3 - n)))
             rows = (ctypes.c_int * 3)(*p["rows"])
             tok = int(self.buffers[b["token"]][0]) if b["token"] else 0
             rtok = int(self.buffers[b["res_token"]][0]) if b["res_token"] else 0
             st = L.fkref_step_gemv(ws, TYPE[wt], ys, rows, n, p["k"], p["pro_mode"], self._p(b["src"]),
                                    self._p(b["src2"]), self._p(b["gamma"]) if p["has_gamma"] else None,
                                    self._p(b["table"] or b["res_table"]), tok, p["table_rows"], p["seg"], p["eps"],
-                                   p["factor"], p["gfactor"], p["epi_mode"], self._p(b["res"]),
-                                   self._p(b["res_table"]), rtok, self._p(b["epi_out"]), launch.threads, self.width)
+                                   p["factor"], p["gfactor"], 0 if folded else epi, self._p(b["res"]),
+                                   self._p(b["res_table"]), rtok, None if folded else self._p(b["epi_out"]),
+                                   launch.threads, self.width)
+            if not st and epi == EPI_SILU_MUL:
+                st = L.fkref_silu_mul(tiles[0].ctypes.data, tiles[1].ctypes.data, self._p(b["epi_out"]), p["rows"][0])
+            if not st and epi == EPI_ARGMAX:
+                # Each threadgroup's largest key into its slot: row blocks of
+                # `rows_per_block` rows, block b taken by wavefront b mod (all
+                # wavefronts), of 64 threads each.
+                n_rows = p["rows"][0]
+                keys = np.array([L.fkref_argmax_key(float(v), i) for i, v in enumerate(tiles[0][:n_rows])],
+                                np.uint64)
+                rows_per_block = -(-n_rows // p["blocks"])
+                waves = launch.threads // 64
+                total_waves = launch.groups * waves
+                blocks = np.arange(n_rows) // rows_per_block
+                group = (blocks % total_waves) // waves
+                arg = self.buffers[b["arg"]]
+                arg[:] = 0
+                np.maximum.at(arg, group, keys)
+        elif e == "fk_step_token":
+            top = int(self.buffers[b["arg"]][:p["slots"]].max())
+            t = 0xFFFFFFFF - (top & 0xFFFFFFFF)
+            self.buffers[b["out"]][0] = t
+            if p["advance"]:
+                self.buffers[b["token"]][0] = t
+                pos = self.buffers[b["position"]]
+                pos[0] = (int(pos[0]) + p["step"]) % p["context"]
+            st = 0
         elif e == "fk_step_store":
             st = L.fkref_step_store(self._p(b["x0"]), self._p(b["x1"]), self._p(b["c0"]), self._p(b["c1"]),
                                     p["n_stores"], p["rope"][0], p["rope"][1], p["kv_heads"], p["head_dim"],

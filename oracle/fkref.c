@@ -540,3 +540,24 @@ uint32_t fkref_argmax(const float *x, int n) {
     if (x[i] > x[best]) best = (uint32_t)i;
   return best;
 }
+
+uint64_t fkref_argmax_key(float v, uint32_t index) {
+  uint32_t hi;
+  if (isnan(v)) {
+    hi = index == 0 ? 0xFFFFFFFFu : 0u;
+  } else {
+    uint32_t b = 0;
+    if (v != 0.0f) memcpy(&b, &v, 4);
+    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - index);
+}
+
+uint64_t fkref_argmax_keyed(const float *x, int n) {
+  uint64_t best = 0;
+  for (int i = 0; i < n; i++) {
+    uint64_t k = fkref_argmax_key(x[i], (uint32_t)i);
+    if (k > best) best = k;
+  }
+  return best;
+}

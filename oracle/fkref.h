@@ -118,6 +118,12 @@ int fkref_step_combine(const float *partials, float *out, int heads, int head_di
 
 /* The index of the largest element, ties to the lowest (Eval.hs:681-685). */
 uint32_t fkref_argmax(const float *x, int n);
+/* The greedy token's fold as a maximum of 64-bit keys (the order of the value,
+ * +0 and -0 equal, a NaN at index 0 above all and one elsewhere below all;
+ * then the complement of the index): the key of one element, and the largest
+ * key of a row of n (0 for n = 0). */
+uint64_t fkref_argmax_key(float v, uint32_t index);
+uint64_t fkref_argmax_keyed(const float *x, int n);
 
 /* SiLU(a) * b elementwise: a / (1 + exp(-a)) * b, exp binary64's rounded once. */
 int fkref_silu_mul(const float *a, const float *b, float *y, int n);

@@ -1,0 +1,142 @@
+"""Every memory access a GEMV step launch makes, computed on the CPU the way
+fk_step_gemv.h computes it (the prologue's loads, each wavefront's blocks of
+rows and their weight loads, the residual loads, the stores, the argmax
+slots, the LDS slots), and checked against the sizes of the buffers the
+launch binds.  A launch is never sent to the GPU with a grid or a shape
+whose accesses this finds out of bounds.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+WAVE = 64
+THREADS = 512
+PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = range(5)
+EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX = range(5)
+ELT = {"f32": 4, "f16": 2, "bf16": 2, "u32": 4, "u16": 2, "u64": 8}
+
+
+def shape_of(entry: str) -> tuple[int, int, int, int]:
+    """(weight bytes, pack elements P, rows a block R, packs a lane KPL)."""
+    parts = entry.split("_")  # fk step gemv <wt> k<K> r<R> p<> e<>
+    wt, kmax, r = parts[3], int(parts[4][1:]), int(parts[5][1:])
+    eb = 2 if wt == "f16" else 4
+    p = 16 // eb
+    return eb, p, r, kmax // (WAVE * p)
+
+
+class Bad(AssertionError):
+    pass
+
+
+def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
+    """Raises Bad naming the first access out of bounds; `buffers` maps a
+    logical buffer to its BufferSpec, `groups` overrides the launch's grid."""
+    prm, bind = launch.params, launch.bind
+    groups = launch.groups if groups is None else groups
+    if launch.threads != THREADS:
+        raise Bad(f"{launch.entry}: {launch.threads} threads")
+    eb, P, R, KPL = shape_of(launch.entry)
+    pro, epi = prm["pro_mode"], prm["epi_mode"]
+    k, n_anchors, rows, first = prm["k"], prm["n_anchors"], prm["rows"], prm["first_row"]
+    blocks = prm["blocks"]
+    C = P // 4
+    NPK = max(1, KPL * P // 32)
+    XT = WAVE * P * KPL // 4
+    packs, packs4 = k // P, k // 4
+    gather = pro in (PRO_GATHER, PRO_GATHER_RMSNORM)
+    norm = pro in (PRO_RMSNORM, PRO_GATHER_RMSNORM)
+
+    def elems(name: str) -> int:
+        if bind.get(name) is None:
+            raise Bad(f"{launch.entry}: {name} is read or written but not bound")
+        return buffers[bind[name]].count
+
+    def need(name: str, idx: np.ndarray, what: str, width: int = 1) -> None:
+        n = elems(name)
+        idx = np.asarray(idx)
+        if idx.size and (idx.min() < 0 or idx.max() + width > n):
+            raise Bad(f"{launch.entry}: {what} reads/writes {name}[{int(idx.min())}..{int(idx.max()) + width - 1}] "
+                      f"of {n}")
+
+    # LDS: the kernel's dynamic LDS holds xt[XT] float4s (and gt[XT] for the norm).
+    if launch.lds_bytes < XT * 16 * (2 if norm else 1):
+        raise Bad(f"{launch.entry}: {launch.lds_bytes} bytes of LDS for {XT} float4s")
+    if k > WAVE * P * KPL or k % P or k % 4:
+        raise Bad(f"{launch.entry}: k = {k} for packs of {P}, {KPL} a lane")
+    if n_anchors < 1 or n_anchors > 3 or any(rows[a] < 1 for a in range(n_anchors)):
+        raise Bad(f"{launch.entry}: anchors {rows}")
+
+    # Prologue loads (thread t, m < NPK): j = min(t + 512 m, packs4 - 1).
+    t = np.arange(THREADS)
+    j = np.minimum(t[:, None] + THREADS * np.arange(NPK)[None, :], packs4 - 1).ravel()
+    if gather:
+        table_rows = prm["table_rows"]
+        need("token", np.array([0]), "the token")
+        tok = table_rows - 1  # the largest row a clamped token reaches
+        need("table", tok * k + 4 * j, "the gathered row", 4)
+    else:
+        need("src", 4 * j, "the stored row", 4)
+    if pro == PRO_SILU_MUL:
+        need("src2", 4 * j, "the second row", 4)
+    if norm:
+        need("gamma", 4 * j, "the gains", 4)
+    # LDS writes: xt_at(j) for j < max(packs4, XT) within t + 512 m.
+    jj = (t[:, None] + THREADS * np.arange(NPK)[None, :]).ravel()
+    jj = jj[jj < max(packs4, XT)]
+    pk = jj // C
+    at = ((pk // WAVE) * C + jj % C) * WAVE + pk % WAVE
+    if at.size and at.max() >= XT:
+        raise Bad(f"{launch.entry}: LDS slot {int(at.max())} of {XT}")
+
+    # Blocks: wavefront gw takes b = gw, gw + total, ... while b < blocks, and
+    # issues its first block's loads (clamped) even when gw is past the blocks.
+    total_waves = groups * (THREADS // WAVE)
+    issued = np.unique(np.concatenate([np.arange(total_waves), np.arange(blocks)]))
+
+    lanes = np.arange(WAVE)
+    jl = np.minimum(lanes[:, None] + WAVE * np.arange(KPL)[None, :], packs - 1).ravel()
+    for q in range(R):
+        b = issued
+        if epi == EPI_SILU_MUL:
+            H = max(R // 2, 1)
+            a = np.where(q < H, 0, 1)
+            a = np.full(b.shape, a)
+            row = b * H + q % H
+            live = (b < blocks) & (row < rows[0])
+        else:
+            g = b * R + q
+            a = ((n_anchors > 1) & (g >= first[1])).astype(int) + ((n_anchors > 2) & (g >= first[2])).astype(int)
+            row = g - np.array(first)[a]
+            live = (b < blocks) & (g < first[n_anchors])
+        for an in range(n_anchors):
+            sel = a == an
+            if not sel.any():
+                continue
+            n = rows[an]
+            r = np.minimum(row[sel], n - 1)
+            need(f"w{an}", (r[:, None] * k + jl[None, :] * P).ravel(), f"anchor {an}'s weights", P)
+            lv = live[sel]
+            rl = row[sel][lv]
+            if rl.size:
+                if prm["store_tile"]:
+                    need(f"y{an}", rl, f"anchor {an}'s tile")
+                if epi in (EPI_ADD_STORED, EPI_ADD_GATHER):
+                    need("epi_out", rl, "the epilogue row")
+                    if epi == EPI_ADD_STORED:
+                        need("res", np.minimum(rl, n - 1), "the residual")
+                    else:
+                        need("res_token", np.array([0]), "the residual's token")
+                        need("res_table", (prm["table_rows"] - 1) * n + np.minimum(rl, n - 1), "the gathered residual")
+                if epi == EPI_SILU_MUL and an == 0:
+                    need("epi_out", rl, "the SiLU·mul row")
+            # residual loads also happen for live blocks' lanes < R with a clamped row
+            if epi == EPI_ADD_STORED and (b[sel] < blocks).any():
+                need("res", np.minimum(row[sel][b[sel] < blocks], n - 1), "the residual (clamped)")
+    if epi == EPI_ARGMAX:
+        slots = prm["arg_slots"]
+        if slots > elems("arg"):
+            raise Bad(f"{launch.entry}: {slots} argmax slots in a buffer of {elems('arg')}")
+    if epi == EPI_SILU_MUL and (n_anchors != 2 or rows[0] != rows[1] or R < 2):
+        raise Bad(f"{launch.entry}: the SiLU·mul epilogue on anchors {rows[:n_anchors]}, blocks of {R}")

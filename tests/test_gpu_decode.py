@@ -80,16 +80,20 @@ def test_tiny_decode_graph_replays_agree_with_eager(device, kernels):
         s.close()
 
 
-@pytest.mark.parametrize("layers", [2])
-def test_1b_decode_step_bit_exact(device, kernels, layers):
+@pytest.mark.parametrize("store_gelus", [False, True])
+def test_1b_decode_step_bit_exact(device, kernels, store_gelus):
     """The 1B-class step's real shapes (2 of its 16 layers, and the head) at the
-    full context: position 4095 reads all 4096 positions of every cache."""
-    s = DecodeSession(device, kernels, ONE_B, PlanOptions(), embed=True, layers=layers)
+    full context: position 4095 reads all 4096 positions of every cache.  With
+    the plan's SiLU·mul recomputed in the down projection's prologue, and
+    stored (folded into the gate/up step's epilogue)."""
+    layers = 2
+    s = DecodeSession(device, kernels, ONE_B, PlanOptions(store_gelus=store_gelus), embed=True, layers=layers)
     try:
         s.init_synthetic()
         s.set_position(4095, token=31999)
         cpu = mirror(s)
-        print(f"1B decode ({layers} layers) at position 4095: {len(s.lowered.launches)} launches", flush=True)
+        print(f"1B decode ({layers} layers, store_gelus {store_gelus}) at position 4095: "
+              f"{len(s.lowered.launches)} launches", flush=True)
         s.step()
         device.sync()
         cpu.run()
@@ -100,9 +104,9 @@ def test_1b_decode_step_bit_exact(device, kernels, layers):
 
 
 def test_1b_full_decode_greedy_tokens_via_graph(device, kernels):
-    """All 16 layers: three greedy tokens by graph replay, each step's token the
-    CPU target's for the same state."""
-    s = DecodeSession(device, kernels, ONE_B, PlanOptions(), embed=True)
+    """All 16 layers, planned as the benchmark plans them: three greedy tokens by
+    graph replay, each step's token the CPU target's for the same state."""
+    s = DecodeSession(device, kernels, ONE_B, PlanOptions(store_gelus=True), embed=True)
     try:
         s.init_synthetic()
         s.set_position(4000, token=7)

@@ -50,30 +50,64 @@ def test_a_1b_layer_is_six_launches():
     low = lowered(ONE_B, embed=True)
     entries = [launch.entry for launch in low.launches]
     assert len(entries) == 16 * 6 + 2
-    assert entries[:6] == ["fk_step_gemv_f16_r1", "fk_step_attend", "fk_step_combine"] + \
-        ["fk_step_gemv_f16_r1"] * 3
+    assert entries[:6] == ["fk_step_gemv_f16_k2048_r1_p3_e0", "fk_step_attend", "fk_step_combine",
+                           "fk_step_gemv_f16_k2048_r1_p0_e2", "fk_step_gemv_f16_k2048_r2_p1_e0",
+                           "fk_step_gemv_f16_k8192_r1_p4_e1"]
+    assert entries[6:12] == ["fk_step_gemv_f16_k2048_r1_p1_e0", "fk_step_attend", "fk_step_combine",
+                             "fk_step_gemv_f16_k2048_r1_p0_e1", "fk_step_gemv_f16_k2048_r2_p1_e0",
+                             "fk_step_gemv_f16_k8192_r1_p4_e1"]
     attend = low.launches[1]
     assert attend.step == "s1_store+s2_attend"
     assert (attend.params["store"], attend.params["krope"]) == (1, 1)
     assert attend.groups == ONE_B.kv_heads * attend.params["splits"]
+    # The greedy token folds into the logits' GEMV step, then a token launch.
+    head, token = low.launches[-2:]
+    assert head.entry == "fk_step_gemv_f16_k2048_r2_p1_e4" and head.bind["arg"] == "argmax:token"
+    assert low.buffers["argmax:token"].count == head.groups == token.params["slots"]
+    assert token.entry == "fk_step_token" and token.bind["out"] == "value:token"
+
+
+def test_a_stored_silu_mul_folds_into_the_gate_and_up_step():
+    low = lowered(ONE_B, PlanOptions(store_gelus=True), embed=True)
+    assert len(low.launches) == 16 * 6 + 2
+    gu, down = low.launches[4], low.launches[5]
+    assert gu.step.endswith("_act") and gu.params["epi_mode"] == 3 and gu.bind["epi_out"] == "value:l0_act"
+    assert gu.entry == "fk_step_gemv_f16_k2048_r2_p1_e3" and gu.params["blocks"] == ONE_B.ffn
+    assert down.entry == "fk_step_gemv_f16_k8192_r1_p0_e1" and down.bind["src"] == "value:l0_act"
 
 
 def test_unfused_lowering_keeps_the_plans_steps():
     low = lowered(ONE_B, embed=True, fuse=False)
     assert [launch.entry for launch in low.launches[:7]] == [
-        "fk_step_gemv_f16_r1", "fk_step_store", "fk_step_attend", "fk_step_combine"] + ["fk_step_gemv_f16_r1"] * 3
+        "fk_step_gemv_f16_k2048_r1_p3_e0", "fk_step_store", "fk_step_attend", "fk_step_combine",
+        "fk_step_gemv_f16_k2048_r1_p0_e2", "fk_step_gemv_f16_k2048_r2_p1_e0", "fk_step_gemv_f16_k8192_r1_p4_e1"]
+    assert low.launches[-1].entry == "fk_step_argmax"
 
 
 @pytest.mark.parametrize("position", [0, 5, 31])
 @pytest.mark.parametrize("options", [PlanOptions(), PlanOptions(store_gelus=True)])
-def test_fused_attention_computes_the_two_steps(position, options):
+def test_fused_launches_compute_the_plans_steps(position, options):
+    """Each layer's KV store folded into its attention (and, when the plan
+    stores the SiLU·mul, that light step folded into the gate/up GEMV step);
+    the greedy token folded into the logits' step and a token launch."""
     fused, apart = lowered(TINY32, options), lowered(TINY32, options, fuse=False)
-    assert len(apart.launches) - len(fused.launches) == TINY32.layers
+    per_layer = 2 if options.store_gelus else 1
+    assert len(apart.launches) - len(fused.launches) == TINY32.layers * per_layer
     a, b = seeded(fused, 7, position), seeded(apart, 7, position)
     a.run()
     b.run()
     for name in apart.buffers:
         assert np.array_equal(a.read(name).view(np.uint8), b.read(name).view(np.uint8)), name
+
+
+def test_every_lowered_entry_is_in_the_launch_table():
+    from furykernel_amd.kernels import ABIS
+
+    for dims, opts in [(ONE_B, PlanOptions()), (ONE_B, PlanOptions(store_gelus=True)), (TINY32, PlanOptions()),
+                       (TINY32, PlanOptions(store_gelus=True))]:
+        for fuse in (True, False):
+            for launch in lowered(dims, opts, fuse=fuse, embed=True).launches:
+                assert launch.entry in ABIS, launch.entry
 
 
 def test_bf16_caches_fuse_the_same_way():

@@ -102,3 +102,38 @@ def test_softmax_against_f64():
     spec = e / e.sum(axis=1, keepdims=True)
     assert np.max(np.abs(y - spec) / spec) < 1e-5
     assert np.allclose(y.sum(axis=1), 1.0, atol=1e-5)
+
+
+def _fold(x):
+    """src/FuryKernel/Program/Eval.hs:681-685: foldl1, a later element wins
+    only if strictly larger."""
+    best = 0
+    for i in range(1, len(x)):
+        if x[i] > x[best]:
+            best = i
+    return best
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_argmax_keys_give_the_folds_index(seed):
+    """The 64-bit key maximum the logits' GEMV step folds the greedy token into
+    picks the index the evaluator's fold picks: ties to the lowest index, +0
+    and -0 equal, a NaN at index 0 kept, NaNs elsewhere never taken."""
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 300))
+    pool = np.array([0.0, -0.0, 1.0, -1.0, 2.5, np.inf, -np.inf, np.nan, 1e-40, -1e-40], np.float32)
+    x = np.where(rng.random(n) < 0.5, rng.choice(pool, n), rng.integers(-3, 4, n)).astype(np.float32)
+    if seed % 5 == 0:
+        x[0] = np.nan
+    L = fkref.lib()
+    key = int(L.fkref_argmax_keyed(x.ctypes.data, n))
+    assert 0xFFFFFFFF - (key & 0xFFFFFFFF) == _fold(x.tolist()) == int(L.fkref_argmax(x.ctypes.data, n))
+
+
+def test_argmax_key_special_cases():
+    L = fkref.lib()
+    for x, want in [([-0.0, 0.0], 0), ([0.0, -0.0], 0), ([np.nan, 5.0], 0), ([5.0, np.nan, 6.0], 2),
+                    ([-np.inf, np.nan], 0), ([1.0, 1.0, 2.0, 2.0], 2), ([-np.inf] * 3, 0), ([np.nan] * 3, 0)]:
+        a = np.array(x, np.float32)
+        key = int(L.fkref_argmax_keyed(a.ctypes.data, len(a)))
+        assert 0xFFFFFFFF - (key & 0xFFFFFFFF) == want == _fold(a.tolist()), x
