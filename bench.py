@@ -57,7 +57,36 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="queue each step's launches on the stream instead of replaying a HIP graph")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only read and write 1 GiB with the streaming kernels (the known sizes that scale the "
+                         "HBM counters FETCH_SIZE and WRITE_SIZE)")
     return ap.parse_args()
+
+
+CALIBRATE_BYTES = 1 << 30
+
+
+def calibrate() -> int:
+    """Three fills (1 GiB written) and three streaming reads (1 GiB read) of one
+    buffer, each its own dispatch: what FETCH_SIZE and WRITE_SIZE count for a
+    known size, per dispatch."""
+    from furykernel_amd import kernels, runtime
+
+    dev = runtime.Device(0)
+    ks = kernels.Kernels(dev)
+    buf = dev.alloc(CALIBRATE_BYTES)
+    out = dev.alloc(1 << 20)
+    for _ in range(3):
+        ks.fill_u32(buf, 0x3C003C00)
+    for _ in range(3):
+        ks.stream_read(buf, out, 4096)
+    dev.sync()
+    print(json.dumps({"calibrate": {"fk_fill_u32": {"dispatches": 3, "bytes_written": CALIBRATE_BYTES},
+                                    "fk_stream_read": {"dispatches": 3, "bytes_read": CALIBRATE_BYTES}}}), flush=True)
+    buf.free()
+    out.free()
+    dev.close()
+    return 0
 
 
 def log(msg: str) -> None:
@@ -110,6 +139,22 @@ def kernel_table(session, reps: int, eager: bool) -> dict:
     return table
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "traffic_decode_1b_f16.md"
+
+
+def measured_traffic(entry: str):
+    """HBM bytes a launch of `entry` moves, as the committed rocprofv3 counter
+    runs measured them (FETCH_SIZE and WRITE_SIZE, each scaled by what it
+    reads for a copy of known size); None if the profile has no row for it."""
+    if not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 7 and cells[0] == entry:
+            return int(cells[4])
+    return None
+
+
 def cpu_baseline(dims, seconds: float) -> dict:
     """The oracle's CPU target (width 32, one thread) on layer 0's launches and
     the head's, repeated for about `seconds`; a token costs the layers' launches
@@ -157,6 +202,8 @@ def cpu_baseline(dims, seconds: float) -> dict:
 
 def main() -> int:
     args = parse()
+    if args.calibrate:
+        return calibrate()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} (WORLD_SIZE {world}) is not run. "
@@ -237,7 +284,7 @@ def main() -> int:
                 "frac_of_peak": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4), "peak_gbps": HBM_PEAK_GBPS,
                 "ms_per_step_events": round(event_ms / args.steps, 4)},
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(dominant),
                      "avg_launch_us": dom["avg_us"], "bytes_per_launch": dom["bytes_per_launch"],
                      "launches_per_step": dom["launches"]},
         "kernels": table,

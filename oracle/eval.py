@@ -1,0 +1,278 @@
+"""The program evaluator in binary64: what a checked program's step computes,
+each operation exact to double precision, rounded only where the program
+rounds (its cache stores), following src/FuryKernel/Program/Eval.hs
+operation for operation.  The values only: the per-element bounds
+(`Approx`, Eval.hs:691-918) are not restated.
+
+TEST INFRASTRUCTURE: imported only by tests/, as the f64 checker of the
+target's f32 arithmetic (and of the oracle's CPU target).
+
+Bindings (Eval.hs:126-140): ``inputs`` name -> rows of values; ``weights``
+name -> flat values; ``row_ints`` name -> rows of integers; ``caches`` name ->
+{slot: flat values of the slot}.  Rows are evaluated together, ``rows`` of
+them.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from furykernel_amd.program.check import CheckedProgram
+from furykernel_amd.program.graph import (
+    CACHE_BF16, Add, ArgMax, Attend, Concat, Gather, GatedGelu, GELU_TANH, GeluMul, Input, KvStore, Linear, Ring,
+    RmsNorm, Rope, SCache, ScaleBy, SILU, Softcap)
+
+from . import fkref
+
+
+class EvalError(ValueError):
+    """What the evaluator refuses, as Eval.hs's Left."""
+
+
+@dataclass
+class Bindings:
+    rows: int = 1
+    inputs: dict = field(default_factory=dict)
+    weights: dict = field(default_factory=dict)
+    row_ints: dict = field(default_factory=dict)
+    caches: dict = field(default_factory=dict)
+
+
+@dataclass
+class Evaluation:
+    values: dict    # value name -> [rows] of f64 arrays
+    outputs: dict   # output name -> [rows] of f64 arrays
+    caches: dict    # cache name -> {slot: f64 array}
+
+
+def hsum(xs) -> float:
+    """Haskell's ``sum`` of a list of Doubles: a left fold from 0, each
+    addition rounded (the evaluator's sums, e.g. ``dot`` at Eval.hs:973-974)."""
+    s = 0.0
+    for v in xs:
+        s = s + float(v)
+    return s
+
+
+def round_bf16(x: float) -> float:
+    """roundBF16 (Eval.hs:669-684): to eight significant bits, ties to even,
+    binary32's exponent range with gradual underflow, overflow to infinity —
+    directly from the double."""
+    if math.isnan(x) or math.isinf(x) or x == 0:
+        return x
+    _, e = math.frexp(x)          # x = m 2^e, 1/2 <= |m| < 1: the leading bit is 2^(e-1)
+    ulp = math.ldexp(1.0, max(-126, e - 1) - 7)
+    r = round(x / ulp) * ulp      # x / ulp is exact; round() is to nearest, ties to even
+    return math.copysign(math.inf, x) if abs(r) >= 2.0 ** 128 else r
+
+
+def round_f16(x: float) -> float:
+    """roundTo CacheF16 (Eval.hs:937-939): binary64 to binary16 in one rounding."""
+    return float(fkref.widen_f16(fkref.narrow_f16_f64(x)))
+
+
+def round_cache(elem: str, x: float) -> float:
+    return round_bf16(x) if elem == CACHE_BF16 else round_f16(x)
+
+
+def gelu(form: str, x: float) -> float:
+    """GELU-tanh (Eval.hs:658-663), and the SiLU form this repository adds:
+    x / (1 + e^-x)."""
+    if form == GELU_TANH:
+        return 0.5 * x * (1 + math.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x * x * x)))
+    if form == SILU:
+        return x / (1 + math.exp(-x))
+    raise EvalError(f"no GELU form {form}")
+
+
+def rotate(theta: float, rotated: int, d: int, position: float, xs: np.ndarray) -> np.ndarray:
+    """The exact rotation of one head of width d, NeoX halves (Eval.hs:634-645)."""
+    half = d // 2
+    out = np.empty(d)
+    for j in range(d):
+        i = j if j < half else j - half
+        t = position * math.pow(theta, -(2 * i) / d) if i < rotated else 0.0
+        if j < half:
+            out[j] = xs[j] * math.cos(t) - xs[j + half] * math.sin(t)
+        else:
+            out[j] = xs[j] * math.cos(t) + xs[i] * math.sin(t)
+    return out
+
+
+def arg_max(xs) -> int:
+    """Eval.hs:681-685: a later element wins only if strictly larger."""
+    best = 0
+    for j in range(1, len(xs)):
+        if xs[j] > xs[best]:
+            best = j
+    return best
+
+
+def evaluate(checked: CheckedProgram, b: Bindings) -> Evaluation:
+    """Eval.hs:186-228: every node in program order."""
+    p = checked.program
+    m = b.rows
+    sources = {s.id: s for s in p.sources}
+    values = {v.id: v for v in p.values}
+    env: dict = {}
+    caches = {name: {u: np.array(xs, np.float64) for u, xs in units.items()} for name, units in b.caches.items()}
+    stored: set = set()
+
+    def weight(s: int) -> np.ndarray:
+        src = sources[s]
+        if src.name not in b.weights:
+            raise EvalError(f"No weight {src.name}.")
+        a = np.asarray(b.weights[src.name], np.float64).ravel()
+        want = int(np.prod(src.kind.dims))
+        if a.size != want:
+            raise EvalError(f"{src.name} is bound to {a.size} elements, not the {want} it declares.")
+        return a
+
+    def ints(s: int) -> list:
+        src = sources[s]
+        if src.name not in b.row_ints:
+            raise EvalError(f"No row integers {src.name}.")
+        rows = b.row_ints[src.name]
+        if len(rows) != m:
+            raise EvalError(f"{src.name} has {len(rows)} rows, not {m}.")
+        for r, row in enumerate(rows):
+            for i in row:
+                if i >= src.kind.bound:
+                    raise EvalError(f"{src.name}: row {r} holds {i}, which isn't below its bound of {src.kind.bound}.")
+        return [[int(i) for i in row] for row in rows]
+
+    def cache_index(layout, seqs: list, position: int, h: int) -> tuple[int, int]:
+        if not isinstance(layout, Ring):
+            raise EvalError("paged caches are not evaluated here")
+        s = seqs[0] if seqs else 0
+        return s, (h * layout.length + position % layout.length) * layout.head_dim
+
+    for n in p.nodes:
+        op = n.op
+        out = n.outputs[0] if n.outputs else None
+        if isinstance(op, Input):
+            src = sources[op.source]
+            rows = b.inputs.get(src.name)
+            if rows is None:
+                raise EvalError(f"No input {src.name}.")
+            env[out] = [np.asarray(r, np.float64) for r in rows]
+        elif isinstance(op, Linear):
+            w = weight(op.weight)
+            k = values[op.x].shape.width
+            n_out = values[out].shape.width
+            wm = w.reshape(n_out, k)
+            env[out] = [np.array([hsum(wm[j] * x) for j in range(n_out)]) for x in env[op.x]]
+        elif isinstance(op, RmsNorm):
+            gamma = None if op.gamma is None else weight(op.gamma)
+            seg = values[op.x].shape.segment
+            res = []
+            for x in env[op.x]:
+                parts = []
+                for c in range(0, len(x), seg):
+                    v = x[c:c + seg]
+                    ms = hsum(v * v) / seg
+                    s = (ms + op.eps) ** -0.5
+                    g = gamma if gamma is not None else np.ones(seg)
+                    parts.append(v * s * g[:seg] * op.factor)
+                res.append(np.concatenate(parts))
+            env[out] = res
+        elif isinstance(op, Add):
+            env[out] = [x + y for x, y in zip(env[op.a], env[op.b])]
+        elif isinstance(op, Concat):
+            env[out] = [np.concatenate([x, y]) for x, y in zip(env[op.a], env[op.b])]
+        elif isinstance(op, ScaleBy):
+            w = weight(op.weight)
+            env[out] = [x * w[0] for x in env[op.x]]
+        elif isinstance(op, GatedGelu):
+            seg = values[op.x].shape.segment
+            res = []
+            for x in env[op.x]:
+                parts = []
+                for c in range(0, len(x), seg):
+                    a, g = x[c:c + seg // 2], x[c + seg // 2:c + seg]
+                    parts.append(np.array([gelu(op.form, u) * v for u, v in zip(a, g)]))
+                res.append(np.concatenate(parts))
+            env[out] = res
+        elif isinstance(op, GeluMul):
+            env[out] = [np.array([gelu(op.form, u) * v for u, v in zip(x, y)]) for x, y in zip(env[op.a], env[op.b])]
+        elif isinstance(op, Rope):
+            spec = op.spec
+            if spec.axes != 1:
+                raise EvalError("RoPE of several axes is not evaluated here")
+            d = values[op.x].shape.segment
+            ps = ints(op.positions)
+            res = []
+            for pos, x in zip(ps, env[op.x]):
+                res.append(np.concatenate([rotate(spec.theta, spec.rotated, d, float(pos[0]), x[c:c + d])
+                                           for c in range(0, len(x), d)]))
+            env[out] = res
+        elif isinstance(op, Softcap):
+            env[out] = [np.array([op.cap * math.tanh(v / op.cap) for v in x]) for x in env[op.x]]
+        elif isinstance(op, KvStore):
+            src = sources[op.at.cache]
+            if not isinstance(src.kind, SCache):
+                raise EvalError(f"{src.name} is not a cache.")
+            if src.name in stored:
+                raise EvalError(f"{n.name} stores into {src.name} again: a program stores into a cache once.")
+            stored.add(src.name)
+            lay, elem = src.kind.layout, src.kind.elem
+            units = caches.get(src.name)
+            if units is None:
+                raise EvalError(f"No cache {src.name}.")
+            ps, seqs = ints(op.at.positions), ints(op.at.sequences)
+            d, heads = lay.head_dim, lay.kv_heads
+            for pos, sq, x in zip(ps, seqs, env[op.x]):
+                for h in range(heads):
+                    u, at = cache_index(lay, sq, pos[0], h)
+                    if u not in units:
+                        raise EvalError(f"{src.name} binds no slot {u}.")
+                    for i in range(d):
+                        units[u][at + i] = round_cache(elem, float(x[h * d + i]))
+        elif isinstance(op, Attend):
+            spec = op.spec
+            ksrc, vsrc = sources[op.to.keys], sources[op.to.values]
+            lay = ksrc.kind.layout
+            if spec.reach is not None:
+                raise EvalError("attention with a reach is not evaluated here")
+            ps, seqs = ints(op.to.positions), ints(op.to.sequences)
+            d, heads = spec.head_dim, spec.heads
+            group = heads // spec.kv_heads
+            res = []
+            for pos, sq, q in zip(ps, seqs, env[op.q]):
+                position = pos[0]
+                first = max(0, position - spec.window + 1) if spec.window else 0
+                ts = range(first, position + 1)
+                row = []
+                for h in range(heads):
+                    kvh = h // group
+                    query = q[h * d:(h + 1) * d]
+                    keys, vals = [], []
+                    for t in ts:
+                        u, at = cache_index(lay, sq, t, kvh)
+                        keys.append(caches[ksrc.name][u][at:at + d])
+                        vals.append(caches[vsrc.name][u][at:at + d])
+                    scores = [spec.scale * hsum(query * kk) for kk in keys]
+                    top = max(scores)
+                    es = [math.exp(s - top) for s in scores]
+                    total = hsum(es)
+                    row.append(np.array([hsum(e / total * vv[i] for e, vv in zip(es, vals)) for i in range(d)]))
+                res.append(np.concatenate(row))
+            env[out] = res
+        elif isinstance(op, Gather):
+            table = weight(op.table)
+            width = values[out].shape.width
+            tm = table.reshape(-1, width)
+            env[out] = [sum(tm[t] for t in toks) * op.factor for toks in ints(op.tokens)]
+        elif isinstance(op, ArgMax):
+            env[out] = [np.array([float(arg_max(list(x)))]) for x in env[op.x]]
+        else:
+            raise EvalError(f"{n.name}: {type(op).__name__} is not evaluated here")
+    outs = {}
+    for o in p.outputs:
+        if o.value not in env:
+            raise EvalError(f"The output {o.name} was never made.")
+        outs[o.name] = env[o.value]
+    return Evaluation({values[v].name: rows for v, rows in env.items()}, outs, caches)

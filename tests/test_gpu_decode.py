@@ -125,3 +125,34 @@ def test_1b_full_decode_greedy_tokens_via_graph(device, kernels):
         g.destroy()
     finally:
         s.close()
+
+
+def test_tiny_decode_on_the_gpu_within_1e4_of_the_f64_evaluator(device, kernels):
+    """The tiny configuration (d_model 64, 2 layers, 4 heads of 16, FFN 256
+    SiLU-gated, vocab 256; weights, caches and input N(0, 0.02); 16 cached
+    positions before the token) on the GPU: its logits within 1e-4 (of the
+    row's largest magnitude) of the f64 program evaluator, and bit for bit the
+    CPU target's."""
+    from test_evaluator import rel, run_cpu_target, run_evaluator, tiny_state
+
+    checked, w, c, x, position = tiny_state()
+    s = DecodeSession(device, kernels, TINY32, PlanOptions(), embed=False)
+    try:
+        for name, v in w.items():
+            if f"weight:{name}" in s.lowered.buffers:
+                s.engine.write(f"weight:{name}", v)
+        for name, v in c.items():
+            s.engine.write(f"cache:{name}", v)
+        s.engine.write("value:x", x)
+        s.set_position(position)
+        print(f"tiny decode vs the f64 evaluator at position {position}", flush=True)
+        s.step()
+        device.sync()
+        logits = s.logits()
+        ev = run_evaluator(checked, w, c, x, position)
+        assert rel(logits, ev.outputs["logits"][0]) <= 1e-4
+        cpu = run_cpu_target(checked, w, c, x, position, 64)
+        assert np.array_equal(bits(logits), bits(cpu.read("value:logits")))
+        assert s.token() == int(cpu.read("value:token")[0])
+    finally:
+        s.close()
