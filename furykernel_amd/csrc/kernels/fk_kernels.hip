@@ -5,3 +5,4 @@
 #include "fk_rows.h"
 #include "fk_misc.h"
 #include "fk_step.h"
+#include "fk_gemm.h"

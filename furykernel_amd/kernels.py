@@ -81,6 +81,11 @@ class StepGemvParams(ctypes.Structure):
     ]
 
 
+class GemmParams(ctypes.Structure):
+    _fields_ = [("m", ctypes.c_uint32), ("k", ctypes.c_uint32), ("n_anchors", ctypes.c_uint32),
+                ("first_col", ctypes.c_uint32 * 4), ("ldc", ctypes.c_uint32 * 3)]
+
+
 class StepTokenParams(ctypes.Structure):
     _fields_ = [("slots", ctypes.c_uint32), ("context", ctypes.c_uint32), ("step", ctypes.c_uint32),
                 ("advance", ctypes.c_uint32)]
@@ -185,6 +190,8 @@ ABIS: dict[str, KernelAbi] = {
     "fk_fill_u32": KernelAbi("fk_fill_u32", ("dst",), FillParams),
     **{e: KernelAbi(e, STEP_GEMV_BUFFERS, StepGemvParams, 512) for e in STEP_GEMV_ENTRIES},
     "fk_step_token": KernelAbi("fk_step_token", ("arg", "out", "token", "position"), StepTokenParams, 64),
+    **{f"fk_gemm_f16_{mode}": KernelAbi(f"fk_gemm_f16_{mode}", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0"),
+                                        GemmParams, 256) for mode in ("store", "add", "silu_mul")},
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
     "fk_step_attend": KernelAbi("fk_step_attend", ("q", "knew", "vnew", "kc", "vc", "position", "slot", "rope",
@@ -252,6 +259,53 @@ class Kernels:
         rows_per_group = threads // WAVE * rows_per_wave
         groups = (n + rows_per_group - 1) // rows_per_group
         self.launch(entry, groups, threads, bound, GemvParams(n, k), stream)
+
+    # C = A Bᵀ on the matrix cores (fk_gemm.h): the prefill GEMM.
+    GEMM_TILE, GEMM_BK, GEMM_LDS = 256, 32, 2 * 256 * 40 * 2
+
+    def gemm(self, a: runtime.Buffer, bs: list, cs: list, m: int, k: int, rows: list, mode: str = "store",
+             r: runtime.Buffer | None = None, stream: runtime.Stream | None = None) -> None:
+        """A [m, k] f16 times the weights bs[j] ([rows[j], k] f16, the anchors)
+        into cs[j] ([m, rows[j]] f32; "add": plus r, [m, rows[0]] f32; "silu_mul":
+        two anchors, gate and up, into cs[0] [m, rows[0]] f16 as silu(gate) up)."""
+        entry = f"fk_gemm_f16_{mode}"
+        if entry not in ABIS:
+            raise LaunchError(f"no GEMM {entry}")
+        t = self.GEMM_TILE
+        if m <= 0 or m % t or k <= 0 or k % self.GEMM_BK:
+            raise LaunchError(f"{entry}: m = {m} must be a multiple of {t}, k = {k} of {self.GEMM_BK}")
+        if not 1 <= len(bs) <= 3 or len(bs) != len(rows) or len(cs) != (1 if mode == "silu_mul" else len(bs)):
+            raise LaunchError(f"{entry}: {len(bs)} weights, {len(cs)} outputs, {len(rows)} row counts")
+        unit = t // 2 if mode == "silu_mul" else t
+        if any(n <= 0 or n % unit for n in rows):
+            raise LaunchError(f"{entry}: anchors of {rows} rows, not multiples of {unit}")
+        if mode == "silu_mul" and (len(bs) != 2 or rows[0] != rows[1]):
+            raise LaunchError(f"{entry}: the SiLU·mul epilogue takes gate and up of one size")
+        if mode == "add" and (len(bs) != 1 or r is None):
+            raise LaunchError(f"{entry}: the residual epilogue takes one anchor and its residual")
+        _need(a, m * k * 2, "A", entry)
+        for j, (b, n) in enumerate(zip(bs, rows)):
+            _need(b, n * k * 2, f"B{j}", entry)
+        if mode == "silu_mul":
+            _need(cs[0], m * rows[0] * 2, "C", entry)
+            groups = (m // t) * (rows[0] // unit)
+        else:
+            for j, (c, n) in enumerate(zip(cs, rows)):
+                _need(c, m * n * 4, f"C{j}", entry)
+            groups = (m // t) * (sum(rows) // t)
+        if r is not None:
+            _need(r, m * rows[0] * 4, "R", entry)
+        first = [0]
+        for n in rows:
+            first.append(first[-1] + n)
+        first += [first[-1]] * (4 - len(first))
+        ldc = (list(rows) + [0, 0, 0])[:3]
+        bufs = {"a": a.ptr, "r0": r.ptr if r is not None else 0}
+        for j in range(3):
+            bufs[f"b{j}"] = bs[j].ptr if j < len(bs) else 0
+            bufs[f"c{j}"] = cs[j].ptr if j < len(cs) else 0
+        params = GemmParams(m, k, len(bs), (ctypes.c_uint32 * 4)(*first), (ctypes.c_uint32 * 3)(*ldc))
+        self.launch(entry, groups, 256, bufs, params, stream, lds_bytes=self.GEMM_LDS)
 
     def rmsnorm(self, x: runtime.Buffer, gamma: runtime.Buffer | None, y: runtime.Buffer, rows: int, width: int,
                 seg: int | None = None, eps: float = 1e-6, factor: float = 1.0, threads: int = 256,

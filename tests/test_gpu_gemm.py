@@ -1,0 +1,142 @@
+"""The prefill GEMM (fk_gemm.h) on the GPU against f64 sums of its f16 operands.
+
+The matrix cores sum over k in their own order, so the bar is the reference's
+bound for binary32 accumulation (test/Test/FuryKernel/GemvTest.hs:127-130;
+the tile contract of src/FuryKernel/Tile.hs:5-24): |C - exact| <=
+2 (k + 64) 2^-24 sum |a b| + 2^-126.  Small shapes check every element (and so
+the lane layout of v_mfma_f32_16x16x32_f16); the 1B prefill's shapes check
+sampled rows.  The SiLU·mul epilogue rounds to f16: within 2e-3 relative
+(the f16 bar) of the f64 value of its f32 inputs' bounds.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(2028)
+
+
+def f16(shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float16)
+
+
+def bound(a, b):
+    """Per element of a b^T: 2 (k + 64) 2^-24 sum |a b| + 2^-126."""
+    k = a.shape[1]
+    mag = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64)).T
+    return 2 * (k + 64) * 2.0**-24 * mag + 2.0**-126
+
+
+def run(device, kernels, a, bs, mode="store", r=None):
+    m, k = a.shape
+    rows = [b.shape[0] for b in bs]
+    ba = device.upload(a)
+    bb = [device.upload(b) for b in bs]
+    if mode == "silu_mul":
+        cs = [device.alloc(m * rows[0] * 2)]
+    else:
+        cs = [device.alloc(m * n * 4) for n in rows]
+    br = device.upload(r) if r is not None else None
+    print(f"gemm {mode} m {m} k {k} rows {rows}", flush=True)
+    kernels.gemm(ba, bb, cs, m, k, rows, mode, br)
+    device.sync()
+    if mode == "silu_mul":
+        out = [cs[0].read(np.float16, m * rows[0]).reshape(m, rows[0])]
+    else:
+        out = [c.read(np.float32, m * n).reshape(m, n) for c, n in zip(cs, rows)]
+    for buf in [ba, *bb, *cs] + ([br] if br is not None else []):
+        buf.free()
+    return out
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 32, 256), (256, 64, 256), (512, 128, 512), (256, 2048, 768)])
+def test_gemm_every_element_within_the_accumulation_bound(device, kernels, m, k, n):
+    a, b = f16((m, k)), f16((n, k))
+    (c,) = run(device, kernels, a, [b])
+    exact = a.astype(np.float64) @ b.astype(np.float64).T
+    assert np.all(np.abs(c - exact) <= bound(a, b))
+
+
+def test_gemm_exact_on_small_integers(device, kernels):
+    """Integers of f16 whose products and sums stay below 2^24: every order
+    gives the exact sum, so the kernel's result is bit for bit the sum."""
+    a = RNG.integers(-8, 9, (256, 256)).astype(np.float16)
+    b = RNG.integers(-8, 9, (512, 256)).astype(np.float16)
+    (c,) = run(device, kernels, a, [b])
+    assert np.array_equal(c, (a.astype(np.int64) @ b.astype(np.int64).T).astype(np.float32))
+
+
+def test_gemm_three_anchors_into_three_outputs(device, kernels):
+    """q, k, v projections of one input: anchors of 512, 256, 256 rows."""
+    a = f16((256, 128))
+    bs = [f16((512, 128)), f16((256, 128)), f16((256, 128))]
+    outs = run(device, kernels, a, bs)
+    for b, c in zip(bs, outs):
+        exact = a.astype(np.float64) @ b.astype(np.float64).T
+        assert np.all(np.abs(c - exact) <= bound(a, b))
+
+
+def test_gemm_residual_epilogue(device, kernels):
+    a, b = f16((512, 256)), f16((256, 256))
+    r = RNG.standard_normal((512, 256)).astype(np.float32)
+    (c,) = run(device, kernels, a, [b], "add", r)
+    exact = r.astype(np.float64) + a.astype(np.float64) @ b.astype(np.float64).T
+    # the residual's addition rounds once more
+    assert np.all(np.abs(c - exact) <= bound(a, b) + np.abs(exact) * 2.0**-24)
+
+
+def test_gemm_silu_mul_epilogue(device, kernels):
+    a = f16((256, 256), 0.5)
+    g, u = f16((384, 256), 0.5), f16((384, 256), 0.5)
+    (c,) = run(device, kernels, a, [g, u], "silu_mul")
+    ge = a.astype(np.float64) @ g.astype(np.float64).T
+    ue = a.astype(np.float64) @ u.astype(np.float64).T
+    exact = ge / (1 + np.exp(-ge)) * ue
+    err = np.abs(c.astype(np.float64) - exact)
+    scale = np.max(np.abs(exact))
+    assert np.max(err) <= 2e-3 * scale
+
+
+@pytest.mark.parametrize("k,rows,mode", [(2048, [2048, 512, 512], "store"), (2048, [2048], "add"),
+                                         (2048, [8192, 8192], "silu_mul"), (8192, [2048], "add")])
+def test_gemm_at_the_1b_prefill_shapes(device, kernels, k, rows, mode):
+    """8192 rows (4 sequences of 2048); QKV, O, gate/up with SiLU·mul, down.
+    Sampled rows against f64."""
+    m = 8192
+    a = f16((m, k), 0.5)
+    bs = [f16((n, k), 0.02) for n in rows]
+    r = RNG.standard_normal((m, rows[0])).astype(np.float32) if mode == "add" else None
+    outs = run(device, kernels, a, bs, mode, r)
+    pick = np.sort(RNG.choice(m, 48, replace=False))
+    ad = a[pick].astype(np.float64)
+    if mode == "silu_mul":
+        ge = ad @ bs[0].astype(np.float64).T
+        ue = ad @ bs[1].astype(np.float64).T
+        exact = ge / (1 + np.exp(-ge)) * ue
+        err = np.abs(outs[0][pick].astype(np.float64) - exact)
+        assert np.max(err) <= 2e-3 * np.max(np.abs(exact))
+        return
+    for b, c in zip(bs, outs):
+        exact = ad @ b.astype(np.float64).T
+        bnd = bound(a[pick], b)
+        if r is not None:
+            exact = exact + r[pick]
+            bnd = bnd + np.abs(exact) * 2.0**-24
+        assert np.all(np.abs(c[pick] - exact) <= bnd)
+
+
+def test_gemm_refuses_shapes_it_does_not_take(device, kernels):
+    from furykernel_amd.kernels import LaunchError
+
+    a, b = device.alloc(256 * 64 * 2), device.alloc(256 * 64 * 2)
+    c = device.alloc(256 * 256 * 4)
+    with pytest.raises(LaunchError):
+        kernels.gemm(a, [b], [c], 200, 64, [256])      # m not a multiple of 256
+    with pytest.raises(LaunchError):
+        kernels.gemm(a, [b], [c], 256, 48, [256])      # k not a multiple of 32
+    with pytest.raises(LaunchError):
+        kernels.gemm(a, [b], [c], 256, 64, [300])      # rows not a multiple of 256
+    with pytest.raises(LaunchError):
+        kernels.gemm(a, [b], [c], 256, 64, [1024])     # B smaller than the launch reads
+    for x in (a, b, c):
+        x.free()
