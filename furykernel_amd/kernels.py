@@ -260,36 +260,42 @@ class Kernels:
         groups = (n + rows_per_group - 1) // rows_per_group
         self.launch(entry, groups, threads, bound, GemvParams(n, k), stream)
 
-    # C = A Bᵀ on the matrix cores (fk_gemm.h): the prefill GEMM.
-    GEMM_TILE, GEMM_BK, GEMM_LDS = 256, 32, 2 * 256 * 40 * 2
+    # C = A Bᵀ on the matrix cores (fk_gemm.h): the prefill GEMM.  256 × 256
+    # tiles, K steps of 32 taken in pairs; LDS: a ring of 4 stages of A's and
+    # B's 256 rows × 32 halves.
+    GEMM_TILE, GEMM_K, GEMM_LDS = 256, 64, 4 * 2 * 256 * 32 * 2
 
     def gemm(self, a: runtime.Buffer, bs: list, cs: list, m: int, k: int, rows: list, mode: str = "store",
              r: runtime.Buffer | None = None, stream: runtime.Stream | None = None) -> None:
-        """A [m, k] f16 times the weights bs[j] ([rows[j], k] f16, the anchors)
-        into cs[j] ([m, rows[j]] f32; "add": plus r, [m, rows[0]] f32; "silu_mul":
-        two anchors, gate and up, into cs[0] [m, rows[0]] f16 as silu(gate) up)."""
+        """A [m, k] f16 in the tile layout (furykernel_amd.layout) times the
+        weights bs[j] ([rows[j], k] f16, tiled: the anchors) into cs[j]
+        ([m, rows[j]] f32 rows; "add": plus r, [m, rows[0]] f32, which may be
+        cs[0]).  "silu_mul": one weight, the pair of gate and up ([2 rows[0],
+        k], layout.pair), into cs[0] [m, rows[0]] f16 tiled as silu(gate) up."""
         entry = f"fk_gemm_f16_{mode}"
         if entry not in ABIS:
             raise LaunchError(f"no GEMM {entry}")
         t = self.GEMM_TILE
-        if m <= 0 or m % t or k <= 0 or k % self.GEMM_BK:
-            raise LaunchError(f"{entry}: m = {m} must be a multiple of {t}, k = {k} of {self.GEMM_BK}")
-        if not 1 <= len(bs) <= 3 or len(bs) != len(rows) or len(cs) != (1 if mode == "silu_mul" else len(bs)):
+        if m <= 0 or m % t or k <= 0 or k % self.GEMM_K:
+            raise LaunchError(f"{entry}: m = {m} must be a multiple of {t}, k = {k} of {self.GEMM_K}")
+        silu = mode == "silu_mul"
+        if not 1 <= len(bs) <= (1 if silu else 3) or len(bs) != len(rows) or len(cs) != len(bs):
             raise LaunchError(f"{entry}: {len(bs)} weights, {len(cs)} outputs, {len(rows)} row counts")
-        unit = t // 2 if mode == "silu_mul" else t
+        unit = t // 2 if silu else t
         if any(n <= 0 or n % unit for n in rows):
             raise LaunchError(f"{entry}: anchors of {rows} rows, not multiples of {unit}")
-        if mode == "silu_mul" and (len(bs) != 2 or rows[0] != rows[1]):
-            raise LaunchError(f"{entry}: the SiLU·mul epilogue takes gate and up of one size")
         if mode == "add" and (len(bs) != 1 or r is None):
             raise LaunchError(f"{entry}: the residual epilogue takes one anchor and its residual")
+        if mode != "add" and r is not None:
+            raise LaunchError(f"{entry}: a residual without the residual epilogue")
         _need(a, m * k * 2, "A", entry)
-        for j, (b, n) in enumerate(zip(bs, rows)):
-            _need(b, n * k * 2, f"B{j}", entry)
-        if mode == "silu_mul":
+        if silu:
+            _need(bs[0], 2 * rows[0] * k * 2, "the gate/up pair", entry)
             _need(cs[0], m * rows[0] * 2, "C", entry)
             groups = (m // t) * (rows[0] // unit)
         else:
+            for j, (b, n) in enumerate(zip(bs, rows)):
+                _need(b, n * k * 2, f"B{j}", entry)
             for j, (c, n) in enumerate(zip(cs, rows)):
                 _need(c, m * n * 4, f"C{j}", entry)
             groups = (m // t) * (sum(rows) // t)

@@ -4,13 +4,15 @@ The matrix cores sum over k in their own order, so the bar is the reference's
 bound for binary32 accumulation (test/Test/FuryKernel/GemvTest.hs:127-130;
 the tile contract of src/FuryKernel/Tile.hs:5-24): |C - exact| <=
 2 (k + 64) 2^-24 sum |a b| + 2^-126.  Small shapes check every element (and so
-the lane layout of v_mfma_f32_16x16x32_f16); the 1B prefill's shapes check
-sampled rows.  The SiLU·mul epilogue rounds to f16: within 2e-3 relative
-(the f16 bar) of the f64 value of its f32 inputs' bounds.
+the lane layout of v_mfma_f32_32x32x16_f16 and the tile layout); the 1B
+prefill's shapes check sampled rows.  The SiLU·mul epilogue rounds to f16:
+within 2e-3 relative (the f16 bar) of the f64 value.
 """
 
 import numpy as np
 import pytest
+
+from furykernel_amd.layout import pack, pair, unpack
 
 pytestmark = pytest.mark.gpu
 RNG = np.random.default_rng(2028)
@@ -28,20 +30,23 @@ def bound(a, b):
 
 
 def run(device, kernels, a, bs, mode="store", r=None):
+    """bs: the weights; for "silu_mul", [gate, up]."""
     m, k = a.shape
-    rows = [b.shape[0] for b in bs]
-    ba = device.upload(a)
-    bb = [device.upload(b) for b in bs]
+    ba = device.upload(pack(a))
     if mode == "silu_mul":
+        rows = [bs[0].shape[0]]
+        bb = [device.upload(pack(pair(*bs)))]
         cs = [device.alloc(m * rows[0] * 2)]
     else:
+        rows = [b.shape[0] for b in bs]
+        bb = [device.upload(pack(b)) for b in bs]
         cs = [device.alloc(m * n * 4) for n in rows]
     br = device.upload(r) if r is not None else None
     print(f"gemm {mode} m {m} k {k} rows {rows}", flush=True)
     kernels.gemm(ba, bb, cs, m, k, rows, mode, br)
     device.sync()
     if mode == "silu_mul":
-        out = [cs[0].read(np.float16, m * rows[0]).reshape(m, rows[0])]
+        out = [unpack(cs[0].read(np.float16, m * rows[0]), m, rows[0])]
     else:
         out = [c.read(np.float32, m * n).reshape(m, n) for c, n in zip(cs, rows)]
     for buf in [ba, *bb, *cs] + ([br] if br is not None else []):
@@ -49,7 +54,13 @@ def run(device, kernels, a, bs, mode="store", r=None):
     return out
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 32, 256), (256, 64, 256), (512, 128, 512), (256, 2048, 768)])
+def silu_mul(a, g, u):
+    ge = a.astype(np.float64) @ g.astype(np.float64).T
+    ue = a.astype(np.float64) @ u.astype(np.float64).T
+    return ge / (1 + np.exp(-ge)) * ue
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 64, 256), (256, 128, 256), (512, 192, 512), (256, 2048, 768)])
 def test_gemm_every_element_within_the_accumulation_bound(device, kernels, m, k, n):
     a, b = f16((m, k)), f16((n, k))
     (c,) = run(device, kernels, a, [b])
@@ -85,37 +96,46 @@ def test_gemm_residual_epilogue(device, kernels):
     assert np.all(np.abs(c - exact) <= bound(a, b) + np.abs(exact) * 2.0**-24)
 
 
-def test_gemm_silu_mul_epilogue(device, kernels):
+def test_gemm_residual_in_place(device, kernels):
+    """The residual epilogue reads and writes the same rows: R may be C."""
+    a, b = f16((256, 128)), f16((256, 128))
+    r = RNG.standard_normal((256, 256)).astype(np.float32)
+    ba, bb, br = device.upload(pack(a)), device.upload(pack(b)), device.upload(r)
+    kernels.gemm(ba, [bb], [br], 256, 128, [256], "add", br)
+    device.sync()
+    c = br.read(np.float32, 256 * 256).reshape(256, 256)
+    exact = r.astype(np.float64) + a.astype(np.float64) @ b.astype(np.float64).T
+    assert np.all(np.abs(c - exact) <= bound(a, b) + np.abs(exact) * 2.0**-24)
+    for x in (ba, bb, br):
+        x.free()
+
+
+def test_gemm_silu_mul_epilogue_writes_the_tile_layout(device, kernels):
     a = f16((256, 256), 0.5)
     g, u = f16((384, 256), 0.5), f16((384, 256), 0.5)
     (c,) = run(device, kernels, a, [g, u], "silu_mul")
-    ge = a.astype(np.float64) @ g.astype(np.float64).T
-    ue = a.astype(np.float64) @ u.astype(np.float64).T
-    exact = ge / (1 + np.exp(-ge)) * ue
+    exact = silu_mul(a, g, u)
     err = np.abs(c.astype(np.float64) - exact)
-    scale = np.max(np.abs(exact))
-    assert np.max(err) <= 2e-3 * scale
+    assert np.max(err) <= 2e-3 * np.max(np.abs(exact))
 
 
 @pytest.mark.parametrize("k,rows,mode", [(2048, [2048, 512, 512], "store"), (2048, [2048], "add"),
-                                         (2048, [8192, 8192], "silu_mul"), (8192, [2048], "add")])
+                                         (2048, [8192], "silu_mul"), (8192, [2048], "add")])
 def test_gemm_at_the_1b_prefill_shapes(device, kernels, k, rows, mode):
     """8192 rows (4 sequences of 2048); QKV, O, gate/up with SiLU·mul, down.
     Sampled rows against f64."""
     m = 8192
     a = f16((m, k), 0.5)
-    bs = [f16((n, k), 0.02) for n in rows]
+    bs = [f16((n, k), 0.02) for n in rows] if mode != "silu_mul" else [f16((rows[0], k), 0.02) for _ in range(2)]
     r = RNG.standard_normal((m, rows[0])).astype(np.float32) if mode == "add" else None
     outs = run(device, kernels, a, bs, mode, r)
     pick = np.sort(RNG.choice(m, 48, replace=False))
-    ad = a[pick].astype(np.float64)
     if mode == "silu_mul":
-        ge = ad @ bs[0].astype(np.float64).T
-        ue = ad @ bs[1].astype(np.float64).T
-        exact = ge / (1 + np.exp(-ge)) * ue
+        exact = silu_mul(a[pick], bs[0], bs[1])
         err = np.abs(outs[0][pick].astype(np.float64) - exact)
         assert np.max(err) <= 2e-3 * np.max(np.abs(exact))
         return
+    ad = a[pick].astype(np.float64)
     for b, c in zip(bs, outs):
         exact = ad @ b.astype(np.float64).T
         bnd = bound(a[pick], b)
@@ -133,10 +153,12 @@ def test_gemm_refuses_shapes_it_does_not_take(device, kernels):
     with pytest.raises(LaunchError):
         kernels.gemm(a, [b], [c], 200, 64, [256])      # m not a multiple of 256
     with pytest.raises(LaunchError):
-        kernels.gemm(a, [b], [c], 256, 48, [256])      # k not a multiple of 32
+        kernels.gemm(a, [b], [c], 256, 32, [256])      # k not a multiple of 64
     with pytest.raises(LaunchError):
         kernels.gemm(a, [b], [c], 256, 64, [300])      # rows not a multiple of 256
     with pytest.raises(LaunchError):
         kernels.gemm(a, [b], [c], 256, 64, [1024])     # B smaller than the launch reads
+    with pytest.raises(LaunchError):
+        kernels.gemm(a, [b], [c], 256, 64, [256], "silu_mul")  # the pair is 2 x 256 rows
     for x in (a, b, c):
         x.free()
