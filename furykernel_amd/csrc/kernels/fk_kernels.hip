@@ -6,3 +6,4 @@
 #include "fk_misc.h"
 #include "fk_step.h"
 #include "fk_gemm.h"
+#include "fk_prefill.h"

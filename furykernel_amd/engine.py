@@ -28,6 +28,14 @@ _STRUCTS = {
     "fk_step_argmax": K.CountParams,
     "fk_step_silu_mul": K.CountParams,
     "fk_step_token": K.StepTokenParams,
+    "fk_gemm_f16_store": K.GemmParams,
+    "fk_gemm_f16_add": K.GemmParams,
+    "fk_gemm_f16_silu_mul": K.GemmParams,
+    "fk_prefill_gather": K.PrefillGatherParams,
+    "fk_prefill_norm_pack": K.PrefillNormParams,
+    "fk_prefill_rope_store": K.PrefillRopeParams,
+    "fk_prefill_attend": K.PrefillAttendParams,
+    "fk_prefill_argmax": K.PrefillArgmaxParams,
 }
 
 

@@ -19,6 +19,8 @@ import struct
 from dataclasses import dataclass
 from pathlib import Path
 
+import numpy as np
+
 from . import runtime
 
 PACKAGE = Path(__file__).resolve().parent
@@ -84,6 +86,32 @@ class StepGemvParams(ctypes.Structure):
 class GemmParams(ctypes.Structure):
     _fields_ = [("m", ctypes.c_uint32), ("k", ctypes.c_uint32), ("n_anchors", ctypes.c_uint32),
                 ("first_col", ctypes.c_uint32 * 4), ("ldc", ctypes.c_uint32 * 3)]
+
+
+class PrefillGatherParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("width", ctypes.c_uint32), ("table_rows", ctypes.c_uint32),
+                ("table_f16", ctypes.c_uint32), ("factor", ctypes.c_float)]
+
+
+class PrefillNormParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("width", ctypes.c_uint32), ("eps", ctypes.c_float),
+                ("factor", ctypes.c_float), ("has_gamma", ctypes.c_uint32)]
+
+
+class PrefillRopeParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("rotated", ctypes.c_uint32), ("rope_rows", ctypes.c_uint32),
+                ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32), ("cache_bf16", ctypes.c_uint32)]
+
+
+class PrefillAttendParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
+                ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32), ("window", ctypes.c_uint32),
+                ("cache_bf16", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+class PrefillArgmaxParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("width", ctypes.c_uint32)]
 
 
 class StepTokenParams(ctypes.Structure):
@@ -192,6 +220,13 @@ ABIS: dict[str, KernelAbi] = {
     "fk_step_token": KernelAbi("fk_step_token", ("arg", "out", "token", "position"), StepTokenParams, 64),
     **{f"fk_gemm_f16_{mode}": KernelAbi(f"fk_gemm_f16_{mode}", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0"),
                                         GemmParams, 256) for mode in ("store", "add", "silu_mul")},
+    "fk_prefill_gather": KernelAbi("fk_prefill_gather", ("table", "tokens", "x"), PrefillGatherParams, 256),
+    "fk_prefill_norm_pack": KernelAbi("fk_prefill_norm_pack", ("x", "gamma", "y"), PrefillNormParams, 256),
+    "fk_prefill_rope_store": KernelAbi("fk_prefill_rope_store", ("q", "k", "v", "position", "slot", "rope", "qr",
+                                                                 "kc", "vc"), PrefillRopeParams),
+    "fk_prefill_attend": KernelAbi("fk_prefill_attend", ("qr", "kc", "vc", "position", "slot", "out"),
+                                   PrefillAttendParams),
+    "fk_prefill_argmax": KernelAbi("fk_prefill_argmax", ("x", "out"), PrefillArgmaxParams, 256),
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
     "fk_step_attend": KernelAbi("fk_step_attend", ("q", "knew", "vnew", "kc", "vc", "position", "slot", "rope",
@@ -312,6 +347,48 @@ class Kernels:
             bufs[f"c{j}"] = cs[j].ptr if j < len(cs) else 0
         params = GemmParams(m, k, len(bs), (ctypes.c_uint32 * 4)(*first), (ctypes.c_uint32 * 3)(*ldc))
         self.launch(entry, groups, 256, bufs, params, stream, lds_bytes=self.GEMM_LDS)
+
+    # The kernels around the prefill GEMM (fk_prefill.h).
+
+    def prefill_norm_pack(self, x: runtime.Buffer, gamma: runtime.Buffer | None, y: runtime.Buffer, rows: int,
+                          width: int, eps: float = 1e-5, factor: float = 1.0,
+                          stream: runtime.Stream | None = None) -> None:
+        """RMSNorm of f32 rows [rows, width] into f16 tiles (the GEMM's A)."""
+        entry = "fk_prefill_norm_pack"
+        if rows <= 0 or rows % 256 or width <= 0 or width % 32:
+            raise LaunchError(f"{entry}: [{rows}, {width}] does not tile (rows of 256, columns of 32)")
+        _need(x, rows * width * 4, "x", entry)
+        _need(y, rows * width * 2, "y", entry)
+        if gamma is not None:
+            _need(gamma, width * 4, "gamma", entry)
+        self.launch(entry, rows // 4, 256, {"x": x.ptr, "gamma": gamma.ptr if gamma is not None else 0, "y": y.ptr},
+                    PrefillNormParams(rows, width, eps, factor, int(gamma is not None)), stream)
+
+    def prefill_attend(self, qr: runtime.Buffer, kc: runtime.Buffer, vc: runtime.Buffer, position: runtime.Buffer,
+                       slot: runtime.Buffer, out: runtime.Buffer, rows: int, heads: int, kv_heads: int,
+                       length: int, slots: int, scale: float, window: int = 0, cache_bf16: bool = False,
+                       positions=None, seqs=None, stream: runtime.Stream | None = None) -> None:
+        """Causal attention of f16 rows q [rows, heads · 64] (RoPE'd) over the
+        caches [slots][kv_heads][length][64] into f16 tiles [rows, heads · 64].
+        Every block of 32 rows must be one sequence's consecutive positions:
+        given the host copies (positions, seqs), that is checked here."""
+        entry = "fk_prefill_attend"
+        if rows <= 0 or rows % 256 or kv_heads <= 0 or heads % kv_heads or heads // kv_heads not in (1, 2, 4):
+            raise LaunchError(f"{entry}: {rows} rows, {heads} heads over {kv_heads}")
+        if positions is not None:
+            from .prefill import check_rows
+            check_rows(positions, seqs)
+            if np.max(np.asarray(positions)) >= length:
+                raise LaunchError(f"{entry}: positions past the ring's {length}")
+        _need(qr, rows * heads * 64 * 2, "q", entry)
+        for b, what in ((kc, "K cache"), (vc, "V cache")):
+            _need(b, slots * kv_heads * length * 64 * 2, what, entry)
+        _need(position, rows * 4, "position", entry)
+        _need(slot, rows * 4, "slot", entry)
+        _need(out, rows * heads * 64 * 2, "out", entry)
+        bound = {"qr": qr.ptr, "kc": kc.ptr, "vc": vc.ptr, "position": position.ptr, "slot": slot.ptr, "out": out.ptr}
+        self.launch(entry, (rows // 32) * kv_heads, 64 * (heads // kv_heads), bound,
+                    PrefillAttendParams(rows, heads, kv_heads, length, slots, window, int(cache_bf16), scale), stream)
 
     def rmsnorm(self, x: runtime.Buffer, gamma: runtime.Buffer | None, y: runtime.Buffer, rows: int, width: int,
                 seg: int | None = None, eps: float = 1e-6, factor: float = 1.0, threads: int = 256,

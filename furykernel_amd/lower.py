@@ -70,6 +70,7 @@ class Lowered:
     buffers: dict = field(default_factory=dict)  # name -> BufferSpec
     launches: list = field(default_factory=list)
     constants: dict = field(default_factory=dict)  # name -> what fills it: ("rope", theta, d, rotated, rows)
+    layouts: dict = field(default_factory=dict)    # weight buffer -> (layout, source names) when not as given
 
     def buffer(self, name: str, dtype: str, count: int) -> str:
         spec = BufferSpec(name, dtype, count)

@@ -1,0 +1,490 @@
+"""A plan's steps, for a step of many rows (the prefill of one or more
+sequences), as launches of the prefill kernels: the tile-layout GEMM
+(fk_gemm.h) for the Linear anchors and the kernels of fk_prefill.h around it.
+
+The decode lowering (lower.py) turns each step into one launch that works on
+one row; here a step of M rows is a few launches, and values live in one of
+two layouts: f32 rows (``value:`` buffers: the residual stream, q/k/v, the
+logits) or f16 in the tile layout (``tiled:`` buffers: what feeds the matrix
+cores).  Each value is made in the layout its readers take:
+
+- a Linear step's input is its RMSNorm (recomputed in the plan) packed to
+  f16 tiles by ``fk_prefill_norm_pack``, or a value already tiled;
+- two anchors whose only reader is one SiLU·mul (gate, up) run as one paired
+  GEMM whose epilogue writes the product tiled — the down projection's input;
+- a residual add epilogue is the GEMM's add mode, into f32 rows;
+- KV stores are held until the attention of the same caches, which runs as
+  ``fk_prefill_rope_store`` (q RoPE'd to f16 rows, k RoPE'd and v into the
+  caches) then ``fk_prefill_attend`` (tiled output: the o projection's input);
+- the greedy token is ``fk_prefill_argmax`` over each row's logits.
+
+Steps of other shapes (staged KV stores, a gathered Linear input, segments
+narrower than the row) are refused with ``LoweringError``.  Pure host logic:
+the lowering a ``Backend Rocm`` does for a step of many rows
+(src/FuryKernel/Backend.hs:29-101, src/FuryKernel/Program/Plan.hs:270-300 for
+the sequence rows of a step).
+"""
+
+from __future__ import annotations
+
+from collections import defaultdict
+from typing import Optional
+
+import numpy as np
+
+from .layout import SLAB, pack, pair
+from .lower import Launch, Lowered, LoweringError, rope_table
+from .program.check import CheckedProgram
+from .program.graph import (
+    CACHE_BF16, F16, F32, SILU, U32, Add, ArgMax, Attend, Gather, GeluMul, Input, KvStore, Linear, Ring, RmsNorm,
+    Rope, ROPE_HALVES, SCache, SInput, SRowInts, SWeight, op_values)
+from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
+
+GEMM_K = 64                        # the GEMM's K granule
+GEMM_LDS = 4 * 2 * 256 * 32 * 2    # its LDS ring
+QBLOCK = 32                        # rows an attention threadgroup takes
+HEAD_DIM = 64                      # the attention kernel's head dimension
+
+
+def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int) -> Lowered:
+    """The launches of every step of the plan for a step of `rows` rows (a
+    multiple of 256: the sequences' rows one after another, each sequence's
+    run a multiple of 32 rows)."""
+    if rows <= 0 or rows % SLAB:
+        raise LoweringError(f"a step of {rows} rows; the prefill kernels take multiples of {SLAB}")
+    out = Lowered(checked.program, plan, rows)
+    _Prefill(out).run()
+    return out
+
+
+class _Prefill:
+    def __init__(self, out: Lowered):
+        self.out = out
+        self.p = out.program
+        self.rows = out.rows
+        self.producer = {v: n for n in self.p.nodes for v in n.outputs}
+        self.readers = defaultdict(list)
+        for n in self.p.nodes:
+            for v in op_values(n.op):
+                self.readers[v].append(n)
+        self.rows_of: dict = {}    # value -> its f32 rows buffer
+        self.tiled_of: dict = {}   # value -> its f16 tile-layout buffer
+        self.pending: list = []    # KvStore nodes waiting for their attention
+        for n in self.p.nodes:
+            if isinstance(n.op, Input):
+                src = self.p.source(n.op.source)
+                if not isinstance(src.kind, SInput) or src.kind.type != F32:
+                    raise LoweringError(f"input {src.name}: the prefill kernels read f32 rows")
+                self.rows_of[n.outputs[0]] = self.value_rows(n.outputs[0])
+
+    def run(self) -> None:
+        for step in self.out.plan.steps:
+            self.step(step)
+        if self.pending:
+            raise LoweringError(f"KV stores {[n.name for n in self.pending]} with no attention after them")
+        for o in self.p.outputs:
+            if o.value not in self.rows_of:
+                raise LoweringError(f"output {o.name} is never made as rows")
+
+    # Buffers -------------------------------------------------------------------
+
+    def width(self, v: int) -> int:
+        return self.p.value(v).shape.width
+
+    def value_rows(self, v: int) -> str:
+        val = self.p.value(v)
+        return self.out.buffer(f"value:{val.name}", "u32" if val.type == U32 else "f32", val.shape.width * self.rows)
+
+    def value_tiled(self, v: int) -> str:
+        val = self.p.value(v)
+        if val.shape.width % 32:
+            raise LoweringError(f"{val.name}: rows of {val.shape.width} do not tile (multiples of 32)")
+        return self.out.buffer(f"tiled:{val.name}", "f16", val.shape.width * self.rows)
+
+    def weight_source(self, s: int) -> tuple:
+        src = self.p.source(s)
+        if not isinstance(src.kind, SWeight):
+            raise LoweringError(f"{src.name} is not a weight")
+        return src, src.kind.type, tuple(src.kind.dims)
+
+    def weight_plain(self, s: int) -> tuple[str, str]:
+        src, t, dims = self.weight_source(s)
+        name = self.out.buffer(f"weight:{src.name}", t, int(np.prod(dims)))
+        self.out.layouts[name] = ("plain", (src.name,))
+        return name, t
+
+    def weight_tiled(self, s: int, unit: int = SLAB) -> tuple[str, int, int]:
+        src, t, dims = self.weight_source(s)
+        if t != F16 or len(dims) != 2 or dims[0] % unit or dims[1] % GEMM_K:
+            raise LoweringError(f"weight {src.name} {t}{list(dims)}: the GEMM takes f16 [n, k], n a multiple of "
+                                f"{unit}, k of {GEMM_K}")
+        name = self.out.buffer(f"tiled:{src.name}", "f16", dims[0] * dims[1])
+        self.out.layouts[name] = ("tiled", (src.name,))
+        return name, dims[0], dims[1]
+
+    def ints(self, s: int) -> str:
+        src = self.p.source(s)
+        if not isinstance(src.kind, SRowInts) or src.kind.count != 1:
+            raise LoweringError(f"{src.name}: the prefill kernels take one integer a row")
+        return self.out.buffer(f"ints:{src.name}", "u32", self.rows)
+
+    def cache(self, s: int) -> tuple[str, Ring, bool]:
+        src = self.p.source(s)
+        if not isinstance(src.kind, SCache) or not isinstance(src.kind.layout, Ring):
+            raise LoweringError(f"{src.name}: the prefill attention takes ring caches")
+        lay = src.kind.layout
+        bf16 = src.kind.elem == CACHE_BF16
+        count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
+        return self.out.buffer(f"cache:{src.name}", "bf16" if bf16 else "f16", count), lay, bf16
+
+    def rope(self, spec, d: int, rows: int) -> str:
+        name = f"rope:{spec.theta!r}:{d}:{spec.rotated}:{rows}"
+        self.out.buffer(name, "f32", rows * spec.rotated * 2)
+        self.out.constants[name] = ("rope", float(spec.theta), d, spec.rotated, rows)
+        return name
+
+    def launch(self, step: Step, entry: str, groups: int, threads: int, bind: dict, params: dict,
+               lds: int = 0) -> None:
+        self.out.launches.append(Launch(step.name, entry, groups, threads, bind, params, {}, lds))
+
+    # Values in their layouts -------------------------------------------------------
+
+    def rows_value(self, step: Step, v: int) -> str:
+        """v's f32 rows, gathering them the first time when v is an embedding."""
+        got = self.rows_of.get(v)
+        if got is not None:
+            return got
+        node = self.producer.get(v)
+        if node is None or not isinstance(node.op, Gather):
+            raise LoweringError(f"{step.name}: {self.p.value(v).name} is not made as rows before this step")
+        table, t, dims = self.weight_source(node.op.table)
+        tname, ttype = self.weight_plain(node.op.table)
+        if ttype not in (F16, F32) or dims[1] != self.width(v) or dims[1] % 4:
+            raise LoweringError(f"{step.name}: a gather from {table.name} {ttype}{list(dims)}")
+        buf = self.value_rows(v)
+        self.launch(step, "fk_prefill_gather", self.rows // 4, 256,
+                    {"table": tname, "tokens": self.ints(node.op.tokens), "x": buf},
+                    {"rows": self.rows, "width": dims[1], "table_rows": dims[0], "table_f16": int(ttype == F16),
+                     "factor": float(np.float32(node.op.factor))})
+        self.rows_of[v] = buf
+        return buf
+
+    def tiled_input(self, step: Step, x: int, rec: dict) -> str:
+        """The GEMM's A: x tiled, made here from x's RMSNorm when the plan
+        recomputes it."""
+        got = self.tiled_of.get(x)
+        if got is not None:
+            return got
+        node = rec.get(x)
+        if node is None or not isinstance(node.op, RmsNorm):
+            raise LoweringError(f"{step.name}: the anchors' input {self.p.value(x).name} is neither tiled nor an "
+                                f"RMSNorm this step makes")
+        op = node.op
+        width = self.width(op.x)
+        if self.p.value(op.x).shape.segment != width:
+            raise LoweringError(f"{step.name}: an RMSNorm in segments narrower than the row")
+        src = self.rows_value(step, op.x)
+        bind = {"x": src, "gamma": None, "y": self.value_tiled(x)}
+        if op.gamma is not None:
+            gname, gt = self.weight_plain(op.gamma)
+            if gt != F32:
+                raise LoweringError(f"{step.name}: a gamma of {gt}; the kernels read f32 gammas")
+            bind["gamma"] = gname
+        self.launch(step, "fk_prefill_norm_pack", self.rows // 4, 256, bind,
+                    {"rows": self.rows, "width": width, "eps": float(np.float32(op.eps)),
+                     "factor": float(np.float32(op.factor)), "has_gamma": int(op.gamma is not None)})
+        self.tiled_of[x] = bind["y"]
+        return bind["y"]
+
+    # Steps -------------------------------------------------------------------------
+
+    def step(self, step: Step) -> None:
+        kinds = {w.kind for w in step.work}
+        if STAGE in kinds or LAND in kinds:
+            raise LoweringError(f"{step.name}: staged KV stores (the ring has no room for the step's rows); the "
+                                f"prefill lowering stores in place")
+        anchors = [self.p.node(w.node) for w in step.work if w.kind == ANCHOR]
+        if anchors and all(isinstance(a.op, Linear) for a in anchors):
+            return self.linear_step(step, anchors)
+        if len(anchors) == 1 and isinstance(anchors[0].op, Attend):
+            return self.attend_step(step, anchors[0])
+        if anchors:
+            raise LoweringError(f"{step.name}: anchors of mixed or unknown kinds")
+        if EFFECT in kinds:
+            return self.store_step(step)
+        if COMBINE in kinds:
+            return self.combine_step(step)
+        return self.light_step(step)
+
+    def recomputes(self, step: Step) -> dict:
+        return {self.p.node(w.node).outputs[0]: self.p.node(w.node) for w in step.work if w.kind == RECOMPUTE}
+
+    def silu_pair(self, outs: list) -> Optional[tuple]:
+        """The SiLU·mul node two anchor outputs feed, and nothing else does:
+        (node, gate index, up index)."""
+        if len(outs) != 2:
+            return None
+        readers = {n.id: n for v in outs for n in self.readers[v]}
+        if len(readers) != 1:
+            return None
+        node = next(iter(readers.values()))
+        if not (isinstance(node.op, GeluMul) and node.op.form == SILU and {node.op.a, node.op.b} == set(outs)):
+            return None
+        if any(o.value in outs for o in self.p.outputs):
+            return None
+        return node, outs.index(node.op.a), outs.index(node.op.b)
+
+    def linear_step(self, step: Step, anchors: list) -> None:
+        if len(anchors) > 3:
+            raise LoweringError(f"{step.name}: {len(anchors)} anchors; the GEMM takes up to 3")
+        xs = {a.op.x for a in anchors}
+        if len(xs) != 1:
+            raise LoweringError(f"{step.name}: anchors of different inputs")
+        x = xs.pop()
+        rec = self.recomputes(step)
+        k = self.width(x)
+        if k % GEMM_K:
+            raise LoweringError(f"{step.name}: an input row of {k}, not a multiple of {GEMM_K}")
+        a_buf = self.tiled_input(step, x, rec)
+        outs = [a.outputs[0] for a in anchors]
+        bind = {"a": a_buf, "b0": None, "b1": None, "b2": None, "c0": None, "c1": None, "c2": None, "r0": None}
+        m = self.rows
+        epis = [self.p.node(w.node) for w in step.work if w.kind == EPILOGUE]
+
+        sp = self.silu_pair(outs)
+        if sp is not None and not epis:
+            node, gi, ui = sp
+            gsrc, gt, gdims = self.weight_source(anchors[gi].op.weight)
+            usrc, ut, udims = self.weight_source(anchors[ui].op.weight)
+            if gt != F16 or ut != F16 or gdims != udims or gdims[0] % (SLAB // 2) or gdims[1] != k:
+                raise LoweringError(f"{step.name}: gate {gsrc.name} and up {usrc.name} do not pair")
+            n = gdims[0]
+            pname = self.out.buffer(f"pair:{gsrc.name}|{usrc.name}", "f16", 2 * n * k)
+            self.out.layouts[pname] = ("pair", (gsrc.name, usrc.name))
+            act = node.outputs[0]
+            bind.update(b0=pname, c0=self.value_tiled(act))
+            self.tiled_of[act] = bind["c0"]
+            self.launch(step, "fk_gemm_f16_silu_mul", (m // SLAB) * (n // (SLAB // 2)), 256, bind,
+                        {"m": m, "k": k, "n_anchors": 1, "first_col": [0, n, n, n], "ldc": [n, 0, 0]}, GEMM_LDS)
+            return
+
+        rows, first = [], [0]
+        for j, a in enumerate(anchors):
+            wname, n, kk = self.weight_tiled(a.op.weight)
+            if kk != k or n != self.width(a.outputs[0]):
+                raise LoweringError(f"{step.name}: weight of {a.name} is [{n}, {kk}] for a row of {k}")
+            bind[f"b{j}"] = wname
+            rows.append(n)
+            first.append(first[-1] + n)
+        first += [first[-1]] * (4 - len(first))
+        params = {"m": m, "k": k, "n_anchors": len(anchors), "first_col": first, "ldc": (rows + [0, 0, 0])[:3]}
+        groups = (m // SLAB) * (sum(rows) // SLAB)
+        if epis:
+            if len(epis) != 1 or len(anchors) != 1 or not isinstance(epis[0].op, Add):
+                raise LoweringError(f"{step.name}: epilogues other than one residual add on one anchor")
+            op = epis[0].op
+            tile = outs[0]
+            if tile not in (op.a, op.b):
+                raise LoweringError(f"{step.name}: an epilogue off its anchor's tile")
+            other = op.b if op.a == tile else op.a
+            bind["r0"] = self.rows_value(step, other)
+            bind["c0"] = self.value_rows(epis[0].outputs[0])
+            self.rows_of[epis[0].outputs[0]] = bind["c0"]
+            self.launch(step, "fk_gemm_f16_add", groups, 256, bind, params, GEMM_LDS)
+            return
+        for j, v in enumerate(outs):
+            bind[f"c{j}"] = self.value_rows(v)
+            self.rows_of[v] = bind[f"c{j}"]
+        self.launch(step, "fk_gemm_f16_store", groups, 256, bind, params, GEMM_LDS)
+
+    def store_step(self, step: Step) -> None:
+        for w in step.work:
+            node = self.p.node(w.node)
+            if w.kind == EFFECT:
+                if not isinstance(node.op, KvStore):
+                    raise LoweringError(f"{step.name}: an effect other than a KV store")
+                self.pending.append(node)
+            elif w.kind != RECOMPUTE or not isinstance(node.op, Rope):
+                raise LoweringError(f"{step.name}: {w.kind} {node.name} in a store step")
+
+    def roped(self, step: Step, v: int) -> tuple[int, object]:
+        """(the value RoPE turns, its Rope op), for v made by a Rope."""
+        node = self.producer.get(v)
+        if node is None or not isinstance(node.op, Rope):
+            raise LoweringError(f"{step.name}: {self.p.value(v).name} is not RoPE'd; the prefill attention "
+                                f"takes RoPE'd queries and keys")
+        return node.op.x, node.op
+
+    def attend_step(self, step: Step, anchor) -> None:
+        op = anchor.op
+        spec = op.spec
+        if spec.reach is not None:
+            raise LoweringError(f"{step.name}: attention with a reach")
+        if spec.head_dim != HEAD_DIM or spec.heads % spec.kv_heads or spec.heads // spec.kv_heads not in (1, 2, 4):
+            raise LoweringError(f"{step.name}: {spec.heads} heads over {spec.kv_heads} of {spec.head_dim}; the "
+                                f"prefill attention takes heads of {HEAD_DIM}, 1, 2 or 4 a kv head")
+        kname, klay, kbf = self.cache(op.to.keys)
+        vname, vlay, vbf = self.cache(op.to.values)
+        if klay != vlay or kbf != vbf or klay.kv_heads != spec.kv_heads or klay.head_dim != HEAD_DIM:
+            raise LoweringError(f"{step.name}: key and value caches of different layouts")
+        stores = {}
+        for n in self.pending:
+            at = n.op.at
+            if at.cache in (op.to.keys, op.to.values):
+                if (at.positions, at.sequences) != (op.to.positions, op.to.sequences):
+                    raise LoweringError(f"{step.name}: a store at other positions than the attention reads")
+                stores[at.cache] = n
+        if set(stores) != {op.to.keys, op.to.values} or len(self.pending) != 2:
+            raise LoweringError(f"{step.name}: the attention's key and value stores are not the steps before it")
+        self.pending = []
+        k_raw, k_rope = self.roped(step, stores[op.to.keys].op.x)
+        q_raw, q_rope = self.roped(step, op.q)
+        v_raw = stores[op.to.values].op.x
+        if q_rope.spec != k_rope.spec or q_rope.positions != op.to.positions or k_rope.positions != op.to.positions:
+            raise LoweringError(f"{step.name}: q and k RoPE'd differently")
+        rs = q_rope.spec
+        if rs.axes != 1 or rs.pairs != ROPE_HALVES or 2 * rs.rotated > HEAD_DIM:
+            raise LoweringError(f"{step.name}: RoPE other than NeoX halves on one axis")
+        heads, kvh = spec.heads, spec.kv_heads
+        if self.width(q_raw) != heads * HEAD_DIM or self.width(k_raw) != kvh * HEAD_DIM or \
+                self.width(v_raw) != kvh * HEAD_DIM:
+            raise LoweringError(f"{step.name}: q, k, v rows of other widths than the heads'")
+        pos, seq = self.ints(op.to.positions), self.ints(op.to.sequences)
+        qr = self.out.buffer(f"qrot:{self.p.value(op.q).name}", "f16", heads * HEAD_DIM * self.rows)
+        self.launch(step, "fk_prefill_rope_store", self.rows, 256,
+                    {"q": self.rows_value(step, q_raw), "k": self.rows_value(step, k_raw),
+                     "v": self.rows_value(step, v_raw), "position": pos, "slot": seq,
+                     "rope": self.rope(rs, HEAD_DIM, klay.length), "qr": qr, "kc": kname, "vc": vname},
+                    {"rows": self.rows, "heads": heads, "kv_heads": kvh, "head_dim": HEAD_DIM, "rotated": rs.rotated,
+                     "rope_rows": klay.length, "length": klay.length, "slots": klay.slots, "cache_bf16": int(kbf)})
+        outv = anchor.outputs[0]
+        obuf = self.value_tiled(outv)
+        self.tiled_of[outv] = obuf
+        g = heads // kvh
+        self.launch(step, "fk_prefill_attend", (self.rows // QBLOCK) * kvh, 64 * g,
+                    {"qr": qr, "kc": kname, "vc": vname, "position": pos, "slot": seq, "out": obuf},
+                    {"rows": self.rows, "heads": heads, "kv_heads": kvh, "length": klay.length,
+                     "slots": klay.slots, "window": spec.window or 0, "cache_bf16": int(kbf),
+                     "scale": float(np.float32(spec.scale))})
+
+    def combine_step(self, step: Step) -> None:
+        # The prefill attention finishes its rows in one launch: nothing to combine.
+        for w in step.work:
+            node = self.p.node(w.node)
+            if w.kind != COMBINE or not isinstance(node.op, Attend) or node.outputs[0] not in self.tiled_of:
+                raise LoweringError(f"{step.name}: {w.kind} {node.name} in a combine step")
+
+    def light_step(self, step: Step) -> None:
+        rec = self.recomputes(step)
+        for v, node in rec.items():
+            if isinstance(node.op, ArgMax):
+                width = self.width(node.op.x)
+                self.launch(step, "fk_prefill_argmax", self.rows // 4, 256,
+                            {"x": self.rows_value(step, node.op.x), "out": self.value_rows(v)},
+                            {"rows": self.rows, "width": width})
+                self.rows_of[v] = self.value_rows(v)
+            else:
+                raise LoweringError(f"{step.name}: a light step of {type(node.op).__name__}")
+
+
+# Weights and rows ---------------------------------------------------------------------
+
+
+def weight_image(lowered: Lowered, name: str, weights: dict) -> np.ndarray:
+    """The contents of weight buffer `name` from the host weights (source
+    name -> array): as given, tiled, or the gate/up pair tiled."""
+    kind, srcs = lowered.layouts[name]
+    if kind == "plain":
+        return np.asarray(weights[srcs[0]])
+    dims = [tuple(lowered.program.source_named(s).kind.dims) for s in srcs]
+    mats = [np.asarray(weights[s], np.float16).reshape(d) for s, d in zip(srcs, dims)]
+    if kind == "tiled":
+        return pack(mats[0])
+    return pack(pair(mats[0], mats[1]))
+
+
+def check_rows(positions, slots, qblock: int = QBLOCK) -> None:
+    """The attention's contract on a step's rows: every block of `qblock`
+    rows is one sequence's (one slot) at consecutive positions."""
+    pos = np.asarray(positions, np.int64).reshape(-1)
+    sl = np.asarray(slots, np.int64).reshape(-1)
+    if pos.size != sl.size or pos.size % qblock:
+        raise LoweringError(f"{pos.size} rows: the prefill attention takes blocks of {qblock}")
+    pb, sb = pos.reshape(-1, qblock), sl.reshape(-1, qblock)
+    if np.any(sb != sb[:, :1]) or np.any(pb - pb[:, :1] != np.arange(qblock)):
+        raise LoweringError(f"rows of a block of {qblock} are not one sequence's consecutive positions")
+
+
+class PrefillSession:
+    """The prefill of `seqs` sequences of `seq_rows` rows each (positions 0 ..
+    seq_rows - 1, sequence i in ring slot i) through one decoder program:
+    gated, planned with steps of the sequence's rows, lowered to the prefill
+    kernels and resident on one GPU.  The KV caches it fills are the decode
+    step's (the same names, layout and rounding)."""
+
+    def __init__(self, device, kernels, dims, seqs: int, seq_rows: int, layers: Optional[int] = None,
+                 embed: bool = True):
+        from .engine import Engine
+        from .program.check import check_program
+        from .program.decoder import decoder_step
+        from .program.plan import PlanOptions, plan
+
+        if seqs < 1 or seqs > dims.slots:
+            raise LoweringError(f"{seqs} sequences for caches of {dims.slots} slots")
+        self.device, self.kernels, self.dims = device, kernels, dims
+        self.seqs, self.seq_rows, self.rows = seqs, seq_rows, seqs * seq_rows
+        self.embed = embed
+        self.program = decoder_step(dims, "prefill", embed, layers, position_bound=seq_rows)
+        self.checked = check_program(self.program)
+        self.plan = plan(PlanOptions(sequence_rows=seq_rows), self.checked)
+        self.lowered = lower_prefill(self.checked, self.plan, self.rows)
+        self.engine = Engine(device, kernels, self.lowered)
+        positions = np.tile(np.arange(seq_rows, dtype=np.uint32), seqs)
+        slots = np.repeat(np.arange(seqs, dtype=np.uint32), seq_rows)
+        check_rows(positions, slots)
+        self.engine.set_ints("position", positions, seq_rows)
+        self.engine.set_ints("slot", slots, dims.slots)
+
+    def weight_buffers(self):
+        return [name for name in self.lowered.layouts]
+
+    def write_weights(self, weights: dict) -> None:
+        """Host weights (source name -> array), each into its buffer's layout."""
+        for name in self.lowered.layouts:
+            self.engine.write(name, weight_image(self.lowered, name, weights))
+
+    def init_synthetic(self, seed: int = 2026, std: float = 0.02) -> None:
+        """Weights std · N(0, 1) on the device (a layout permutes them, so the
+        draw is the same in any layout), norm gains 1."""
+        for i, name in enumerate(sorted(self.lowered.layouts)):
+            kind, srcs = self.lowered.layouts[name]
+            dims = self.lowered.program.source_named(srcs[0]).kind.dims
+            if kind == "plain" and len(dims) == 1:
+                self.engine.write(name, np.ones(dims[0], np.float32))
+            else:
+                self.engine.init_normal(name, seed + 7919 * i, std)
+        self.device.sync()
+
+    def set_tokens(self, tokens) -> None:
+        self.engine.set_ints("tokens", np.asarray(tokens, np.uint32).reshape(-1), self.dims.vocab)
+
+    def set_rows(self, x: np.ndarray) -> None:
+        self.engine.write("value:x", np.asarray(x, np.float32).reshape(-1))
+
+    def run(self, stream=None) -> None:
+        self.engine.enqueue(stream)
+
+    def graph(self, stream=None):
+        return self.engine.capture(stream=stream)
+
+    def logits(self) -> np.ndarray:
+        return self.engine.read("value:logits").reshape(self.rows, -1)
+
+    def tokens(self) -> np.ndarray:
+        return self.engine.read("value:token")
+
+    def cache(self, name: str) -> np.ndarray:
+        return self.engine.read(f"cache:{name}")
+
+    def close(self) -> None:
+        self.engine.close()

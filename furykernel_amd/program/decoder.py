@@ -54,17 +54,29 @@ class DecoderDims:
 TINY = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=4, head_dim=16, ffn=256, vocab=256, context=16,
                    weight_type=F32)
 ONE_B = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000, context=4096)
+# The 1B prefill: four sequences of 2048 rows into a ring of 4096 positions.
+ONE_B_PREFILL = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000,
+                            context=4096, slots=4)
+# A small f16 decoder the prefill kernels take whole (anchors of 256 rows,
+# heads of 64, two kv heads to a group), for checking prefill against the
+# f64 evaluator.
+SMALL_PREFILL = DecoderDims(d_model=256, layers=2, heads=8, kv_heads=4, head_dim=64, ffn=512, vocab=512, context=256,
+                            slots=2)
 
 
 def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
-                 layers: Optional[int] = None) -> Program:
-    """One decode step: ``embed`` gathers the token's row of ``embed`` (else the
-    row ``x`` is an input); outputs ``logits`` and the greedy ``token``."""
+                 layers: Optional[int] = None, position_bound: Optional[int] = None) -> Program:
+    """One step of the decoder over the rows it is given (one a decode step,
+    a sequence's run of rows a prefill): ``embed`` gathers each token's row
+    of ``embed`` (else the rows ``x`` are an input); outputs ``logits`` and
+    the greedy ``token`` of every row.  Positions are declared below
+    ``position_bound`` (default: the context), which decides whether a
+    step's KV stores fit the ring in place (Plan.hs:276-281)."""
     L = dims.layers if layers is None else layers
     wt = dims.weight_type
 
     def body(b: ProgramBuilder):
-        pos = b.row_ints("position", 1, dims.context)
+        pos = b.row_ints("position", 1, dims.context if position_bound is None else position_bound)
         slot = b.row_ints("slot", 1, dims.slots)
         if embed:
             tokens = b.row_ints("tokens", 1, dims.vocab)

@@ -276,3 +276,112 @@ def evaluate(checked: CheckedProgram, b: Bindings) -> Evaluation:
             raise EvalError(f"The output {o.name} was never made.")
         outs[o.name] = env[o.value]
     return Evaluation({values[v].name: rows for v, rows in env.items()}, outs, caches)
+
+
+def evaluate_fast(checked: CheckedProgram, b: Bindings) -> Evaluation:
+    """The same evaluation with numpy's binary64 sums over all rows at once:
+    equal to ``evaluate`` but for the order of each sum's additions (the last
+    bits of binary64), so within 1e-12 of it — the evaluator for programs too
+    big for the left folds (tests pin the two together).  Supports the
+    operations the decoder programs use."""
+    p = checked.program
+    m = b.rows
+    sources = {s.id: s for s in p.sources}
+    values = {v.id: v for v in p.values}
+    env: dict = {}
+    caches = {name: {u: np.array(xs, np.float64) for u, xs in units.items()} for name, units in b.caches.items()}
+
+    def weight(s: int) -> np.ndarray:
+        src = sources[s]
+        if src.name not in b.weights:
+            raise EvalError(f"No weight {src.name}.")
+        a = np.asarray(b.weights[src.name], np.float64).ravel()
+        if a.size != int(np.prod(src.kind.dims)):
+            raise EvalError(f"{src.name} is bound to {a.size} elements.")
+        return a
+
+    def ints(s: int) -> np.ndarray:
+        src = sources[s]
+        rows = np.asarray(b.row_ints[src.name], np.int64).reshape(m, -1)
+        if np.any(rows >= src.kind.bound):
+            raise EvalError(f"{src.name}: a row holds an integer not below its bound of {src.kind.bound}.")
+        return rows
+
+    for n in p.nodes:
+        op = n.op
+        out = n.outputs[0] if n.outputs else None
+        if isinstance(op, Input):
+            env[out] = np.asarray(b.inputs[sources[op.source].name], np.float64).reshape(m, -1)
+        elif isinstance(op, Linear):
+            k = values[op.x].shape.width
+            w = weight(op.weight).reshape(-1, k)
+            env[out] = env[op.x] @ w.T
+        elif isinstance(op, RmsNorm):
+            seg = values[op.x].shape.segment
+            x = env[op.x].reshape(m, -1, seg)
+            s = (np.sum(x * x, axis=-1, keepdims=True) / seg + op.eps) ** -0.5
+            g = weight(op.gamma)[:seg] if op.gamma is not None else np.ones(seg)
+            env[out] = (x * s * g * op.factor).reshape(m, -1)
+        elif isinstance(op, Add):
+            env[out] = env[op.a] + env[op.b]
+        elif isinstance(op, GeluMul):
+            a = env[op.a]
+            if op.form == SILU:
+                ga = a / (1 + np.exp(-a))
+            else:
+                ga = 0.5 * a * (1 + np.tanh(math.sqrt(2 / math.pi) * (a + 0.044715 * a * a * a)))
+            env[out] = ga * env[op.b]
+        elif isinstance(op, Rope):
+            spec = op.spec
+            d = values[op.x].shape.segment
+            half = d // 2
+            pos = ints(op.positions)[:, 0].astype(np.float64)
+            i = np.arange(half)
+            freq = np.array([math.pow(spec.theta, -(2 * j) / d) if j < spec.rotated else 0.0 for j in i])
+            t = pos[:, None] * freq[None, :]                       # [m, half]
+            c, s_ = np.cos(t)[:, None, :], np.sin(t)[:, None, :]
+            x = env[op.x].reshape(m, -1, d)
+            lo, hi = x[..., :half], x[..., half:]
+            env[out] = np.concatenate([lo * c - hi * s_, hi * c + lo * s_], axis=-1).reshape(m, -1)
+        elif isinstance(op, KvStore):
+            src = sources[op.at.cache]
+            lay, elem = src.kind.layout, src.kind.elem
+            pos, seq = ints(op.at.positions)[:, 0], ints(op.at.sequences)[:, 0]
+            d, heads = lay.head_dim, lay.kv_heads
+            x = env[op.x].reshape(m, heads, d)
+            rounded = x.astype(np.float16).astype(np.float64) if elem != CACHE_BF16 else \
+                np.vectorize(round_bf16)(x)
+            for r in range(m):
+                unit = caches[src.name][int(seq[r])].reshape(heads, lay.length, d)
+                unit[:, int(pos[r]) % lay.length, :] = rounded[r]
+        elif isinstance(op, Attend):
+            spec = op.spec
+            lay = sources[op.to.keys].kind.layout
+            pos, seq = ints(op.to.positions)[:, 0], ints(op.to.sequences)[:, 0]
+            d, heads, kvh = spec.head_dim, spec.heads, spec.kv_heads
+            group = heads // kvh
+            q = env[op.q].reshape(m, heads, d)
+            res = np.empty((m, heads, d))
+            for r in range(m):
+                position = int(pos[r])
+                first = max(0, position - spec.window + 1) if spec.window else 0
+                ts = np.arange(first, position + 1) % lay.length
+                keys = caches[sources[op.to.keys].name][int(seq[r])].reshape(kvh, lay.length, d)[:, ts, :]
+                vals = caches[sources[op.to.values].name][int(seq[r])].reshape(kvh, lay.length, d)[:, ts, :]
+                kk = np.repeat(keys, group, axis=0)                # [heads, t, d]
+                vv = np.repeat(vals, group, axis=0)
+                scores = spec.scale * np.einsum("htd,hd->ht", kk, q[r])
+                e = np.exp(scores - scores.max(axis=1, keepdims=True))
+                res[r] = np.einsum("ht,htd->hd", e / e.sum(axis=1, keepdims=True), vv)
+            env[out] = res.reshape(m, -1)
+        elif isinstance(op, Gather):
+            width = values[out].shape.width
+            tm = weight(op.table).reshape(-1, width)
+            toks = ints(op.tokens)
+            env[out] = tm[toks].sum(axis=1) * op.factor
+        elif isinstance(op, ArgMax):
+            env[out] = np.argmax(env[op.x], axis=1).astype(np.float64)[:, None]
+        else:
+            raise EvalError(f"{n.name}: {type(op).__name__} is not evaluated here")
+    outs = {o.name: env[o.value] for o in p.outputs}
+    return Evaluation({values[v].name: rows for v, rows in env.items()}, outs, caches)

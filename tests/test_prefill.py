@@ -1,0 +1,116 @@
+"""The prefill path on the host: the vectorised f64 evaluator pinned to the
+exact one, and the lowering of a step of many rows (furykernel_amd/prefill.py)."""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+from furykernel_amd.layout import pack, pair, unpack
+from furykernel_amd.lower import LoweringError
+from furykernel_amd.prefill import check_rows, lower_prefill, weight_image
+from furykernel_amd.program.check import check_program
+from furykernel_amd.program.decoder import ONE_B_PREFILL, SMALL_PREFILL, TINY, decoder_step
+from furykernel_amd.program.plan import PlanOptions, plan
+from oracle.eval import Bindings, evaluate, evaluate_fast
+
+
+def tiny_rows_bindings(checked, rows, seed=11):
+    rng = np.random.default_rng(seed)
+    weights = {}
+    for src in checked.program.sources:
+        if type(src.kind).__name__ == "SWeight":
+            n = int(np.prod(src.kind.dims))
+            weights[src.name] = 1 + 0.1 * rng.standard_normal(n) if len(src.kind.dims) == 1 else \
+                0.1 * rng.standard_normal(n)
+    caches = {}
+    for src in checked.program.sources:
+        if type(src.kind).__name__ == "SCache":
+            lay = src.kind.layout
+            caches[src.name] = {s: np.zeros(lay.kv_heads * lay.length * lay.head_dim) for s in range(lay.slots)}
+    return Bindings(rows, inputs={"x": rng.standard_normal((rows, TINY.d_model)).tolist()}, weights=weights,
+                    row_ints={"position": [[p] for p in range(rows)], "slot": [[0]] * rows}, caches=caches)
+
+
+def test_fast_evaluator_agrees_with_the_exact_one_over_several_rows():
+    """Six rows of one sequence at positions 0..5, causal: the two evaluators
+    differ only in the order of each binary64 sum."""
+    checked = check_program(decoder_step(TINY, embed=False))
+    b = tiny_rows_bindings(checked, 6)
+    ex, fa = evaluate(checked, b), evaluate_fast(checked, b)
+    want = np.array(ex.outputs["logits"])
+    got = fa.outputs["logits"]
+    assert np.max(np.abs(got - want)) <= 1e-12 * np.max(np.abs(want))
+    for name, units in ex.caches.items():
+        assert np.max(np.abs(fa.caches[name][0] - units[0])) <= 1e-12 * max(1e-300, np.max(np.abs(units[0])))
+    assert [int(t[0]) for t in ex.outputs["token"]] == [int(t) for t in fa.outputs["token"][:, 0]]
+
+
+def small_lowered(seq_rows=128, seqs=2, **kw):
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=seq_rows, **kw))
+    return c, lower_prefill(c, plan(PlanOptions(sequence_rows=seq_rows), c), seqs * seq_rows)
+
+
+def test_prefill_lowering_of_the_small_decoder():
+    _, low = small_lowered()
+    entries = [l.entry for l in low.launches]
+    per_layer = ["fk_prefill_norm_pack", "fk_gemm_f16_store", "fk_prefill_rope_store", "fk_prefill_attend",
+                 "fk_gemm_f16_add", "fk_prefill_norm_pack", "fk_gemm_f16_silu_mul", "fk_gemm_f16_add"]
+    assert entries == ["fk_prefill_gather"] + per_layer * 2 + ["fk_prefill_norm_pack", "fk_gemm_f16_store",
+                                                               "fk_prefill_argmax"]
+    qkv = low.launches[2]
+    assert qkv.params["first_col"] == [0, 512, 768, 1024] and qkv.groups == 1 * 4
+    att = low.launches[4]
+    assert att.threads == 128 and att.groups == (256 // 32) * 4       # two heads a kv head
+    silu = low.launches[7]
+    assert silu.bind["b0"] == "pair:l0_gate_proj|l0_up_proj" and silu.bind["c0"] == "tiled:l0_act"
+    assert low.launches[8].bind["a"] == "tiled:l0_act"
+    # the o projection reads the attention's tiled output, adds the gathered rows
+    o = low.launches[5]
+    assert o.bind["a"] == "tiled:l0_attn" and o.bind["r0"] == "value:x0"
+
+
+def test_prefill_lowering_of_the_1b_decoder():
+    c = check_program(decoder_step(ONE_B_PREFILL, name="prefill", position_bound=2048))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=2048), c), 8192)
+    assert len(low.launches) == 1 + 16 * 8 + 3
+    gu = [l for l in low.launches if l.entry == "fk_gemm_f16_silu_mul"][0]
+    assert gu.groups == 32 * (8192 // 128)
+    att = [l for l in low.launches if l.entry == "fk_prefill_attend"][0]
+    assert att.threads == 256 and att.groups == 256 * 8
+    assert low.buffers["cache:l0_k_cache"].count == 4 * 8 * 4096 * 64
+
+
+def test_prefill_refuses_what_its_kernels_do_not_take():
+    with pytest.raises(LoweringError):   # positions up to the ring's length: no room, staged stores
+        c = check_program(decoder_step(SMALL_PREFILL, name="prefill"))
+        lower_prefill(c, plan(PlanOptions(sequence_rows=256), c), 256)
+    with pytest.raises(LoweringError):   # rows not a multiple of 256
+        c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128))
+        lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 128)
+    with pytest.raises(LoweringError):   # anchors narrower than a tile
+        c = check_program(decoder_step(dataclasses.replace(TINY, weight_type="f16"), name="prefill", position_bound=8))
+        lower_prefill(c, plan(PlanOptions(sequence_rows=8), c), 256)
+
+
+def test_weight_images_are_the_layouts():
+    c, low = small_lowered()
+    rng = np.random.default_rng(3)
+    g = rng.standard_normal((512, 256)).astype(np.float16)
+    u = rng.standard_normal((512, 256)).astype(np.float16)
+    q = rng.standard_normal((512, 256)).astype(np.float16)
+    img = weight_image(low, "pair:l0_gate_proj|l0_up_proj", {"l0_gate_proj": g, "l0_up_proj": u})
+    back = unpack(img, 1024, 256)
+    assert np.array_equal(back[:128], g[:128]) and np.array_equal(back[128:256], u[:128])
+    assert np.array_equal(weight_image(low, "tiled:l0_q_proj", {"l0_q_proj": q}), pack(q))
+
+
+def test_check_rows_takes_blocks_of_one_sequence():
+    pos = np.tile(np.arange(64), 2)
+    check_rows(pos, np.repeat([0, 1], 64))
+    with pytest.raises(LoweringError):   # a block's rows from two sequences
+        check_rows(pos, np.arange(128) % 2)
+    with pytest.raises(LoweringError):
+        bad = pos.copy()
+        bad[5] = 7
+        check_rows(bad, np.repeat([0, 1], 64))
