@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="queue each step's launches on the stream instead of replaying a HIP graph")
+    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+                    help="decode (the headline metric) or the 1B prefill of 4 x 2048 rows")
     ap.add_argument("--calibrate", action="store_true",
                     help="only read and write 1 GiB with the streaming kernels (the known sizes that scale the "
                          "HBM counters FETCH_SIZE and WRITE_SIZE)")
@@ -200,6 +202,163 @@ def cpu_baseline(dims, seconds: float) -> dict:
             "host_cpus": os.cpu_count()}
 
 
+MFMA_PEAK_TFLOPS = 2500.0
+PREFILL_METRIC = "prefill tokens/sec + MFMA utilization (% of 2.5 PFLOP/s f16 dense), 1 GPU"
+PREFILL_SEQS, PREFILL_ROWS = 4, 2048
+
+
+def launch_flops(low, launch) -> float:
+    """Matrix-core arithmetic of a launch: 2 m k n for a GEMM (n the gate and
+    up columns together for SiLU·mul); for the attention, the causal
+    QKᵀ and PV products its rows' positions call for (2 · 2 · 64 per
+    query head and attended position)."""
+    p = launch.params
+    if launch.entry.startswith("fk_gemm_f16_"):
+        n = 2 * p["ldc"][0] if launch.entry.endswith("silu_mul") else p["first_col"][p["n_anchors"]]
+        return 2.0 * p["m"] * p["k"] * n
+    if launch.entry == "fk_prefill_attend":
+        per_seq = PREFILL_ROWS * (PREFILL_ROWS + 1) / 2
+        return 2.0 * 2.0 * 64 * p["heads"] * per_seq * (p["rows"] / PREFILL_ROWS)
+    return 0.0
+
+
+def prefill_cpu_baseline(dims, seconds: float, rows: int = 64) -> dict:
+    """The oracle (the vectorised binary64 evaluator, numpy on the host's
+    cores) on one layer of the same decoder program and `rows` rows of one
+    sequence, with the head, repeated for about `seconds`; a token costs that
+    layer 16 times, the embedding and the head once."""
+    import numpy as np
+
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.decoder import decoder_step
+    from oracle.eval import Bindings, evaluate_fast
+
+    checked = check_program(decoder_step(dims, "prefill", True, 1, position_bound=rows))
+    rng = np.random.default_rng(5)
+    weights = {}
+    for src in checked.program.sources:
+        if type(src.kind).__name__ == "SWeight":
+            d = src.kind.dims
+            weights[src.name] = np.ones(d[0]) if len(d) == 1 else rng.standard_normal(d) * 0.02
+    caches = {}
+    for src in checked.program.sources:
+        if type(src.kind).__name__ == "SCache":
+            lay = src.kind.layout
+            caches[src.name] = {0: np.zeros(lay.kv_heads * lay.length * lay.head_dim)}
+    b = Bindings(rows, weights=weights, caches=caches,
+                 row_ints={"tokens": rng.integers(0, dims.vocab, (rows, 1)), "position": np.arange(rows)[:, None],
+                           "slot": np.zeros((rows, 1), np.int64)})
+    runs = 0
+    t0 = time.perf_counter()
+    while runs == 0 or time.perf_counter() - t0 < seconds:
+        evaluate_fast(checked, b)
+        runs += 1
+    total = time.perf_counter() - t0
+    one = total / runs
+    # the head and embedding share of the one-layer run, measured alone
+    b0 = time.perf_counter()
+    x = rng.standard_normal((rows, dims.d_model))
+    _ = x @ weights["lm_head"].T
+    head = time.perf_counter() - b0
+    per_token = ((one - head) * dims.layers + head) / rows
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(1.0 / per_token, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"the binary64 evaluator (oracle/eval.py evaluate_fast, numpy) on layer 0 of the 1B prefill "
+                      f"program for {rows} rows of one sequence with the head, {runs} runs in {total:.1f} s; the "
+                      f"layer's time counted {dims.layers} times a token"}
+
+
+def main_prefill(args) -> int:
+    import numpy as np
+
+    from furykernel_amd import kernels, runtime
+    from furykernel_amd.prefill import PrefillSession
+    from furykernel_amd.program.decoder import ONE_B_PREFILL as D
+
+    dev = runtime.Device(0)
+    ks = kernels.Kernels(dev)
+    s = PrefillSession(dev, ks, D, PREFILL_SEQS, PREFILL_ROWS)
+    rows = s.rows
+    s.init_synthetic()
+    s.set_tokens(np.random.default_rng(3).integers(0, D.vocab, rows))
+    low = s.lowered
+    log(f"prefill of {PREFILL_SEQS} x {PREFILL_ROWS} rows: {len(low.launches)} launches in one graph")
+    graph = s.graph()
+    for _ in range(args.warmup):
+        graph.replay()
+    dev.sync()
+    start, end = dev.event(), dev.event()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    end.record()
+    dev.sync()
+    elapsed = time.perf_counter() - t0
+    graph.destroy()
+    ms = elapsed * 1e3 / args.steps
+    flops = sum(launch_flops(low, l) for l in low.launches)
+    log(f"{args.steps} timed prefills: {ms:.3f} ms each, {flops / 1e12:.2f} TFLOP")
+
+    by_entry: dict = {}
+    for i, launch in enumerate(low.launches):
+        by_entry.setdefault(launch.entry, []).append(i)
+    table = {}
+    for entry, idx in by_entry.items():
+        g = s.engine.capture(only=idx)
+        g.replay()
+        dev.sync()
+        start.record()
+        for _ in range(args.kernel_reps):
+            g.replay()
+        end.record()
+        end.synchronize()
+        g.destroy()
+        avg_us = start.elapsed_ms(end) * 1e3 / (args.kernel_reps * len(idx))
+        fl = sum(launch_flops(low, low.launches[i]) for i in idx) / len(idx)
+        row = {"launches": len(idx), "avg_us": round(avg_us, 2), "us_per_prefill": round(avg_us * len(idx), 1)}
+        if fl:
+            row.update(flops_per_launch=fl, tflops=round(fl / avg_us / 1e6, 1))
+        table[entry] = row
+        log(f"{entry}: {len(idx)} launches, {avg_us:.1f} us a launch" +
+            (f", {fl / avg_us / 1e6:.1f} TFLOP/s" if fl else ""))
+    gemms = {e: r for e, r in table.items() if "tflops" in r}
+    dominant = max(gemms, key=lambda e: gemms[e]["us_per_prefill"])
+    dom = table[dominant]
+    tflops = flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": PREFILL_METRIC,
+        "value": round(rows / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: weights N(0, 0.02) (norm gains 1) generated on the device, random tokens",
+        "config": {"workload": "1B-class f16 prefill via the planner: 4 sequences x 2048 rows (positions 0..2047) "
+                               "into 4 ring slots of 4096, logits and greedy token for every row",
+                   "d_model": D.d_model, "layers": D.layers, "heads": D.heads, "kv_heads": D.kv_heads,
+                   "head_dim": D.head_dim, "ffn": D.ffn, "vocab": D.vocab, "kv_length": D.context,
+                   "rows": rows, "launches": len(low.launches), "launch": "one HIP graph per prefill"},
+        "mfma": {"flops_per_prefill": flops, "achieved_tflops": round(tflops, 1),
+                 "frac_of_peak": round(tflops / MFMA_PEAK_TFLOPS, 4), "peak_tflops": MFMA_PEAK_TFLOPS},
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": dom["tflops"], "peak": MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(dom["tflops"] / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "avg_launch_us": dom["avg_us"], "flops_per_launch": dom["flops_per_launch"],
+                     "launches_per_step": dom["launches"]},
+        "kernels": table,
+    }
+    s.close()
+    dev.close()
+    line["cpu_baseline"] = None if args.no_cpu_baseline else prefill_cpu_baseline(D, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.calibrate:
@@ -210,6 +369,8 @@ def main() -> int:
               f"The decode step is one GPU's work at its real shape; sharding it is described, not built.",
               file=sys.stderr)
         return 2
+    if args.workload == "prefill":
+        return main_prefill(args)
 
     from furykernel_amd import kernels, runtime
     from furykernel_amd.decode import DecodeSession
