@@ -25,6 +25,7 @@ ARCH = "gfx950"
 
 RUNTIME_SO = PACKAGE / "libfkrocm.so"
 KERNELS_CO = PACKAGE / "fk_kernels.hsaco"
+ATTEND_CO = PACKAGE / "fk_attend.hsaco"
 
 KERNEL_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -63,8 +64,18 @@ def build_kernels() -> Path:
     return KERNELS_CO
 
 
+def build_attend() -> Path:
+    """The prefill attention's code object: the same flags, and the matrix
+    operations in their VGPR form (fk_attend.h says why)."""
+    src = CSRC / "kernels" / "fk_attend.hip"
+    tmp = ATTEND_CO.with_suffix(".hsaco.tmp")
+    _run([HIPCC, "--genco", *KERNEL_FLAGS, "-mllvm", "-amdgpu-mfma-vgpr-form=1", str(src), "-o", str(tmp)])
+    os.replace(tmp, ATTEND_CO)
+    return ATTEND_CO
+
+
 def build_all() -> list[Path]:
-    return [build_runtime(), build_kernels()]
+    return [build_runtime(), build_kernels(), build_attend()]
 
 
 if __name__ == "__main__":

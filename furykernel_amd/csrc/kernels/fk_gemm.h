@@ -34,6 +34,7 @@
 
 #include "fk_common.h"
 #include "fk_layout.h"
+#include "fk_mfma.h"
 
 #define FK_GEMM_THREADS 256
 #define FK_GEMM_BM 256
@@ -43,9 +44,6 @@
 #define FK_GEMM_LDS (FK_GEMM_STAGES * 2 * FK_GEMM_BM * FK_GEMM_BK * 2)
 #define FK_LDS __attribute__((address_space(3)))
 
-typedef _Float16 fk_half8 __attribute__((ext_vector_type(8)));
-typedef float fk_float4v __attribute__((ext_vector_type(4)));
-typedef float fk_float16v __attribute__((ext_vector_type(16)));
 
 enum : uint32_t {
   FK_GEMM_STORE = 0,     // C = A Bᵀ (f32 rows)
@@ -60,21 +58,6 @@ struct fk_gemm_params {
   uint32_t first_col[4]; // anchor j's columns of C are [first_col[j], first_col[j + 1]), each a multiple of 256
   uint32_t ldc[3];       // row stride of anchor j's output (its columns; SiLU·mul: N, gate's rows)
 };
-
-namespace fk {
-
-union Half8 {
-  fk_half8 h;
-  uint4 u;
-};
-
-// A raw buffer over [base, base + bytes): loads past its end read zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void *base, size_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0,
-                                           (int)(uint32_t)(bytes < 0xffffffffu ? bytes : 0xffffffffu), 0x00020000);
-}
-
-}  // namespace fk
 
 // One threadgroup's tile.  MODE: the epilogue.
 template <uint32_t MODE>
@@ -270,11 +253,12 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
           for (int r = 0; r < 4; r++) {
             const float gt = acc[i][j][4 * g + r];
             const float u = acc[i][j + 2][4 * g + r];
-            // e^-g by the device library's binary32 exp (within the 4 ulp the
-            // evaluator's contract allows, src/FuryKernel/Program/Eval.hs:48):
-            // binary64's here would spill the accumulators.
-            const float e = expf(-gt);
-            h[r] = fk::narrow_f16((gt / (1.0f + e)) * u);
+            // silu(g) u = g / (1 + e^-g) · u with the hardware's exp and
+            // reciprocal (a few ulp of binary32), then rounded once to f16
+            // (2^-11): the f16 rounding bounds the error.  e^-g overflowing
+            // gives silu 0, as the limit.
+            const float e = __expf(-gt);
+            h[r] = fk::to_f16(gt * __builtin_amdgcn_rcpf(1.0f + e) * u);
           }
           uint2 w;
           w.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);

@@ -25,6 +25,7 @@ from . import runtime
 
 PACKAGE = Path(__file__).resolve().parent
 CODE_OBJECT = PACKAGE / "fk_kernels.hsaco"
+ATTEND_OBJECT = PACKAGE / "fk_attend.hsaco"   # the prefill attention, built apart (fk_attend.h)
 WAVE = 64
 
 
@@ -224,8 +225,9 @@ ABIS: dict[str, KernelAbi] = {
     "fk_prefill_norm_pack": KernelAbi("fk_prefill_norm_pack", ("x", "gamma", "y"), PrefillNormParams, 256),
     "fk_prefill_rope_store": KernelAbi("fk_prefill_rope_store", ("q", "k", "v", "position", "slot", "rope", "qr",
                                                                  "kc", "vc"), PrefillRopeParams),
-    "fk_prefill_attend": KernelAbi("fk_prefill_attend", ("qr", "kc", "vc", "position", "slot", "out"),
-                                   PrefillAttendParams),
+    **{f"fk_prefill_attend_g{g}": KernelAbi(f"fk_prefill_attend_g{g}", ("qr", "kc", "vc", "position", "slot",
+                                                                        "out"), PrefillAttendParams, 64 * g)
+       for g in (1, 2, 4)},
     "fk_prefill_argmax": KernelAbi("fk_prefill_argmax", ("x", "out"), PrefillArgmaxParams, 256),
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
@@ -252,17 +254,23 @@ def _need(buf: runtime.Buffer, nbytes: int, what: str, entry: str) -> None:
         raise LaunchError(f"{entry}: {what} is not 16-byte aligned")
 
 
+ATTEND_PREFIX = "fk_prefill_attend"
+
+
 class Kernels:
     """The code object loaded on a device, and a launcher per kernel family."""
 
-    def __init__(self, device: runtime.Device, path: Path = CODE_OBJECT):
-        if not Path(path).exists():
-            raise runtime.NativeMissing(f"{path} is not built; run __graft_entry__.build()")
+    def __init__(self, device: runtime.Device, path: Path = CODE_OBJECT, attend_path: Path = ATTEND_OBJECT):
+        for p in (path, attend_path):
+            if not Path(p).exists():
+                raise runtime.NativeMissing(f"{p} is not built; run __graft_entry__.build()")
         self.device = device
         self.module = device.load_module(path)
+        self.attend_module = device.load_module(attend_path)
 
     def fn(self, entry: str) -> runtime.Function:
-        return self.module.function(entry)
+        module = self.attend_module if entry.startswith(ATTEND_PREFIX) else self.module
+        return module.function(entry)
 
     def launch(self, entry: str, groups: int, threads: int, bound: dict[str, int], params: ctypes.Structure,
                stream: runtime.Stream | None = None, lds_bytes: int = 0) -> None:
@@ -372,9 +380,11 @@ class Kernels:
         caches [slots][kv_heads][length][64] into f16 tiles [rows, heads · 64].
         Every block of 32 rows must be one sequence's consecutive positions:
         given the host copies (positions, seqs), that is checked here."""
-        entry = "fk_prefill_attend"
+        entry = f"fk_prefill_attend_g{heads // kv_heads if kv_heads and heads % kv_heads == 0 else 0}"
         if rows <= 0 or rows % 256 or kv_heads <= 0 or heads % kv_heads or heads // kv_heads not in (1, 2, 4):
             raise LaunchError(f"{entry}: {rows} rows, {heads} heads over {kv_heads}")
+        if length <= 0 or length % 32:
+            raise LaunchError(f"{entry}: a ring of {length}; keys go by blocks of 32 that must not wrap")
         if positions is not None:
             from .prefill import check_rows
             check_rows(positions, seqs)

@@ -327,6 +327,9 @@ class _Prefill:
         vname, vlay, vbf = self.cache(op.to.values)
         if klay != vlay or kbf != vbf or klay.kv_heads != spec.kv_heads or klay.head_dim != HEAD_DIM:
             raise LoweringError(f"{step.name}: key and value caches of different layouts")
+        if klay.length % QBLOCK:
+            raise LoweringError(f"{step.name}: a ring of {klay.length}; the prefill attention reads keys by "
+                                f"blocks of {QBLOCK} that must not wrap")
         stores = {}
         for n in self.pending:
             at = n.op.at
@@ -361,7 +364,7 @@ class _Prefill:
         obuf = self.value_tiled(outv)
         self.tiled_of[outv] = obuf
         g = heads // kvh
-        self.launch(step, "fk_prefill_attend", (self.rows // QBLOCK) * kvh, 64 * g,
+        self.launch(step, f"fk_prefill_attend_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
                     {"qr": qr, "kc": kname, "vc": vname, "position": pos, "slot": seq, "out": obuf},
                     {"rows": self.rows, "heads": heads, "kv_heads": kvh, "length": klay.length,
                      "slots": klay.slots, "window": spec.window or 0, "cache_bf16": int(kbf),

@@ -35,8 +35,10 @@ def test_code_object_holds_every_kernel_entry():
     from furykernel_amd import kernels
 
     blob = kernels.CODE_OBJECT.read_bytes()
+    attend = kernels.ATTEND_OBJECT.read_bytes()
     for entry in kernels.ABIS:
-        assert entry.encode() + b"\0" in blob, entry
+        where = attend if entry.startswith(kernels.ATTEND_PREFIX) else blob
+        assert entry.encode() + b"\0" in where, entry
 
 
 def test_kernarg_is_pointers_then_c_layout_params():

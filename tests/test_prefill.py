@@ -54,14 +54,14 @@ def small_lowered(seq_rows=128, seqs=2, **kw):
 def test_prefill_lowering_of_the_small_decoder():
     _, low = small_lowered()
     entries = [l.entry for l in low.launches]
-    per_layer = ["fk_prefill_norm_pack", "fk_gemm_f16_store", "fk_prefill_rope_store", "fk_prefill_attend",
+    per_layer = ["fk_prefill_norm_pack", "fk_gemm_f16_store", "fk_prefill_rope_store", "fk_prefill_attend_g2",
                  "fk_gemm_f16_add", "fk_prefill_norm_pack", "fk_gemm_f16_silu_mul", "fk_gemm_f16_add"]
     assert entries == ["fk_prefill_gather"] + per_layer * 2 + ["fk_prefill_norm_pack", "fk_gemm_f16_store",
                                                                "fk_prefill_argmax"]
     qkv = low.launches[2]
     assert qkv.params["first_col"] == [0, 512, 768, 1024] and qkv.groups == 1 * 4
     att = low.launches[4]
-    assert att.threads == 128 and att.groups == (256 // 32) * 4       # two heads a kv head
+    assert att.entry == "fk_prefill_attend_g2" and att.threads == 128 and att.groups == (256 // 32) * 4
     silu = low.launches[7]
     assert silu.bind["b0"] == "pair:l0_gate_proj|l0_up_proj" and silu.bind["c0"] == "tiled:l0_act"
     assert low.launches[8].bind["a"] == "tiled:l0_act"
@@ -76,8 +76,8 @@ def test_prefill_lowering_of_the_1b_decoder():
     assert len(low.launches) == 1 + 16 * 8 + 3
     gu = [l for l in low.launches if l.entry == "fk_gemm_f16_silu_mul"][0]
     assert gu.groups == 32 * (8192 // 128)
-    att = [l for l in low.launches if l.entry == "fk_prefill_attend"][0]
-    assert att.threads == 256 and att.groups == 256 * 8
+    att = [l for l in low.launches if l.entry.startswith("fk_prefill_attend")][0]
+    assert att.entry == "fk_prefill_attend_g4" and att.threads == 256 and att.groups == 256 * 8
     assert low.buffers["cache:l0_k_cache"].count == 4 * 8 * 4096 * 64
 
 
@@ -108,6 +108,8 @@ def test_weight_images_are_the_layouts():
 def test_check_rows_takes_blocks_of_one_sequence():
     pos = np.tile(np.arange(64), 2)
     check_rows(pos, np.repeat([0, 1], 64))
+    with pytest.raises(LoweringError):   # sequences of 16 rows: a block of 32 spans two
+        check_rows(np.tile(np.arange(16), 8), np.repeat(np.arange(8), 16))
     with pytest.raises(LoweringError):   # a block's rows from two sequences
         check_rows(pos, np.arange(128) % 2)
     with pytest.raises(LoweringError):
