@@ -216,7 +216,7 @@ def launch_flops(low, launch) -> float:
     if launch.entry.startswith("fk_gemm_f16_"):
         n = 2 * p["ldc"][0] if launch.entry.endswith("silu_mul") else p["first_col"][p["n_anchors"]]
         return 2.0 * p["m"] * p["k"] * n
-    if launch.entry == "fk_prefill_attend":
+    if launch.entry.startswith("fk_prefill_attend"):
         per_seq = PREFILL_ROWS * (PREFILL_ROWS + 1) / 2
         return 2.0 * 2.0 * 64 * p["heads"] * per_seq * (p["rows"] / PREFILL_ROWS)
     return 0.0

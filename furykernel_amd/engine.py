@@ -34,7 +34,9 @@ _STRUCTS = {
     "fk_prefill_gather": K.PrefillGatherParams,
     "fk_prefill_norm_pack": K.PrefillNormParams,
     "fk_prefill_rope_store": K.PrefillRopeParams,
-    "fk_prefill_attend": K.PrefillAttendParams,
+    "fk_prefill_attend_g1": K.PrefillAttendParams,
+    "fk_prefill_attend_g2": K.PrefillAttendParams,
+    "fk_prefill_attend_g4": K.PrefillAttendParams,
     "fk_prefill_argmax": K.PrefillArgmaxParams,
 }
 
