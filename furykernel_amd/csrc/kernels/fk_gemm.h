@@ -49,6 +49,8 @@ enum : uint32_t {
   FK_GEMM_STORE = 0,     // C = A Bᵀ (f32 rows)
   FK_GEMM_ADD = 1,       // C = R + A Bᵀ (f32 rows), R [M, ldc]; R may be C
   FK_GEMM_SILU_MUL = 2,  // C = f16(silu(A Gᵀ) · (A Uᵀ)) in the tile layout; B0 the paired gate/up weights
+  FK_GEMM_QKV_ROPE = 3,  // anchors q, k, v: q RoPE'd into f16 rows (C0), k RoPE'd into the K cache (C1), v
+                         // into the V cache (C2), at each row's slot and position
 };
 
 struct fk_gemm_params {
@@ -59,12 +61,30 @@ struct fk_gemm_params {
   uint32_t ldc[3];       // row stride of anchor j's output (its columns; SiLU·mul: N, gate's rows)
 };
 
+// The QKV epilogue's RoPE and caches (heads of 64, every pair turned).
+struct fk_gemm_rope_params {
+  uint32_t kv_heads;
+  uint32_t rope_rows;    // positions the RoPE table holds
+  uint32_t length;       // ring length
+  uint32_t slots;
+  uint32_t cache_bf16;
+};
+
+struct fk_gemm_qkv_params {
+  fk_gemm_params g;
+  fk_gemm_rope_params r;
+};
+
 // One threadgroup's tile.  MODE: the epilogue.
 template <uint32_t MODE>
 __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const _Float16 *__restrict__ b0,
                                           const _Float16 *__restrict__ b1, const _Float16 *__restrict__ b2,
                                           void *__restrict__ c0, void *__restrict__ c1, void *__restrict__ c2,
-                                          const float *r0, const fk_gemm_params &p) {
+                                          const float *r0, const fk_gemm_params &p,
+                                          const uint32_t *__restrict__ position = nullptr,
+                                          const uint32_t *__restrict__ slot = nullptr,
+                                          const float *__restrict__ rope = nullptr,
+                                          const fk_gemm_rope_params &rp = fk_gemm_rope_params{}) {
   extern __shared__ uint4 gemm_lds[];
   constexpr uint32_t ROW16 = FK_GEMM_BK * 2 / 16;           // 16-byte units a staged row takes
   constexpr uint32_t TILEB = FK_GEMM_BM * FK_GEMM_BK * 2;    // bytes of one operand's staged tile
@@ -266,6 +286,64 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
           // Four consecutive columns of one row: half of one 16-byte unit.
           *reinterpret_cast<uint2 *>(out + fk::tile_offset(m + 32 * i, n, ncols)) = w;
         }
+  } else if (MODE == FK_GEMM_QKV_ROPE) {
+    // A 256-column tile is 4 whole heads; a lane's blocks 2 jp and 2 jp + 1
+    // are the low and high halves of one head, so it holds both elements of
+    // each pair RoPE turns (NeoX halves, as rope_elem: x_j c - x_{j+32} s below
+    // the half, x_j c + x_{j-32} s above, the table's cos and sin of the row's
+    // position).  q goes to f16 rows (the attention's), k and v to the caches
+    // rounded as the decode step's stores round.
+    const bool bf16 = rp.cache_bf16 != 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t row = m + 32 * i;
+      const uint32_t pos = position[row];
+      const uint32_t sl = min(slot[row], rp.slots - 1);
+      const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
+#pragma unroll
+      for (int jp = 0; jp < 2; jp++) {
+        const uint32_t head = (n0 + wn * 128 + 64 * jp) / 64;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const uint32_t d = 8 * g + nq;  // the low half's first of four columns; their partners d + 32 ..
+          float lo[4], hi[4];
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            lo[r] = acc[i][2 * jp][4 * g + r];
+            hi[r] = acc[i][2 * jp + 1][4 * g + r];
+          }
+          if (anchor != 2) {
+            const float4 t01 = *reinterpret_cast<const float4 *>(cs + 2 * d);      // (cos, sin) of pairs d, d + 1
+            const float4 t23 = *reinterpret_cast<const float4 *>(cs + 2 * d + 4);  // pairs d + 2, d + 3
+            const float cc[4] = {t01.x, t01.z, t23.x, t23.z};
+            const float sn[4] = {t01.y, t01.w, t23.y, t23.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const float x = lo[r] * cc[r] - hi[r] * sn[r];
+              const float y = hi[r] * cc[r] + lo[r] * sn[r];
+              lo[r] = x;
+              hi[r] = y;
+            }
+          }
+          if (anchor == 0) {
+            uint16_t *q = reinterpret_cast<uint16_t *>(c0) + (size_t)row * p.ldc[0] + head * 64 + d;
+            *reinterpret_cast<uint2 *>(q) = make_uint2(fk::to_f16(lo[0]) | ((uint32_t)fk::to_f16(lo[1]) << 16),
+                                                       fk::to_f16(lo[2]) | ((uint32_t)fk::to_f16(lo[3]) << 16));
+            *reinterpret_cast<uint2 *>(q + 32) = make_uint2(fk::to_f16(hi[0]) | ((uint32_t)fk::to_f16(hi[1]) << 16),
+                                                            fk::to_f16(hi[2]) | ((uint32_t)fk::to_f16(hi[3]) << 16));
+          } else {
+            uint16_t *c = reinterpret_cast<uint16_t *>(anchor == 1 ? c1 : c2) +
+                          (((size_t)sl * rp.kv_heads + head) * rp.length + pos % rp.length) * 64 + d;
+            *reinterpret_cast<uint2 *>(c) =
+                make_uint2(fk::narrow_cache(lo[0], bf16) | ((uint32_t)fk::narrow_cache(lo[1], bf16) << 16),
+                           fk::narrow_cache(lo[2], bf16) | ((uint32_t)fk::narrow_cache(lo[3], bf16) << 16));
+            *reinterpret_cast<uint2 *>(c + 32) =
+                make_uint2(fk::narrow_cache(hi[0], bf16) | ((uint32_t)fk::narrow_cache(hi[1], bf16) << 16),
+                           fk::narrow_cache(hi[2], bf16) | ((uint32_t)fk::narrow_cache(hi[3], bf16) << 16));
+          }
+        }
+      }
+    }
   } else {
     float *out = reinterpret_cast<float *>(anchor == 0 ? c0 : (anchor == 1 ? c1 : c2));
     const uint32_t ld = anchor == 0 ? p.ldc[0] : (anchor == 1 ? p.ldc[1] : p.ldc[2]);
@@ -296,3 +374,16 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
 FK_GEMM_ENTRY(fk_gemm_f16_store, FK_GEMM_STORE)
 FK_GEMM_ENTRY(fk_gemm_f16_add, FK_GEMM_ADD)
 FK_GEMM_ENTRY(fk_gemm_f16_silu_mul, FK_GEMM_SILU_MUL)
+
+// The QKV projection with RoPE and the KV store in its epilogue: anchors q,
+// k, v (in that order), C0 the f16 q rows, C1 and C2 the K and V caches
+// ([slots][kv_heads][length][64]), then each row's position and slot and the
+// RoPE table ([position][32 pairs][cos, sin]).
+extern "C" __global__ void __launch_bounds__(FK_GEMM_THREADS)
+    fk_gemm_f16_qkv_rope(const _Float16 *__restrict__ a, const _Float16 *__restrict__ b0,
+                         const _Float16 *__restrict__ b1, const _Float16 *__restrict__ b2, void *__restrict__ c0,
+                         void *__restrict__ c1, void *__restrict__ c2, const float *r0,
+                         const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot,
+                         const float *__restrict__ rope, fk_gemm_qkv_params p) {
+  gemm_tile<FK_GEMM_QKV_ROPE>(a, b0, b1, b2, c0, c1, c2, r0, p.g, position, slot, rope, p.r);
+}

@@ -20,7 +20,6 @@
 #include "fk_common.h"
 #include "fk_layout.h"
 #include "fk_mfma.h"
-#include "fk_step.h"  // rope_elem, narrow_cache: the decode step's RoPE and cache rounding
 
 // x[r] = table[tokens[r]] · factor.  One wave a row, 4 columns a lane at a
 // time; rows × width f32 out.  A token past the table reads its last row
@@ -105,6 +104,60 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_norm_pack(const flo
     *reinterpret_cast<uint4 *>(y + fk::tile_offset(row, 8 * u, p.width)) = make_uint4(h[0], h[1], h[2], h[3]);
   }
 }
+
+// The same in one pass for rows of exactly 512 U columns: a lane holds its
+// U units of 8 in registers between the sum and the output, so each row is
+// read from HBM once.
+template <int U>
+__device__ __forceinline__ void norm_pack_held(const float *__restrict__ x, const float *__restrict__ gamma,
+                                               uint16_t *__restrict__ y, const fk_prefill_norm_params &p) {
+  const uint32_t row = blockIdx.x * 4 + threadIdx.x / FK_WAVE;
+  if (row >= p.rows) return;
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+  constexpr uint32_t width = 512 * U;
+  const float *xr = x + (size_t)row * width;
+  float4 a[U], b[U];
+#pragma unroll
+  for (int t = 0; t < U; t++) {
+    a[t] = *reinterpret_cast<const float4 *>(xr + 8 * (lane + 64 * t));
+    b[t] = *reinterpret_cast<const float4 *>(xr + 8 * (lane + 64 * t) + 4);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int t = 0; t < U; t++)
+    ss += ((a[t].x * a[t].x + a[t].y * a[t].y) + (a[t].z * a[t].z + a[t].w * a[t].w)) +
+          ((b[t].x * b[t].x + b[t].y * b[t].y) + (b[t].z * b[t].z + b[t].w * b[t].w));
+  ss = fk::wave_sum(ss);
+  const float s = fk::rsqrt_once(ss / (float)width + p.eps);
+#pragma unroll
+  for (int t = 0; t < U; t++) {
+    const uint32_t u = lane + 64 * t;
+    float g[8] = {1, 1, 1, 1, 1, 1, 1, 1};
+    if (p.has_gamma) {
+      const float4 ga = *reinterpret_cast<const float4 *>(gamma + 8 * u);
+      const float4 gb = *reinterpret_cast<const float4 *>(gamma + 8 * u + 4);
+      g[0] = ga.x; g[1] = ga.y; g[2] = ga.z; g[3] = ga.w; g[4] = gb.x; g[5] = gb.y; g[6] = gb.z; g[7] = gb.w;
+    }
+    const float v[8] = {a[t].x, a[t].y, a[t].z, a[t].w, b[t].x, b[t].y, b[t].z, b[t].w};
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      h[e] = fk::to_f16(v[2 * e] * s * g[2 * e] * p.factor) |
+             ((uint32_t)fk::to_f16(v[2 * e + 1] * s * g[2 * e + 1] * p.factor) << 16);
+    *reinterpret_cast<uint4 *>(y + fk::tile_offset(row, 8 * u, width)) = make_uint4(h[0], h[1], h[2], h[3]);
+  }
+}
+
+#define FK_NORM_PACK_HELD(W, U)                                                                                 \
+  extern "C" __global__ void __launch_bounds__(256) fk_prefill_norm_pack_w##W(                                  \
+      const float *__restrict__ x, const float *__restrict__ gamma, uint16_t *__restrict__ y,                   \
+      fk_prefill_norm_params p) {                                                                               \
+    norm_pack_held<U>(x, gamma, y, p);                                                                          \
+  }
+FK_NORM_PACK_HELD(512, 1)
+FK_NORM_PACK_HELD(1024, 2)
+FK_NORM_PACK_HELD(2048, 4)
+FK_NORM_PACK_HELD(4096, 8)
 
 // q RoPE'd into f16 rows [rows, heads · d]; k RoPE'd and v into the caches
 // ([slots][kv_heads][length][d], f16 or bf16) at (slot, head, position mod

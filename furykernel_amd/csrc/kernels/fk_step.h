@@ -26,30 +26,6 @@
 
 // KV stores ----------------------------------------------------------------
 
-namespace fk {
-
-// Element j of a head of width d turned by RoPE (NeoX halves, Graph.hs:209-221),
-// pair i's cosine and sine from `cs` (the position's row of the RoPE table:
-// cos, sin of the binary32 angle position * theta^(-2i/d), each binary64's
-// rounded once): (x_j c - x_{j+d/2} s) below the half, (x_j c + x_{j-d/2} s)
-// above; pairs past `rotated` stay.
-__device__ __forceinline__ float rope_elem(const float *head, uint32_t j, uint32_t d, uint32_t rotated,
-                                           const float *__restrict__ cs) {
-  const uint32_t half = d / 2;
-  const uint32_t i = j < half ? j : j - half;
-  if (i >= rotated) return head[j];
-  const float c = cs[2 * i];
-  const float s = cs[2 * i + 1];
-  return j < half ? head[j] * c - head[j + half] * s : head[j] * c + head[j - half] * s;
-}
-
-__device__ __forceinline__ uint16_t narrow_cache(float v, bool bf16) { return bf16 ? narrow_bf16(v) : narrow_f16(v); }
-
-__device__ __forceinline__ float widen_cache(uint16_t h, bool bf16) {
-  return bf16 ? __uint_as_float((uint32_t)h << 16) : widen_f16(h);
-}
-
-}  // namespace fk
 
 struct fk_step_store_params {
   uint32_t n_stores;    // 1 or 2

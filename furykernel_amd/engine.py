@@ -31,8 +31,10 @@ _STRUCTS = {
     "fk_gemm_f16_store": K.GemmParams,
     "fk_gemm_f16_add": K.GemmParams,
     "fk_gemm_f16_silu_mul": K.GemmParams,
+    "fk_gemm_f16_qkv_rope": K.GemmQkvParams,
     "fk_prefill_gather": K.PrefillGatherParams,
     "fk_prefill_norm_pack": K.PrefillNormParams,
+    **{f"fk_prefill_norm_pack_w{w}": K.PrefillNormParams for w in K.NORM_PACK_HELD},
     "fk_prefill_rope_store": K.PrefillRopeParams,
     "fk_prefill_attend_g1": K.PrefillAttendParams,
     "fk_prefill_attend_g2": K.PrefillAttendParams,

@@ -89,6 +89,13 @@ class GemmParams(ctypes.Structure):
                 ("first_col", ctypes.c_uint32 * 4), ("ldc", ctypes.c_uint32 * 3)]
 
 
+class GemmQkvParams(ctypes.Structure):
+    """fk_gemm_qkv_params: the GEMM's parameters, then the RoPE and caches'."""
+    _fields_ = GemmParams._fields_ + [("kv_heads", ctypes.c_uint32), ("rope_rows", ctypes.c_uint32),
+                                      ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32),
+                                      ("cache_bf16", ctypes.c_uint32)]
+
+
 class PrefillGatherParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("width", ctypes.c_uint32), ("table_rows", ctypes.c_uint32),
                 ("table_f16", ctypes.c_uint32), ("factor", ctypes.c_float)]
@@ -212,6 +219,9 @@ STEP_GEMV_ENTRIES = tuple(f"{shape}_p{pro}_e{epi}" for shape, pairs in STEP_GEMV
 STEP_GEMV_BUFFERS = ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
                      "res_token", "epi_out", "arg")
 
+# Row widths the one-pass RMSNorm-to-tiles holds in registers (fk_prefill.h).
+NORM_PACK_HELD = (512, 1024, 2048, 4096)
+
 ABIS: dict[str, KernelAbi] = {
     **_gemv_abis(),
     "fk_rmsnorm_f32": KernelAbi("fk_rmsnorm_f32", ("x", "gamma", "y"), RmsNormParams),
@@ -221,8 +231,12 @@ ABIS: dict[str, KernelAbi] = {
     "fk_step_token": KernelAbi("fk_step_token", ("arg", "out", "token", "position"), StepTokenParams, 64),
     **{f"fk_gemm_f16_{mode}": KernelAbi(f"fk_gemm_f16_{mode}", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0"),
                                         GemmParams, 256) for mode in ("store", "add", "silu_mul")},
+    "fk_gemm_f16_qkv_rope": KernelAbi("fk_gemm_f16_qkv_rope", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0",
+                                                               "position", "slot", "rope"), GemmQkvParams, 256),
     "fk_prefill_gather": KernelAbi("fk_prefill_gather", ("table", "tokens", "x"), PrefillGatherParams, 256),
     "fk_prefill_norm_pack": KernelAbi("fk_prefill_norm_pack", ("x", "gamma", "y"), PrefillNormParams, 256),
+    **{f"fk_prefill_norm_pack_w{w}": KernelAbi(f"fk_prefill_norm_pack_w{w}", ("x", "gamma", "y"), PrefillNormParams,
+                                               256) for w in NORM_PACK_HELD},
     "fk_prefill_rope_store": KernelAbi("fk_prefill_rope_store", ("q", "k", "v", "position", "slot", "rope", "qr",
                                                                  "kc", "vc"), PrefillRopeParams),
     **{f"fk_prefill_attend_g{g}": KernelAbi(f"fk_prefill_attend_g{g}", ("qr", "kc", "vc", "position", "slot",
@@ -362,7 +376,7 @@ class Kernels:
                           width: int, eps: float = 1e-5, factor: float = 1.0,
                           stream: runtime.Stream | None = None) -> None:
         """RMSNorm of f32 rows [rows, width] into f16 tiles (the GEMM's A)."""
-        entry = "fk_prefill_norm_pack"
+        entry = f"fk_prefill_norm_pack_w{width}" if width in NORM_PACK_HELD else "fk_prefill_norm_pack"
         if rows <= 0 or rows % 256 or width <= 0 or width % 32:
             raise LaunchError(f"{entry}: [{rows}, {width}] does not tile (rows of 256, columns of 32)")
         _need(x, rows * width * 4, "x", entry)

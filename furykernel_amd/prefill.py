@@ -16,6 +16,9 @@ cores).  Each value is made in the layout its readers take:
 - KV stores are held until the attention of the same caches, which runs as
   ``fk_prefill_rope_store`` (q RoPE'd to f16 rows, k RoPE'd and v into the
   caches) then ``fk_prefill_attend`` (tiled output: the o projection's input);
+  when the three came from one GEMM and every pair of the heads turns, the
+  GEMM's epilogue does the RoPE and the stores (``fk_gemm_f16_qkv_rope``) and
+  q, k, v are never f32 rows in HBM;
 - the greedy token is ``fk_prefill_argmax`` over each row's logits.
 
 Steps of other shapes (staged KV stores, a gathered Linear input, segments
@@ -32,6 +35,7 @@ from typing import Optional
 
 import numpy as np
 
+from .kernels import NORM_PACK_HELD
 from .layout import SLAB, pack, pair
 from .lower import Launch, Lowered, LoweringError, rope_table
 from .program.check import CheckedProgram
@@ -54,7 +58,49 @@ def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int) -> Lowered:
         raise LoweringError(f"a step of {rows} rows; the prefill kernels take multiples of {SLAB}")
     out = Lowered(checked.program, plan, rows)
     _Prefill(out).run()
+    _fuse_qkv_rope(out)
     return out
+
+
+def _fuse_qkv_rope(out: Lowered) -> None:
+    """Folds each ``fk_prefill_rope_store`` into the GEMM that made its q, k
+    and v (its three anchors, in that order) when the RoPE turns every pair
+    of the heads of 64: the GEMM's epilogue then RoPEs q into the attention's
+    f16 rows and k into the K cache and stores v, with the same arithmetic,
+    and the f32 rows of q, k, v go.  Nothing between the GEMM and the RoPE
+    launch may touch what either writes or reads."""
+    launches = out.launches
+    i = 0
+    while i < len(launches):
+        rs = launches[i]
+        if rs.entry != "fk_prefill_rope_store" or rs.params["rotated"] != HEAD_DIM // 2 or \
+                rs.params["head_dim"] != HEAD_DIM:
+            i += 1
+            continue
+        qkv = (rs.bind["q"], rs.bind["k"], rs.bind["v"])
+        j = next((j for j in range(i - 1, -1, -1) if set(qkv) & set(launches[j].bind.values())), None)
+        gm = launches[j] if j is not None else None
+        if gm is None or gm.entry != "fk_gemm_f16_store" or gm.params["n_anchors"] != 3 or \
+                (gm.bind["c0"], gm.bind["c1"], gm.bind["c2"]) != qkv:
+            i += 1
+            continue
+        touched = set(qkv) | {rs.bind[b] for b in ("qr", "kc", "vc")}
+        between = any(touched & set(launches[t].bind.values()) for t in range(j + 1, i))
+        elsewhere = any(set(qkv) & set(l.bind.values()) for t, l in enumerate(launches) if t not in (i, j))
+        if between or elsewhere or any(f"value:{out.program.value(o.value).name}" in qkv
+                                       for o in out.program.outputs):
+            i += 1
+            continue
+        p = rs.params
+        bind = dict(gm.bind, c0=rs.bind["qr"], c1=rs.bind["kc"], c2=rs.bind["vc"], position=rs.bind["position"],
+                    slot=rs.bind["slot"], rope=rs.bind["rope"])
+        params = dict(gm.params, kv_heads=p["kv_heads"], rope_rows=p["rope_rows"], length=p["length"],
+                      slots=p["slots"], cache_bf16=p["cache_bf16"])
+        launches[j] = Launch(gm.step, "fk_gemm_f16_qkv_rope", gm.groups, gm.threads, bind, params, {},
+                             gm.lds_bytes)
+        del launches[i]
+        for name in qkv:
+            del out.buffers[name]
 
 
 class _Prefill:
@@ -190,7 +236,8 @@ class _Prefill:
             if gt != F32:
                 raise LoweringError(f"{step.name}: a gamma of {gt}; the kernels read f32 gammas")
             bind["gamma"] = gname
-        self.launch(step, "fk_prefill_norm_pack", self.rows // 4, 256, bind,
+        entry = f"fk_prefill_norm_pack_w{width}" if width in NORM_PACK_HELD else "fk_prefill_norm_pack"
+        self.launch(step, entry, self.rows // 4, 256, bind,
                     {"rows": self.rows, "width": width, "eps": float(np.float32(op.eps)),
                      "factor": float(np.float32(op.factor)), "has_gamma": int(op.gamma is not None)})
         self.tiled_of[x] = bind["y"]
@@ -426,7 +473,7 @@ class PrefillSession:
     step's (the same names, layout and rounding)."""
 
     def __init__(self, device, kernels, dims, seqs: int, seq_rows: int, layers: Optional[int] = None,
-                 embed: bool = True):
+                 embed: bool = True, rope_rotated: Optional[int] = None):
         from .engine import Engine
         from .program.check import check_program
         from .program.decoder import decoder_step
@@ -437,7 +484,8 @@ class PrefillSession:
         self.device, self.kernels, self.dims = device, kernels, dims
         self.seqs, self.seq_rows, self.rows = seqs, seq_rows, seqs * seq_rows
         self.embed = embed
-        self.program = decoder_step(dims, "prefill", embed, layers, position_bound=seq_rows)
+        self.program = decoder_step(dims, "prefill", embed, layers, position_bound=seq_rows,
+                                    rope_rotated=rope_rotated)
         self.checked = check_program(self.program)
         self.plan = plan(PlanOptions(sequence_rows=seq_rows), self.checked)
         self.lowered = lower_prefill(self.checked, self.plan, self.rows)

@@ -65,13 +65,15 @@ SMALL_PREFILL = DecoderDims(d_model=256, layers=2, heads=8, kv_heads=4, head_dim
 
 
 def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
-                 layers: Optional[int] = None, position_bound: Optional[int] = None) -> Program:
+                 layers: Optional[int] = None, position_bound: Optional[int] = None,
+                 rope_rotated: Optional[int] = None) -> Program:
     """One step of the decoder over the rows it is given (one a decode step,
     a sequence's run of rows a prefill): ``embed`` gathers each token's row
     of ``embed`` (else the rows ``x`` are an input); outputs ``logits`` and
     the greedy ``token`` of every row.  Positions are declared below
     ``position_bound`` (default: the context), which decides whether a
-    step's KV stores fit the ring in place (Plan.hs:276-281)."""
+    step's KV stores fit the ring in place (Plan.hs:276-281).  RoPE turns
+    ``rope_rotated`` pairs of each head (default: all, head_dim / 2)."""
     L = dims.layers if layers is None else layers
     wt = dims.weight_type
 
@@ -84,7 +86,7 @@ def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
             x = b.gather("x0", table, tokens, 1.0)
         else:
             x = b.input("x", whole_row(dims.d_model), F32)
-        rope = RopeSpec(dims.rope_theta, dims.head_dim // 2)
+        rope = RopeSpec(dims.rope_theta, dims.head_dim // 2 if rope_rotated is None else rope_rotated)
         attn = AttnSpec(dims.heads, dims.kv_heads, dims.head_dim, None, 1.0 / math.sqrt(dims.head_dim))
         for i in range(L):
             p = f"l{i}_"

@@ -6,7 +6,9 @@ prefill (furykernel_amd/prefill.py): every row's logits and the KV caches it
 fills within the f16 bar, 2e-3 of the largest magnitude, of the vectorised
 binary64 evaluator (oracle/eval.py, pinned to the exact one).  The GEMM
 operands and the attention's probabilities are f16 on this path; the
-evaluator rounds only the cache stores.
+evaluator rounds only the cache stores.  With every pair of the heads turned
+the QKV GEMM RoPEs and stores in its epilogue; with 16 of the 32 the RoPE
+kernel does (both run).
 """
 
 import numpy as np
@@ -43,18 +45,21 @@ def rel(a, b):
     return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
 
 
-@pytest.fixture(scope="module")
-def run(device, kernels):
+@pytest.fixture(scope="module", params=[None, 16], ids=["rope-all-pairs", "rope-16-pairs"])
+def run(request, device, kernels):
     from furykernel_amd.prefill import PrefillSession
 
-    s = PrefillSession(device, kernels, SMALL_PREFILL, SEQS, SEQ_ROWS)
+    s = PrefillSession(device, kernels, SMALL_PREFILL, SEQS, SEQ_ROWS, rope_rotated=request.param)
+    entries = {l.entry for l in s.lowered.launches}
+    fused = "fk_gemm_f16_qkv_rope" in entries
+    assert fused == (request.param is None) and fused != ("fk_prefill_rope_store" in entries)
     weights, tokens = small_state(s.checked)
     s.write_weights(weights)
     for name in s.lowered.buffers:
         if name.startswith("cache:"):
             s.engine.zero(name)
     s.set_tokens(tokens)
-    print(f"prefill small: {len(s.lowered.launches)} launches", flush=True)
+    print(f"prefill small, rotated {request.param}: {len(s.lowered.launches)} launches", flush=True)
     s.run()
     device.sync()
     lay = SMALL_PREFILL
@@ -151,16 +156,19 @@ def test_prefill_attention_with_a_window_against_f64(device, kernels):
         b.free()
 
 
-def test_prefill_norm_pack_against_f64(device, kernels):
+@pytest.mark.parametrize("width", [512, 2048, 768])
+def test_prefill_norm_pack_against_f64(device, kernels, width):
+    """The one-pass entries (rows of 512 and 2048 held in registers) and the
+    two-pass kernel (768)."""
     from furykernel_amd.layout import unpack
 
     rng = np.random.default_rng(4)
-    x = rng.standard_normal((256, 512)).astype(np.float32)
-    g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
-    bx, bg, by = device.upload(x), device.upload(g), device.alloc(256 * 512 * 2)
-    kernels.prefill_norm_pack(bx, bg, by, 256, 512, eps=1e-5)
+    x = rng.standard_normal((256, width)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(width)).astype(np.float32)
+    bx, bg, by = device.upload(x), device.upload(g), device.alloc(256 * width * 2)
+    kernels.prefill_norm_pack(bx, bg, by, 256, width, eps=1e-5)
     device.sync()
-    got = unpack(by.read(np.float16, 256 * 512), 256, 512).astype(np.float64)
+    got = unpack(by.read(np.float16, 256 * width), 256, width).astype(np.float64)
     xd = x.astype(np.float64)
     want = xd * (np.mean(xd * xd, axis=1, keepdims=True) + 1e-5) ** -0.5 * g
     # one f16 rounding: within half an f16 ulp of the value, up to f32 noise

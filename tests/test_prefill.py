@@ -54,31 +54,43 @@ def small_lowered(seq_rows=128, seqs=2, **kw):
 def test_prefill_lowering_of_the_small_decoder():
     _, low = small_lowered()
     entries = [l.entry for l in low.launches]
-    per_layer = ["fk_prefill_norm_pack", "fk_gemm_f16_store", "fk_prefill_rope_store", "fk_prefill_attend_g2",
-                 "fk_gemm_f16_add", "fk_prefill_norm_pack", "fk_gemm_f16_silu_mul", "fk_gemm_f16_add"]
-    assert entries == ["fk_prefill_gather"] + per_layer * 2 + ["fk_prefill_norm_pack", "fk_gemm_f16_store",
-                                                               "fk_prefill_argmax"]
+    norm = "fk_prefill_norm_pack"     # rows of 256: the two-pass kernel
+    # the QKV GEMM RoPEs and stores in its epilogue: no RoPE launch, no f32 q, k, v
+    per_layer = [norm, "fk_gemm_f16_qkv_rope", "fk_prefill_attend_g2",
+                 "fk_gemm_f16_add", norm, "fk_gemm_f16_silu_mul", "fk_gemm_f16_add"]
+    assert entries == ["fk_prefill_gather"] + per_layer * 2 + [norm, "fk_gemm_f16_store", "fk_prefill_argmax"]
     qkv = low.launches[2]
     assert qkv.params["first_col"] == [0, 512, 768, 1024] and qkv.groups == 1 * 4
-    att = low.launches[4]
+    att = low.launches[3]
     assert att.entry == "fk_prefill_attend_g2" and att.threads == 128 and att.groups == (256 // 32) * 4
-    silu = low.launches[7]
+    assert (qkv.bind["c0"], qkv.bind["c1"], qkv.bind["c2"]) == (att.bind["qr"], att.bind["kc"], att.bind["vc"])
+    assert (qkv.params["kv_heads"], qkv.params["length"], qkv.params["slots"]) == (4, 256, 2)
+    assert not any(b.startswith(("value:l0_q", "value:l0_k", "value:l0_v")) for b in low.buffers)
+    silu = low.launches[6]
     assert silu.bind["b0"] == "pair:l0_gate_proj|l0_up_proj" and silu.bind["c0"] == "tiled:l0_act"
-    assert low.launches[8].bind["a"] == "tiled:l0_act"
+    assert low.launches[7].bind["a"] == "tiled:l0_act"
     # the o projection reads the attention's tiled output, adds the gathered rows
-    o = low.launches[5]
+    o = low.launches[4]
     assert o.bind["a"] == "tiled:l0_attn" and o.bind["r0"] == "value:x0"
+
+
+def test_prefill_keeps_the_rope_launch_when_only_some_pairs_turn():
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128, rope_rotated=16))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256)
+    entries = [l.entry for l in low.launches]
+    assert "fk_prefill_rope_store" in entries and "fk_gemm_f16_qkv_rope" not in entries
 
 
 def test_prefill_lowering_of_the_1b_decoder():
     c = check_program(decoder_step(ONE_B_PREFILL, name="prefill", position_bound=2048))
     low = lower_prefill(c, plan(PlanOptions(sequence_rows=2048), c), 8192)
-    assert len(low.launches) == 1 + 16 * 8 + 3
+    assert len(low.launches) == 1 + 16 * 7 + 3
     gu = [l for l in low.launches if l.entry == "fk_gemm_f16_silu_mul"][0]
     assert gu.groups == 32 * (8192 // 128)
     att = [l for l in low.launches if l.entry.startswith("fk_prefill_attend")][0]
     assert att.entry == "fk_prefill_attend_g4" and att.threads == 256 and att.groups == 256 * 8
     assert low.buffers["cache:l0_k_cache"].count == 4 * 8 * 4096 * 64
+    assert low.launches[1].entry == "fk_prefill_norm_pack_w2048"   # the one-pass norm of rows of 2048
 
 
 def test_prefill_refuses_what_its_kernels_do_not_take():
