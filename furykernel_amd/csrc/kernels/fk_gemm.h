@@ -13,19 +13,22 @@
 // whole share of 512) takes a 256 × 256 tile of C (for SiLU·mul, 256 rows ×
 // 128 columns of gate and the same 128 of up, held together as one 256-row
 // slab of the paired weights).  Wavefront (wm, wn) holds 128 × 128 of it as
-// 4 × 4 blocks of 32 × 32 in AGPRs, accumulated by v_mfma_f32_32x32x16_f16:
-// 32 matrix operations a wavefront each K step of 32, on 16 reads of 16
+// 8 × 8 blocks of 16 × 16 in AGPRs, accumulated by v_mfma_f32_16x16x32_f16:
+// 64 matrix operations a wavefront each K step of 32, on 16 reads of 16
 // bytes a lane from LDS.
 //
-// v_mfma_f32_32x32x16_f16 (D = A B + C, A 32 × 16, B 16 × 32): lane l holds
-// A[l mod 32][8 (l div 32) .. + 7] and B[8 (l div 32) .. + 7][l mod 32] as 8
-// halves each, and D[8 g + 4 (l div 32) + r][l mod 32] as register 4 g + r.
-// The weights are the first operand, so D's rows are C's columns and a lane
-// holds four consecutive columns of one C row: 16-byte stores.
+// v_mfma_f32_16x16x32_f16 (D = A B + C, A 16 × 32, B 32 × 16): lane l holds
+// A[l mod 16][8 (l div 16) .. + 7] and B[8 (l div 16) .. + 7][l mod 16] as 8
+// halves each, and D[4 (l div 16) + r][l mod 16] as register r.  The
+// weights are the first operand, so D's rows are C's columns and a lane
+// holds four consecutive columns of one C row: 16-byte stores.  (The 16 × 16
+// form rather than 32 × 32: a step's 64 operations have no dependence among
+// them, and the shorter operations leave more places for the step's loads
+// and reads between them; measured faster at every shape here.)
 //
-// The K loop is a ring of 4 LDS stages (4 × 32 KB): tiles go in 3 steps
-// ahead by direct loads (buffer_load ... lds), the fragments of the next
-// step are read while this step's are multiplied, one barrier a step.
+// The K loop is a ring of 4 LDS stages (4 × 32 KB), loaded by direct loads
+// (buffer_load ... lds) 2 tiles ahead of the one being read; a step's loads,
+// reads and matrix operations are interleaved, one barrier a step.
 //
 // The order of the sums over k is the matrix core's; results are held to the
 // binary32 accumulation bound of the f16 products (the contract of Tile.hs's
@@ -40,7 +43,9 @@
 #define FK_GEMM_BM 256
 #define FK_GEMM_BN 256
 #define FK_GEMM_BK 32
+#ifndef FK_GEMM_STAGES
 #define FK_GEMM_STAGES 4
+#endif
 #define FK_GEMM_LDS (FK_GEMM_STAGES * 2 * FK_GEMM_BM * FK_GEMM_BK * 2)
 #define FK_LDS __attribute__((address_space(3)))
 
@@ -125,70 +130,46 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
   const auto rb_src = fk::buffer(bslab, slab_bytes);
   const uint32_t vl = wave_s * 4 * 1024 + lane * 16;
   FK_LDS char *const stage0 = (FK_LDS char *)gemm_lds + wave_s * 4 * 1024;
-#define FK_GEMM_LOAD_TILE(T, ST)                                                                          \
-  do {                                                                                                    \
-    const uint32_t so_ = (T) * TILEB;                                                                     \
-    FK_LDS char *d_ = stage0 + (ST) * STAGEB;                                                             \
-    _Pragma("unroll") for (int q = 0; q < 4; q++) {                                                       \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_src, d_ + q * 1024, 16, vl + q * 1024, so_, 0, 0);      \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_src, d_ + TILEB + q * 1024, 16, vl + q * 1024, so_, 0, 0); \
-    }                                                                                                     \
-  } while (0)
 
-  // Fragment reads: lane l reads row l mod 32 of a 32-row block and logical
-  // unit 2 h + l div 32 of the step's k-half h, at its swizzled place; A's
-  // blocks are rows wm 128 + 32 i, B's columns wn 128 + 32 j of the tile, or
-  // for SiLU·mul gate columns wn 64 + 32 j (blocks 0-1) and the same up
-  // columns (blocks 2-3), so that a lane holds gate and up of one element.
-  const uint32_t rsw = fk::tile_swizzle(lane % 16);
-  const uint32_t ra = (wm * 128 + lane % 32) * ROW16;
-  const uint32_t rb = TILEB / 16 + (wn * (MODE == FK_GEMM_SILU_MUL ? 64 : 128) + lane % 32) * ROW16;
-  const uint32_t kc0 = (lane / 32) ^ rsw, kc1 = (2 + lane / 32) ^ rsw;
-#define FK_GEMM_BROW(J) (MODE == FK_GEMM_SILU_MUL ? ((J) < 2 ? 32 * (J) : FK_GEMM_BN / 2 + 32 * ((J) - 2)) : 32 * (J))
+  // Fragment reads.  v_mfma_f32_16x16x32_f16 takes from lane l row l mod 16
+  // of a 16-row block and k 8 (l div 16) .. + 7 of the step: a block is one
+  // 1 KB chunk of the staged tile, lane l reading its row's logical unit
+  // l div 16 at the swizzled place, and 16 lanes a cycle meet 16 different
+  // bank groups.  A's blocks are rows wm 128 + 16 i of the tile; B's are
+  // columns wn 128 + 16 j, or for SiLU·mul gate columns wn 64 + 16 j (blocks
+  // 0-3) and the same up columns (blocks 4-7), so that a lane holds gate and
+  // up of one element.
+  const uint32_t lu = (lane % 16) * 4 + ((lane / 16) ^ fk::tile_swizzle(lane % 16));
+  const uint32_t ra = wm * 8 * 64 + lu;
+  const uint32_t rb = TILEB / 16 + (MODE == FK_GEMM_SILU_MUL ? wn * 4 : wn * 8) * 64 + lu;
+#define FK_GEMM_BOFF(J) ((MODE == FK_GEMM_SILU_MUL && (J) >= 4 ? 4 + (J) : (J)) * 64)
 
-  fk_float16v acc[4][4];
+  // 8 × 8 blocks of 16 × 16, 4 registers each: the 256 AGPRs.
+  fk_float4v acc[8][8];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < 8; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < 8; j++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
-  // Two sets of fragments: [A | B][k-half][block].
-  fk::Half8 fr0[2][2][4], fr1[2][2][4];
-#define FK_GEMM_READ(FA, FB, ST)                                                                          \
-  do {                                                                                                    \
-    const uint4 *s_ = gemm_lds + (ST) * (STAGEB / 16);                                                    \
-    _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                       \
-      FB[0][j].u = s_[rb + FK_GEMM_BROW(j) * ROW16 + kc0];                                                \
-      FB[1][j].u = s_[rb + FK_GEMM_BROW(j) * ROW16 + kc1];                                                \
-    }                                                                                                     \
-    _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                       \
-      FA[0][i].u = s_[ra + 32 * i * ROW16 + kc0];                                                         \
-      FA[1][i].u = s_[ra + 32 * i * ROW16 + kc1];                                                         \
-    }                                                                                                     \
-  } while (0)
+  // Two sets of fragments (A's 8 blocks, B's 8).
+  fk::Half8 fa0[8], fb0[8], fa1[8], fb1[8];
   // The fragments stay in VGPRs: the matrix operation would also take them
   // from AGPRs, and an allocation that puts them there moves accumulators
   // around the loop.  The constraint also completes their reads here.
-#define FK_GEMM_PIN(FA, FB)                                                                               \
-  do {                                                                                                    \
-    _Pragma("unroll") for (int h = 0; h < 2; h++)                                                         \
-    _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                       \
-      asm volatile("" : "+v"(FB[h][j].h));                                                                \
-      asm volatile("" : "+v"(FA[h][j].h));                                                                \
-    }                                                                                                     \
-  } while (0)
-#define FK_GEMM_MFMA(FA, FB)                                                                              \
-  do {                                                                                                    \
-    _Pragma("unroll") for (int h = 0; h < 2; h++)                                                         \
-    _Pragma("unroll") for (int i = 0; i < 4; i++)                                                         \
-    _Pragma("unroll") for (int j = 0; j < 4; j++)                                                         \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(FB[h][j].h, FA[h][i].h, acc[i][j], 0, 0, 0);     \
-  } while (0)
-  // s_waitcnt vmcnt(8), the other counters untouched: at most one tile's
-  // loads (8 a thread) still in flight, so the one before it has landed.
-#define FK_GEMM_WAIT_TILE() __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0xf << 8))
+#define FK_GEMM_PIN(X) asm volatile("" : "+v"((X).h))
+  // The accumulators stay in AGPRs across steps: left free, the allocator
+  // moves some of the 64 tuples through VGPRs every iteration.
+#define FK_GEMM_PIN_ACC()                                                                                 \
+  _Pragma("unroll") for (int i_ = 0; i_ < 8; i_++)                                                        \
+  _Pragma("unroll") for (int j_ = 0; j_ < 8; j_++) asm volatile("" : "+a"(acc[i_][j_]))
+#define FK_GEMM_MFMA_ROW(FA, FB, I)                                                                       \
+  _Pragma("unroll") for (int j_ = 0; j_ < 8; j_++)                                                        \
+    acc[I][j_] = __builtin_amdgcn_mfma_f32_16x16x32_f16(FB[j_].h, FA[I].h, acc[I][j_], 0, 0, 0)
+  // s_waitcnt vmcnt(n), the other counters untouched (vmcnt's low four bits
+  // at 3:0, its high two at 15:14).
+#define FK_GEMM_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (0x7 << 4) | (0xf << 8))
   // The workgroup barrier without the release fence of __syncthreads, which
   // would wait for every load in flight into LDS (vmcnt(0)); the loads this
   // barrier publishes are the ones the wait before it has seen land.  The
@@ -199,104 +180,157 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
     __builtin_amdgcn_s_barrier();         \
     asm volatile("" ::: "memory");        \
   } while (0)
-  // One K step: tile s's fragments FC in registers, tile s + 1's read into
-  // FN while FC is multiplied; the tile loads go out between the matrix
-  // operations, one after every four.
-#define FK_GEMM_STEP(FC, FN, T_LOAD, ST_LOAD, ST_READ)                                                   \
+  // One K step of tile s (fragments FA, FB in registers; A's blocks 4-7
+  // still on their way) in two halves of 32 matrix operations, A's blocks
+  // 0-3 then 4-7 against all of B's.  The first half issues the loads of A's
+  // part of tile s - 1 + S, and reads tile s + 1's B blocks and A blocks 0-3,
+  // spread among its operations; the second completes the reads of FA's
+  // blocks 4-7 (issued in the step before), issues B's loads and reads tile
+  // s + 1's A blocks 4-7; the step ends completing the first half's reads.
+  // So a read is waited for half a step after it goes out, the LDS sees the
+  // step's reads spread over its matrix operations, and the address units
+  // the loads the same way.
+#define FK_GEMM_STEP(FA, FB, NA, NB, T_LOAD, ST_LOAD, ST_READ)                                           \
   do {                                                                                                    \
-    FK_GEMM_WAIT_TILE();                                                                                  \
+    FK_GEMM_VMCNT(8 * (FK_GEMM_STAGES - 3));                                                              \
     FK_GEMM_BARRIER();                                                                                    \
-    FK_GEMM_READ(FN[0], FN[1], ST_READ);                                                                  \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
-    FK_GEMM_MFMA(FC[0], FC[1]);                                                                           \
-    FK_GEMM_LOAD_TILE(T_LOAD, ST_LOAD);                                                                   \
-    _Pragma("unroll") for (int g_ = 0; g_ < 8; g_++) {                                                    \
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                                  \
+    const uint32_t so_ = (T_LOAD) * TILEB;                                                                \
+    FK_LDS char *d_ = stage0 + (ST_LOAD) * STAGEB;                                                        \
+    const uint4 *s_ = gemm_lds + (ST_READ) * (STAGEB / 16);                                               \
+    _Pragma("unroll") for (int q = 0; q < 4; q++) {                                                       \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_src, d_ + q * 1024, 16, vl + q * 1024, so_, 0, 0);      \
+      NB[2 * q].u = s_[rb + FK_GEMM_BOFF(2 * q)];                                                         \
+      NB[2 * q + 1].u = s_[rb + FK_GEMM_BOFF(2 * q + 1)];                                                 \
+      NA[q].u = s_[ra + 64 * q];                                                                          \
+    }                                                                                                     \
+    _Pragma("unroll") for (int i_ = 0; i_ < 4; i_++) { FK_GEMM_MFMA_ROW(FA, FB, i_); }                    \
+    _Pragma("unroll") for (int g_ = 0; g_ < 4; g_++) {                                                    \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                                  \
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                  \
     }                                                                                                     \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
-    FK_GEMM_PIN(FN[0], FN[1]);                                                                            \
+    _Pragma("unroll") for (int i_ = 4; i_ < 8; i_++) FK_GEMM_PIN(FA[i_]);                                 \
+    _Pragma("unroll") for (int q = 0; q < 4; q++) {                                                       \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_src, d_ + TILEB + q * 1024, 16, vl + q * 1024, so_, 0, 0); \
+      NA[4 + q].u = s_[ra + 64 * (4 + q)];                                                                \
+    }                                                                                                     \
+    _Pragma("unroll") for (int i_ = 4; i_ < 8; i_++) { FK_GEMM_MFMA_ROW(FA, FB, i_); }                    \
+    _Pragma("unroll") for (int g_ = 0; g_ < 4; g_++) {                                                    \
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                  \
+    }                                                                                                     \
+    __builtin_amdgcn_sched_barrier(0);                                                                    \
+    _Pragma("unroll") for (int j_ = 0; j_ < 8; j_++) FK_GEMM_PIN(NB[j_]);                                 \
+    _Pragma("unroll") for (int i_ = 0; i_ < 4; i_++) FK_GEMM_PIN(NA[i_]);                                 \
+    FK_GEMM_PIN_ACC();                                                                                    \
   } while (0)
 
-  // The pipeline.  At step s the fragments of tile s are in registers and
-  // tiles s + 1, s + 2 are in LDS stages (s + 1) mod 4, (s + 2) mod 4 or on
-  // their way there.  Step s waits for its own loads of tile s + 1, meets the
-  // others at the barrier (after which all of tile s + 1 is in LDS), reads
-  // tile s + 1's fragments, multiplies tile s's and loads tile s + 3 into
-  // stage (s + 3) mod 4 (tile s - 1's, whose fragments every wave read before
-  // this step's barrier).  Loads past the last tile repeat it into stages no
-  // step reads.
+  // The pipeline, S = STAGES deep.  At step s (after its barrier) tile s's
+  // fragments are in registers but for A's blocks 4-7, on the way from LDS
+  // stage s mod S, and tiles s + 1 .. s + S - 2 are in their stages (numbers
+  // mod S) or on their way there.  Step s waits for its own loads of tile s
+  // + 1, meets the others at the barrier (after which all of tile s + 1 is in
+  // LDS and every wave has completed its reads of tile s - 1), loads tile s -
+  // 1 + S into tile s - 1's stage, reads tile s + 1's fragments and
+  // multiplies tile s's.  Loads past the last tile repeat it into stages no
+  // step reads, so every step's wait counts the same loads.
   const uint32_t steps = k / FK_GEMM_BK;  // even
   const uint32_t last = steps - 1;
 #define FK_GEMM_T(X) ((X) < last ? (X) : last)
-  FK_GEMM_LOAD_TILE(0, 0);
-  FK_GEMM_LOAD_TILE(FK_GEMM_T(1), 1);
-  FK_GEMM_LOAD_TILE(FK_GEMM_T(2), 2);
-  __builtin_amdgcn_s_waitcnt((1 << 14) | (0x7 << 4) | (0xf << 8));  // vmcnt(16): tile 0 landed
+#pragma unroll
+  for (uint32_t t = 0; t + 1 < FK_GEMM_STAGES; t++) {
+    const uint32_t so_ = FK_GEMM_T(t) * TILEB;
+    FK_LDS char *d_ = stage0 + t * STAGEB;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_src, d_ + q * 1024, 16, vl + q * 1024, so_, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_src, d_ + TILEB + q * 1024, 16, vl + q * 1024, so_, 0, 0);
+    }
+  }
+  FK_GEMM_VMCNT(8 * (FK_GEMM_STAGES - 2));  // tile 0 landed
   FK_GEMM_BARRIER();
-  FK_GEMM_READ(fr0[0], fr0[1], 0);
-  FK_GEMM_PIN(fr0[0], fr0[1]);
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    fb0[q].u = gemm_lds[rb + FK_GEMM_BOFF(q)];
+    fa0[q].u = gemm_lds[ra + 64 * q];
+  }
+#pragma unroll
+  for (int q = 0; q < 8; q++) FK_GEMM_PIN(fb0[q]);
+#pragma unroll
+  for (int q = 0; q < 4; q++) FK_GEMM_PIN(fa0[q]);
   for (uint32_t s = 0; s < steps; s += 2) {
-    FK_GEMM_STEP(fr0, fr1, FK_GEMM_T(s + 3), (s + 3) % FK_GEMM_STAGES, (s + 1) % FK_GEMM_STAGES);
-    FK_GEMM_STEP(fr1, fr0, FK_GEMM_T(s + 4), (s + 4) % FK_GEMM_STAGES, (s + 2) % FK_GEMM_STAGES);
+    FK_GEMM_STEP(fa0, fb0, fa1, fb1, FK_GEMM_T(s - 1 + FK_GEMM_STAGES), (s + FK_GEMM_STAGES - 1) % FK_GEMM_STAGES,
+                 (s + 1) % FK_GEMM_STAGES);
+    FK_GEMM_STEP(fa1, fb1, fa0, fb0, FK_GEMM_T(s + FK_GEMM_STAGES), s % FK_GEMM_STAGES, (s + 2) % FK_GEMM_STAGES);
   }
   // Nothing may still be landing in LDS when the threadgroup ends.
   __builtin_amdgcn_s_waitcnt(0);
-#undef FK_GEMM_LOAD_TILE
-#undef FK_GEMM_READ
 #undef FK_GEMM_PIN
-#undef FK_GEMM_MFMA
-#undef FK_GEMM_WAIT_TILE
+#undef FK_GEMM_PIN_ACC
+#undef FK_GEMM_MFMA_ROW
+#undef FK_GEMM_VMCNT
 #undef FK_GEMM_BARRIER
 #undef FK_GEMM_STEP
 #undef FK_GEMM_T
-#undef FK_GEMM_BROW
+#undef FK_GEMM_BOFF
 
-  // Epilogue.  Block (i, j)'s lane l holds C row m = wm 128 + 32 i + l mod 32
-  // and, for each g < 4, columns 32 j + 8 g + 4 (l div 32) .. + 3 (of the
-  // wavefront's) as registers 4 g .. 4 g + 3.
-  const uint32_t m = m0 + wm * 128 + lane % 32;
-  const uint32_t nq = 4 * (lane / 32);
+  // Epilogue.  Block (i, j)'s lane l holds C row m = wm 128 + 16 i + l mod 16
+  // and columns 16 j + 4 (l div 16) .. + 3 (of the wavefront's).  (The lane
+  // index is taken anew through an asm statement, so that nothing of the
+  // epilogue is computed before the loop and held in registers across it.)
+  uint32_t lane_e;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(lane_e) : "v"(lane));
+  const uint32_t m = m0 + wm * 128 + lane_e % 16;
+  const uint32_t nq = 4 * (lane_e / 16);
   if (MODE == FK_GEMM_SILU_MUL) {
     uint16_t *out = reinterpret_cast<uint16_t *>(c0);
     const uint32_t ncols = p.ldc[0];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 8; i++)
 #pragma unroll
-      for (int j = 0; j < 2; j++)
+      for (int j = 0; j < 4; j++) {
+        // Blocks 0-3: gate columns wn 64 + 16 j; blocks 4-7 the same up columns.
+        const uint32_t n = n0 + wn * 64 + 16 * j + nq;
+        uint16_t h[4];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          // Blocks 0-1: gate columns wn 64 + 32 j; blocks 2-3 the same up columns.
-          const uint32_t n = n0 + wn * 64 + 32 * j + 8 * g + nq;
-          uint16_t h[4];
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float gt = acc[i][j][4 * g + r];
-            const float u = acc[i][j + 2][4 * g + r];
-            // silu(g) u = g / (1 + e^-g) · u with the hardware's exp and
-            // reciprocal (a few ulp of binary32), then rounded once to f16
-            // (2^-11): the f16 rounding bounds the error.  e^-g overflowing
-            // gives silu 0, as the limit.
-            const float e = __expf(-gt);
-            h[r] = fk::to_f16(gt * __builtin_amdgcn_rcpf(1.0f + e) * u);
-          }
-          uint2 w;
-          w.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-          w.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
-          // Four consecutive columns of one row: half of one 16-byte unit.
-          *reinterpret_cast<uint2 *>(out + fk::tile_offset(m + 32 * i, n, ncols)) = w;
+        for (int r = 0; r < 4; r++) {
+          const float gt = acc[i][j][r];
+          const float u = acc[i][j + 4][r];
+          // silu(g) u = g / (1 + e^-g) · u with the hardware's exp and
+          // reciprocal (a few ulp of binary32), then rounded once to f16
+          // (2^-11): the f16 rounding bounds the error.  e^-g overflowing
+          // gives silu 0, as the limit.
+          const float e = __expf(-gt);
+          h[r] = fk::to_f16(gt * __builtin_amdgcn_rcpf(1.0f + e) * u);
         }
+        uint2 w;
+        w.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        w.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+        // Four consecutive columns of one row: half of one 16-byte unit.
+        *reinterpret_cast<uint2 *>(out + fk::tile_offset(m + 16 * i, n, ncols)) = w;
+        if (j == 3) asm volatile("" ::: "memory");  // one row block at a time
+      }
   } else if (MODE == FK_GEMM_QKV_ROPE) {
-    // A 256-column tile is 4 whole heads; a lane's blocks 2 jp and 2 jp + 1
-    // are the low and high halves of one head, so it holds both elements of
-    // each pair RoPE turns (NeoX halves, as rope_elem: x_j c - x_{j+32} s below
-    // the half, x_j c + x_{j-32} s above, the table's cos and sin of the row's
-    // position).  q goes to f16 rows (the attention's), k and v to the caches
-    // rounded as the decode step's stores round.
+    // A 256-column tile is 4 whole heads, a wavefront's 128 columns 2; a
+    // lane's blocks 4 jp + jj and 4 jp + jj + 2 hold columns d and d + 32 of
+    // head jp, both elements of each pair RoPE turns (NeoX halves, as
+    // rope_elem: x_j c - x_{j+32} s below the half, x_j c + x_{j-32} s above,
+    // the table's cos and sin of the row's position).  q goes to f16 rows
+    // (the attention's), k and v to the caches rounded as the decode step's
+    // stores round.
     const bool bf16 = rp.cache_bf16 != 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t row = m + 32 * i;
+    for (int i = 0; i < 8; i++) {
+      const uint32_t row = m + 16 * i;
       const uint32_t pos = position[row];
       const uint32_t sl = min(slot[row], rp.slots - 1);
       const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
@@ -304,13 +338,13 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
       for (int jp = 0; jp < 2; jp++) {
         const uint32_t head = (n0 + wn * 128 + 64 * jp) / 64;
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const uint32_t d = 8 * g + nq;  // the low half's first of four columns; their partners d + 32 ..
+        for (int jj = 0; jj < 2; jj++) {
+          const uint32_t d = 16 * jj + nq;  // the low half's first of four columns; their partners d + 32 ..
           float lo[4], hi[4];
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            lo[r] = acc[i][2 * jp][4 * g + r];
-            hi[r] = acc[i][2 * jp + 1][4 * g + r];
+            lo[r] = acc[i][4 * jp + jj][r];
+            hi[r] = acc[i][4 * jp + jj + 2][r];
           }
           if (anchor != 2) {
             const float4 t01 = *reinterpret_cast<const float4 *>(cs + 2 * d);      // (cos, sin) of pairs d, d + 1
@@ -343,21 +377,33 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
           }
         }
       }
+      asm volatile("" ::: "memory");  // one row block at a time
     }
   } else {
     float *out = reinterpret_cast<float *>(anchor == 0 ? c0 : (anchor == 1 ? c1 : c2));
     const uint32_t ld = anchor == 0 ? p.ldc[0] : (anchor == 1 ? p.ldc[1] : p.ldc[2]);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 8; i++) {
+      const size_t row = (size_t)(m + 16 * i) * ld + n0 + wn * 128 + nq;
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+      for (int j = 0; j < 8; j++) {
+        fk_float4v v = acc[i][j];
+        if (MODE == FK_GEMM_ADD) v = *reinterpret_cast<const fk_float4v *>(r0 + row + 16 * j) + v;
+        else {
+          // Through an arithmetic copy (the canonical value: the same number):
+          // a store straight from the accumulator leaves the allocator free
+          // to hold accumulators in VGPRs through the loop, copying them at
+          // every step.
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const size_t at = (size_t)(m + 32 * i) * ld + n0 + wn * 128 + 32 * j + 8 * g + nq;
-          fk_float4v v = fk_float4v{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          if (MODE == FK_GEMM_ADD) v = *reinterpret_cast<const fk_float4v *>(r0 + at) + v;
-          *reinterpret_cast<fk_float4v *>(out + at) = v;
+          for (int r = 0; r < 4; r++) v[r] = __builtin_canonicalizef(v[r]);
         }
+        *reinterpret_cast<fk_float4v *>(out + row + 16 * j) = v;
+      }
+      // One row block at a time: the compiler may not gather every block's
+      // addresses (and loads) ahead, which would crowd the registers the
+      // accumulators hold.
+      asm volatile("" ::: "memory");
+    }
   }
 }
 

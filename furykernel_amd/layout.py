@@ -6,7 +6,7 @@ A matrix X [R, K] of f16 (R a multiple of 256, K of 32) is held as slabs of
 256 rows; a slab, for each step of 32 columns, as 16 chunks of 1 KB (rows
 16 c .. 16 c + 15 of the slab); a chunk as 64 units of 16 bytes, unit L
 holding row L div 4 of the chunk and the 8 columns of logical unit
-(L mod 4) ^ ((row div 2) mod 4) of the step.  It is the image the GEMM
+(L mod 4) ^ ((row div 4) mod 4) of the step.  It is the image the GEMM
 stages in LDS (furykernel_amd/csrc/kernels/fk_layout.h says the same in C).
 
 The SiLU·mul GEMM takes its gate and up weights paired: slab j of the pair is
@@ -28,7 +28,7 @@ class LayoutError(ValueError):
 
 def _swizzle_index() -> np.ndarray:
     rows = np.arange(16)
-    return np.arange(4)[None, :] ^ ((rows // 2) % 4)[:, None]   # [row, place] -> logical unit
+    return np.arange(4)[None, :] ^ ((rows // 4) % 4)[:, None]   # [row, place] -> logical unit
 
 
 def pack(x: np.ndarray) -> np.ndarray:
@@ -69,5 +69,5 @@ def tile_offset(row: int, col: int, k: int) -> int:
     """Offset in elements of (row, col) in a tiled matrix of k columns."""
     slab, chunk, r = row // SLAB, (row // 16) % 16, row % 16
     step, unit, half = col // STEP, (col // 8) % 4, col % 8
-    place = unit ^ ((r // 2) % 4)
+    place = unit ^ ((r // 4) % 4)
     return ((slab * (k // STEP) + step) * 16 + chunk) * 512 + (4 * r + place) * 8 + half

@@ -30,8 +30,11 @@ def test_a_chunk_is_16_rows_of_one_step_and_units_are_swizzled():
     x = np.arange(256 * 32, dtype=np.uint32).reshape(256, 32)
     flat = pack(x).reshape(16, 64, 8)            # one slab, one step: 16 chunks of 64 units
     assert np.array_equal(flat[1, 0], x[16, 0:8])  # chunk 1 starts at row 16
-    # row 2 of a chunk has swizzle 1: its place 0 holds logical unit 1
-    assert np.array_equal(flat[0, 8], x[2, 8:16])
+    # rows 0-3 of a chunk are unswizzled; row 4 has swizzle 1: its place 0
+    # holds logical unit 1, row 13 (swizzle 3) place 1 holds unit 2
+    assert np.array_equal(flat[0, 8], x[2, 0:8])
+    assert np.array_equal(flat[0, 16], x[4, 8:16])
+    assert np.array_equal(flat[0, 4 * 13 + 1], x[13, 16:24])
 
 
 def test_pair_alternates_128_row_blocks():
