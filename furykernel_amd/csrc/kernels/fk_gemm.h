@@ -325,58 +325,47 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
     // head jp, both elements of each pair RoPE turns (NeoX halves, as
     // rope_elem: x_j c - x_{j+32} s below the half, x_j c + x_{j-32} s above,
     // the table's cos and sin of the row's position).  q goes to f16 rows
-    // (the attention's), k and v to the caches rounded as the decode step's
-    // stores round.
+    // (the attention's), k and v to the caches.  Every choice is uniform and
+    // made by selects, with the hardware's f16 conversion (to nearest even,
+    // gradual underflow: narrow_f16's rounding), so the row-block loop
+    // unrolls and the accumulators stay in registers.
     const bool bf16 = rp.cache_bf16 != 0;
+    const bool turn = anchor != 2;
+    const uint32_t head0 = (n0 + wn * 128) / 64;
+    uint16_t *const dst = reinterpret_cast<uint16_t *>(anchor == 0 ? c0 : (anchor == 1 ? c1 : c2));
+    const size_t hstride = anchor == 0 ? 64 : (size_t)rp.length * 64;  // halves from head to head
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t row = m + 16 * i;
       const uint32_t pos = position[row];
       const uint32_t sl = min(slot[row], rp.slots - 1);
       const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
+      uint16_t *const base = anchor == 0
+                                 ? dst + (size_t)row * p.ldc[0] + head0 * 64
+                                 : dst + (((size_t)sl * rp.kv_heads + head0) * rp.length + pos % rp.length) * 64;
 #pragma unroll
-      for (int jp = 0; jp < 2; jp++) {
-        const uint32_t head = (n0 + wn * 128 + 64 * jp) / 64;
+      for (int jp = 0; jp < 2; jp++)
 #pragma unroll
         for (int jj = 0; jj < 2; jj++) {
           const uint32_t d = 16 * jj + nq;  // the low half's first of four columns; their partners d + 32 ..
-          float lo[4], hi[4];
+          const float4 t01 = *reinterpret_cast<const float4 *>(cs + 2 * d);      // (cos, sin) of pairs d, d + 1
+          const float4 t23 = *reinterpret_cast<const float4 *>(cs + 2 * d + 4);  // pairs d + 2, d + 3
+          const float cc[4] = {t01.x, t01.z, t23.x, t23.z};
+          const float sn[4] = {t01.y, t01.w, t23.y, t23.w};
+          uint16_t lo[4], hi[4];
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            lo[r] = acc[i][4 * jp + jj][r];
-            hi[r] = acc[i][4 * jp + jj + 2][r];
+            const float x = acc[i][4 * jp + jj][r], y = acc[i][4 * jp + jj + 2][r];
+            const float xr = turn ? x * cc[r] - y * sn[r] : x;
+            const float yr = turn ? y * cc[r] + x * sn[r] : y;
+            lo[r] = bf16 && anchor != 0 ? fk::narrow_bf16(xr) : fk::to_f16(xr);
+            hi[r] = bf16 && anchor != 0 ? fk::narrow_bf16(yr) : fk::to_f16(yr);
           }
-          if (anchor != 2) {
-            const float4 t01 = *reinterpret_cast<const float4 *>(cs + 2 * d);      // (cos, sin) of pairs d, d + 1
-            const float4 t23 = *reinterpret_cast<const float4 *>(cs + 2 * d + 4);  // pairs d + 2, d + 3
-            const float cc[4] = {t01.x, t01.z, t23.x, t23.z};
-            const float sn[4] = {t01.y, t01.w, t23.y, t23.w};
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-              const float x = lo[r] * cc[r] - hi[r] * sn[r];
-              const float y = hi[r] * cc[r] + lo[r] * sn[r];
-              lo[r] = x;
-              hi[r] = y;
-            }
-          }
-          if (anchor == 0) {
-            uint16_t *q = reinterpret_cast<uint16_t *>(c0) + (size_t)row * p.ldc[0] + head * 64 + d;
-            *reinterpret_cast<uint2 *>(q) = make_uint2(fk::to_f16(lo[0]) | ((uint32_t)fk::to_f16(lo[1]) << 16),
-                                                       fk::to_f16(lo[2]) | ((uint32_t)fk::to_f16(lo[3]) << 16));
-            *reinterpret_cast<uint2 *>(q + 32) = make_uint2(fk::to_f16(hi[0]) | ((uint32_t)fk::to_f16(hi[1]) << 16),
-                                                            fk::to_f16(hi[2]) | ((uint32_t)fk::to_f16(hi[3]) << 16));
-          } else {
-            uint16_t *c = reinterpret_cast<uint16_t *>(anchor == 1 ? c1 : c2) +
-                          (((size_t)sl * rp.kv_heads + head) * rp.length + pos % rp.length) * 64 + d;
-            *reinterpret_cast<uint2 *>(c) =
-                make_uint2(fk::narrow_cache(lo[0], bf16) | ((uint32_t)fk::narrow_cache(lo[1], bf16) << 16),
-                           fk::narrow_cache(lo[2], bf16) | ((uint32_t)fk::narrow_cache(lo[3], bf16) << 16));
-            *reinterpret_cast<uint2 *>(c + 32) =
-                make_uint2(fk::narrow_cache(hi[0], bf16) | ((uint32_t)fk::narrow_cache(hi[1], bf16) << 16),
-                           fk::narrow_cache(hi[2], bf16) | ((uint32_t)fk::narrow_cache(hi[3], bf16) << 16));
-          }
+          uint16_t *const at = base + jp * hstride + d;
+          *reinterpret_cast<uint2 *>(at) = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+          *reinterpret_cast<uint2 *>(at + 32) =
+              make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
         }
-      }
       asm volatile("" ::: "memory");  // one row block at a time
     }
   } else {
