@@ -10,33 +10,49 @@
 #include "fk_layout.h"
 #include "fk_mfma.h"
 
+#define FK_ATT_LDS __attribute__((address_space(3)))
+
 // Causal attention of a step's rows over their sequences' caches, on the
 // matrix cores.  A threadgroup takes 32 rows (one sequence's, consecutive
 // positions p0 .. p0 + 31) and one kv head (grid: rows / 32 × kv_heads,
 // query blocks first); its G wavefronts are the G query heads of that kv
-// head.  Keys go by blocks of 32 positions through LDS (K rows padded to 144
-// bytes, V transposed); a wavefront computes Sᵀ = K Qᵀ
-// (v_mfma_f32_32x32x16_f16: lane l holds query l mod 32 and 16 of the
-// block's keys), the online softmax in binary32 — exp2 of one FMA of the
+// head.  Keys go by blocks of 64 positions through two LDS buffers: while a
+// block is multiplied, the next block's K and V rows are on their way from
+// the caches into registers, and go into the other buffer after; one
+// barrier a block.  A wavefront computes Sᵀ = K Qᵀ
+// (v_mfma_f32_32x32x16_f16: lane l holds query l mod 32 and 16 keys of each
+// half block), the online softmax in binary32 — exp2 of one FMA of the
 // score, the scale·log2 e and the running maximum; the causal and window
 // masks only on the blocks that cross them; the output rescaled only when a
-// maximum moved — and Oᵀ += Vᵀ Pᵀ with Pᵀ rounded to f16 straight from the
-// scores' registers.  Head dimension 64.  Output: O / sum into the tile
+// maximum moved; the row sums from the f16 probabilities the matrix
+// operation takes (v_dot2) — and Oᵀ += Vᵀ Pᵀ with Pᵀ rounded to f16 straight
+// from the scores' registers and Vᵀ read transposed out of V's rows
+// (ds_read_b64_tr_b16).  Head dimension 64.  Output: O / sum into the tile
 // layout of [rows, heads · 64], the output projection's A.
 struct fk_prefill_attend_params {
   uint32_t rows;        // a multiple of 32
   uint32_t heads;
   uint32_t kv_heads;    // heads / kv_heads (G) is 1, 2 or 4
-  uint32_t length;      // ring length
+  uint32_t length;      // ring length, a multiple of 64
   uint32_t slots;
   uint32_t window;      // 0: none; else a row sees positions > position - window
   uint32_t cache_bf16;
   float scale;
 };
 
-#define FK_ATT_KROW 72   // halves a staged K row takes: 64 and 8 of padding
-#define FK_ATT_VROW 34   // halves a staged Vᵀ row (one d, 32 keys) takes: 32 and 2, so that rows 17 banks
-                         // apart keep both the staging writes and the fragment reads on distinct banks
+#define FK_ATT_KB 64     // keys a block
+// Staged rows are 64 halves (128 bytes), swizzled rather than padded.  K: a
+// row's 16-byte unit u sits at u ^ ((key >> 1) mod 8), so that the fragment
+// reads (16 lanes: 16 keys, one unit) meet 16 different bank groups and the
+// staging writes (16 lanes: 2 keys' 8 units) too.  V: the two 64-byte halves
+// of a row swap places when key bit 1 is set, so that a transposed read's 4
+// consecutive rows × 64 bytes cover the 256 bytes of banks once.
+__device__ __forceinline__ uint32_t fk_att_kplace(uint32_t key, uint32_t half_off) {
+  return key * 64 + (half_off ^ (((key >> 1) & 7u) << 3));
+}
+__device__ __forceinline__ uint32_t fk_att_vplace(uint32_t key, uint32_t half_off) {
+  return key * 64 + (half_off ^ (((key >> 1) & 1u) << 5));
+}
 
 namespace fk {
 
@@ -45,17 +61,25 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
   return to_f16(__uint_as_float(w << 16)) | ((uint32_t)to_f16(__uint_as_float(w & 0xffff0000u)) << 16);
 }
 
+__device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v) {
+  return make_uint4(bf16x2_to_f16x2(v.x), bf16x2_to_f16x2(v.y), bf16x2_to_f16x2(v.z), bf16x2_to_f16x2(v.w));
+}
+
 }  // namespace fk
+
+typedef short fk_short4 __attribute__((ext_vector_type(4)));
+typedef _Float16 fk_half2 __attribute__((ext_vector_type(2)));
+typedef float fk_float2v __attribute__((ext_vector_type(2)));
 
 template <uint32_t G>
 __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc,
                                                const uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                                                const uint32_t *__restrict__ slot, uint16_t *__restrict__ out,
                                                const fk_prefill_attend_params &p) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[32 * FK_ATT_KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vts[64 * FK_ATT_VROW];
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][FK_ATT_KB * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][FK_ATT_KB * 64];
   constexpr uint32_t nthreads = G * FK_WAVE;
-  constexpr uint32_t per = 256 / nthreads;   // staging units a thread
+  constexpr uint32_t per = FK_ATT_KB * 8 / nthreads;   // 16-byte units of K (and of V) a thread stages
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & (FK_WAVE - 1);
   const uint32_t wave = tid / FK_WAVE;
@@ -91,104 +115,167 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // Blocks with every key visible to every row of the block need no mask.
   const uint32_t win_lo = p.window && last_pos + 1 > p.window ? last_pos + 1 - p.window : 0;
   const size_t cache_base = ((size_t)sl * p.kv_heads + g) * p.length * 64;
-  for (uint32_t kb = first_pos / 32; kb * 32 <= last_pos; kb++) {
-    // The block's first key in the ring (a ring length is a multiple of 32,
-    // so the block does not wrap).
-    const uint32_t ring0 = (kb * 32) % p.length;
-    // Stage the block's K rows (unit u: key u div 8, d 8 (u mod 8) .. + 7,
-    // 16 bytes) and Vᵀ (item u: keys 2 (u div 16) and the next, d 4 (u mod
-    // 16) .. + 3: four dwords of two keys each); keys past the block's last
-    // query stay zero.
-    __syncthreads();
+
+  // Where lane l's transposed V reads start (see softmax_pv).
+  const uint32_t tq = lane & 15;
+  const uint32_t tr_key = 4 * (lane / 32) + tq / 4;
+  const uint32_t tr_d = 16 * ((lane / 16) & 1) + 4 * (tq & 3);
+
+  // A block's K (or V) rows into registers (unit u: key u div 8, d 8 (u mod
+  // 8) .. + 7, 16 bytes), keys past the block's last query zero (the ring
+  // length is a multiple of 64, so a block does not wrap); then into an LDS
+  // buffer, bf16 caches converted on the way (a uniform branch, so that f16
+  // caches pay nothing for it).
+  uint4 kreg[per], vreg[per];
+  auto fetch = [&](uint4 (&reg)[per], const uint16_t *__restrict__ cache, uint32_t kb) {
+    const uint32_t ring0 = (kb * FK_ATT_KB) % p.length;
 #pragma unroll
     for (uint32_t e = 0; e < per; e++) {
       const uint32_t u = tid + e * nthreads;
       const uint32_t key = u / 8, c8 = (u % 8) * 8;
-      uint4 kv = make_uint4(0, 0, 0, 0);
-      if (kb * 32 + key <= last_pos) kv = *reinterpret_cast<const uint4 *>(kc + cache_base + (size_t)(ring0 + key) * 64 + c8);
-      if (bf16)
-        kv = make_uint4(fk::bf16x2_to_f16x2(kv.x), fk::bf16x2_to_f16x2(kv.y), fk::bf16x2_to_f16x2(kv.z),
-                        fk::bf16x2_to_f16x2(kv.w));
-      *reinterpret_cast<uint4 *>(ks + key * FK_ATT_KROW + c8) = kv;
-      const uint32_t k2 = 2 * (u / 16), d4 = 4 * (u % 16);
-      uint2 va = make_uint2(0, 0), vb = make_uint2(0, 0);
-      if (kb * 32 + k2 <= last_pos) va = *reinterpret_cast<const uint2 *>(vc + cache_base + (size_t)(ring0 + k2) * 64 + d4);
-      if (kb * 32 + k2 + 1 <= last_pos)
-        vb = *reinterpret_cast<const uint2 *>(vc + cache_base + (size_t)(ring0 + k2 + 1) * 64 + d4);
-      if (bf16) {
-        va = make_uint2(fk::bf16x2_to_f16x2(va.x), fk::bf16x2_to_f16x2(va.y));
-        vb = make_uint2(fk::bf16x2_to_f16x2(vb.x), fk::bf16x2_to_f16x2(vb.y));
-      }
-      uint32_t *vt = reinterpret_cast<uint32_t *>(vts);
-      vt[((d4 + 0) * FK_ATT_VROW + k2) / 2] = (va.x & 0xffffu) | (vb.x << 16);
-      vt[((d4 + 1) * FK_ATT_VROW + k2) / 2] = (va.x >> 16) | (vb.x & 0xffff0000u);
-      vt[((d4 + 2) * FK_ATT_VROW + k2) / 2] = (va.y & 0xffffu) | (vb.y << 16);
-      vt[((d4 + 3) * FK_ATT_VROW + k2) / 2] = (va.y >> 16) | (vb.y & 0xffff0000u);
+      const bool live = kb * FK_ATT_KB + key <= last_pos;
+      reg[e] = live ? *reinterpret_cast<const uint4 *>(cache + cache_base + (size_t)(ring0 + key) * 64 + c8)
+                    : make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();
+  };
+  auto stash_k = [&](uint32_t buf) {
+    if (bf16) {
+#pragma unroll
+      for (uint32_t e = 0; e < per; e++) kreg[e] = fk::bf16x8_to_f16x8(kreg[e]);
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < per; e++) {
+      const uint32_t u = tid + e * nthreads;
+      *reinterpret_cast<uint4 *>(&ks[buf][fk_att_kplace(u / 8, (u % 8) * 8)]) = kreg[e];
+    }
+  };
+  auto stash_v = [&](uint32_t buf) {
+    if (bf16) {
+#pragma unroll
+      for (uint32_t e = 0; e < per; e++) vreg[e] = fk::bf16x8_to_f16x8(vreg[e]);
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < per; e++) {
+      const uint32_t u = tid + e * nthreads;
+      *reinterpret_cast<uint4 *>(&vs[buf][fk_att_vplace(u / 8, (u % 8) * 8)]) = vreg[e];
+    }
+  };
 
-    // Sᵀ = K Qᵀ: 4 chunks of 16 d.  A = K: lane l holds K[key l mod 32][16 c + 8 (l div 32) .. + 7].
-    fk_float16v s;
+  // A block: its scores, the online softmax and Oᵀ += Vᵀ Pᵀ, from K and V
+  // buffer buf.  mref is each row's reference maximum in log2 units (score ·
+  // scale · log2 e): it moves only when a block's maximum passes it by more
+  // than 8, so that Oᵀ and the sum are rescaled rarely; the probabilities
+  // exp2(score · c - mref) are then at most 2^8, which f16 holds with its
+  // full relative precision, and O / sum does not depend on the reference.
+  // A row that has seen no key yet keeps nothing: its reference and every
+  // score are -inf, and with mc = 0 each exp2 is exp2(-inf) = 0.
+  auto step = [&](uint32_t kb, uint32_t buf) {
+    // Sᵀ = K Qᵀ: two halves of 32 keys, 4 chunks of 16 d each.  A = K: lane
+    // l holds K[key 32 sb + l mod 32][16 c + 8 (l div 32) .. + 7].
+    fk_float16v sc[2];
 #pragma unroll
-    for (int r = 0; r < 16; r++) s[r] = 0.0f;
+    for (int sb = 0; sb < 2; sb++) {
 #pragma unroll
-    for (int k4 = 0; k4 < 4; k4++) {
-      fk::Half8 kf;
-      kf.u = *reinterpret_cast<const uint4 *>(ks + (lane % 32) * FK_ATT_KROW + 16 * k4 + 8 * (lane / 32));
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf.h, qf[k4].h, s, 0, 0, 0);
-    }
-    // Register 4 gg + r: key kb 32 + 8 gg + 4 (l div 32) + r of query qpos.
-    // The mask where the block crosses the causal edge or the window's start.
-    if (kb * 32 + 31 > p0 || kb * 32 < win_lo) {
+      for (int r = 0; r < 16; r++) sc[sb][r] = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t kp = kb * 32 + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-        s[r] = kp <= qpos && kp >= qfirst ? s[r] : -__builtin_inff();
+      for (int k4 = 0; k4 < 4; k4++) {
+        fk::Half8 kf;
+        kf.u = *reinterpret_cast<const uint4 *>(&ks[buf][fk_att_kplace(32 * sb + lane % 32, 16 * k4 + 8 * (lane / 32))]);
+        sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf.h, qf[k4].h, sc[sb], 0, 0, 0);
       }
     }
-    float mblk = s[0];
+    // Register 4 gg + r of half sb: key 32 sb + 8 gg + 4 (l div 32) + r of
+    // the block, of query qpos.  The mask where the block crosses the causal
+    // edge or the window's start.
+    if (kb * FK_ATT_KB + FK_ATT_KB - 1 > p0 || kb * FK_ATT_KB < win_lo) {
 #pragma unroll
-    for (int r = 1; r < 16; r++) mblk = fmaxf(mblk, s[r]);
-    mblk = fmaxf(mblk, __shfl_xor(mblk, 32));
-    const float mnew = fmaxf(mrun, mblk);
-    // A row that has seen no key yet keeps nothing (its maximum is -inf).
-    const bool none = mnew == -__builtin_inff();
-    const float mc = none ? 0.0f : mnew * c;
-    float psum = 0.0f;
-    fk::Half8 pf[2];   // Pᵀ chunks (B of Oᵀ += Vᵀ Pᵀ): registers 8 k2 .. 8 k2 + 7
+      for (int sb = 0; sb < 2; sb++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float e = none ? 0.0f : __builtin_amdgcn_exp2f(fmaf(s[r], c, -mc));
-      psum += e;
-      pf[r / 8].h[r % 8] = (_Float16)e;
+        for (int r = 0; r < 16; r++) {
+          const uint32_t kp = kb * FK_ATT_KB + 32 * sb + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+          sc[sb][r] = kp <= qpos && kp >= qfirst ? sc[sb][r] : -__builtin_inff();
+        }
     }
-    psum += __shfl_xor(psum, 32);
-    // Rescale what the rows have so far only when some maximum moved.
-    if (__any(mnew != mrun)) {
-      const float alpha = none || mrun == -__builtin_inff() ? (none ? 1.0f : 0.0f)
-                                                            : __builtin_amdgcn_exp2f(mrun * c - mc);
+    // The block's maximum of each row: three-way maxima down the 32 scores.
+    float mblk = __builtin_fmaxf(__builtin_fmaxf(sc[0][0], sc[1][0]), sc[0][1]);
+#pragma unroll
+    for (int r = 1; r < 16; r++)
+      mblk = __builtin_fmaxf(__builtin_fmaxf(mblk, sc[1][r]), r + 1 < 16 ? sc[0][r + 1] : sc[1][r]);
+    mblk = __builtin_fmaxf(mblk, __shfl_xor(mblk, 32)) * c;
+    const bool passed = mblk > mrun + 8.0f;
+    if (__any(passed)) {
+      const float mnew = passed ? mblk : mrun;
+      const float alpha = mnew == mrun ? 1.0f : __builtin_amdgcn_exp2f(mrun - mnew);
       lrun *= alpha;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         o[0][r] *= alpha;
         o[1][r] *= alpha;
       }
+      mrun = mnew;
     }
-    lrun += psum;
-    mrun = mnew;
-    // Oᵀ += Vᵀ Pᵀ.  Chunk k2's k index 8 (l div 32) + e is key 16 k2 + 8 (e div 4)
-    // + 4 (l div 32) + e mod 4 (the scores' register order); A = Vᵀ: lane l
-    // holds V[those keys][d = 32 db + l mod 32], two runs of 4 keys.
+    const float mc = mrun == -__builtin_inff() ? 0.0f : mrun;
+
+    // Pᵀ chunk 2 sb + k2 (B of Oᵀ += Vᵀ Pᵀ): registers 8 k2 .. 8 k2 + 7 of
+    // half sb, converted in pairs; the row's sum taken from those same f16
+    // pairs, as the matrix operation takes them.
+    fk::Half8 pf[4];
+    float psum = 0.0f;
+    const fk_half2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float e0 = __builtin_amdgcn_exp2f(fmaf(sc[sb][r], c, -mc));
+        const float e1 = __builtin_amdgcn_exp2f(fmaf(sc[sb][r + 1], c, -mc));
+        const fk_half2 pair = __builtin_convertvector((fk_float2v){e0, e1}, fk_half2);
+        reinterpret_cast<fk_half2 *>(&pf[2 * sb + r / 8])[(r % 8) / 2] = pair;
+        psum = __builtin_amdgcn_fdot2(pair, ones, psum, false);
+      }
+    lrun += psum + __shfl_xor(psum, 32);
+    // Oᵀ += Vᵀ Pᵀ, chunk by chunk.  Transposed V reads: within each 16
+    // lanes, lane 4 k + q reads key K0 + k, d D0 + 4 q .. + 3 and receives
+    // keys K0 .. K0 + 3 of d D0 + (its index in the 16); for chunk (sb, k2)
+    // lane l wants d 32 db + l mod 32 and keys 32 sb + 16 k2 + 8 t + 4 (l div
+    // 32) + 0 .. 3 (t = 0, 1): the scores' register order, which Pᵀ keeps.
 #pragma unroll
     for (int db = 0; db < 2; db++)
 #pragma unroll
-      for (int k2 = 0; k2 < 2; k2++) {
-        const uint32_t *vrow = reinterpret_cast<const uint32_t *>(vts) +
-                               ((32 * db + lane % 32) * FK_ATT_VROW + 16 * k2 + 4 * (lane / 32)) / 2;
+      for (int q = 0; q < 4; q++) {
+        const uint32_t key0 = 32 * (q / 2) + 16 * (q % 2) + tr_key;
+        const fk_short4 t0 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((FK_ATT_LDS fk_short4 *)&vs[buf][fk_att_vplace(key0, 32 * db + tr_d)]);
+        const fk_short4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (FK_ATT_LDS fk_short4 *)&vs[buf][fk_att_vplace(key0 + 8, 32 * db + tr_d)]);
+        const uint2 w0 = __builtin_bit_cast(uint2, t0), w1 = __builtin_bit_cast(uint2, t1);
         fk::Half8 vf;
-        vf.u = make_uint4(vrow[0], vrow[1], vrow[4], vrow[5]);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf.h, pf[k2].h, o[db], 0, 0, 0);
+        vf.u = make_uint4(w0.x, w0.y, w1.x, w1.y);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf.h, pf[q].h, o[db], 0, 0, 0);
       }
+  };
+
+  // The loop: while block kb is multiplied from one pair of LDS buffers,
+  // block kb + 1's K and V rows are on their way from the caches into
+  // registers, and go into the other pair after (every wavefront left it at
+  // the last barrier); one barrier a block.
+  const uint32_t kb0 = first_pos / FK_ATT_KB, kb_last = last_pos / FK_ATT_KB;
+  fetch(kreg, kc, kb0);
+  fetch(vreg, vc, kb0);
+  stash_k(0);
+  stash_v(0);
+  __syncthreads();
+  for (uint32_t kb = kb0; kb <= kb_last; kb++) {
+    const uint32_t buf = (kb - kb0) & 1;
+    if (kb < kb_last) {
+      fetch(kreg, kc, kb + 1);
+      fetch(vreg, vc, kb + 1);
+    }
+    step(kb, buf);
+    if (kb < kb_last) {
+      stash_k(buf ^ 1);
+      stash_v(buf ^ 1);
+    }
+    __syncthreads();
   }
 
   // O = Oᵀ / sum into the tile layout: lane l's query row, d = 32 db + 8 gg +
@@ -207,7 +294,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
 
 // One entry a group size G = heads / kv_heads (threads 64 G).
 #define FK_PREFILL_ATTEND(G)                                                                                    \
-  extern "C" __global__ void __launch_bounds__(64 * G) fk_prefill_attend_g##G(                                  \
+  extern "C" __global__ void __launch_bounds__(64 * G) fk_prefill_attend_g##G(                         \
       const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,       \
       const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot, uint16_t *__restrict__ out,   \
       fk_prefill_attend_params p) {                                                                             \

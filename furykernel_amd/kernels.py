@@ -219,6 +219,10 @@ STEP_GEMV_ENTRIES = tuple(f"{shape}_p{pro}_e{epi}" for shape, pairs in STEP_GEMV
 STEP_GEMV_BUFFERS = ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
                      "res_token", "epi_out", "arg")
 
+# Keys a block of the prefill attention stages (fk_attend.h): ring lengths are
+# multiples of it.
+ATTEND_KEYS = 64
+
 # Row widths the one-pass RMSNorm-to-tiles holds in registers (fk_prefill.h).
 NORM_PACK_HELD = (512, 1024, 2048, 4096)
 
@@ -397,8 +401,8 @@ class Kernels:
         entry = f"fk_prefill_attend_g{heads // kv_heads if kv_heads and heads % kv_heads == 0 else 0}"
         if rows <= 0 or rows % 256 or kv_heads <= 0 or heads % kv_heads or heads // kv_heads not in (1, 2, 4):
             raise LaunchError(f"{entry}: {rows} rows, {heads} heads over {kv_heads}")
-        if length <= 0 or length % 32:
-            raise LaunchError(f"{entry}: a ring of {length}; keys go by blocks of 32 that must not wrap")
+        if length <= 0 or length % ATTEND_KEYS:
+            raise LaunchError(f"{entry}: a ring of {length}; keys go by blocks of {ATTEND_KEYS} that must not wrap")
         if positions is not None:
             from .prefill import check_rows
             check_rows(positions, seqs)

@@ -35,7 +35,7 @@ from typing import Optional
 
 import numpy as np
 
-from .kernels import NORM_PACK_HELD
+from .kernels import ATTEND_KEYS, NORM_PACK_HELD
 from .layout import SLAB, pack, pair
 from .lower import Launch, Lowered, LoweringError, rope_table
 from .program.check import CheckedProgram
@@ -374,9 +374,9 @@ class _Prefill:
         vname, vlay, vbf = self.cache(op.to.values)
         if klay != vlay or kbf != vbf or klay.kv_heads != spec.kv_heads or klay.head_dim != HEAD_DIM:
             raise LoweringError(f"{step.name}: key and value caches of different layouts")
-        if klay.length % QBLOCK:
+        if klay.length % ATTEND_KEYS:
             raise LoweringError(f"{step.name}: a ring of {klay.length}; the prefill attention reads keys by "
-                                f"blocks of {QBLOCK} that must not wrap")
+                                f"blocks of {ATTEND_KEYS} that must not wrap")
         stores = {}
         for n in self.pending:
             at = n.op.at
