@@ -57,7 +57,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="queue each step's launches on the stream instead of replaying a HIP graph")
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "kernels"), default="decode",
                     help="decode (the headline metric) or the 1B prefill of 4 x 2048 rows")
     ap.add_argument("--calibrate", action="store_true",
                     help="only read and write 1 GiB with the streaming kernels (the known sizes that scale the "
@@ -359,6 +359,159 @@ def main_prefill(args) -> int:
     return 0
 
 
+KERNELS_METRIC = "standalone kernels: achieved HBM GB/s (% of ~8 TB/s), 1 GPU"
+COPY_BYTES = 512 << 20   # inputs a kernel's launches cycle through: twice the 256 MB memory-side cache
+
+
+def main_kernels(args) -> int:
+    """The standalone kernels at their configurations' sizes: f32 matvec
+    W[4096 × 4096]·x, RMSNorm and row softmax over [64 × 4096] f32, and the
+    int8 weight-only matvec W[8192 × 8192] with per-row f32 scales and f16 x.
+    Each launch of a kernel reads its own copy of the inputs — 512 MB of
+    copies, twice the memory-side cache, so that every launch reads HBM —
+    and the launches run back to back in one HIP graph, timed with HIP
+    events on its stream: the average launch, gaps between dispatches
+    included.  Algorithmic bytes: every input element read once and every
+    output written once.  The CPU baseline: the oracle's C GEMV (the
+    reference GEMV's order, one thread) on the f32 matvec."""
+    import numpy as np
+
+    from furykernel_amd import kernels, runtime
+
+    dev = runtime.Device(0)
+    ks = kernels.Kernels(dev)
+
+    def normal(buf, seed, f16):
+        cnt = buf.size // (2 if f16 else 4)
+        ks.launch("fk_init_normal", min(max(cnt // 256, 1), 65536), 256, {"dst": buf.ptr},
+                  kernels.InitNormalParams(cnt, seed, 1.0, 1 if f16 else 0))
+
+    def timed(launches: list, reps: int) -> float:
+        with dev.capture() as g:
+            for run in launches:
+                run()
+        graph = g[0]
+        graph.replay()
+        dev.sync()
+        start, end = dev.event(), dev.event()
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        end.synchronize()
+        graph.destroy()
+        return start.elapsed_ms(end) * 1e3 / (reps * len(launches))
+
+    table = {}
+    bufs = []
+
+    def copies_of(nbytes: int) -> int:
+        return max(2, -(-COPY_BYTES // nbytes))
+
+    # f32 matvec 4096 × 4096: the variant of rows a wavefront with the best rate.
+    n = k = 4096
+    cw = copies_of(n * k * 4)
+    ws = [dev.alloc(n * k * 4) for _ in range(cw)]
+    x, y = dev.alloc(k * 4), dev.alloc(n * 4)
+    for i, w in enumerate(ws):
+        normal(w, 100 + i, False)
+    normal(x, 99, False)
+    bufs += ws + [x, y]
+    nbytes = n * k * 4 + k * 4 + n * 4
+    best = None
+    for r in (1, 2, 4):
+        us = timed([lambda w=w, r=r: ks.gemv(w, x, y, n, k, "f32", rows_per_wave=r) for w in ws], 20)
+        log(f"fk_gemv_f32_f32_r{r} 4096 x 4096: {us:.2f} us a launch, {nbytes / us / 1e3:.1f} GB/s")
+        if best is None or us < best[1]:
+            best = (f"fk_gemv_f32_f32_r{r}", us)
+    table["matvec_f32_4096x4096"] = {"kernel": best[0], "avg_us": round(best[1], 3), "bytes": nbytes,
+                                     "gbps": round(nbytes / best[1] / 1e3, 1),
+                                     "frac": round(nbytes / best[1] / 1e3 / HBM_PEAK_GBPS, 4)}
+
+    # RMSNorm and softmax over 64 × 4096 f32.
+    rows, width = 64, 4096
+    cr = copies_of(rows * width * 4)
+    xs = [dev.alloc(rows * width * 4) for _ in range(cr)]
+    gamma, out = dev.alloc(width * 4), dev.alloc(rows * width * 4)
+    for i, b in enumerate(xs):
+        normal(b, 300 + i, False)
+    normal(gamma, 298, False)
+    bufs += xs + [gamma, out]
+    for name, entry, run, nb in (
+            ("rmsnorm_64x4096", "fk_rmsnorm_f32", lambda b: ks.rmsnorm(b, gamma, out, rows, width),
+             2 * rows * width * 4 + width * 4),
+            ("softmax_64x4096", "fk_softmax_f32", lambda b: ks.softmax(b, out, rows, width), 2 * rows * width * 4)):
+        us = timed([lambda b=b: run(b) for b in xs], 20)
+        log(f"{entry} 64 x 4096: {us:.2f} us a launch, {nb / us / 1e3:.1f} GB/s")
+        table[name] = {"kernel": entry, "avg_us": round(us, 3), "bytes": nb, "gbps": round(nb / us / 1e3, 1),
+                       "frac": round(nb / us / 1e3 / HBM_PEAK_GBPS, 4)}
+
+    # int8 weight-only matvec 8192 × 8192.
+    n = k = 8192
+    ci = copies_of(n * k)
+    wi = [dev.alloc(n * k) for _ in range(ci)]
+    scale, xh, yi = dev.alloc(n * 4), dev.alloc(k * 2), dev.alloc(n * 4)
+    for i, w in enumerate(wi):
+        ks.fill_u32(w, 0x05fb11ef ^ (i * 0x01010101), n * k // 4)
+    normal(scale, 297, False)
+    normal(xh, 296, True)
+    bufs += wi + [scale, xh, yi]
+    nbytes = n * k + n * 4 + k * 2 + n * 4
+    best = None
+    for r in (1, 2, 4):
+        us = timed([lambda w=w, r=r: ks.gemv(w, xh, yi, n, k, "i8", rows_per_wave=r, scale=scale) for w in wi], 20)
+        log(f"fk_gemv_i8_f16_r{r} 8192 x 8192: {us:.2f} us a launch, {nbytes / us / 1e3:.1f} GB/s")
+        if best is None or us < best[1]:
+            best = (f"fk_gemv_i8_f16_r{r}", us)
+    table["matvec_i8_8192x8192"] = {"kernel": best[0], "avg_us": round(best[1], 3), "bytes": nbytes,
+                                    "gbps": round(nbytes / best[1] / 1e3, 1),
+                                    "frac": round(nbytes / best[1] / 1e3 / HBM_PEAK_GBPS, 4)}
+    for b in bufs:
+        b.free()
+
+    head = table["matvec_f32_4096x4096"]
+    line = {
+        "metric": KERNELS_METRIC, "value": head["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": 20, "warmup": 1,
+        "ms_per_step": round(head["avg_us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: N(0, 1) matrices, vectors and rows generated on the device; int8 weights a fixed "
+                "byte pattern",
+        "config": {"workload": "standalone kernels: f32 matvec 4096 x 4096, RMSNorm and row softmax over 64 x 4096 "
+                               "f32, int8 weight-only matvec 8192 x 8192 (per-row scales, f16 x); each launch on "
+                               "its own copy of the inputs (512 MB of copies)"},
+        "roofline": {"kernel": head["kernel"], "bound": "hbm", "achieved": head["gbps"], "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": head["frac"], "traffic": None, "avg_launch_us": head["avg_us"],
+                     "bytes_per_launch": head["bytes"]},
+        "kernels": table,
+        "cpu_baseline": None if args.no_cpu_baseline else matvec_cpu_baseline(args.cpu_seconds),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def matvec_cpu_baseline(seconds: float) -> dict:
+    """The oracle's C GEMV (the reference GEMV's order at width 32, one
+    thread) on an f32 4096 × 4096 matvec, repeated for about `seconds`."""
+    import numpy as np
+
+    from oracle import fkref
+
+    rng = np.random.default_rng(1)
+    w = rng.uniform(-1, 1, (4096, 4096)).astype(np.float32)
+    x = rng.uniform(-1, 1, 4096).astype(np.float32)
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        fkref.gemv(w, x, 32, 4)
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    nbytes = w.nbytes + x.nbytes + 4096 * 4
+    return {"value": round(nbytes * runs / el / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"the oracle's C GEMV (oracle/fkref.c, width 32, pack 4) on the f32 4096 x 4096 matvec, "
+                      f"{runs} runs in {el:.1f} s"}
+
+
 def main() -> int:
     args = parse()
     if args.calibrate:
@@ -371,6 +524,8 @@ def main() -> int:
         return 2
     if args.workload == "prefill":
         return main_prefill(args)
+    if args.workload == "kernels":
+        return main_kernels(args)
 
     from furykernel_amd import kernels, runtime
     from furykernel_amd.decode import DecodeSession

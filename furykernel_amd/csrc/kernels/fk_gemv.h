@@ -86,6 +86,35 @@ __device__ __forceinline__ void unpack(const uint4 (&u)[P / 8], float (&out)[P],
   }
 }
 
+// One 16-byte word of W widened to f32 exactly: 4 f32, 8 f16 or 16 int8.
+template <int P>
+__device__ __forceinline__ void unpack_w(const uint4 &u, float (&out)[P], float) {
+  static_assert(P == 4, "four f32 a word");
+  out[0] = __uint_as_float(u.x);
+  out[1] = __uint_as_float(u.y);
+  out[2] = __uint_as_float(u.z);
+  out[3] = __uint_as_float(u.w);
+}
+
+template <int P>
+__device__ __forceinline__ void unpack_w(const uint4 &u, float (&out)[P], _Float16) {
+  static_assert(P == 8, "eight f16 a word");
+  const uint32_t words[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int h = 0; h < 4; h++) {
+    out[2 * h] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] & 0xFFFFu));
+    out[2 * h + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] >> 16));
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void unpack_w(const uint4 &u, float (&out)[P], int8_t) {
+  static_assert(P == 16, "sixteen int8 a word");
+  const uint32_t words[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int b = 0; b < 16; b++) out[b] = (float)(int8_t)(words[b / 4] >> (8 * (b % 4)));
+}
+
 // R rows of y = W x (times a per-row scale if given) by one wavefront.
 template <typename WT, typename XT, int P, int R>
 __device__ __forceinline__ void gemv_wave(const WT *__restrict__ w, const XT *__restrict__ x, const float *__restrict__ scale,
@@ -132,38 +161,122 @@ __device__ __forceinline__ void gemv_wave(const WT *__restrict__ w, const XT *__
   }
 }
 
+// The same rows and order with every load in flight at once, for rows of at
+// most 64 KPL packs: each lane issues all of its packs' 16-byte loads — W's
+// first, then x's, the indices clamped into the row so every load is
+// unconditional and the compiler keeps them all outstanding — and only then
+// computes, packs past the row skipped.  One round trip to memory a
+// wavefront, where the loop above waits for each unrolled group of packs in
+// turn.  FULL: the row fills every lane's KPL packs (k = 64 KPL P), so no
+// pack needs the check.
+template <typename WT, typename XT, int P, int R, int KPL, bool FULL>
+__device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, const XT *__restrict__ x,
+                                                   const float *__restrict__ scale, float *__restrict__ y,
+                                                   uint32_t n, uint32_t k, uint32_t row0) {
+  constexpr int C = P / 4;
+  constexpr int XW = P * (int)sizeof(XT) / 16;  // 16-byte words of an x pack
+  static_assert(P * sizeof(WT) == 16, "a W pack is one 16-byte load");
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+  const uint32_t packs = k / P;
+  const WT *wr[R];
+#pragma unroll
+  for (int q = 0; q < R; q++) wr[q] = w + (size_t)min(row0 + q, n - 1) * k;
+  uint4 wv[R][KPL], xv[KPL][XW];
+#pragma unroll
+  for (int it = 0; it < KPL; it++) {
+    const uint32_t jc = min(lane + FK_WAVE * (uint32_t)it, packs - 1);
+#pragma unroll
+    for (int q = 0; q < R; q++) wv[q][it] = *reinterpret_cast<const uint4 *>(wr[q] + (size_t)jc * P);
+  }
+#pragma unroll
+  for (int it = 0; it < KPL; it++) {
+    const uint32_t jc = min(lane + FK_WAVE * (uint32_t)it, packs - 1);
+#pragma unroll
+    for (int u = 0; u < XW; u++) xv[it][u] = reinterpret_cast<const uint4 *>(x + (size_t)jc * P)[u];
+  }
+  float acc[R][C];
+#pragma unroll
+  for (int q = 0; q < R; q++)
+#pragma unroll
+    for (int c = 0; c < C; c++) acc[q][c] = 0.0f;
+#pragma unroll
+  for (int it = 0; it < KPL; it++) {
+    // A pack past the row is computed from the clamped loads and not added:
+    // a select, so that no load sits in a branch.
+    const bool live = lane + FK_WAVE * (uint32_t)it < packs;
+    float xf[P];
+    unpack<P>(xv[it], xf, XT{});
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      float wf[P];
+      unpack_w<P>(wv[q][it], wf, WT{});
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        float p0 = xf[4 * c] * wf[4 * c];
+        float p1 = xf[4 * c + 1] * wf[4 * c + 1];
+        float p2 = xf[4 * c + 2] * wf[4 * c + 2];
+        float p3 = xf[4 * c + 3] * wf[4 * c + 3];
+        const float sum = acc[q][c] + ((p0 + p1) + (p2 + p3));
+        acc[q][c] = FULL || live ? sum : acc[q][c];
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < R; q++) {
+    float t = acc[q][0];
+#pragma unroll
+    for (int c = 1; c < C; c++) t = t + acc[q][c];
+    t = wave_sum(t);
+    const uint32_t row = row0 + q;
+    if (lane == 0 && row < n) y[row] = scale ? t * scale[row] : t;
+  }
+}
+
 }  // namespace fk
 
-// Entry points: a threadgroup of W wavefronts takes W * R consecutive rows.
+// Entry points: a threadgroup of W wavefronts takes W * R consecutive rows;
+// rows of at most 64 KPL packs take the all-in-flight form.
 // Kernargs: the buffers in binding order, then the parameter struct.
 struct fk_gemv_params {
   uint32_t n;  // rows of W (outputs)
   uint32_t k;  // columns of W (inputs), a multiple of the pack
 };
 
-#define FK_GEMV_ENTRY(NAME, WT, XT, P, R)                                                                      \
+#define FK_GEMV_ENTRY(NAME, WT, XT, P, R, KPL)                                                                 \
   extern "C" __global__ void __launch_bounds__(256) NAME(const WT *__restrict__ w, const XT *__restrict__ x, \
                                                          float *__restrict__ y, fk_gemv_params p) {         \
     const uint32_t row0 = (blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * (R);             \
     if (row0 >= p.n) return;                                                                                 \
-    fk::gemv_wave<WT, XT, P, R>(w, x, nullptr, y, p.n, p.k, row0);                                           \
+    if (p.k / (P) == FK_WAVE * (KPL))                                                                        \
+      fk::gemv_wave_inflight<WT, XT, P, R, KPL, true>(w, x, nullptr, y, p.n, p.k, row0);                    \
+    else if (p.k / (P) < FK_WAVE * (KPL))                                                                    \
+      fk::gemv_wave_inflight<WT, XT, P, R, KPL, false>(w, x, nullptr, y, p.n, p.k, row0);                   \
+    else                                                                                                     \
+      fk::gemv_wave<WT, XT, P, R>(w, x, nullptr, y, p.n, p.k, row0);                                         \
   }
 
-#define FK_GEMV_SCALED_ENTRY(NAME, WT, XT, P, R)                                                           \
+#define FK_GEMV_SCALED_ENTRY(NAME, WT, XT, P, R, KPL)                                                      \
   extern "C" __global__ void __launch_bounds__(256)                                                        \
       NAME(const WT *__restrict__ w, const float *__restrict__ scale, const XT *__restrict__ x,            \
            float *__restrict__ y, fk_gemv_params p) {                                                      \
     const uint32_t row0 = (blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * (R);           \
     if (row0 >= p.n) return;                                                                               \
-    fk::gemv_wave<WT, XT, P, R>(w, x, scale, y, p.n, p.k, row0);                                           \
+    if (p.k / (P) == FK_WAVE * (KPL))                                                                      \
+      fk::gemv_wave_inflight<WT, XT, P, R, KPL, true>(w, x, scale, y, p.n, p.k, row0);                    \
+    else if (p.k / (P) < FK_WAVE * (KPL))                                                                  \
+      fk::gemv_wave_inflight<WT, XT, P, R, KPL, false>(w, x, scale, y, p.n, p.k, row0);                   \
+    else                                                                                                   \
+      fk::gemv_wave<WT, XT, P, R>(w, x, scale, y, p.n, p.k, row0);                                         \
   }
 
-FK_GEMV_ENTRY(fk_gemv_f32_f32_r1, float, float, 4, 1)
-FK_GEMV_ENTRY(fk_gemv_f32_f32_r2, float, float, 4, 2)
-FK_GEMV_ENTRY(fk_gemv_f32_f32_r4, float, float, 4, 4)
-FK_GEMV_ENTRY(fk_gemv_f16_f32_r1, _Float16, float, 8, 1)
-FK_GEMV_ENTRY(fk_gemv_f16_f32_r2, _Float16, float, 8, 2)
-FK_GEMV_ENTRY(fk_gemv_f16_f32_r4, _Float16, float, 8, 4)
-FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r1, int8_t, _Float16, 16, 1)
-FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r2, int8_t, _Float16, 16, 2)
-FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r4, int8_t, _Float16, 16, 4)
+// Packs a lane holds in flight: rows of 4096 f32, 4096 f16 (by one row or
+// two) and 8192 int8; wider rows take the loop.
+FK_GEMV_ENTRY(fk_gemv_f32_f32_r1, float, float, 4, 1, 16)
+FK_GEMV_ENTRY(fk_gemv_f32_f32_r2, float, float, 4, 2, 16)
+FK_GEMV_ENTRY(fk_gemv_f32_f32_r4, float, float, 4, 4, 4)
+FK_GEMV_ENTRY(fk_gemv_f16_f32_r1, _Float16, float, 8, 1, 8)
+FK_GEMV_ENTRY(fk_gemv_f16_f32_r2, _Float16, float, 8, 2, 8)
+FK_GEMV_ENTRY(fk_gemv_f16_f32_r4, _Float16, float, 8, 4, 4)
+FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r1, int8_t, _Float16, 16, 1, 8)
+FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r2, int8_t, _Float16, 16, 2, 8)
+FK_GEMV_SCALED_ENTRY(fk_gemv_i8_f16_r4, int8_t, _Float16, 16, 4, 4)
