@@ -371,7 +371,8 @@ def main_kernels(args) -> int:
     copies, twice the memory-side cache, so that every launch reads HBM —
     and the launches run back to back in one HIP graph, timed with HIP
     events on its stream: the average launch, gaps between dispatches
-    included.  Algorithmic bytes: every input element read once and every
+    included (with --eager the launches are queued one by one instead, so
+    the average also holds each launch's host cost).  Algorithmic bytes: every input element read once and every
     output written once.  The CPU baseline: the oracle's C GEMV (the
     reference GEMV's order, one thread) on the f32 matvec."""
     import numpy as np
@@ -387,19 +388,26 @@ def main_kernels(args) -> int:
                   kernels.InitNormalParams(cnt, seed, 1.0, 1 if f16 else 0))
 
     def timed(launches: list, reps: int) -> float:
-        with dev.capture() as g:
-            for run in launches:
-                run()
-        graph = g[0]
-        graph.replay()
+        if args.eager:   # queued one by one, each launch a dispatch of its own in a kernel trace
+            def replay():
+                for run in launches:
+                    run()
+            finish = None
+        else:
+            with dev.capture() as g:
+                for run in launches:
+                    run()
+            replay, finish = g[0].replay, g[0].destroy
+        replay()
         dev.sync()
         start, end = dev.event(), dev.event()
         start.record()
         for _ in range(reps):
-            graph.replay()
+            replay()
         end.record()
         end.synchronize()
-        graph.destroy()
+        if finish is not None:
+            finish()
         return start.elapsed_ms(end) * 1e3 / (reps * len(launches))
 
     table = {}
