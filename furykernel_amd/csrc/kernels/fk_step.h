@@ -123,7 +123,8 @@ struct AttendLds {
 // binary64's rounded once.  The weights' sum and the weighted sum of the
 // values over 8 runs of split/8 positions (wavefront w's run w), each in
 // order of position from +0, then the runs' sums in order.  Stored as
-// partials: per (head, split) [max, sum, acc[head_dim]].
+// partials: acc[heads][splits][head_dim], then [heads][splits][max, sum] —
+// each (head, split)'s values 16-byte aligned for a consumer's vector loads.
 template <uint32_t G, uint32_t D, uint32_t S, int CB>
 __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restrict__ q,
                                              const float *__restrict__ knew, const float *__restrict__ vnew,
@@ -344,12 +345,13 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
         lt = lt + sh.pl[w * FK_ATTN_MAX_GROUP + h];
         at = at + pacc[(w * FK_ATTN_MAX_GROUP + h) * FK_ATTN_MAX_DIM + i];
       }
-      float *o = partials + ((size_t)(g * group + h) * p.splits + t) * (d + 2);
+      const size_t ht = (size_t)(g * group + h) * p.splits + t;
       if (i == 0) {
+        float *o = partials + (size_t)p.heads * p.splits * d + 2 * ht;
         o[0] = split > FK_WAVE ? max_number(sh.pm[h * 2], sh.pm[h * 2 + 1]) : sh.pm[h * 2];
         o[1] = lt;
       }
-      o[2 + i] = at;
+      partials[ht * d + i] = at;
     }
   }
 }
@@ -381,49 +383,81 @@ struct fk_step_combine_params {
 // (exact whatever the order), the splits' weights w_t = exp(max_t - M),
 // binary64's rounded once, then lane i: out_i = (sum_t acc_t[i] w_t) /
 // (sum_t l_t w_t), both sums in split order from +0.  Every load of a chunk of
-// 64 splits is issued before any is used — the maxima and weight sums by lane
-// t, the values acc_t[i] by lane i — so a chunk costs one round trip to memory;
-// lane t makes split t's weight and l_t w_t, which the sums read by lane.
+// up to 64 splits is issued before any is used — the maxima and weight sums by
+// lane t, the values acc_t[i] by lane i — so a chunk costs one round trip to
+// memory; lane t makes split t's weight and l_t w_t and puts them in LDS,
+// where the sums read them four at a time.
+// The partials as the attention stores them: acc[heads][splits][head_dim],
+// then [heads][splits][max, sum].
 #define FK_COMBINE_CHUNK 64
-extern "C" __global__ void __launch_bounds__(FK_WAVE)
-    fk_step_combine(const float *__restrict__ partials, float *__restrict__ out, fk_step_combine_params p) {
-  const uint32_t h = blockIdx.x;
+
+namespace fk {
+
+// One chunk of CH >= splits: every load first, each index clamped into the
+// partials so that the compiler keeps them all in flight together.
+template <int CH>
+__device__ __forceinline__ void combine_chunk(const float *__restrict__ ph, const float *__restrict__ st,
+                                              float *__restrict__ out, uint32_t head_dim, uint32_t splits,
+                                              float *sw, float *slw) {
   const uint32_t lane = threadIdx.x;
-  const uint32_t stride = p.head_dim + 2;
-  const float *ph = partials + (size_t)h * p.splits * stride;
-  if (p.splits <= FK_COMBINE_CHUNK && p.head_dim <= FK_WAVE) {
-    // One chunk: every load first.
-    // Every load unconditional, its index clamped into the partials, so the
-    // compiler keeps them all in flight together.
-    const uint32_t i = lane;
-    const uint32_t ic = min(i, p.head_dim - 1);
-    const uint32_t tc = min(lane, p.splits - 1);
-    float mt = ph[(size_t)tc * stride];
-    const float lt = ph[(size_t)tc * stride + 1];
-    float av[FK_COMBINE_CHUNK];
+  const uint32_t ic = min(lane, head_dim - 1);
+  const uint32_t tc = min(lane, splits - 1);
+  float mt = st[(size_t)tc * 2];
+  const float lt = st[(size_t)tc * 2 + 1];
+  float av[CH];
 #pragma unroll
-    for (int j = 0; j < FK_COMBINE_CHUNK; j++) av[j] = ph[(size_t)min((uint32_t)j, p.splits - 1) * stride + 2 + ic];
-    if (lane >= p.splits) mt = -__builtin_inff();
-    const float top = fk::wave_max(mt);
-    float wt = 0.0f, lw = 0.0f;
-    if (lane < p.splits) {
-      wt = fk::exp_once(mt - top);
-      lw = lt * wt;
-    }
-    float l = 0.0f;
-    float acc = 0.0f;
+  for (int j = 0; j < CH; j++) av[j] = ph[(size_t)min((uint32_t)j, splits - 1) * head_dim + ic];
+  if (lane >= splits) mt = -__builtin_inff();
+  const float top = wave_max(mt);
+  float wt = 0.0f, lw = 0.0f;
+  if (lane < splits) {
+    wt = exp_once(mt - top);
+    lw = lt * wt;
+  }
+  sw[lane] = wt;
+  slw[lane] = lw;
+  __syncthreads();
+  float l = 0.0f;
+  float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < FK_COMBINE_CHUNK; j++) {
-      if ((uint32_t)j < p.splits) {
-        l = l + fk::readlane_f(lw, j);
-        acc = acc + av[j] * fk::readlane_f(wt, j);
+  for (int j4 = 0; j4 < CH / 4; j4++) {
+    const float4 w4 = reinterpret_cast<const float4 *>(sw)[j4];
+    const float4 l4 = reinterpret_cast<const float4 *>(slw)[j4];
+    const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      if ((uint32_t)(4 * j4 + q) < splits) {
+        l = l + lv[q];
+        acc = acc + av[4 * j4 + q] * w[q];
       }
     }
-    if (i < p.head_dim) out[(size_t)h * p.head_dim + i] = acc / l;
+  }
+  if (lane < head_dim) out[lane] = acc / l;
+}
+
+}  // namespace fk
+
+extern "C" __global__ void __launch_bounds__(FK_WAVE)
+    fk_step_combine(const float *__restrict__ partials, float *__restrict__ out, fk_step_combine_params p) {
+  __shared__ float4 sw4[FK_COMBINE_CHUNK / 4], slw4[FK_COMBINE_CHUNK / 4];
+  const uint32_t h = blockIdx.x;
+  const uint32_t lane = threadIdx.x;
+  const uint32_t stride = p.head_dim;
+  const float *ph = partials + (size_t)h * p.splits * stride;
+  const float *st = partials + (size_t)p.heads * p.splits * stride + (size_t)h * p.splits * 2;
+  if (p.splits <= FK_COMBINE_CHUNK && p.head_dim <= FK_WAVE) {
+    float *o = out + (size_t)h * p.head_dim;
+    if (p.splits <= 32)
+      fk::combine_chunk<32>(ph, st, o, p.head_dim, p.splits, reinterpret_cast<float *>(sw4),
+                            reinterpret_cast<float *>(slw4));
+    else
+      fk::combine_chunk<64>(ph, st, o, p.head_dim, p.splits, reinterpret_cast<float *>(sw4),
+                            reinterpret_cast<float *>(slw4));
     return;
   }
   float m = -__builtin_inff();
-  for (uint32_t t = lane; t < p.splits; t += FK_WAVE) m = fk::max_number(m, ph[(size_t)t * stride]);
+  for (uint32_t t = lane; t < p.splits; t += FK_WAVE) m = fk::max_number(m, st[(size_t)t * 2]);
   const float top = fk::wave_max(m);
   for (uint32_t i0 = 0; i0 < p.head_dim; i0 += FK_WAVE) {
     const uint32_t i = i0 + lane;
@@ -433,23 +467,29 @@ extern "C" __global__ void __launch_bounds__(FK_WAVE)
       const uint32_t t = t0 + lane;
       float mt = 0.0f, lt = 0.0f;
       if (t < p.splits) {
-        mt = ph[(size_t)t * stride];
-        lt = ph[(size_t)t * stride + 1];
+        mt = st[(size_t)t * 2];
+        lt = st[(size_t)t * 2 + 1];
       }
       float av[FK_COMBINE_CHUNK];
+      const uint32_t ic = min(i, p.head_dim - 1);
 #pragma unroll
-      for (int j = 0; j < FK_COMBINE_CHUNK; j++)
-        av[j] = (t0 + j < p.splits && i < p.head_dim) ? ph[(size_t)(t0 + j) * stride + 2 + i] : 0.0f;
+      for (int j = 0; j < FK_COMBINE_CHUNK; j++) av[j] = ph[(size_t)min(t0 + j, p.splits - 1) * stride + ic];
       float wt = 0.0f, lw = 0.0f;
       if (t < p.splits) {
         wt = fk::exp_once(mt - top);
         lw = lt * wt;
       }
+      float *sw = reinterpret_cast<float *>(sw4);
+      float *slw = reinterpret_cast<float *>(slw4);
+      __syncthreads();  // the last chunk's weights are read
+      sw[lane] = wt;
+      slw[lane] = lw;
+      __syncthreads();
 #pragma unroll
       for (int j = 0; j < FK_COMBINE_CHUNK; j++) {
         if (t0 + j < p.splits) {
-          l = l + fk::readlane_f(lw, j);
-          acc = acc + av[j] * fk::readlane_f(wt, j);
+          l = l + slw[j];
+          acc = acc + av[j] * sw[j];
         }
       }
     }

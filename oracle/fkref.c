@@ -486,7 +486,10 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
        * position from +0, then the runs' sums added in order. */
       const int run = split / ATTEND_CHUNKS;
       for (int h = 0; h < group; h++) {
-        float *out = partials + ((size_t)(g * group + h) * splits + t) * (d + 2);
+        /* Partials: acc[heads][splits][d], then [heads][splits][max, sum]. */
+        const size_t ht = (size_t)(g * group + h) * splits + t;
+        float *out = partials + ht * d;
+        float *stat = partials + (size_t)heads * splits * d + 2 * ht;
         for (int i = 0; i < d; i++) {
           float l = 0.0f;
           float acc = 0.0f;
@@ -503,10 +506,10 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
             acc = acc + ac;
           }
           if (i == 0) {
-            out[0] = mx[h];
-            out[1] = l;
+            stat[0] = mx[h];
+            stat[1] = l;
           }
-          out[2 + i] = acc;
+          out[i] = acc;
         }
       }
     }
@@ -515,18 +518,18 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
 }
 
 int fkref_step_combine(const float *partials, float *out, int heads, int head_dim, int splits) {
-  const int stride = head_dim + 2;
   for (int h = 0; h < heads; h++) {
-    const float *ph = partials + (size_t)h * splits * stride;
+    const float *ph = partials + (size_t)h * splits * head_dim;
+    const float *st = partials + (size_t)heads * splits * head_dim + (size_t)h * splits * 2;
     float m = -INFINITY;
-    for (int t = 0; t < splits; t++) m = fkref_max(m, ph[(size_t)t * stride]);
+    for (int t = 0; t < splits; t++) m = fkref_max(m, st[2 * t]);
     for (int i = 0; i < head_dim; i++) {
       float l = 0.0f;
       float acc = 0.0f;
       for (int t = 0; t < splits; t++) {
-        float w = fkref_exp(ph[(size_t)t * stride] - m);
-        l = l + ph[(size_t)t * stride + 1] * w;
-        acc = acc + ph[(size_t)t * stride + 2 + i] * w;
+        float w = fkref_exp(st[2 * t] - m);
+        l = l + st[2 * t + 1] * w;
+        acc = acc + ph[(size_t)t * head_dim + i] * w;
       }
       out[(size_t)h * head_dim + i] = acc / l;
     }

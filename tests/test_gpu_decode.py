@@ -46,8 +46,8 @@ def compare_all(session, cpu, names=None):
 
 @pytest.mark.parametrize("position,fuse", [(0, True), (16, True), (31, True), (0, False), (31, False)])
 def test_tiny_decode_step_bit_exact(device, kernels, position, fuse):
-    """With the KV store and the combine folded into the attention launch
-    (fuse), and as the plan's separate store, attention and combine steps."""
+    """With the KV store folded into the attention launch (fuse), and as the
+    plan's separate store and attention steps."""
     s = DecodeSession(device, kernels, TINY32, PlanOptions(), embed=False, fuse=fuse)
     try:
         s.init_synthetic()
