@@ -100,9 +100,21 @@ struct AttendLds {
   alignas(16) u32x4 ks[FK_ATTN_MAX_SPLIT * FK_ATTN_KROW / 8];   // later: the runs' weighted values
   alignas(16) u32x4 vs[FK_ATTN_MAX_SPLIT * FK_ATTN_MAX_DIM / 8];
   alignas(16) float wt[FK_ATTN_MAX_SPLIT * FK_ATTN_MAX_GROUP];  // [position][head]
-  alignas(16) float pm[FK_ATTN_MAX_GROUP * 2];  // per head, the maxima of the split's 64-position halves
-  alignas(16) float pl[FK_ATTN_WAVES * FK_ATTN_MAX_GROUP];     // the runs' weight sums
+  alignas(16) float pm[FK_ATTN_MAX_GROUP * FK_ATTN_WAVES];     // [head][wave]: the maxima of each wave's positions
+  alignas(16) float pl[FK_ATTN_WAVES * FK_ATTN_MAX_GROUP];     // [run][head]: the runs' weight sums
 };
+
+// Head h's largest of the wavefronts' maxima pm[h][wave] (maximumNumber,
+// exact whatever the order), on max_key's integers so that no branch
+// separates the reads.
+__device__ __forceinline__ float waves_max(const float *pm, uint32_t h) {
+  static_assert(FK_ATTN_WAVES == 8, "two 16-byte reads of a head's maxima");
+  const float4 a = *reinterpret_cast<const float4 *>(pm + h * FK_ATTN_WAVES);
+  const float4 b = *reinterpret_cast<const float4 *>(pm + h * FK_ATTN_WAVES + 4);
+  const int k = max(max(max(max_key(a.x), max_key(a.y)), max(max_key(a.z), max_key(a.w))),
+                    max(max(max_key(b.x), max_key(b.y)), max(max_key(b.z), max_key(b.w))));
+  return from_max_key(k);
+}
 
 // Threadgroup (kv head g, split t) of 512 threads.  G, D, S, CB: the
 // group's query heads, the head dimension, the split's positions and the
@@ -118,11 +130,14 @@ struct AttendLds {
 // what the ring holds), so no other threadgroup reads it.
 //
 // Attend: for each query head h of the group and each position r of the
-// split, score = (sum over i in order of q_i k_i) * scale; the head's maximum
-// over the split (exact whatever the order); the weights exp(score - max),
-// binary64's rounded once.  The weights' sum and the weighted sum of the
-// values over 8 runs of split/8 positions (wavefront w's run w), each in
-// order of position from +0, then the runs' sums in order.  Stored as
+// split, score = ((c0 + c1) + (c2 + c3)) * scale, c_j the fused multiply-add
+// chain from +0 over the dimensions of quarter j in order (c = fma(q_i, k_i,
+// c)); the head's maximum over the split (exact whatever the order); the
+// weights exp(score - max), binary64's rounded once.  Over 8 runs of split/8
+// positions: the weights' pairwise sum (((w0 + w1) + (w2 + w3)) + ...), a
+// position past those the split holds adding +0, and the weighted values in
+// order of position from +0 (acc = fma(w, v_i, acc)); then the runs' sums in
+// order from +0.  Stored as
 // partials: acc[heads][splits][head_dim], then [heads][splits][max, sum] —
 // each (head, split)'s values 16-byte aligned for a consumer's vector loads.
 template <uint32_t G, uint32_t D, uint32_t S, int CB>
@@ -133,7 +148,7 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
                                              const float *__restrict__ rope, float *__restrict__ partials,
                                              const fk_step_attend_params &p) {
   constexpr uint32_t T = FK_ATTN_THREADS;
-  constexpr uint32_t HPT = FK_ATTN_MAX_GROUP * FK_ATTN_MAX_SPLIT / T;  // heads a thread scores, at most
+  static_assert(T == 4 * FK_ATTN_MAX_SPLIT, "four threads a position of the largest split");
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & (FK_WAVE - 1);
   const uint32_t wave = tid / FK_WAVE;
@@ -212,10 +227,12 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
     if (p.rope && i < p.rotated) v = j < half ? qx * qc - qp * qn : qx * qc + qp * qn;
     sh.qs[tid] = v;
   }
+  // Rows past the positions the split holds get zeros: their weights are
+  // zero and their values then add exact zeros.
 #pragma unroll
   for (int m = 0; m < 2; m++) {
     const uint32_t e = tid + m * T;
-    if (e < chunks) {
+    if (e < split * per_row) {
       const uint32_t r = e / per_row;
       const uint32_t c8 = e % per_row;
       sh.ks[r * (FK_ATTN_KROW / 8) + c8] = kr[m];
@@ -238,88 +255,106 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
   }
   __syncthreads();
 
-  // Scores: thread (r, hs) takes position r of the split for the heads hs,
-  // hs + 512/split: its key row read once, 16 bytes at a time.  Each
-  // wavefront holds 64 positions of its heads: their maximum by DPP.
-  const uint32_t nh = T / split;
-  const uint32_t r = tid % split;
-  const uint32_t hs = tid / split;
-  const uint32_t halfk = r / FK_WAVE;
-  float sc[HPT];
+  // Scores: thread (r, j) = (tid / 4, tid % 4) takes quarter j of position
+  // r's key (read once from LDS, widened once) against every head of the
+  // group; the quad's four chains are added by DPP, ((c0 + c1) + (c2 + c3)),
+  // so each lane of the quad holds every head's score.  Lane 4p + j then
+  // keeps heads j and j + 4, and a wavefront's 16 positions give each head's
+  // maximum (rotations within rows of 16 lanes, then across rows) into
+  // pm[head][wave].
+  const uint32_t r = tid / 4;
+  const uint32_t jq = tid % 4;
+  const uint32_t dq = d / 4;
+  constexpr uint32_t HL = FK_ATTN_MAX_GROUP / 4;  // heads a lane keeps
+  float hs[HL];
   {
-    float kf[FK_ATTN_MAX_DIM];
+    constexpr uint32_t DQ = FK_ATTN_MAX_DIM / 4;
+    const bool live = r < n;
+    const uint32_t *krow = reinterpret_cast<const uint32_t *>(sh.ks) + (size_t)min(r, split - 1) * (FK_ATTN_KROW / 2) +
+                           jq * (dq / 2);
+    float kf[DQ];
 #pragma unroll
-    for (uint32_t c8 = 0; c8 < FK_ATTN_MAX_DIM / 8; c8++) {
-      u32x4 kk = u32x4{0u, 0u, 0u, 0u};
-      if (c8 < per_row && r < n) kk = sh.ks[r * (FK_ATTN_KROW / 8) + c8];
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        kf[8 * c8 + 2 * j] = widen_cache((uint16_t)(kk[j] & 0xFFFFu), bf16);
-        kf[8 * c8 + 2 * j + 1] = widen_cache((uint16_t)(kk[j] >> 16), bf16);
-      }
+    for (uint32_t w2 = 0; w2 < DQ / 2; w2++) {
+      uint32_t kk = 0u;
+      if (w2 < dq / 2) kk = krow[w2];
+      kf[2 * w2] = widen_cache((uint16_t)(kk & 0xFFFFu), bf16);
+      kf[2 * w2 + 1] = widen_cache((uint16_t)(kk >> 16), bf16);
     }
+    float sc[FK_ATTN_MAX_GROUP];
 #pragma unroll
-    for (uint32_t a = 0; a < HPT; a++) {
-      const uint32_t h = hs + a * nh;
-      sc[a] = -__builtin_inff();
-      if (h < group && r < n) {
-        const float4 *qh = reinterpret_cast<const float4 *>(sh.qs + h * d);
-        float dot = 0.0f;
-#pragma unroll
-        for (uint32_t c4 = 0; c4 < FK_ATTN_MAX_DIM / 4; c4++) {
-          if (c4 < d / 4) {
-            const float4 qq = qh[c4];
-            dot = dot + qq.x * kf[4 * c4];
-            dot = dot + qq.y * kf[4 * c4 + 1];
-            dot = dot + qq.z * kf[4 * c4 + 2];
-            dot = dot + qq.w * kf[4 * c4 + 3];
-          }
-        }
-        sc[a] = dot * p.scale;
-      }
-    }
-#pragma unroll
-    for (uint32_t a = 0; a < HPT; a++) {
-      const uint32_t h = hs + a * nh;
+    for (uint32_t h = 0; h < FK_ATTN_MAX_GROUP; h++) {
+      float c = 0.0f;
       if (h < group) {
-        const float m = wave_max(sc[a]);
-        if (lane == 0) sh.pm[h * 2 + halfk] = m;
+        const float *qh = sh.qs + h * d + jq * dq;
+#pragma unroll
+        for (uint32_t i = 0; i < DQ; i++)
+          if (i < dq) c = __builtin_fmaf(qh[i], kf[i], c);
+      }
+      c = c + dpp_f<0xB1>(c);  // quad_perm [1, 0, 3, 2]: c0 + c1, c2 + c3
+      c = c + dpp_f<0x4E>(c);  // quad_perm [2, 3, 0, 1]: (c0 + c1) + (c2 + c3)
+      sc[h] = live ? c * p.scale : -__builtin_inff();
+    }
+#pragma unroll
+    for (uint32_t a = 0; a < HL; a++) {
+      float v = sc[a * 4];
+#pragma unroll
+      for (uint32_t q = 1; q < 4; q++) v = jq == q ? sc[a * 4 + q] : v;
+      hs[a] = v;
+      if (a * 4 < group) {
+        int k = max_key(v);
+        k = max(k, dpp_i<0x124>(k));  // row_ror:4, the next position of this head
+        k = max(k, dpp_i<0x128>(k));  // row_ror:8
+        k = max(k, __shfl_xor(k, 16));
+        k = max(k, __shfl_xor(k, 32));
+        if (lane < 4 && a * 4 + lane < group) sh.pm[(a * 4 + lane) * FK_ATTN_WAVES + wave] = from_max_key(k);
       }
     }
   }
   __syncthreads();
-  // The weights exp(score - max), the head's maximum the larger of its halves'.
+  // The weights exp(score - max), the head's maximum the largest of the
+  // wavefronts': thread (r, j) makes heads j and j + 4 (zero past the
+  // positions the split holds), then each run's pairwise sum over its
+  // positions by shuffles (lane 4p + j's partner at level m holds position
+  // p ^ m, same head).
+  {
+    const uint32_t rl = split / FK_ATTN_WAVES;  // a run's positions: 16 or 8
 #pragma unroll
-  for (uint32_t a = 0; a < HPT; a++) {
-    const uint32_t h = hs + a * nh;
-    if (h < group && r < n) {
-      const float m = split > FK_WAVE ? max_number(sh.pm[h * 2], sh.pm[h * 2 + 1]) : sh.pm[h * 2];
-      sh.wt[r * FK_ATTN_MAX_GROUP + h] = exp_once(sc[a] - m);
+    for (uint32_t a = 0; a < HL; a++) {
+      const uint32_t h = jq + 4 * a;
+      if (a * 4 < group) {
+        const float m = waves_max(sh.pm, min(h, group - 1));
+        float w = 0.0f;
+        if (h < group && r < n) w = exp_once(hs[a] - m);
+        if (h < group && r < split) sh.wt[r * FK_ATTN_MAX_GROUP + h] = w;
+        float t = w;
+#pragma unroll
+        for (uint32_t m2 = 1; m2 < FK_ATTN_MAX_SPLIT / FK_ATTN_WAVES; m2 <<= 1)
+          if (m2 < rl) t = t + __shfl_xor(t, 4 * m2);
+        if (h < group && r < split && r % rl == 0) sh.pl[(r / rl) * FK_ATTN_MAX_GROUP + h] = t;
+      }
     }
   }
   __syncthreads();
   // Wavefront w's run of positions, lane i's dimension, every head at once.
   {
+    constexpr uint32_t RUN_MAX = FK_ATTN_MAX_SPLIT / FK_ATTN_WAVES;
     const uint32_t run = split / FK_ATTN_WAVES;
     const uint32_t u0 = wave * run;
-    const uint32_t u1 = min(u0 + run, n);
-    float l[FK_ATTN_MAX_GROUP], acc[FK_ATTN_MAX_GROUP];
+    float acc[FK_ATTN_MAX_GROUP];
 #pragma unroll
-    for (int h = 0; h < FK_ATTN_MAX_GROUP; h++) l[h] = acc[h] = 0.0f;
-    if (lane < d) {
-      for (uint32_t u = u0; u < u1; u++) {
-        const float v = widen_cache(vsh[u * d + lane], bf16);
-        const float4 w0 = *reinterpret_cast<const float4 *>(sh.wt + u * FK_ATTN_MAX_GROUP);
-        const float4 w1 = group > 4 ? *reinterpret_cast<const float4 *>(sh.wt + u * FK_ATTN_MAX_GROUP + 4)
+    for (int h = 0; h < FK_ATTN_MAX_GROUP; h++) acc[h] = 0.0f;
+    const uint32_t ic = min(lane, d - 1);
+#pragma unroll
+    for (uint32_t u = 0; u < RUN_MAX; u++) {
+      if (u < run) {
+        const float v = widen_cache(vsh[(u0 + u) * d + ic], bf16);
+        const float4 w0 = *reinterpret_cast<const float4 *>(sh.wt + (u0 + u) * FK_ATTN_MAX_GROUP);
+        const float4 w1 = group > 4 ? *reinterpret_cast<const float4 *>(sh.wt + (u0 + u) * FK_ATTN_MAX_GROUP + 4)
                                     : float4{0.0f, 0.0f, 0.0f, 0.0f};
         const float w[FK_ATTN_MAX_GROUP] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int h = 0; h < FK_ATTN_MAX_GROUP; h++) {
-          if ((uint32_t)h < group) {
-            l[h] = l[h] + w[h];
-            acc[h] = acc[h] + w[h] * v;
-          }
-        }
+        for (int h = 0; h < FK_ATTN_MAX_GROUP; h++)
+          if ((uint32_t)h < group) acc[h] = __builtin_fmaf(w[h], v, acc[h]);
       }
     }
     __syncthreads();  // the keys are no longer read: their LDS holds the runs' sums
@@ -328,11 +363,6 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
 #pragma unroll
       for (int h = 0; h < FK_ATTN_MAX_GROUP; h++)
         if ((uint32_t)h < group) pacc[(wave * FK_ATTN_MAX_GROUP + h) * FK_ATTN_MAX_DIM + lane] = acc[h];
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int h = 0; h < FK_ATTN_MAX_GROUP; h++)
-        if ((uint32_t)h < group) sh.pl[wave * FK_ATTN_MAX_GROUP + h] = l[h];
     }
     __syncthreads();
     if (tid < group * d) {
@@ -348,7 +378,7 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
       const size_t ht = (size_t)(g * group + h) * p.splits + t;
       if (i == 0) {
         float *o = partials + (size_t)p.heads * p.splits * d + 2 * ht;
-        o[0] = split > FK_WAVE ? max_number(sh.pm[h * 2], sh.pm[h * 2 + 1]) : sh.pm[h * 2];
+        o[0] = waves_max(sh.pm, h);
         o[1] = lt;
       }
       partials[ht * d + i] = at;

@@ -443,6 +443,13 @@ int fkref_step_store(const float *x0, const float *x1, uint16_t *c0, uint16_t *c
 #define SPLIT_MAX 128
 #define ATTEND_CHUNKS 8
 
+/* The pairwise sum of n values (n a power of two): the halves' sums added,
+ * ((a0 + a1) + (a2 + a3)) + ... */
+static float pairwise_sum(const float *a, int n) {
+  if (n == 1) return a[0];
+  return pairwise_sum(a, n / 2) + pairwise_sum(a + n / 2, n / 2);
+}
+
 int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
                       int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
                       int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
@@ -450,7 +457,8 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
   const int group = heads / kv_heads;
   const int d = head_dim;
   const uint32_t SPLIT = (uint32_t)split;
-  if (group > 8 || d > 64 || split < ATTEND_CHUNKS || split > SPLIT_MAX || split % ATTEND_CHUNKS) return -1;
+  if (group > 8 || d > 64 || d % 8 || split < ATTEND_CHUNKS || split > SPLIT_MAX || split % ATTEND_CHUNKS) return -1;
+  if ((split / ATTEND_CHUNKS) & (split / ATTEND_CHUNKS - 1)) return -1; /* runs of a power of two */
   uint32_t s = slot < (uint32_t)slots ? slot : 0;
   float qs[8 * 64];
   float wt[8 * SPLIT_MAX];
@@ -466,12 +474,19 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
         qs[e] = rope ? fkref_rope_elem(head, e % d, d, rotated, position, theta) : head[e % d];
       }
       size_t base = ((size_t)s * kv_heads + g) * length;
+      /* A score: four fused multiply-add chains from +0, one a quarter of
+       * the dimensions in order, added ((c0 + c1) + (c2 + c3)), then scaled. */
+      const int dq = d / 4;
       for (int h = 0; h < group; h++) {
         for (int r = 0; r < count; r++) {
           size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
-          float dot = 0.0f;
-          for (int i = 0; i < d; i++) dot = dot + qs[h * d + i] * widen_cache(kc[at + i], cache_bf16);
-          wt[h * SPLIT + r] = dot * scale;
+          float c[4];
+          for (int j = 0; j < 4; j++) {
+            c[j] = 0.0f;
+            for (int i = j * dq; i < (j + 1) * dq; i++)
+              c[j] = fmaf(qs[h * d + i], widen_cache(kc[at + i], cache_bf16), c[j]);
+          }
+          wt[h * SPLIT + r] = ((c[0] + c[1]) + (c[2] + c[3])) * scale;
         }
       }
       for (int h = 0; h < group; h++) {
@@ -481,10 +496,13 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
       }
       for (int h = 0; h < group; h++)
         for (int r = 0; r < count; r++) wt[h * SPLIT + r] = fkref_exp(wt[h * SPLIT + r] - mx[h]);
-      /* The weights' sum and the weighted values: the split's positions in
-       * ATTEND_CHUNKS runs of split / ATTEND_CHUNKS, each summed in order of
-       * position from +0, then the runs' sums added in order. */
+      /* The weights' sum and the weighted values over the split's positions
+       * in ATTEND_CHUNKS runs of split / ATTEND_CHUNKS: a run's weights by
+       * pairwise_sum (a position past `count` adding +0), its values in order
+       * of position from +0 (acc = fma(w, v, acc)); then the runs' sums
+       * added in order from +0. */
       const int run = split / ATTEND_CHUNKS;
+      float runw[SPLIT_MAX / ATTEND_CHUNKS];
       for (int h = 0; h < group; h++) {
         /* Partials: acc[heads][splits][d], then [heads][splits][max, sum]. */
         const size_t ht = (size_t)(g * group + h) * splits + t;
@@ -494,13 +512,12 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
           float l = 0.0f;
           float acc = 0.0f;
           for (int c = 0; c < ATTEND_CHUNKS; c++) {
-            float lc = 0.0f;
+            for (int u = 0; u < run; u++) runw[u] = c * run + u < count ? wt[h * SPLIT + c * run + u] : 0.0f;
+            float lc = pairwise_sum(runw, run);
             float ac = 0.0f;
             for (int r = c * run; r < (c + 1) * run && r < count; r++) {
               size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
-              float w = wt[h * SPLIT + r];
-              lc = lc + w;
-              ac = ac + w * widen_cache(vc[at + i], cache_bf16);
+              ac = fmaf(wt[h * SPLIT + r], widen_cache(vc[at + i], cache_bf16), ac);
             }
             l = l + lc;
             acc = acc + ac;
