@@ -20,13 +20,27 @@
 
 namespace fk {
 
+// 16 bytes; NT: a non-temporal load, for data read once (the weights, which
+// a step streams past every cache), so that it does not displace the rows
+// and partials every threadgroup reads.
+template <bool NT>
+__device__ __forceinline__ uint4 load16(const void *p) {
+  if constexpr (NT) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return uint4{v[0], v[1], v[2], v[3]};
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+
 // A pack of P elements of W or x, widened to f32 exactly.
-template <int P>
+template <int P, bool NT = false>
 __device__ __forceinline__ void load_pack(const float *__restrict__ p, float (&out)[P]) {
   static_assert(P % 4 == 0, "f32 packs are float4s");
 #pragma unroll
   for (int i = 0; i < P / 4; i++) {
-    float4 v = *reinterpret_cast<const float4 *>(p + 4 * i);
+    const uint4 u = load16<NT>(p + 4 * i);
+    const float4 v = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
     out[4 * i] = v.x;
     out[4 * i + 1] = v.y;
     out[4 * i + 2] = v.z;
@@ -34,12 +48,12 @@ __device__ __forceinline__ void load_pack(const float *__restrict__ p, float (&o
   }
 }
 
-template <int P>
+template <int P, bool NT = false>
 __device__ __forceinline__ void load_pack(const _Float16 *__restrict__ p, float (&out)[P]) {
   static_assert(P % 8 == 0, "f16 packs are 16-byte loads");
 #pragma unroll
   for (int i = 0; i < P / 8; i++) {
-    uint4 v = *reinterpret_cast<const uint4 *>(p + 8 * i);
+    uint4 v = load16<NT>(p + 8 * i);
     uint32_t words[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int h = 0; h < 4; h++) {
@@ -49,12 +63,12 @@ __device__ __forceinline__ void load_pack(const _Float16 *__restrict__ p, float 
   }
 }
 
-template <int P>
+template <int P, bool NT = false>
 __device__ __forceinline__ void load_pack(const int8_t *__restrict__ p, float (&out)[P]) {
   static_assert(P % 16 == 0, "i8 packs are 16-byte loads");
 #pragma unroll
   for (int i = 0; i < P / 16; i++) {
-    uint4 v = *reinterpret_cast<const uint4 *>(p + 16 * i);
+    uint4 v = load16<NT>(p + 16 * i);
     uint32_t words[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int b = 0; b < 16; b++) out[16 * i + b] = (float)(int8_t)(words[b / 4] >> (8 * (b % 4)));
@@ -139,7 +153,7 @@ __device__ __forceinline__ void gemv_wave(const WT *__restrict__ w, const XT *__
 #pragma unroll
     for (int q = 0; q < R; q++) {
       float wv[P];
-      load_pack<P>(wr[q] + (size_t)j * P, wv);
+      load_pack<P, true>(wr[q] + (size_t)j * P, wv);
 #pragma unroll
       for (int c = 0; c < C; c++) {
         float p0 = xv[4 * c] * wv[4 * c];
@@ -186,7 +200,7 @@ __device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, con
   for (int it = 0; it < KPL; it++) {
     const uint32_t jc = min(lane + FK_WAVE * (uint32_t)it, packs - 1);
 #pragma unroll
-    for (int q = 0; q < R; q++) wv[q][it] = *reinterpret_cast<const uint4 *>(wr[q] + (size_t)jc * P);
+    for (int q = 0; q < R; q++) wv[q][it] = load16<true>(wr[q] + (size_t)jc * P);
   }
 #pragma unroll
   for (int it = 0; it < KPL; it++) {

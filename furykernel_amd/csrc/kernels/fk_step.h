@@ -214,8 +214,9 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
       uint32_t ring = ring0 + e / per_row;
       ring = ring >= p.length ? ring - p.length : ring;
       const size_t at = (base + ring) * d + 8 * (e % per_row);
-      kr[m] = *reinterpret_cast<const u32x4 *>(kc + at);
-      vr[m] = *reinterpret_cast<const u32x4 *>(vc + at);
+      // Non-temporal: a step reads each cached row once.
+      kr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kc + at));
+      vr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vc + at));
     }
   }
 

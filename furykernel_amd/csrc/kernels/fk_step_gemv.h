@@ -148,7 +148,8 @@ struct Block {
 
 namespace fk {
 
-// A block's weights: R rows of KPL 16-byte packs a lane.
+// A block's weights: R rows of KPL 16-byte packs a lane, loaded non-temporal
+// (a step streams each weight once).
 template <typename WT, int P, int R, int KPL>
 __device__ __forceinline__ void issue_block(uint4 (&dst)[R][KPL], const Block<R> &blk, const WT *__restrict__ w0,
                                             const WT *__restrict__ w1, const WT *__restrict__ w2, uint32_t k,
@@ -161,7 +162,7 @@ __device__ __forceinline__ void issue_block(uint4 (&dst)[R][KPL], const Block<R>
 #pragma unroll
     for (int it = 0; it < KPL; it++) {
       const uint32_t j = lane + it * FK_WAVE;
-      dst[q][it] = *reinterpret_cast<const uint4 *>(wr + (size_t)min(j, packs - 1) * P);
+      dst[q][it] = load16<true>(wr + (size_t)min(j, packs - 1) * P);
     }
   }
 }
