@@ -205,22 +205,32 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
   const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
   // Ring index of row r: (lo + r) mod length, where r < n <= length.
   const uint32_t ring0 = lo % p.length;
-  u32x4 kr[2], vr[2];
+  // The row the new key and value replace (none unless this split stores).
+  const uint32_t srow = stores ? pos - lo : 0xFFFFFFFFu;
+  // The split's keys, then its values, 16 bytes a load, non-temporal (a step
+  // reads each cached row once): K is staged before the scores, V while they
+  // are made.  Every load unconditional, a chunk past the split's rows
+  // reading its last chunk (or the ring's row lo) and replaced by zeros.
+  size_t at2[2];
+  bool live2[2];
 #pragma unroll
   for (int m = 0; m < 2; m++) {
     const uint32_t e = tid + m * T;
-    kr[m] = vr[m] = u32x4{0u, 0u, 0u, 0u};
-    if (e < chunks) {
-      uint32_t ring = ring0 + e / per_row;
-      ring = ring >= p.length ? ring - p.length : ring;
-      const size_t at = (base + ring) * d + 8 * (e % per_row);
-      // Non-temporal: a step reads each cached row once.
-      kr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kc + at));
-      vr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vc + at));
-    }
+    live2[m] = e < chunks;
+    const uint32_t ec = min(e, chunks > 0 ? chunks - 1 : 0u);
+    uint32_t ring = ring0 + ec / per_row;
+    ring = ring >= p.length ? ring - p.length : ring;
+    at2[m] = (base + ring) * d + 8 * (ec % per_row);
   }
+  u32x4 kr[2], vr[2];
+#pragma unroll
+  for (int m = 0; m < 2; m++) kr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kc + at2[m]));
+#pragma unroll
+  for (int m = 0; m < 2; m++) vr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vc + at2[m]));
 
-  // The query rows, RoPE'd as rope_elem does, and the tile into LDS.
+  // The query rows, RoPE'd as rope_elem does, and the keys into LDS; rows
+  // past the positions the split holds get zeros (their weights are zero and
+  // their values then add exact zeros).  The new key row replaces row srow.
   if (tid < group * d) {
     const uint32_t j = tid % d;
     const uint32_t i = j < half ? j : j - half;
@@ -228,31 +238,25 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
     if (p.rope && i < p.rotated) v = j < half ? qx * qc - qp * qn : qx * qc + qp * qn;
     sh.qs[tid] = v;
   }
-  // Rows past the positions the split holds get zeros: their weights are
-  // zero and their values then add exact zeros.
 #pragma unroll
   for (int m = 0; m < 2; m++) {
     const uint32_t e = tid + m * T;
-    if (e < split * per_row) {
-      const uint32_t r = e / per_row;
-      const uint32_t c8 = e % per_row;
-      sh.ks[r * (FK_ATTN_KROW / 8) + c8] = kr[m];
-      sh.vs[r * per_row + c8] = vr[m];
-    }
+    const uint32_t r = e / per_row;
+    if (e < split * per_row && r != srow)
+      sh.ks[r * (FK_ATTN_KROW / 8) + e % per_row] = live2[m] ? kr[m] : u32x4{0u, 0u, 0u, 0u};
   }
-  __syncthreads();
+  uint16_t vh = 0;
   if (stores && tid < d) {
     const uint32_t j = tid;
     const uint32_t i = j < half ? j : j - half;
     float k = kx;
     if (p.krope && i < p.rotated) k = j < half ? kx * kcs - kp * ksn : kx * kcs + kp * ksn;
     const uint16_t kh = narrow_cache(k, bf16);
-    const uint16_t vh = narrow_cache(vx, bf16);
+    vh = narrow_cache(vx, bf16);
     const size_t at = (base + pos % p.length) * d + j;
     kc[at] = kh;
     vc[at] = vh;
-    ksh[(pos - lo) * FK_ATTN_KROW + j] = kh;
-    reinterpret_cast<uint16_t *>(sh.vs)[(pos - lo) * d + j] = vh;
+    ksh[srow * FK_ATTN_KROW + j] = kh;
   }
   __syncthreads();
 
@@ -334,6 +338,14 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
         if (h < group && r < split && r % rl == 0) sh.pl[(r / rl) * FK_ATTN_MAX_GROUP + h] = t;
       }
     }
+    // The values into LDS as the keys went (the new value row replacing row srow).
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+      const uint32_t e = tid + m * T;
+      const uint32_t rr = e / per_row;
+      if (e < split * per_row && rr != srow) sh.vs[rr * per_row + e % per_row] = live2[m] ? vr[m] : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (stores && tid < d) reinterpret_cast<uint16_t *>(sh.vs)[srow * d + tid] = vh;
   }
   __syncthreads();
   // Wavefront w's run of positions, lane i's dimension, every head at once.
@@ -358,7 +370,8 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
           if ((uint32_t)h < group) acc[h] = __builtin_fmaf(w[h], v, acc[h]);
       }
     }
-    __syncthreads();  // the keys are no longer read: their LDS holds the runs' sums
+    // The keys were last read before the maxima's barrier: their LDS now holds
+    // the runs' sums.
     float *pacc = reinterpret_cast<float *>(sh.ks);  // [wave][head][dim]
     if (lane < d) {
 #pragma unroll
