@@ -1,8 +1,8 @@
 """The program evaluator in binary64: what a checked program's step computes,
 each operation exact to double precision, rounded only where the program
 rounds (its cache stores), following src/FuryKernel/Program/Eval.hs
-operation for operation.  The values only: the per-element bounds
-(`Approx`, Eval.hs:691-918) are not restated.
+operation for operation.  The values; the per-element bounds (`Approx`,
+Eval.hs:686-966) are oracle/bounds.py's.
 
 TEST INFRASTRUCTURE: imported only by tests/, as the f64 checker of the
 target's f32 arithmetic (and of the oracle's CPU target).

@@ -1,0 +1,219 @@
+"""The evaluator's per-element bounds (oracle/bounds.py, Eval.hs:686-966),
+pinned three ways.
+
+- Soundness, by brute force: binary32 sums, dot products (fused or not),
+  products and quotients of random and cancellation-heavy operands, computed
+  in many orders, each within its bound of the exact value.  A dropped term
+  (the gamma factor, the operands' own bounds) fails these.
+- The cases the definitions fix: exact constants, NaN, overflow, flushing,
+  divisors whose bound reaches zero, decided and undecided arg-maxes.
+- The tiny decode: every value the CPU target stores (SIMD widths 64 and 32)
+  within its element bounds of the exact values, every new cache element one
+  a kernel may store, the token equal where its arg-max is decided.  With the
+  gamma factor planted away in the oracle, some element falls outside.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import bounds as B
+from oracle.bounds import Approx
+from test_evaluator import run_cpu_target, run_evaluator, tiny_state
+from furykernel_amd.program.plan import PlanOptions
+
+
+def f32(x):
+    return np.float32(x)
+
+
+def orders(n, rng, count=12):
+    out = [list(range(n)), list(range(n))[::-1]]
+    out += [list(rng.permutation(n)) for _ in range(count)]
+    return out
+
+
+def f32_sum(vals, order):
+    s = np.float32(0.0)
+    for i in order:
+        s = np.float32(s + vals[i])
+    return float(s)
+
+
+def f32_pairwise(vals):
+    v = [np.float32(x) for x in vals]
+    while len(v) > 1:
+        v = [np.float32(v[i] + v[i + 1]) if i + 1 < len(v) else v[i] for i in range(0, len(v), 2)]
+    return float(v[0])
+
+
+def operands(rng, n, kind):
+    if kind == "random":
+        return (rng.standard_normal(n) * 10.0 ** rng.uniform(-3, 3, n)).astype(np.float32)
+    # cancellation-heavy: large pairs that cancel, small terms between
+    big = (rng.standard_normal(n // 2) * 1e4).astype(np.float32)
+    small = (rng.standard_normal(n - 2 * (n // 4)) * 1e-3).astype(np.float32)
+    return np.concatenate([big[: n // 4], -big[: n // 4], small]).astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["random", "cancelling"])
+@pytest.mark.parametrize("n", [2, 7, 64, 257])
+def test_sum_bound_holds_in_every_order(n, kind):
+    rng = np.random.default_rng(n * 7 + len(kind))
+    for _ in range(20):
+        x = operands(rng, n, kind)
+        a = B.sum_a([B.exact_a(float(v)) for v in x])
+        exact = math.fsum(float(v) for v in x)
+        got = [f32_sum(x, o) for o in orders(n, rng)] + [f32_pairwise(x)]
+        for g in got:
+            assert abs(g - exact) <= a.bound, (g, exact, a.bound)
+
+
+@pytest.mark.parametrize("kind", ["random", "cancelling"])
+@pytest.mark.parametrize("n", [3, 16, 64, 200])
+def test_dot_bound_holds_in_every_order_fused_or_not(n, kind):
+    rng = np.random.default_rng(n * 11 + len(kind))
+    for _ in range(20):
+        x = operands(rng, n, kind)
+        w = (rng.standard_normal(n)).astype(np.float32)
+        a = B.dot_a([(B.exact_a(float(u)), B.exact_a(float(v))) for u, v in zip(w, x)])
+        exact = math.fsum(float(u) * float(v) for u, v in zip(w, x))
+        for o in orders(n, rng, 8):
+            s = np.float32(0.0)
+            f = np.float32(0.0)
+            for i in o:
+                s = np.float32(s + np.float32(w[i] * x[i]))
+                f = np.float32(float(w[i]) * float(x[i]) + float(f))   # a fused multiply-add
+            assert abs(float(s) - exact) <= a.bound
+            assert abs(float(f) - exact) <= a.bound
+
+
+def test_dot_bound_covers_operand_bounds():
+    """Operands known only within bounds: every binary32 value within them,
+    multiplied and summed in binary32, stays within the dot product's bound."""
+    rng = np.random.default_rng(5)
+    n = 32
+    for _ in range(50):
+        xe = rng.standard_normal(n)
+        xb = np.abs(rng.standard_normal(n)) * 1e-3
+        w = rng.standard_normal(n).astype(np.float32)
+        a = B.dot_a([(B.exact_a(float(u)), Approx(float(v), float(e))) for u, v, e in zip(w, xe, xb)])
+        exact = sum(float(u) * float(v) for u, v in zip(w, xe))
+        for _ in range(10):
+            xk = (xe + xb * rng.uniform(-1, 1, n)).astype(np.float32)
+            got = f32_sum([np.float32(u * v) for u, v in zip(w, xk)], rng.permutation(n))
+            assert abs(got - exact) <= a.bound
+
+
+def test_product_and_quotient_bounds_hold():
+    rng = np.random.default_rng(9)
+    for _ in range(200):
+        fs = rng.standard_normal(4) * 10.0 ** rng.uniform(-2, 2, 4)
+        a = B.product_a([B.exact_a(float(f32(v))) for v in fs])
+        exact = math.prod(float(f32(v)) for v in fs)
+        for o in orders(4, rng, 6):
+            p = np.float32(1.0)
+            for i in o:
+                p = np.float32(p * f32(fs[i]))
+            assert abs(float(p) - exact) <= a.bound
+        n, d = float(f32(fs[0])), float(f32(fs[1]))
+        q = B.quotient_a(B.exact_a(n), B.exact_a(d))
+        assert abs(float(np.float32(f32(n) / f32(d))) - n / d) <= q.bound
+
+
+def test_the_cases_the_definitions_fix():
+    assert B.const_a(0.5).bound == 0 and B.const_a(3.0).bound == 0
+    assert B.const_a(0.1).bound == abs(0.1 - float(np.float32(0.1)))
+    assert math.isinf(B.settle(Approx(3e38, 1e38)).bound)        # a value that can overflow
+    assert math.isnan(B.settle(Approx(math.nan, 0.0)).exact)
+    assert B.settle(Approx(1e-39, 0.0)).bound == 1e-39             # can flush to zero
+    assert math.isinf(B.quotient_a(B.exact_a(1.0), Approx(1.0, 1.0)).bound)
+    assert B.gamma_n(0) == 0 and math.isinf(B.gamma_n(2 ** 23))
+    assert B.arg_max_decided([Approx(1.0, 0.1), Approx(0.5, 0.1)])
+    assert not B.arg_max_decided([Approx(1.0, 0.3), Approx(0.5, 0.3)])
+    # a tie decided towards the lower index
+    assert B.arg_max_decided([Approx(1.0, 0.0), Approx(1.0, 0.0)])
+    assert B.may_store("f16", Approx(1.0, 0.0), 1.0) and not B.may_store("f16", Approx(1.0, 0.0), 1.0009765625)
+
+
+def check_tiny(cpu, ev, bd, checked, caches):
+    bad = []
+    for name, rows in bd.values.items():
+        buf = f"value:{name}"
+        if buf not in cpu.lowered.buffers:
+            continue
+        got = cpu.read(buf).astype(np.float64)
+        exact = ev.values[name][0]
+        for i, (g, x, e) in enumerate(zip(got, exact, rows[0])):
+            if not B.within(float(g), float(x), float(e)):
+                bad.append((name, i, float(g), float(x), float(e)))
+    for cname, held in bd.stores.items():
+        got = cpu.read(f"cache:{cname}").astype(np.float64)
+        elem = [s for s in checked.program.sources if s.name == cname][0].kind.elem
+        for (slot, at), (element, _) in held.items():
+            if not B.may_store(elem, element, float(got[at])):
+                bad.append((cname, at, float(got[at]), element.exact, element.bound))
+    return bad
+
+
+@pytest.mark.parametrize("width", [64, 32])
+@pytest.mark.parametrize("store_gelus", [False, True])
+@pytest.mark.parametrize("position", [16, 31])
+def test_tiny_decode_within_the_element_bounds(width, store_gelus, position):
+    checked, w, c, x, _ = tiny_state(position=position)
+    ev = run_evaluator(checked, w, c, x, position)
+    bd = B.evaluate_bounds(checked, bindings(w, c, x, position), ev)
+    cpu = run_cpu_target(checked, w, c, x, position, width, PlanOptions(store_gelus=store_gelus))
+    assert check_tiny(cpu, ev, bd, checked, c) == []
+    # A decided arg-max (bound 0) fixes the token; an undecided one (the top
+    # logits within each other's bounds) allows any of them.
+    if bd.values["token"][0][0] == 0:
+        assert int(cpu.read("value:token")[0]) == int(ev.values["token"][0][0])
+    # Worst-case bounds compound through each RMSNorm (they scale by the
+    # inverse of the row's RMS): the first layer's are all finite; later ones
+    # may lose everything (infinite, which any value meets).
+    first = np.concatenate([r[0] for n, r in bd.values.items() if n == "x" or n.startswith("l0_")])
+    assert np.all(np.isfinite(first))
+
+
+def bindings(w, c, x, position):
+    from oracle.eval import Bindings
+
+    return Bindings(1, inputs={"x": [x.astype(np.float64)]}, weights={k: v.astype(np.float64) for k, v in w.items()},
+                    row_ints={"position": [[position]], "slot": [[0]]},
+                    caches={k: {0: v.astype(np.float64)} for k, v in c.items()})
+
+
+def test_a_dropped_gamma_factor_is_caught(monkeypatch):
+    """The brute-force checks have teeth: bounds without the roundings'
+    gamma factor fail them (sums and dot products, random and cancelling)."""
+    monkeypatch.setattr(B, "gamma_n", lambda n: 0.0)
+    for check, n in ((test_sum_bound_holds_in_every_order, 64), (test_dot_bound_holds_in_every_order_fused_or_not, 64)):
+        for kind in ("random", "cancelling"):
+            with pytest.raises(AssertionError):
+                check(n, kind)
+
+
+def test_a_wrong_exact_value_falls_outside_the_bounds(monkeypatch):
+    """The decode check has teeth: an evaluator whose RoPE forgets the
+    partner term (planted in the oracle) leaves the CPU target's values
+    outside their bounds."""
+    import oracle.eval as E
+
+    checked, w, c, x, position = tiny_state()
+    cpu = run_cpu_target(checked, w, c, x, position, 64)
+    good = E.rotate
+
+    def dropped(theta, rotated, d, pos, xs):
+        ys = good(theta, rotated, d, pos, xs)
+        half = d // 2
+        for i in range(rotated):
+            ang = pos * theta ** (-(2.0 * i) / d)
+            ys[i] = xs[i] * math.cos(ang)
+            ys[i + half] = xs[i + half] * math.cos(ang)
+        return ys
+    monkeypatch.setattr(E, "rotate", dropped)
+    ev = run_evaluator(checked, w, c, x, position)
+    bd = B.evaluate_bounds(checked, bindings(w, c, x, position), ev)
+    assert check_tiny(cpu, ev, bd, checked, c) != []

@@ -156,3 +156,41 @@ def test_tiny_decode_on_the_gpu_within_1e4_of_the_f64_evaluator(device, kernels)
         assert s.token() == int(cpu.read("value:token")[0])
     finally:
         s.close()
+
+
+def test_tiny_decode_on_the_gpu_within_the_element_bounds(device, kernels):
+    """The tiny configuration on the GPU against the evaluator's per-element
+    bounds (Eval.hs:686-966): every value the step stores within its
+    element's bound of the exact value, every new cache element one a kernel
+    may store, the token the evaluator's where its arg-max is decided."""
+    from oracle import bounds as B
+    from test_bounds import bindings, check_tiny
+    from test_evaluator import run_evaluator, tiny_state
+
+    checked, w, c, x, position = tiny_state()
+    s = DecodeSession(device, kernels, TINY32, PlanOptions(), embed=False)
+    try:
+        for name, v in w.items():
+            if f"weight:{name}" in s.lowered.buffers:
+                s.engine.write(f"weight:{name}", v)
+        for name, v in c.items():
+            s.engine.write(f"cache:{name}", v)
+        s.engine.write("value:x", x)
+        s.set_position(position)
+        print(f"tiny decode on the GPU against the element bounds at position {position}", flush=True)
+        s.step()
+        device.sync()
+        ev = run_evaluator(checked, w, c, x, position)
+        bd = B.evaluate_bounds(checked, bindings(w, c, x, position), ev)
+
+        class Read:
+            lowered = s.lowered
+
+            @staticmethod
+            def read(name):
+                return s.engine.read(name)
+        assert check_tiny(Read, ev, bd, checked, c) == []
+        if bd.values["token"][0][0] == 0:
+            assert s.token() == int(ev.values["token"][0][0])
+    finally:
+        s.close()
