@@ -283,9 +283,12 @@ class Bounds:
     stores: dict   # cache name -> {(slot, element): (element Approx, stored Approx)}
 
 
-def evaluate_bounds(checked, b, ev: Evaluation) -> Bounds:
+def evaluate_bounds(checked, b, ev: Evaluation, kept=None) -> Bounds:
     """Every value's element bounds, in program order (Eval.hs:268-560), from
-    the bindings `b` and the exact values of `ev = evaluate(checked, b)`."""
+    the bindings `b` and the exact values of `ev = evaluate(checked, b, kept)`.
+    Given what the kernels stored (`kept`, an `oracle.eval.Kept`), each stored
+    element must be one its bound allows (else EvalError, as
+    evaluateStored's Left), and it is then read exactly."""
     p = checked.program
     sources = {s.id: s for s in p.sources}
     values = {v.id: v for v in p.values}
@@ -374,11 +377,25 @@ def evaluate_bounds(checked, b, ev: Evaluation) -> Bounds:
             d = lay.head_dim
             xs = approx(op.x)
             held = stores.setdefault(src.name, {})
+            staged = kept.rows.get(src.name) if kept is not None else None
+            left = kept.caches.get(src.name) if kept is not None else None
             for h in range(lay.kv_heads):
                 at = (h * lay.length + pos % lay.length) * d
                 for i in range(d):
                     el = xs[h * d + i]
-                    held[(s, at + i)] = (el, own_rounding(elem, el))
+                    if staged is None and left is None:
+                        held[(s, at + i)] = (el, own_rounding(elem, el))
+                        continue
+                    k = float(staged[0][h * d + i]) if staged is not None else float(left[s][at + i])
+                    if not may_store(elem, el, k):
+                        lo, hi = storable(elem, el)
+                        raise EvalError(f"The kernels stored {k} in {src.name} at slot {s}, element {at + i}, where "
+                                        f"the exact {el.exact}, within {el.bound}, rounds to between {lo} and {hi}.")
+                    if staged is not None and left is not None and float(left[s][at + i]) != k and \
+                            not (math.isnan(k) and math.isnan(float(left[s][at + i]))):
+                        raise EvalError(f"The kernels left {left[s][at + i]} in {src.name} at slot {s}, element "
+                                        f"{at + i}, not the {k} they staged for it.")
+                    held[(s, at + i)] = (el, exact_a(k))
         elif isinstance(op, Attend):
             spec = op.spec
             ksrc, vsrc = sources[op.to.keys], sources[op.to.values]
@@ -423,6 +440,16 @@ def evaluate_bounds(checked, b, ev: Evaluation) -> Bounds:
         else:
             raise EvalError(f"{n.name}: no bounds of {type(op).__name__} here")
     return Bounds({values[v].name: [np.array([a.bound for a in row])] for v, row in env.items()}, stores)
+
+
+def evaluate_stored(checked, b, kept):
+    """evaluateStored (Eval.hs:189-198): the evaluation given what the
+    kernels stored, and its bounds; EvalError where a stored element is not
+    one its bound allows."""
+    from .eval import evaluate
+
+    ev = evaluate(checked, b, kept)
+    return ev, evaluate_bounds(checked, b, ev, kept)
 
 
 def within(value: float, exact: float, bound: float) -> bool:

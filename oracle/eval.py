@@ -42,6 +42,15 @@ class Bindings:
 
 
 @dataclass
+class Kept:
+    """What a step's kernels stored (Eval.hs:174-184): ``caches`` name ->
+    {slot: flat values as the step left them}; ``rows`` name -> [rows] of the
+    values the kernels staged for the cache's store, if they staged them."""
+    caches: dict = field(default_factory=dict)
+    rows: dict = field(default_factory=dict)
+
+
+@dataclass
 class Evaluation:
     values: dict    # value name -> [rows] of f64 arrays
     outputs: dict   # output name -> [rows] of f64 arrays
@@ -111,8 +120,13 @@ def arg_max(xs) -> int:
     return best
 
 
-def evaluate(checked: CheckedProgram, b: Bindings) -> Evaluation:
-    """Eval.hs:186-228: every node in program order."""
+def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> Evaluation:
+    """Eval.hs:186-228: every node in program order.  Given `kept`, each store
+    into a cache keeps the element the kernels stored (staged, if they staged
+    it, else as they left the cache), so that what attends over the caches
+    reads what the kernels read; `oracle.bounds.evaluate_bounds` with the same
+    `kept` checks that each element's bound allows it (evaluateStored,
+    Eval.hs:189-198)."""
     p = checked.program
     m = b.rows
     sources = {s.id: s for s in p.sources}
@@ -224,13 +238,21 @@ def evaluate(checked: CheckedProgram, b: Bindings) -> Evaluation:
                 raise EvalError(f"No cache {src.name}.")
             ps, seqs = ints(op.at.positions), ints(op.at.sequences)
             d, heads = lay.head_dim, lay.kv_heads
-            for pos, sq, x in zip(ps, seqs, env[op.x]):
+            staged = kept.rows.get(src.name) if kept is not None else None
+            left = kept.caches.get(src.name) if kept is not None else None
+            for r, (pos, sq, x) in enumerate(zip(ps, seqs, env[op.x])):
                 for h in range(heads):
                     u, at = cache_index(lay, sq, pos[0], h)
                     if u not in units:
                         raise EvalError(f"{src.name} binds no slot {u}.")
                     for i in range(d):
-                        units[u][at + i] = round_cache(elem, float(x[h * d + i]))
+                        if staged is not None:
+                            v = float(staged[r][h * d + i])
+                        elif left is not None:
+                            v = float(left[u][at + i])
+                        else:
+                            v = round_cache(elem, float(x[h * d + i]))
+                        units[u][at + i] = v
         elif isinstance(op, Attend):
             spec = op.spec
             ksrc, vsrc = sources[op.to.keys], sources[op.to.values]

@@ -217,3 +217,37 @@ def test_a_wrong_exact_value_falls_outside_the_bounds(monkeypatch):
     ev = run_evaluator(checked, w, c, x, position)
     bd = B.evaluate_bounds(checked, bindings(w, c, x, position), ev)
     assert check_tiny(cpu, ev, bd, checked, c) != []
+
+
+def kept_of(cpu, checked):
+    from oracle.eval import Kept
+
+    names = [src.name for src in checked.program.sources if type(src.kind).__name__ == "SCache"]
+    return Kept(caches={n: {0: cpu.read(f"cache:{n}").astype(np.float64)} for n in names})
+
+
+def test_evaluate_stored_reads_what_the_kernels_stored():
+    """evaluateStored (Eval.hs:189-198): given the caches the CPU target left,
+    the evaluation keeps its stores, checks each against its bound, and the
+    step's values stay within their bounds of the new exact values."""
+    checked, w, c, x, position = tiny_state()
+    cpu = run_cpu_target(checked, w, c, x, position, 64)
+    kept = kept_of(cpu, checked)
+    ev, bd = B.evaluate_stored(checked, bindings(w, c, x, position), kept)
+    assert check_tiny(cpu, ev, bd, checked, c) == []
+    for name, units in kept.caches.items():
+        assert np.array_equal(ev.caches[name][0], units[0])
+
+
+def test_evaluate_stored_refuses_a_store_its_bound_does_not_allow():
+    from oracle.eval import EvalError
+
+    checked, w, c, x, position = tiny_state()
+    cpu = run_cpu_target(checked, w, c, x, position, 64)
+    kept = kept_of(cpu, checked)
+    name = "l0_k_cache"
+    lay = [s for s in checked.program.sources if s.name == name][0].kind.layout
+    at = (position % lay.length) * lay.head_dim          # kv head 0, element 0 of the new row
+    kept.caches[name][0][at] += 0.25
+    with pytest.raises(EvalError, match="The kernels stored"):
+        B.evaluate_stored(checked, bindings(w, c, x, position), kept)

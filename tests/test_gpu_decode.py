@@ -192,5 +192,11 @@ def test_tiny_decode_on_the_gpu_within_the_element_bounds(device, kernels):
         assert check_tiny(Read, ev, bd, checked, c) == []
         if bd.values["token"][0][0] == 0:
             assert s.token() == int(ev.values["token"][0][0])
+        # evaluateStored: the evaluation given the caches the kernels left
+        # (each new element checked against its bound), and the step's values
+        # within their bounds of it.
+        from test_bounds import kept_of
+        ev2, bd2 = B.evaluate_stored(checked, bindings(w, c, x, position), kept_of(Read, checked))
+        assert check_tiny(Read, ev2, bd2, checked, c) == []
     finally:
         s.close()
