@@ -192,16 +192,15 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
   constexpr bool NORM = PRO == FK_PRO_RMSNORM || PRO == FK_PRO_GATHER_RMSNORM;
   constexpr bool SILU = PRO == FK_PRO_SILU_MUL;
   constexpr bool RESIDUAL = EPI == FK_EPI_ADD_STORED || EPI == FK_EPI_ADD_GATHER;
-  // The input row (and the norm's gains) in LDS transposed to the lanes'
-  // packs: chunk c (4 elements) of lane l's pack it is float4 (it C + c) 64 + l,
+  // The input row (normalized, for the norm prologues) in LDS transposed to
+  // the lanes' packs: chunk c (4 elements) of lane l's pack it is float4 (it C + c) 64 + l,
   // so a wavefront reads a chunk of all its lanes' packs with one conflict-free
   // 16-byte load a lane.  XT float4s: 64 P KPL / 4 a row.
   constexpr uint32_t XT = 64 * P * KPL / 4;
-  extern __shared__ float4 lds4[];  // xt[XT], then gt[XT]
+  extern __shared__ float4 lds4[];  // xt[XT]
   __shared__ float slots[16];
   __shared__ unsigned long long bests[16];
   float4 *xt = lds4;
-  float4 *gt = lds4 + XT;
   const uint32_t k = p.k;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & (FK_WAVE - 1);
@@ -278,12 +277,10 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
         acc = acc + v.y * v.y;
         acc = acc + v.z * v.z;
         acc = acc + v.w * v.w;
-        gt[xt_at(j)] = ga[m];
       }
       xt[xt_at(j)] = v;
     } else if (j < XT) {
       xt[xt_at(j)] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if constexpr (NORM) gt[xt_at(j)] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
   }
   if constexpr (NORM) {
@@ -298,27 +295,31 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
     const float sl = slots[min(lane, waves - 1)];
     const float t = -0.0f + (lane < waves ? sl : -0.0f);
     scale = fk::rsqrt_once(fk::wave_sum(t) / (float)p.seg + eps);
-  }
-  // Chunk c of lane l's pack it of the anchors' input row: ((x scale) gamma)
-  // factor for the norm, x otherwise; both products made, one kept (a select,
-  // not a branch, so the chunk's loads are issued together).
-  auto xin4 = [&](int it, int c) -> float4 {
-    float4 v = xt[(it * C + c) * FK_WAVE + lane];
-    if constexpr (NORM) {
-      const float4 g = gt[(it * C + c) * FK_WAVE + lane];
-      float e[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
-      const float gg[4] = {g.x, g.y, g.z, g.w};
+    // The normalized row, once: each thread's own packs of 4 to ((x scale)
+    // gamma) factor (both products made, one kept by a select), written over
+    // their place; one more barrier.  Every block then reads the row as it
+    // stands instead of normalizing it again.
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float eg = e[q] * gg[q];
-        e[q] = has_gamma ? eg : e[q];
-        const float ef = e[q] * factor;
-        e[q] = factor != 1.0f ? ef : e[q];
+    for (int m = 0; m < NPK; m++) {
+      const uint32_t j = tid + m * FK_GEMV_THREADS;
+      if (j < packs4) {
+        const float4 v = xt[xt_at(j)];
+        float e[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+        const float gg[4] = {ga[m].x, ga[m].y, ga[m].z, ga[m].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float eg = e[q] * gg[q];
+          e[q] = has_gamma ? eg : e[q];
+          const float ef = e[q] * factor;
+          e[q] = factor != 1.0f ? ef : e[q];
+        }
+        xt[xt_at(j)] = make_float4(e[0], e[1], e[2], e[3]);
       }
-      v = make_float4(e[0], e[1], e[2], e[3]);
     }
-    return v;
-  };
+    __syncthreads();
+  }
+  // Chunk c of lane l's pack it of the anchors' input row.
+  auto xin4 = [&](int it, int c) -> float4 { return xt[(it * C + c) * FK_WAVE + lane]; };
   uint64_t best = 0;
   // Block `blk`'s rows from the weights `w`: the residuals loaded first (lane q
   // holds slot q's), then (with DB) the next block's weights issued into `wn`,
