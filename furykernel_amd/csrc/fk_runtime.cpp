@@ -417,6 +417,12 @@ int fk_memset_async(fk_ctx *ctx, fk_buf *dst, size_t off, int value, size_t byte
   if (!ctx) return fail(ctx, FK_ERR_ARG, "fk_memset_async: null context");
   if (int st = check_span(ctx, dst, off, bytes, "fk_memset_async")) return st;
   if (bytes == 0) return FK_OK;
+  // A memset node in a captured graph has given wrong results on replays
+  // after the first on this platform: a graph clears memory with a kernel.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  FK_HIP(ctx, hipStreamIsCapturing(stream_of(ctx, s), &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(ctx, FK_ERR_STATE, "fk_memset_async: the stream is being captured; clear memory with a kernel");
   FK_HIP(ctx, hipMemsetAsync(static_cast<char *>(dst->ptr) + off, value, bytes, stream_of(ctx, s)));
   return FK_OK;
 }

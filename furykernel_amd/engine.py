@@ -59,6 +59,82 @@ def params_struct(launch: Launch) -> ctypes.Structure:
     return s
 
 
+_ELT = {"f32": 4, "f16": 2, "bf16": 2, "u32": 4, "u16": 2, "u64": 8}
+
+
+def _gemv_needs(launch: Launch) -> dict:
+    """Bytes (and element type) each buffer of a GEMV step launch must hold
+    for every access its kernel makes: the weights and the gathered tables
+    are read as the entry's weight type, the rows as f32."""
+    p = launch.params
+    _, wt, _, _, _, epi = K.gemv_entry(launch.entry)
+    wb = _ELT[wt]
+    n, rows, k = p["n_anchors"], p["rows"], p["k"]
+    widest = max(rows[:n])
+    need = {"src": (k * 4, "f32"), "src2": (k * 4, "f32"), "gamma": (k * 4, "f32"),
+            "table": (p.get("table_rows", 1) * k * wb, wt), "token": (4, "u32"), "res_token": (4, "u32"),
+            "res": (widest * 4, "f32"), "res_table": (p.get("table_rows", 1) * widest * wb, wt),
+            "epi_out": ((rows[0] if epi == K.EPI_SILU_MUL else widest) * 4, "f32"),
+            "arg": (p.get("arg_slots", 0) * 8, "u64")}
+    for j in range(n):
+        need[f"w{j}"] = (rows[j] * k * wb, wt)
+        need[f"y{j}"] = (rows[j] * 4, "f32")
+    return need
+
+
+def _attend_needs(launch: Launch) -> dict:
+    p = launch.params
+    d, kv, heads = p["head_dim"], p["kv_heads"], p["heads"]
+    cache = "bf16" if p["cache_bf16"] else "f16"
+    return {"q": (heads * d * 4, "f32"), "knew": (kv * d * 4, "f32"), "vnew": (kv * d * 4, "f32"),
+            "kc": (p["slots"] * kv * p["length"] * d * 2, cache), "vc": (p["slots"] * kv * p["length"] * d * 2, cache),
+            "position": (4, "u32"), "slot": (4, "u32"), "rope": (p["rope_rows"] * p["rotated"] * 8, "f32"),
+            "partials": (heads * p["splits"] * (d + 2) * 4, "f32")}
+
+
+def check_launch(launch: Launch, specs: dict) -> None:
+    """Refuses (LaunchError) a launch whose kernel would dereference a buffer
+    it has not bound, whose entry's modes disagree with its parameters, or
+    (for the GEMV step and attention families) whose buffers are smaller or of
+    another type than what its kernel reads: every check made before a
+    launch's kernarg is built.  `specs` maps logical buffers to BufferSpecs."""
+    e = launch.entry
+    abi = K.ABIS.get(e)
+    if abi is None:
+        raise K.LaunchError(f"{e}: no such kernel")
+    if abi.threads and launch.threads != abi.threads:
+        raise K.LaunchError(f"{e} is compiled for {abi.threads} threads, not {launch.threads}")
+    extra = set(launch.bind) - set(abi.buffers)
+    if extra:
+        raise K.LaunchError(f"{e}: binds {sorted(extra)}, which the kernel does not take")
+    if e.startswith("fk_step_gemv"):
+        _, _, kmax, r, pro, epi = K.gemv_entry(e)
+        p = launch.params
+        if (p.get("pro_mode"), p.get("epi_mode")) != (pro, epi):
+            raise K.LaunchError(f"{e} runs prologue {pro} and epilogue {epi}; its parameters say "
+                                f"{p.get('pro_mode')} and {p.get('epi_mode')}")
+        if p["k"] > kmax or not 1 <= p["n_anchors"] <= 3:
+            raise K.LaunchError(f"{e}: k = {p['k']} past {kmax}, or {p['n_anchors']} anchors")
+        if epi == K.EPI_SILU_MUL and (p["n_anchors"] != 2 or p["rows"][0] != p["rows"][1] or r < 2):
+            raise K.LaunchError(f"{e}: the SiLU·mul epilogue on anchors {p['rows']}, blocks of {r}")
+    reads = K.launch_reads(e, launch.params)
+    unbound = sorted(b for b in reads if launch.bind.get(b) is None)
+    if unbound:
+        raise K.LaunchError(f"{e}: reads or writes {unbound}, which the launch leaves unbound")
+    needs = _gemv_needs(launch) if e.startswith("fk_step_gemv") else \
+        _attend_needs(launch) if e == "fk_step_attend" else {}
+    for b in sorted(reads & set(needs)):
+        spec = specs[launch.bind[b]]
+        nbytes, dtype = needs[b]
+        if spec.dtype != dtype:
+            raise K.LaunchError(f"{e}: {b} is {spec.name} of {spec.dtype}; the kernel reads {dtype}")
+        if spec.nbytes < nbytes:
+            raise K.LaunchError(f"{e}: {b} is {spec.name}, {spec.nbytes} bytes; the kernel touches {nbytes}")
+    arg = launch.bind.get("arg")
+    if arg is not None and launch.params.get("arg_slots", 0) > specs[arg].count:
+        raise K.LaunchError(f"{e}: {launch.params['arg_slots']} argmax slots in a buffer of {specs[arg].count}")
+
+
 class Engine:
     def __init__(self, device: runtime.Device, ks: K.Kernels, lowered: Lowered, extra_bytes: int = 0):
         self.device = device
@@ -84,12 +160,7 @@ class Engine:
 
     def _kernarg(self, launch: Launch) -> bytes:
         abi = K.ABIS[launch.entry]
-        if abi.threads and launch.threads != abi.threads:
-            raise K.LaunchError(f"{launch.entry} is compiled for {abi.threads} threads, not {launch.threads}")
-        arg = launch.bind.get("arg")
-        if arg is not None and launch.params.get("arg_slots", 0) > self.lowered.buffers[arg].count:
-            raise K.LaunchError(f"{launch.entry}: {launch.params['arg_slots']} argmax slots in a buffer of "
-                                f"{self.lowered.buffers[arg].count}")
+        check_launch(launch, self.lowered.buffers)
         bound = {}
         for b in abi.buffers:
             name = launch.bind.get(b)

@@ -15,6 +15,7 @@ a shape it would read or write past.
 from __future__ import annotations
 
 import ctypes
+import re
 import struct
 from dataclasses import dataclass
 from pathlib import Path
@@ -465,3 +466,83 @@ class Kernels:
         _need(x, rows * n * 4, "x", entry)
         _need(y, rows * n * 4, "y", entry)
         self.launch(entry, rows, threads, {"x": x.ptr, "y": y.ptr}, SoftmaxParams(rows, n), stream)
+
+
+# What each launch reads and writes: the buffers its kernel dereferences for
+# its entry and parameters.  A buffer outside this set may be unbound (passed
+# as address 0); one inside it never may.
+
+_GEMV_SUFFIX = re.compile(r"^(fk_step_gemv_(f16|f32)_k(\d+)_r(\d+))_p(\d)_e(\d)$")
+PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = range(5)
+EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX = range(5)
+
+
+def gemv_entry(entry: str) -> tuple[str, str, int, int, int, int]:
+    """(shape, weight type, widest k, rows a block, prologue, epilogue) of a
+    GEMV step entry: the kernel is specialised on the modes its name carries,
+    whatever its parameter struct says."""
+    m = _GEMV_SUFFIX.match(entry)
+    if m is None:
+        raise LaunchError(f"{entry} is not a GEMV step entry")
+    return m.group(1), m.group(2), int(m.group(3)), int(m.group(4)), int(m.group(5)), int(m.group(6))
+
+
+def gemv_reads(pro: int, epi: int, n_anchors: int, store_tile: bool) -> set[str]:
+    """The buffers a GEMV step kernel of prologue `pro` and epilogue `epi`
+    dereferences (fk_step_gemv.h): the gathers read the token unconditionally,
+    the norms their gains, and so on."""
+    need = {f"w{j}" for j in range(n_anchors)}
+    if store_tile:
+        need |= {f"y{j}" for j in range(n_anchors)}
+    if pro in (PRO_GATHER, PRO_GATHER_RMSNORM):
+        need |= {"table", "token"}
+    else:
+        need.add("src")
+    if pro == PRO_SILU_MUL:
+        need.add("src2")
+    if pro in (PRO_RMSNORM, PRO_GATHER_RMSNORM):
+        need.add("gamma")
+    if epi == EPI_ADD_STORED:
+        need |= {"res", "epi_out"}
+    elif epi == EPI_ADD_GATHER:
+        need |= {"res_table", "res_token", "epi_out"}
+    elif epi == EPI_SILU_MUL:
+        need.add("epi_out")
+    elif epi == EPI_ARGMAX:
+        need.add("arg")
+    return need
+
+
+def launch_reads(entry: str, params: dict) -> set[str]:
+    """The buffers a launch of `entry` with `params` dereferences."""
+    abi = ABIS[entry]
+    if entry.startswith("fk_step_gemv"):
+        _, _, _, _, pro, epi = gemv_entry(entry)
+        return gemv_reads(pro, epi, params["n_anchors"], bool(params.get("store_tile", 0)))
+    if entry == "fk_step_attend":
+        need = {"q", "kc", "vc", "position", "slot", "partials"}
+        if params.get("store"):
+            need |= {"knew", "vnew"}
+        if params.get("rope") or params.get("krope"):
+            need.add("rope")
+        return need
+    if entry == "fk_step_store":
+        need = {"x0", "c0", "position", "slot"}
+        if params.get("n_stores", 1) > 1:
+            need |= {"x1", "c1"}
+        if any(params.get("rope", (0, 0))):
+            need.add("rope")
+        return need
+    if entry == "fk_step_token":
+        return {"arg", "out"} | ({"token", "position"} if params.get("advance") else set())
+    if entry.startswith("fk_gemm_f16_"):
+        n = params.get("n_anchors", 1)
+        need = {"a"} | {f"b{j}" for j in range(n)} | {f"c{j}" for j in range(n)}
+        if entry == "fk_gemm_f16_add":
+            need.add("r0")
+        if entry == "fk_gemm_f16_qkv_rope":
+            need |= {"position", "slot", "rope"}
+        return need
+    if entry == "fk_rmsnorm_f32" or entry.startswith("fk_prefill_norm_pack"):
+        return set(abi.buffers) - ({"gamma"} if not params.get("has_gamma") else set())
+    return set(abi.buffers)

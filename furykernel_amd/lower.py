@@ -345,6 +345,8 @@ class _StepLowering:
         if k > MAX_K or k % 8:
             raise LoweringError(f"{step.name}: an input row of {k}, not a multiple of 8 up to {MAX_K}")
 
+        gathers: list = []
+
         def gather_of(v: int):
             n = rec.get(v)
             if n is None or not isinstance(n.op, Gather):
@@ -354,8 +356,13 @@ class _StepLowering:
                 raise LoweringError(f"{step.name}: a gather of several rows is not lowered yet")
             used.add(v)
             tname, ttype = self.weight(n.op.table)
-            params["table_rows"] = self.p.source(n.op.table).kind.dims[0]
-            params["gfactor"] = float(np.float32(n.op.factor))
+            rows_, factor = self.p.source(n.op.table).kind.dims[0], float(np.float32(n.op.factor))
+            # One launch's gathers share table_rows and gfactor (the prologue's
+            # and the epilogue's): a second gather must be of the same table.
+            if gathers and gathers[0] != (tname, rows_, factor):
+                raise LoweringError(f"{step.name}: gathers of two tables or factors in one launch")
+            gathers.append((tname, rows_, factor))
+            params["table_rows"], params["gfactor"] = rows_, factor
             return tname, self.ints(n.op.tokens), ttype
 
         # Prologue: how the anchors' input row is made.
@@ -441,7 +448,11 @@ class _StepLowering:
             g2 = gather_of(other)
             if g2 is not None:
                 epi = EPI_ADD_GATHER
-                bind["res_table"], bind["res_token"], _ = g2
+                bind["res_table"], bind["res_token"], rtype = g2
+                # The kernel reads the residual's table as the weights' type.
+                if rtype != wt:
+                    raise LoweringError(f"{step.name}: a residual gathered from a table of {rtype} under weights of "
+                                        f"{wt}; the kernel reads both as one type")
             elif self.stored_before(step, other):
                 epi = EPI_ADD_STORED
                 bind["res"] = self.value(other)

@@ -53,6 +53,10 @@ class DecoderDims:
 # The configurations: the tiny f32 decode and the 1B-class f16 decode.
 TINY = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=4, head_dim=16, ffn=256, vocab=256, context=16,
                    weight_type=F32)
+# The tiny decode with grouped queries (4 heads over 2 kv heads) and a ring of
+# 256 positions, so that attention at a position past 127 runs in two splits.
+TINY_GQA = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=2, head_dim=16, ffn=256, vocab=256, context=256,
+                       weight_type=F32)
 ONE_B = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000, context=4096)
 # The 1B prefill: four sequences of 2048 rows into a ring of 4096 positions.
 ONE_B_PREFILL = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000,

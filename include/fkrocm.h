@@ -126,8 +126,9 @@ int fk_copy_d2h_async(fk_ctx *ctx, void *dst, const fk_buf *src, size_t src_offs
                       fk_stream *stream);
 int fk_copy_d2d_async(fk_ctx *ctx, fk_buf *dst, size_t dst_offset, const fk_buf *src,
                       size_t src_offset, size_t bytes, fk_stream *stream);
-/* Sets `bytes` bytes to `value`.  Not for code a graph captures: a graph
- * clears memory with a kernel of the module instead. */
+/* Sets `bytes` bytes to `value`.  Not for code a graph captures: on a stream
+ * being captured it returns FK_ERR_STATE, and a graph clears memory with a
+ * kernel of the module instead. */
 int fk_memset_async(fk_ctx *ctx, fk_buf *dst, size_t dst_offset, int value, size_t bytes,
                     fk_stream *stream);
 

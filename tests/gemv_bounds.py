@@ -26,6 +26,14 @@ def shape_of(entry: str) -> tuple[int, int, int, int]:
     return eb, p, r, kmax // (WAVE * p)
 
 
+def modes_of(entry: str) -> tuple[int, int]:
+    """(prologue, epilogue) from the entry's `_p<pro>_e<epi>` suffix."""
+    parts = entry.split("_")
+    if not (parts[-2].startswith("p") and parts[-1].startswith("e")):
+        raise Bad(f"{entry}: no _p<prologue>_e<epilogue> suffix")
+    return int(parts[-2][1:]), int(parts[-1][1:])
+
+
 class Bad(AssertionError):
     pass
 
@@ -38,7 +46,10 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
     if launch.threads != THREADS:
         raise Bad(f"{launch.entry}: {launch.threads} threads")
     eb, P, R, KPL = shape_of(launch.entry)
-    pro, epi = prm["pro_mode"], prm["epi_mode"]
+    # The kernel is specialised on the modes its entry's name carries
+    # (<shape>_p<prologue>_e<epilogue>); its parameter struct's modes are
+    # never read on the device.
+    pro, epi = modes_of(launch.entry)
     k, n_anchors, rows, first = prm["k"], prm["n_anchors"], prm["rows"], prm["first_row"]
     blocks = prm["blocks"]
     C = P // 4
@@ -48,10 +59,18 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
     gather = pro in (PRO_GATHER, PRO_GATHER_RMSNORM)
     norm = pro in (PRO_RMSNORM, PRO_GATHER_RMSNORM)
 
+    # Element sizes the kernel reads each buffer at: the weights and the
+    # gathered tables as the entry's weight type, the argmax slots as u64, the
+    # tokens as u32, every row as f32.
+    at_size = {**{f"w{j}": eb for j in range(3)}, "table": eb, "res_table": eb, "arg": 8}
+
     def elems(name: str) -> int:
+        """The buffer's extent in elements of the size the kernel reads it at
+        (an unbound buffer is address 0: any access to it is out of bounds)."""
         if bind.get(name) is None:
-            raise Bad(f"{launch.entry}: {name} is read or written but not bound")
-        return buffers[bind[name]].count
+            raise Bad(f"{launch.entry}: {name} is read or written but not bound (address 0)")
+        spec = buffers[bind[name]]
+        return spec.count * ELT[spec.dtype] // at_size.get(name, 4)
 
     def need(name: str, idx: np.ndarray, what: str, width: int = 1) -> None:
         n = elems(name)
@@ -90,6 +109,10 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
     if at.size and at.max() >= XT:
         raise Bad(f"{launch.entry}: LDS slot {int(at.max())} of {XT}")
 
+    if epi == EPI_ADD_GATHER:
+        # The residual's token is read before the first block, by every thread.
+        need("res_token", np.array([0]), "the residual's token")
+
     # Blocks: wavefront gw takes b = gw, gw + total, ... while b < blocks, and
     # issues its first block's loads (clamped) even when gw is past the blocks.
     total_waves = groups * (THREADS // WAVE)
@@ -126,14 +149,15 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
                     need("epi_out", rl, "the epilogue row")
                     if epi == EPI_ADD_STORED:
                         need("res", np.minimum(rl, n - 1), "the residual")
-                    else:
-                        need("res_token", np.array([0]), "the residual's token")
-                        need("res_table", (prm["table_rows"] - 1) * n + np.minimum(rl, n - 1), "the gathered residual")
                 if epi == EPI_SILU_MUL and an == 0:
                     need("epi_out", rl, "the SiLU·mul row")
-            # residual loads also happen for live blocks' lanes < R with a clamped row
-            if epi == EPI_ADD_STORED and (b[sel] < blocks).any():
-                need("res", np.minimum(row[sel][b[sel] < blocks], n - 1), "the residual (clamped)")
+            # The residual of every block below `blocks` is loaded (its row
+            # clamped into the anchor), live or not.
+            ran = row[sel][b[sel] < blocks]
+            if ran.size and epi == EPI_ADD_STORED:
+                need("res", np.minimum(ran, n - 1), "the residual (clamped)")
+            if ran.size and epi == EPI_ADD_GATHER:
+                need("res_table", (prm["table_rows"] - 1) * n + np.minimum(ran, n - 1), "the gathered residual")
     if epi == EPI_ARGMAX:
         slots = prm["arg_slots"]
         if slots > elems("arg"):

@@ -18,7 +18,7 @@ import pytest
 from furykernel_amd.lower import lower_plan, rope_table
 from furykernel_amd.program.build import program
 from furykernel_amd.program.check import check_program
-from furykernel_amd.program.decoder import TINY, decoder_step
+from furykernel_amd.program.decoder import TINY, TINY_GQA, decoder_step
 from furykernel_amd.program.graph import AttnSpec, F32, Ring, RopeSpec, Shape, whole_row
 from furykernel_amd.program.plan import PlanOptions, plan
 from oracle import fkref
@@ -109,11 +109,12 @@ def test_rotation_closed_forms():
 
 # The tiny decode step -------------------------------------------------------
 
-def tiny_state(seed=2026, position=16):
+def tiny_state(seed=2026, position=16, dims=None):
     """The tiny configuration: weights, caches and the input row N(0, 0.02)
     from one seed (norm gains 1), caches rounded to their f16, at a position
     whose ring holds 16 earlier tokens."""
-    checked = check_program(decoder_step(TINY32, embed=False))
+    dims = TINY32 if dims is None else dims
+    checked = check_program(decoder_step(dims, embed=False))
     rng = np.random.default_rng(seed)
     weights, caches = {}, {}
     for src in checked.program.sources:
@@ -126,7 +127,7 @@ def tiny_state(seed=2026, position=16):
             lay = src.kind.layout
             n = lay.kv_heads * lay.length * lay.head_dim
             caches[src.name] = (rng.standard_normal(n) * 0.02).astype(np.float16)
-    x = (rng.standard_normal(TINY32.d_model) * 0.02).astype(np.float32)
+    x = (rng.standard_normal(dims.d_model) * 0.02).astype(np.float32)
     return checked, weights, caches, x, position
 
 
@@ -213,3 +214,46 @@ def test_a_dropped_rope_term_is_caught():
     finally:
         E.rotate = good
     assert rel(cpu, bad) > 1e-3
+
+
+@pytest.mark.parametrize("position", [130, 255])
+def test_tiny_gqa_decode_in_two_splits_within_1e4_of_the_f64_evaluator(position):
+    """Grouped queries (4 heads over 2 kv heads) over a ring of 256, at
+    positions whose attention runs in two splits of 128 combined: the CPU
+    target's logits within 1e-4 of the f64 evaluator, and its new cache rows
+    within f16 rounding."""
+    checked, w, c, x, _ = tiny_state(position=position, dims=TINY_GQA)
+    cpu = run_cpu_target(checked, w, c, x, position, 64)
+    attend = [L for L in cpu.lowered.launches if L.entry == "fk_step_attend"]
+    assert attend and all(L.params["splits"] == 2 and L.params["heads"] // L.params["kv_heads"] == 2 for L in attend)
+    ev = run_evaluator(checked, w, c, x, position)
+    assert rel(cpu.read("value:logits"), ev.outputs["logits"][0]) <= 1e-4
+    for layer in range(TINY_GQA.layers):
+        for kv in ("k", "v"):
+            name = f"l{layer}_{kv}_cache"
+            got = cpu.read(f"cache:{name}").astype(np.float64)
+            want = ev.caches[name][0]
+            assert np.max(np.abs(got - want)) <= 2.0**-10 * np.max(np.abs(want))
+
+
+def test_tiny_gqa_with_a_split_dropped_is_caught():
+    """The check has teeth for the combine: the CPU target run with its
+    combines told of one split fewer (the last split's positions left out)
+    misses the evaluator by far more than 1e-4."""
+    checked, w, c, x, position = tiny_state(position=255, dims=TINY_GQA)
+    good = run_cpu_target(checked, w, c, x, position, 64)
+    low = good.lowered
+    for L in low.launches:
+        if L.entry == "fk_step_combine":
+            L.params["splits"] -= 1
+    bad = CpuTarget(low, 64)
+    for name in low.buffers:
+        if not name.startswith(("partials:", "value:")) or name == "value:x":
+            bad.buffers[name][:] = good.buffers[name]
+    bad.write("value:x", x)
+    for name in c:
+        bad.write(f"cache:{name}", c[name])
+    bad.run()
+    ev = run_evaluator(checked, w, c, x, position)
+    assert rel(good.read("value:logits"), ev.outputs["logits"][0]) <= 1e-4
+    assert rel(bad.read("value:logits"), ev.outputs["logits"][0]) > 1e-3

@@ -49,3 +49,68 @@ def test_the_checker_sees_a_short_weight_buffer():
     bufs[qkv.bind["w1"]] = dataclasses.replace(w, count=w.count - 8)
     with pytest.raises(Bad):
         check_launch(qkv, bufs)
+
+
+def probe_swaps(low, key: int):
+    """The launches a grid sweep made when it put the first launch's entry of a
+    class of the step (launch i with i mod 6 == key, one per layer) onto every
+    launch of the class: its parameters and bindings stayed each launch's own."""
+    idx = [i for i in range(96) if i % 6 == key]
+    first = low.launches[idx[0]].entry
+    return [dataclasses.replace(low.launches[i], entry=first) for i in idx]
+
+
+@pytest.mark.parametrize("key,unbound", [(0, "token"), (3, "res_token")])
+def test_a_swapped_entry_reading_an_unbound_buffer_is_refused(key, unbound):
+    """Layer 0's QKV step gathers its row (_p3) and its O step adds a gathered
+    residual (_e2); layers 1-15's do not, and leave token / res_token unbound.
+    The layer-0 entry on a later layer's launch reads address 0: the CPU model
+    of the kernel's accesses and the engine's launch check both refuse it."""
+    from furykernel_amd.engine import check_launch as engine_check
+    from furykernel_amd.kernels import LaunchError
+    c = check_program(decoder_step(ONE_B, embed=True))
+    low = lower_plan(c, plan(PlanOptions(store_gelus=True), c))
+    swapped = probe_swaps(low, key)
+    assert low.launches[0 if key == 0 else 3].bind[unbound] is not None
+    refused = 0
+    for L in swapped[1:]:
+        assert L.bind[unbound] is None
+        with pytest.raises(Bad, match=f"{unbound} is read or written but not bound"):
+            check_launch(L, low.buffers)
+        with pytest.raises(LaunchError):
+            engine_check(L, low.buffers)
+        refused += 1
+    assert refused == 15
+    # The launches as lowered pass both.
+    for i in range(96):
+        if i % 6 == key:
+            check_launch(low.launches[i], low.buffers)
+            engine_check(low.launches[i], low.buffers)
+
+
+def test_the_engine_refuses_modes_that_disagree_with_the_entry():
+    from furykernel_amd.engine import check_launch as engine_check
+    from furykernel_amd.kernels import LaunchError
+    low, launches = gemv_launches(ONE_B, PlanOptions(), 1)
+    qkv = launches[0]
+    bad = dataclasses.replace(qkv, params=dict(qkv.params, pro_mode=1 if qkv.params["pro_mode"] != 1 else 0))
+    with pytest.raises(LaunchError, match="its parameters say"):
+        engine_check(bad, low.buffers)
+
+
+def test_a_gathered_table_is_read_at_the_weights_element_size():
+    """A table of f32 read by an f16 entry is the wrong type; an f16 table read
+    by an f32 entry would read twice its bytes: both refused."""
+    from furykernel_amd.engine import check_launch as engine_check
+    from furykernel_amd.kernels import LaunchError
+    c = check_program(decoder_step(ONE_B, embed=True, layers=1))
+    low = lower_plan(c, plan(PlanOptions(), c))
+    first = low.launches[0]
+    assert first.params["pro_mode"] == 3
+    bufs = dict(low.buffers)
+    t = bufs[first.bind["table"]]
+    bufs[first.bind["table"]] = dataclasses.replace(t, dtype="f32", count=t.count // 2)
+    with pytest.raises(LaunchError, match="the kernel reads f16"):
+        engine_check(first, bufs)
+    with pytest.raises(Bad):
+        check_launch(dataclasses.replace(first, entry=first.entry.replace("f16_k2048", "f32_k1024")), bufs)

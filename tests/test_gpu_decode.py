@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from furykernel_amd.decode import DecodeSession
-from furykernel_amd.program.decoder import ONE_B, TINY
+from furykernel_amd.program.decoder import ONE_B, TINY, TINY_GQA
 from furykernel_amd.program.plan import PlanOptions
 from oracle.cpu_target import CpuTarget
 
@@ -153,6 +153,39 @@ def test_tiny_decode_on_the_gpu_within_1e4_of_the_f64_evaluator(device, kernels)
         assert rel(logits, ev.outputs["logits"][0]) <= 1e-4
         cpu = run_cpu_target(checked, w, c, x, position, 64)
         assert np.array_equal(bits(logits), bits(cpu.read("value:logits")))
+        assert s.token() == int(cpu.read("value:token")[0])
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("position", [130, 255])
+def test_tiny_gqa_decode_on_the_gpu_in_two_splits(device, kernels, position):
+    """Grouped queries (4 heads over 2 kv heads, ring of 256) at positions
+    whose attention runs in two splits: the GPU's logits within 1e-4 of the
+    f64 evaluator, and logits, caches and token bit for bit the CPU target's."""
+    from test_evaluator import rel, run_cpu_target, run_evaluator, tiny_state
+
+    checked, w, c, x, _ = tiny_state(position=position, dims=TINY_GQA)
+    s = DecodeSession(device, kernels, TINY_GQA, PlanOptions(), embed=False)
+    try:
+        for name, v in w.items():
+            if f"weight:{name}" in s.lowered.buffers:
+                s.engine.write(f"weight:{name}", v)
+        for name, v in c.items():
+            s.engine.write(f"cache:{name}", v)
+        s.engine.write("value:x", x)
+        s.set_position(position)
+        print(f"tiny GQA decode vs the f64 evaluator at position {position}", flush=True)
+        s.step()
+        device.sync()
+        logits = s.logits()
+        ev = run_evaluator(checked, w, c, x, position)
+        assert rel(logits, ev.outputs["logits"][0]) <= 1e-4
+        cpu = run_cpu_target(checked, w, c, x, position, 64)
+        assert np.array_equal(bits(logits), bits(cpu.read("value:logits")))
+        for name in c:
+            assert np.array_equal(s.engine.read(f"cache:{name}").view(np.uint16),
+                                  cpu.read(f"cache:{name}").view(np.uint16)), name
         assert s.token() == int(cpu.read("value:token")[0])
     finally:
         s.close()

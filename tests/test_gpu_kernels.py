@@ -140,3 +140,23 @@ def test_softmax_64x4096(device, kernels, threads):
     e = np.exp(xd - xd.max(axis=1, keepdims=True))
     spec = e / e.sum(axis=1, keepdims=True)
     assert np.max(np.abs(got - spec) / spec) < 1e-5
+
+
+def test_memset_is_refused_while_the_stream_is_captured(device, kernels):
+    """fk_memset_async returns FK_ERR_STATE under capture (a graph clears
+    memory with a kernel); outside capture it sets the bytes."""
+    from furykernel_amd import runtime
+
+    buf = device.alloc(4096)
+    print("memset under capture", flush=True)
+    with pytest.raises(runtime.FkError) as err:
+        with device.capture() as out:
+            buf.fill_bytes(7)
+    assert err.value.status == -5
+    buf.fill_bytes(7)
+    device.sync()
+    assert np.all(buf.read(np.uint8, 4096) == 7)
+    kernels.fill_u32(buf, 0)
+    device.sync()
+    assert np.all(buf.read(np.uint32, 1024) == 0)
+    buf.free()

@@ -121,3 +121,31 @@ def test_bf16_caches_fuse_the_same_way():
     b.run()
     for name in apart.buffers:
         assert np.array_equal(a.read(name).view(np.uint8), b.read(name).view(np.uint8)), name
+
+
+def _residual_gather_program(table_type):
+    from furykernel_amd.program.build import program
+    from furykernel_amd.program.graph import F16, F32, whole_row
+
+    def body(b):
+        tokens = b.row_ints("tokens", 1, 16)
+        table = b.weight("embed", [16, 64], table_type)
+        s = b.input("s", whole_row(64), F32)
+        w = b.weight("w", [64, 64], F16)
+        x0 = b.gather("x0", table, tokens, 1.0)
+        y = b.linear("y", w, 0, s)
+        b.output("out", b.add("out", x0, y))
+    return program("residual_gather", body)
+
+
+def test_a_residual_gathered_from_a_table_of_another_type_is_refused():
+    """The GEMV step's epilogue reads the gathered residual's table as the
+    weights' element type: an f32 table under f16 weights is refused, the
+    same table in f16 lowers to the gathered-residual epilogue."""
+    from furykernel_amd.program.graph import F16, F32
+    ok = check_program(_residual_gather_program(F16))
+    low = lower_plan(ok, plan(PlanOptions(), ok))
+    assert [L.entry for L in low.launches] == ["fk_step_gemv_f16_k2048_r1_p0_e2"]
+    bad = check_program(_residual_gather_program(F32))
+    with pytest.raises(LoweringError, match="table of f32 under weights of f16"):
+        lower_plan(bad, plan(PlanOptions(), bad))
