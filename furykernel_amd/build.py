@@ -48,10 +48,10 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_runtime() -> Path:
-    src = CSRC / "fk_runtime.cpp"
+    srcs = [CSRC / "fk_runtime.cpp", CSRC / "fk_manifest.cpp"]
     tmp = RUNTIME_SO.with_suffix(".so.tmp")
     _run([HIPCC, "-shared", "-fPIC", "-O2", "-std=c++17", "-Wno-unused-value", "-Wno-unused-result",
-          f"-I{ROOT / 'include'}", str(src), "-o", str(tmp)])
+          f"-I{ROOT / 'include'}", *map(str, srcs), "-o", str(tmp)])
     os.replace(tmp, RUNTIME_SO)
     return RUNTIME_SO
 

@@ -1,0 +1,506 @@
+// fk_manifest.cpp — what each kernel of the target's code objects is: its
+// ABI (buffers in binding order with their access, type and alignment, then
+// the parameter struct's fields at their C offsets), the canonical text the
+// ABI hash covers and the hash itself (src/FuryKernel/Abi.hs:98-133,
+// abiDescription :135-162, fnv1a64 :255-262), and the checks a launch table
+// makes before it builds a launch's kernarg: the ABI hash the caller's
+// lowering carries must be the kernel's, the buffers and parameter bytes must
+// be the kernel's count and size, every buffer the kernel dereferences for its
+// entry and parameters must be bound, and (for the GEMV step and the decode
+// attention) every bound buffer must hold the bytes the kernel touches.
+//
+// Host code only: the checks run without a GPU.
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <string>
+#include <vector>
+
+#include "../../include/fkrocm.h"
+#include "../../include/fkrocm_kernels.h"
+
+namespace {
+
+struct Entry {
+  std::string entry;
+  uint32_t threads = 0;
+  std::vector<fk_abi_buffer> buffers;
+  std::vector<fk_abi_param> params;
+  uint32_t params_size = 0;
+  fk_kernel_abi abi{};
+};
+
+// Strings the manifest points at live as long as it does (a deque never
+// moves its elements).
+const char *keep(const std::string &s) {
+  static std::deque<std::string> kept;
+  kept.push_back(s);
+  return kept.back().c_str();
+}
+
+#define FK_P(S, f, ty) fk_abi_param{#f, ty, (uint32_t)offsetof(S, f)}
+#define FK_PA(S, f, i, ty) fk_abi_param{#f "_" #i, ty, (uint32_t)(offsetof(S, f) + (i) * 4)}
+
+fk_abi_buffer buf(const char *name, const char *access, const char *type) {
+  return fk_abi_buffer{name, access, type, 16};
+}
+
+std::vector<fk_abi_param> gemv_step_params() {
+  using S = fk_step_gemv_params;
+  return {FK_P(S, n_anchors, "u32"),   FK_PA(S, rows, 0, "u32"),      FK_PA(S, rows, 1, "u32"),
+          FK_PA(S, rows, 2, "u32"),    FK_PA(S, first_row, 0, "u32"), FK_PA(S, first_row, 1, "u32"),
+          FK_PA(S, first_row, 2, "u32"), FK_PA(S, first_row, 3, "u32"), FK_P(S, k, "u32"),
+          FK_P(S, pro_mode, "u32"),    FK_P(S, seg, "u32"),           FK_P(S, eps, "f32"),
+          FK_P(S, factor, "f32"),      FK_P(S, gfactor, "f32"),       FK_P(S, has_gamma, "u32"),
+          FK_P(S, epi_mode, "u32"),    FK_P(S, store_tile, "u32"),    FK_P(S, table_rows, "u32"),
+          FK_P(S, blocks, "u32"),      FK_P(S, arg_slots, "u32")};
+}
+
+std::vector<fk_abi_param> gemm_params() {
+  using S = fk_gemm_params;
+  return {FK_P(S, m, "u32"),          FK_P(S, k, "u32"),          FK_P(S, n_anchors, "u32"),
+          FK_PA(S, first_col, 0, "u32"), FK_PA(S, first_col, 1, "u32"), FK_PA(S, first_col, 2, "u32"),
+          FK_PA(S, first_col, 3, "u32"), FK_PA(S, ldc, 0, "u32"),       FK_PA(S, ldc, 1, "u32"),
+          FK_PA(S, ldc, 2, "u32")};
+}
+
+std::vector<Entry> build() {
+  std::vector<Entry> out;
+  auto add = [&](const std::string &entry, uint32_t threads, std::vector<fk_abi_buffer> b,
+                 std::vector<fk_abi_param> p, uint32_t size) {
+    Entry e;
+    e.entry = entry;
+    e.threads = threads;
+    e.buffers = std::move(b);
+    e.params = std::move(p);
+    e.params_size = size;
+    out.push_back(std::move(e));
+  };
+
+  // The standalone GEMVs, RMSNorm, softmax and helpers.
+  for (const char *wt : {"f32", "f16"})
+    for (int r : {1, 2, 4})
+      add(std::string("fk_gemv_") + wt + "_f32_r" + std::to_string(r), 0,
+          {buf("w", "read", wt), buf("x", "read", "f32"), buf("y", "write", "f32")},
+          {FK_P(fk_gemv_params, n, "u32"), FK_P(fk_gemv_params, k, "u32")}, sizeof(fk_gemv_params));
+  for (int r : {1, 2, 4})
+    add("fk_gemv_i8_f16_r" + std::to_string(r), 0,
+        {buf("w", "read", "i8"), buf("scale", "read", "f32"), buf("x", "read", "f16"), buf("y", "write", "f32")},
+        {FK_P(fk_gemv_params, n, "u32"), FK_P(fk_gemv_params, k, "u32")}, sizeof(fk_gemv_params));
+  {
+    using S = fk_rmsnorm_params;
+    add("fk_rmsnorm_f32", 0, {buf("x", "read", "f32"), buf("gamma", "read", "f32"), buf("y", "write", "f32")},
+        {FK_P(S, rows, "u32"), FK_P(S, width, "u32"), FK_P(S, seg, "u32"), FK_P(S, eps, "f32"),
+         FK_P(S, factor, "f32"), FK_P(S, has_gamma, "u32")},
+        sizeof(S));
+  }
+  add("fk_softmax_f32", 0, {buf("x", "read", "f32"), buf("y", "write", "f32")},
+      {FK_P(fk_softmax_params, rows, "u32"), FK_P(fk_softmax_params, n, "u32")}, sizeof(fk_softmax_params));
+  add("fk_fill_u32", 0, {buf("dst", "write", "u32")},
+      {FK_P(fk_fill_params, count, "u32"), FK_P(fk_fill_params, value, "u32")}, sizeof(fk_fill_params));
+  add("fk_noop", 0, {}, {FK_P(fk_noop_params, unused, "u32")}, sizeof(fk_noop_params));
+  add("fk_stream_read", 0, {buf("src", "read", "u32"), buf("out", "write", "u32")},
+      {FK_P(fk_stream_read_params, words, "u64")}, sizeof(fk_stream_read_params));
+  {
+    using S = fk_init_normal_params;
+    add("fk_init_normal", 0, {buf("dst", "write", "f32")},
+        {FK_P(S, count, "u64"), FK_P(S, seed, "u64"), FK_P(S, std, "f32"), FK_P(S, f16, "u32")}, sizeof(S));
+  }
+
+  // The GEMV step: every shape with every prologue and epilogue it is built for.
+  struct Shape {
+    const char *name, *wt;
+    bool pairs;
+  };
+  const Shape shapes[] = {{"fk_step_gemv_f16_k2048_r1", "f16", false}, {"fk_step_gemv_f16_k2048_r2", "f16", true},
+                          {"fk_step_gemv_f16_k8192_r1", "f16", false}, {"fk_step_gemv_f32_k256_r1", "f32", false},
+                          {"fk_step_gemv_f32_k256_r2", "f32", true},   {"fk_step_gemv_f32_k1024_r1", "f32", false},
+                          {"fk_step_gemv_f32_k1024_r2", "f32", true}};
+  for (const Shape &s : shapes) {
+    const char *wt = keep(s.wt);
+    std::vector<fk_abi_buffer> b = {
+        buf("w0", "read", wt),        buf("w1", "read", wt),         buf("w2", "read", wt),
+        buf("y0", "write", "f32"),    buf("y1", "write", "f32"),     buf("y2", "write", "f32"),
+        buf("src", "read", "f32"),    buf("src2", "read", "f32"),    buf("gamma", "read", "f32"),
+        buf("table", "read", wt),     buf("token", "read", "u32"),   buf("res", "read", "f32"),
+        buf("res_table", "read", wt), buf("res_token", "read", "u32"), buf("epi_out", "write", "f32"),
+        buf("arg", "read_write", "u64")};
+    for (int pro = 0; pro < 5; pro++)
+      for (int epi = 0; epi < 5; epi++) {
+        if (epi == FK_EPI_SILU_MUL && !s.pairs) continue;
+        add(std::string(s.name) + "_p" + std::to_string(pro) + "_e" + std::to_string(epi), 512, b,
+            gemv_step_params(), sizeof(fk_step_gemv_params));
+      }
+  }
+  {
+    using S = fk_step_token_params;
+    add("fk_step_token", 64,
+        {buf("arg", "read", "u64"), buf("out", "write", "u32"), buf("token", "write", "u32"),
+         buf("position", "read_write", "u32")},
+        {FK_P(S, slots, "u32"), FK_P(S, context, "u32"), FK_P(S, step, "u32"), FK_P(S, advance, "u32")}, sizeof(S));
+  }
+  {
+    using S = fk_step_store_params;
+    add("fk_step_store", 0,
+        {buf("x0", "read", "f32"), buf("x1", "read", "f32"), buf("c0", "read_write", "f16"),
+         buf("c1", "read_write", "f16"), buf("position", "read", "u32"), buf("slot", "read", "u32"),
+         buf("rope", "read", "f32")},
+        {FK_P(S, n_stores, "u32"), FK_PA(S, rope, 0, "u32"), FK_PA(S, rope, 1, "u32"), FK_P(S, kv_heads, "u32"),
+         FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"), FK_P(S, slots, "u32"), FK_P(S, rotated, "u32"),
+         FK_P(S, rope_rows, "u32"), FK_P(S, cache_bf16, "u32")},
+        sizeof(S));
+  }
+  {
+    using S = fk_step_attend_params;
+    add("fk_step_attend", 0,
+        {buf("q", "read", "f32"), buf("knew", "read", "f32"), buf("vnew", "read", "f32"),
+         buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16"), buf("position", "read", "u32"),
+         buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("partials", "write", "f32")},
+        {FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"),
+         FK_P(S, slots, "u32"), FK_P(S, splits, "u32"), FK_P(S, split, "u32"), FK_P(S, rope, "u32"),
+         FK_P(S, rotated, "u32"), FK_P(S, rope_rows, "u32"), FK_P(S, scale, "f32"), FK_P(S, window, "u32"),
+         FK_P(S, cache_bf16, "u32"), FK_P(S, store, "u32"), FK_P(S, krope, "u32")},
+        sizeof(S));
+  }
+  {
+    using S = fk_step_combine_params;
+    add("fk_step_combine", 64, {buf("partials", "read", "f32"), buf("out", "write", "f32")},
+        {FK_P(S, heads, "u32"), FK_P(S, head_dim, "u32"), FK_P(S, splits, "u32")}, sizeof(S));
+  }
+  add("fk_step_argmax", 0, {buf("x", "read", "f32"), buf("out", "write", "u32")},
+      {FK_P(fk_step_argmax_params, n, "u32")}, sizeof(fk_step_argmax_params));
+  add("fk_step_silu_mul", 0, {buf("a", "read", "f32"), buf("b", "read", "f32"), buf("y", "write", "f32")},
+      {FK_P(fk_step_silu_mul_params, n, "u32")}, sizeof(fk_step_silu_mul_params));
+  add("fk_step_advance", 0,
+      {buf("next_token", "read", "u32"), buf("token", "write", "u32"), buf("position", "read_write", "u32")},
+      {FK_P(fk_step_advance_params, context, "u32"), FK_P(fk_step_advance_params, step, "u32")},
+      sizeof(fk_step_advance_params));
+
+  // The prefill.
+  for (const char *mode : {"store", "add", "silu_mul"}) {
+    const char *ct = std::strcmp(mode, "silu_mul") == 0 ? "f16" : "f32";
+    add(std::string("fk_gemm_f16_") + mode, 256,
+        {buf("a", "read", "f16"), buf("b0", "read", "f16"), buf("b1", "read", "f16"), buf("b2", "read", "f16"),
+         buf("c0", "write", ct), buf("c1", "write", ct), buf("c2", "write", ct), buf("r0", "read", "f32")},
+        gemm_params(), sizeof(fk_gemm_params));
+  }
+  {
+    using S = fk_gemm_qkv_params;
+    std::vector<fk_abi_param> p = gemm_params();
+    p.push_back(fk_abi_param{"kv_heads", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, kv_heads))});
+    p.push_back(fk_abi_param{"rope_rows", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, rope_rows))});
+    p.push_back(fk_abi_param{"length", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, length))});
+    p.push_back(fk_abi_param{"slots", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, slots))});
+    p.push_back(fk_abi_param{"cache_bf16", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, cache_bf16))});
+    add("fk_gemm_f16_qkv_rope", 256,
+        {buf("a", "read", "f16"), buf("b0", "read", "f16"), buf("b1", "read", "f16"), buf("b2", "read", "f16"),
+         buf("c0", "write", "f16"), buf("c1", "read_write", "f16"), buf("c2", "read_write", "f16"),
+         buf("r0", "read", "f32"), buf("position", "read", "u32"), buf("slot", "read", "u32"),
+         buf("rope", "read", "f32")},
+        p, sizeof(S));
+  }
+  {
+    using S = fk_prefill_gather_params;
+    add("fk_prefill_gather", 256, {buf("table", "read", "f16"), buf("tokens", "read", "u32"), buf("x", "write", "f32")},
+        {FK_P(S, rows, "u32"), FK_P(S, width, "u32"), FK_P(S, table_rows, "u32"), FK_P(S, table_f16, "u32"),
+         FK_P(S, factor, "f32")},
+        sizeof(S));
+  }
+  {
+    using S = fk_prefill_norm_params;
+    const std::vector<fk_abi_param> p = {FK_P(S, rows, "u32"), FK_P(S, width, "u32"), FK_P(S, eps, "f32"),
+                                         FK_P(S, factor, "f32"), FK_P(S, has_gamma, "u32")};
+    const std::vector<fk_abi_buffer> b = {buf("x", "read", "f32"), buf("gamma", "read", "f32"), buf("y", "write", "f16")};
+    add("fk_prefill_norm_pack", 256, b, p, sizeof(S));
+    for (int w : {512, 1024, 2048, 4096}) add("fk_prefill_norm_pack_w" + std::to_string(w), 256, b, p, sizeof(S));
+  }
+  {
+    using S = fk_prefill_rope_params;
+    add("fk_prefill_rope_store", 0,
+        {buf("q", "read", "f32"), buf("k", "read", "f32"), buf("v", "read", "f32"), buf("position", "read", "u32"),
+         buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("qr", "write", "f16"),
+         buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16")},
+        {FK_P(S, rows, "u32"), FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"),
+         FK_P(S, rotated, "u32"), FK_P(S, rope_rows, "u32"), FK_P(S, length, "u32"), FK_P(S, slots, "u32"),
+         FK_P(S, cache_bf16, "u32")},
+        sizeof(S));
+  }
+  {
+    using S = fk_prefill_attend_params;
+    for (int g : {1, 2, 4})
+      add("fk_prefill_attend_g" + std::to_string(g), 64 * g,
+          {buf("qr", "read", "f16"), buf("kc", "read", "f16"), buf("vc", "read", "f16"),
+           buf("position", "read", "u32"), buf("slot", "read", "u32"), buf("out", "write", "f16")},
+          {FK_P(S, rows, "u32"), FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, length, "u32"),
+           FK_P(S, slots, "u32"), FK_P(S, window, "u32"), FK_P(S, cache_bf16, "u32"), FK_P(S, scale, "f32")},
+          sizeof(S));
+  }
+  add("fk_prefill_argmax", 256, {buf("x", "read", "f32"), buf("out", "write", "u32")},
+      {FK_P(fk_prefill_argmax_params, rows, "u32"), FK_P(fk_prefill_argmax_params, width, "u32")},
+      sizeof(fk_prefill_argmax_params));
+
+  for (Entry &e : out) {
+    e.abi.entry = e.entry.c_str();
+    e.abi.threads = e.threads;
+    e.abi.n_buffers = (uint32_t)e.buffers.size();
+    e.abi.buffers = e.buffers.data();
+    e.abi.n_params = (uint32_t)e.params.size();
+    e.abi.params = e.params.data();
+    e.abi.params_size = e.params_size;
+    e.abi.abi_hash = fk_abi_hash(&e.abi);
+  }
+  return out;
+}
+
+const std::vector<Entry> &manifest() {
+  static const std::vector<Entry> m = build();
+  return m;
+}
+
+std::string describe(const fk_kernel_abi *a) {
+  std::string t = "abi 1\n";
+  for (uint32_t i = 0; i < a->n_buffers; i++) {
+    const fk_abi_buffer &b = a->buffers[i];
+    t += std::string("buffer ") + b.name + " " + b.access + " " + b.type + " align " + std::to_string(b.align) + "\n";
+  }
+  for (uint32_t i = 0; i < a->n_params; i++) {
+    const fk_abi_param &p = a->params[i];
+    t += std::string("param ") + p.name + " " + p.type + " at " + std::to_string(p.offset) + "\n";
+  }
+  t += "params size " + std::to_string(a->params_size) + "\n";
+  return t;
+}
+
+// Launch checks ---------------------------------------------------------------
+
+int bad(char *err, size_t cap, int code, const char *fmt, ...) __attribute__((format(printf, 4, 5)));
+int bad(char *err, size_t cap, int code, const char *fmt, ...) {
+  if (err && cap) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, cap, fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+int index_of(const fk_kernel_abi *a, const char *name) {
+  for (uint32_t i = 0; i < a->n_buffers; i++)
+    if (std::strcmp(a->buffers[i].name, name) == 0) return (int)i;
+  return -1;
+}
+
+// The (prologue, epilogue) of a GEMV step entry: the suffix the kernel is
+// specialised on.
+bool gemv_modes(const char *entry, int *pro, int *epi, int *wbytes, int *kmax, int *r) {
+  const char *pfx = "fk_step_gemv_";
+  if (std::strncmp(entry, pfx, std::strlen(pfx)) != 0) return false;
+  char wt[8] = {0};
+  if (std::sscanf(entry + std::strlen(pfx), "%3[a-z0-9]_k%d_r%d_p%d_e%d", wt, kmax, r, pro, epi) != 5) return false;
+  *wbytes = std::strcmp(wt, "f16") == 0 ? 2 : 4;
+  return true;
+}
+
+struct Need {
+  const char *name;
+  uint64_t bytes;  // 0: only bound
+};
+
+}  // namespace
+
+extern "C" {
+
+uint64_t fk_fnv1a64(const void *bytes, size_t n) {
+  const unsigned char *p = static_cast<const unsigned char *>(bytes);
+  uint64_t h = 0xcbf29ce484222325ull;
+  for (size_t i = 0; i < n; i++) {
+    h ^= p[i];
+    h *= 0x100000001b3ull;
+  }
+  return h;
+}
+
+size_t fk_abi_description(const fk_kernel_abi *abi, char *out, size_t cap) {
+  if (!abi) return 0;
+  const std::string t = describe(abi);
+  if (out && cap) {
+    const size_t n = t.size() < cap - 1 ? t.size() : cap - 1;
+    std::memcpy(out, t.data(), n);
+    out[n] = '\0';
+  }
+  return t.size();
+}
+
+uint64_t fk_abi_hash(const fk_kernel_abi *abi) {
+  if (!abi) return 0;
+  const std::string t = describe(abi);
+  return fk_fnv1a64(t.data(), t.size());
+}
+
+int fk_manifest_count(void) { return (int)manifest().size(); }
+
+const fk_kernel_abi *fk_manifest_at(int i) {
+  const auto &m = manifest();
+  return i >= 0 && (size_t)i < m.size() ? &m[i].abi : nullptr;
+}
+
+const fk_kernel_abi *fk_manifest_find(const char *entry) {
+  if (!entry) return nullptr;
+  for (const Entry &e : manifest())
+    if (e.entry == entry) return &e.abi;
+  return nullptr;
+}
+
+int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32_t lds_bytes,
+                    const fk_binding *b, uint32_t n_buffers, const void *params, size_t params_bytes,
+                    uint64_t abi_hash, char *err, size_t cap) {
+  const fk_kernel_abi *a = fk_manifest_find(entry);
+  if (!a) return bad(err, cap, FK_ERR_NOT_FOUND, "%s: no such kernel in the manifest", entry ? entry : "(null)");
+  if (abi_hash != a->abi_hash)
+    return bad(err, cap, FK_ERR_ARG, "%s: the launch's ABI hash 0x%016llx is not the kernel's 0x%016llx", entry,
+               (unsigned long long)abi_hash, (unsigned long long)a->abi_hash);
+  if (n_buffers != a->n_buffers)
+    return bad(err, cap, FK_ERR_ARG, "%s: %u buffers bound, the kernel takes %u", entry, n_buffers, a->n_buffers);
+  if (params_bytes != a->params_size || (a->params_size && !params))
+    return bad(err, cap, FK_ERR_ARG, "%s: %zu parameter bytes, the kernel's struct is %u", entry, params_bytes,
+               a->params_size);
+  if (n_buffers && !b) return bad(err, cap, FK_ERR_ARG, "%s: null bindings", entry);
+  if (threads == 0 || threads > 1024 || (a->threads && threads != a->threads))
+    return bad(err, cap, FK_ERR_RANGE, "%s: %u threads a group (the kernel is built for %u)", entry, threads,
+               a->threads);
+  if (lds_bytes > 160 * 1024)
+    return bad(err, cap, FK_ERR_RANGE, "%s: %u bytes of threadgroup memory, more than 160 KiB", entry, lds_bytes);
+  (void)groups;
+
+  std::vector<Need> need;
+  int pro = 0, epi = 0, wb = 0, kmax = 0, r = 0;
+  if (gemv_modes(entry, &pro, &epi, &wb, &kmax, &r)) {
+    fk_step_gemv_params p;
+    std::memcpy(&p, params, sizeof p);
+    if ((int)p.pro_mode != pro || (int)p.epi_mode != epi)
+      return bad(err, cap, FK_ERR_ARG, "%s runs prologue %d and epilogue %d; its parameters say %u and %u", entry,
+                 pro, epi, p.pro_mode, p.epi_mode);
+    if (p.n_anchors < 1 || p.n_anchors > 3 || p.k == 0 || (int)p.k > kmax)
+      return bad(err, cap, FK_ERR_RANGE, "%s: %u anchors, k = %u (at most %d)", entry, p.n_anchors, p.k, kmax);
+    uint64_t widest = 0;
+    for (uint32_t j = 0; j < p.n_anchors; j++) widest = p.rows[j] > widest ? p.rows[j] : widest;
+    if (epi == FK_EPI_SILU_MUL && (p.n_anchors != 2 || p.rows[0] != p.rows[1] || r < 2))
+      return bad(err, cap, FK_ERR_ARG, "%s: the SiLU·mul epilogue on %u anchors, blocks of %d", entry, p.n_anchors, r);
+    static const char *w[3] = {"w0", "w1", "w2"}, *y[3] = {"y0", "y1", "y2"};
+    for (uint32_t j = 0; j < p.n_anchors; j++) {
+      need.push_back({w[j], (uint64_t)p.rows[j] * p.k * wb});
+      if (p.store_tile) need.push_back({y[j], (uint64_t)p.rows[j] * 4});
+    }
+    const uint64_t k4 = (uint64_t)p.k * 4;
+    if (pro == FK_PRO_GATHER || pro == FK_PRO_GATHER_RMSNORM) {
+      need.push_back({"table", (uint64_t)p.table_rows * p.k * wb});
+      need.push_back({"token", 4});
+    } else {
+      need.push_back({"src", k4});
+    }
+    if (pro == FK_PRO_SILU_MUL) need.push_back({"src2", k4});
+    if (pro == FK_PRO_RMSNORM || pro == FK_PRO_GATHER_RMSNORM) need.push_back({"gamma", k4});
+    if (epi == FK_EPI_ADD_STORED) {
+      need.push_back({"res", widest * 4});
+      need.push_back({"epi_out", widest * 4});
+    } else if (epi == FK_EPI_ADD_GATHER) {
+      need.push_back({"res_table", (uint64_t)p.table_rows * widest * wb});
+      need.push_back({"res_token", 4});
+      need.push_back({"epi_out", widest * 4});
+    } else if (epi == FK_EPI_SILU_MUL) {
+      need.push_back({"epi_out", (uint64_t)p.rows[0] * 4});
+    } else if (epi == FK_EPI_ARGMAX) {
+      need.push_back({"arg", (uint64_t)p.arg_slots * 8});
+    }
+  } else if (std::strcmp(entry, "fk_step_attend") == 0) {
+    fk_step_attend_params p;
+    std::memcpy(&p, params, sizeof p);
+    if (p.kv_heads == 0 || p.heads % p.kv_heads || p.head_dim == 0 || p.head_dim > 64 || p.head_dim % 8 ||
+        (p.split != 64 && p.split != 128) || p.heads / p.kv_heads > 8 || groups != p.kv_heads * p.splits)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u heads over %u, width %u, splits of %u, %u groups for %u splits", entry,
+                 p.heads, p.kv_heads, p.head_dim, p.split, groups, p.splits);
+    const uint64_t cache = (uint64_t)p.slots * p.kv_heads * p.length * p.head_dim * 2;
+    need = {{"q", (uint64_t)p.heads * p.head_dim * 4},
+            {"kc", cache},
+            {"vc", cache},
+            {"position", 4},
+            {"slot", 4},
+            {"partials", (uint64_t)p.heads * p.splits * (p.head_dim + 2) * 4}};
+    if (p.store) {
+      need.push_back({"knew", (uint64_t)p.kv_heads * p.head_dim * 4});
+      need.push_back({"vnew", (uint64_t)p.kv_heads * p.head_dim * 4});
+    }
+    if (p.rope || p.krope) need.push_back({"rope", (uint64_t)p.rope_rows * p.rotated * 8});
+  } else if (std::strcmp(entry, "fk_step_combine") == 0) {
+    fk_step_combine_params p;
+    std::memcpy(&p, params, sizeof p);
+    need = {{"partials", (uint64_t)p.heads * p.splits * (p.head_dim + 2) * 4},
+            {"out", (uint64_t)p.heads * p.head_dim * 4}};
+  } else if (std::strcmp(entry, "fk_step_store") == 0) {
+    fk_step_store_params p;
+    std::memcpy(&p, params, sizeof p);
+    need = {{"x0", 0}, {"c0", 0}, {"position", 4}, {"slot", 4}};
+    if (p.n_stores > 1) {
+      need.push_back({"x1", 0});
+      need.push_back({"c1", 0});
+    }
+    if (p.rope[0] || p.rope[1]) need.push_back({"rope", 0});
+  } else if (std::strcmp(entry, "fk_step_token") == 0) {
+    fk_step_token_params p;
+    std::memcpy(&p, params, sizeof p);
+    need = {{"arg", (uint64_t)p.slots * 8}, {"out", 4}};
+    if (p.advance) {
+      need.push_back({"token", 4});
+      need.push_back({"position", 4});
+    }
+  } else if (std::strncmp(entry, "fk_gemm_f16_", 12) == 0) {
+    fk_gemm_params p;
+    std::memcpy(&p, params, sizeof p);
+    static const char *bn[3] = {"b0", "b1", "b2"}, *cn[3] = {"c0", "c1", "c2"};
+    need.push_back({"a", 0});
+    for (uint32_t j = 0; j < p.n_anchors && j < 3; j++) {
+      need.push_back({bn[j], 0});
+      need.push_back({cn[j], 0});
+    }
+    if (std::strcmp(entry, "fk_gemm_f16_add") == 0) need.push_back({"r0", 0});
+    if (std::strcmp(entry, "fk_gemm_f16_qkv_rope") == 0) {
+      need.push_back({"position", 0});
+      need.push_back({"slot", 0});
+      need.push_back({"rope", 0});
+    }
+  } else {
+    // Every other kernel dereferences each of its buffers (a norm without
+    // gains excepted).
+    bool gains = true;
+    if (std::strcmp(entry, "fk_rmsnorm_f32") == 0) {
+      fk_rmsnorm_params p;
+      std::memcpy(&p, params, sizeof p);
+      gains = p.has_gamma != 0;
+    } else if (std::strncmp(entry, "fk_prefill_norm_pack", 20) == 0) {
+      fk_prefill_norm_params p;
+      std::memcpy(&p, params, sizeof p);
+      gains = p.has_gamma != 0;
+    }
+    for (uint32_t i = 0; i < a->n_buffers; i++)
+      if (gains || std::strcmp(a->buffers[i].name, "gamma") != 0) need.push_back({a->buffers[i].name, 0});
+  }
+  for (const Need &n : need) {
+    const int i = index_of(a, n.name);
+    if (i < 0) return bad(err, cap, FK_ERR_ARG, "%s: no buffer %s", entry, n.name);
+    if (b[i].addr == 0)
+      return bad(err, cap, FK_ERR_ARG, "%s: reads or writes %s, which the launch leaves unbound", entry, n.name);
+    if (b[i].addr % a->buffers[i].align)
+      return bad(err, cap, FK_ERR_ARG, "%s: %s at 0x%llx is not %u-byte aligned", entry, n.name,
+                 (unsigned long long)b[i].addr, a->buffers[i].align);
+    if (n.bytes && b[i].bytes < n.bytes)
+      return bad(err, cap, FK_ERR_RANGE, "%s: %s holds %llu bytes, the kernel touches %llu", entry, n.name,
+                 (unsigned long long)b[i].bytes, (unsigned long long)n.bytes);
+  }
+  return FK_OK;
+}
+
+}  // extern "C"

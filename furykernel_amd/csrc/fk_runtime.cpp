@@ -32,6 +32,7 @@ struct fk_ctx {
   std::set<fk_stream *> streams;
   std::set<fk_event *> events;
   std::set<fk_graph *> graphs;
+  std::set<fk_table *> tables;
   std::set<void *> host;
 };
 
@@ -76,6 +77,16 @@ struct fk_graph {
   fk_ctx *ctx;
   hipGraph_t graph;
   hipGraphExec_t exec;
+};
+
+struct fk_table {
+  struct Launch {
+    fk_fn *fn;
+    uint32_t groups, threads, lds_bytes;
+    std::vector<unsigned char> kernarg;
+  };
+  fk_ctx *ctx;
+  std::vector<Launch> launches;
 };
 
 namespace {
@@ -177,6 +188,7 @@ int fk_fini(fk_ctx *ctx) {
     hipModuleUnload(m->mod);
     delete m;
   }
+  for (fk_table *t : ctx->tables) delete t;
   for (void *p : ctx->host) hipHostFree(p);
   hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -481,6 +493,62 @@ int fk_launch(fk_fn *fn, uint32_t groups, uint32_t threads, uint32_t lds_bytes, 
   hipError_t e = hipModuleLaunchKernel(fn->fn, groups, 1, 1, threads, 1, 1, lds_bytes, stream_of(ctx, s), nullptr,
                                        kernarg_bytes ? config : nullptr);
   if (e != hipSuccess) return fail(ctx, FK_ERR_HIP, "fk_launch %s: %s", fn->entry.c_str(), hipGetErrorString(e));
+  return FK_OK;
+}
+
+// Launch tables ---------------------------------------------------------------
+
+int fk_table_create(fk_ctx *ctx, fk_table **out) {
+  if (!ctx || !out) return fail(ctx, FK_ERR_ARG, "fk_table_create: null argument");
+  fk_table *t = new fk_table{ctx, {}};
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->tables.insert(t);
+  *out = t;
+  return FK_OK;
+}
+
+int fk_table_destroy(fk_table *t) {
+  if (!t) return fail(nullptr, FK_ERR_ARG, "fk_table_destroy: null table");
+  {
+    std::lock_guard<std::mutex> lock(t->ctx->mu);
+    t->ctx->tables.erase(t);
+  }
+  delete t;
+  return FK_OK;
+}
+
+int fk_table_add(fk_table *t, fk_fn *fn, uint32_t groups, uint32_t threads, uint32_t lds_bytes,
+                 const fk_binding *buffers, uint32_t n_buffers, const void *params, size_t params_bytes,
+                 uint64_t abi_hash, uint32_t *index) {
+  if (!t || !fn) return fail(t ? t->ctx : nullptr, FK_ERR_ARG, "fk_table_add: null table or function");
+  char err[512];
+  const int st = fk_launch_check(fn->entry.c_str(), groups, threads, lds_bytes, buffers, n_buffers, params,
+                                 params_bytes, abi_hash, err, sizeof err);
+  if (st != FK_OK) return fail(t->ctx, st, "fk_table_add: %s", err);
+  fk_table::Launch l{fn, groups, threads, lds_bytes, {}};
+  l.kernarg.resize(8 * (size_t)n_buffers + params_bytes);
+  for (uint32_t i = 0; i < n_buffers; i++) std::memcpy(l.kernarg.data() + 8 * i, &buffers[i].addr, 8);
+  if (params_bytes) std::memcpy(l.kernarg.data() + 8 * (size_t)n_buffers, params, params_bytes);
+  t->launches.push_back(std::move(l));
+  if (index) *index = (uint32_t)(t->launches.size() - 1);
+  return FK_OK;
+}
+
+int fk_table_count(const fk_table *t, uint32_t *count) {
+  if (!t || !count) return fail(t ? t->ctx : nullptr, FK_ERR_ARG, "fk_table_count: null argument");
+  *count = (uint32_t)t->launches.size();
+  return FK_OK;
+}
+
+int fk_table_enqueue(fk_table *t, uint32_t first, uint32_t count, fk_stream *s) {
+  if (!t) return fail(nullptr, FK_ERR_ARG, "fk_table_enqueue: null table");
+  if (first > t->launches.size() || count > t->launches.size() - first)
+    return fail(t->ctx, FK_ERR_RANGE, "fk_table_enqueue: launches [%u, %u) of %zu", first, first + count,
+                t->launches.size());
+  for (uint32_t i = first; i < first + count; i++) {
+    const fk_table::Launch &l = t->launches[i];
+    if (int st = fk_launch(l.fn, l.groups, l.threads, l.lds_bytes, l.kernarg.data(), l.kernarg.size(), s)) return st;
+  }
   return FK_OK;
 }
 

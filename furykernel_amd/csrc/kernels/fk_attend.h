@@ -29,16 +29,6 @@
 // from the scores' registers and Vᵀ read transposed out of V's rows
 // (ds_read_b64_tr_b16).  Head dimension 64.  Output: O / sum into the tile
 // layout of [rows, heads · 64], the output projection's A.
-struct fk_prefill_attend_params {
-  uint32_t rows;        // a multiple of 32
-  uint32_t heads;
-  uint32_t kv_heads;    // heads / kv_heads (G) is 1, 2 or 4
-  uint32_t length;      // ring length, a multiple of 64
-  uint32_t slots;
-  uint32_t window;      // 0: none; else a row sees positions > position - window
-  uint32_t cache_bf16;
-  float scale;
-};
 
 #define FK_ATT_KB 64     // keys a block
 // Staged rows are 64 halves (128 bytes), swizzled rather than padded.  K: a

@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../../include/fkrocm_kernels.h"
+
 #define FK_WAVE 64
 
 namespace fk {

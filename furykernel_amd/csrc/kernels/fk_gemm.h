@@ -49,36 +49,7 @@
 #define FK_GEMM_LDS (FK_GEMM_STAGES * 2 * FK_GEMM_BM * FK_GEMM_BK * 2)
 #define FK_LDS __attribute__((address_space(3)))
 
-
-enum : uint32_t {
-  FK_GEMM_STORE = 0,     // C = A Bᵀ (f32 rows)
-  FK_GEMM_ADD = 1,       // C = R + A Bᵀ (f32 rows), R [M, ldc]; R may be C
-  FK_GEMM_SILU_MUL = 2,  // C = f16(silu(A Gᵀ) · (A Uᵀ)) in the tile layout; B0 the paired gate/up weights
-  FK_GEMM_QKV_ROPE = 3,  // anchors q, k, v: q RoPE'd into f16 rows (C0), k RoPE'd into the K cache (C1), v
-                         // into the V cache (C2), at each row's slot and position
-};
-
-struct fk_gemm_params {
-  uint32_t m;            // rows of A and C, a multiple of 256
-  uint32_t k;            // a multiple of 64
-  uint32_t n_anchors;    // 1 to 3 weights (SiLU·mul: 1, the pair)
-  uint32_t first_col[4]; // anchor j's columns of C are [first_col[j], first_col[j + 1]), each a multiple of 256
-  uint32_t ldc[3];       // row stride of anchor j's output (its columns; SiLU·mul: N, gate's rows)
-};
-
 // The QKV epilogue's RoPE and caches (heads of 64, every pair turned).
-struct fk_gemm_rope_params {
-  uint32_t kv_heads;
-  uint32_t rope_rows;    // positions the RoPE table holds
-  uint32_t length;       // ring length
-  uint32_t slots;
-  uint32_t cache_bf16;
-};
-
-struct fk_gemm_qkv_params {
-  fk_gemm_params g;
-  fk_gemm_rope_params r;
-};
 
 // One threadgroup's tile.  MODE: the epilogue.
 template <uint32_t MODE>

@@ -251,10 +251,6 @@ __device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, con
 // Entry points: a threadgroup of W wavefronts takes W * R consecutive rows;
 // rows of at most 64 KPL packs take the all-in-flight form.
 // Kernargs: the buffers in binding order, then the parameter struct.
-struct fk_gemv_params {
-  uint32_t n;  // rows of W (outputs)
-  uint32_t k;  // columns of W (inputs), a multiple of the pack
-};
 
 #define FK_GEMV_ENTRY(NAME, WT, XT, P, R, KPL)                                                                 \
   extern "C" __global__ void __launch_bounds__(256) NAME(const WT *__restrict__ w, const XT *__restrict__ x, \

@@ -5,24 +5,11 @@
 
 #include "fk_common.h"
 
-struct fk_fill_params {
-  uint32_t count;  // 32-bit words
-  uint32_t value;
-};
-
 extern "C" __global__ void __launch_bounds__(256) fk_fill_u32(uint32_t *__restrict__ dst, fk_fill_params p) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < p.count; i += gridDim.x * blockDim.x) dst[i] = p.value;
 }
 
-struct fk_noop_params {
-  uint32_t unused;
-};
-
 extern "C" __global__ void __launch_bounds__(1024) fk_noop(fk_noop_params) {}
-
-struct fk_stream_read_params {
-  uint64_t words;  // 16-byte words to read
-};
 
 // Reads a buffer once, 16 bytes a lane, grid-strided, and stores one word a
 // threadgroup: the attainable HBM read bandwidth, the ceiling the

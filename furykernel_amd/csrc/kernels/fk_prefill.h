@@ -24,13 +24,6 @@
 // x[r] = table[tokens[r]] · factor.  One wave a row, 4 columns a lane at a
 // time; rows × width f32 out.  A token past the table reads its last row
 // (the host refuses such tokens before they get here).
-struct fk_prefill_gather_params {
-  uint32_t rows;
-  uint32_t width;       // a multiple of 4
-  uint32_t table_rows;
-  uint32_t table_f16;   // the table is f16 (else f32)
-  float factor;
-};
 
 extern "C" __global__ void __launch_bounds__(256) fk_prefill_gather(const void *__restrict__ table,
                                                                     const uint32_t *__restrict__ tokens,
@@ -59,13 +52,6 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_gather(const void *
 // [rows, width] matrix.  One wave a row: a pass for the sum of squares (a
 // lane's units, then the wave's tree), a pass (the row now in L2) for the
 // output, one 16-byte unit of 8 columns a lane at a time.
-struct fk_prefill_norm_params {
-  uint32_t rows;      // a multiple of 256
-  uint32_t width;     // a multiple of 32
-  float eps;
-  float factor;
-  uint32_t has_gamma;
-};
 
 extern "C" __global__ void __launch_bounds__(256) fk_prefill_norm_pack(const float *__restrict__ x,
                                                                        const float *__restrict__ gamma,
@@ -163,17 +149,6 @@ FK_NORM_PACK_HELD(4096, 8)
 // ([slots][kv_heads][length][d], f16 or bf16) at (slot, head, position mod
 // length).  One threadgroup a row.  The cache stores round as the decode
 // step's stores do (narrowF16 / narrowBF16).
-struct fk_prefill_rope_params {
-  uint32_t rows;
-  uint32_t heads;
-  uint32_t kv_heads;
-  uint32_t head_dim;
-  uint32_t rotated;    // pairs RoPE turns
-  uint32_t rope_rows;  // positions the RoPE table holds
-  uint32_t length;     // ring length
-  uint32_t slots;
-  uint32_t cache_bf16;
-};
 
 extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
@@ -208,10 +183,6 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store(
 // of equals, by the decode step's 64-bit keys (value order, then the
 // complement of the index; a NaN at index 0 wins, elsewhere loses:
 // src/FuryKernel/Program/Eval.hs:681-685).  One wave a row.
-struct fk_prefill_argmax_params {
-  uint32_t rows;
-  uint32_t width;
-};
 
 extern "C" __global__ void __launch_bounds__(256) fk_prefill_argmax(const float *__restrict__ x,
                                                                     uint32_t *__restrict__ out,

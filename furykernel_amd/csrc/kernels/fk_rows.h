@@ -11,15 +11,6 @@
 
 #include "fk_common.h"
 
-struct fk_rmsnorm_params {
-  uint32_t rows;    // rows of x
-  uint32_t width;   // elements per row
-  uint32_t seg;     // elements per segment (a multiple of 4 dividing width)
-  float eps;        // rounded once to binary32
-  float factor;     // a constant factor; 1 multiplies by nothing
-  uint32_t has_gamma;
-};
-
 namespace fk {
 
 // Segments of at most H packs a thread: the thread's packs (t, t + T, ...)
@@ -113,11 +104,6 @@ extern "C" __global__ void __launch_bounds__(1024)
     *reinterpret_cast<float4 *>(ys + 4 * (size_t)j) = make_float4(o[0], o[1], o[2], o[3]);
   }
 }
-
-struct fk_softmax_params {
-  uint32_t rows;
-  uint32_t n;  // elements per row, a multiple of 4
-};
 
 // One threadgroup per row: exp(x - max) / sum, the maximum from -inf and the
 // sum from -0, exp in binary64 rounded once.

@@ -26,19 +26,6 @@
 
 // KV stores ----------------------------------------------------------------
 
-
-struct fk_step_store_params {
-  uint32_t n_stores;    // 1 or 2
-  uint32_t rope[2];     // store j's value is RoPE'd first
-  uint32_t kv_heads;
-  uint32_t head_dim;
-  uint32_t length;      // the ring's positions
-  uint32_t slots;       // the ring's sequences
-  uint32_t rotated;     // pairs turned
-  uint32_t rope_rows;   // positions the RoPE table holds
-  uint32_t cache_bf16;  // the caches round to bf16 (else f16)
-};
-
 // One threadgroup: every element of one row's kv heads, for each store, at
 // ((s * kvHeads + h) * length + pos mod length) * headDim (Graph.hs:138-143).
 extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
@@ -73,24 +60,6 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
 // A key row in LDS: 64 halves and 8 of padding (144 bytes), so that lanes
 // reading 16 bytes of consecutive rows hit distinct banks.
 #define FK_ATTN_KROW (FK_ATTN_MAX_DIM + 8)
-
-struct fk_step_attend_params {
-  uint32_t heads;
-  uint32_t kv_heads;
-  uint32_t head_dim;  // a multiple of 8, at most 64
-  uint32_t length;    // the ring's positions
-  uint32_t slots;
-  uint32_t splits;    // threadgroups per kv head
-  uint32_t split;     // positions a split covers: split t is [t split, (t + 1) split); 64 or 128
-  uint32_t rope;      // q is RoPE'd first
-  uint32_t rotated;
-  uint32_t rope_rows;
-  float scale;        // the attention's scale, rounded once to binary32
-  uint32_t window;    // 0: none
-  uint32_t cache_bf16;
-  uint32_t store;     // the new key and value rows are stored into the caches first
-  uint32_t krope;     // the stored key row is RoPE'd first (q's table)
-};
 
 namespace fk {
 
@@ -417,12 +386,6 @@ extern "C" __global__ void __launch_bounds__(FK_ATTN_THREADS)
     fk::attend_split<0, 0, 0, -1>(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, p);
 }
 
-struct fk_step_combine_params {
-  uint32_t heads;
-  uint32_t head_dim;
-  uint32_t splits;
-};
-
 // Threadgroup (one wavefront) per head: M the largest of the splits' maxima
 // (exact whatever the order), the splits' weights w_t = exp(max_t - M),
 // binary64's rounded once, then lane i: out_i = (sum_t acc_t[i] w_t) /
@@ -541,10 +504,6 @@ extern "C" __global__ void __launch_bounds__(FK_WAVE)
   }
 }
 
-struct fk_step_argmax_params {
-  uint32_t n;
-};
-
 namespace fk {
 // Of two (value, index) candidates, the larger value; of equal values (or
 // values neither larger), the lower index: the fold of Eval.hs:681-685 where
@@ -591,21 +550,12 @@ extern "C" __global__ void __launch_bounds__(1024)
   }
 }
 
-struct fk_step_silu_mul_params {
-  uint32_t n;
-};
-
 extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
     fk_step_silu_mul(const float *__restrict__ a, const float *__restrict__ b, float *__restrict__ y,
                      fk_step_silu_mul_params p) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < p.n) y[i] = fk::silu_mul(a[i], b[i]);
 }
-
-struct fk_step_advance_params {
-  uint32_t context;  // positions wrap below this
-  uint32_t step;     // positions advance by this (0 holds the position)
-};
 
 // The next decode step's inputs: its token is this step's greedy token, its
 // position `step` more.
@@ -616,13 +566,6 @@ extern "C" __global__ void fk_step_advance(const uint32_t *__restrict__ next_tok
     position[0] = (position[0] + p.step) % p.context;
   }
 }
-
-struct fk_init_normal_params {
-  uint64_t count;
-  uint64_t seed;
-  float std;
-  uint32_t f16;  // store binary16 (else binary32)
-};
 
 // Synthetic weights: element i is std * N(0, 1), the normal by Box-Muller from
 // the SplitMix64 stream of `seed` (uniforms (u >> 40) 2^-24), rounded once to

@@ -36,42 +36,6 @@
 // the launch's size costs the kernel a load from the dispatch packet.
 #define FK_GEMV_THREADS 512
 
-// Prologue modes: how a GEMV step's threadgroups make the anchors' input row.
-enum : uint32_t {
-  FK_PRO_STORED = 0,          // x = src
-  FK_PRO_RMSNORM = 1,         // x = rmsnorm(src) * gamma * factor
-  FK_PRO_GATHER = 2,          // x = table[token] * gfactor
-  FK_PRO_GATHER_RMSNORM = 3,  // x = rmsnorm(table[token] * gfactor) * gamma * factor
-  FK_PRO_SILU_MUL = 4,        // x = silu(src) * src2
-};
-
-// Epilogue modes: work on the anchors' tile.
-enum : uint32_t {
-  FK_EPI_NONE = 0,
-  FK_EPI_ADD_STORED = 1,  // out = res + tile
-  FK_EPI_ADD_GATHER = 2,  // out = table[token] * gfactor + tile
-  FK_EPI_SILU_MUL = 3,    // out = silu(tile of anchor 0) * tile of anchor 1 (a stored SiLU·mul, folded in)
-  FK_EPI_ARGMAX = 4,      // arg = max(arg, argmax key of each row) (the greedy token, folded in)
-};
-
-struct fk_step_gemv_params {
-  uint32_t n_anchors;     // 1 to 3
-  uint32_t rows[3];       // each anchor's outputs
-  uint32_t first_row[4];  // anchor j's rows are [first_row[j], first_row[j + 1]) of the numbered rows
-  uint32_t k;             // the input row's width
-  uint32_t pro_mode;
-  uint32_t seg;           // RMSNorm's segment: the row (k)
-  float eps;
-  float factor;           // RMSNorm's factor
-  float gfactor;          // the gather's factor
-  uint32_t has_gamma;
-  uint32_t epi_mode;
-  uint32_t store_tile;    // the anchors' own values are stored (into y[j])
-  uint32_t table_rows;    // the gathered table's rows: a token past them reads its last (the engine refuses one)
-  uint32_t blocks;        // row blocks
-  uint32_t arg_slots;     // the argmax epilogue's slots (one a threadgroup); a threadgroup past them stores none
-};
-
 namespace fk {
 
 // SiLU(a) · b: a / (1 + e^-a), e^-a binary64's rounded once, then times b.
@@ -484,13 +448,6 @@ FK_STEP_GEMV_SHAPE(fk_step_gemv_f32_k256_r1, float, 4, 1, 1, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k256_r2, float, 4, 2, 1, false)
 FK_STEP_GEMV_SHAPE(fk_step_gemv_f32_k1024_r1, float, 4, 1, 4, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k1024_r2, float, 4, 2, 4, false)
-
-struct fk_step_token_params {
-  uint32_t slots;    // the folded argmax's slots: one a threadgroup of the logits' step
-  uint32_t context;  // positions wrap below this
-  uint32_t step;     // positions advance by this (0 holds the position)
-  uint32_t advance;  // also set the next step's token and position
-};
 
 // The greedy token from the folded argmax: the largest of the threadgroups'
 // keys (exact whatever the order), its index the complement of the key's low

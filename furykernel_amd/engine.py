@@ -155,17 +155,22 @@ class Engine:
                 self.write(name, np.ones(specs[name].count, np.float32))
             else:
                 raise ValueError(f"{name}: no constant {what[0]}")
-        self._kernargs = [self._kernarg(launch) for launch in lowered.launches]
-        self._fns = [ks.fn(launch.entry) for launch in lowered.launches]
+        # The step's launches in a native launch table: each checked once
+        # (here, against the buffers' types; in the library, against the
+        # kernel's manifest) and kept with its kernarg.
+        self.table = runtime.Table(device)
+        for launch in lowered.launches:
+            self._add(launch)
+        self._advance: dict = {}
 
-    def _kernarg(self, launch: Launch) -> bytes:
-        abi = K.ABIS[launch.entry]
+    def _add(self, launch: Launch) -> int:
         check_launch(launch, self.lowered.buffers)
-        bound = {}
-        for b in abi.buffers:
+        spans = []
+        for b in K.ABIS[launch.entry].buffers:
             name = launch.bind.get(b)
-            bound[b] = 0 if name is None else self.buffers[name].ptr
-        return abi.kernarg(bound, params_struct(launch))
+            spans.append((0, 0) if name is None else (self.buffers[name].ptr, self.lowered.buffers[name].nbytes))
+        return self.table.add(self.kernels.fn(launch.entry), launch.groups, launch.threads, launch.lds_bytes, spans,
+                              params_struct(launch))
 
     # State -------------------------------------------------------------------
 
@@ -210,26 +215,38 @@ class Engine:
         """Queues every launch of the step (or those at the indices `only`),
         in plan order; with `advance`, then the next step's token and
         position (see ``enqueue_advance``)."""
-        picks = list(range(len(self.lowered.launches))) if only is None else list(only)
-        last = len(self.lowered.launches) - 1
+        n = len(self.lowered.launches)
+        picks = list(range(n)) if only is None else list(only)
+        last = n - 1
         folded = advance is not None and self.lowered.launches[last].entry == "fk_step_token" and \
             (not picks or picks[-1] == last)
-        for i in picks:
-            launch = self.lowered.launches[i]
-            kernarg = self._advance_kernarg(launch, **advance) if folded and i == last else self._kernargs[i]
-            self._fns[i].launch(launch.groups, launch.threads, kernarg, launch.lds_bytes, stream)
+        if folded:
+            picks[-1] = self._advance_index(**advance)
+        # runs of consecutive indices go to the table in one call each
+        i = 0
+        while i < len(picks):
+            j = i
+            while j + 1 < len(picks) and picks[j + 1] == picks[j] + 1:
+                j += 1
+            self.table.enqueue(picks[i], j - i + 1, stream)
+            i = j + 1
         if advance is not None and not folded:
             self.enqueue_advance(stream=stream, **advance)
 
-    def _advance_kernarg(self, launch: Launch, token_out: str, token_in: str, position: str, context: int,
-                         step: int = 1) -> bytes:
-        """The token launch that also advances: the greedy token it makes is
-        the next step's token, the position `step` on."""
-        if launch.bind["out"] != token_out:
-            raise ValueError(f"the step's token is {launch.bind['out']}, not {token_out}")
-        bind = dict(launch.bind, token=token_in, position=position)
-        params = dict(launch.params, context=context, step=step, advance=1)
-        return self._kernarg(Launch(launch.step, launch.entry, launch.groups, launch.threads, bind, params))
+    def _advance_index(self, token_out: str, token_in: str, position: str, context: int, step: int = 1) -> int:
+        """The token launch that also advances (the greedy token it makes is
+        the next step's token, the position `step` on), added to the table
+        once per set of arguments."""
+        key = (token_out, token_in, position, context, step)
+        if key not in self._advance:
+            launch = self.lowered.launches[-1]
+            if launch.bind["out"] != token_out:
+                raise ValueError(f"the step's token is {launch.bind['out']}, not {token_out}")
+            bind = dict(launch.bind, token=token_in, position=position)
+            params = dict(launch.params, context=context, step=step, advance=1)
+            self._advance[key] = self._add(Launch(launch.step, launch.entry, launch.groups, launch.threads, bind,
+                                                  params))
+        return self._advance[key]
 
     def enqueue_advance(self, token_out: str, token_in: str, position: str, context: int, step: int = 1,
                         stream: runtime.Stream | None = None) -> None:
@@ -249,4 +266,5 @@ class Engine:
         return out[0]
 
     def close(self) -> None:
+        self.table.destroy()
         self.arena.destroy()

@@ -56,6 +56,32 @@ class DeviceInfo(ctypes.Structure):
     ]
 
 
+class AbiBuffer(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("access", ctypes.c_char_p), ("type", ctypes.c_char_p),
+                ("align", ctypes.c_uint32)]
+
+
+class AbiParam(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_char_p), ("offset", ctypes.c_uint32)]
+
+
+class KernelAbi(ctypes.Structure):
+    """``fk_kernel_abi``: a kernel's buffers, its parameter fields, its hash."""
+
+    _fields_ = [("entry", ctypes.c_char_p), ("threads", ctypes.c_uint32), ("n_buffers", ctypes.c_uint32),
+                ("buffers", ctypes.POINTER(AbiBuffer)), ("n_params", ctypes.c_uint32),
+                ("params", ctypes.POINTER(AbiParam)), ("params_size", ctypes.c_uint32),
+                ("abi_hash", ctypes.c_uint64)]
+
+
+class Binding(ctypes.Structure):
+    """``fk_binding``: a buffer's device address and the bytes it holds there."""
+
+    _fields_ = [("addr", ctypes.c_uint64), ("bytes", ctypes.c_uint64)]
+
+
+_ABI_P = ctypes.POINTER(KernelAbi)
+
 ENTRY_POINTS: list[tuple[str, object, list]] = [
     ("fk_init", _int, [_int, _PP]),
     ("fk_fini", _int, [_vp]),
@@ -94,6 +120,20 @@ ENTRY_POINTS: list[tuple[str, object, list]] = [
     ("fk_graph_end", _int, [_vp, _vp, _PP]),
     ("fk_graph_replay", _int, [_vp, _vp]),
     ("fk_graph_destroy", _int, [_vp]),
+    ("fk_fnv1a64", ctypes.c_uint64, [_vp, _sz]),
+    ("fk_abi_description", _sz, [_ABI_P, ctypes.c_char_p, _sz]),
+    ("fk_abi_hash", ctypes.c_uint64, [_ABI_P]),
+    ("fk_manifest_count", _int, []),
+    ("fk_manifest_at", _ABI_P, [_int]),
+    ("fk_manifest_find", _ABI_P, [ctypes.c_char_p]),
+    ("fk_launch_check", _int, [ctypes.c_char_p, _u32, _u32, _u32, ctypes.POINTER(Binding), _u32, _vp, _sz,
+                               ctypes.c_uint64, ctypes.c_char_p, _sz]),
+    ("fk_table_create", _int, [_vp, _PP]),
+    ("fk_table_destroy", _int, [_vp]),
+    ("fk_table_add", _int, [_vp, _vp, _u32, _u32, _u32, ctypes.POINTER(Binding), _u32, _vp, _sz, ctypes.c_uint64,
+                            ctypes.POINTER(_u32)]),
+    ("fk_table_count", _int, [_vp, ctypes.POINTER(_u32)]),
+    ("fk_table_enqueue", _int, [_vp, _u32, _u32, _vp]),
 ]
 
 
@@ -271,6 +311,83 @@ class Graph:
     def destroy(self) -> None:
         if self.handle:
             _check(self.device.ctx, library().fk_graph_destroy(self.handle))
+            self.handle = None
+
+
+def abi_of(entry: str) -> KernelAbi:
+    """The manifest's ABI of a kernel (host only: no GPU)."""
+    p = library().fk_manifest_find(entry.encode())
+    if not p:
+        raise KeyError(f"{entry}: no such kernel in the manifest")
+    return p.contents
+
+
+def manifest_entries() -> list[str]:
+    lib = library()
+    return [lib.fk_manifest_at(i).contents.entry.decode() for i in range(lib.fk_manifest_count())]
+
+
+def abi_description(abi: KernelAbi) -> str:
+    lib = library()
+    n = lib.fk_abi_description(ctypes.byref(abi), None, 0)
+    out = ctypes.create_string_buffer(n + 1)
+    lib.fk_abi_description(ctypes.byref(abi), out, n + 1)
+    return out.value.decode()
+
+
+def bindings(spans: list[tuple[int, int]]):
+    arr = (Binding * max(len(spans), 1))()
+    for i, (addr, nbytes) in enumerate(spans):
+        arr[i].addr, arr[i].bytes = int(addr), int(nbytes)
+    return arr
+
+
+def launch_check(entry: str, groups: int, threads: int, lds_bytes: int, spans: list[tuple[int, int]],
+                 params: ctypes.Structure, abi_hash: int | None = None) -> None:
+    """The native launch table's checks of one launch, on the host (raises
+    ``FkError`` with the reason)."""
+    lib = library()
+    if abi_hash is None:
+        abi_hash = abi_of(entry).abi_hash
+    err = ctypes.create_string_buffer(512)
+    st = lib.fk_launch_check(entry.encode(), groups, threads, lds_bytes, bindings(spans), len(spans),
+                             ctypes.byref(params), ctypes.sizeof(params), abi_hash, err, 512)
+    if st != FK_OK:
+        raise FkError(st, err.value.decode())
+
+
+class Table:
+    """A native launch table: launches checked once (``fk_launch_check``),
+    kept with their kernargs, queued in order by one call."""
+
+    def __init__(self, device: "Device"):
+        self.device = device
+        h = ctypes.c_void_p()
+        _check(device.ctx, library().fk_table_create(device.ctx, ctypes.byref(h)))
+        self.handle = h.value
+
+    def add(self, fn: "Function", groups: int, threads: int, lds_bytes: int, spans: list[tuple[int, int]],
+            params: ctypes.Structure, abi_hash: int | None = None) -> int:
+        if abi_hash is None:
+            abi_hash = abi_of(fn.entry).abi_hash
+        idx = ctypes.c_uint32()
+        _check(self.device.ctx, library().fk_table_add(self.handle, fn.handle, groups, threads, lds_bytes,
+                                                       bindings(spans), len(spans), ctypes.byref(params),
+                                                       ctypes.sizeof(params), abi_hash, ctypes.byref(idx)))
+        return idx.value
+
+    def __len__(self) -> int:
+        n = ctypes.c_uint32()
+        _check(self.device.ctx, library().fk_table_count(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def enqueue(self, first: int = 0, count: int | None = None, stream: "Stream | None" = None) -> None:
+        count = len(self) - first if count is None else count
+        _check(self.device.ctx, library().fk_table_enqueue(self.handle, first, count, _sh(stream)))
+
+    def destroy(self) -> None:
+        if self.handle:
+            _check(self.device.ctx, library().fk_table_destroy(self.handle))
             self.handle = None
 
 

@@ -148,6 +148,86 @@ int fk_stream_sync(fk_ctx *ctx, fk_stream *stream);
 int fk_launch(fk_fn *fn, uint32_t groups, uint32_t threads, uint32_t lds_bytes, const void *kernarg,
               size_t kernarg_bytes, fk_stream *stream);
 
+/* The manifest: what each kernel of the code objects is. --------------------
+ * A kernel's ABI is its buffers in binding order (name, access, type,
+ * alignment), then its parameter struct's fields at their C offsets
+ * (fkrocm_kernels.h) and the struct's size; its hash is 64-bit FNV-1a over
+ * the canonical text `fk_abi_description` writes (src/FuryKernel/Abi.hs:
+ * 98-133,135-162,255-262), so a `LoweredKernel`'s `lkAbi` hash and this
+ * library's agree exactly when both describe one interface. */
+
+typedef struct fk_abi_buffer {
+  const char *name;
+  const char *access; /* "read", "write", "read_write" */
+  const char *type;   /* "f32", "f16", "bf16", "i8", "u32", "u64", ... */
+  uint32_t align;     /* bytes */
+} fk_abi_buffer;
+
+typedef struct fk_abi_param {
+  const char *name;
+  const char *type;
+  uint32_t offset; /* bytes into the struct */
+} fk_abi_param;
+
+typedef struct fk_kernel_abi {
+  const char *entry;
+  uint32_t threads; /* the threads every launch has; 0: any count up to 1024 */
+  uint32_t n_buffers;
+  const fk_abi_buffer *buffers;
+  uint32_t n_params;
+  const fk_abi_param *params;
+  uint32_t params_size;
+  uint64_t abi_hash;
+} fk_kernel_abi;
+
+/* 64-bit FNV-1a (src/FuryKernel/Abi.hs:255-262). */
+uint64_t fk_fnv1a64(const void *bytes, size_t n);
+/* The canonical text of an ABI ("abi 1", its buffers, its params, "params
+ * size"), written NUL-terminated into `out` (up to cap - 1 bytes); returns
+ * its full length. */
+size_t fk_abi_description(const fk_kernel_abi *abi, char *out, size_t cap);
+uint64_t fk_abi_hash(const fk_kernel_abi *abi);
+/* Every kernel of this library's code objects. */
+int fk_manifest_count(void);
+const fk_kernel_abi *fk_manifest_at(int index);
+const fk_kernel_abi *fk_manifest_find(const char *entry);
+
+/* A buffer a launch binds: its device address and the bytes it holds there. */
+typedef struct fk_binding {
+  uint64_t addr;
+  uint64_t bytes;
+} fk_binding;
+
+/* The checks a launch table makes before it builds a launch (host only, no
+ * GPU): `abi_hash` is the kernel's; the buffers and parameter bytes are its
+ * count and size; the threads are what it is built for; every buffer its
+ * kernel dereferences for this entry and these parameters is bound (a GEMV
+ * step entry's `_p<pro>_e<epi>` modes must agree with its parameters, and
+ * decide what it reads), 16-byte aligned, and, for the GEMV steps, the decode
+ * attention, its combine and the token, holds every byte the kernel touches.
+ * FK_OK, or a status with the reason in `err`. */
+int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32_t lds_bytes,
+                    const fk_binding *buffers, uint32_t n_buffers, const void *params, size_t params_bytes,
+                    uint64_t abi_hash, char *err, size_t err_cap);
+
+/* Launch tables: a planned step's launches, each checked once and kept with
+ * its kernarg, queued in order by one call (the per-token path of a
+ * `Backend`'s `loweredKernels`, src/FuryKernel/Backend.hs:76-101). --------- */
+
+typedef struct fk_table fk_table;
+
+int fk_table_create(fk_ctx *ctx, fk_table **out);
+int fk_table_destroy(fk_table *table);
+/* Appends a launch of `fn` after `fk_launch_check` passes; its index into
+ * `*index` (may be NULL).  Zero groups: kept, and skipped when queued. */
+int fk_table_add(fk_table *table, fk_fn *fn, uint32_t groups, uint32_t threads, uint32_t lds_bytes,
+                 const fk_binding *buffers, uint32_t n_buffers, const void *params, size_t params_bytes,
+                 uint64_t abi_hash, uint32_t *index);
+int fk_table_count(const fk_table *table, uint32_t *count);
+/* Queues launches [first, first + count) in order on the stream (a graph
+ * capture records them). */
+int fk_table_enqueue(fk_table *table, uint32_t first, uint32_t count, fk_stream *stream);
+
 /* Events, for timing on the stream the kernels run on. */
 int fk_event_create(fk_ctx *ctx, fk_event **out);
 int fk_event_destroy(fk_event *event);

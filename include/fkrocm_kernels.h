@@ -1,0 +1,252 @@
+/*
+ * fkrocm_kernels.h — the parameter structs of the target's gfx950 kernels,
+ * in C layout: what a launch's kernarg carries after its buffers' addresses
+ * (src/FuryKernel/Abi.hs:113-133, a kernel's one parameter struct laid out
+ * as C lays out a struct of its fields).  The kernels include this header,
+ * so the device code and every binding read one definition; the manifest
+ * (fkrocm.h, `fk_manifest_*`) describes each kernel's buffers and these
+ * fields with their offsets, and its ABI hash covers both.
+ *
+ * Entry names and their buffers in binding order:
+ *   fk_step_gemv_<f16|f32>_k<K>_r<R>_p<PRO>_e<EPI>
+ *       w0 w1 w2 y0 y1 y2 src src2 gamma table token res res_table res_token
+ *       epi_out arg                                    fk_step_gemv_params
+ *   fk_step_token        arg out token position       fk_step_token_params
+ *   fk_step_store        x0 x1 c0 c1 position slot rope
+ *                                                      fk_step_store_params
+ *   fk_step_attend       q knew vnew kc vc position slot rope partials
+ *                                                      fk_step_attend_params
+ *   fk_step_combine      partials out                 fk_step_combine_params
+ *   fk_gemm_f16_<store|add|silu_mul>  a b0 b1 b2 c0 c1 c2 r0   fk_gemm_params
+ *   fk_gemm_f16_qkv_rope a b0 b1 b2 c0 c1 c2 r0 position slot rope
+ *                                                      fk_gemm_qkv_params
+ *   (the manifest lists every entry.)
+ */
+#ifndef FKROCM_KERNELS_H
+#define FKROCM_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The GEMV step (a planned step of one row: Plan.hs:17-31). ---------------- */
+
+/* Prologue modes: how a GEMV step's threadgroups make the anchors' input row.
+ * An entry's `_p<mode>` suffix is the mode it runs; its parameter struct's
+ * pro_mode must agree (the launch table refuses it otherwise). */
+enum {
+  FK_PRO_STORED = 0,         /* x = src */
+  FK_PRO_RMSNORM = 1,        /* x = rmsnorm(src) * gamma * factor */
+  FK_PRO_GATHER = 2,         /* x = table[token] * gfactor */
+  FK_PRO_GATHER_RMSNORM = 3, /* x = rmsnorm(table[token] * gfactor) * gamma * factor */
+  FK_PRO_SILU_MUL = 4        /* x = silu(src) * src2 */
+};
+
+/* Epilogue modes, on the anchors' tile (the entry's `_e<mode>` suffix). */
+enum {
+  FK_EPI_NONE = 0,
+  FK_EPI_ADD_STORED = 1, /* out = res + tile */
+  FK_EPI_ADD_GATHER = 2, /* out = table[token] * gfactor + tile */
+  FK_EPI_SILU_MUL = 3,   /* out = silu(tile of anchor 0) * tile of anchor 1 */
+  FK_EPI_ARGMAX = 4      /* arg = max(arg, argmax key of each row) (the greedy token, folded in) */
+};
+
+typedef struct fk_step_gemv_params {
+  uint32_t n_anchors;    /* 1 to 3 */
+  uint32_t rows[3];      /* each anchor's outputs */
+  uint32_t first_row[4]; /* anchor j's rows are [first_row[j], first_row[j + 1]) of the numbered rows */
+  uint32_t k;            /* the input row's width */
+  uint32_t pro_mode;
+  uint32_t seg;          /* RMSNorm's segment: the row (k) */
+  float eps;
+  float factor;          /* RMSNorm's factor */
+  float gfactor;         /* the gather's factor */
+  uint32_t has_gamma;
+  uint32_t epi_mode;
+  uint32_t store_tile;   /* the anchors' own values are stored (into y[j]) */
+  uint32_t table_rows;   /* the gathered table's rows: a token past them reads its last */
+  uint32_t blocks;       /* row blocks */
+  uint32_t arg_slots;    /* the argmax epilogue's slots (one a threadgroup); a threadgroup past them stores none */
+} fk_step_gemv_params;
+
+typedef struct fk_step_token_params {
+  uint32_t slots;   /* the folded argmax's slots: one a threadgroup of the logits' step */
+  uint32_t context; /* positions wrap below this */
+  uint32_t step;    /* positions advance by this (0 holds the position) */
+  uint32_t advance; /* also set the next step's token and position */
+} fk_step_token_params;
+
+/* KV stores, decode attention and its combine (Eval.hs:415-527). ---------- */
+
+typedef struct fk_step_store_params {
+  uint32_t n_stores;   /* 1 or 2 */
+  uint32_t rope[2];    /* store j's value is RoPE'd first */
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t length;     /* the ring's positions */
+  uint32_t slots;      /* the ring's sequences */
+  uint32_t rotated;    /* pairs turned */
+  uint32_t rope_rows;  /* positions the RoPE table holds */
+  uint32_t cache_bf16; /* the caches round to bf16 (else f16) */
+} fk_step_store_params;
+
+typedef struct fk_step_attend_params {
+  uint32_t heads;
+  uint32_t kv_heads;
+  uint32_t head_dim; /* a multiple of 8, at most 64 */
+  uint32_t length;   /* the ring's positions */
+  uint32_t slots;
+  uint32_t splits;   /* threadgroups per kv head */
+  uint32_t split;    /* positions a split covers: split t is [t split, (t + 1) split); 64 or 128 */
+  uint32_t rope;     /* q is RoPE'd first */
+  uint32_t rotated;
+  uint32_t rope_rows;
+  float scale;       /* the attention's scale, rounded once to binary32 */
+  uint32_t window;   /* 0: none */
+  uint32_t cache_bf16;
+  uint32_t store;    /* the new key and value rows are stored into the caches first */
+  uint32_t krope;    /* the stored key row is RoPE'd first (q's table) */
+} fk_step_attend_params;
+
+typedef struct fk_step_combine_params {
+  uint32_t heads;
+  uint32_t head_dim;
+  uint32_t splits;
+} fk_step_combine_params;
+
+typedef struct fk_step_argmax_params {
+  uint32_t n;
+} fk_step_argmax_params;
+
+typedef struct fk_step_silu_mul_params {
+  uint32_t n;
+} fk_step_silu_mul_params;
+
+typedef struct fk_step_advance_params {
+  uint32_t context; /* positions wrap below this */
+  uint32_t step;    /* positions advance by this (0 holds the position) */
+} fk_step_advance_params;
+
+typedef struct fk_init_normal_params {
+  uint64_t count;
+  uint64_t seed;
+  float std;
+  uint32_t f16; /* store binary16 (else binary32) */
+} fk_init_normal_params;
+
+/* Standalone kernels. ----------------------------------------------------- */
+
+typedef struct fk_gemv_params {
+  uint32_t n; /* rows of W (outputs) */
+  uint32_t k; /* columns of W (inputs), a multiple of the pack */
+} fk_gemv_params;
+
+typedef struct fk_rmsnorm_params {
+  uint32_t rows;  /* rows of x */
+  uint32_t width; /* elements per row */
+  uint32_t seg;   /* elements per segment (a multiple of 4 dividing width) */
+  float eps;      /* rounded once to binary32 */
+  float factor;   /* a constant factor; 1 multiplies by nothing */
+  uint32_t has_gamma;
+} fk_rmsnorm_params;
+
+typedef struct fk_softmax_params {
+  uint32_t rows;
+  uint32_t n; /* elements per row, a multiple of 4 */
+} fk_softmax_params;
+
+typedef struct fk_fill_params {
+  uint32_t count; /* 32-bit words */
+  uint32_t value;
+} fk_fill_params;
+
+typedef struct fk_noop_params {
+  uint32_t unused;
+} fk_noop_params;
+
+typedef struct fk_stream_read_params {
+  uint64_t words; /* 16-byte words to read */
+} fk_stream_read_params;
+
+/* The prefill (steps of many rows, Tile.hs:76-157). ----------------------- */
+
+enum {
+  FK_GEMM_STORE = 0,    /* C = A B^T (f32 rows) */
+  FK_GEMM_ADD = 1,      /* C = R + A B^T (f32 rows), R [M, ldc]; R may be C */
+  FK_GEMM_SILU_MUL = 2, /* C = f16(silu(A G^T) (A U^T)) in the tile layout; B0 the paired gate/up weights */
+  FK_GEMM_QKV_ROPE = 3  /* anchors q, k, v: q RoPE'd into f16 rows (C0), k RoPE'd into the K cache (C1), v into
+                           the V cache (C2), at each row's slot and position */
+};
+
+typedef struct fk_gemm_params {
+  uint32_t m;            /* rows of A and C, a multiple of 256 */
+  uint32_t k;            /* a multiple of 64 */
+  uint32_t n_anchors;    /* 1 to 3 weights (SiLU·mul: 1, the pair) */
+  uint32_t first_col[4]; /* anchor j's columns of C are [first_col[j], first_col[j + 1]), each a multiple of 256 */
+  uint32_t ldc[3];       /* row stride of anchor j's output (its columns; SiLU·mul: N, gate's rows) */
+} fk_gemm_params;
+
+typedef struct fk_gemm_rope_params {
+  uint32_t kv_heads;
+  uint32_t rope_rows; /* positions the RoPE table holds */
+  uint32_t length;    /* ring length */
+  uint32_t slots;
+  uint32_t cache_bf16;
+} fk_gemm_rope_params;
+
+typedef struct fk_gemm_qkv_params {
+  fk_gemm_params g;
+  fk_gemm_rope_params r;
+} fk_gemm_qkv_params;
+
+typedef struct fk_prefill_gather_params {
+  uint32_t rows;
+  uint32_t width;      /* a multiple of 4 */
+  uint32_t table_rows;
+  uint32_t table_f16;  /* the table is f16 (else f32) */
+  float factor;
+} fk_prefill_gather_params;
+
+typedef struct fk_prefill_norm_params {
+  uint32_t rows;  /* a multiple of 256 */
+  uint32_t width; /* a multiple of 32 */
+  float eps;
+  float factor;
+  uint32_t has_gamma;
+} fk_prefill_norm_params;
+
+typedef struct fk_prefill_rope_params {
+  uint32_t rows;
+  uint32_t heads;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t rotated;   /* pairs RoPE turns */
+  uint32_t rope_rows; /* positions the RoPE table holds */
+  uint32_t length;    /* ring length */
+  uint32_t slots;
+  uint32_t cache_bf16;
+} fk_prefill_rope_params;
+
+typedef struct fk_prefill_attend_params {
+  uint32_t rows;     /* a multiple of 32 */
+  uint32_t heads;
+  uint32_t kv_heads; /* heads / kv_heads (G) is 1, 2 or 4 */
+  uint32_t length;   /* ring length, a multiple of 64 */
+  uint32_t slots;
+  uint32_t window;   /* 0: none; else a row sees positions > position - window */
+  uint32_t cache_bf16;
+  float scale;
+} fk_prefill_attend_params;
+
+typedef struct fk_prefill_argmax_params {
+  uint32_t rows;
+  uint32_t width;
+} fk_prefill_argmax_params;
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FKROCM_KERNELS_H */

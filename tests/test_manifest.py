@@ -1,0 +1,196 @@
+"""The kernels' manifest and ABI hashes (src/FuryKernel/Abi.hs,
+Manifest.hs), and the native launch table's checks, on the CPU.
+
+Pins: the reference's FNV-1a vectors (test/Test/FuryKernel/AbiTest.hs:33-36),
+its ABI description text of rmsnorm (:43-53), its pinned ABI hash of scale
+(:69-72, a hash of the whole canonical text, so a changed line or format
+fails it), the C struct layout rule (:37-42), and its manifest of scale
+(:73-122, rendered by the same writer)."""
+
+import ctypes
+import dataclasses
+
+import pytest
+
+from furykernel_amd import kernels as K
+from furykernel_amd import manifest as M
+from furykernel_amd import runtime
+
+
+def abi(buffers, params, size, entry="k"):
+    """A fk_kernel_abi built on the host, its strings kept alive on it."""
+    keep = []
+
+    def c(s):
+        b = ctypes.c_char_p(s.encode())
+        keep.append(b)
+        return b
+
+    bufs = (runtime.AbiBuffer * max(len(buffers), 1))()
+    for i, (n, a, t, al) in enumerate(buffers):
+        bufs[i].name, bufs[i].access, bufs[i].type, bufs[i].align = c(n).value, c(a).value, c(t).value, al
+    prms = (runtime.AbiParam * max(len(params), 1))()
+    for i, (n, t, o) in enumerate(params):
+        prms[i].name, prms[i].type, prms[i].offset = c(n).value, c(t).value, o
+    a = runtime.KernelAbi(entry.encode(), 0, len(buffers), bufs, len(params), prms, size, 0)
+    a._keep = (keep, bufs, prms)
+    return a
+
+
+def test_fnv1a_reference_vectors():
+    lib = runtime.library()
+    for text, want in ((b"", 0xcbf29ce484222325), (b"a", 0xaf63dc4c8601ec8c), (b"foobar", 0x85944171f73967e8)):
+        assert lib.fk_fnv1a64(text, len(text)) == want
+
+
+def test_the_description_the_hash_covers():
+    a = abi([("x", "read", "bf16", 16), ("w", "read", "bf16", 16), ("y", "write", "bf16", 16)],
+            [("rows", "u32", 0), ("eps", "f32", 4)], 8)
+    assert runtime.abi_description(a) == "\n".join([
+        "abi 1", "buffer x read bf16 align 16", "buffer w read bf16 align 16", "buffer y write bf16 align 16",
+        "param rows u32 at 0", "param eps f32 at 4", "params size 8"]) + "\n"
+
+
+def test_the_pinned_abi_hash_of_scale():
+    a = abi([("x", "read", "bf16", 16), ("y", "write", "bf16", 16)], [("n", "u32", 0), ("s", "f32", 4)], 8)
+    assert runtime.library().fk_abi_hash(ctypes.byref(a)) == 0xe99ad54061a304ff
+    renamed = abi([("x", "read", "bf16", 16), ("z", "write", "bf16", 16)], [("n", "u32", 0), ("s", "f32", 4)], 8)
+    assert runtime.library().fk_abi_hash(ctypes.byref(renamed)) != 0xe99ad54061a304ff
+
+
+def test_the_parameter_struct_is_laid_out_as_c_lays_it_out():
+    class S(ctypes.Structure):
+        _fields_ = [("a", ctypes.c_uint8), ("b", ctypes.c_float), ("c", ctypes.c_uint16), ("d", ctypes.c_uint32)]
+
+    class T(ctypes.Structure):
+        _fields_ = [("a", ctypes.c_float), ("b", ctypes.c_uint8)]
+    assert [getattr(S, f).offset for f in "abcd"] == [0, 4, 8, 12] and ctypes.sizeof(S) == 16
+    assert ctypes.sizeof(T) == 8
+
+
+def test_the_manifest_of_scale_renders_as_the_reference_renders_it():
+    text = M.render_json(M.kernel_manifest(
+        "scale", 0xe99ad54061a304ff, 0x60c50bd78967a3d0, 64, "1u",
+        [("x", "read", "bf16", 16, "$n"), ("y", "write", "bf16", 16, "$n")],
+        [("n", "u32", 0, (1, 65536, 1)), ("s", "f32", 4, None)], 8, 0, target="T32"))
+    assert text == "\n".join([
+        "{", '  "format": "furykernel-manifest",', '  "version": 1,', '  "target": "T32",', '  "name": "scale",',
+        '  "abi_hash": "0xe99ad54061a304ff",', '  "ir_hash": "0x60c50bd78967a3d0",', '  "threads": 64,',
+        '  "groups": "1u",', '  "buffers": [', "    {", '      "name": "x",', '      "access": "read",',
+        '      "type": "bf16",', '      "align": 16,', '      "extent": "$n"', "    },", "    {",
+        '      "name": "y",', '      "access": "write",', '      "type": "bf16",', '      "align": 16,',
+        '      "extent": "$n"', "    }", "  ],", '  "params": [', "    {", '      "name": "n",',
+        '      "type": "u32",', '      "offset": 0,', '      "dim": {', '        "min": 1,',
+        '        "max": 65536,', '        "multiple_of": 1', "      }", "    },", "    {", '      "name": "s",',
+        '      "type": "f32",', '      "offset": 4', "    }", "  ],", '  "params_size": 8,',
+        '  "threadgroup_memory": 0', "}"]) + "\n"
+
+
+def _flat_fields(cls, base=0):
+    out = []
+    for name, ty in cls._fields_:
+        off = getattr(cls, name).offset + base
+        if isinstance(ty, type) and issubclass(ty, ctypes.Structure):
+            out += _flat_fields(ty, off)
+        elif hasattr(ty, "_length_"):
+            out += [(f"{name}_{i}", off + 4 * i) for i in range(ty._length_)]
+        else:
+            out.append((name, off))
+    return out
+
+
+def test_every_kernel_is_in_the_manifest_with_the_bindings_abi():
+    entries = set(runtime.manifest_entries())
+    assert entries == set(K.ABIS)
+    for entry, kabi in K.ABIS.items():
+        a = runtime.abi_of(entry)
+        assert [a.buffers[i].name.decode() for i in range(a.n_buffers)] == list(kabi.buffers), entry
+        assert a.params_size == ctypes.sizeof(kabi.params), entry
+        # the host binding's structs are the kernels' (fields and offsets)
+        want = [(a.params[i].name.decode(), a.params[i].offset) for i in range(a.n_params)]
+        got = _flat_fields(kabi.params)
+        assert [o for _, o in got] == [o for _, o in want], entry
+        assert a.abi_hash == runtime.library().fk_abi_hash(ctypes.byref(a))
+
+
+def test_every_manifest_renders_and_parses():
+    import json
+    for entry in ("fk_step_gemv_f16_k2048_r2_p1_e3", "fk_step_attend", "fk_gemm_f16_qkv_rope", "fk_noop"):
+        m = json.loads(M.render_json(M.manifest_of(entry)))
+        assert m["format"] == "furykernel-manifest" and m["name"] == entry and m["target"] == "MI355X"
+        assert m["abi_hash"] == M.hex64(runtime.abi_of(entry).abi_hash)
+
+
+# The launch table's checks -----------------------------------------------------
+
+def _spans(launch, specs, base=1 << 32):
+    """Fake, distinct, aligned addresses of the right sizes for a launch's buffers."""
+    out, at = [], base
+    for b in K.ABIS[launch.entry].buffers:
+        name = launch.bind.get(b)
+        if name is None:
+            out.append((0, 0))
+        else:
+            out.append((at, specs[name].nbytes))
+            at += (specs[name].nbytes + 255) // 256 * 256
+    return out
+
+
+def _lowered_1b(options=None):
+    from furykernel_amd.lower import lower_plan
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.decoder import ONE_B, decoder_step
+    from furykernel_amd.program.plan import PlanOptions, plan
+    c = check_program(decoder_step(ONE_B, embed=True))
+    return lower_plan(c, plan(options or PlanOptions(store_gelus=True), c))
+
+
+def _check(launch, specs, **kw):
+    from furykernel_amd.engine import params_struct
+    runtime.launch_check(launch.entry, launch.groups, launch.threads, launch.lds_bytes,
+                         kw.get("spans") or _spans(launch, specs), kw.get("params") or params_struct(launch),
+                         kw.get("abi_hash"))
+
+
+def test_the_launch_check_accepts_every_lowered_launch():
+    low = _lowered_1b()
+    for L in low.launches:
+        _check(L, low.buffers)
+
+
+@pytest.mark.parametrize("key,unbound", [(0, "token"), (3, "res_token")])
+def test_the_launch_check_refuses_the_probes_swapped_entries(key, unbound):
+    low = _lowered_1b()
+    idx = [i for i in range(96) if i % 6 == key]
+    first = low.launches[idx[0]].entry
+    for i in idx[1:]:
+        L = dataclasses.replace(low.launches[i], entry=first)
+        with pytest.raises(runtime.FkError, match="prologue|unbound"):
+            _check(L, low.buffers)
+
+
+def test_the_launch_check_refuses_wrong_hashes_sizes_and_short_buffers():
+    from furykernel_amd.engine import params_struct
+    low = _lowered_1b()
+    qkv = low.launches[6]
+    good = runtime.abi_of(qkv.entry).abi_hash
+    with pytest.raises(runtime.FkError, match="ABI hash"):
+        _check(qkv, low.buffers, abi_hash=good ^ 1)
+    spans = _spans(qkv, low.buffers)
+    spans[1] = (spans[1][0], spans[1][1] - 2)  # w1 two bytes short
+    with pytest.raises(runtime.FkError, match="w1 holds"):
+        _check(qkv, low.buffers, spans=spans)
+    spans = _spans(qkv, low.buffers)
+    spans[0] = (spans[0][0] + 8, spans[0][1])  # w0 misaligned
+    with pytest.raises(runtime.FkError, match="aligned"):
+        _check(qkv, low.buffers, spans=spans)
+    p = params_struct(qkv)
+    p.pro_mode = 0
+    with pytest.raises(runtime.FkError, match="its parameters say"):
+        _check(qkv, low.buffers, params=p)
+    att = low.launches[7]
+    assert att.entry == "fk_step_attend"
+    spans = _spans(att, low.buffers)
+    spans[8] = (spans[8][0], spans[8][1] - 4)  # partials short
+    with pytest.raises(runtime.FkError, match="partials holds"):
+        _check(att, low.buffers, spans=spans)

@@ -13,7 +13,8 @@ ROOT = Path(__file__).resolve().parents[1]
 
 
 def declared_entry_points() -> list[str]:
-    text = (ROOT / "include" / "fkrocm.h").read_text()
+    """Every function declared in include/*.h."""
+    text = "".join(p.read_text() for p in sorted((ROOT / "include").glob("*.h")))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(fk_[a-z0-9_]+)\s*\(", text)))
 
