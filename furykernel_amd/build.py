@@ -48,10 +48,21 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_runtime() -> Path:
-    srcs = [CSRC / "fk_runtime.cpp", CSRC / "fk_manifest.cpp"]
+    """The C ABI's library: the runtime and manifest (host code) and the
+    operations (fk_ops.hip, whose kernels are built with the kernels' flags)."""
     tmp = RUNTIME_SO.with_suffix(".so.tmp")
-    _run([HIPCC, "-shared", "-fPIC", "-O2", "-std=c++17", "-Wno-unused-value", "-Wno-unused-result",
-          f"-I{ROOT / 'include'}", *map(str, srcs), "-o", str(tmp)])
+    objs = []
+    for src in (CSRC / "fk_runtime.cpp", CSRC / "fk_manifest.cpp"):
+        obj = PACKAGE / f".{src.stem}.o"
+        _run([HIPCC, "-c", "-fPIC", "-O2", "-std=c++17", "-Wno-unused-value", "-Wno-unused-result",
+              f"-I{ROOT / 'include'}", str(src), "-o", str(obj)])
+        objs.append(obj)
+    obj = PACKAGE / ".fk_ops.o"
+    _run([HIPCC, "-c", "-fPIC", *KERNEL_FLAGS, f"-I{ROOT / 'include'}", str(CSRC / "fk_ops.hip"), "-o", str(obj)])
+    objs.append(obj)
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
+    for o in objs:
+        o.unlink()
     os.replace(tmp, RUNTIME_SO)
     return RUNTIME_SO
 

@@ -21,73 +21,7 @@
 #include <string>
 #include <vector>
 
-struct fk_ctx {
-  int device = 0;
-  hipStream_t stream = nullptr;
-  std::string last_error;
-  std::mutex mu;  // guards the ownership sets below
-  std::set<fk_module *> modules;
-  std::set<fk_buf *> buffers;
-  std::set<fk_arena *> arenas;
-  std::set<fk_stream *> streams;
-  std::set<fk_event *> events;
-  std::set<fk_graph *> graphs;
-  std::set<fk_table *> tables;
-  std::set<void *> host;
-};
-
-struct fk_module {
-  fk_ctx *ctx;
-  hipModule_t mod;
-  std::vector<fk_fn *> fns;
-};
-
-struct fk_fn {
-  fk_module *mod;
-  hipFunction_t fn;
-  std::string entry;
-};
-
-struct fk_buf {
-  fk_ctx *ctx;
-  fk_arena *arena;  // null when the buffer owns its memory
-  void *ptr;
-  size_t size;
-};
-
-struct fk_arena {
-  fk_ctx *ctx;
-  void *base;
-  size_t capacity;
-  size_t used;
-  std::vector<fk_buf *> handed;
-};
-
-struct fk_stream {
-  fk_ctx *ctx;
-  hipStream_t stream;
-};
-
-struct fk_event {
-  fk_ctx *ctx;
-  hipEvent_t event;
-};
-
-struct fk_graph {
-  fk_ctx *ctx;
-  hipGraph_t graph;
-  hipGraphExec_t exec;
-};
-
-struct fk_table {
-  struct Launch {
-    fk_fn *fn;
-    uint32_t groups, threads, lds_bytes;
-    std::vector<unsigned char> kernarg;
-  };
-  fk_ctx *ctx;
-  std::vector<Launch> launches;
-};
+#include "fk_internal.h"
 
 namespace {
 
@@ -132,6 +66,15 @@ int use_device(fk_ctx *ctx) {
 
 }  // namespace
 
+int fk_fail(fk_ctx *ctx, int code, const char *fmt, ...) {
+  char msg[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(msg, sizeof msg, fmt, ap);
+  va_end(ap);
+  return fail(ctx, code, "%s", msg);
+}
+
 extern "C" {
 
 int fk_init(int device, fk_ctx **out) {
@@ -151,6 +94,12 @@ int fk_init(int device, fk_ctx **out) {
   if (e != hipSuccess) {
     delete ctx;
     return fail(nullptr, FK_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  if (int st = fk_ops_setup(ctx)) {
+    const std::string msg = ctx->last_error;
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return fail(nullptr, st, "%s", msg.c_str());
   }
   *out = ctx;
   return FK_OK;
@@ -189,6 +138,7 @@ int fk_fini(fk_ctx *ctx) {
     delete m;
   }
   for (fk_table *t : ctx->tables) delete t;
+  fk_ops_teardown(ctx);
   for (void *p : ctx->host) hipHostFree(p);
   hipStreamDestroy(ctx->stream);
   delete ctx;

@@ -162,6 +162,15 @@ class StepAttendParams(ctypes.Structure):
     ]
 
 
+class AttendArgs(ctypes.Structure):
+    """``fk_attend_args`` (include/fkrocm_ops.h): device addresses, then the
+    attention's parameters."""
+    _fields_ = [("q", ctypes.c_uint64), ("knew", ctypes.c_uint64), ("vnew", ctypes.c_uint64),
+                ("kc", ctypes.c_uint64), ("vc", ctypes.c_uint64), ("position", ctypes.c_uint64),
+                ("slot", ctypes.c_uint64), ("rope", ctypes.c_uint64), ("out", ctypes.c_uint64),
+                ("p", StepAttendParams)]
+
+
 class StepCombineParams(ctypes.Structure):
     _fields_ = [("heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32), ("splits", ctypes.c_uint32)]
 

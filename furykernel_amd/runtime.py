@@ -134,6 +134,7 @@ ENTRY_POINTS: list[tuple[str, object, list]] = [
                             ctypes.POINTER(_u32)]),
     ("fk_table_count", _int, [_vp, ctypes.POINTER(_u32)]),
     ("fk_table_enqueue", _int, [_vp, _u32, _u32, _vp]),
+    ("fk_attend_decode", _int, [_vp, _vp, _vp]),
 ]
 
 
@@ -389,6 +390,13 @@ class Table:
         if self.handle:
             _check(self.device.ctx, library().fk_table_destroy(self.handle))
             self.handle = None
+
+
+def attend_decode(device: "Device", args: ctypes.Structure, stream: "Stream | None" = None,
+                  entry: str = "fk_attend_decode") -> None:
+    """One decode attention step through the library's operation
+    (include/fkrocm_ops.h); `args` is a ``kernels.AttendArgs``."""
+    _check(device.ctx, getattr(library(), entry)(device.ctx, ctypes.byref(args), _sh(stream)))
 
 
 class Device:

@@ -1,0 +1,48 @@
+/*
+ * fkrocm_ops.h — whole operations as one C call each, over device buffers
+ * the caller holds: for callers that want an operation rather than a launch
+ * table of their own.
+ *
+ * The decode attention step over a ring KV cache: the new key and value rows
+ * stored at the row's position (the key RoPE'd), the attention of each query
+ * head over its kv head's positions in splits, and the combine of the splits
+ * — the planned step's KvStore effects, Partials anchor and Combine
+ * (src/FuryKernel/Program/Eval.hs:415-527, src/FuryKernel/Program/Plan.hs:
+ * 174-181), with the same kernels and bits as the planned step's launches.
+ */
+#ifndef FKROCM_OPS_H
+#define FKROCM_OPS_H
+
+#include "fkrocm.h"
+#include "fkrocm_kernels.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Device addresses (16-byte aligned) and the attention's parameters. */
+typedef struct fk_attend_args {
+  uint64_t q;        /* f32 [heads * head_dim]: the row's queries, before RoPE */
+  uint64_t knew;     /* f32 [kv_heads * head_dim]: the new key row (read when p.store) */
+  uint64_t vnew;     /* f32 [kv_heads * head_dim]: the new value row (read when p.store) */
+  uint64_t kc;       /* f16 or bf16 [slots][kv_heads][length][head_dim]: the key ring */
+  uint64_t vc;       /* the value ring, the same layout */
+  uint64_t position; /* u32 [1] */
+  uint64_t slot;     /* u32 [1] */
+  uint64_t rope;     /* f32 [rope_rows][rotated][2]: cosines and sines (read when p.rope or p.krope) */
+  uint64_t out;      /* f32 [heads * head_dim]: the attention's rows */
+  fk_step_attend_params p; /* p.splits: ceil(length / p.split) */
+} fk_attend_args;
+
+/* The attention step; its splits' partial results go to a workspace the
+ * context allocates (hipMalloc) on first use and grows when a call needs
+ * more, which it refuses (FK_ERR_STATE) on a stream being captured.
+ * Source: src/FuryKernel/Program/Eval.hs:474-527 (Attend), Plan.hs:174-181
+ * (Partials + Combine). */
+int fk_attend_decode(fk_ctx *ctx, const fk_attend_args *args, fk_stream *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FKROCM_OPS_H */
