@@ -7,6 +7,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "fk_internal.h"
 #include "kernels/fk_attention.h"
 
@@ -71,10 +73,32 @@ int launch_attend(fk_ctx *ctx, const fk_attend_args *a, float *partials, hipStre
   return FK_OK;
 }
 
+// fk_attend_decode_noalloc's partial results: one static array on each GPU,
+// held until the process ends.  In host code `scratch` names a host-side
+// stand-in, not a device address: only the address hipGetSymbolAddress gives
+// for a device (kept per device below) is passed to kernels.
+__device__ __align__(256) float scratch[FK_ATTEND_SCRATCH_BYTES / sizeof(float)];
+
+std::mutex g_scratch_mu;
+void *g_scratch[64];  // by device ordinal
+
 }  // namespace
 
+// At fk_init, with the context's device current: the static scratch's address
+// on that device, looked up once per device.
 int fk_ops_setup(fk_ctx *ctx) {
-  (void)ctx;
+  if (ctx->device < 0 || ctx->device >= 64)
+    return fk_fail(ctx, FK_ERR_RANGE, "fk_init: device %d past the 64 the operations track", ctx->device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[ctx->device]) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fk_fail(ctx, FK_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
+                     hipGetErrorString(e));
+    g_scratch[ctx->device] = ptr;
+  }
+  ctx->scratch = g_scratch[ctx->device];
   return FK_OK;
 }
 
@@ -112,4 +136,20 @@ extern "C" int fk_attend_decode(fk_ctx *ctx, const fk_attend_args *a, fk_stream 
     ctx->workspace_bytes = bytes;
   }
   return launch_attend(ctx, a, static_cast<float *>(ctx->workspace), s, "fk_attend_decode");
+}
+
+extern "C" int fk_attend_decode_noalloc(fk_ctx *ctx, const fk_attend_args *a, fk_stream *stream) {
+  if (!ctx || !a) return fk_fail(ctx, FK_ERR_ARG, "fk_attend_decode_noalloc: null argument");
+  const size_t bytes = check_attend(ctx, a, "fk_attend_decode_noalloc");
+  if (bytes == 0) return FK_ERR_ARG;
+  if (bytes > FK_ATTEND_SCRATCH_BYTES)
+    return fk_fail(ctx, FK_ERR_RANGE,
+                   "fk_attend_decode_noalloc: %zu bytes of partial results (heads %u x splits %u x (head_dim %u + 2) "
+                   "x 4); the static scratch holds %u",
+                   bytes, a->p.heads, a->p.splits, a->p.head_dim, FK_ATTEND_SCRATCH_BYTES);
+  if (!ctx->scratch) return fk_fail(ctx, FK_ERR_STATE, "fk_attend_decode_noalloc: no scratch on this device");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return fk_fail(ctx, FK_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
+  return launch_attend(ctx, a, static_cast<float *>(ctx->scratch), stream ? stream->stream : ctx->stream,
+                       "fk_attend_decode_noalloc");
 }

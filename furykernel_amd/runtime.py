@@ -135,6 +135,7 @@ ENTRY_POINTS: list[tuple[str, object, list]] = [
     ("fk_table_count", _int, [_vp, ctypes.POINTER(_u32)]),
     ("fk_table_enqueue", _int, [_vp, _u32, _u32, _vp]),
     ("fk_attend_decode", _int, [_vp, _vp, _vp]),
+    ("fk_attend_decode_noalloc", _int, [_vp, _vp, _vp]),
 ]
 
 

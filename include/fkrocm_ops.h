@@ -41,6 +41,21 @@ typedef struct fk_attend_args {
  * (Partials + Combine). */
 int fk_attend_decode(fk_ctx *ctx, const fk_attend_args *args, fk_stream *stream);
 
+/* The most bytes of partial results fk_attend_decode_noalloc takes:
+ * heads * splits * (head_dim + 2) * 4 must not exceed it (4 MiB; the 1B
+ * decode's 32 heads x 32 splits x 66 x 4 is 270,336). */
+#define FK_ATTEND_SCRATCH_BYTES (4u << 20)
+
+/* fk_attend_decode with no allocation at all: its partial results go to a
+ * static device array of FK_ATTEND_SCRATCH_BYTES that the library holds on
+ * each GPU until the process ends (its address looked up at fk_init).  No
+ * counterpart in the reference: for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * A larger step is refused with FK_ERR_RANGE.  Every call on a GPU shares that
+ * GPU's array and each call overwrites the partials it reads (nothing needs
+ * clearing): calls that overlap on one GPU (two streams, two contexts) race. */
+int fk_attend_decode_noalloc(fk_ctx *ctx, const fk_attend_args *args, fk_stream *stream);
+
 #ifdef __cplusplus
 }
 #endif
