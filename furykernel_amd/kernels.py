@@ -407,7 +407,11 @@ class Kernels:
         """Causal attention of f16 rows q [rows, heads · 64] (RoPE'd) over the
         caches [slots][kv_heads][length][64] into f16 tiles [rows, heads · 64].
         Every block of 32 rows must be one sequence's consecutive positions:
-        given the host copies (positions, seqs), that is checked here."""
+        given the host copies (positions, seqs), that is checked here.  A bf16
+        cache is converted to f16 as it is staged (the matrix operations take
+        f16): an element beyond f16's range (|x| > 65504) becomes infinite and
+        one below 2^-24 flushes to zero, so bf16 caches are for values inside
+        f16's range, as the prefill's own stores of f16-range rows are."""
         entry = f"fk_prefill_attend_g{heads // kv_heads if kv_heads and heads % kv_heads == 0 else 0}"
         if rows <= 0 or rows % 256 or kv_heads <= 0 or heads % kv_heads or heads // kv_heads not in (1, 2, 4):
             raise LaunchError(f"{entry}: {rows} rows, {heads} heads over {kv_heads}")

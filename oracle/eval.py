@@ -384,17 +384,21 @@ def evaluate_fast(checked: CheckedProgram, b: Bindings) -> Evaluation:
             group = heads // kvh
             q = env[op.q].reshape(m, heads, d)
             res = np.empty((m, heads, d))
-            for r in range(m):
-                position = int(pos[r])
-                first = max(0, position - spec.window + 1) if spec.window else 0
-                ts = np.arange(first, position + 1) % lay.length
-                keys = caches[sources[op.to.keys].name][int(seq[r])].reshape(kvh, lay.length, d)[:, ts, :]
-                vals = caches[sources[op.to.values].name][int(seq[r])].reshape(kvh, lay.length, d)[:, ts, :]
-                kk = np.repeat(keys, group, axis=0)                # [heads, t, d]
-                vv = np.repeat(vals, group, axis=0)
-                scores = spec.scale * np.einsum("htd,hd->ht", kk, q[r])
-                e = np.exp(scores - scores.max(axis=1, keepdims=True))
-                res[r] = np.einsum("ht,htd->hd", e / e.sum(axis=1, keepdims=True), vv)
+            # The rows of one sequence together: row r's scores over positions
+            # t in [first_r, pos_r] (the others masked to weight zero), the
+            # key of position t at ring index t mod length.
+            for u in np.unique(seq):
+                rows = np.nonzero(seq == u)[0]
+                ps = pos[rows]
+                ts = np.arange(int(ps.max()) + 1)
+                keys = caches[sources[op.to.keys].name][int(u)].reshape(kvh, lay.length, d)[:, ts % lay.length, :]
+                vals = caches[sources[op.to.values].name][int(u)].reshape(kvh, lay.length, d)[:, ts % lay.length, :]
+                first = np.maximum(0, ps - spec.window + 1) if spec.window else np.zeros_like(ps)
+                seen = (ts[None, :] <= ps[:, None]) & (ts[None, :] >= first[:, None])
+                for h in range(heads):
+                    scores = np.where(seen, spec.scale * (q[rows, h, :] @ keys[h // group].T), -np.inf)
+                    e = np.exp(scores - scores.max(axis=1, keepdims=True))
+                    res[rows, h] = (e / e.sum(axis=1, keepdims=True)) @ vals[h // group]
             env[out] = res.reshape(m, -1)
         elif isinstance(op, Gather):
             width = values[out].shape.width
