@@ -167,6 +167,7 @@ def cpu_baseline(dims, seconds: float) -> dict:
     import numpy as np
 
     from furykernel_amd.lower import rope_table
+    from oracle import fkref
     from oracle.cpu_target import CpuTarget
 
     one = lowered_for(dims, layers=1)
@@ -186,23 +187,36 @@ def cpu_baseline(dims, seconds: float) -> dict:
     cpu.write("ints:position", [POSITION])
     cpu.write("ints:tokens", [7])
     layer, head = one.launches[:per_layer], one.launches[per_layer:]
-    t_layer = t_head = 0.0
-    reps = 0
-    while reps == 0 or t_layer + t_head < seconds:
-        t0 = time.perf_counter()
-        for launch in layer:
-            cpu.run_launch(launch)
-        t1 = time.perf_counter()
-        for launch in head:
-            cpu.run_launch(launch)
-        t_head += time.perf_counter() - t1
-        t_layer += t1 - t0
-        reps += 1
-    per_token = (t_layer * dims.layers + t_head) / reps
+
+    def sample(threads: int, budget: float):
+        fkref.lib().fkref_set_threads(threads)
+        t_layer = t_head = 0.0
+        reps = 0
+        while reps == 0 or t_layer + t_head < budget:
+            t0 = time.perf_counter()
+            for launch in layer:
+                cpu.run_launch(launch)
+            t1 = time.perf_counter()
+            for launch in head:
+                cpu.run_launch(launch)
+            t_head += time.perf_counter() - t1
+            t_layer += t1 - t0
+            reps += 1
+        fkref.lib().fkref_set_threads(1)
+        return (t_layer * dims.layers + t_head) / reps, reps, t_layer + t_head
+
+    # One thread (the CPU target: threadgroups one after another), then the
+    # GEMVs' rows spread over the host's cores (the box's share of them).
+    per_token, reps, spent = sample(1, seconds)
+    cores = max(1, min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), os.cpu_count() or 1))
+    per_token_all, reps_all, spent_all = sample(cores, seconds / 2)
     return {"value": round(1.0 / per_token, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
             "sample": f"layer 0's {len(layer)} launches and the head's {len(head)} of the same step at position "
-                      f"{POSITION}, run {reps} times ({t_layer + t_head:.1f} s); a token = {dims.layers} x layer + head",
-            "host_cpus": os.cpu_count()}
+                      f"{POSITION}, run {reps} times ({spent:.1f} s); a token = {dims.layers} x layer + head",
+            "host_cpus": os.cpu_count(),
+            "omp": {"value": round(1.0 / per_token_all, 4), "unit": "tokens/s", "cores": cores, "kind": "port",
+                    "sample": f"the same sample with the GEMVs' rows spread over {cores} threads (each row's "
+                              f"arithmetic unchanged), run {reps_all} times ({spent_all:.1f} s)"}}
 
 
 MFMA_PEAK_TFLOPS = 2500.0
@@ -618,6 +632,8 @@ def main() -> int:
                 "ms_per_step_events": round(event_ms / args.steps, 4)},
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(dominant),
+                     "traffic_source": "read from profiles/traffic_decode_1b_f16.md (the committed rocprofv3 "
+                                       "FETCH_SIZE and WRITE_SIZE runs of this workload), not measured in this run",
                      "avg_launch_us": dom["avg_us"], "bytes_per_launch": dom["bytes_per_launch"],
                      "launches_per_step": dom["launches"]},
         "kernels": table,

@@ -217,52 +217,66 @@ static float element(const void *base, int type, size_t i) {
   }
 }
 
-int fkref_gemv(const void *w, int wtype, const void *x, int xtype, float *y, const float *row_scale, int n, int k,
-               int m, int width, int pack, int split) {
-  if (n < 0 || k <= 0 || m <= 0 || width <= 0 || width > 1024 || pack < 4 || pack % 4 || k % pack || split <= 0 ||
-      split > 64)
-    return -1;
+/* Threads the GEMV's rows are spread over (the CPU target runs threadgroups
+ * one after another on one thread; the all-cores figure spreads them, with
+ * every row's arithmetic unchanged). */
+static int g_threads = 1;
+
+int fkref_set_threads(int threads) {
+  if (threads < 1 || threads > 1024) return -1;
+  g_threads = threads;
+  return 0;
+}
+
+/* Row j of input row i, in the reference GEMV's order. */
+static float gemv_row(const void *w, int wtype, const void *x, int xtype, int i, int j, int k, int width, int pack,
+                      int split) {
   const int packs = k / pack;
   const int vlanes = split * width;
   const int chains = pack / 4;
-  float *lane_total = (float *)malloc(sizeof(float) * (size_t)vlanes);
-  float *acc = (float *)malloc(sizeof(float) * (size_t)chains);
+  float small[4096];
+  float *lane_total = vlanes <= 4096 ? small : (float *)malloc(sizeof(float) * (size_t)vlanes);
+  float acc[16];
   float partial[64];
-  if (!lane_total || !acc) {
-    free(lane_total);
-    free(acc);
-    return -2;
-  }
-  for (int i = 0; i < m; i++) {
-    for (int j = 0; j < n; j++) {
-      for (int v = 0; v < vlanes; v++) {
-        /* Lane v of the virtual lanes (split q = v / width) visits packs
-         * v, v + split * width, ...; each pack's elements go four to a chain,
-         * ((x0 w0 + x1 w1) + (x2 w2 + x3 w3)), each chain its own sum. */
-        for (int c = 0; c < chains; c++) acc[c] = 0.0f;
-        for (int jp = v; jp < packs; jp += vlanes) {
-          for (int c = 0; c < chains; c++) {
-            size_t at = (size_t)jp * pack + 4 * c;
-            float p0 = element(x, xtype, (size_t)i * k + at) * element(w, wtype, (size_t)j * k + at);
-            float p1 = element(x, xtype, (size_t)i * k + at + 1) * element(w, wtype, (size_t)j * k + at + 1);
-            float p2 = element(x, xtype, (size_t)i * k + at + 2) * element(w, wtype, (size_t)j * k + at + 2);
-            float p3 = element(x, xtype, (size_t)i * k + at + 3) * element(w, wtype, (size_t)j * k + at + 3);
-            acc[c] = acc[c] + ((p0 + p1) + (p2 + p3));
-          }
-        }
-        /* The lane's chains in order (Gemv.hs:216-220, inOrder). */
-        float t = acc[0];
-        for (int c = 1; c < chains; c++) t = t + acc[c];
-        lane_total[v] = t;
+  if (!lane_total) return __builtin_nanf("");
+  for (int v = 0; v < vlanes; v++) {
+    /* Lane v of the virtual lanes (split q = v / width) visits packs
+     * v, v + split * width, ...; each pack's elements go four to a chain,
+     * ((x0 w0 + x1 w1) + (x2 w2 + x3 w3)), each chain its own sum. */
+    for (int c = 0; c < chains; c++) acc[c] = 0.0f;
+    for (int jp = v; jp < packs; jp += vlanes) {
+      for (int c = 0; c < chains; c++) {
+        size_t at = (size_t)jp * pack + 4 * c;
+        float p0 = element(x, xtype, (size_t)i * k + at) * element(w, wtype, (size_t)j * k + at);
+        float p1 = element(x, xtype, (size_t)i * k + at + 1) * element(w, wtype, (size_t)j * k + at + 1);
+        float p2 = element(x, xtype, (size_t)i * k + at + 2) * element(w, wtype, (size_t)j * k + at + 2);
+        float p3 = element(x, xtype, (size_t)i * k + at + 3) * element(w, wtype, (size_t)j * k + at + 3);
+        acc[c] = acc[c] + ((p0 + p1) + (p2 + p3));
       }
-      for (int q = 0; q < split; q++) partial[q] = fkref_simd_sum(lane_total + (size_t)q * width, width);
-      float total = fkref_combine_splits(partial, split);
+    }
+    /* The lane's chains in order (Gemv.hs:216-220, inOrder). */
+    float t = acc[0];
+    for (int c = 1; c < chains; c++) t = t + acc[c];
+    lane_total[v] = t;
+  }
+  for (int q = 0; q < split; q++) partial[q] = fkref_simd_sum(lane_total + (size_t)q * width, width);
+  if (lane_total != small) free(lane_total);
+  return fkref_combine_splits(partial, split);
+}
+
+int fkref_gemv(const void *w, int wtype, const void *x, int xtype, float *y, const float *row_scale, int n, int k,
+               int m, int width, int pack, int split) {
+  if (n < 0 || k <= 0 || m <= 0 || width <= 0 || width > 1024 || pack < 4 || pack > 64 || pack % 4 || k % pack ||
+      split <= 0 || split > 64)
+    return -1;
+  for (int i = 0; i < m; i++) {
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
+    for (int j = 0; j < n; j++) {
+      float total = gemv_row(w, wtype, x, xtype, i, j, k, width, pack, split);
       if (row_scale) total = total * row_scale[j];
       y[(size_t)i * n + j] = total;
     }
   }
-  free(lane_total);
-  free(acc);
   return 0;
 }
 

@@ -58,6 +58,9 @@ float fkref_combine_splits(const float *partials, int splits);
  * pack: elements a lane loads at once (a multiple of 4); split: SIMD groups
  * sharing a row.  `row_scale` (n f32, or NULL) multiplies each output row's
  * sum: y = total * scale (the int8 weight-only layer). */
+/* Threads the GEMVs' rows are spread over (1: the CPU target's one thread).
+ * Each row's arithmetic is the same at any count. */
+int fkref_set_threads(int threads);
 int fkref_gemv(const void *w, int wtype, const void *x, int xtype, float *y, const float *row_scale, int n, int k,
                int m, int width, int pack, int split);
 

@@ -44,6 +44,7 @@ def lib() -> ctypes.CDLL:
             "fkref_tg_reduce_sum": (ctypes.c_float, [_vp, _i, _i]),
             "fkref_tg_reduce_max": (ctypes.c_float, [_vp, _i, _i]),
             "fkref_combine_splits": (ctypes.c_float, [_vp, _i]),
+            "fkref_set_threads": (_i, [_i]),
             "fkref_gemv": (_i, [_vp, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i]),
             "fkref_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_float, ctypes.c_float, _i, _i, _i]),
             "fkref_softmax": (_i, [_vp, _vp, _i, _i, _i, _i, _i]),

@@ -4,7 +4,7 @@ The matrix cores sum over k in their own order, so the bar is the reference's
 bound for binary32 accumulation (test/Test/FuryKernel/GemvTest.hs:127-130;
 the tile contract of src/FuryKernel/Tile.hs:5-24): |C - exact| <=
 2 (k + 64) 2^-24 sum |a b| + 2^-126.  Small shapes check every element (and so
-the lane layout of v_mfma_f32_32x32x16_f16 and the tile layout); the 1B
+the lane layout of v_mfma_f32_16x16x32_f16 and the tile layout); the 1B
 prefill's shapes check sampled rows.  The SiLU·mul epilogue rounds to f16:
 within 2e-3 relative (the f16 bar) of the f64 value.
 """

@@ -137,3 +137,20 @@ def test_argmax_key_special_cases():
         a = np.array(x, np.float32)
         key = int(L.fkref_argmax_keyed(a.ctypes.data, len(a)))
         assert 0xFFFFFFFF - (key & 0xFFFFFFFF) == want == _fold(a.tolist()), x
+
+
+def test_gemv_rows_spread_over_threads_are_the_same_bits():
+    """The all-cores CPU figure spreads the GEMV's rows over threads: each
+    row's arithmetic, and so its bits, is the one thread's."""
+    rng = np.random.default_rng(11)
+    w = rng.standard_normal((300, 512)).astype(np.float16)
+    x = rng.standard_normal(512).astype(np.float32)
+    one = fkref.gemv(w, x, width=32, pack=8)
+    L = fkref.lib()
+    assert L.fkref_set_threads(8) == 0
+    try:
+        many = fkref.gemv(w, x, width=32, pack=8)
+    finally:
+        L.fkref_set_threads(1)
+    assert np.array_equal(one.view(np.uint32), many.view(np.uint32))
+    assert L.fkref_set_threads(0) != 0
