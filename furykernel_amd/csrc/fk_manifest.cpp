@@ -57,7 +57,8 @@ std::vector<fk_abi_param> gemv_step_params() {
           FK_P(S, pro_mode, "u32"),    FK_P(S, seg, "u32"),           FK_P(S, eps, "f32"),
           FK_P(S, factor, "f32"),      FK_P(S, gfactor, "f32"),       FK_P(S, has_gamma, "u32"),
           FK_P(S, epi_mode, "u32"),    FK_P(S, store_tile, "u32"),    FK_P(S, table_rows, "u32"),
-          FK_P(S, blocks, "u32"),      FK_P(S, arg_slots, "u32")};
+          FK_P(S, blocks, "u32"),      FK_P(S, arg_slots, "u32"),      FK_P(S, act, "u32"),
+          FK_P(S, src2_off, "u32"),    FK_P(S, cap, "f32")};
 }
 
 std::vector<fk_abi_param> gemm_params() {
@@ -65,7 +66,7 @@ std::vector<fk_abi_param> gemm_params() {
   return {FK_P(S, m, "u32"),          FK_P(S, k, "u32"),          FK_P(S, n_anchors, "u32"),
           FK_PA(S, first_col, 0, "u32"), FK_PA(S, first_col, 1, "u32"), FK_PA(S, first_col, 2, "u32"),
           FK_PA(S, first_col, 3, "u32"), FK_PA(S, ldc, 0, "u32"),       FK_PA(S, ldc, 1, "u32"),
-          FK_PA(S, ldc, 2, "u32")};
+          FK_PA(S, ldc, 2, "u32"),     FK_P(S, act, "u32")};
 }
 
 std::vector<Entry> build() {
@@ -108,7 +109,7 @@ std::vector<Entry> build() {
   {
     using S = fk_init_normal_params;
     add("fk_init_normal", 0, {buf("dst", "write", "f32")},
-        {FK_P(S, count, "u64"), FK_P(S, seed, "u64"), FK_P(S, std, "f32"), FK_P(S, f16, "u32")}, sizeof(S));
+        {FK_P(S, count, "u64"), FK_P(S, seed, "u64"), FK_P(S, std, "f32"), FK_P(S, dtype, "u32")}, sizeof(S));
   }
 
   // The GEMV step: every shape with every prologue and epilogue it is built for.
@@ -117,7 +118,9 @@ std::vector<Entry> build() {
     bool pairs;
   };
   const Shape shapes[] = {{"fk_step_gemv_f16_k2048_r1", "f16", false}, {"fk_step_gemv_f16_k2048_r2", "f16", true},
-                          {"fk_step_gemv_f16_k8192_r1", "f16", false}, {"fk_step_gemv_f32_k256_r1", "f32", false},
+                          {"fk_step_gemv_f16_k8192_r1", "f16", false}, {"fk_step_gemv_bf16_k2048_r1", "bf16", false},
+                          {"fk_step_gemv_bf16_k2048_r2", "bf16", true}, {"fk_step_gemv_bf16_k8192_r1", "bf16", false},
+                          {"fk_step_gemv_f32_k256_r1", "f32", false},
                           {"fk_step_gemv_f32_k256_r2", "f32", true},   {"fk_step_gemv_f32_k1024_r1", "f32", false},
                           {"fk_step_gemv_f32_k1024_r2", "f32", true}};
   for (const Shape &s : shapes) {
@@ -130,7 +133,7 @@ std::vector<Entry> build() {
         buf("res_table", "read", wt), buf("res_token", "read", "u32"), buf("epi_out", "write", "f32"),
         buf("arg", "read_write", "u64")};
     for (int pro = 0; pro < 5; pro++)
-      for (int epi = 0; epi < 5; epi++) {
+      for (int epi = 0; epi < 6; epi++) {
         if (epi == FK_EPI_SILU_MUL && !s.pairs) continue;
         add(std::string(s.name) + "_p" + std::to_string(pro) + "_e" + std::to_string(epi), 512, b,
             gemv_step_params(), sizeof(fk_step_gemv_params));
@@ -173,8 +176,10 @@ std::vector<Entry> build() {
   }
   add("fk_step_argmax", 0, {buf("x", "read", "f32"), buf("out", "write", "u32")},
       {FK_P(fk_step_argmax_params, n, "u32")}, sizeof(fk_step_argmax_params));
-  add("fk_step_silu_mul", 0, {buf("a", "read", "f32"), buf("b", "read", "f32"), buf("y", "write", "f32")},
-      {FK_P(fk_step_silu_mul_params, n, "u32")}, sizeof(fk_step_silu_mul_params));
+  add("fk_step_act_mul", 0, {buf("a", "read", "f32"), buf("b", "read", "f32"), buf("y", "write", "f32")},
+      {FK_P(fk_step_act_mul_params, n, "u32"), FK_P(fk_step_act_mul_params, act, "u32"),
+       FK_P(fk_step_act_mul_params, b_off, "u32")},
+      sizeof(fk_step_act_mul_params));
   add("fk_step_advance", 0,
       {buf("next_token", "read", "u32"), buf("token", "write", "u32"), buf("position", "read_write", "u32")},
       {FK_P(fk_step_advance_params, context, "u32"), FK_P(fk_step_advance_params, step, "u32")},
@@ -239,6 +244,9 @@ std::vector<Entry> build() {
            FK_P(S, slots, "u32"), FK_P(S, window, "u32"), FK_P(S, cache_bf16, "u32"), FK_P(S, scale, "f32")},
           sizeof(S));
   }
+  add("fk_prefill_softcap", 256, {buf("x", "read", "f32"), buf("y", "write", "f32")},
+      {FK_P(fk_prefill_softcap_params, count, "u32"), FK_P(fk_prefill_softcap_params, cap, "f32")},
+      sizeof(fk_prefill_softcap_params));
   add("fk_prefill_argmax", 256, {buf("x", "read", "f32"), buf("out", "write", "u32")},
       {FK_P(fk_prefill_argmax_params, rows, "u32"), FK_P(fk_prefill_argmax_params, width, "u32")},
       sizeof(fk_prefill_argmax_params));
@@ -300,8 +308,8 @@ bool gemv_modes(const char *entry, int *pro, int *epi, int *wbytes, int *kmax, i
   const char *pfx = "fk_step_gemv_";
   if (std::strncmp(entry, pfx, std::strlen(pfx)) != 0) return false;
   char wt[8] = {0};
-  if (std::sscanf(entry + std::strlen(pfx), "%3[a-z0-9]_k%d_r%d_p%d_e%d", wt, kmax, r, pro, epi) != 5) return false;
-  *wbytes = std::strcmp(wt, "f16") == 0 ? 2 : 4;
+  if (std::sscanf(entry + std::strlen(pfx), "%4[a-z0-9]_k%d_r%d_p%d_e%d", wt, kmax, r, pro, epi) != 5) return false;
+  *wbytes = std::strcmp(wt, "f32") == 0 ? 4 : 2;
   return true;
 }
 
@@ -390,6 +398,10 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
     for (uint32_t j = 0; j < p.n_anchors; j++) widest = p.rows[j] > widest ? p.rows[j] : widest;
     if (epi == FK_EPI_SILU_MUL && (p.n_anchors != 2 || p.rows[0] != p.rows[1] || r < 2))
       return bad(err, cap, FK_ERR_ARG, "%s: the SiLU·mul epilogue on %u anchors, blocks of %d", entry, p.n_anchors, r);
+    if (epi == FK_EPI_SOFTCAP && (p.n_anchors != 1 || !(p.cap > 0.0f && p.cap < __builtin_inff())))
+      return bad(err, cap, FK_ERR_ARG, "%s: a softcap of %g on %u anchors", entry, (double)p.cap, p.n_anchors);
+    if ((p.act != FK_ACT_SILU && p.act != FK_ACT_GELU_TANH) || p.src2_off % 4)
+      return bad(err, cap, FK_ERR_ARG, "%s: activation %u, second row at %u", entry, p.act, p.src2_off);
     static const char *w[3] = {"w0", "w1", "w2"}, *y[3] = {"y0", "y1", "y2"};
     for (uint32_t j = 0; j < p.n_anchors; j++) {
       need.push_back({w[j], (uint64_t)p.rows[j] * p.k * wb});
@@ -402,7 +414,7 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
     } else {
       need.push_back({"src", k4});
     }
-    if (pro == FK_PRO_SILU_MUL) need.push_back({"src2", k4});
+    if (pro == FK_PRO_SILU_MUL) need.push_back({"src2", k4 + (uint64_t)p.src2_off * 4});
     if (pro == FK_PRO_RMSNORM || pro == FK_PRO_GATHER_RMSNORM) need.push_back({"gamma", k4});
     if (epi == FK_EPI_ADD_STORED) {
       need.push_back({"res", widest * 4});
@@ -415,6 +427,9 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({"epi_out", (uint64_t)p.rows[0] * 4});
     } else if (epi == FK_EPI_ARGMAX) {
       need.push_back({"arg", (uint64_t)p.arg_slots * 8});
+    } else if (epi == FK_EPI_SOFTCAP) {
+      need.push_back({"epi_out", (uint64_t)p.rows[0] * 4});
+      if (p.arg_slots) need.push_back({"arg", (uint64_t)p.arg_slots * 8});
     }
   } else if (std::strcmp(entry, "fk_step_attend") == 0) {
     fk_step_attend_params p;

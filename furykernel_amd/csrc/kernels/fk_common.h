@@ -131,6 +131,39 @@ __device__ __forceinline__ float block_reduce(float v, float *slots) {
 // rsqrt, exp: binary64's, rounded once to binary32 (src/FuryKernel/Interp.hs:828-854).
 __device__ __forceinline__ float rsqrt_once(float x) { return (float)(1.0 / ::sqrt((double)x)); }
 __device__ __forceinline__ float exp_once(float x) { return (float)::exp((double)x); }
+__device__ __forceinline__ float tanh_once(float x) { return (float)::tanh((double)x); }
+
+// SiLU(a) · b: a / (1 + e^-a), e^-a binary64's rounded once, then times b.
+__device__ __forceinline__ float silu_mul(float a, float b) {
+  const float e = exp_once(-a);
+  const float d = 1.0f + e;
+  return (a / d) * b;
+}
+
+// GELU in its tanh form (src/FuryKernel/Program/Eval.hs:658-659) in binary32,
+// left to right as the formula reads, its constants rounded once and tanh
+// binary64's rounded once: (0.5 a) (1 + tanh(c0 (a + ((c1 a) a) a))).
+__device__ __forceinline__ float gelu_tanh(float a) {
+  const float c0 = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float c1 = 0.044715f;
+  const float cube = ((c1 * a) * a) * a;
+  const float t = tanh_once(c0 * (a + cube));
+  return (0.5f * a) * (1.0f + t);
+}
+
+// act(a) · b for an activation FK_ACT_*.
+__device__ __forceinline__ float act_mul(float a, float b, uint32_t act) {
+  return act == FK_ACT_GELU_TANH ? gelu_tanh(a) * b : silu_mul(a, b);
+}
+
+// A softcap (Eval.hs:384-390): cap tanh(x / cap).
+__device__ __forceinline__ float softcap(float x, float cap) { return cap * tanh_once(x / cap); }
+
+// A bfloat16 element, as its bits (weights of the reference's builder are
+// bf16: src/FuryKernel/Program/Build.hs:175-176).
+struct bf16_t {
+  uint16_t bits;
+};
 
 // widenF16 (src/FuryKernel/Numerics.hs:51-71): exact; a NaN comes out quiet
 // with its sign and payload.

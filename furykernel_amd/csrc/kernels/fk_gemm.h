@@ -276,12 +276,18 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
         for (int r = 0; r < 4; r++) {
           const float gt = acc[i][j][r];
           const float u = acc[i][j + 4][r];
-          // silu(g) u = g / (1 + e^-g) · u with the hardware's exp and
-          // reciprocal (a few ulp of binary32), then rounded once to f16
-          // (2^-11): the f16 rounding bounds the error.  e^-g overflowing
-          // gives silu 0, as the limit.
+          // silu(g) u = g / (1 + e^-g) · u, or gelu(g) u = 0.5 g (1 +
+          // tanh(y)) u with tanh(y) = 1 - 2 / (1 + e^2y), with the hardware's
+          // exp and reciprocal (a few ulp of binary32), then rounded once to
+          // f16 (2^-11): the f16 rounding bounds the error.  An exponential
+          // overflowing gives the limits (silu 0, tanh 1).  The choice is a
+          // select, uniform over the launch.
           const float e = __expf(-gt);
-          h[r] = fk::to_f16(gt * __builtin_amdgcn_rcpf(1.0f + e) * u);
+          const float silu = gt * __builtin_amdgcn_rcpf(1.0f + e);
+          const float y = 0.7978845608028654f * (gt + ((0.044715f * gt) * gt) * gt);
+          const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(2.0f * y));
+          const float gelu = (0.5f * gt) * (1.0f + th);
+          h[r] = fk::to_f16((p.act == FK_ACT_GELU_TANH ? gelu : silu) * u);
         }
         uint2 w;
         w.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);

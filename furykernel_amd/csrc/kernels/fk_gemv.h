@@ -102,6 +102,18 @@ __device__ __forceinline__ void unpack(const uint4 (&u)[P / 8], float (&out)[P],
 
 // One 16-byte word of W widened to f32 exactly: 4 f32, 8 f16 or 16 int8.
 template <int P>
+__device__ __forceinline__ void unpack(const uint4 (&u)[P / 8], float (&out)[P], bf16_t) {
+#pragma unroll
+  for (int i = 0; i < P / 8; i++) {
+    const uint32_t words[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      out[8 * i + 2 * h] = __uint_as_float(words[h] << 16);
+      out[8 * i + 2 * h + 1] = __uint_as_float(words[h] & 0xFFFF0000u);
+    }
+  }
+}
+template <int P>
 __device__ __forceinline__ void unpack_w(const uint4 &u, float (&out)[P], float) {
   static_assert(P == 4, "four f32 a word");
   out[0] = __uint_as_float(u.x);

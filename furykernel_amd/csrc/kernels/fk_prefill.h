@@ -7,6 +7,7 @@
 //                          (the GEMM's A)
 //   fk_prefill_rope_store  q RoPE'd into f16 rows; k RoPE'd and v stored into
 //                          the caches at each row's position
+//   fk_prefill_softcap     a softcap over rows (the head's, before the argmax)
 //   fk_prefill_argmax      the greedy token of each row
 //
 // (The causal attention between them, fk_prefill_attend_g*, is fk_attend.h:
@@ -183,6 +184,15 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store(
 // of equals, by the decode step's 64-bit keys (value order, then the
 // complement of the index; a NaN at index 0 wins, elsewhere loses:
 // src/FuryKernel/Program/Eval.hs:681-685).  One wave a row.
+
+// A softcap over the logits of every row (src/FuryKernel/Program/Eval.hs:
+// 384-390), in place or into another buffer: y = cap tanh(x / cap), as the
+// decode step's epilogue computes it.
+extern "C" __global__ void __launch_bounds__(256) fk_prefill_softcap(const float *__restrict__ x,
+                                                                     float *__restrict__ y,
+                                                                     fk_prefill_softcap_params p) {
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < p.count; i += gridDim.x * 256) y[i] = fk::softcap(x[i], p.cap);
+}
 
 extern "C" __global__ void __launch_bounds__(256) fk_prefill_argmax(const float *__restrict__ x,
                                                                     uint32_t *__restrict__ out,

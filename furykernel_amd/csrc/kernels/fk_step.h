@@ -9,7 +9,7 @@
 //                    positions for one KV head, stored as partials
 //   fk_step_combine  attention's combine of its splits
 //   fk_step_argmax   the greedy token of a stored row
-//   fk_step_silu_mul a stored SiLU·mul (the light step `store_gelus` plans)
+//   fk_step_act_mul  a stored act·mul, SiLU or GELU-tanh (the light step `store_gelus` plans)
 //   fk_step_advance  the next decode step's token and position, on the device
 //
 // Arithmetic follows the evaluator's contract (src/FuryKernel/Program/Eval.hs:
@@ -114,10 +114,10 @@ extern "C" __global__ void __launch_bounds__(1024)
 }
 
 extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
-    fk_step_silu_mul(const float *__restrict__ a, const float *__restrict__ b, float *__restrict__ y,
-                     fk_step_silu_mul_params p) {
+    fk_step_act_mul(const float *__restrict__ a, const float *__restrict__ b, float *__restrict__ y,
+                    fk_step_act_mul_params p) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < p.n) y[i] = fk::silu_mul(a[i], b[i]);
+  if (i < p.n) y[i] = fk::act_mul(a[i], b[p.b_off + i], p.act);
 }
 
 // The next decode step's inputs: its token is this step's greedy token, its
@@ -149,8 +149,10 @@ extern "C" __global__ void __launch_bounds__(256) fk_init_normal(void *__restric
     const double t = 6.283185307179586 * u2;
     const double z = (i & 1) ? r * ::sin(t) : r * ::cos(t);
     const float v = (float)(z * (double)p.std);
-    if (p.f16)
+    if (p.dtype == 1)
       reinterpret_cast<uint16_t *>(dst)[i] = fk::narrow_f16(v);
+    else if (p.dtype == 2)
+      reinterpret_cast<uint16_t *>(dst)[i] = fk::narrow_bf16(v);
     else
       reinterpret_cast<float *>(dst)[i] = v;
   }

@@ -38,11 +38,14 @@
 
 namespace fk {
 
-// SiLU(a) · b: a / (1 + e^-a), e^-a binary64's rounded once, then times b.
-__device__ __forceinline__ float silu_mul(float a, float b) {
-  const float e = exp_once(-a);
-  const float d = 1.0f + e;
-  return (a / d) * b;
+// A weight or table element as binary32 (exact for every type here).
+__device__ __forceinline__ float to_float(float x) { return x; }
+__device__ __forceinline__ float to_float(_Float16 x) { return (float)x; }
+__device__ __forceinline__ float to_float(bf16_t x) { return __uint_as_float((uint32_t)x.bits << 16); }
+template <typename WT>
+__device__ __forceinline__ float widen_half(uint16_t h) {
+  if constexpr (__is_same(WT, bf16_t)) return __uint_as_float((uint32_t)h << 16);
+  else return widen_f16(h);
 }
 
 // An anchor's pointer or count by index, without indexing an array: a
@@ -194,8 +197,8 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
       const WT *row = table + (size_t)tok * k + 4 * j;
       if constexpr (sizeof(WT) == 2) {
         const uint2 h = *reinterpret_cast<const uint2 *>(row);
-        xa[m] = make_float4(fk::widen_f16((uint16_t)(h.x & 0xFFFFu)), fk::widen_f16((uint16_t)(h.x >> 16)),
-                            fk::widen_f16((uint16_t)(h.y & 0xFFFFu)), fk::widen_f16((uint16_t)(h.y >> 16)));
+        xa[m] = make_float4(fk::widen_half<WT>((uint16_t)(h.x & 0xFFFFu)), fk::widen_half<WT>((uint16_t)(h.x >> 16)),
+                            fk::widen_half<WT>((uint16_t)(h.y & 0xFFFFu)), fk::widen_half<WT>((uint16_t)(h.y >> 16)));
       } else {
         const float4 v = *reinterpret_cast<const float4 *>(row);
         xa[m] = v;
@@ -203,7 +206,7 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
     } else {
       xa[m] = reinterpret_cast<const float4 *>(src)[j];
     }
-    if constexpr (SILU) xb[m] = reinterpret_cast<const float4 *>(src2)[j];
+    if constexpr (SILU) xb[m] = reinterpret_cast<const float4 *>(src2 + p.src2_off)[j];
     // A norm without gains has a row of ones bound here (the product is then
     // not taken), so the load is unconditional.
     if constexpr (NORM) ga[m] = reinterpret_cast<const float4 *>(gamma)[j];
@@ -232,8 +235,9 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
       v.w = v.w * gfactor;
     }
     if constexpr (SILU) {
-      v = make_float4(fk::silu_mul(v.x, xb[m].x), fk::silu_mul(v.y, xb[m].y), fk::silu_mul(v.z, xb[m].z),
-                      fk::silu_mul(v.w, xb[m].w));
+      const uint32_t act = p.act;
+      v = make_float4(fk::act_mul(v.x, xb[m].x, act), fk::act_mul(v.y, xb[m].y, act),
+                      fk::act_mul(v.z, xb[m].z, act), fk::act_mul(v.w, xb[m].w, act));
     }
     if (j < packs4) {
       if constexpr (NORM) {
@@ -300,7 +304,7 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
       if constexpr (EPI == FK_EPI_ADD_STORED) {
         resv = res[min(r, n - 1)];
       } else {
-        resv = (float)res_table[(size_t)rtok * n + min(r, n - 1)] * gfactor;
+        resv = fk::to_float(res_table[(size_t)rtok * n + min(r, n - 1)]) * gfactor;
       }
     }
     if constexpr (DB) {
@@ -353,8 +357,14 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
 #pragma unroll
     for (int q = 0; q < R; q++) {
       if (blk.live[q]) {
+        float capped = 0.0f;
+        if constexpr (EPI == FK_EPI_SOFTCAP) capped = fk::softcap(t[q], p.cap);
         if constexpr (EPI == FK_EPI_ARGMAX) {
           const uint64_t key = fk::argmax_key(t[q], blk.row[q]);
+          best = key > best ? key : best;
+        }
+        if constexpr (EPI == FK_EPI_SOFTCAP) {
+          const uint64_t key = fk::argmax_key(capped, blk.row[q]);
           best = key > best ? key : best;
         }
         if (lane == (uint32_t)q) {
@@ -363,8 +373,9 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
           if (p.store_tile) fk::pick3(a, y0, y1, y2)[r] = t[q];
           if constexpr (RESIDUAL) epi_out[r] = resv + t[q];
           if constexpr (EPI == FK_EPI_SILU_MUL) {
-            if (q < R / 2) epi_out[r] = fk::silu_mul(t[q], t[(q + R / 2) % R]);
+            if (q < R / 2) epi_out[r] = fk::act_mul(t[q], t[(q + R / 2) % R], p.act);
           }
+          if constexpr (EPI == FK_EPI_SOFTCAP) epi_out[r] = capped;
         }
       }
     }
@@ -387,9 +398,10 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
       fk::issue_block<WT, P, R, KPL>(wa, ba, w0, w1, w2, k, packs, lane, p);
     }
   }
-  if constexpr (EPI == FK_EPI_ARGMAX) {
+  if constexpr (EPI == FK_EPI_ARGMAX || EPI == FK_EPI_SOFTCAP) {
     // The threadgroup's largest key into its own slot of `arg`; the token
-    // launch takes the largest of the slots.
+    // launch takes the largest of the slots (a softcap with no slots folds no
+    // argmax).
     if (lane == 0) bests[wave] = best;
     __syncthreads();
     if (tid == 0 && blockIdx.x < p.arg_slots) {
@@ -419,7 +431,8 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
   FK_STEP_GEMV(NAME##_p##PRO##_e0, WT, P, R, KPL, DB, PRO, 0) \
   FK_STEP_GEMV(NAME##_p##PRO##_e1, WT, P, R, KPL, DB, PRO, 1) \
   FK_STEP_GEMV(NAME##_p##PRO##_e2, WT, P, R, KPL, DB, PRO, 2) \
-  FK_STEP_GEMV(NAME##_p##PRO##_e4, WT, P, R, KPL, DB, PRO, 4)
+  FK_STEP_GEMV(NAME##_p##PRO##_e4, WT, P, R, KPL, DB, PRO, 4) \
+  FK_STEP_GEMV(NAME##_p##PRO##_e5, WT, P, R, KPL, DB, PRO, 5)
 #define FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, PRO) \
   FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, PRO)         \
   FK_STEP_GEMV(NAME##_p##PRO##_e3, WT, P, R, KPL, DB, PRO, 3)
@@ -443,6 +456,10 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
 FK_STEP_GEMV_SHAPE(fk_step_gemv_f16_k2048_r1, _Float16, 8, 1, 4, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f16_k2048_r2, _Float16, 8, 2, 4, false)
 FK_STEP_GEMV_SHAPE(fk_step_gemv_f16_k8192_r1, _Float16, 8, 1, 16, false)
+// bf16 weights (the reference builder's): the f16 shapes.
+FK_STEP_GEMV_SHAPE(fk_step_gemv_bf16_k2048_r1, fk::bf16_t, 8, 1, 4, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_bf16_k2048_r2, fk::bf16_t, 8, 2, 4, false)
+FK_STEP_GEMV_SHAPE(fk_step_gemv_bf16_k8192_r1, fk::bf16_t, 8, 1, 16, false)
 // f32 weights: k up to 256 and 1024.
 FK_STEP_GEMV_SHAPE(fk_step_gemv_f32_k256_r1, float, 4, 1, 1, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k256_r2, float, 4, 2, 1, false)

@@ -54,6 +54,8 @@ class DecodeSession:
                     self.engine.write(name, np.ones(src.kind.dims[0], np.float32))
                 else:
                     self.engine.init_normal(name, seed + 7919 * i, std)
+            if f"widen:{src.name}" in self.lowered.buffers:
+                self.engine.write(f"widen:{src.name}", np.ones(int(np.prod(src.kind.dims)), np.float32))
             if isinstance(src.kind, SCache):
                 self.engine.init_normal(f"cache:{src.name}", cache_seed + 7919 * i, 1.0)
             if isinstance(src.kind, SInput):

@@ -26,7 +26,8 @@ _STRUCTS = {
     "fk_step_attend": K.StepAttendParams,
     "fk_step_combine": K.StepCombineParams,
     "fk_step_argmax": K.CountParams,
-    "fk_step_silu_mul": K.CountParams,
+    "fk_step_act_mul": K.ActMulParams,
+    "fk_prefill_softcap": K.PrefillSoftcapParams,
     "fk_step_token": K.StepTokenParams,
     "fk_gemm_f16_store": K.GemmParams,
     "fk_gemm_f16_add": K.GemmParams,
@@ -41,6 +42,14 @@ _STRUCTS = {
     "fk_prefill_attend_g4": K.PrefillAttendParams,
     "fk_prefill_argmax": K.PrefillArgmaxParams,
 }
+
+
+def widen(wtype: str, w) -> np.ndarray:
+    """Weights of type `wtype` (bf16 as uint16 bits) as exact f32 values."""
+    a = np.asarray(w)
+    if wtype == "bf16":
+        return (a.astype(np.uint32) << 16).view(np.float32)
+    return a.astype(np.float32)
 
 
 def params_struct(launch: Launch) -> ctypes.Structure:
@@ -71,10 +80,10 @@ def _gemv_needs(launch: Launch) -> dict:
     wb = _ELT[wt]
     n, rows, k = p["n_anchors"], p["rows"], p["k"]
     widest = max(rows[:n])
-    need = {"src": (k * 4, "f32"), "src2": (k * 4, "f32"), "gamma": (k * 4, "f32"),
+    need = {"src": (k * 4, "f32"), "src2": ((k + p.get("src2_off", 0)) * 4, "f32"), "gamma": (k * 4, "f32"),
             "table": (p.get("table_rows", 1) * k * wb, wt), "token": (4, "u32"), "res_token": (4, "u32"),
             "res": (widest * 4, "f32"), "res_table": (p.get("table_rows", 1) * widest * wb, wt),
-            "epi_out": ((rows[0] if epi == K.EPI_SILU_MUL else widest) * 4, "f32"),
+            "epi_out": ((rows[0] if epi in (K.EPI_SILU_MUL, K.EPI_SOFTCAP) else widest) * 4, "f32"),
             "arg": (p.get("arg_slots", 0) * 8, "u64")}
     for j in range(n):
         need[f"w{j}"] = (rows[j] * k * wb, wt)
@@ -117,6 +126,10 @@ def check_launch(launch: Launch, specs: dict) -> None:
             raise K.LaunchError(f"{e}: k = {p['k']} past {kmax}, or {p['n_anchors']} anchors")
         if epi == K.EPI_SILU_MUL and (p["n_anchors"] != 2 or p["rows"][0] != p["rows"][1] or r < 2):
             raise K.LaunchError(f"{e}: the SiLU·mul epilogue on anchors {p['rows']}, blocks of {r}")
+        if epi == K.EPI_SOFTCAP and (p["n_anchors"] != 1 or not 0 < p.get("cap", 0) < float("inf")):
+            raise K.LaunchError(f"{e}: a softcap of {p.get('cap')} on {p['n_anchors']} anchors")
+        if p.get("act", 0) not in (K.ACT_SILU, K.ACT_GELU_TANH) or p.get("src2_off", 0) % 4:
+            raise K.LaunchError(f"{e}: activation {p.get('act')}, second row at {p.get('src2_off')}")
     reads = K.launch_reads(e, launch.params)
     unbound = sorted(b for b in reads if launch.bind.get(b) is None)
     if unbound:
@@ -184,6 +197,17 @@ class Engine:
             raise ValueError(f"{name}: {a.size} elements for a buffer of {spec.count}")
         self.buffers[name].write(a)
 
+    def write_weights(self, weights: dict) -> None:
+        """Host weights by source name (bf16 ones as their uint16 bits) into
+        the buffers the step reads them from: as given, and widened exactly to
+        f32 where the lowering keeps an f32 copy (an RMSNorm's gains)."""
+        for src, w in weights.items():
+            if f"weight:{src}" in self.lowered.buffers:
+                self.write(f"weight:{src}", w)
+            wide = f"widen:{src}"
+            if wide in self.lowered.buffers:
+                self.write(wide, widen(self.lowered.program.source_named(src).kind.type, w))
+
     def read(self, name: str) -> np.ndarray:
         spec = self.spec(name)
         return self.buffers[name].read(_NP[spec.dtype], spec.count)
@@ -197,13 +221,13 @@ class Engine:
     def init_normal(self, name: str, seed: int, std: float) -> None:
         """Synthetic values on the device: std * N(0, 1), SplitMix64 + Box-Muller."""
         spec = self.spec(name)
-        if spec.dtype not in ("f16", "f32"):
+        codes = {"f32": 0, "f16": 1, "bf16": 2}
+        if spec.dtype not in codes:
             raise ValueError(f"{name}: normals of {spec.dtype}")
         buf = self.buffers[name]
         groups = min(max(spec.count // 256, 1), 65536)
         self.kernels.launch("fk_init_normal", groups, 256, {"dst": buf.ptr},
-                            K.InitNormalParams(spec.count, seed & 0xFFFFFFFFFFFFFFFF, std,
-                                               1 if spec.dtype == "f16" else 0))
+                            K.InitNormalParams(spec.count, seed & 0xFFFFFFFFFFFFFFFF, std, codes[spec.dtype]))
 
     def zero(self, name: str) -> None:
         self.kernels.fill_u32(self.buffers[name], 0, (self.spec(name).nbytes + 3) // 4)

@@ -82,12 +82,15 @@ class StepGemvParams(ctypes.Structure):
         ("table_rows", ctypes.c_uint32),
         ("blocks", ctypes.c_uint32),
         ("arg_slots", ctypes.c_uint32),
+        ("act", ctypes.c_uint32),
+        ("src2_off", ctypes.c_uint32),
+        ("cap", ctypes.c_float),
     ]
 
 
 class GemmParams(ctypes.Structure):
     _fields_ = [("m", ctypes.c_uint32), ("k", ctypes.c_uint32), ("n_anchors", ctypes.c_uint32),
-                ("first_col", ctypes.c_uint32 * 4), ("ldc", ctypes.c_uint32 * 3)]
+                ("first_col", ctypes.c_uint32 * 4), ("ldc", ctypes.c_uint32 * 3), ("act", ctypes.c_uint32)]
 
 
 class GemmQkvParams(ctypes.Structure):
@@ -117,6 +120,14 @@ class PrefillAttendParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
                 ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32), ("window", ctypes.c_uint32),
                 ("cache_bf16", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+class PrefillSoftcapParams(ctypes.Structure):
+    _fields_ = [("count", ctypes.c_uint32), ("cap", ctypes.c_float)]
+
+
+class ActMulParams(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_uint32), ("act", ctypes.c_uint32), ("b_off", ctypes.c_uint32)]
 
 
 class PrefillArgmaxParams(ctypes.Structure):
@@ -185,7 +196,7 @@ class AdvanceParams(ctypes.Structure):
 
 class InitNormalParams(ctypes.Structure):
     _fields_ = [("count", ctypes.c_uint64), ("seed", ctypes.c_uint64), ("std", ctypes.c_float),
-                ("f16", ctypes.c_uint32)]
+                ("dtype", ctypes.c_uint32)]
 
 
 @dataclass(frozen=True)
@@ -221,11 +232,13 @@ def _gemv_abis() -> dict[str, KernelAbi]:
 # shape being the weight type, the largest input width it takes and its rows a
 # block; the SiLU·mul epilogue (3) only on shapes of row pairs.
 STEP_GEMV_SHAPES = {"fk_step_gemv_f16_k2048_r1": False, "fk_step_gemv_f16_k2048_r2": True,
-                    "fk_step_gemv_f16_k8192_r1": False, "fk_step_gemv_f32_k256_r1": False,
+                    "fk_step_gemv_f16_k8192_r1": False, "fk_step_gemv_bf16_k2048_r1": False,
+                    "fk_step_gemv_bf16_k2048_r2": True, "fk_step_gemv_bf16_k8192_r1": False,
+                    "fk_step_gemv_f32_k256_r1": False,
                     "fk_step_gemv_f32_k256_r2": True, "fk_step_gemv_f32_k1024_r1": False,
                     "fk_step_gemv_f32_k1024_r2": True}
 STEP_GEMV_ENTRIES = tuple(f"{shape}_p{pro}_e{epi}" for shape, pairs in STEP_GEMV_SHAPES.items() for pro in range(5)
-                          for epi in ((0, 1, 2, 3, 4) if pairs else (0, 1, 2, 4)))
+                          for epi in ((0, 1, 2, 3, 4, 5) if pairs else (0, 1, 2, 4, 5)))
 STEP_GEMV_BUFFERS = ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
                      "res_token", "epi_out", "arg")
 
@@ -257,13 +270,14 @@ ABIS: dict[str, KernelAbi] = {
                                                                         "out"), PrefillAttendParams, 64 * g)
        for g in (1, 2, 4)},
     "fk_prefill_argmax": KernelAbi("fk_prefill_argmax", ("x", "out"), PrefillArgmaxParams, 256),
+    "fk_prefill_softcap": KernelAbi("fk_prefill_softcap", ("x", "y"), PrefillSoftcapParams, 256),
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
     "fk_step_attend": KernelAbi("fk_step_attend", ("q", "knew", "vnew", "kc", "vc", "position", "slot", "rope",
                                                    "partials"), StepAttendParams),
     "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams, 64),
     "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
-    "fk_step_silu_mul": KernelAbi("fk_step_silu_mul", ("a", "b", "y"), CountParams),
+    "fk_step_act_mul": KernelAbi("fk_step_act_mul", ("a", "b", "y"), ActMulParams),
     "fk_step_advance": KernelAbi("fk_step_advance", ("next_token", "token", "position"), AdvanceParams),
     "fk_init_normal": KernelAbi("fk_init_normal", ("dst",), InitNormalParams),
     "fk_noop": KernelAbi("fk_noop", (), NoopParams),
@@ -337,7 +351,7 @@ class Kernels:
     GEMM_TILE, GEMM_K, GEMM_LDS = 256, 64, 4 * 2 * 256 * 32 * 2
 
     def gemm(self, a: runtime.Buffer, bs: list, cs: list, m: int, k: int, rows: list, mode: str = "store",
-             r: runtime.Buffer | None = None, stream: runtime.Stream | None = None) -> None:
+             r: runtime.Buffer | None = None, stream: runtime.Stream | None = None, act: int = 0) -> None:
         """A [m, k] f16 in the tile layout (furykernel_amd.layout) times the
         weights bs[j] ([rows[j], k] f16, tiled: the anchors) into cs[j]
         ([m, rows[j]] f32 rows; "add": plus r, [m, rows[0]] f32, which may be
@@ -381,7 +395,9 @@ class Kernels:
         for j in range(3):
             bufs[f"b{j}"] = bs[j].ptr if j < len(bs) else 0
             bufs[f"c{j}"] = cs[j].ptr if j < len(cs) else 0
-        params = GemmParams(m, k, len(bs), (ctypes.c_uint32 * 4)(*first), (ctypes.c_uint32 * 3)(*ldc))
+        if act not in (ACT_SILU, ACT_GELU_TANH):
+            raise LaunchError(f"{entry}: activation {act}")
+        params = GemmParams(m, k, len(bs), (ctypes.c_uint32 * 4)(*first), (ctypes.c_uint32 * 3)(*ldc), act)
         self.launch(entry, groups, 256, bufs, params, stream, lds_bytes=self.GEMM_LDS)
 
     # The kernels around the prefill GEMM (fk_prefill.h).
@@ -485,9 +501,10 @@ class Kernels:
 # its entry and parameters.  A buffer outside this set may be unbound (passed
 # as address 0); one inside it never may.
 
-_GEMV_SUFFIX = re.compile(r"^(fk_step_gemv_(f16|f32)_k(\d+)_r(\d+))_p(\d)_e(\d)$")
+_GEMV_SUFFIX = re.compile(r"^(fk_step_gemv_(f16|bf16|f32)_k(\d+)_r(\d+))_p(\d)_e(\d)$")
 PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = range(5)
-EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX = range(5)
+EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = range(6)
+ACT_SILU, ACT_GELU_TANH = 0, 1
 
 
 def gemv_entry(entry: str) -> tuple[str, str, int, int, int, int]:
@@ -500,7 +517,7 @@ def gemv_entry(entry: str) -> tuple[str, str, int, int, int, int]:
     return m.group(1), m.group(2), int(m.group(3)), int(m.group(4)), int(m.group(5)), int(m.group(6))
 
 
-def gemv_reads(pro: int, epi: int, n_anchors: int, store_tile: bool) -> set[str]:
+def gemv_reads(pro: int, epi: int, n_anchors: int, store_tile: bool, arg_slots: int = 0) -> set[str]:
     """The buffers a GEMV step kernel of prologue `pro` and epilogue `epi`
     dereferences (fk_step_gemv.h): the gathers read the token unconditionally,
     the norms their gains, and so on."""
@@ -523,6 +540,10 @@ def gemv_reads(pro: int, epi: int, n_anchors: int, store_tile: bool) -> set[str]
         need.add("epi_out")
     elif epi == EPI_ARGMAX:
         need.add("arg")
+    elif epi == EPI_SOFTCAP:
+        need.add("epi_out")
+        if arg_slots:
+            need.add("arg")
     return need
 
 
@@ -531,7 +552,7 @@ def launch_reads(entry: str, params: dict) -> set[str]:
     abi = ABIS[entry]
     if entry.startswith("fk_step_gemv"):
         _, _, _, _, pro, epi = gemv_entry(entry)
-        return gemv_reads(pro, epi, params["n_anchors"], bool(params.get("store_tile", 0)))
+        return gemv_reads(pro, epi, params["n_anchors"], bool(params.get("store_tile", 0)), params.get("arg_slots", 0))
     if entry == "fk_step_attend":
         need = {"q", "kc", "vc", "position", "slot", "partials"}
         if params.get("store"):

@@ -21,8 +21,8 @@ import numpy as np
 
 from .program.check import CheckedProgram
 from .program.graph import (
-    BF16, CACHE_BF16, F16, F32, SILU, U32, Add, ArgMax, Attend, Gather, GeluMul, Input, KvStore, Linear, Ring, RmsNorm,
-    Rope, ROPE_HALVES, SCache, SInput, SRowInts, SWeight)
+    BF16, CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, Gather, GatedGelu, GeluMul, Input, KvStore,
+    Linear, Ring, RmsNorm, Rope, ROPE_HALVES, SCache, SInput, Softcap, SRowInts, SWeight)
 from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
 
 THREADS = 256
@@ -32,7 +32,9 @@ MAX_K = 8192
 
 # GEMV step prologue and epilogue modes (fk_step_gemv.h).
 PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = 0, 1, 2, 3, 4
-EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX = 0, 1, 2, 3, 4
+EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = 0, 1, 2, 3, 4, 5
+# Activations of an act·mul (the SiLU form this target adds, GELU-tanh the reference's).
+ACT = {SILU: 0, GELU_TANH: 1}
 
 
 class LoweringError(ValueError):
@@ -152,28 +154,33 @@ def _store_into_attend(st: Launch, at: Launch) -> Optional[Launch]:
 
 
 def _fuse_light(out: Lowered, compute_units: int) -> None:
-    """A light step of one stored SiLU·mul of the two anchors of the GEMV
-    step right before it becomes that step's epilogue: its wavefronts hold row
-    j of both anchors and store silu(gate_j) * up_j — the light kernel's
-    arithmetic.  A light step of the greedy token of the row the GEMV step
-    before it stores becomes that step's epilogue (each row's argmax key into
-    a 64-bit maximum) and a one-thread launch that turns the key into the
-    token and clears it for the next step."""
+    """A light step of one stored act·mul (SiLU or GELU-tanh) of the two
+    anchors of the GEMV step right before it becomes that step's epilogue: its
+    wavefronts hold row j of both anchors and store act(gate_j) * up_j — the
+    light kernel's arithmetic.  A light step of the greedy token of the row the
+    GEMV step before it stores (its tile, or the softcap its epilogue stores)
+    becomes part of that step's epilogue (each row's argmax key into a 64-bit
+    maximum) and a one-thread launch that turns the key into the token."""
     fused: list = []
     for launch in out.launches:
         prev = fused[-1] if fused else None
-        if prev is not None and prev.entry.startswith("fk_step_gemv") and prev.params["epi_mode"] == EPI_NONE:
+        if prev is not None and prev.entry.startswith("fk_step_gemv"):
             pp, pb = prev.params, prev.bind
-            if (launch.entry == "fk_step_silu_mul" and pp["n_anchors"] == 2 and pp["rows"][0] == pp["rows"][1]
+            epi = pp["epi_mode"]
+            if (epi == EPI_NONE and launch.entry == "fk_step_act_mul" and launch.params["b_off"] == 0
+                    and pp["n_anchors"] == 2 and pp["rows"][0] == pp["rows"][1]
                     and pb["y0"] == launch.bind["a"] and pb["y1"] == launch.bind["b"]):
                 pp["epi_mode"] = EPI_SILU_MUL
+                pp["act"] = launch.params["act"]
                 pb["epi_out"] = launch.bind["y"]
                 prev.step = f"{prev.step}+{launch.step}"
                 _shape_gemv(prev, compute_units)
                 continue
-            if (launch.entry == "fk_step_argmax" and pp["n_anchors"] == 1 and pb["y0"] == launch.bind["x"]
-                    and pp["store_tile"]):
-                pp["epi_mode"] = EPI_ARGMAX
+            keyed = (epi == EPI_NONE and pp["n_anchors"] == 1 and pp["store_tile"] and pb["y0"] == launch.bind.get("x")) \
+                or (epi == EPI_SOFTCAP and pb["epi_out"] == launch.bind.get("x"))
+            if launch.entry == "fk_step_argmax" and keyed:
+                if epi == EPI_NONE:
+                    pp["epi_mode"] = EPI_ARGMAX
                 prev.step = f"{prev.step}+{launch.step}"
                 _shape_gemv(prev, compute_units)
                 arg = out.buffer(f"argmax:{launch.bind['out'].split(':', 1)[1]}", "u64", prev.groups)
@@ -199,14 +206,14 @@ def _shape_gemv(launch: Launch, compute_units: int) -> None:
     k, wt = p["k"], launch.meta["wtype"]
     total = p["first_row"][p["n_anchors"]]
     pairs = p["epi_mode"] == EPI_SILU_MUL
-    if wt == F16:
+    if wt in (F16, BF16):
         if k <= 2048:
             r = 2 if pairs or total > 4096 else 1
-            entry, kmax = f"fk_step_gemv_f16_k2048_r{r}", 2048
+            entry, kmax = f"fk_step_gemv_{wt}_k2048_r{r}", 2048
         elif k <= MAX_K:
-            r, entry, kmax = 1, "fk_step_gemv_f16_k8192_r1", 8192
+            r, entry, kmax = 1, f"fk_step_gemv_{wt}_k8192_r1", 8192
         else:
-            raise LoweringError(f"{launch.step}: an input row of {k}; the f16 GEMV steps take up to {MAX_K}")
+            raise LoweringError(f"{launch.step}: an input row of {k}; the {wt} GEMV steps take up to {MAX_K}")
     elif wt == F32:
         r = 2 if pairs else 1
         if k <= 256:
@@ -273,9 +280,20 @@ class _StepLowering:
         if not isinstance(src.kind, SWeight):
             raise LoweringError(f"{src.name} is not a weight")
         t = src.kind.type
-        if t not in (F16, F32):
-            raise LoweringError(f"weight {src.name} of {t}: the GEMV steps take f16 and f32 weights")
+        if t not in (F16, BF16, F32):
+            raise LoweringError(f"weight {src.name} of {t}: the GEMV steps take f16, bf16 and f32 weights")
         return self.out.buffer(f"weight:{src.name}", t, int(np.prod(src.kind.dims))), t
+
+    def gains(self, s: int) -> str:
+        """An RMSNorm's gains as the f32 row the kernels read: an f32 weight as
+        it is, a bf16 or f16 one widened (exactly) into a buffer of its own."""
+        name, t = self.weight(s)
+        if t == F32:
+            return name
+        src = self.p.source(s)
+        wide = self.out.buffer(f"widen:{src.name}", "f32", int(np.prod(src.kind.dims)))
+        self.out.layouts[wide] = ("widen", (src.name,))
+        return wide
 
     def ints(self, s: int) -> str:
         src = self.p.source(s)
@@ -339,7 +357,8 @@ class _StepLowering:
         used: set = set()
         bind: dict = {k: None for k in ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token",
                                         "res", "res_table", "res_token", "epi_out", "arg")}
-        params: dict = {"eps": 0.0, "factor": 1.0, "gfactor": 1.0, "has_gamma": 0, "table_rows": 1, "arg_slots": 0}
+        params: dict = {"eps": 0.0, "factor": 1.0, "gfactor": 1.0, "has_gamma": 0, "table_rows": 1, "arg_slots": 0,
+                        "act": 0, "src2_off": 0, "cap": 0.0}
         wtypes = set()
         k = self.p.value(x).shape.width
         if k > MAX_K or k % 8:
@@ -381,10 +400,7 @@ class _StepLowering:
                 params["seg"] = self.p.value(op.x).shape.segment
                 if op.gamma is not None:
                     params["has_gamma"] = 1
-                    gname, gt = self.weight(op.gamma)
-                    if gt != F32:
-                        raise LoweringError(f"{step.name}: a gamma of {gt}; the kernels read f32 gammas")
-                    bind["gamma"] = gname
+                    bind["gamma"] = self.gains(op.gamma)
                 else:
                     # The kernel loads gains whatever the norm: a row of ones
                     # it never multiplies by.
@@ -405,11 +421,22 @@ class _StepLowering:
                 pro = PRO_GATHER
                 bind["table"], bind["token"], gtype = gather_of(x)
                 wtypes.add(gtype)
-            elif isinstance(op, GeluMul) and op.form == SILU:
+            elif isinstance(op, GeluMul) and op.form in ACT:
                 if not (self.stored_before(step, op.a) and self.stored_before(step, op.b)):
-                    raise LoweringError(f"{step.name}: a SiLU·mul of values not stored")
+                    raise LoweringError(f"{step.name}: an act·mul of values not stored")
                 pro = PRO_SILU_MUL
+                params["act"] = ACT[op.form]
                 bind["src"], bind["src2"] = self.value(op.a), self.value(op.b)
+            elif isinstance(op, GatedGelu) and op.form in ACT:
+                # act(first half) * second half of one stored row, whose one
+                # segment is the whole row (Eval.hs:356-362).
+                shape = self.p.value(op.x).shape
+                if shape.segment != shape.width or not self.stored_before(step, op.x):
+                    raise LoweringError(f"{step.name}: a gated activation in segments of {shape.segment} of a row "
+                                        f"of {shape.width}, or of a value not stored")
+                pro = PRO_SILU_MUL
+                params["act"], params["src2_off"] = ACT[op.form], shape.width // 2
+                bind["src"] = bind["src2"] = self.value(op.x)
             else:
                 raise LoweringError(f"{step.name}: no prologue computes {type(op).__name__}")
         params["pro_mode"] = pro
@@ -434,12 +461,20 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: weights of several types {wtypes}")
         wt = wtypes.pop()
 
-        # Epilogues: one residual add on a single anchor's tile.
+        # Epilogues: one residual add, or one softcap, on a single anchor's tile.
         epis = [self.p.node(w.node) for w in step.work if w.kind == EPILOGUE]
         epi, epi_value = EPI_NONE, None
-        if epis:
+        if epis and len(epis) == 1 and len(anchors) == 1 and isinstance(epis[0].op, Softcap):
+            if epis[0].op.x != anchors[0].outputs[0]:
+                raise LoweringError(f"{step.name}: a softcap off its anchor's tile")
+            cap = float(np.float32(epis[0].op.cap))
+            if not 0 < cap < math.inf:
+                raise LoweringError(f"{step.name}: a softcap of {epis[0].op.cap}")
+            epi, epi_value = EPI_SOFTCAP, epis[0].outputs[0]
+            params["cap"] = cap
+        elif epis:
             if len(epis) != 1 or len(anchors) != 1 or not isinstance(epis[0].op, Add):
-                raise LoweringError(f"{step.name}: epilogues other than one residual add on one anchor")
+                raise LoweringError(f"{step.name}: epilogues other than one residual add or one softcap on one anchor")
             op = epis[0].op
             tile = anchors[0].outputs[0]
             if tile not in (op.a, op.b):
@@ -625,10 +660,27 @@ class _StepLowering:
             n = self.p.value(op.x).shape.width
             return Launch(step.name, "fk_step_argmax", 1, 1024,
                           {"x": self.value(op.x), "out": self.value(node.outputs[0])}, {"n": n})
-        if isinstance(op, GeluMul) and op.form == SILU and self.stored_before(step, op.a) and \
+        if isinstance(op, GeluMul) and op.form in ACT and self.stored_before(step, op.a) and \
                 self.stored_before(step, op.b):
             n = self.p.value(op.a).shape.width
-            return Launch(step.name, "fk_step_silu_mul", -(-n // THREADS), THREADS,
+            return Launch(step.name, "fk_step_act_mul", -(-n // THREADS), THREADS,
                           {"a": self.value(op.a), "b": self.value(op.b), "y": self.value(node.outputs[0])},
-                          {"n": n})
+                          {"n": n, "act": ACT[op.form], "b_off": 0})
+        if isinstance(op, GatedGelu) and op.form in ACT and self.stored_before(step, op.x):
+            shape = self.p.value(op.x).shape
+            if shape.segment != shape.width:
+                raise LoweringError(f"{step.name}: a gated activation in segments of {shape.segment} of a row of "
+                                    f"{shape.width}")
+            n = shape.width // 2
+            x = self.value(op.x)
+            return Launch(step.name, "fk_step_act_mul", -(-n // THREADS), THREADS,
+                          {"a": x, "b": x, "y": self.value(node.outputs[0])},
+                          {"n": n, "act": ACT[op.form], "b_off": n})
+        if isinstance(op, Softcap) and self.stored_before(step, op.x):
+            n = self.p.value(op.x).shape.width
+            cap = float(np.float32(op.cap))
+            if not 0 < cap < math.inf:
+                raise LoweringError(f"{step.name}: a softcap of {op.cap}")
+            return Launch(step.name, "fk_prefill_softcap", max(1, -(-n // 256)), 256,
+                          {"x": self.value(op.x), "y": self.value(node.outputs[0])}, {"count": n, "cap": cap})
         raise LoweringError(f"{step.name}: no light kernel recomputes {type(op).__name__}")

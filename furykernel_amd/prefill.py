@@ -37,10 +37,11 @@ import numpy as np
 
 from .kernels import ATTEND_KEYS, NORM_PACK_HELD
 from .layout import SLAB, pack, pair
-from .lower import Launch, Lowered, LoweringError, rope_table
+from .lower import ACT, Launch, Lowered, LoweringError, rope_table
 from .program.check import CheckedProgram
 from .program.graph import (
-    CACHE_BF16, F16, F32, SILU, U32, Add, ArgMax, Attend, Gather, GeluMul, Input, KvStore, Linear, Ring, RmsNorm,
+    CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, Gather, GeluMul, Input, KvStore, Linear, Ring,
+    RmsNorm, Softcap,
     Rope, ROPE_HALVES, SCache, SInput, SRowInts, SWeight, op_values)
 from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
 
@@ -275,7 +276,7 @@ class _Prefill:
         if len(readers) != 1:
             return None
         node = next(iter(readers.values()))
-        if not (isinstance(node.op, GeluMul) and node.op.form == SILU and {node.op.a, node.op.b} == set(outs)):
+        if not (isinstance(node.op, GeluMul) and node.op.form in ACT and {node.op.a, node.op.b} == set(outs)):
             return None
         if any(o.value in outs for o in self.p.outputs):
             return None
@@ -312,7 +313,8 @@ class _Prefill:
             bind.update(b0=pname, c0=self.value_tiled(act))
             self.tiled_of[act] = bind["c0"]
             self.launch(step, "fk_gemm_f16_silu_mul", (m // SLAB) * (n // (SLAB // 2)), 256, bind,
-                        {"m": m, "k": k, "n_anchors": 1, "first_col": [0, n, n, n], "ldc": [n, 0, 0]}, GEMM_LDS)
+                        {"m": m, "k": k, "n_anchors": 1, "first_col": [0, n, n, n], "ldc": [n, 0, 0],
+                         "act": ACT[node.op.form]}, GEMM_LDS)
             return
 
         rows, first = [], [0]
@@ -326,9 +328,24 @@ class _Prefill:
         first += [first[-1]] * (4 - len(first))
         params = {"m": m, "k": k, "n_anchors": len(anchors), "first_col": first, "ldc": (rows + [0, 0, 0])[:3]}
         groups = (m // SLAB) * (sum(rows) // SLAB)
+        if len(epis) == 1 and len(anchors) == 1 and isinstance(epis[0].op, Softcap) and epis[0].op.x == outs[0]:
+            # The tile stored as rows, then the softcap over them into the
+            # capped value's rows.
+            cap = float(np.float32(epis[0].op.cap))
+            if not 0 < cap < float("inf"):
+                raise LoweringError(f"{step.name}: a softcap of {epis[0].op.cap}")
+            bind["c0"] = self.value_rows(outs[0])
+            self.rows_of[outs[0]] = bind["c0"]
+            self.launch(step, "fk_gemm_f16_store", groups, 256, bind, params, GEMM_LDS)
+            capped = epis[0].outputs[0]
+            count = self.rows * rows[0]
+            self.launch(step, "fk_prefill_softcap", min(max(1, count // 1024), 4096), 256,
+                        {"x": bind["c0"], "y": self.value_rows(capped)}, {"count": count, "cap": cap})
+            self.rows_of[capped] = self.value_rows(capped)
+            return
         if epis:
             if len(epis) != 1 or len(anchors) != 1 or not isinstance(epis[0].op, Add):
-                raise LoweringError(f"{step.name}: epilogues other than one residual add on one anchor")
+                raise LoweringError(f"{step.name}: epilogues other than one residual add or softcap on one anchor")
             op = epis[0].op
             tile = outs[0]
             if tile not in (op.a, op.b):

@@ -15,7 +15,7 @@ from dataclasses import dataclass
 from typing import Optional
 
 from .build import ProgramBuilder, program
-from .graph import CACHE_F16, F16, F32, SILU, AttnSpec, Program, Ring, RopeSpec, whole_row
+from .graph import BF16, CACHE_F16, F16, F32, GELU_TANH, SILU, AttnSpec, Program, Ring, RopeSpec, whole_row
 
 
 @dataclass(frozen=True)
@@ -33,6 +33,7 @@ class DecoderDims:
     weight_type: str = F16
     cache_elem: str = CACHE_F16
     slots: int = 1        # sequences the caches hold
+    act: str = SILU       # the gated MLP's activation: SILU or GELU_TANH
 
     @property
     def q_width(self) -> int:
@@ -57,6 +58,10 @@ TINY = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=4, head_dim=16, ffn=2
 # 256 positions, so that attention at a position past 127 runs in two splits.
 TINY_GQA = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=2, head_dim=16, ffn=256, vocab=256, context=256,
                        weight_type=F32)
+# The tiny decode with bf16 weights (the reference builder's type) and a
+# GELU-tanh gated MLP (the reference's activation).
+TINY_GELU_BF16 = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=2, head_dim=16, ffn=256, vocab=256, context=32,
+                             weight_type=BF16, act=GELU_TANH)
 ONE_B = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000, context=4096)
 # The 1B prefill: four sequences of 2048 rows into a ring of 4096 positions.
 ONE_B_PREFILL = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000,
@@ -119,7 +124,7 @@ def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
             m = b.rmsnorm(p + "mlp_in", dims.eps, g_mlp, 1.0, x1)
             gate = b.linear(p + "gate", wg, 0, m)
             up = b.linear(p + "up", wu, 0, m)
-            act = b.gelu_mul(p + "act", gate, up, SILU)
+            act = b.gelu_mul(p + "act", gate, up, dims.act)
             down = b.linear(p + "down", wd, 0, act)
             x = b.add(p + "x2", x1, down)
         g_final = b.weight("final_norm", [dims.d_model], F32)

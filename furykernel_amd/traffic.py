@@ -21,8 +21,8 @@ Counted per launch, from its parameters and the buffer types it binds:
 
 from __future__ import annotations
 
-from .lower import EPI_ADD_GATHER, EPI_ADD_STORED, EPI_ARGMAX, EPI_SILU_MUL, PRO_GATHER, PRO_GATHER_RMSNORM, \
-    PRO_SILU_MUL, Launch, Lowered
+from .lower import EPI_ADD_GATHER, EPI_ADD_STORED, EPI_ARGMAX, EPI_SILU_MUL, EPI_SOFTCAP, PRO_GATHER, \
+    PRO_GATHER_RMSNORM, PRO_SILU_MUL, Launch, Lowered
 
 _ELT = {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2, "u64": 8}
 
@@ -60,6 +60,8 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
             total += rows[0] * 4
         elif p["epi_mode"] == EPI_ARGMAX:
             total += 8 * launch.groups
+        elif p["epi_mode"] == EPI_SOFTCAP:
+            total += rows[0] * 4 + (8 * launch.groups if p.get("arg_slots") else 0)
         return total
     if e == "fk_step_token":
         return 8 * p["slots"] + 4
@@ -87,8 +89,10 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
         return p["heads"] * p["splits"] * (d + 2) * 4 + p["heads"] * d * 4
     if e == "fk_step_argmax":
         return p["n"] * 4 + 4
-    if e == "fk_step_silu_mul":
+    if e == "fk_step_act_mul":
         return p["n"] * 4 * 3
+    if e == "fk_prefill_softcap":
+        return p["count"] * 4 * 2
     raise ValueError(f"no byte count for {e}")
 
 

@@ -41,7 +41,7 @@ enum {
   FK_PRO_RMSNORM = 1,        /* x = rmsnorm(src) * gamma * factor */
   FK_PRO_GATHER = 2,         /* x = table[token] * gfactor */
   FK_PRO_GATHER_RMSNORM = 3, /* x = rmsnorm(table[token] * gfactor) * gamma * factor */
-  FK_PRO_SILU_MUL = 4        /* x = silu(src) * src2 */
+  FK_PRO_SILU_MUL = 4        /* x = act(src) * src2[src2_off ..] (act: FK_ACT_*, SiLU or GELU-tanh) */
 };
 
 /* Epilogue modes, on the anchors' tile (the entry's `_e<mode>` suffix). */
@@ -49,8 +49,17 @@ enum {
   FK_EPI_NONE = 0,
   FK_EPI_ADD_STORED = 1, /* out = res + tile */
   FK_EPI_ADD_GATHER = 2, /* out = table[token] * gfactor + tile */
-  FK_EPI_SILU_MUL = 3,   /* out = silu(tile of anchor 0) * tile of anchor 1 */
-  FK_EPI_ARGMAX = 4      /* arg = max(arg, argmax key of each row) (the greedy token, folded in) */
+  FK_EPI_SILU_MUL = 3,   /* out = act(tile of anchor 0) * tile of anchor 1 (act: FK_ACT_*) */
+  FK_EPI_ARGMAX = 4,     /* arg = max(arg, argmax key of each row) (the greedy token, folded in) */
+  FK_EPI_SOFTCAP = 5     /* out = cap tanh(tile / cap); with arg_slots, also the argmax keys of out */
+};
+
+/* The activation of an act·mul (src/FuryKernel/Program/Graph.hs:287-291): the
+ * GEMV step's act·mul prologue and epilogue, the light act·mul step, the
+ * prefill GEMM's act·mul epilogue. */
+enum {
+  FK_ACT_SILU = 0,     /* a / (1 + e^-a) */
+  FK_ACT_GELU_TANH = 1 /* 0.5 a (1 + tanh(sqrt(2/pi) (a + 0.044715 a^3))) */
 };
 
 typedef struct fk_step_gemv_params {
@@ -69,6 +78,9 @@ typedef struct fk_step_gemv_params {
   uint32_t table_rows;   /* the gathered table's rows: a token past them reads its last */
   uint32_t blocks;       /* row blocks */
   uint32_t arg_slots;    /* the argmax epilogue's slots (one a threadgroup); a threadgroup past them stores none */
+  uint32_t act;          /* the act·mul prologue's and epilogue's activation (FK_ACT_*) */
+  uint32_t src2_off;     /* elements into src2 where the act·mul prologue's second row starts */
+  float cap;             /* the softcap epilogue's cap (positive, finite) */
 } fk_step_gemv_params;
 
 typedef struct fk_step_token_params {
@@ -120,9 +132,11 @@ typedef struct fk_step_argmax_params {
   uint32_t n;
 } fk_step_argmax_params;
 
-typedef struct fk_step_silu_mul_params {
+typedef struct fk_step_act_mul_params {
   uint32_t n;
-} fk_step_silu_mul_params;
+  uint32_t act;   /* FK_ACT_* */
+  uint32_t b_off; /* elements into b where the second row starts (a gated activation's second half) */
+} fk_step_act_mul_params;
 
 typedef struct fk_step_advance_params {
   uint32_t context; /* positions wrap below this */
@@ -133,7 +147,7 @@ typedef struct fk_init_normal_params {
   uint64_t count;
   uint64_t seed;
   float std;
-  uint32_t f16; /* store binary16 (else binary32) */
+  uint32_t dtype; /* what is stored: 0 binary32, 1 binary16, 2 bfloat16 (each the value rounded once) */
 } fk_init_normal_params;
 
 /* Standalone kernels. ----------------------------------------------------- */
@@ -186,6 +200,7 @@ typedef struct fk_gemm_params {
   uint32_t n_anchors;    /* 1 to 3 weights (SiLU·mul: 1, the pair) */
   uint32_t first_col[4]; /* anchor j's columns of C are [first_col[j], first_col[j + 1]), each a multiple of 256 */
   uint32_t ldc[3];       /* row stride of anchor j's output (its columns; SiLU·mul: N, gate's rows) */
+  uint32_t act;          /* the act·mul epilogue's activation (FK_ACT_*) */
 } fk_gemm_params;
 
 typedef struct fk_gemm_rope_params {
@@ -239,6 +254,11 @@ typedef struct fk_prefill_attend_params {
   uint32_t cache_bf16;
   float scale;
 } fk_prefill_attend_params;
+
+typedef struct fk_prefill_softcap_params {
+  uint32_t count; /* elements */
+  float cap;
+} fk_prefill_softcap_params;
 
 typedef struct fk_prefill_argmax_params {
   uint32_t rows;

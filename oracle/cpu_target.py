@@ -20,8 +20,8 @@ from . import fkref
 
 NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16,
       "u64": np.uint64}
-EPI_SILU_MUL, EPI_ARGMAX = 3, 4
-TYPE = {"f16": fkref.F16, "f32": fkref.F32}
+EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = 3, 4, 5
+TYPE = {"f16": fkref.F16, "bf16": fkref.BF16, "f32": fkref.F32}
 
 
 class CpuTarget:
@@ -51,10 +51,10 @@ class CpuTarget:
         b, p = launch.bind, launch.params
         e = launch.entry
         if e.startswith("fk_step_gemv"):
-            wt = "f16" if "_f16_" in e else "f32"
+            wt = e.split("_")[3]
             n = p["n_anchors"]
             epi = p["epi_mode"]
-            folded = epi in (EPI_SILU_MUL, EPI_ARGMAX)
+            folded = epi in (EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP)
             # A folded epilogue reads the anchors' tiles: kept here whether or not
             # the step stores them.
             tiles = [self.buffers[b[f"y{j}"]] if b[f"y{j}"] else np.zeros(p["rows"][j], np.float32)
@@ -69,15 +69,24 @@ class CpuTarget:
                                    self._p(b["table"] or b["res_table"]), tok, p["table_rows"], p["seg"], p["eps"],
                                    p["factor"], p["gfactor"], 0 if folded else epi, self._p(b["res"]),
                                    self._p(b["res_table"]), rtok, None if folded else self._p(b["epi_out"]),
-                                   launch.threads, self.width)
+                                   launch.threads, self.width, p.get("act", 0), p.get("src2_off", 0))
             if not st and epi == EPI_SILU_MUL:
-                st = L.fkref_silu_mul(tiles[0].ctypes.data, tiles[1].ctypes.data, self._p(b["epi_out"]), p["rows"][0])
+                st = L.fkref_act_mul(tiles[0].ctypes.data, tiles[1].ctypes.data, self._p(b["epi_out"]), p["rows"][0],
+                                     p.get("act", 0))
+            keyed = None
+            if not st and epi == EPI_SOFTCAP:
+                out = self.buffers[b["epi_out"]]
+                for i, v in enumerate(tiles[0][:p["rows"][0]]):
+                    out[i] = L.fkref_softcap(float(v), p["cap"])
+                keyed = out if p.get("arg_slots", 0) else None
             if not st and epi == EPI_ARGMAX:
+                keyed = tiles[0]
+            if keyed is not None:
                 # Each threadgroup's largest key into its slot: row blocks of
                 # `rows_per_block` rows, block b taken by wavefront b mod (all
                 # wavefronts), of 64 threads each.
                 n_rows = p["rows"][0]
-                keys = np.array([L.fkref_argmax_key(float(v), i) for i, v in enumerate(tiles[0][:n_rows])],
+                keys = np.array([L.fkref_argmax_key(float(v), i) for i, v in enumerate(keyed[:n_rows])],
                                 np.uint64)
                 rows_per_block = -(-n_rows // p["blocks"])
                 waves = launch.threads // 64
@@ -120,8 +129,10 @@ class CpuTarget:
         elif e == "fk_step_argmax":
             self.buffers[b["out"]][0] = L.fkref_argmax(self._p(b["x"]), p["n"])
             st = 0
-        elif e == "fk_step_silu_mul":
-            st = L.fkref_silu_mul(self._p(b["a"]), self._p(b["b"]), self._p(b["y"]), p["n"])
+        elif e == "fk_step_act_mul":
+            off = p.get("b_off", 0)
+            bb = self.buffers[b["b"]][off:]
+            st = L.fkref_act_mul(self._p(b["a"]), bb.ctypes.data, self._p(b["y"]), p["n"], p.get("act", 0))
         else:
             raise ValueError(f"the CPU target has no kernel {e}")
         if st:

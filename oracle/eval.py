@@ -353,6 +353,17 @@ def evaluate_fast(checked: CheckedProgram, b: Bindings) -> Evaluation:
             else:
                 ga = 0.5 * a * (1 + np.tanh(math.sqrt(2 / math.pi) * (a + 0.044715 * a * a * a)))
             env[out] = ga * env[op.b]
+        elif isinstance(op, GatedGelu):
+            seg = values[op.x].shape.segment
+            x = env[op.x].reshape(m, -1, seg)
+            a, c = x[..., :seg // 2], x[..., seg // 2:]
+            if op.form == SILU:
+                ga = a / (1 + np.exp(-a))
+            else:
+                ga = 0.5 * a * (1 + np.tanh(math.sqrt(2 / math.pi) * (a + 0.044715 * a * a * a)))
+            env[out] = (ga * c).reshape(m, -1)
+        elif isinstance(op, Softcap):
+            env[out] = op.cap * np.tanh(env[op.x] / op.cap)
         elif isinstance(op, Rope):
             spec = op.spec
             d = values[op.x].shape.segment

@@ -152,6 +152,21 @@ float fkref_max(float x, float y) {
 float fkref_rsqrt(float x) { return (float)(1.0 / sqrt((double)x)); }
 
 float fkref_exp(float x) { return (float)exp((double)x); }
+float fkref_tanh(float x) { return (float)tanh((double)x); }
+
+/* GELU in its tanh form (src/FuryKernel/Program/Eval.hs:658-659) in binary32,
+ * left to right as the formula reads, its constants rounded once and tanh
+ * binary64's rounded once: (0.5 a) (1 + tanh(c0 (a + ((c1 a) a) a))). */
+float fkref_gelu_tanh(float a) {
+  const float c0 = 0.7978845608028654f; /* sqrt(2 / pi) */
+  const float c1 = 0.044715f;
+  float cube = ((c1 * a) * a) * a;
+  float t = fkref_tanh(c0 * (a + cube));
+  return (0.5f * a) * (1.0f + t);
+}
+
+/* A softcap (Eval.hs:384-390): cap tanh(x / cap). */
+float fkref_softcap(float x, float cap) { return cap * fkref_tanh(x / cap); }
 
 /* ------------------------------------------------------------------------ */
 /* Reductions: Interp.hs:733-745, Reduce.hs                                  */
@@ -354,6 +369,16 @@ static float silu_mul_1(float a, float b) {
   return (a / d) * b;
 }
 
+static float act_mul_1(float a, float b, int act) {
+  return act == FKREF_ACT_GELU_TANH ? fkref_gelu_tanh(a) * b : silu_mul_1(a, b);
+}
+
+int fkref_act_mul(const float *a, const float *b, float *y, int n, int act) {
+  if (act != FKREF_ACT_SILU && act != FKREF_ACT_GELU_TANH) return -1;
+  for (int i = 0; i < n; i++) y[i] = act_mul_1(a[i], b[i], act);
+  return 0;
+}
+
 int fkref_silu_mul(const float *a, const float *b, float *y, int n) {
   for (int i = 0; i < n; i++) y[i] = silu_mul_1(a[i], b[i]);
   return 0;
@@ -373,7 +398,7 @@ int fkref_step_gemv(const void *const *w, int wtype, float *const *y, const int 
                     int pro_mode, const float *src, const float *src2, const float *gamma, const void *table,
                     uint32_t token, int table_rows, int seg, float eps, float factor, float gfactor, int epi_mode,
                     const float *res, const void *res_table, uint32_t res_token, float *epi_out, int threads,
-                    int width) {
+                    int width, int act, int src2_off) {
   if (n_anchors < 1 || n_anchors > 3 || k <= 0) return -1;
   float *x = (float *)malloc(sizeof(float) * (size_t)k);
   if (!x) return -2;
@@ -382,7 +407,7 @@ int fkref_step_gemv(const void *const *w, int wtype, float *const *y, const int 
     switch (pro_mode) {
       case FKREF_PRO_GATHER:
       case FKREF_PRO_GATHER_RMSNORM: x[i] = element(table, wtype, (size_t)tok * k + i) * gfactor; break;
-      case FKREF_PRO_SILU_MUL: x[i] = silu_mul_1(src[i], src2[i]); break;
+      case FKREF_PRO_SILU_MUL: x[i] = act_mul_1(src[i], src2[src2_off + i], act); break;
       default: x[i] = src[i]; break;
     }
   }

@@ -95,7 +95,7 @@ int fkref_step_gemv(const void *const *w, int wtype, float *const *y, const int 
                     int pro_mode, const float *src, const float *src2, const float *gamma, const void *table,
                     uint32_t token, int table_rows, int seg, float eps, float factor, float gfactor, int epi_mode,
                     const float *res, const void *res_table, uint32_t res_token, float *epi_out, int threads,
-                    int width);
+                    int width, int act, int src2_off);
 
 /* RoPE (NeoX halves) of element j of a head of width d turned by `position`:
  * freq = theta^(-2i/d) and cos/sin in binary64 rounded once, the angle the
@@ -130,6 +130,12 @@ uint64_t fkref_argmax_keyed(const float *x, int n);
 
 /* SiLU(a) * b elementwise: a / (1 + exp(-a)) * b, exp binary64's rounded once. */
 int fkref_silu_mul(const float *a, const float *b, float *y, int n);
+/* The activations of an act·mul (FKREF_ACT_SILU, FKREF_ACT_GELU_TANH). */
+enum { FKREF_ACT_SILU = 0, FKREF_ACT_GELU_TANH = 1 };
+float fkref_tanh(float x);
+float fkref_gelu_tanh(float a);
+float fkref_softcap(float x, float cap);
+int fkref_act_mul(const float *a, const float *b, float *y, int n, int act);
 
 #ifdef __cplusplus
 }

@@ -50,7 +50,11 @@ def lib() -> ctypes.CDLL:
             "fkref_softmax": (_i, [_vp, _vp, _i, _i, _i, _i, _i]),
             "fkref_step_gemv": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, ctypes.c_uint32, _i, _i,
                                      ctypes.c_float, ctypes.c_float, ctypes.c_float, _i, _vp, _vp, ctypes.c_uint32,
-                                     _vp, _i, _i]),
+                                     _vp, _i, _i, _i, _i]),
+            "fkref_tanh": (ctypes.c_float, [ctypes.c_float]),
+            "fkref_gelu_tanh": (ctypes.c_float, [ctypes.c_float]),
+            "fkref_softcap": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+            "fkref_act_mul": (_i, [_vp, _vp, _vp, _i, _i]),
             "fkref_rope_elem": (ctypes.c_float, [_vp, _i, _i, _i, ctypes.c_uint32, ctypes.c_float]),
             "fkref_step_store": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
                                       ctypes.c_uint32, ctypes.c_uint32, _i]),

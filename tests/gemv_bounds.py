@@ -13,7 +13,7 @@ import numpy as np
 WAVE = 64
 THREADS = 512
 PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = range(5)
-EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX = range(5)
+EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = range(6)
 ELT = {"f32": 4, "f16": 2, "bf16": 2, "u32": 4, "u16": 2, "u64": 8}
 
 
@@ -21,7 +21,7 @@ def shape_of(entry: str) -> tuple[int, int, int, int]:
     """(weight bytes, pack elements P, rows a block R, packs a lane KPL)."""
     parts = entry.split("_")  # fk step gemv <wt> k<K> r<R> p<> e<>
     wt, kmax, r = parts[3], int(parts[4][1:]), int(parts[5][1:])
-    eb = 2 if wt == "f16" else 4
+    eb = 4 if wt == "f32" else 2
     p = 16 // eb
     return eb, p, r, kmax // (WAVE * p)
 
@@ -98,7 +98,7 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
     else:
         need("src", 4 * j, "the stored row", 4)
     if pro == PRO_SILU_MUL:
-        need("src2", 4 * j, "the second row", 4)
+        need("src2", prm.get("src2_off", 0) + 4 * j, "the second row", 4)
     if norm:
         need("gamma", 4 * j, "the gains", 4)
     # LDS writes: xt_at(j) for j < max(packs4, XT) within t + 512 m.
@@ -151,6 +151,8 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
                         need("res", np.minimum(rl, n - 1), "the residual")
                 if epi == EPI_SILU_MUL and an == 0:
                     need("epi_out", rl, "the SiLU·mul row")
+                if epi == EPI_SOFTCAP:
+                    need("epi_out", rl, "the softcap row")
             # The residual of every block below `blocks` is loaded (its row
             # clamped into the anchor), live or not.
             ran = row[sel][b[sel] < blocks]
@@ -158,7 +160,7 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
                 need("res", np.minimum(ran, n - 1), "the residual (clamped)")
             if ran.size and epi == EPI_ADD_GATHER:
                 need("res_table", (prm["table_rows"] - 1) * n + np.minimum(ran, n - 1), "the gathered residual")
-    if epi == EPI_ARGMAX:
+    if epi == EPI_ARGMAX or (epi == EPI_SOFTCAP and prm.get("arg_slots", 0)):
         slots = prm["arg_slots"]
         if slots > elems("arg"):
             raise Bad(f"{launch.entry}: {slots} argmax slots in a buffer of {elems('arg')}")
