@@ -58,7 +58,8 @@ std::vector<fk_abi_param> gemv_step_params() {
           FK_P(S, factor, "f32"),      FK_P(S, gfactor, "f32"),       FK_P(S, has_gamma, "u32"),
           FK_P(S, epi_mode, "u32"),    FK_P(S, store_tile, "u32"),    FK_P(S, table_rows, "u32"),
           FK_P(S, blocks, "u32"),      FK_P(S, arg_slots, "u32"),      FK_P(S, act, "u32"),
-          FK_P(S, src2_off, "u32"),    FK_P(S, cap, "f32")};
+          FK_P(S, src2_off, "u32"),    FK_P(S, cap, "f32"),            FK_P(S, splits, "u32"),
+          FK_P(S, head_dim, "u32")};
 }
 
 std::vector<fk_abi_param> gemm_params() {
@@ -132,7 +133,7 @@ std::vector<Entry> build() {
         buf("table", "read", wt),     buf("token", "read", "u32"),   buf("res", "read", "f32"),
         buf("res_table", "read", wt), buf("res_token", "read", "u32"), buf("epi_out", "write", "f32"),
         buf("arg", "read_write", "u64")};
-    for (int pro = 0; pro < 5; pro++)
+    for (int pro = 0; pro < 6; pro++)
       for (int epi = 0; epi < 6; epi++) {
         if (epi == FK_EPI_SILU_MUL && !s.pairs) continue;
         add(std::string(s.name) + "_p" + std::to_string(pro) + "_e" + std::to_string(epi), 512, b,
@@ -160,6 +161,18 @@ std::vector<Entry> build() {
   {
     using S = fk_step_attend_params;
     add("fk_step_attend", 0,
+        {buf("q", "read", "f32"), buf("knew", "read", "f32"), buf("vnew", "read", "f32"),
+         buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16"), buf("position", "read", "u32"),
+         buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("partials", "write", "f32")},
+        {FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"),
+         FK_P(S, slots, "u32"), FK_P(S, splits, "u32"), FK_P(S, split, "u32"), FK_P(S, rope, "u32"),
+         FK_P(S, rotated, "u32"), FK_P(S, rope_rows, "u32"), FK_P(S, scale, "f32"), FK_P(S, window, "u32"),
+         FK_P(S, cache_bf16, "u32"), FK_P(S, store, "u32"), FK_P(S, krope, "u32")},
+        sizeof(S));
+  }
+  {
+    using S = fk_step_attend_params;
+    add("fk_step_attend_wide", 0,
         {buf("q", "read", "f32"), buf("knew", "read", "f32"), buf("vnew", "read", "f32"),
          buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16"), buf("position", "read", "u32"),
          buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("partials", "write", "f32")},
@@ -411,6 +424,10 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
     if (pro == FK_PRO_GATHER || pro == FK_PRO_GATHER_RMSNORM) {
       need.push_back({"table", (uint64_t)p.table_rows * p.k * wb});
       need.push_back({"token", 4});
+    } else if (pro == FK_PRO_COMBINE) {
+      if (p.splits < 1 || p.splits > 8 || p.head_dim == 0 || p.head_dim % 4 || p.k % p.head_dim)
+        return bad(err, cap, FK_ERR_ARG, "%s: a combine of %u splits of heads of %u", entry, p.splits, p.head_dim);
+      need.push_back({"src", (uint64_t)(p.k / p.head_dim) * p.splits * (p.head_dim + 2) * 4});
     } else {
       need.push_back({"src", k4});
     }
@@ -431,11 +448,18 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({"epi_out", (uint64_t)p.rows[0] * 4});
       if (p.arg_slots) need.push_back({"arg", (uint64_t)p.arg_slots * 8});
     }
-  } else if (std::strcmp(entry, "fk_step_attend") == 0) {
+  } else if (std::strcmp(entry, "fk_step_attend") == 0 || std::strcmp(entry, "fk_step_attend_wide") == 0) {
     fk_step_attend_params p;
     std::memcpy(&p, params, sizeof p);
+    const bool wide = entry[14] == '_';
+    // Wide splits: 64 positions a wavefront, up to 8 wavefronts, the LDS of
+    // fk_attention.h's wide_lds_floats.
+    const bool split_ok = wide ? (p.split % 64 == 0 && p.split == threads && threads >= 64 && threads <= 512 &&
+                                  (p.head_dim == 16 || p.head_dim == 32 || p.head_dim == 64) &&
+                                  (uint64_t)lds_bytes >= 4ull * (584 + (threads / 64) * (32 * 68 + 2 * 512 + 24)))
+                               : (p.split == 64 || p.split == 128);
     if (p.kv_heads == 0 || p.heads % p.kv_heads || p.head_dim == 0 || p.head_dim > 64 || p.head_dim % 8 ||
-        (p.split != 64 && p.split != 128) || p.heads / p.kv_heads > 8 || groups != p.kv_heads * p.splits)
+        !split_ok || p.heads / p.kv_heads > 8 || groups != p.kv_heads * p.splits)
       return bad(err, cap, FK_ERR_ARG, "%s: %u heads over %u, width %u, splits of %u, %u groups for %u splits", entry,
                  p.heads, p.kv_heads, p.head_dim, p.split, groups, p.splits);
     const uint64_t cache = (uint64_t)p.slots * p.kv_heads * p.length * p.head_dim * 2;

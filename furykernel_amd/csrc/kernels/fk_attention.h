@@ -469,3 +469,360 @@ __device__ __forceinline__ void step_combine(const float *__restrict__ partials,
 }
 }  // namespace fk
 
+
+// Wide splits ---------------------------------------------------------------
+//
+// The attention of one kv head's split of S = 64 W positions by W wavefronts
+// of 64 positions each (W = blockDim / 64, up to 8), for splits few enough
+// that the consumer of the partials (the combine, or the next GEMV step's
+// prologue) reads them all cheaply.  Threadgroup (kv head g, split t); the
+// partials' layout is the narrow kernel's.
+//
+// Lane l of wavefront w holds position r = t S + 64 w + l, its whole key and
+// value rows in registers.  For query head h of the group:
+//   score = (fma chain from +0 over the dimensions in order, q_i k_i) * scale
+//           (-inf for a position off the split);
+//   m_w   = the wave's maximumNumber of the scores (exact);
+//   p     = exp(score - m_w) binary64's rounded once (0 if m_w is -inf);
+//   l_w   = the pairwise sum of p over the 64 positions in order
+//           ((p0 + p1) + (p2 + p3)) + ... (the wave_sum tree);
+//   acc_w = for each dimension i, the fma chain from +0 of p_r v_r[i] over
+//           the 64 positions in order.
+// Then the threadgroup's: M the maximumNumber of the waves' m_w (exact);
+// e_w = exp(m_w - M) binary64's rounded once (0 for a wave with no
+// positions); L = sum over w in order from +0 of l_w e_w; A[i] = sum over w in
+// order from +0 of acc_w[i] e_w (products rounded, then added).  A split
+// with no positions stores M = -inf, L = 0, A = 0.
+//
+// The new key and value rows (if asked) are made by threads j < d, element j
+// each, as the narrow kernel makes them, and the lane holding the position
+// takes them from LDS.  Values of positions off the split are zeros in LDS
+// (their weights are zero), so a cache's other contents never reach the sums.
+
+#define FK_WIDE_MAX_WAVES 8
+#define FK_WIDE_RUN 64
+#define FK_WIDE_VT 68  // a transposed value row in LDS: 64 positions and 4 of padding
+
+namespace fk {
+
+// LDS of the wide attention, in floats: the queries [8][64], the new rows
+// (64 halves each), the heads' maxima [8], then per wavefront the values
+// transposed [32 pairs][68], the weights [8][64], the sums [8][64], the
+// maxima and weight sums [8][2] and the waves' factors [8].
+constexpr uint32_t WIDE_WAVE_FLOATS = 32 * FK_WIDE_VT + 8 * 64 + 8 * 64 + 16 + 8;
+__host__ __device__ constexpr uint32_t wide_lds_floats(uint32_t waves) {
+  return 512 + 64 + 8 + waves * WIDE_WAVE_FLOATS;
+}
+
+// R maxima at once, wave_max's steps interleaved.
+template <int R>
+__device__ __forceinline__ void wave_maxes(float (&x)[R]) {
+  int v[R];
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = max_key(x[q]);
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = max(v[q], dpp_i<0xB1>(v[q]));
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = max(v[q], dpp_i<0x4E>(v[q]));
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = max(v[q], dpp_i<0x141>(v[q]));
+#pragma unroll
+  for (int q = 0; q < R; q++) v[q] = max(v[q], dpp_i<0x140>(v[q]));
+#pragma unroll
+  for (int q = 0; q < R; q++)
+    x[q] = from_max_key(max(max(__builtin_amdgcn_readlane(v[q], 0), __builtin_amdgcn_readlane(v[q], 16)),
+                            max(__builtin_amdgcn_readlane(v[q], 32), __builtin_amdgcn_readlane(v[q], 48))));
+}
+
+// One wavefront's 64 positions for the group's first R heads (R >= group):
+// scores, maxima, weights and weight sums; the weights into et[h][lane].
+template <int R>
+__device__ __forceinline__ void wide_weights(const float *qs, const float (&kf)[64], uint32_t d, uint32_t group,
+                                             bool live, float scale, float *et, float (&m)[R], float (&l)[R]) {
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+#pragma unroll
+  for (int h = 0; h < R; h++) {
+    float c = 0.0f;
+    if ((uint32_t)h < group) {
+      const float4 *q4 = reinterpret_cast<const float4 *>(qs + h * d);
+#pragma unroll
+      for (int i4 = 0; i4 < 16; i4++) {
+        if ((uint32_t)i4 < d / 4) {
+          const float4 qv = q4[i4];
+          c = __builtin_fmaf(qv.x, kf[4 * i4], c);
+          c = __builtin_fmaf(qv.y, kf[4 * i4 + 1], c);
+          c = __builtin_fmaf(qv.z, kf[4 * i4 + 2], c);
+          c = __builtin_fmaf(qv.w, kf[4 * i4 + 3], c);
+        }
+      }
+    }
+    m[h] = live && (uint32_t)h < group ? c * scale : -__builtin_inff();
+  }
+  float sc[R];
+#pragma unroll
+  for (int h = 0; h < R; h++) sc[h] = m[h];
+  wave_maxes<R>(m);
+#pragma unroll
+  for (int h = 0; h < R; h++) {
+    l[h] = m[h] == -__builtin_inff() ? 0.0f : exp_once(sc[h] - m[h]);
+    if ((uint32_t)h < group) et[h * 64 + lane] = l[h];
+  }
+  wave_sums<R>(l);
+}
+
+template <int CB>
+__device__ __forceinline__ void attend_wide(const float *__restrict__ q, const float *__restrict__ knew,
+                                            const float *__restrict__ vnew, uint16_t *__restrict__ kc,
+                                            uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
+                                            const uint32_t *__restrict__ slot, const float *__restrict__ rope,
+                                            float *__restrict__ partials, const fk_step_attend_params &p) {
+  extern __shared__ float lds[];
+  const uint32_t W = blockDim.x / FK_WAVE;
+  float *qs = lds;                                                  // [group][d]
+  uint16_t *kn = reinterpret_cast<uint16_t *>(lds + 512);          // [d]
+  uint16_t *vn = kn + 64;                                           // [d]
+  float *mm = lds + 512 + 64;                                       // [group]
+  float *waves = lds + 512 + 64 + 8;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (FK_WAVE - 1);
+  const uint32_t wave = tid / FK_WAVE;
+  float *wv = waves + (size_t)wave * WIDE_WAVE_FLOATS;
+  uint32_t *vt = reinterpret_cast<uint32_t *>(wv);                  // [pair][FK_WIDE_VT]
+  float *et = wv + 32 * FK_WIDE_VT;                                 // [h][64]
+
+  const uint32_t g = blockIdx.x / p.splits;
+  const uint32_t t = blockIdx.x % p.splits;
+  const uint32_t group = p.heads / p.kv_heads;
+  const uint32_t d = p.head_dim;
+  const uint32_t half = d / 2;
+  const uint32_t S = p.split;
+  const bool bf16 = CB >= 0 ? CB != 0 : p.cache_bf16 != 0;
+  const uint32_t pos = position[0];
+  const uint32_t sraw = slot[0];
+  const uint32_t s = sraw < p.slots ? sraw : 0;
+  const uint32_t first = (p.window && pos + 1 > p.window) ? pos + 1 - p.window : 0;
+  const uint32_t lo = max(first, t * S);
+  const uint32_t hi = min(pos + 1, (t + 1) * S);
+  const bool stores = p.store && sraw < p.slots && lo <= pos && pos < hi;
+  const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
+  const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
+
+  // This lane's position.
+  const uint32_t at = t * S + FK_WIDE_RUN * wave + lane;
+  const bool live = at >= lo && at < hi;
+  const uint32_t ring = (live ? at : (hi > lo ? lo : 0)) % p.length;
+  const uint16_t *krow = kc + (base + ring) * d;
+  const uint16_t *vrow = vc + (base + ring) * d;
+
+  // Loads first: the queries (and their RoPE partners and cosines), the new
+  // rows' elements, then the lane's key and value rows, 16 bytes a load.
+  float qx = 0.0f, qp = 0.0f, qc = 1.0f, qn = 0.0f;
+  const uint32_t qj = tid % d;
+  const uint32_t qi = qj < half ? qj : qj - half;
+  if (tid < group * d) {
+    const float *head = q + (size_t)(g * group + tid / d) * d;
+    qx = head[qj];
+    if (p.rope && qi < p.rotated) {
+      qp = head[qj < half ? qj + half : qj - half];
+      qc = cs[2 * qi];
+      qn = cs[2 * qi + 1];
+    }
+  }
+  float kx = 0.0f, kp = 0.0f, kcs = 1.0f, ksn = 0.0f, vx = 0.0f;
+  if (stores && tid < d) {
+    const float *head = knew + (size_t)g * d;
+    kx = head[qj];
+    if (p.krope && qi < p.rotated) {
+      kp = head[qj < half ? qj + half : qj - half];
+      kcs = cs[2 * qi];
+      ksn = cs[2 * qi + 1];
+    }
+    vx = vnew[(size_t)g * d + qj];
+  }
+  u32x4 kr[8], vr[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    if ((uint32_t)c < d / 8) {
+      kr[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(krow) + c);
+      vr[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vrow) + c);
+    } else {
+      kr[c] = vr[c] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // The queries RoPE'd as rope_elem does, into LDS (a threadgroup of fewer
+  // threads than the group's query elements takes the rest in more passes).
+  if (tid < group * d) {
+    float v = qx;
+    if (p.rope && qi < p.rotated) v = qj < half ? qx * qc - qp * qn : qx * qc + qp * qn;
+    qs[tid] = v;
+  }
+  for (uint32_t o = tid + blockDim.x; o < group * d; o += blockDim.x) {
+    const float *head = q + (size_t)(g * group + o / d) * d;
+    const uint32_t j = o % d;
+    const uint32_t i = j < half ? j : j - half;
+    float v = head[j];
+    if (p.rope && i < p.rotated) {
+      const float partner = head[j < half ? j + half : j - half];
+      v = j < half ? v * cs[2 * i] - partner * cs[2 * i + 1] : v * cs[2 * i] + partner * cs[2 * i + 1];
+    }
+    qs[o] = v;
+  }
+  // The new rows, element tid: RoPE'd and rounded as the plan's store does,
+  // into the caches and LDS.
+  if (stores && tid < d) {
+    float k = kx;
+    if (p.krope && qi < p.rotated) k = qj < half ? kx * kcs - kp * ksn : kx * kcs + kp * ksn;
+    const uint16_t kh = narrow_cache(k, bf16), vh = narrow_cache(vx, bf16);
+    const size_t where = (base + pos % p.length) * d + qj;
+    kc[where] = kh;
+    vc[where] = vh;
+    kn[qj] = kh;
+    vn[qj] = vh;
+  }
+  __syncthreads();  // the queries and the new rows
+
+  // The lane holding the position takes the new rows.
+  if (stores && at == pos) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      if ((uint32_t)c < d / 8) {
+        kr[c] = reinterpret_cast<const u32x4 *>(kn)[c];
+        vr[c] = reinterpret_cast<const u32x4 *>(vn)[c];
+      }
+    }
+  }
+  float kf[64];
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    const uint32_t w4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      kf[8 * c + 2 * e] = widen_cache((uint16_t)(w4[e] & 0xFFFFu), bf16);
+      kf[8 * c + 2 * e + 1] = widen_cache((uint16_t)(w4[e] >> 16), bf16);
+    }
+  }
+  // The values transposed into this wave's LDS, zeros off the split.
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    if ((uint32_t)c < d / 8) {
+      vt[(4 * c) * FK_WIDE_VT + lane] = live ? vr[c].x : 0u;
+      vt[(4 * c + 1) * FK_WIDE_VT + lane] = live ? vr[c].y : 0u;
+      vt[(4 * c + 2) * FK_WIDE_VT + lane] = live ? vr[c].z : 0u;
+      vt[(4 * c + 3) * FK_WIDE_VT + lane] = live ? vr[c].w : 0u;
+    }
+  }
+  // Scores, maxima, weights (into et) and weight sums.
+  float *aw = et + 8 * 64;  // [h][64]
+  float *ml = aw + 8 * 64;  // [h][2]
+  float *ew = ml + 16;      // [h]
+  if (group <= 4) {
+    float m[4], l[4];
+    wide_weights<4>(qs, kf, d, group, live, p.scale, et, m, l);
+    if (lane < 4) {
+      ml[2 * lane] = lane == 0 ? m[0] : lane == 1 ? m[1] : lane == 2 ? m[2] : m[3];
+      ml[2 * lane + 1] = lane == 0 ? l[0] : lane == 1 ? l[1] : lane == 2 ? l[2] : l[3];
+    }
+  } else {
+    float m[8], l[8];
+    wide_weights<8>(qs, kf, d, group, live, p.scale, et, m, l);
+    if (lane < 8) {
+      float mv = m[0], lv = l[0];
+#pragma unroll
+      for (int h = 1; h < 8; h++)
+        if ((uint32_t)h == lane) mv = m[h], lv = l[h];
+      ml[2 * lane] = mv;
+      ml[2 * lane + 1] = lv;
+    }
+  }
+  __syncthreads();  // the weights and values
+
+  // The wave's weighted values: lane (a, j) = (lane / P, lane % P), P = d / 2
+  // pairs, takes dimensions 2j and 2j + 1 of heads a, a + 64 / P, ...; four
+  // positions a step, in order.
+  {
+    const uint32_t P = d / 2;
+    const uint32_t jp = lane % P, a = lane / P, L = FK_WAVE / P;
+    float acc[4][2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) acc[k][0] = acc[k][1] = 0.0f;
+    for (uint32_t p0 = 0; p0 < FK_WIDE_RUN; p0 += 4) {
+      const u32x4 v4 = *reinterpret_cast<const u32x4 *>(vt + jp * FK_WIDE_VT + p0);
+      const uint32_t vw[4] = {v4.x, v4.y, v4.z, v4.w};
+      float vlo[4], vhi[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        vlo[e] = widen_cache((uint16_t)(vw[e] & 0xFFFFu), bf16);
+        vhi[e] = widen_cache((uint16_t)(vw[e] >> 16), bf16);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t h = a + k * L;
+        if (h < group) {
+          const float4 e4 = *reinterpret_cast<const float4 *>(et + h * 64 + p0);
+          const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            acc[k][0] = __builtin_fmaf(ev[e], vlo[e], acc[k][0]);
+            acc[k][1] = __builtin_fmaf(ev[e], vhi[e], acc[k][1]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t h = a + k * L;
+      if (h < group) *reinterpret_cast<float2 *>(aw + h * 64 + 2 * jp) = make_float2(acc[k][0], acc[k][1]);
+    }
+  }
+  __syncthreads();  // every wave's sums, maxima and weight sums
+
+  // The waves' factors: thread (w, h) takes e_w of head h, and wave 0's
+  // threads the heads' maxima.
+  if (tid < W * group) {
+    const uint32_t w = tid / group, h = tid % group;
+    int mk = max_key(-__builtin_inff());
+    for (uint32_t u = 0; u < W; u++) mk = max(mk, max_key(waves[(size_t)u * WIDE_WAVE_FLOATS + 32 * FK_WIDE_VT +
+                                                                 16 * 64 + 2 * h]));
+    const float M = from_max_key(mk);
+    float *mlw = waves + (size_t)w * WIDE_WAVE_FLOATS + 32 * FK_WIDE_VT + 16 * 64;
+    const float mw = mlw[2 * h];
+    mlw[16 + h] = mw == -__builtin_inff() ? 0.0f : exp_once(mw - M);
+    if (w == 0) mm[h] = M;
+  }
+  __syncthreads();  // the factors
+
+  // The threadgroup's partials.
+  for (uint32_t o = tid; o < group * d; o += blockDim.x) {
+    const uint32_t h = o / d, i = o % d;
+    const float M = mm[h];
+    float L = 0.0f, A = 0.0f;
+    if (M != -__builtin_inff()) {
+      for (uint32_t w = 0; w < W; w++) {
+        const float *b = waves + (size_t)w * WIDE_WAVE_FLOATS + 32 * FK_WIDE_VT + 8 * 64;  // aw of wave w
+        const float e = b[8 * 64 + 16 + h];
+        L = L + b[8 * 64 + 2 * h + 1] * e;
+        A = A + b[h * 64 + i] * e;
+      }
+    }
+    const size_t ht = (size_t)(g * group + h) * p.splits + t;
+    partials[ht * d + i] = A;
+    if (i == 0) {
+      float *st = partials + (size_t)p.heads * p.splits * d + 2 * ht;
+      st[0] = M;
+      st[1] = L;
+    }
+  }
+}
+
+__device__ __forceinline__ void step_attend_wide(const float *__restrict__ q, const float *__restrict__ knew,
+                                                 const float *__restrict__ vnew, uint16_t *__restrict__ kc,
+                                                 uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
+                                                 const uint32_t *__restrict__ slot, const float *__restrict__ rope,
+                                                 float *__restrict__ partials, const fk_step_attend_params &p) {
+  if (p.cache_bf16)
+    attend_wide<1>(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+  else
+    attend_wide<0>(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+}
+
+}  // namespace fk

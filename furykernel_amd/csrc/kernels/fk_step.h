@@ -62,6 +62,16 @@ extern "C" __global__ void __launch_bounds__(FK_ATTN_THREADS)
   fk::step_attend(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
 }
 
+// The attention in wide splits (fk_attention.h): 32 positions a wavefront,
+// up to 16 wavefronts a threadgroup, the LDS fk::wide_lds_floats(waves) floats.
+extern "C" __global__ void __launch_bounds__(FK_WAVE * FK_WIDE_MAX_WAVES)
+    fk_step_attend_wide(const float *__restrict__ q, const float *__restrict__ knew, const float *__restrict__ vnew,
+                        uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
+                        const uint32_t *__restrict__ slot, const float *__restrict__ rope,
+                        float *__restrict__ partials, fk_step_attend_params p) {
+  fk::step_attend_wide(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+}
+
 extern "C" __global__ void __launch_bounds__(FK_WAVE)
     fk_step_combine(const float *__restrict__ partials, float *__restrict__ out, fk_step_combine_params p) {
   fk::step_combine(partials, out, p);

@@ -158,6 +158,9 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
   constexpr bool GATHER = PRO == FK_PRO_GATHER || PRO == FK_PRO_GATHER_RMSNORM;
   constexpr bool NORM = PRO == FK_PRO_RMSNORM || PRO == FK_PRO_GATHER_RMSNORM;
   constexpr bool SILU = PRO == FK_PRO_SILU_MUL;
+  constexpr bool COMBINE = PRO == FK_PRO_COMBINE;
+  // The combine prologue's splits at most (its loads are straight-line).
+  constexpr uint32_t CS = 8;
   constexpr bool RESIDUAL = EPI == FK_EPI_ADD_STORED || EPI == FK_EPI_ADD_GATHER;
   // The input row (normalized, for the norm prologues) in LDS transposed to
   // the lanes' packs: chunk c (4 elements) of lane l's pack it is float4 (it C + c) 64 + l,
@@ -190,10 +193,27 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
   // Prologue loads: thread t's packs of 4, t, t + T, ... (tgReduceSum's order).
   const uint32_t tok = GATHER ? min(token[0], p.table_rows - 1) : 0u;
   float4 xa[NPK], xb[NPK], ga[NPK];
+  // The combine prologue: pack-of-4 j of the row is head h's dimensions
+  // i .. i + 3; its splits' accumulators (float4 each) and (max, sum) pairs.
+  float4 ca[COMBINE ? NPK : 1][COMBINE ? CS : 1];
+  float2 cst[COMBINE ? NPK : 1][COMBINE ? CS : 1];
 #pragma unroll
   for (int m = 0; m < NPK; m++) {
     const uint32_t j = min(tid + m * FK_GEMV_THREADS, packs4 - 1);
-    if constexpr (GATHER) {
+    if constexpr (COMBINE) {
+      const uint32_t e = 4 * j;
+      const uint32_t hd = p.head_dim;
+      const uint32_t h = e / hd, i = e % hd;
+      const uint32_t heads = k / hd;
+      const float *st = src + (size_t)heads * p.splits * hd + (size_t)h * p.splits * 2;
+#pragma unroll
+      for (uint32_t tt = 0; tt < CS; tt++) {
+        const uint32_t tc = min(tt, p.splits - 1);
+        ca[m][tt] = *reinterpret_cast<const float4 *>(src + ((size_t)h * p.splits + tc) * hd + i);
+        cst[m][tt] = *reinterpret_cast<const float2 *>(st + 2 * tc);
+      }
+      xa[m] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else if constexpr (GATHER) {
       const WT *row = table + (size_t)tok * k + 4 * j;
       if constexpr (sizeof(WT) == 2) {
         const uint2 h = *reinterpret_cast<const uint2 *>(row);
@@ -233,6 +253,31 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
       v.y = v.y * gfactor;
       v.z = v.z * gfactor;
       v.w = v.w * gfactor;
+    }
+    if constexpr (COMBINE) {
+      // The combine kernel's arithmetic (fk_step_combine): the splits' largest
+      // maximum, their weights exp(m_t - top) binary64's rounded once, then in
+      // split order from +0: l += l_t w_t, acc += acc_t w_t; x = acc / l.
+      int tk = fk::max_key(-__builtin_inff());
+#pragma unroll
+      for (uint32_t tt = 0; tt < CS; tt++)
+        if (tt < p.splits) tk = max(tk, fk::max_key(cst[m][tt].x));
+      const float top = fk::from_max_key(tk);
+      float l = 0.0f;
+      float a4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t tt = 0; tt < CS; tt++) {
+        if (tt < p.splits) {
+          const float w = fk::exp_once(cst[m][tt].x - top);
+          const float lw = cst[m][tt].y * w;
+          l = l + lw;
+          a4[0] = a4[0] + ca[m][tt].x * w;
+          a4[1] = a4[1] + ca[m][tt].y * w;
+          a4[2] = a4[2] + ca[m][tt].z * w;
+          a4[3] = a4[3] + ca[m][tt].w * w;
+        }
+      }
+      v = make_float4(a4[0] / l, a4[1] / l, a4[2] / l, a4[3] / l);
     }
     if constexpr (SILU) {
       const uint32_t act = p.act;
@@ -441,13 +486,15 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
   FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 1)      \
   FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 2)      \
   FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 3)      \
-  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 4)
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 4)      \
+  FK_STEP_GEMV_PRO(NAME, WT, P, R, KPL, DB, 5)
 #define FK_STEP_GEMV_SHAPE_PAIRS(NAME, WT, P, R, KPL, DB) \
   FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 0)          \
   FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 1)          \
   FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 2)          \
   FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 3)          \
-  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 4)
+  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 4)          \
+  FK_STEP_GEMV_PAIRS(NAME, WT, P, R, KPL, DB, 5)
 
 // f16 weights: k up to 2048 (4 packs a lane) in blocks of 1 or 2 rows; k up to
 // 8192 (16 packs a lane), one row a block.  A block's loads are issued when the

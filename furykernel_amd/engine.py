@@ -24,6 +24,7 @@ _NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32
 _STRUCTS = {
     "fk_step_store": K.StepStoreParams,
     "fk_step_attend": K.StepAttendParams,
+    "fk_step_attend_wide": K.StepAttendParams,
     "fk_step_combine": K.StepCombineParams,
     "fk_step_argmax": K.CountParams,
     "fk_step_act_mul": K.ActMulParams,
@@ -80,7 +81,11 @@ def _gemv_needs(launch: Launch) -> dict:
     wb = _ELT[wt]
     n, rows, k = p["n_anchors"], p["rows"], p["k"]
     widest = max(rows[:n])
-    need = {"src": (k * 4, "f32"), "src2": ((k + p.get("src2_off", 0)) * 4, "f32"), "gamma": (k * 4, "f32"),
+    _, _, _, _, pro, _ = K.gemv_entry(launch.entry)
+    src_bytes = k * 4
+    if pro == K.PRO_COMBINE:
+        src_bytes = (k // p["head_dim"]) * p["splits"] * (p["head_dim"] + 2) * 4
+    need = {"src": (src_bytes, "f32"), "src2": ((k + p.get("src2_off", 0)) * 4, "f32"), "gamma": (k * 4, "f32"),
             "table": (p.get("table_rows", 1) * k * wb, wt), "token": (4, "u32"), "res_token": (4, "u32"),
             "res": (widest * 4, "f32"), "res_table": (p.get("table_rows", 1) * widest * wb, wt),
             "epi_out": ((rows[0] if epi in (K.EPI_SILU_MUL, K.EPI_SOFTCAP) else widest) * 4, "f32"),
@@ -128,6 +133,9 @@ def check_launch(launch: Launch, specs: dict) -> None:
             raise K.LaunchError(f"{e}: the SiLU·mul epilogue on anchors {p['rows']}, blocks of {r}")
         if epi == K.EPI_SOFTCAP and (p["n_anchors"] != 1 or not 0 < p.get("cap", 0) < float("inf")):
             raise K.LaunchError(f"{e}: a softcap of {p.get('cap')} on {p['n_anchors']} anchors")
+        if pro == K.PRO_COMBINE and (not 1 <= p.get("splits", 0) <= K.COMBINE_SPLITS or not p.get("head_dim")
+                                     or p["head_dim"] % 4 or p["k"] % p["head_dim"]):
+            raise K.LaunchError(f"{e}: a combine of {p.get('splits')} splits of heads of {p.get('head_dim')}")
         if p.get("act", 0) not in (K.ACT_SILU, K.ACT_GELU_TANH) or p.get("src2_off", 0) % 4:
             raise K.LaunchError(f"{e}: activation {p.get('act')}, second row at {p.get('src2_off')}")
     reads = K.launch_reads(e, launch.params)
@@ -135,7 +143,7 @@ def check_launch(launch: Launch, specs: dict) -> None:
     if unbound:
         raise K.LaunchError(f"{e}: reads or writes {unbound}, which the launch leaves unbound")
     needs = _gemv_needs(launch) if e.startswith("fk_step_gemv") else \
-        _attend_needs(launch) if e == "fk_step_attend" else {}
+        _attend_needs(launch) if e in ("fk_step_attend", "fk_step_attend_wide") else {}
     for b in sorted(reads & set(needs)):
         spec = specs[launch.bind[b]]
         nbytes, dtype = needs[b]

@@ -85,6 +85,8 @@ class StepGemvParams(ctypes.Structure):
         ("act", ctypes.c_uint32),
         ("src2_off", ctypes.c_uint32),
         ("cap", ctypes.c_float),
+        ("splits", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
     ]
 
 
@@ -237,7 +239,7 @@ STEP_GEMV_SHAPES = {"fk_step_gemv_f16_k2048_r1": False, "fk_step_gemv_f16_k2048_
                     "fk_step_gemv_f32_k256_r1": False,
                     "fk_step_gemv_f32_k256_r2": True, "fk_step_gemv_f32_k1024_r1": False,
                     "fk_step_gemv_f32_k1024_r2": True}
-STEP_GEMV_ENTRIES = tuple(f"{shape}_p{pro}_e{epi}" for shape, pairs in STEP_GEMV_SHAPES.items() for pro in range(5)
+STEP_GEMV_ENTRIES = tuple(f"{shape}_p{pro}_e{epi}" for shape, pairs in STEP_GEMV_SHAPES.items() for pro in range(6)
                           for epi in ((0, 1, 2, 3, 4, 5) if pairs else (0, 1, 2, 4, 5)))
 STEP_GEMV_BUFFERS = ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token", "res", "res_table",
                      "res_token", "epi_out", "arg")
@@ -275,6 +277,8 @@ ABIS: dict[str, KernelAbi] = {
                                StepStoreParams),
     "fk_step_attend": KernelAbi("fk_step_attend", ("q", "knew", "vnew", "kc", "vc", "position", "slot", "rope",
                                                    "partials"), StepAttendParams),
+    "fk_step_attend_wide": KernelAbi("fk_step_attend_wide", ("q", "knew", "vnew", "kc", "vc", "position", "slot",
+                                                             "rope", "partials"), StepAttendParams),
     "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams, 64),
     "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
     "fk_step_act_mul": KernelAbi("fk_step_act_mul", ("a", "b", "y"), ActMulParams),
@@ -502,7 +506,8 @@ class Kernels:
 # as address 0); one inside it never may.
 
 _GEMV_SUFFIX = re.compile(r"^(fk_step_gemv_(f16|bf16|f32)_k(\d+)_r(\d+))_p(\d)_e(\d)$")
-PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = range(5)
+PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, PRO_COMBINE = range(6)
+COMBINE_SPLITS = 8  # the combine prologue's splits at most
 EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = range(6)
 ACT_SILU, ACT_GELU_TANH = 0, 1
 
@@ -553,7 +558,7 @@ def launch_reads(entry: str, params: dict) -> set[str]:
     if entry.startswith("fk_step_gemv"):
         _, _, _, _, pro, epi = gemv_entry(entry)
         return gemv_reads(pro, epi, params["n_anchors"], bool(params.get("store_tile", 0)), params.get("arg_slots", 0))
-    if entry == "fk_step_attend":
+    if entry in ("fk_step_attend", "fk_step_attend_wide"):
         need = {"q", "kc", "vc", "position", "slot", "partials"}
         if params.get("store"):
             need |= {"knew", "vnew"}

@@ -26,12 +26,21 @@ from .program.graph import (
 from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
 
 THREADS = 256
-ATTN_SPLIT = 128      # positions a split of the attention covers (64 or 128)
+ATTN_SPLIT = 128      # positions a split of the narrow attention covers (64 or 128)
 ATTN_THREADS = 512
+WIDE_RUN, WIDE_MAX_WAVES = 64, 8    # the wide attention: positions a wavefront, wavefronts a threadgroup
+COMBINE_SPLITS = 8                  # splits the GEMV step's combine prologue takes
+
+
+def wide_lds_floats(waves: int) -> int:
+    """The wide attention's LDS (fk_attention.h: wide_lds_floats)."""
+    return 512 + 64 + 8 + waves * (32 * 68 + 8 * 64 + 8 * 64 + 16 + 8)
+
+
 MAX_K = 8192
 
 # GEMV step prologue and epilogue modes (fk_step_gemv.h).
-PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = 0, 1, 2, 3, 4
+PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, PRO_COMBINE = 0, 1, 2, 3, 4, 5
 EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = 0, 1, 2, 3, 4, 5
 # Activations of an act·mul (the SiLU form this target adds, GELU-tanh the reference's).
 ACT = {SILU: 0, GELU_TANH: 1}
@@ -84,22 +93,63 @@ class Lowered:
 
 
 def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units: int = 256,
-               fuse: bool = True) -> Lowered:
+               fuse: bool = True, wide: bool = False) -> Lowered:
     """The launches of every step of the plan, in order, for steps of `rows`
     rows (one, a decode step's), on a device of `compute_units` CUs.  With
     `fuse`, light steps fold into the launch before them: a KV store into the
-    attention right after it, a stored SiLU·mul into the GEMV step of its two
-    anchors, the greedy token into the GEMV step of its logits."""
+    attention right after it, a stored act·mul into the GEMV step of its two
+    anchors, the greedy token into the GEMV step of its logits, and the
+    attention's combine into the GEMV step that reads its output.  With
+    `wide`, attention over heads of 16, 32 or 64 runs in wide splits (at most
+    8 a head, 64 positions a wavefront); else in splits of 128 positions.  The
+    narrow splits are the default: at 4096 positions the wide kernel's 64
+    threadgroups leave three CUs in four idle and are bound by each CU's LDS
+    bandwidth (14-16 us a launch against 5.5 us for the narrow kernel and its
+    combine's 3 us)."""
     if rows != 1:
         raise LoweringError(f"steps of {rows} rows: the decode kernels take one row a step")
     out = Lowered(checked.program, plan, rows)
-    low = _StepLowering(out, compute_units)
+    low = _StepLowering(out, compute_units, wide)
     for step in plan.steps:
         out.launches.append(low.step(step))
     if fuse:
         _fuse_attention(out)
         _fuse_light(out, compute_units)
+        _fuse_combine(out, compute_units)
     return out
+
+
+def _fuse_combine(out: Lowered, compute_units: int) -> None:
+    """A combine launch whose output only the GEMV step right after it reads,
+    as its stored input row, becomes that step's combine prologue: each of its
+    threadgroups combines the partials (at most 8 splits a head) as the
+    combine kernel does, then runs the GEMV on the row.  One launch fewer, and
+    the row never leaves the registers: its buffer is dropped."""
+    fused: list = []
+    launches = out.launches
+    for i, launch in enumerate(launches):
+        prev = fused[-1] if fused else None
+        if (prev is not None and prev.entry == "fk_step_combine" and launch.entry.startswith("fk_step_gemv")
+                and launch.params["pro_mode"] == PRO_STORED and launch.bind["src"] == prev.bind["out"]
+                and prev.params["splits"] <= COMBINE_SPLITS and prev.params["head_dim"] % 4 == 0
+                and launch.params["k"] == prev.params["heads"] * prev.params["head_dim"]
+                and not any(prev.bind["out"] in L.bind.values() for L in launches[i + 1:])
+                and prev.bind["out"] not in _program_outputs(out)):
+            launch.params.update(pro_mode=PRO_COMBINE, splits=prev.params["splits"],
+                                 head_dim=prev.params["head_dim"])
+            launch.bind["src"] = prev.bind["partials"]
+            launch.step = f"{prev.step}+{launch.step}"
+            _shape_gemv(launch, compute_units)
+            del out.buffers[prev.bind["out"]]  # the combined row lives in registers only
+            fused[-1] = launch
+            continue
+        fused.append(launch)
+    out.launches = fused
+
+
+def _program_outputs(out: Lowered) -> set:
+    p = out.program
+    return {f"value:{p.value(o.value).name}" for o in p.outputs}
 
 
 def _fuse_attention(out: Lowered) -> None:
@@ -114,7 +164,8 @@ def _fuse_attention(out: Lowered) -> None:
     for launch in out.launches:
         prev = fused[-1] if fused else None
         merged = None
-        if prev is not None and launch.entry == "fk_step_attend" and prev.entry == "fk_step_store":
+        if prev is not None and launch.entry in ("fk_step_attend", "fk_step_attend_wide") and \
+                prev.entry == "fk_step_store":
             merged = _store_into_attend(prev, launch)
         if merged is not None:
             fused[-1] = merged
@@ -257,9 +308,10 @@ def rope_table(theta: float, d: int, rotated: int, rows: int) -> np.ndarray:
 
 
 class _StepLowering:
-    def __init__(self, out: Lowered, compute_units: int = 256):
+    def __init__(self, out: Lowered, compute_units: int = 256, wide: bool = True):
         self.out = out
         self.compute_units = compute_units
+        self.wide = wide
         self.p = out.program
         self.producer = {v: n for n in self.p.nodes for v in n.outputs}
 
@@ -618,17 +670,27 @@ class _StepLowering:
         if ATTN_SPLIT not in (64, 128):
             raise LoweringError(f"{step.name}: attention splits of {ATTN_SPLIT} positions; the kernel takes 64 or 128")
         bound = self.p.source(op.to.positions).kind.bound
-        splits = -(-min(bound, lay.length if spec.window is None else bound) // ATTN_SPLIT)
+        positions = min(bound, lay.length if spec.window is None else bound)
+        entry, threads, lds = "fk_step_attend", ATTN_THREADS, 0
+        split = ATTN_SPLIT
+        if self.wide and spec.head_dim in (16, 32, 64):
+            # Wide splits: 64 positions a wavefront, up to 8 wavefronts, so
+            # that a head has at most 8 splits (the combine prologue's) up to
+            # 4096 positions.
+            waves = min(WIDE_MAX_WAVES, max(1, -(-positions // (WIDE_RUN * COMBINE_SPLITS))))
+            split, entry, threads = WIDE_RUN * waves, "fk_step_attend_wide", 64 * waves
+            lds = 4 * wide_lds_floats(waves)
+        splits = -(-positions // split)
         if splits > 4096:
             raise LoweringError(f"{step.name}: {splits} splits")
-        params["splits"] = splits
+        params["splits"], params["split"] = splits, split
         out = anchor.outputs[0]
         pname = self.out.buffer(f"partials:{self.p.value(out).name}", "f32",
                                 spec.heads * splits * (spec.head_dim + 2))
         pos_buf = self.ints(op.to.positions)
         bind = {"q": qbuf, "knew": None, "vnew": None, "kc": kname, "vc": vname, "position": pos_buf,
                 "slot": self.ints(op.to.sequences), "rope": rope_buf or pos_buf, "partials": pname}
-        return Launch(step.name, "fk_step_attend", spec.kv_heads * splits, ATTN_THREADS, bind, params, meta)
+        return Launch(step.name, entry, spec.kv_heads * splits, threads, bind, params, meta, lds)
 
     def combine_step(self, step: Step) -> Launch:
         combines = [self.p.node(w.node) for w in step.work if w.kind == COMBINE]

@@ -21,7 +21,7 @@ Counted per launch, from its parameters and the buffer types it binds:
 
 from __future__ import annotations
 
-from .lower import EPI_ADD_GATHER, EPI_ADD_STORED, EPI_ARGMAX, EPI_SILU_MUL, EPI_SOFTCAP, PRO_GATHER, \
+from .lower import EPI_ADD_GATHER, EPI_ADD_STORED, EPI_ARGMAX, EPI_SILU_MUL, EPI_SOFTCAP, PRO_COMBINE, PRO_GATHER, \
     PRO_GATHER_RMSNORM, PRO_SILU_MUL, Launch, Lowered
 
 _ELT = {"f32": 4, "u32": 4, "f16": 2, "bf16": 2, "u16": 2, "u64": 8}
@@ -46,6 +46,8 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
         total = sum(r * k * _elt(lowered, b[f"w{j}"]) for j, r in enumerate(rows))
         if p["pro_mode"] in (PRO_GATHER, PRO_GATHER_RMSNORM):
             total += k * _elt(lowered, b["table"]) + 4
+        elif p["pro_mode"] == PRO_COMBINE:
+            total += (k // p["head_dim"]) * p["splits"] * (p["head_dim"] + 2) * 4
         else:
             total += k * 4 * (2 if p["pro_mode"] == PRO_SILU_MUL else 1)
         if p["has_gamma"]:
@@ -72,7 +74,7 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
         if p["rope"] != [0, 0]:
             total += p["rotated"] * 8
         return total
-    if e == "fk_step_attend":
+    if e in ("fk_step_attend", "fk_step_attend_wide"):
         n = positions_read(p["length"], p["window"], position)
         elt = _elt(lowered, b["kc"])
         d = p["head_dim"]

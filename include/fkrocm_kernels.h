@@ -41,7 +41,9 @@ enum {
   FK_PRO_RMSNORM = 1,        /* x = rmsnorm(src) * gamma * factor */
   FK_PRO_GATHER = 2,         /* x = table[token] * gfactor */
   FK_PRO_GATHER_RMSNORM = 3, /* x = rmsnorm(table[token] * gfactor) * gamma * factor */
-  FK_PRO_SILU_MUL = 4        /* x = act(src) * src2[src2_off ..] (act: FK_ACT_*, SiLU or GELU-tanh) */
+  FK_PRO_SILU_MUL = 4,       /* x = act(src) * src2[src2_off ..] (act: FK_ACT_*, SiLU or GELU-tanh) */
+  FK_PRO_COMBINE = 5         /* x = the attention's combine of the partials at src (at most 8 splits): the
+                                plan's Combine step folded into the GEMV step that reads its output */
 };
 
 /* Epilogue modes, on the anchors' tile (the entry's `_e<mode>` suffix). */
@@ -81,6 +83,8 @@ typedef struct fk_step_gemv_params {
   uint32_t act;          /* the act·mul prologue's and epilogue's activation (FK_ACT_*) */
   uint32_t src2_off;     /* elements into src2 where the act·mul prologue's second row starts */
   float cap;             /* the softcap epilogue's cap (positive, finite) */
+  uint32_t splits;       /* the combine prologue's partials: splits a head (at most 8) */
+  uint32_t head_dim;     /* ... and the heads' width (k / head_dim heads, a multiple of 4) */
 } fk_step_gemv_params;
 
 typedef struct fk_step_token_params {

@@ -21,6 +21,7 @@ from . import fkref
 NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u32": np.uint32, "u16": np.uint16,
       "u64": np.uint64}
 EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = 3, 4, 5
+PRO_COMBINE = 5
 TYPE = {"f16": fkref.F16, "bf16": fkref.BF16, "f32": fkref.F32}
 
 
@@ -53,6 +54,17 @@ class CpuTarget:
         if e.startswith("fk_step_gemv"):
             wt = e.split("_")[3]
             n = p["n_anchors"]
+            src = self._p(b["src"])
+            pro = p["pro_mode"]
+            if pro == PRO_COMBINE:
+                # The combine prologue: the combine kernel's row, then the
+                # GEMV step on it as a stored row.
+                d = p["head_dim"]
+                row = np.zeros(p["k"], np.float32)
+                st = L.fkref_step_combine(src, row.ctypes.data, p["k"] // d, d, p["splits"])
+                if st:
+                    raise ValueError(f"{launch.step} ({e}): the oracle refused its combine (status {st})")
+                src, pro = row.ctypes.data, 0
             epi = p["epi_mode"]
             folded = epi in (EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP)
             # A folded epilogue reads the anchors' tiles: kept here whether or not
@@ -64,7 +76,7 @@ class CpuTarget:
             rows = (ctypes.c_int * 3)(*p["rows"])
             tok = int(self.buffers[b["token"]][0]) if b["token"] else 0
             rtok = int(self.buffers[b["res_token"]][0]) if b["res_token"] else 0
-            st = L.fkref_step_gemv(ws, TYPE[wt], ys, rows, n, p["k"], p["pro_mode"], self._p(b["src"]),
+            st = L.fkref_step_gemv(ws, TYPE[wt], ys, rows, n, p["k"], pro, src,
                                    self._p(b["src2"]), self._p(b["gamma"]) if p["has_gamma"] else None,
                                    self._p(b["table"] or b["res_table"]), tok, p["table_rows"], p["seg"], p["eps"],
                                    p["factor"], p["gfactor"], 0 if folded else epi, self._p(b["res"]),
@@ -123,6 +135,18 @@ class CpuTarget:
                                            self._p(b["partials"]), p["heads"], p["kv_heads"], p["head_dim"],
                                            p["length"], p["slots"], p["splits"], p["split"], p["rope"], p["rotated"],
                                            launch.meta["theta"], p["scale"], p["window"], pos, slot, p["cache_bf16"])
+        elif e == "fk_step_attend_wide":
+            pos, slot = int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0])
+            st = 0
+            if p["store"]:
+                st = L.fkref_step_store(self._p(b["knew"]), self._p(b["vnew"]), self._p(b["kc"]), self._p(b["vc"]),
+                                        2, p["krope"], 0, p["kv_heads"], p["head_dim"], p["length"], p["slots"],
+                                        p["rotated"], launch.meta["store_theta"], pos, slot, p["cache_bf16"])
+            st = st or L.fkref_step_attend_wide(self._p(b["q"]), self._p(b["kc"]), self._p(b["vc"]),
+                                                self._p(b["partials"]), p["heads"], p["kv_heads"], p["head_dim"],
+                                                p["length"], p["slots"], p["splits"], p["split"], p["rope"],
+                                                p["rotated"], launch.meta["theta"], p["scale"], p["window"], pos,
+                                                slot, p["cache_bf16"])
         elif e == "fk_step_combine":
             st = L.fkref_step_combine(self._p(b["partials"]), self._p(b["out"]), p["heads"], p["head_dim"],
                                       p["splits"])

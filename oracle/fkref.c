@@ -573,6 +573,100 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
   return 0;
 }
 
+/* The attention in wide splits (fk_attention.h, attend_wide): a split of S =
+ * 64 W positions taken by W runs of 64 (W <= 8); in each run, for each query
+ * head, the score of position r is its fma chain from +0 over the dimensions
+ * in order, times scale (-inf off the split); the run's maximum m; weights
+ * exp(score - m) binary64's rounded once; their sum by the pairwise tree over
+ * the run's positions in order (pairs r, r ^ 1, then pairs of pairs, ...);
+ * for each dimension the fma chain over r of weight * value; then the runs
+ * merged in order by exp(m_run - M).  Reads the caches as they stand (the
+ * store, if any, is the caller's). */
+int fkref_step_attend_wide(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
+                           int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
+                           int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
+                           int cache_bf16) {
+  const int group = kv_heads > 0 ? heads / kv_heads : 0;
+  const int d = head_dim;
+  const int W = split / 64;
+  if (group < 1 || group > 8 || heads % kv_heads || (d != 16 && d != 32 && d != 64) || split % 64 || W < 1 ||
+      W > 8)
+    return -1;
+  uint32_t s = slot < (uint32_t)slots ? slot : 0;
+  uint32_t first = (window && position + 1 > (uint32_t)window) ? position + 1 - (uint32_t)window : 0;
+  float qs[8 * 64], kf[64][64], vf[64][64], sc[64], e[64], bt[64];
+  float mw[8][8], lw[8][8], aw[8][8][64];
+  for (int g = 0; g < kv_heads; g++) {
+    for (int h = 0; h < group; h++)
+      for (int j = 0; j < d; j++) {
+        const float *head = q + (size_t)(g * group + h) * d;
+        qs[h * d + j] = rope ? fkref_rope_elem(head, j, d, rotated, position, theta) : head[j];
+      }
+    for (int t = 0; t < splits; t++) {
+      uint32_t lo = (uint32_t)t * split > first ? (uint32_t)t * split : first;
+      uint32_t hi = position + 1 < (uint32_t)(t + 1) * split ? position + 1 : (uint32_t)(t + 1) * split;
+      const size_t base = ((size_t)s * kv_heads + g) * length;
+      for (int w = 0; w < W; w++) {
+        uint32_t run0 = (uint32_t)t * split + 64u * w;
+        int live[64];
+        for (int r = 0; r < 64; r++) {
+          uint32_t at = run0 + r;
+          live[r] = at >= lo && at < hi;
+          uint32_t ring = (live[r] ? at : (hi > lo ? lo : 0)) % (uint32_t)length;
+          for (int i = 0; i < d; i++) {
+            kf[r][i] = widen_cache(kc[(base + ring) * d + i], cache_bf16);
+            vf[r][i] = live[r] ? widen_cache(vc[(base + ring) * d + i], cache_bf16) : 0.0f;
+          }
+        }
+        for (int h = 0; h < group; h++) {
+          float m = -INFINITY;
+          for (int r = 0; r < 64; r++) {
+            float c = 0.0f;
+            for (int i = 0; i < d; i++) c = fmaf(qs[h * d + i], kf[r][i], c);
+            sc[r] = live[r] ? c * scale : -INFINITY;
+            m = fkref_max(m, sc[r]);
+          }
+          for (int r = 0; r < 64; r++) e[r] = m == -INFINITY ? 0.0f : fkref_exp(sc[r] - m);
+          for (int r = 0; r < 64; r++) bt[r] = e[r];
+          for (int width = 1; width < 64; width <<= 1)
+            for (int r = 0; r < 64; r += 2 * width) bt[r] = bt[r] + bt[r + width];
+          mw[w][h] = m;
+          lw[w][h] = bt[0];
+          for (int i = 0; i < d; i++) {
+            float acc = 0.0f;
+            for (int r = 0; r < 64; r++) acc = fmaf(e[r], vf[r][i], acc);
+            aw[w][h][i] = acc;
+          }
+        }
+      }
+      for (int h = 0; h < group; h++) {
+        float M = -INFINITY;
+        for (int w = 0; w < W; w++) M = fkref_max(M, mw[w][h]);
+        const size_t ht = (size_t)(g * group + h) * splits + t;
+        for (int i = 0; i < d; i++) {
+          float L = 0.0f, A = 0.0f;
+          if (M != -INFINITY) {
+            for (int w = 0; w < W; w++) {
+              float ew = mw[w][h] == -INFINITY ? 0.0f : fkref_exp(mw[w][h] - M);
+              float lp = lw[w][h] * ew;
+              float ap = aw[w][h][i] * ew;
+              L = L + lp;
+              A = A + ap;
+            }
+          }
+          partials[ht * d + i] = A;
+          if (i == 0) {
+            float *st = partials + (size_t)heads * splits * d + 2 * ht;
+            st[0] = M;
+            st[1] = L;
+          }
+        }
+      }
+    }
+  }
+  return 0;
+}
+
 int fkref_step_combine(const float *partials, float *out, int heads, int head_dim, int splits) {
   for (int h = 0; h < heads; h++) {
     const float *ph = partials + (size_t)h * splits * head_dim;

@@ -117,6 +117,10 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
                       int cache_bf16);
 
 /* The splits combined once, in split order. */
+int fkref_step_attend_wide(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
+                           int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
+                           int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
+                           int cache_bf16);
 int fkref_step_combine(const float *partials, float *out, int heads, int head_dim, int splits);
 
 /* The index of the largest element, ties to the lowest (Eval.hs:681-685). */

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
             "fkref_step_attend": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
                                        ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32, _i]),
             "fkref_step_combine": (_i, [_vp, _vp, _i, _i, _i]),
+            "fkref_step_attend_wide": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
+                                            ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32, _i]),
             "fkref_argmax": (ctypes.c_uint32, [_vp, _i]),
             "fkref_argmax_key": (ctypes.c_uint64, [ctypes.c_float, ctypes.c_uint32]),
             "fkref_argmax_keyed": (ctypes.c_uint64, [_vp, _i]),

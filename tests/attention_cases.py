@@ -75,6 +75,30 @@ def oracle(x: dict) -> dict:
     return dict(kc=kc, vc=vc, partials=part, out=out)
 
 
+def oracle_wide(x: dict, split: int) -> dict:
+    """The oracle's store (if asked), wide-split attention (splits of `split`
+    positions, 64 a run) and combine: the kernels' other attention order."""
+    L = fkref.lib()
+    kc, vc = x["kc"].copy(), x["vc"].copy()
+    heads, kv, d = x["heads"], x["kv"], x["d"]
+    splits = -(-x["length"] // split)
+    part = np.zeros(heads * splits * (d + 2), np.float32)
+    out = np.zeros(heads * d, np.float32)
+    if x["store"]:
+        assert L.fkref_step_store(x["knew"].ctypes.data, x["vnew"].ctypes.data, kc.ctypes.data, vc.ctypes.data, 2,
+                                  x["rope"], 0, kv, d, x["length"], 1, x["rotated"], x["theta"], x["pos"], 0,
+                                  x["bf16"]) == 0
+    assert L.fkref_step_attend_wide(x["q"].ctypes.data, kc.ctypes.data, vc.ctypes.data, part.ctypes.data, heads, kv,
+                                    d, x["length"], 1, splits, split, x["rope"], x["rotated"], x["theta"], x["scale"],
+                                    x["window"], x["pos"], 0, x["bf16"]) == 0
+    assert L.fkref_step_combine(part.ctypes.data, out.ctypes.data, heads, d, splits) == 0
+    return dict(kc=kc, vc=vc, partials=part, out=out, splits=splits)
+
+
+# Cases the wide kernel takes (heads of 16, 32 or 64), with its splits.
+WIDE = [(c, S) for c in CASES if c[2] in (16, 32, 64) for S in ((64, 512) if c[4] >= 1024 else (64, 192))]
+
+
 def widen_cache(c: np.ndarray, bf16: int) -> np.ndarray:
     """Cache elements as binary64 (exact)."""
     if bf16:

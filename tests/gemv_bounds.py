@@ -12,7 +12,8 @@ import numpy as np
 
 WAVE = 64
 THREADS = 512
-PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL = range(5)
+PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, PRO_COMBINE = range(6)
+COMBINE_SPLITS = 8
 EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = range(6)
 ELT = {"f32": 4, "f16": 2, "bf16": 2, "u32": 4, "u16": 2, "u64": 8}
 
@@ -95,6 +96,17 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
         need("token", np.array([0]), "the token")
         tok = table_rows - 1  # the largest row a clamped token reaches
         need("table", tok * k + 4 * j, "the gathered row", 4)
+    elif pro == PRO_COMBINE:
+        # Head h = 4j div d, dimensions i = 4j mod d: each split's (clamped)
+        # accumulators (4 floats) and its (max, sum) pair.
+        d, splits = prm["head_dim"], prm["splits"]
+        heads = k // d
+        if not 1 <= splits <= COMBINE_SPLITS or d % 4 or k % d:
+            raise Bad(f"{launch.entry}: a combine of {splits} splits of heads of {d}")
+        h, i = (4 * j) // d, (4 * j) % d
+        tc = np.minimum(np.arange(COMBINE_SPLITS), splits - 1)
+        need("src", ((h[:, None] * splits + tc[None, :]) * d + i[:, None]).ravel(), "the partials", 4)
+        need("src", (heads * splits * d + (h[:, None] * splits + tc[None, :]) * 2).ravel(), "the splits' stats", 2)
     else:
         need("src", 4 * j, "the stored row", 4)
     if pro == PRO_SILU_MUL:

@@ -137,11 +137,26 @@ def test_the_cases_the_definitions_fix():
     assert B.may_store("f16", Approx(1.0, 0.0), 1.0) and not B.may_store("f16", Approx(1.0, 0.0), 1.0009765625)
 
 
+def written(lowered) -> set:
+    """The buffers some launch of the lowered step writes (the manifest's
+    write and read_write bindings)."""
+    from furykernel_amd import runtime
+    out = set()
+    for L in lowered.launches:
+        a = runtime.abi_of(L.entry)
+        for i in range(a.n_buffers):
+            name = a.buffers[i].name.decode()
+            if a.buffers[i].access.decode() != "read" and L.bind.get(name):
+                out.add(L.bind[name])
+    return out
+
+
 def check_tiny(cpu, ev, bd, checked, caches):
     bad = []
+    stored = written(cpu.lowered)
     for name, rows in bd.values.items():
         buf = f"value:{name}"
-        if buf not in cpu.lowered.buffers:
+        if buf not in cpu.lowered.buffers or buf not in stored:
             continue
         got = cpu.read(buf).astype(np.float64)
         exact = ev.values[name][0]

@@ -15,6 +15,7 @@ import math
 import numpy as np
 import pytest
 
+from furykernel_amd.kernels import PRO_COMBINE
 from furykernel_amd.lower import lower_plan, rope_table
 from furykernel_amd.program.build import program
 from furykernel_amd.program.check import check_program
@@ -131,8 +132,8 @@ def tiny_state(seed=2026, position=16, dims=None):
     return checked, weights, caches, x, position
 
 
-def run_cpu_target(checked, weights, caches, x, position, width, options=PlanOptions()):
-    low = lower_plan(checked, plan(options, checked))
+def run_cpu_target(checked, weights, caches, x, position, width, options=PlanOptions(), wide=False):
+    low = lower_plan(checked, plan(options, checked), wide=wide)
     cpu = CpuTarget(low, width)
     for name, w in weights.items():
         if f"weight:{name}" in low.buffers:
@@ -217,15 +218,21 @@ def test_a_dropped_rope_term_is_caught():
 
 
 @pytest.mark.parametrize("position", [130, 255])
-def test_tiny_gqa_decode_in_two_splits_within_1e4_of_the_f64_evaluator(position):
+@pytest.mark.parametrize("wide", [False, True], ids=["narrow", "wide"])
+def test_tiny_gqa_decode_in_splits_within_1e4_of_the_f64_evaluator(position, wide):
     """Grouped queries (4 heads over 2 kv heads) over a ring of 256, at
-    positions whose attention runs in two splits of 128 combined: the CPU
-    target's logits within 1e-4 of the f64 evaluator, and its new cache rows
-    within f16 rounding."""
+    positions whose attention runs in splits (two of 128, or four wide
+    splits of 64) combined in the O GEMV step's prologue: the CPU target's
+    logits within 1e-4 of the f64 evaluator, and its new cache rows within
+    f16 rounding."""
     checked, w, c, x, _ = tiny_state(position=position, dims=TINY_GQA)
-    cpu = run_cpu_target(checked, w, c, x, position, 64)
-    attend = [L for L in cpu.lowered.launches if L.entry == "fk_step_attend"]
-    assert attend and all(L.params["splits"] == 2 and L.params["heads"] // L.params["kv_heads"] == 2 for L in attend)
+    cpu = run_cpu_target(checked, w, c, x, position, 64, wide=wide)
+    entry, splits = ("fk_step_attend_wide", 4) if wide else ("fk_step_attend", 2)
+    attend = [L for L in cpu.lowered.launches if L.entry == entry]
+    assert attend and all(L.params["splits"] == splits and L.params["heads"] // L.params["kv_heads"] == 2
+                          for L in attend)
+    combined = [L for L in cpu.lowered.launches if L.params.get("pro_mode") == PRO_COMBINE]
+    assert len(combined) == TINY_GQA.layers
     ev = run_evaluator(checked, w, c, x, position)
     assert rel(cpu.read("value:logits"), ev.outputs["logits"][0]) <= 1e-4
     for layer in range(TINY_GQA.layers):
@@ -236,15 +243,17 @@ def test_tiny_gqa_decode_in_two_splits_within_1e4_of_the_f64_evaluator(position)
             assert np.max(np.abs(got - want)) <= 2.0**-10 * np.max(np.abs(want))
 
 
-def test_tiny_gqa_with_a_split_dropped_is_caught():
+@pytest.mark.parametrize("wide", [False, True], ids=["narrow", "wide"])
+def test_tiny_gqa_with_a_split_dropped_is_caught(wide):
     """The check has teeth for the combine: the CPU target run with its
-    combines told of one split fewer (the last split's positions left out)
-    misses the evaluator by far more than 1e-4."""
+    combines (the combine launches, or the O GEMV steps' combine prologues)
+    told of one split fewer (the last split's positions left out) misses the
+    evaluator by far more than 1e-4."""
     checked, w, c, x, position = tiny_state(position=255, dims=TINY_GQA)
-    good = run_cpu_target(checked, w, c, x, position, 64)
+    good = run_cpu_target(checked, w, c, x, position, 64, wide=wide)
     low = good.lowered
     for L in low.launches:
-        if L.entry == "fk_step_combine":
+        if L.entry == "fk_step_combine" or L.params.get("pro_mode") == PRO_COMBINE:
             L.params["splits"] -= 1
     bad = CpuTarget(low, 64)
     for name in low.buffers:

@@ -51,17 +51,23 @@ def test_the_checker_sees_a_short_weight_buffer():
         check_launch(qkv, bufs)
 
 
-def probe_swaps(low, key: int):
+def probe_swaps(low, key: int, period: int):
     """The launches a grid sweep made when it put the first launch's entry of a
-    class of the step (launch i with i mod 6 == key, one per layer) onto every
-    launch of the class: its parameters and bindings stayed each launch's own."""
-    idx = [i for i in range(96) if i % 6 == key]
+    class of the step (launch i with i mod period == key, one per layer, for
+    layers of `period` launches) onto every launch of the class: its
+    parameters and bindings stayed each launch's own."""
+    idx = [i for i in range(16 * period) if i % period == key]
     first = low.launches[idx[0]].entry
     return [dataclasses.replace(low.launches[i], entry=first) for i in idx]
 
 
-@pytest.mark.parametrize("key,unbound", [(0, "token"), (3, "res_token")])
-def test_a_swapped_entry_reading_an_unbound_buffer_is_refused(key, unbound):
+# Layers of six launches (attention in splits of 128, the combine a launch of
+# its own) and of five (wide splits, the combine in the O step's prologue).
+SWAPS = [(False, 6, 0, "token"), (False, 6, 3, "res_token"), (True, 5, 0, "token"), (True, 5, 2, "res_token")]
+
+
+@pytest.mark.parametrize("wide,period,key,unbound", SWAPS)
+def test_a_swapped_entry_reading_an_unbound_buffer_is_refused(wide, period, key, unbound):
     """Layer 0's QKV step gathers its row (_p3) and its O step adds a gathered
     residual (_e2); layers 1-15's do not, and leave token / res_token unbound.
     The layer-0 entry on a later layer's launch reads address 0: the CPU model
@@ -69,9 +75,10 @@ def test_a_swapped_entry_reading_an_unbound_buffer_is_refused(key, unbound):
     from furykernel_amd.engine import check_launch as engine_check
     from furykernel_amd.kernels import LaunchError
     c = check_program(decoder_step(ONE_B, embed=True))
-    low = lower_plan(c, plan(PlanOptions(store_gelus=True), c))
-    swapped = probe_swaps(low, key)
-    assert low.launches[0 if key == 0 else 3].bind[unbound] is not None
+    low = lower_plan(c, plan(PlanOptions(store_gelus=True), c), wide=wide)
+    assert len(low.launches) == 16 * period + 2
+    swapped = probe_swaps(low, key, period)
+    assert low.launches[key].bind[unbound] is not None
     refused = 0
     for L in swapped[1:]:
         assert L.bind[unbound] is None
@@ -82,8 +89,8 @@ def test_a_swapped_entry_reading_an_unbound_buffer_is_refused(key, unbound):
         refused += 1
     assert refused == 15
     # The launches as lowered pass both.
-    for i in range(96):
-        if i % 6 == key:
+    for i in range(16 * period):
+        if i % period == key:
             check_launch(low.launches[i], low.buffers)
             engine_check(low.launches[i], low.buffers)
 

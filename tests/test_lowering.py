@@ -4,6 +4,7 @@ store before it computes, in the oracle's CPU target, exactly what the
 plan's separate store and attention steps compute."""
 
 import dataclasses
+import zlib
 
 import numpy as np
 import pytest
@@ -17,18 +18,18 @@ from oracle.cpu_target import CpuTarget
 TINY32 = dataclasses.replace(TINY, context=32)
 
 
-def lowered(dims, options=PlanOptions(), fuse=True, embed=False, layers=None):
+def lowered(dims, options=PlanOptions(), fuse=True, embed=False, layers=None, wide=False):
     checked = check_program(decoder_step(dims, embed=embed, layers=layers))
-    return lower_plan(checked, plan(options, checked), fuse=fuse)
+    return lower_plan(checked, plan(options, checked), fuse=fuse, wide=wide)
 
 
 def seeded(low, seed, position, width=64):
-    """A CPU target with every buffer the step reads drawn from a seeded
-    stream: weights 0.02 N(0, 1) (norm gains 1), caches N(0, 1), inputs
+    """A CPU target with every buffer the step reads drawn from a stream
+    seeded by `seed` and the buffer's name: weights 0.02 N(0, 1) (norm gains 1), caches N(0, 1), inputs
     0.02 N(0, 1)."""
-    rng = np.random.default_rng(seed)
     cpu = CpuTarget(low, width)
     for name, spec in sorted(low.buffers.items()):
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])  # a buffer's draws its own
         buf = cpu.buffers[name]
         if name.startswith("weight:"):
             if "norm" in name:
@@ -46,25 +47,45 @@ def seeded(low, seed, position, width=64):
     return cpu
 
 
+def test_a_1b_layer_in_wide_splits_is_five_launches():
+    """The QKV GEMV with RoPE on its rows, the attention in wide splits with
+    the KV store folded in, the O GEMV whose prologue combines the splits,
+    gate/up, down."""
+    low = lowered(ONE_B, embed=True, wide=True)
+    entries = [launch.entry for launch in low.launches]
+    assert len(entries) == 16 * 5 + 2
+    assert entries[:5] == ["fk_step_gemv_f16_k2048_r1_p3_e0", "fk_step_attend_wide",
+                           "fk_step_gemv_f16_k2048_r1_p5_e2", "fk_step_gemv_f16_k2048_r2_p1_e0",
+                           "fk_step_gemv_f16_k8192_r1_p4_e1"]
+    assert entries[5:10] == ["fk_step_gemv_f16_k2048_r1_p1_e0", "fk_step_attend_wide",
+                             "fk_step_gemv_f16_k2048_r1_p5_e1", "fk_step_gemv_f16_k2048_r2_p1_e0",
+                             "fk_step_gemv_f16_k8192_r1_p4_e1"]
+    attend, o = low.launches[1], low.launches[2]
+    assert attend.step == "s1_store+s2_attend"
+    assert (attend.params["store"], attend.params["krope"]) == (1, 1)
+    # 4096 positions in 8 splits of 512: 8 wavefronts of 64 positions
+    assert (attend.params["splits"], attend.params["split"], attend.threads) == (8, 512, 512)
+    assert attend.groups == ONE_B.kv_heads * attend.params["splits"]
+    assert o.bind["src"] == attend.bind["partials"] and o.params["splits"] == 8 and o.params["head_dim"] == 64
+    # The greedy token folds into the logits' GEMV step, then a token launch.
+    head, token = low.launches[-2:]
+    assert head.entry == "fk_step_gemv_f16_k2048_r2_p1_e4" and head.bind["arg"] == "argmax:token"
+    assert low.buffers["argmax:token"].count == head.groups == token.params["slots"]
+    assert token.entry == "fk_step_token" and token.bind["out"] == "value:token"
+
+
 def test_a_1b_layer_is_six_launches():
+    """The default, narrow splits: 32 splits of 128 positions, more than the
+    GEMV step's combine prologue takes, so the combine is a launch."""
     low = lowered(ONE_B, embed=True)
     entries = [launch.entry for launch in low.launches]
     assert len(entries) == 16 * 6 + 2
     assert entries[:6] == ["fk_step_gemv_f16_k2048_r1_p3_e0", "fk_step_attend", "fk_step_combine",
                            "fk_step_gemv_f16_k2048_r1_p0_e2", "fk_step_gemv_f16_k2048_r2_p1_e0",
                            "fk_step_gemv_f16_k8192_r1_p4_e1"]
-    assert entries[6:12] == ["fk_step_gemv_f16_k2048_r1_p1_e0", "fk_step_attend", "fk_step_combine",
-                             "fk_step_gemv_f16_k2048_r1_p0_e1", "fk_step_gemv_f16_k2048_r2_p1_e0",
-                             "fk_step_gemv_f16_k8192_r1_p4_e1"]
-    attend = low.launches[1]
-    assert attend.step == "s1_store+s2_attend"
-    assert (attend.params["store"], attend.params["krope"]) == (1, 1)
-    assert attend.groups == ONE_B.kv_heads * attend.params["splits"]
-    # The greedy token folds into the logits' GEMV step, then a token launch.
+    assert low.launches[1].params["splits"] == 32
     head, token = low.launches[-2:]
-    assert head.entry == "fk_step_gemv_f16_k2048_r2_p1_e4" and head.bind["arg"] == "argmax:token"
-    assert low.buffers["argmax:token"].count == head.groups == token.params["slots"]
-    assert token.entry == "fk_step_token" and token.bind["out"] == "value:token"
+    assert head.entry == "fk_step_gemv_f16_k2048_r2_p1_e4" and token.entry == "fk_step_token"
 
 
 def test_a_stored_silu_mul_folds_into_the_gate_and_up_step():
@@ -84,20 +105,38 @@ def test_unfused_lowering_keeps_the_plans_steps():
     assert low.launches[-1].entry == "fk_step_argmax"
 
 
+@pytest.mark.parametrize("wide", [False, True], ids=["narrow", "wide"])
 @pytest.mark.parametrize("position", [0, 5, 31])
 @pytest.mark.parametrize("options", [PlanOptions(), PlanOptions(store_gelus=True)])
-def test_fused_launches_compute_the_plans_steps(position, options):
-    """Each layer's KV store folded into its attention (and, when the plan
-    stores the SiLU·mul, that light step folded into the gate/up GEMV step);
-    the greedy token folded into the logits' step and a token launch."""
-    fused, apart = lowered(TINY32, options), lowered(TINY32, options, fuse=False)
-    per_layer = 2 if options.store_gelus else 1
+def test_fused_launches_compute_the_plans_steps(position, options, wide):
+    """Each layer's KV store folded into its attention, its combine into the
+    O GEMV step's prologue (and, when the plan stores the SiLU·mul, that
+    light step folded into the gate/up GEMV step); the greedy token folded
+    into the logits' step and a token launch.  Every buffer the fused step
+    writes holds the same bits as the unfused step's."""
+    fused, apart = lowered(TINY32, options, wide=wide), lowered(TINY32, options, fuse=False, wide=wide)
+    per_layer = (2 if options.store_gelus else 1) + 1
     assert len(apart.launches) - len(fused.launches) == TINY32.layers * per_layer
-    a, b = seeded(fused, 7, position), seeded(apart, 7, position)
+    same_bits(fused, apart, 7, position)
+
+
+def same_bits(fused, apart, seed, position):
+    """Runs both lowerings from the same seeded buffers: the buffers the
+    fused step writes hold the unfused step's bits, and the ones it no
+    longer writes are only the combined attention rows its GEMV prologues
+    keep in registers."""
+    from test_bounds import written
+
+    a, b = seeded(fused, seed, position), seeded(apart, seed, position)
     a.run()
     b.run()
+    skipped = written(apart) - written(fused)
+    combined = {L.bind["out"] for L in apart.launches if L.entry == "fk_step_combine"}
+    assert skipped <= combined, skipped - combined
+    assert set(apart.buffers) - set(fused.buffers) == skipped
     for name in apart.buffers:
-        assert np.array_equal(a.read(name).view(np.uint8), b.read(name).view(np.uint8)), name
+        if name not in skipped:
+            assert np.array_equal(a.read(name).view(np.uint8), b.read(name).view(np.uint8)), name
 
 
 def test_every_lowered_entry_is_in_the_launch_table():
@@ -116,11 +155,7 @@ def test_bf16_caches_fuse_the_same_way():
         fused, apart = lowered(dims), lowered(dims, fuse=False)
     except (LoweringError, ValueError) as e:  # a program the gate refuses needs no lowering test
         pytest.skip(f"bf16 caches: {e}")
-    a, b = seeded(fused, 9, 17), seeded(apart, 9, 17)
-    a.run()
-    b.run()
-    for name in apart.buffers:
-        assert np.array_equal(a.read(name).view(np.uint8), b.read(name).view(np.uint8)), name
+    same_bits(fused, apart, 9, 17)
 
 
 def _residual_gather_program(table_type):

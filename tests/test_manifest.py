@@ -136,13 +136,13 @@ def _spans(launch, specs, base=1 << 32):
     return out
 
 
-def _lowered_1b(options=None):
+def _lowered_1b(options=None, wide=True):
     from furykernel_amd.lower import lower_plan
     from furykernel_amd.program.check import check_program
     from furykernel_amd.program.decoder import ONE_B, decoder_step
     from furykernel_amd.program.plan import PlanOptions, plan
     c = check_program(decoder_step(ONE_B, embed=True))
-    return lower_plan(c, plan(options or PlanOptions(store_gelus=True), c))
+    return lower_plan(c, plan(options or PlanOptions(store_gelus=True), c), wide=wide)
 
 
 def _check(launch, specs, **kw):
@@ -152,16 +152,19 @@ def _check(launch, specs, **kw):
                          kw.get("abi_hash"))
 
 
-def test_the_launch_check_accepts_every_lowered_launch():
-    low = _lowered_1b()
+@pytest.mark.parametrize("wide", [False, True])
+def test_the_launch_check_accepts_every_lowered_launch(wide):
+    low = _lowered_1b(wide=wide)
     for L in low.launches:
         _check(L, low.buffers)
 
 
-@pytest.mark.parametrize("key,unbound", [(0, "token"), (3, "res_token")])
-def test_the_launch_check_refuses_the_probes_swapped_entries(key, unbound):
-    low = _lowered_1b()
-    idx = [i for i in range(96) if i % 6 == key]
+@pytest.mark.parametrize("wide,period,key", [(False, 6, 0), (False, 6, 3), (True, 5, 0), (True, 5, 2)])
+def test_the_launch_check_refuses_the_probes_swapped_entries(wide, period, key):
+    """Layer 0's gathering QKV (_p3) or O step (_e2) entry on a later layer's
+    launch, whose token or res_token is unbound, is refused."""
+    low = _lowered_1b(wide=wide)
+    idx = [i for i in range(16 * period) if i % period == key]
     first = low.launches[idx[0]].entry
     for i in idx[1:]:
         L = dataclasses.replace(low.launches[i], entry=first)
@@ -171,7 +174,7 @@ def test_the_launch_check_refuses_the_probes_swapped_entries(key, unbound):
 
 def test_the_launch_check_refuses_wrong_hashes_sizes_and_short_buffers():
     from furykernel_amd.engine import params_struct
-    low = _lowered_1b()
+    low = _lowered_1b(wide=False)
     qkv = low.launches[6]
     good = runtime.abi_of(qkv.entry).abi_hash
     with pytest.raises(runtime.FkError, match="ABI hash"):
@@ -194,3 +197,32 @@ def test_the_launch_check_refuses_wrong_hashes_sizes_and_short_buffers():
     spans[8] = (spans[8][0], spans[8][1] - 4)  # partials short
     with pytest.raises(runtime.FkError, match="partials holds"):
         _check(att, low.buffers, spans=spans)
+
+
+def test_the_launch_check_refuses_wide_attention_and_combine_prologues_out_of_shape():
+    from furykernel_amd.engine import params_struct
+    low = _lowered_1b()
+    att, o = low.launches[6], low.launches[7]
+    assert att.entry == "fk_step_attend_wide" and o.params["pro_mode"] == K.PRO_COMBINE
+    _check(att, low.buffers)
+    _check(o, low.buffers)
+    # a split that is not 32 positions a wavefront of the threadgroup
+    p = params_struct(att)
+    p.split = att.params["split"] // 2
+    with pytest.raises(runtime.FkError):
+        _check(att, low.buffers, params=p)
+    # LDS short of what the wavefronts use
+    short = dataclasses.replace(att, lds_bytes=att.lds_bytes - 4)
+    with pytest.raises(runtime.FkError):
+        _check(short, low.buffers)
+    # more splits than the combine prologue takes
+    p = params_struct(o)
+    p.splits = K.COMBINE_SPLITS + 1
+    with pytest.raises(runtime.FkError):
+        _check(o, low.buffers, params=p)
+    # partials shorter than the prologue reads
+    spans = _spans(o, low.buffers)
+    i = list(K.ABIS[o.entry].buffers).index("src")
+    spans[i] = (spans[i][0], spans[i][1] - 4)
+    with pytest.raises(runtime.FkError):
+        _check(o, low.buffers, spans=spans)

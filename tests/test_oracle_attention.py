@@ -14,7 +14,7 @@ the query heads paired with the wrong kv heads."""
 import numpy as np
 import pytest
 
-from attention_cases import CASES, case_id, f64_attention, inputs, oracle, within_bounds
+from attention_cases import WIDE, CASES, case_id, f64_attention, inputs, oracle, oracle_wide, within_bounds
 from oracle import fkref
 
 
@@ -27,6 +27,18 @@ def test_split_attention_and_combine_within_the_f64_bounds(case):
     # and last kv head; the relative bars on every head
     group = heads // x["kv"]
     within_bounds(x, o, o["out"], sorted({0, group - 1, heads - group, heads - 1}))
+
+
+@pytest.mark.parametrize("case,split", WIDE, ids=lambda c: case_id(c) if isinstance(c, tuple) else f"S{c}")
+def test_wide_split_attention_and_combine_within_the_f64_bounds(case, split):
+    """The wide-split order (runs of 64, merged in the threadgroup) against the
+    same binary64 attention and bounds; its caches are the narrow order's."""
+    x = inputs(case)
+    o = oracle_wide(x, split)
+    heads, group = x["heads"], x["heads"] // x["kv"]
+    within_bounds(x, o, o["out"], sorted({0, heads - 1}))
+    n = oracle(x)
+    assert np.array_equal(o["kc"], n["kc"]) and np.array_equal(o["vc"], n["vc"])
 
 
 def test_the_new_rows_are_ones_a_kernel_may_store():
