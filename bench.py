@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=20, help="replays of each kernel's launches for its roofline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU time to spend on the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--untuned", action="store_true",
+                    help="shape the GEMV steps by the lowering's defaults, not the committed selections")
     ap.add_argument("--eager", action="store_true",
                     help="queue each step's launches on the stream instead of replaying a HIP graph")
     ap.add_argument("--workload", choices=("decode", "prefill", "kernels"), default="decode",
@@ -380,6 +382,16 @@ KERNELS_METRIC = "standalone kernels: achieved HBM GB/s (% of ~8 TB/s), 1 GPU"
 COPY_BYTES = 512 << 20   # inputs a kernel's launches cycle through: twice the 256 MB memory-side cache
 
 
+def gemv_variants(wtype: str, n: int, k: int) -> list:
+    """The (rows a wavefront, threads) the committed selection picks for the
+    standalone GEMV class, or every rows a wavefront at 256 threads."""
+    from furykernel_amd import tuning
+    pick = tuning.gemv_pick(wtype, n, k)
+    log(f"gemv_{wtype} n{n}_k{k}: " + (f"the committed selection's r{pick[0]}_t{pick[1]}" if pick else
+                                       "no valid committed selection; every rows a wavefront"))
+    return [pick] if pick else [(r, 256) for r in (1, 2, 4)]
+
+
 def main_kernels(args) -> int:
     """The standalone kernels at their configurations' sizes: f32 matvec
     W[4096 × 4096]·x, RMSNorm and row softmax over [64 × 4096] f32, and the
@@ -444,9 +456,9 @@ def main_kernels(args) -> int:
     bufs += ws + [x, y]
     nbytes = n * k * 4 + k * 4 + n * 4
     best = None
-    for r in (1, 2, 4):
-        us = timed([lambda w=w, r=r: ks.gemv(w, x, y, n, k, "f32", rows_per_wave=r) for w in ws], 20)
-        log(f"fk_gemv_f32_f32_r{r} 4096 x 4096: {us:.2f} us a launch, {nbytes / us / 1e3:.1f} GB/s")
+    for r, t in gemv_variants("f32", n, k):
+        us = timed([lambda w=w, r=r, t=t: ks.gemv(w, x, y, n, k, "f32", rows_per_wave=r, threads=t) for w in ws], 20)
+        log(f"fk_gemv_f32_f32_r{r} 4096 x 4096, {t} threads: {us:.2f} us a launch, {nbytes / us / 1e3:.1f} GB/s")
         if best is None or us < best[1]:
             best = (f"fk_gemv_f32_f32_r{r}", us)
     table["matvec_f32_4096x4096"] = {"kernel": best[0], "avg_us": round(best[1], 3), "bytes": nbytes,
@@ -489,9 +501,10 @@ def main_kernels(args) -> int:
     bufs += wi + [scale, xh, yi]
     nbytes = n * k + n * 4 + k * 2 + n * 4
     best = None
-    for r in (1, 2, 4):
-        us = timed([lambda w=w, r=r: ks.gemv(w, xh, yi, n, k, "i8", rows_per_wave=r, scale=scale) for w in wi], 20)
-        log(f"fk_gemv_i8_f16_r{r} 8192 x 8192: {us:.2f} us a launch, {nbytes / us / 1e3:.1f} GB/s")
+    for r, t in gemv_variants("i8", n, k):
+        us = timed([lambda w=w, r=r, t=t: ks.gemv(w, xh, yi, n, k, "i8", rows_per_wave=r, threads=t, scale=scale)
+                    for w in wi], 20)
+        log(f"fk_gemv_i8_f16_r{r} 8192 x 8192, {t} threads: {us:.2f} us a launch, {nbytes / us / 1e3:.1f} GB/s")
         if best is None or us < best[1]:
             best = (f"fk_gemv_i8_f16_r{r}", us)
     table["matvec_i8_8192x8192"] = {"kernel": best[0], "avg_us": round(best[1], 3), "bytes": nbytes,
@@ -568,7 +581,11 @@ def main() -> int:
 
     dev = runtime.Device(0)
     ks = kernels.Kernels(dev)
-    session = DecodeSession(dev, ks, ONE_B, PLAN, embed=True)
+    session = DecodeSession(dev, ks, ONE_B, PLAN, embed=True, tuned=not args.untuned)
+    from furykernel_amd import tuning
+    tuned = {f: p for f, p in tuning.validated(dev.info.compute_units).items() if f.startswith("step_gemv")}
+    log(f"GEMV step selections used: {sorted(tuned) or 'none'}"
+        + (f"; refused: {tuning.chooser_problems}" if tuning.chooser_problems else ""))
     session.init_synthetic()
     session.set_position(POSITION, token=7)
     log(f"{len(session.lowered.launches)} launches a step resident in HBM; "
@@ -626,7 +643,10 @@ def main() -> int:
                    "d_model": ONE_B.d_model, "layers": ONE_B.layers, "heads": ONE_B.heads,
                    "kv_heads": ONE_B.kv_heads, "head_dim": ONE_B.head_dim, "ffn": ONE_B.ffn, "vocab": ONE_B.vocab,
                    "kv_length": ONE_B.context, "position": POSITION, "launches": len(session.lowered.launches),
-                   "launch": "eager launches per token" if args.eager else "one HIP graph per token"},
+                   "launch": "eager launches per token" if args.eager else "one HIP graph per token",
+                   "gemv_selection": "untuned" if args.untuned else
+                   ({f: {c: "_".join(f"{a}{v}" for a, v in pt) for c, pt in p.items()} for f, p in tuned.items()}
+                    or "none committed")},
         "hbm": {"step_bytes": nbytes, "achieved_gbps": round(nbytes * tok_s / 1e9, 1),
                 "frac_of_peak": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4), "peak_gbps": HBM_PEAK_GBPS,
                 "ms_per_step_events": round(event_ms / args.steps, 4)},

@@ -34,12 +34,19 @@ class DecodeSession:
     embed: bool = True
     layers: Optional[int] = None
     fuse: bool = True
+    tuned: bool = False  # shape the GEMV steps as the committed selections pick
 
     def __post_init__(self):
         self.program = decoder_step(self.dims, embed=self.embed, layers=self.layers)
         self.checked = check_program(self.program)
         self.plan = plan(self.options, self.checked)
-        self.lowered = lower_plan(self.checked, self.plan, fuse=self.fuse)
+        choose = None
+        if self.tuned:
+            from .tuning import committed_chooser
+            choose = committed_chooser(self.device.info.compute_units)
+        self.lowered = lower_plan(self.checked, self.plan, fuse=self.fuse,
+                                  compute_units=self.device.info.compute_units if self.tuned else 256,
+                                  choose=choose)
         self.engine = Engine(self.device, self.kernels, self.lowered)
 
     # Synthetic state ------------------------------------------------------------

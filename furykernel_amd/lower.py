@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
-from typing import Optional
+from typing import Callable, Optional
 
 import numpy as np
 
@@ -93,7 +93,7 @@ class Lowered:
 
 
 def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units: int = 256,
-               fuse: bool = True, wide: bool = False) -> Lowered:
+               fuse: bool = True, wide: bool = False, choose: Optional[Callable] = None) -> Lowered:
     """The launches of every step of the plan, in order, for steps of `rows`
     rows (one, a decode step's), on a device of `compute_units` CUs.  With
     `fuse`, light steps fold into the launch before them: a KV store into the
@@ -105,21 +105,24 @@ def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units
     narrow splits are the default: at 4096 positions the wide kernel's 64
     threadgroups leave three CUs in four idle and are bound by each CU's LDS
     bandwidth (14-16 us a launch against 5.5 us for the narrow kernel and its
-    combine's 3 us)."""
+    combine's 3 us).  `choose`, given a GEMV step launch, may return the
+    (rows a block, threadgroups a CU) a tuned selection picks for it (see
+    ``tuning.committed_chooser``); a pick the launch cannot take is passed
+    over.  None of these changes what any launch computes."""
     if rows != 1:
         raise LoweringError(f"steps of {rows} rows: the decode kernels take one row a step")
     out = Lowered(checked.program, plan, rows)
-    low = _StepLowering(out, compute_units, wide)
+    low = _StepLowering(out, compute_units, wide, choose)
     for step in plan.steps:
         out.launches.append(low.step(step))
     if fuse:
         _fuse_attention(out)
-        _fuse_light(out, compute_units)
-        _fuse_combine(out, compute_units)
+        _fuse_light(out, compute_units, choose)
+        _fuse_combine(out, compute_units, choose)
     return out
 
 
-def _fuse_combine(out: Lowered, compute_units: int) -> None:
+def _fuse_combine(out: Lowered, compute_units: int, choose: Optional[Callable] = None) -> None:
     """A combine launch whose output only the GEMV step right after it reads,
     as its stored input row, becomes that step's combine prologue: each of its
     threadgroups combines the partials (at most 8 splits a head) as the
@@ -139,7 +142,7 @@ def _fuse_combine(out: Lowered, compute_units: int) -> None:
                                  head_dim=prev.params["head_dim"])
             launch.bind["src"] = prev.bind["partials"]
             launch.step = f"{prev.step}+{launch.step}"
-            _shape_gemv(launch, compute_units)
+            _shape_gemv(launch, compute_units, choose=choose)
             del out.buffers[prev.bind["out"]]  # the combined row lives in registers only
             fused[-1] = launch
             continue
@@ -204,7 +207,7 @@ def _store_into_attend(st: Launch, at: Launch) -> Optional[Launch]:
     return Launch(f"{st.step}+{at.step}", at.entry, at.groups, at.threads, bind, params, meta, at.lds_bytes)
 
 
-def _fuse_light(out: Lowered, compute_units: int) -> None:
+def _fuse_light(out: Lowered, compute_units: int, choose: Optional[Callable] = None) -> None:
     """A light step of one stored act·mul (SiLU or GELU-tanh) of the two
     anchors of the GEMV step right before it becomes that step's epilogue: its
     wavefronts hold row j of both anchors and store act(gate_j) * up_j — the
@@ -225,7 +228,7 @@ def _fuse_light(out: Lowered, compute_units: int) -> None:
                 pp["act"] = launch.params["act"]
                 pb["epi_out"] = launch.bind["y"]
                 prev.step = f"{prev.step}+{launch.step}"
-                _shape_gemv(prev, compute_units)
+                _shape_gemv(prev, compute_units, choose=choose)
                 continue
             keyed = (epi == EPI_NONE and pp["n_anchors"] == 1 and pp["store_tile"] and pb["y0"] == launch.bind.get("x")) \
                 or (epi == EPI_SOFTCAP and pb["epi_out"] == launch.bind.get("x"))
@@ -233,7 +236,7 @@ def _fuse_light(out: Lowered, compute_units: int) -> None:
                 if epi == EPI_NONE:
                     pp["epi_mode"] = EPI_ARGMAX
                 prev.step = f"{prev.step}+{launch.step}"
-                _shape_gemv(prev, compute_units)
+                _shape_gemv(prev, compute_units, choose=choose)
                 arg = out.buffer(f"argmax:{launch.bind['out'].split(':', 1)[1]}", "u64", prev.groups)
                 pb["arg"] = arg
                 pp["arg_slots"] = prev.groups
@@ -248,25 +251,41 @@ def _fuse_light(out: Lowered, compute_units: int) -> None:
 GEMV_THREADS = 512
 
 
-def _shape_gemv(launch: Launch, compute_units: int) -> None:
+def _shape_gemv(launch: Launch, compute_units: int, rows: Optional[int] = None, per_cu: int = 2,
+                choose: Optional[Callable] = None) -> None:
     """The GEMV step variant for the launch's weights, input width, rows and
     epilogue — rows a block, packs a lane — and its grid: blocks of rows, and
-    threadgroups of 8 wavefronts up to two a CU, each wavefront taking blocks
-    in turn."""
+    threadgroups of 8 wavefronts up to `per_cu` a CU, each wavefront taking
+    blocks in turn.  `rows` (1 or 2) asks for that many rows a block where the
+    input width has both; by default 2 for a pair epilogue or more than 4096
+    rows.  `choose` (see ``lower_plan``) may pick both."""
+    if choose is not None and rows is None:
+        pick = choose(launch)
+        if pick is not None:
+            saved = (launch.entry, launch.groups, launch.threads, launch.lds_bytes, dict(launch.params))
+            try:
+                _shape_gemv(launch, compute_units, rows=pick[0], per_cu=pick[1])
+                if launch.entry.split("_r")[1].split("_")[0] == str(pick[0]):
+                    return
+            except LoweringError:
+                pass
+            launch.entry, launch.groups, launch.threads, launch.lds_bytes = saved[:4]
+            launch.params.clear()
+            launch.params.update(saved[4])
     p = launch.params
     k, wt = p["k"], launch.meta["wtype"]
     total = p["first_row"][p["n_anchors"]]
     pairs = p["epi_mode"] == EPI_SILU_MUL
     if wt in (F16, BF16):
         if k <= 2048:
-            r = 2 if pairs or total > 4096 else 1
+            r = rows if rows in (1, 2) else (2 if pairs or total > 4096 else 1)
             entry, kmax = f"fk_step_gemv_{wt}_k2048_r{r}", 2048
         elif k <= MAX_K:
             r, entry, kmax = 1, f"fk_step_gemv_{wt}_k8192_r1", 8192
         else:
             raise LoweringError(f"{launch.step}: an input row of {k}; the {wt} GEMV steps take up to {MAX_K}")
     elif wt == F32:
-        r = 2 if pairs else 1
+        r = rows if rows in (1, 2) else (2 if pairs else 1)
         if k <= 256:
             entry, kmax = f"fk_step_gemv_f32_k256_r{r}", 256
         elif k <= 1024:
@@ -286,7 +305,7 @@ def _shape_gemv(launch: Launch, compute_units: int) -> None:
     launch.entry = entry
     launch.threads = GEMV_THREADS
     waves = GEMV_THREADS // 64
-    launch.groups = max(1, min(-(-blocks // waves), 2 * compute_units))
+    launch.groups = max(1, min(-(-blocks // waves), per_cu * compute_units))
     # The input row transposed in LDS, padded to the variant's widest row, and
     # the norm's gains beside it.
     norm = p["pro_mode"] in (PRO_RMSNORM, PRO_GATHER_RMSNORM)
@@ -308,10 +327,12 @@ def rope_table(theta: float, d: int, rotated: int, rows: int) -> np.ndarray:
 
 
 class _StepLowering:
-    def __init__(self, out: Lowered, compute_units: int = 256, wide: bool = True):
+    def __init__(self, out: Lowered, compute_units: int = 256, wide: bool = True,
+                 choose: Optional[Callable] = None):
         self.out = out
         self.compute_units = compute_units
         self.wide = wide
+        self.choose = choose
         self.p = out.program
         self.producer = {v: n for n in self.p.nodes for v in n.outputs}
 
@@ -570,7 +591,7 @@ class _StepLowering:
         params.update(n_anchors=len(anchors), rows=rows + [0] * (3 - len(rows)),
                       first_row=first + [g] * (4 - len(first)), k=k, store_tile=store_tile)
         launch = Launch(step.name, "", 0, GEMV_THREADS, bind, params, {"wtype": wt})
-        _shape_gemv(launch, self.compute_units)
+        _shape_gemv(launch, self.compute_units, choose=self.choose)
         return launch
 
     def rope_of(self, step: Step, node, rec: dict) -> Optional[int]:

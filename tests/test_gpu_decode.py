@@ -80,14 +80,16 @@ def test_tiny_decode_graph_replays_agree_with_eager(device, kernels):
         s.close()
 
 
-@pytest.mark.parametrize("store_gelus", [False, True])
-def test_1b_decode_step_bit_exact(device, kernels, store_gelus):
+@pytest.mark.parametrize("store_gelus,tuned", [(False, False), (True, False), (True, True)])
+def test_1b_decode_step_bit_exact(device, kernels, store_gelus, tuned):
     """The 1B-class step's real shapes (2 of its 16 layers, and the head) at the
     full context: position 4095 reads all 4096 positions of every cache.  With
     the plan's SiLU·mul recomputed in the down projection's prologue, and
-    stored (folded into the gate/up step's epilogue)."""
+    stored (folded into the gate/up step's epilogue); and with the GEMV steps
+    shaped as the committed selections pick (tuned)."""
     layers = 2
-    s = DecodeSession(device, kernels, ONE_B, PlanOptions(store_gelus=store_gelus), embed=True, layers=layers)
+    s = DecodeSession(device, kernels, ONE_B, PlanOptions(store_gelus=store_gelus), embed=True, layers=layers,
+                      tuned=tuned)
     try:
         s.init_synthetic()
         s.set_position(4095, token=31999)
