@@ -44,9 +44,34 @@ const char *keep(const std::string &s) {
 
 #define FK_P(S, f, ty) fk_abi_param{#f, ty, (uint32_t)offsetof(S, f)}
 #define FK_PA(S, f, i, ty) fk_abi_param{#f "_" #i, ty, (uint32_t)(offsetof(S, f) + (i) * 4)}
+#define FK_PX(S, f, name, ty) fk_abi_param{name, ty, (uint32_t)offsetof(S, f)}
 
 fk_abi_buffer buf(const char *name, const char *access, const char *type) {
   return fk_abi_buffer{name, access, type, 16};
+}
+
+std::vector<fk_abi_param> attend_params() {
+  using S = fk_step_attend_params;
+  return {FK_P(S, heads, "u32"),    FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"),
+          FK_P(S, slots, "u32"),    FK_P(S, splits, "u32"),   FK_P(S, split, "u32"),    FK_P(S, rope, "u32"),
+          FK_P(S, rotated, "u32"),  FK_P(S, rope_rows, "u32"), FK_P(S, scale, "f32"),   FK_P(S, window, "u32"),
+          FK_P(S, cache_bf16, "u32"), FK_P(S, store, "u32"),  FK_P(S, krope, "u32"),    FK_P(S, has_reach, "u32")};
+}
+
+std::vector<fk_abi_param> store_params() {
+  using S = fk_step_store_params;
+  return {FK_P(S, n_stores, "u32"), FK_PA(S, rope, 0, "u32"), FK_PA(S, rope, 1, "u32"), FK_P(S, kv_heads, "u32"),
+          FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"),   FK_P(S, slots, "u32"),    FK_P(S, rotated, "u32"),
+          FK_P(S, rope_rows, "u32"), FK_P(S, cache_bf16, "u32")};
+}
+
+// The paging fields of a params struct S that ends in an fk_paging g.
+template <typename S>
+std::vector<fk_abi_param> with_paging(std::vector<fk_abi_param> v) {
+  v.push_back(FK_PX(S, g.block_size, "block_size", "u32"));
+  v.push_back(FK_PX(S, g.table_len, "table_len", "u32"));
+  v.push_back(FK_PX(S, g.blocks, "blocks", "u32"));
+  return v;
 }
 
 std::vector<fk_abi_param> gemv_step_params() {
@@ -153,35 +178,35 @@ std::vector<Entry> build() {
         {buf("x0", "read", "f32"), buf("x1", "read", "f32"), buf("c0", "read_write", "f16"),
          buf("c1", "read_write", "f16"), buf("position", "read", "u32"), buf("slot", "read", "u32"),
          buf("rope", "read", "f32")},
-        {FK_P(S, n_stores, "u32"), FK_PA(S, rope, 0, "u32"), FK_PA(S, rope, 1, "u32"), FK_P(S, kv_heads, "u32"),
-         FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"), FK_P(S, slots, "u32"), FK_P(S, rotated, "u32"),
-         FK_P(S, rope_rows, "u32"), FK_P(S, cache_bf16, "u32")},
-        sizeof(S));
+        store_params(), sizeof(S));
   }
+  add("fk_step_store_paged", 0,
+      {buf("x0", "read", "f32"), buf("x1", "read", "f32"), buf("p0", "read", "u64"), buf("p1", "read", "u64"),
+       buf("position", "read", "u32"), buf("table", "read", "u32"), buf("rope", "read", "f32")},
+      with_paging<fk_step_store_paged_params>(store_params()), sizeof(fk_step_store_paged_params));
   {
     using S = fk_step_attend_params;
     add("fk_step_attend", 0,
         {buf("q", "read", "f32"), buf("knew", "read", "f32"), buf("vnew", "read", "f32"),
          buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16"), buf("position", "read", "u32"),
-         buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("partials", "write", "f32")},
-        {FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"),
-         FK_P(S, slots, "u32"), FK_P(S, splits, "u32"), FK_P(S, split, "u32"), FK_P(S, rope, "u32"),
-         FK_P(S, rotated, "u32"), FK_P(S, rope_rows, "u32"), FK_P(S, scale, "f32"), FK_P(S, window, "u32"),
-         FK_P(S, cache_bf16, "u32"), FK_P(S, store, "u32"), FK_P(S, krope, "u32")},
-        sizeof(S));
+         buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("partials", "write", "f32"),
+         buf("reach", "read", "u32")},
+        attend_params(), sizeof(S));
   }
   {
     using S = fk_step_attend_params;
     add("fk_step_attend_wide", 0,
         {buf("q", "read", "f32"), buf("knew", "read", "f32"), buf("vnew", "read", "f32"),
          buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16"), buf("position", "read", "u32"),
-         buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("partials", "write", "f32")},
-        {FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"),
-         FK_P(S, slots, "u32"), FK_P(S, splits, "u32"), FK_P(S, split, "u32"), FK_P(S, rope, "u32"),
-         FK_P(S, rotated, "u32"), FK_P(S, rope_rows, "u32"), FK_P(S, scale, "f32"), FK_P(S, window, "u32"),
-         FK_P(S, cache_bf16, "u32"), FK_P(S, store, "u32"), FK_P(S, krope, "u32")},
-        sizeof(S));
+         buf("slot", "read", "u32"), buf("rope", "read", "f32"), buf("partials", "write", "f32"),
+         buf("reach", "read", "u32")},
+        attend_params(), sizeof(S));
   }
+  add("fk_step_attend_paged", 0,
+      {buf("q", "read", "f32"), buf("knew", "read", "f32"), buf("vnew", "read", "f32"), buf("kpool", "read", "u64"),
+       buf("vpool", "read", "u64"), buf("position", "read", "u32"), buf("table", "read", "u32"),
+       buf("rope", "read", "f32"), buf("partials", "write", "f32"), buf("reach", "read", "u32")},
+      with_paging<fk_step_attend_paged_params>(attend_params()), sizeof(fk_step_attend_paged_params));
   {
     using S = fk_step_combine_params;
     add("fk_step_combine", 64, {buf("partials", "read", "f32"), buf("out", "write", "f32")},
@@ -448,10 +473,13 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({"epi_out", (uint64_t)p.rows[0] * 4});
       if (p.arg_slots) need.push_back({"arg", (uint64_t)p.arg_slots * 8});
     }
-  } else if (std::strcmp(entry, "fk_step_attend") == 0 || std::strcmp(entry, "fk_step_attend_wide") == 0) {
-    fk_step_attend_params p;
-    std::memcpy(&p, params, sizeof p);
-    const bool wide = entry[14] == '_';
+  } else if (std::strcmp(entry, "fk_step_attend") == 0 || std::strcmp(entry, "fk_step_attend_wide") == 0 ||
+             std::strcmp(entry, "fk_step_attend_paged") == 0) {
+    fk_step_attend_paged_params pp{};
+    std::memcpy(&pp, params, std::strcmp(entry, "fk_step_attend_paged") == 0 ? sizeof pp : sizeof pp.a);
+    const fk_step_attend_params &p = pp.a;
+    const bool paged = entry[14] == '_' && entry[15] == 'p';
+    const bool wide = entry[14] == '_' && entry[15] == 'w';
     // Wide splits: 64 positions a wavefront, up to 8 wavefronts, the LDS of
     // fk_attention.h's wide_lds_floats.
     const bool split_ok = wide ? (p.split % 64 == 0 && p.split == threads && threads >= 64 && threads <= 512 &&
@@ -462,13 +490,28 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
         !split_ok || p.heads / p.kv_heads > 8 || groups != p.kv_heads * p.splits)
       return bad(err, cap, FK_ERR_ARG, "%s: %u heads over %u, width %u, splits of %u, %u groups for %u splits", entry,
                  p.heads, p.kv_heads, p.head_dim, p.split, groups, p.splits);
-    const uint64_t cache = (uint64_t)p.slots * p.kv_heads * p.length * p.head_dim * 2;
-    need = {{"q", (uint64_t)p.heads * p.head_dim * 4},
-            {"kc", cache},
-            {"vc", cache},
-            {"position", 4},
-            {"slot", 4},
-            {"partials", (uint64_t)p.heads * p.splits * (p.head_dim + 2) * 4}};
+    if (paged) {
+      if (pp.g.block_size == 0 || pp.g.table_len == 0 || pp.g.blocks == 0)
+        return bad(err, cap, FK_ERR_ARG, "%s: blocks of %u positions, tables of %u of a pool of %u", entry,
+                   pp.g.block_size, pp.g.table_len, pp.g.blocks);
+      need = {{"q", (uint64_t)p.heads * p.head_dim * 4},
+              {"kpool", (uint64_t)pp.g.blocks * 8},
+              {"vpool", (uint64_t)pp.g.blocks * 8},
+              {"position", 4},
+              {"table", (uint64_t)pp.g.table_len * 4},
+              {"partials", (uint64_t)p.heads * p.splits * (p.head_dim + 2) * 4}};
+    } else {
+      const uint64_t cache = (uint64_t)p.slots * p.kv_heads * p.length * p.head_dim * 2;
+      need = {{"q", (uint64_t)p.heads * p.head_dim * 4},
+              {"kc", cache},
+              {"vc", cache},
+              {"position", 4},
+              {"slot", 4},
+              {"partials", (uint64_t)p.heads * p.splits * (p.head_dim + 2) * 4}};
+    }
+    if (p.has_reach && wide)
+      return bad(err, cap, FK_ERR_ARG, "%s: the wide splits take no reach", entry);
+    if (p.has_reach) need.push_back({"reach", 4});
     if (p.store) {
       need.push_back({"knew", (uint64_t)p.kv_heads * p.head_dim * 4});
       need.push_back({"vnew", (uint64_t)p.kv_heads * p.head_dim * 4});
@@ -479,6 +522,19 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
     std::memcpy(&p, params, sizeof p);
     need = {{"partials", (uint64_t)p.heads * p.splits * (p.head_dim + 2) * 4},
             {"out", (uint64_t)p.heads * p.head_dim * 4}};
+  } else if (std::strcmp(entry, "fk_step_store_paged") == 0) {
+    fk_step_store_paged_params pp;
+    std::memcpy(&pp, params, sizeof pp);
+    if (pp.g.block_size == 0 || pp.g.table_len == 0 || pp.g.blocks == 0 || pp.s.n_stores < 1 || pp.s.n_stores > 2)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u stores, blocks of %u positions, tables of %u of a pool of %u", entry,
+                 pp.s.n_stores, pp.g.block_size, pp.g.table_len, pp.g.blocks);
+    const uint64_t row = (uint64_t)pp.s.kv_heads * pp.s.head_dim * 4;
+    need = {{"x0", row}, {"p0", (uint64_t)pp.g.blocks * 8}, {"position", 4}, {"table", (uint64_t)pp.g.table_len * 4}};
+    if (pp.s.n_stores > 1) {
+      need.push_back({"x1", row});
+      need.push_back({"p1", (uint64_t)pp.g.blocks * 8});
+    }
+    if (pp.s.rope[0] || pp.s.rope[1]) need.push_back({"rope", (uint64_t)pp.s.rope_rows * pp.s.rotated * 8});
   } else if (std::strcmp(entry, "fk_step_store") == 0) {
     fk_step_store_params p;
     std::memcpy(&p, params, sizeof p);

@@ -19,7 +19,7 @@ __global__ void __launch_bounds__(FK_ATTN_THREADS)
               uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
               const uint32_t *__restrict__ slot, const float *__restrict__ rope, float *__restrict__ partials,
               fk_step_attend_params p) {
-  fk::step_attend(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+  fk::step_attend(q, knew, vnew, kc, vc, position, slot, rope, partials, position, p);
 }
 
 __global__ void __launch_bounds__(FK_WAVE)
@@ -31,6 +31,10 @@ __global__ void __launch_bounds__(FK_WAVE)
 // against what the kernels take (0 and a message on the context if not).
 size_t check_attend(fk_ctx *ctx, const fk_attend_args *a, const char *what) {
   const fk_step_attend_params &p = a->p;
+  if (p.has_reach) {
+    fk_fail(ctx, FK_ERR_ARG, "%s: the one-call attention takes no reach", what);
+    return 0;
+  }
   if (p.kv_heads == 0 || p.heads % p.kv_heads || p.heads / p.kv_heads > 8 || p.head_dim == 0 || p.head_dim > 64 ||
       p.head_dim % 8 || (p.split != 64 && p.split != 128) || p.length == 0 || p.slots == 0 ||
       p.splits != (p.length + p.split - 1) / p.split) {

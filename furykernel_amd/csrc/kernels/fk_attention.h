@@ -66,13 +66,35 @@ __device__ __forceinline__ float waves_max(const float *pm, uint32_t h) {
 // order from +0.  Stored as
 // partials: acc[heads][splits][head_dim], then [heads][splits][max, sum] —
 // each (head, split)'s values 16-byte aligned for a consumer's vector loads.
-template <uint32_t G, uint32_t D, uint32_t S, int CB>
+// Where the attention's cached rows live: a ring (kc, vc; `slot` the row's
+// slot) or paged pools (the blocks' addresses; `slot` the row's block table).
+struct CacheRows {
+  uint16_t *kc, *vc;
+  const uint64_t *kpool, *vpool;
+  fk_paging g;
+};
+
+// Row t of kv head g of a paged pool: block table[t / block_size] (the table
+// index and the block clamped into the table and the pool).
+__device__ __forceinline__ uint16_t *paged_row(const uint64_t *pool, const uint32_t *table, const fk_paging &pg,
+                                               uint32_t t, uint32_t g, uint32_t d) {
+  const uint32_t ti = min(t / pg.block_size, pg.table_len - 1);
+  const uint32_t b = min(table[ti], pg.blocks - 1);
+  return reinterpret_cast<uint16_t *>(pool[b]) + ((size_t)g * pg.block_size + t % pg.block_size) * d;
+}
+
+// PG: the caches are paged pools.  With a reach (p.has_reach), the positions
+// run to max(pos, reach[0]) (Graph.hs:223-247), the window's start still the
+// row's own position's.
+template <uint32_t G, uint32_t D, uint32_t S, int CB, bool PG = false>
 __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restrict__ q,
                                              const float *__restrict__ knew, const float *__restrict__ vnew,
-                                             uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
-                                             const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot,
-                                             const float *__restrict__ rope, float *__restrict__ partials,
+                                             const CacheRows &cr, const uint32_t *__restrict__ position,
+                                             const uint32_t *__restrict__ slot, const float *__restrict__ rope,
+                                             float *__restrict__ partials, const uint32_t *__restrict__ reach,
                                              const fk_step_attend_params &p) {
+  uint16_t *__restrict__ kc = cr.kc;
+  uint16_t *__restrict__ vc = cr.vc;
   constexpr uint32_t T = FK_ATTN_THREADS;
   static_assert(T == 4 * FK_ATTN_MAX_SPLIT, "four threads a position of the largest split");
   const uint32_t tid = threadIdx.x;
@@ -85,16 +107,21 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
   const uint32_t split = S ? S : p.split;
   const uint32_t half = d / 2;
   const uint32_t pos = position[0];
-  const uint32_t sraw = slot[0];
+  const uint32_t sraw = PG ? 0u : slot[0];
   const uint32_t s = sraw < p.slots ? sraw : 0;
   const bool bf16 = CB >= 0 ? CB != 0 : p.cache_bf16 != 0;
-  // Positions [first, pos], this split's part of them.
+  // Positions [first, top], this split's part of them.
   const uint32_t first = (p.window && pos + 1 > p.window) ? pos + 1 - p.window : 0;
+  const uint32_t top = p.has_reach ? max(pos, reach[0]) : pos;
   const uint32_t lo = max(first, t * split);
-  const uint32_t hi = min(pos + 1, (t + 1) * split);
+  const uint32_t hi = min(top + 1, (t + 1) * split);
   const uint32_t n = hi > lo ? hi - lo : 0;
   const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
-  const bool stores = p.store && sraw < p.slots && lo <= pos && pos < hi;
+  // A store needs its row's slot (a ring's) or block (a pool's) to exist.
+  const bool held = PG ? (pos / cr.g.block_size < cr.g.table_len &&
+                          slot[pos / cr.g.block_size] < cr.g.blocks)
+                       : sraw < p.slots;
+  const bool stores = p.store && held && lo <= pos && pos < hi;
   uint16_t *ksh = reinterpret_cast<uint16_t *>(sh.ks);
   const uint16_t *vsh = reinterpret_cast<const uint16_t *>(sh.vs);
 
@@ -130,29 +157,38 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
   const uint32_t chunks = n * per_row;
   const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
   // Ring index of row r: (lo + r) mod length, where r < n <= length.
-  const uint32_t ring0 = lo % p.length;
+  const uint32_t ring0 = PG ? 0u : lo % p.length;
   // The row the new key and value replace (none unless this split stores).
   const uint32_t srow = stores ? pos - lo : 0xFFFFFFFFu;
   // The split's keys, then its values, 16 bytes a load, non-temporal (a step
   // reads each cached row once): K is staged before the scores, V while they
   // are made.  Every load unconditional, a chunk past the split's rows
   // reading its last chunk (or the ring's row lo) and replaced by zeros.
-  size_t at2[2];
+  const uint16_t *kp2[2], *vp2[2];
   bool live2[2];
 #pragma unroll
   for (int m = 0; m < 2; m++) {
     const uint32_t e = tid + m * T;
     live2[m] = e < chunks;
     const uint32_t ec = min(e, chunks > 0 ? chunks - 1 : 0u);
-    uint32_t ring = ring0 + ec / per_row;
-    ring = ring >= p.length ? ring - p.length : ring;
-    at2[m] = (base + ring) * d + 8 * (ec % per_row);
+    if constexpr (PG) {
+      // A chunk past the split's rows reads the row of position lo.
+      const uint32_t at = lo + ec / per_row;
+      kp2[m] = paged_row(cr.kpool, slot, cr.g, at, g, d) + 8 * (ec % per_row);
+      vp2[m] = paged_row(cr.vpool, slot, cr.g, at, g, d) + 8 * (ec % per_row);
+    } else {
+      uint32_t ring = ring0 + ec / per_row;
+      ring = ring >= p.length ? ring - p.length : ring;
+      const size_t at = (base + ring) * d + 8 * (ec % per_row);
+      kp2[m] = kc + at;
+      vp2[m] = vc + at;
+    }
   }
   u32x4 kr[2], vr[2];
 #pragma unroll
-  for (int m = 0; m < 2; m++) kr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kc + at2[m]));
+  for (int m = 0; m < 2; m++) kr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kp2[m]));
 #pragma unroll
-  for (int m = 0; m < 2; m++) vr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vc + at2[m]));
+  for (int m = 0; m < 2; m++) vr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vp2[m]));
 
   // The query rows, RoPE'd as rope_elem does, and the keys into LDS; rows
   // past the positions the split holds get zeros (their weights are zero and
@@ -179,9 +215,14 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
     if (p.krope && i < p.rotated) k = j < half ? kx * kcs - kp * ksn : kx * kcs + kp * ksn;
     const uint16_t kh = narrow_cache(k, bf16);
     vh = narrow_cache(vx, bf16);
-    const size_t at = (base + pos % p.length) * d + j;
-    kc[at] = kh;
-    vc[at] = vh;
+    if constexpr (PG) {
+      paged_row(cr.kpool, slot, cr.g, pos, g, d)[j] = kh;
+      paged_row(cr.vpool, slot, cr.g, pos, g, d)[j] = vh;
+    } else {
+      const size_t at = (base + pos % p.length) * d + j;
+      kc[at] = kh;
+      vc[at] = vh;
+    }
     ksh[srow * FK_ATTN_KROW + j] = kh;
   }
   __syncthreads();
@@ -335,15 +376,36 @@ __device__ __forceinline__ void step_attend(const float *__restrict__ q, const f
                                             const float *__restrict__ vnew, uint16_t *__restrict__ kc,
                                             uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                                             const uint32_t *__restrict__ slot, const float *__restrict__ rope,
-                                            float *__restrict__ partials, const fk_step_attend_params &p) {
+                                            float *__restrict__ partials, const uint32_t *__restrict__ reach,
+                                            const fk_step_attend_params &p) {
   __shared__ AttendLds sh;
+  const CacheRows cr{kc, vc, nullptr, nullptr, {1u, 1u, 1u}};
   const uint32_t group = p.heads / p.kv_heads;
   if (group == 4 && p.head_dim == 64 && p.split == 128 && !p.cache_bf16)
-    attend_split<4, 64, 128, 0>(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+    attend_split<4, 64, 128, 0>(sh, q, knew, vnew, cr, position, slot, rope, partials, reach, p);
   else if (group == 4 && p.head_dim == 64 && p.split == 64 && !p.cache_bf16)
-    attend_split<4, 64, 64, 0>(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+    attend_split<4, 64, 64, 0>(sh, q, knew, vnew, cr, position, slot, rope, partials, reach, p);
   else
-    attend_split<0, 0, 0, -1>(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+    attend_split<0, 0, 0, -1>(sh, q, knew, vnew, cr, position, slot, rope, partials, reach, p);
+}
+
+// The attention over paged pools: kpool and vpool the blocks' addresses,
+// `table` the row's block table.
+__device__ __forceinline__ void step_attend_paged(const float *__restrict__ q, const float *__restrict__ knew,
+                                                  const float *__restrict__ vnew, const uint64_t *__restrict__ kpool,
+                                                  const uint64_t *__restrict__ vpool,
+                                                  const uint32_t *__restrict__ position,
+                                                  const uint32_t *__restrict__ table, const float *__restrict__ rope,
+                                                  float *__restrict__ partials, const uint32_t *__restrict__ reach,
+                                                  const fk_step_attend_paged_params &pp) {
+  __shared__ AttendLds sh;
+  const CacheRows cr{nullptr, nullptr, kpool, vpool, pp.g};
+  const fk_step_attend_params &p = pp.a;
+  const uint32_t group = p.heads / p.kv_heads;
+  if (group == 4 && p.head_dim == 64 && p.split == 128 && !p.cache_bf16)
+    attend_split<4, 64, 128, 0, true>(sh, q, knew, vnew, cr, position, table, rope, partials, reach, p);
+  else
+    attend_split<0, 0, 0, -1, true>(sh, q, knew, vnew, cr, position, table, rope, partials, reach, p);
 }
 }  // namespace fk
 
@@ -575,7 +637,8 @@ __device__ __forceinline__ void attend_wide(const float *__restrict__ q, const f
                                             const float *__restrict__ vnew, uint16_t *__restrict__ kc,
                                             uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                                             const uint32_t *__restrict__ slot, const float *__restrict__ rope,
-                                            float *__restrict__ partials, const fk_step_attend_params &p) {
+                                            float *__restrict__ partials, const uint32_t *__restrict__ reach,
+                                            const fk_step_attend_params &p) {
   extern __shared__ float lds[];
   const uint32_t W = blockDim.x / FK_WAVE;
   float *qs = lds;                                                  // [group][d]
@@ -602,7 +665,8 @@ __device__ __forceinline__ void attend_wide(const float *__restrict__ q, const f
   const uint32_t s = sraw < p.slots ? sraw : 0;
   const uint32_t first = (p.window && pos + 1 > p.window) ? pos + 1 - p.window : 0;
   const uint32_t lo = max(first, t * S);
-  const uint32_t hi = min(pos + 1, (t + 1) * S);
+  const uint32_t top = p.has_reach ? max(pos, reach[0]) : pos;
+  const uint32_t hi = min(top + 1, (t + 1) * S);
   const bool stores = p.store && sraw < p.slots && lo <= pos && pos < hi;
   const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
   const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
@@ -818,11 +882,12 @@ __device__ __forceinline__ void step_attend_wide(const float *__restrict__ q, co
                                                  const float *__restrict__ vnew, uint16_t *__restrict__ kc,
                                                  uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                                                  const uint32_t *__restrict__ slot, const float *__restrict__ rope,
-                                                 float *__restrict__ partials, const fk_step_attend_params &p) {
+                                                 float *__restrict__ partials, const uint32_t *__restrict__ reach,
+                                                 const fk_step_attend_params &p) {
   if (p.cache_bf16)
-    attend_wide<1>(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+    attend_wide<1>(q, knew, vnew, kc, vc, position, slot, rope, partials, reach, p);
   else
-    attend_wide<0>(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+    attend_wide<0>(q, knew, vnew, kc, vc, position, slot, rope, partials, reach, p);
 }
 
 }  // namespace fk

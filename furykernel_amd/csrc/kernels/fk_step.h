@@ -50,6 +50,34 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
   }
 }
 
+// The store into paged pools (Graph.hs:144-152): each element at
+// (h * blockSize + pos mod blockSize) * headDim in block table[pos /
+// blockSize], the block at pool[b]; nothing stored for a position past the
+// table or a block past the pool (the gate bounds both).
+extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
+    fk_step_store_paged(const float *__restrict__ x0, const float *__restrict__ x1,
+                        const uint64_t *__restrict__ p0, const uint64_t *__restrict__ p1,
+                        const uint32_t *__restrict__ position, const uint32_t *__restrict__ table,
+                        const float *__restrict__ rope, fk_step_store_paged_params pp) {
+  const fk_step_store_params &p = pp.s;
+  const uint32_t pos = position[0];
+  const uint32_t bs = pp.g.block_size;
+  if (pos / bs >= pp.g.table_len || table[pos / bs] >= pp.g.blocks) return;
+  const uint32_t width = p.kv_heads * p.head_dim;
+  const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
+  const uint32_t b = table[pos / bs];
+  for (uint32_t st = 0; st < p.n_stores; st++) {
+    const float *x = st == 0 ? x0 : x1;
+    uint16_t *c = reinterpret_cast<uint16_t *>((st == 0 ? p0 : p1)[b]);
+    for (uint32_t e = threadIdx.x; e < width; e += blockDim.x) {
+      const uint32_t h = e / p.head_dim;
+      const uint32_t i = e % p.head_dim;
+      const float v = p.rope[st] ? fk::rope_elem(x + h * p.head_dim, i, p.head_dim, p.rotated, cs) : x[e];
+      c[((size_t)h * bs + pos % bs) * p.head_dim + i] = fk::narrow_cache(v, p.cache_bf16);
+    }
+  }
+}
+
 // Attention: the split attention and the combine (fk_attention.h) -----------
 
 #include "fk_attention.h"
@@ -58,8 +86,8 @@ extern "C" __global__ void __launch_bounds__(FK_ATTN_THREADS)
     fk_step_attend(const float *__restrict__ q, const float *__restrict__ knew, const float *__restrict__ vnew,
                    uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                    const uint32_t *__restrict__ slot, const float *__restrict__ rope, float *__restrict__ partials,
-                   fk_step_attend_params p) {
-  fk::step_attend(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+                   const uint32_t *__restrict__ reach, fk_step_attend_params p) {
+  fk::step_attend(q, knew, vnew, kc, vc, position, slot, rope, partials, reach, p);
 }
 
 // The attention in wide splits (fk_attention.h): 32 positions a wavefront,
@@ -68,8 +96,19 @@ extern "C" __global__ void __launch_bounds__(FK_WAVE * FK_WIDE_MAX_WAVES)
     fk_step_attend_wide(const float *__restrict__ q, const float *__restrict__ knew, const float *__restrict__ vnew,
                         uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                         const uint32_t *__restrict__ slot, const float *__restrict__ rope,
-                        float *__restrict__ partials, fk_step_attend_params p) {
-  fk::step_attend_wide(q, knew, vnew, kc, vc, position, slot, rope, partials, p);
+                        float *__restrict__ partials, const uint32_t *__restrict__ reach,
+                        fk_step_attend_params p) {
+  fk::step_attend_wide(q, knew, vnew, kc, vc, position, slot, rope, partials, reach, p);
+}
+
+extern "C" __global__ void __launch_bounds__(FK_ATTN_THREADS)
+    fk_step_attend_paged(const float *__restrict__ q, const float *__restrict__ knew,
+                         const float *__restrict__ vnew, const uint64_t *__restrict__ kpool,
+                         const uint64_t *__restrict__ vpool, const uint32_t *__restrict__ position,
+                         const uint32_t *__restrict__ table, const float *__restrict__ rope,
+                         float *__restrict__ partials, const uint32_t *__restrict__ reach,
+                         fk_step_attend_paged_params p) {
+  fk::step_attend_paged(q, knew, vnew, kpool, vpool, position, table, rope, partials, reach, p);
 }
 
 extern "C" __global__ void __launch_bounds__(FK_WAVE)

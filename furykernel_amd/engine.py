@@ -25,6 +25,8 @@ _STRUCTS = {
     "fk_step_store": K.StepStoreParams,
     "fk_step_attend": K.StepAttendParams,
     "fk_step_attend_wide": K.StepAttendParams,
+    "fk_step_attend_paged": K.StepAttendPagedParams,
+    "fk_step_store_paged": K.StepStorePagedParams,
     "fk_step_combine": K.StepCombineParams,
     "fk_step_argmax": K.CountParams,
     "fk_step_act_mul": K.ActMulParams,
@@ -54,18 +56,26 @@ def widen(wtype: str, w) -> np.ndarray:
 
 
 def params_struct(launch: Launch) -> ctypes.Structure:
+    """The launch's parameter struct from its flat parameters (a paged
+    entry's paging fields go to its ``g``, the rest to its inner struct)."""
     cls = K.StepGemvParams if launch.entry.startswith("fk_step_gemv") else _STRUCTS[launch.entry]
     s = cls()
+    names = [f[0] for f in cls._fields_]
+    inner = None
+    if "g" in names:
+        inner = getattr(s, names[0])
+    paging = {f[0] for f in K.Paging._fields_}
     for name, value in launch.params.items():
-        field = getattr(cls, name, None)
+        target = s if inner is None else (s.g if name in paging else inner)
+        field = getattr(type(target), name, None)
         if field is None:
             raise K.LaunchError(f"{launch.entry}: no parameter {name}")
         if isinstance(value, (list, tuple)):
-            arr = getattr(s, name)
+            arr = getattr(target, name)
             for i, v in enumerate(value):
                 arr[i] = v
         else:
-            setattr(s, name, value)
+            setattr(target, name, value)
     return s
 
 
@@ -100,10 +110,15 @@ def _attend_needs(launch: Launch) -> dict:
     p = launch.params
     d, kv, heads = p["head_dim"], p["kv_heads"], p["heads"]
     cache = "bf16" if p["cache_bf16"] else "f16"
-    return {"q": (heads * d * 4, "f32"), "knew": (kv * d * 4, "f32"), "vnew": (kv * d * 4, "f32"),
-            "kc": (p["slots"] * kv * p["length"] * d * 2, cache), "vc": (p["slots"] * kv * p["length"] * d * 2, cache),
-            "position": (4, "u32"), "slot": (4, "u32"), "rope": (p["rope_rows"] * p["rotated"] * 8, "f32"),
-            "partials": (heads * p["splits"] * (d + 2) * 4, "f32")}
+    out = {"q": (heads * d * 4, "f32"), "knew": (kv * d * 4, "f32"), "vnew": (kv * d * 4, "f32"),
+           "position": (4, "u32"), "rope": (p["rope_rows"] * p["rotated"] * 8, "f32"),
+           "partials": (heads * p["splits"] * (d + 2) * 4, "f32"), "reach": (4, "u32")}
+    if launch.entry == "fk_step_attend_paged":
+        out.update(kpool=(p["blocks"] * 8, "u64"), vpool=(p["blocks"] * 8, "u64"), table=(p["table_len"] * 4, "u32"))
+    else:
+        out.update(kc=(p["slots"] * kv * p["length"] * d * 2, cache), vc=(p["slots"] * kv * p["length"] * d * 2, cache),
+                   slot=(4, "u32"))
+    return out
 
 
 def check_launch(launch: Launch, specs: dict) -> None:
@@ -143,7 +158,7 @@ def check_launch(launch: Launch, specs: dict) -> None:
     if unbound:
         raise K.LaunchError(f"{e}: reads or writes {unbound}, which the launch leaves unbound")
     needs = _gemv_needs(launch) if e.startswith("fk_step_gemv") else \
-        _attend_needs(launch) if e in ("fk_step_attend", "fk_step_attend_wide") else {}
+        _attend_needs(launch) if e in ("fk_step_attend", "fk_step_attend_wide", "fk_step_attend_paged") else {}
     for b in sorted(reads & set(needs)):
         spec = specs[launch.bind[b]]
         nbytes, dtype = needs[b]
@@ -174,6 +189,10 @@ class Engine:
                 self.zero(name)
             elif what[0] == "ones":
                 self.write(name, np.ones(specs[name].count, np.float32))
+            elif what[0] == "addresses":
+                # a paged pool's blocks, in order in its buffer
+                pool, block_bytes = self.buffers[what[1]], what[2]
+                self.write(name, pool.ptr + block_bytes * np.arange(specs[name].count, dtype=np.uint64))
             else:
                 raise ValueError(f"{name}: no constant {what[0]}")
         # The step's launches in a native launch table: each checked once

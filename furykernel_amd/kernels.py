@@ -172,7 +172,22 @@ class StepAttendParams(ctypes.Structure):
         ("cache_bf16", ctypes.c_uint32),
         ("store", ctypes.c_uint32),
         ("krope", ctypes.c_uint32),
+        ("has_reach", ctypes.c_uint32),
     ]
+
+
+class Paging(ctypes.Structure):
+    """``fk_paging``: a paged pool's blocks of block_size positions, a row's
+    table of table_len blocks, the pool's `blocks`."""
+    _fields_ = [("block_size", ctypes.c_uint32), ("table_len", ctypes.c_uint32), ("blocks", ctypes.c_uint32)]
+
+
+class StepAttendPagedParams(ctypes.Structure):
+    _fields_ = [("a", StepAttendParams), ("g", Paging)]
+
+
+class StepStorePagedParams(ctypes.Structure):
+    _fields_ = [("s", StepStoreParams), ("g", Paging)]
 
 
 class AttendArgs(ctypes.Structure):
@@ -275,10 +290,15 @@ ABIS: dict[str, KernelAbi] = {
     "fk_prefill_softcap": KernelAbi("fk_prefill_softcap", ("x", "y"), PrefillSoftcapParams, 256),
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
+    "fk_step_store_paged": KernelAbi("fk_step_store_paged", ("x0", "x1", "p0", "p1", "position", "table", "rope"),
+                                     StepStorePagedParams),
     "fk_step_attend": KernelAbi("fk_step_attend", ("q", "knew", "vnew", "kc", "vc", "position", "slot", "rope",
-                                                   "partials"), StepAttendParams),
+                                                   "partials", "reach"), StepAttendParams),
     "fk_step_attend_wide": KernelAbi("fk_step_attend_wide", ("q", "knew", "vnew", "kc", "vc", "position", "slot",
-                                                             "rope", "partials"), StepAttendParams),
+                                                             "rope", "partials", "reach"), StepAttendParams),
+    "fk_step_attend_paged": KernelAbi("fk_step_attend_paged", ("q", "knew", "vnew", "kpool", "vpool", "position",
+                                                               "table", "rope", "partials", "reach"),
+                                      StepAttendPagedParams),
     "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams, 64),
     "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
     "fk_step_act_mul": KernelAbi("fk_step_act_mul", ("a", "b", "y"), ActMulParams),
@@ -558,11 +578,21 @@ def launch_reads(entry: str, params: dict) -> set[str]:
     if entry.startswith("fk_step_gemv"):
         _, _, _, _, pro, epi = gemv_entry(entry)
         return gemv_reads(pro, epi, params["n_anchors"], bool(params.get("store_tile", 0)), params.get("arg_slots", 0))
-    if entry in ("fk_step_attend", "fk_step_attend_wide"):
-        need = {"q", "kc", "vc", "position", "slot", "partials"}
+    if entry in ("fk_step_attend", "fk_step_attend_wide", "fk_step_attend_paged"):
+        paged = entry == "fk_step_attend_paged"
+        need = {"q", "position", "partials"} | ({"kpool", "vpool", "table"} if paged else {"kc", "vc", "slot"})
         if params.get("store"):
             need |= {"knew", "vnew"}
         if params.get("rope") or params.get("krope"):
+            need.add("rope")
+        if params.get("has_reach"):
+            need.add("reach")
+        return need
+    if entry == "fk_step_store_paged":
+        need = {"x0", "p0", "position", "table"}
+        if params.get("n_stores", 1) > 1:
+            need |= {"x1", "p1"}
+        if any(params.get("rope", (0, 0))):
             need.add("rope")
         return need
     if entry == "fk_step_store":

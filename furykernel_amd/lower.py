@@ -22,7 +22,7 @@ import numpy as np
 from .program.check import CheckedProgram
 from .program.graph import (
     BF16, CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, Gather, GatedGelu, GeluMul, Input, KvStore,
-    Linear, Ring, RmsNorm, Rope, ROPE_HALVES, SCache, SInput, Softcap, SRowInts, SWeight)
+    Linear, Paged, Ring, RmsNorm, Rope, ROPE_HALVES, SCache, SInput, Softcap, SRowInts, SWeight)
 from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
 
 THREADS = 256
@@ -167,8 +167,8 @@ def _fuse_attention(out: Lowered) -> None:
     for launch in out.launches:
         prev = fused[-1] if fused else None
         merged = None
-        if prev is not None and launch.entry in ("fk_step_attend", "fk_step_attend_wide") and \
-                prev.entry == "fk_step_store":
+        if prev is not None and launch.entry in ("fk_step_attend", "fk_step_attend_wide", "fk_step_attend_paged") \
+                and prev.entry in ("fk_step_store", "fk_step_store_paged"):
             merged = _store_into_attend(prev, launch)
         if merged is not None:
             fused[-1] = merged
@@ -179,14 +179,19 @@ def _fuse_attention(out: Lowered) -> None:
 
 def _store_into_attend(st: Launch, at: Launch) -> Optional[Launch]:
     sp, ap, sb, ab = st.params, at.params, st.bind, at.bind
-    if sp["n_stores"] != 2 or ap["store"] or sb["position"] != ab["position"] or sb["slot"] != ab["slot"]:
+    paged = at.entry == "fk_step_attend_paged"
+    if paged != (st.entry == "fk_step_store_paged"):
         return None
-    if (sp["kv_heads"], sp["head_dim"], sp["length"], sp["slots"], sp["cache_bf16"]) != (
-            ap["kv_heads"], ap["head_dim"], ap["length"], ap["slots"], ap["cache_bf16"]):
+    seq, c0, c1, kc, vc = ("table", "p0", "p1", "kpool", "vpool") if paged else ("slot", "c0", "c1", "kc", "vc")
+    if sp["n_stores"] != 2 or ap["store"] or sb["position"] != ab["position"] or sb[seq] != ab[seq]:
         return None
-    if (sb["c0"], sb["c1"]) == (ab["kc"], ab["vc"]):
+    shape = ("kv_heads", "head_dim", "cache_bf16") + (("block_size", "table_len", "blocks") if paged
+                                                      else ("length", "slots"))
+    if any(sp[f] != ap[f] for f in shape):
+        return None
+    if (sb[c0], sb[c1]) == (ab[kc], ab[vc]):
         kj, vj = 0, 1
-    elif (sb["c1"], sb["c0"]) == (ab["kc"], ab["vc"]):
+    elif (sb[c1], sb[c0]) == (ab[kc], ab[vc]):
         kj, vj = 1, 0
     else:
         return None
@@ -374,16 +379,30 @@ class _StepLowering:
             raise LoweringError(f"{src.name} is not a row of integers")
         return self.out.buffer(f"ints:{src.name}", "u32", src.kind.count * self.out.rows)
 
-    def cache(self, s: int) -> tuple[str, Ring, bool]:
+    def cache(self, s: int) -> tuple[str, object, bool]:
+        """A ring's buffer; for a paged pool, the address table of its blocks
+        (u64, one a block), whose buffer ``cache:<name>`` holds the blocks in
+        order and whose addresses the engine writes (the constant
+        ("addresses", pool, block bytes))."""
         src = self.p.source(s)
         if not isinstance(src.kind, SCache):
             raise LoweringError(f"{src.name} is not a cache")
         lay = src.kind.layout
-        if not isinstance(lay, Ring):
-            raise LoweringError(f"cache {src.name}: paged caches are not lowered yet")
-        count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
         bf16 = src.kind.elem == CACHE_BF16
-        return self.out.buffer(f"cache:{src.name}", "bf16" if bf16 else "f16", count), lay, bf16
+        elem = "bf16" if bf16 else "f16"
+        if isinstance(lay, Paged):
+            block = lay.block_size * lay.kv_heads * lay.head_dim
+            pool = self.out.buffer(f"cache:{src.name}", elem, lay.blocks * block)
+            addr = self.out.buffer(f"addr:{src.name}", "u64", lay.blocks)
+            self.out.constants[addr] = ("addresses", pool, block * 2)
+            return addr, lay, bf16
+        count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
+        return self.out.buffer(f"cache:{src.name}", elem, count), lay, bf16
+
+    def paging(self, lay, table: int) -> dict:
+        """A paged pool's paging fields, the row's table of the source `table`."""
+        src = self.p.source(table)
+        return {"block_size": lay.block_size, "table_len": src.kind.count, "blocks": lay.blocks}
 
     def rope(self, spec, d: int, rows: int) -> str:
         name = f"rope:{spec.theta!r}:{d}:{spec.rotated}:{rows}"
@@ -607,19 +626,26 @@ class _StepLowering:
         effects = [self.p.node(w.node) for w in step.work if w.kind == EFFECT]
         if not 1 <= len(effects) <= 2 or not all(isinstance(e.op, KvStore) for e in effects):
             raise LoweringError(f"{step.name}: effects other than one or two KV stores")
-        bind = {"x0": None, "x1": None, "c0": None, "c1": None, "position": None, "slot": None, "rope": None}
+        paged = isinstance(self.p.source(effects[0].op.at.cache).kind.layout, Paged)
+        c, seq = ("p", "table") if paged else ("c", "slot")
+        bind = {"x0": None, "x1": None, f"{c}0": None, f"{c}1": None, "position": None, seq: None, "rope": None}
         params: dict = {"n_stores": len(effects), "rope": [0, 0], "rotated": 0, "rope_rows": 1}
         meta: dict = {"theta": 1.0}
         layouts, used = set(), set()
         for j, e in enumerate(effects):
             at = e.op.at
             cname, lay, bf16 = self.cache(at.cache)
-            layouts.add((lay.kv_heads, lay.head_dim, lay.length, lay.slots, bf16))
-            bind[f"c{j}"] = cname
+            if isinstance(lay, Paged) != paged:
+                raise LoweringError(f"{step.name}: stores into a ring and a paged pool")
+            layouts.add((lay.kv_heads, lay.head_dim, bf16) + ((lay.block_size, lay.blocks) if paged
+                                                              else (lay.length, lay.slots)))
+            bind[f"{c}{j}"] = cname
             pos, slot = self.ints(at.positions), self.ints(at.sequences)
-            if bind["position"] not in (None, pos) or bind["slot"] not in (None, slot):
+            if bind["position"] not in (None, pos) or bind[seq] not in (None, slot):
                 raise LoweringError(f"{step.name}: stores at different positions or sequences")
-            bind["position"], bind["slot"] = pos, slot
+            bind["position"], bind[seq] = pos, slot
+            if paged:
+                params.update(self.paging(lay, at.sequences))
             v = e.op.x
             if v in rec:
                 inner = self.rope_of(step, rec[v], rec)
@@ -647,28 +673,33 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: recomputes no store kernel takes")
         if step.stores:
             raise LoweringError(f"{step.name}: a store step that also stores values")
-        kv, d, length, slots, bf16 = layouts.pop()
-        params.update(kv_heads=kv, head_dim=d, length=length, slots=slots, cache_bf16=int(bf16))
+        kv, d, bf16, a, b = layouts.pop()
+        params.update(kv_heads=kv, head_dim=d, cache_bf16=int(bf16), length=0 if paged else a,
+                      slots=0 if paged else b)
         if bind["rope"] is None:
             bind["rope"] = bind["position"]  # bound but never read
-        return Launch(step.name, "fk_step_store", 1, THREADS, bind, params, meta)
+        return Launch(step.name, "fk_step_store_paged" if paged else "fk_step_store", 1, THREADS, bind, params, meta)
 
     def attend_step(self, step: Step, anchor) -> Launch:
         op = anchor.op
         spec = op.spec
         rec = self.recomputes(step)
-        if spec.reach is not None:
-            raise LoweringError(f"{step.name}: attention with a reach is not lowered yet")
         if spec.head_dim > 64 or spec.heads // spec.kv_heads > 8:
             raise LoweringError(f"{step.name}: heads of {spec.head_dim} or groups of {spec.heads // spec.kv_heads}")
         kname, lay, bf16 = self.cache(op.to.keys)
         vname, vlay, _ = self.cache(op.to.values)
         if spec.head_dim % 8:
             raise LoweringError(f"{step.name}: heads of {spec.head_dim}, not a multiple of 8")
-        params = {"heads": spec.heads, "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "length": lay.length,
-                  "slots": lay.slots, "split": ATTN_SPLIT, "rope": 0, "rotated": 0, "rope_rows": 1,
-                  "scale": float(np.float32(spec.scale)), "window": spec.window or 0, "cache_bf16": int(bf16),
-                  "store": 0, "krope": 0}
+        paged = isinstance(lay, Paged)
+        if paged != isinstance(vlay, Paged):
+            raise LoweringError(f"{step.name}: keys and values of a ring and a paged pool")
+        span = lay.block_size * self.p.source(op.to.sequences).kind.count if paged else lay.length
+        params = {"heads": spec.heads, "kv_heads": spec.kv_heads, "head_dim": spec.head_dim, "length": span,
+                  "slots": 0 if paged else lay.slots, "split": ATTN_SPLIT, "rope": 0, "rotated": 0,
+                  "rope_rows": 1, "scale": float(np.float32(spec.scale)), "window": spec.window or 0,
+                  "cache_bf16": int(bf16), "store": 0, "krope": 0, "has_reach": int(spec.reach is not None)}
+        if paged:
+            params.update(self.paging(lay, op.to.sequences))
         meta = {"theta": 1.0}
         rope_buf = None
         q = op.q
@@ -690,11 +721,15 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: queries neither stored nor recomputed")
         if ATTN_SPLIT not in (64, 128):
             raise LoweringError(f"{step.name}: attention splits of {ATTN_SPLIT} positions; the kernel takes 64 or 128")
+        # The positions a row may read: below the bound of its positions, or
+        # of its reach; a ring without a window holds no more than its length.
         bound = self.p.source(op.to.positions).kind.bound
-        positions = min(bound, lay.length if spec.window is None else bound)
-        entry, threads, lds = "fk_step_attend", ATTN_THREADS, 0
+        if spec.reach is not None:
+            bound = max(bound, self.p.source(spec.reach.source).kind.bound)
+        positions = min(bound, span if spec.window is None else bound)
+        entry, threads, lds = ("fk_step_attend_paged" if paged else "fk_step_attend"), ATTN_THREADS, 0
         split = ATTN_SPLIT
-        if self.wide and spec.head_dim in (16, 32, 64):
+        if self.wide and not paged and spec.reach is None and spec.head_dim in (16, 32, 64):
             # Wide splits: 64 positions a wavefront, up to 8 wavefronts, so
             # that a head has at most 8 splits (the combine prologue's) up to
             # 4096 positions.
@@ -709,8 +744,12 @@ class _StepLowering:
         pname = self.out.buffer(f"partials:{self.p.value(out).name}", "f32",
                                 spec.heads * splits * (spec.head_dim + 2))
         pos_buf = self.ints(op.to.positions)
-        bind = {"q": qbuf, "knew": None, "vnew": None, "kc": kname, "vc": vname, "position": pos_buf,
-                "slot": self.ints(op.to.sequences), "rope": rope_buf or pos_buf, "partials": pname}
+        bind = {"q": qbuf, "knew": None, "vnew": None, "position": pos_buf, "rope": rope_buf or pos_buf,
+                "partials": pname, "reach": None if spec.reach is None else self.ints(spec.reach.source)}
+        if paged:
+            bind.update(kpool=kname, vpool=vname, table=self.ints(op.to.sequences))
+        else:
+            bind.update(kc=kname, vc=vname, slot=self.ints(op.to.sequences))
         return Launch(step.name, entry, spec.kv_heads * splits, threads, bind, params, meta, lds)
 
     def combine_step(self, step: Step) -> Launch:

@@ -14,8 +14,12 @@
  *   fk_step_token        arg out token position       fk_step_token_params
  *   fk_step_store        x0 x1 c0 c1 position slot rope
  *                                                      fk_step_store_params
- *   fk_step_attend       q knew vnew kc vc position slot rope partials
+ *   fk_step_attend       q knew vnew kc vc position slot rope partials reach
  *                                                      fk_step_attend_params
+ *   fk_step_attend_paged q knew vnew kpool vpool position table rope partials reach
+ *                                                      fk_step_attend_paged_params
+ *   fk_step_store_paged  x0 x1 p0 p1 position table rope
+ *                                                      fk_step_store_paged_params
  *   fk_step_combine      partials out                 fk_step_combine_params
  *   fk_gemm_f16_<store|add|silu_mul>  a b0 b1 b2 c0 c1 c2 r0   fk_gemm_params
  *   fk_gemm_f16_qkv_rope a b0 b1 b2 c0 c1 c2 r0 position slot rope
@@ -124,7 +128,34 @@ typedef struct fk_step_attend_params {
   uint32_t cache_bf16;
   uint32_t store;    /* the new key and value rows are stored into the caches first */
   uint32_t krope;    /* the stored key row is RoPE'd first (q's table) */
+  uint32_t has_reach; /* positions up to max(position, reach[0]) (Graph.hs:223-247); else up to position */
 } fk_step_attend_params;
+
+/* A paged pool (Graph.hs:144-152): blocks of block_size positions, each an
+ * array of its own at the address pool[b] (an array of the blocks' device
+ * addresses); position t, kv head h of a row at (h block_size + t mod
+ * block_size) head_dim in block table[t / block_size] of the row's block
+ * table.  A table index past table_len or a block past `blocks` is clamped
+ * into them (the gate keeps a valid program's inside). */
+typedef struct fk_paging {
+  uint32_t block_size;
+  uint32_t table_len;  /* blocks a row's table lists */
+  uint32_t blocks;     /* the pool's blocks */
+} fk_paging;
+
+/* fk_step_attend_paged: the attention over paged pools (`a.length` the
+ * positions the table covers, table_len block_size; `a.slots` unused). */
+typedef struct fk_step_attend_paged_params {
+  fk_step_attend_params a;
+  fk_paging g;
+} fk_step_attend_paged_params;
+
+/* fk_step_store_paged: the KV store into paged pools (`s.length` and
+ * `s.slots` unused). */
+typedef struct fk_step_store_paged_params {
+  fk_step_store_params s;
+  fk_paging g;
+} fk_step_store_paged_params;
 
 typedef struct fk_step_combine_params {
   uint32_t heads;

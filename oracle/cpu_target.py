@@ -43,6 +43,18 @@ class CpuTarget:
     def _p(self, name):
         return None if name is None else self.buffers[name].ctypes.data
 
+    def _pool(self, addr: str):
+        """A paged pool's blocks as this target holds them: an array of the
+        blocks' host addresses, in order in the pool's buffer (the device's
+        address table, which the engine writes, read here as that)."""
+        kind, pool, block_bytes = self.lowered.constants[addr]
+        base = self.buffers[pool].ctypes.data
+        n = self.lowered.buffers[addr].count
+        return (ctypes.c_void_p * n)(*[base + i * block_bytes for i in range(n)])
+
+    def _reach(self, b, p, pos: int) -> int:
+        return int(self.buffers[b["reach"]][0]) if p.get("has_reach") else pos
+
     def run(self) -> None:
         for launch in self.lowered.launches:
             self.run_launch(launch)
@@ -131,10 +143,31 @@ class CpuTarget:
                 st = L.fkref_step_store(self._p(b["knew"]), self._p(b["vnew"]), self._p(b["kc"]), self._p(b["vc"]),
                                         2, p["krope"], 0, p["kv_heads"], p["head_dim"], p["length"], p["slots"],
                                         p["rotated"], launch.meta["store_theta"], pos, slot, p["cache_bf16"])
-            st = st or L.fkref_step_attend(self._p(b["q"]), self._p(b["kc"]), self._p(b["vc"]),
-                                           self._p(b["partials"]), p["heads"], p["kv_heads"], p["head_dim"],
-                                           p["length"], p["slots"], p["splits"], p["split"], p["rope"], p["rotated"],
-                                           launch.meta["theta"], p["scale"], p["window"], pos, slot, p["cache_bf16"])
+            st = st or L.fkref_step_attend_reach(self._p(b["q"]), self._p(b["kc"]), self._p(b["vc"]),
+                                                 self._p(b["partials"]), p["heads"], p["kv_heads"], p["head_dim"],
+                                                 p["length"], p["slots"], p["splits"], p["split"], p["rope"],
+                                                 p["rotated"], launch.meta["theta"], p["scale"], p["window"], pos,
+                                                 slot, self._reach(b, p, pos), p["cache_bf16"])
+        elif e == "fk_step_attend_paged":
+            pos = int(self.buffers[b["position"]][0])
+            kp, vp = self._pool(b["kpool"]), self._pool(b["vpool"])
+            st = 0
+            if p["store"]:
+                st = L.fkref_step_store_paged(self._p(b["knew"]), self._p(b["vnew"]), kp, vp, 2, p["krope"], 0,
+                                              p["kv_heads"], p["head_dim"], p["block_size"], self._p(b["table"]),
+                                              p["table_len"], p["blocks"], p["rotated"], launch.meta["store_theta"],
+                                              pos, p["cache_bf16"])
+            st = st or L.fkref_step_attend_paged(self._p(b["q"]), kp, vp, self._p(b["partials"]), p["heads"],
+                                                 p["kv_heads"], p["head_dim"], p["block_size"], self._p(b["table"]),
+                                                 p["table_len"], p["blocks"], p["splits"], p["split"], p["rope"],
+                                                 p["rotated"], launch.meta["theta"], p["scale"], p["window"], pos,
+                                                 self._reach(b, p, pos), p["cache_bf16"])
+        elif e == "fk_step_store_paged":
+            pools = [self._pool(b["p0"]), self._pool(b["p1"]) if b["p1"] else None]
+            st = L.fkref_step_store_paged(self._p(b["x0"]), self._p(b["x1"]), pools[0], pools[1], p["n_stores"],
+                                          p["rope"][0], p["rope"][1], p["kv_heads"], p["head_dim"], p["block_size"],
+                                          self._p(b["table"]), p["table_len"], p["blocks"], p["rotated"],
+                                          launch.meta["theta"], int(self.buffers[b["position"]][0]), p["cache_bf16"])
         elif e == "fk_step_attend_wide":
             pos, slot = int(self.buffers[b["position"]][0]), int(self.buffers[b["slot"]][0])
             st = 0

@@ -134,6 +134,10 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
     env: dict = {}
     caches = {name: {u: np.array(xs, np.float64) for u, xs in units.items()} for name, units in b.caches.items()}
     stored: set = set()
+    # Each cache a step stores into: its units before the step, and each
+    # element's stores in row order, (row, position, value) (Eval.hs:415-473).
+    before: dict = {}
+    row_stores: dict = {}
 
     def weight(s: int) -> np.ndarray:
         src = sources[s]
@@ -159,10 +163,18 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
         return [[int(i) for i in row] for row in rows]
 
     def cache_index(layout, seqs: list, position: int, h: int) -> tuple[int, int]:
-        if not isinstance(layout, Ring):
-            raise EvalError("paged caches are not evaluated here")
-        s = seqs[0] if seqs else 0
-        return s, (h * layout.length + position % layout.length) * layout.head_dim
+        """Eval.hs:592-602: where head h of a position starts, its slot (a
+        ring's) or its block (a paged pool's, through the block table)."""
+        if isinstance(layout, Ring):
+            s = seqs[0] if seqs else 0
+            return s, (h * layout.length + position % layout.length) * layout.head_dim
+        bs = layout.block_size
+        if position // bs >= len(seqs):
+            raise EvalError(f"Position {position} is past the block table.")
+        return seqs[position // bs], (h * bs + position % bs) * layout.head_dim
+
+    def unit_name(layout) -> str:
+        return "slot" if isinstance(layout, Ring) else "block"
 
     for n in p.nodes:
         op = n.op
@@ -232,6 +244,8 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
             if src.name in stored:
                 raise EvalError(f"{n.name} stores into {src.name} again: a program stores into a cache once.")
             stored.add(src.name)
+            before[src.name] = {u: a.copy() for u, a in caches.get(src.name, {}).items()}
+            row_stores[src.name] = elem_stores = {}
             lay, elem = src.kind.layout, src.kind.elem
             units = caches.get(src.name)
             if units is None:
@@ -244,7 +258,8 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
                 for h in range(heads):
                     u, at = cache_index(lay, sq, pos[0], h)
                     if u not in units:
-                        raise EvalError(f"{src.name} binds no slot {u}.")
+                        raise EvalError(f"A store to {src.name} at {unit_name(lay)} {u}, element {at}, which "
+                                        "isn't bound.")
                     for i in range(d):
                         if staged is not None:
                             v = float(staged[r][h * d + i])
@@ -253,20 +268,55 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
                         else:
                             v = round_cache(elem, float(x[h * d + i]))
                         units[u][at + i] = v
+                        elem_stores.setdefault((u, at + i), []).append((r, pos[0], v))
         elif isinstance(op, Attend):
             spec = op.spec
             ksrc, vsrc = sources[op.to.keys], sources[op.to.values]
             lay = ksrc.kind.layout
-            if spec.reach is not None:
-                raise EvalError("attention with a reach is not evaluated here")
             ps, seqs = ints(op.to.positions), ints(op.to.sequences)
+            reaches = ps if spec.reach is None else ints(spec.reach.source)
+            if spec.reach is not None:
+                for i, (pos, rc) in enumerate(zip(ps, reaches)):
+                    if rc[0] > pos[0] + spec.reach.ahead:
+                        raise EvalError(f"{n.name}: row {i} reaches {rc[0]}, more than {spec.reach.ahead} past its "
+                                        f"position, {pos[0]}.")
             d, heads = spec.head_dim, spec.heads
             group = heads // spec.kv_heads
+
+            def read(name, u, at, r0, r, t):
+                """Eval.hs:563-576: row r0 reads position t as the row r that
+                stored its reach does: a store of t by a row after r0 up to
+                r, else the last store of rows up to r0 into the element (of
+                position t, or the read is refused), else the cache before
+                the step."""
+                units = before.get(name, caches.get(name, {}))
+                if u not in units or at + d > len(units[u]):
+                    raise EvalError(f"{name}: {unit_name(lay)} {u}, element {at}, isn't bound.")
+                elems = row_stores.get(name)
+                if elems is None:
+                    return units[u][at:at + d]
+                out = np.empty(d)
+                for i in range(d):
+                    st = elems.get((u, at + i), [])
+                    ahead = [v for j, t2, v in reversed(st) if r0 < j <= r and t2 == t]
+                    mine = [(t2, v) for j, t2, v in st if j <= r0]
+                    if ahead:
+                        out[i] = ahead[0]
+                    elif mine:
+                        if mine[-1][0] != t:
+                            raise EvalError(f"{name}: row {r0} reads position {t} where a row stored {mine[-1][0]}.")
+                        out[i] = mine[-1][1]
+                    else:
+                        out[i] = units[u][at + i]
+                return out
+
             res = []
-            for pos, sq, q in zip(ps, seqs, env[op.q]):
+            for r0, (pos, rc, sq, q) in enumerate(zip(ps, reaches, seqs, env[op.q])):
                 position = pos[0]
+                # the row that stored this row's reach, if one of the step's did
+                r = next((j for j in range(r0, len(ps)) if ps[j][0] == rc[0] and seqs[j] == sq), r0)
                 first = max(0, position - spec.window + 1) if spec.window else 0
-                ts = range(first, position + 1)
+                ts = range(first, max(position, rc[0]) + 1)
                 row = []
                 for h in range(heads):
                     kvh = h // group
@@ -274,8 +324,8 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
                     keys, vals = [], []
                     for t in ts:
                         u, at = cache_index(lay, sq, t, kvh)
-                        keys.append(caches[ksrc.name][u][at:at + d])
-                        vals.append(caches[vsrc.name][u][at:at + d])
+                        keys.append(read(ksrc.name, u, at, r0, r, t))
+                        vals.append(read(vsrc.name, u, at, r0, r, t))
                     scores = [spec.scale * hsum(query * kk) for kk in keys]
                     top = max(scores)
                     es = [math.exp(s - top) for s in scores]
@@ -379,6 +429,8 @@ def evaluate_fast(checked: CheckedProgram, b: Bindings) -> Evaluation:
         elif isinstance(op, KvStore):
             src = sources[op.at.cache]
             lay, elem = src.kind.layout, src.kind.elem
+            if not isinstance(lay, Ring):
+                raise EvalError("the fast evaluation takes ring caches; evaluate paged ones with evaluate")
             pos, seq = ints(op.at.positions)[:, 0], ints(op.at.sequences)[:, 0]
             d, heads = lay.head_dim, lay.kv_heads
             x = env[op.x].reshape(m, heads, d)
@@ -390,6 +442,8 @@ def evaluate_fast(checked: CheckedProgram, b: Bindings) -> Evaluation:
         elif isinstance(op, Attend):
             spec = op.spec
             lay = sources[op.to.keys].kind.layout
+            if not isinstance(lay, Ring) or spec.reach is not None:
+                raise EvalError("the fast evaluation takes ring caches and no reach; evaluate others with evaluate")
             pos, seq = ints(op.to.positions)[:, 0], ints(op.to.sequences)[:, 0]
             d, heads, kvh = spec.head_dim, spec.heads, spec.kv_heads
             group = heads // kvh

@@ -459,24 +459,79 @@ static uint16_t narrow_cache(float v, int bf16) { return bf16 ? fkref_narrow_bf1
 
 static float widen_cache(uint16_t h, int bf16) { return bf16 ? fkref_widen_bf16(h) : fkref_widen_f16(h); }
 
-int fkref_step_store(const float *x0, const float *x1, uint16_t *c0, uint16_t *c1, int n_stores, int rope0,
-                     int rope1, int kv_heads, int head_dim, int length, int slots, int rotated, float theta,
-                     uint32_t position, uint32_t slot, int cache_bf16) {
-  if (slot >= (uint32_t)slots) return 0;
-  const int width = kv_heads * head_dim;
+/* Where a cached row (position t, kv head h) starts.  A ring (Graph.hs:
+ * 138-143): slot s's ring of `length` positions, ((s kvHeads + h) length + t
+ * mod length) headDim.  A paged pool (Graph.hs:144-152): block table[t /
+ * blockSize] of the row's block table, (h blockSize + t mod blockSize)
+ * headDim within it, the blocks anywhere (an array of their addresses).
+ * Indexes past the table or the pool are clamped into them, as the kernels
+ * clamp them (the gate keeps a valid program's inside). */
+typedef struct {
+  int paged;
+  int kv_heads, head_dim;
+  int length; uint32_t slot;                                  /* a ring */
+  int block_size, table_len, blocks; const uint32_t *table;   /* a pool */
+} fkref_rows;
+
+static size_t row_index(const fkref_rows *L, uint32_t t, int h, uint32_t *block) {
+  if (!L->paged) {
+    *block = 0;
+    return (((size_t)L->slot * L->kv_heads + h) * L->length + t % (uint32_t)L->length) * L->head_dim;
+  }
+  uint32_t ti = t / (uint32_t)L->block_size;
+  if (ti >= (uint32_t)L->table_len) ti = (uint32_t)L->table_len - 1;
+  uint32_t b = L->table[ti];
+  *block = b < (uint32_t)L->blocks ? b : (uint32_t)L->blocks - 1;
+  return ((size_t)h * L->block_size + t % (uint32_t)L->block_size) * L->head_dim;
+}
+
+/* A cache's row: `cache` for a ring, `pool[block]` for a paged pool. */
+static uint16_t *row_of(const fkref_rows *L, uint16_t *cache, uint16_t *const *pool, uint32_t t, int h) {
+  uint32_t b;
+  size_t at = row_index(L, t, h, &b);
+  return (L->paged ? pool[b] : cache) + at;
+}
+
+static int store_rows(const fkref_rows *L, const float *x0, const float *x1, uint16_t *c0, uint16_t *c1,
+                      uint16_t *const *p0, uint16_t *const *p1, int n_stores, int rope0, int rope1, int rotated,
+                      float theta, uint32_t position, int cache_bf16) {
+  const int head_dim = L->head_dim;
+  const int width = L->kv_heads * head_dim;
   for (int st = 0; st < n_stores; st++) {
     const float *x = st == 0 ? x0 : x1;
-    uint16_t *c = st == 0 ? c0 : c1;
     int rope = st == 0 ? rope0 : rope1;
     for (int e = 0; e < width; e++) {
       int h = e / head_dim;
       int i = e % head_dim;
       float v = rope ? fkref_rope_elem(x + (size_t)h * head_dim, i, head_dim, rotated, position, theta) : x[e];
-      size_t at = (((size_t)slot * kv_heads + h) * length + position % (uint32_t)length) * head_dim + i;
-      c[at] = narrow_cache(v, cache_bf16);
+      uint16_t *row = row_of(L, st == 0 ? c0 : c1, st == 0 ? p0 : p1, position, h);
+      row[i] = narrow_cache(v, cache_bf16);
     }
   }
   return 0;
+}
+
+int fkref_step_store(const float *x0, const float *x1, uint16_t *c0, uint16_t *c1, int n_stores, int rope0,
+                     int rope1, int kv_heads, int head_dim, int length, int slots, int rotated, float theta,
+                     uint32_t position, uint32_t slot, int cache_bf16) {
+  if (slot >= (uint32_t)slots) return 0;
+  fkref_rows L = {0, kv_heads, head_dim, length, slot, 0, 0, 0, NULL};
+  return store_rows(&L, x0, x1, c0, c1, NULL, NULL, n_stores, rope0, rope1, rotated, theta, position, cache_bf16);
+}
+
+/* The store into a paged pool: `table` the row's block table of `table_len`
+ * blocks; nothing stored for a position past the table or a block past the
+ * pool. */
+int fkref_step_store_paged(const float *x0, const float *x1, uint16_t *const *p0, uint16_t *const *p1,
+                           int n_stores, int rope0, int rope1, int kv_heads, int head_dim, int block_size,
+                           const uint32_t *table, int table_len, int blocks, int rotated, float theta,
+                           uint32_t position, int cache_bf16) {
+  if (block_size <= 0 || table_len <= 0 || blocks <= 0) return -1;
+  if (position / (uint32_t)block_size >= (uint32_t)table_len ||
+      table[position / (uint32_t)block_size] >= (uint32_t)blocks)
+    return 0;
+  fkref_rows L = {1, kv_heads, head_dim, 0, 0, block_size, table_len, blocks, table};
+  return store_rows(&L, x0, x1, NULL, NULL, p0, p1, n_stores, rope0, rope1, rotated, theta, position, cache_bf16);
 }
 
 #define SPLIT_MAX 128
@@ -489,41 +544,41 @@ static float pairwise_sum(const float *a, int n) {
   return pairwise_sum(a, n / 2) + pairwise_sum(a + n / 2, n / 2);
 }
 
-int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
-                      int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
-                      int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
-                      int cache_bf16) {
+static int attend_rows(const fkref_rows *L, const float *q, const uint16_t *kc, const uint16_t *vc,
+                       uint16_t *const *kp, uint16_t *const *vp, float *partials, int heads, int kv_heads,
+                       int head_dim, int splits, int split, int rope, int rotated, float theta, float scale,
+                       int window, uint32_t position, uint32_t reach, int cache_bf16) {
   const int group = heads / kv_heads;
   const int d = head_dim;
   const uint32_t SPLIT = (uint32_t)split;
   if (group > 8 || d > 64 || d % 8 || split < ATTEND_CHUNKS || split > SPLIT_MAX || split % ATTEND_CHUNKS) return -1;
   if ((split / ATTEND_CHUNKS) & (split / ATTEND_CHUNKS - 1)) return -1; /* runs of a power of two */
-  uint32_t s = slot < (uint32_t)slots ? slot : 0;
   float qs[8 * 64];
   float wt[8 * SPLIT_MAX];
   float mx[8];
   uint32_t first = (window && position + 1 > (uint32_t)window) ? position + 1 - (uint32_t)window : 0;
+  /* The last position read: the row's own, or its reach past it. */
+  const uint32_t top = reach > position ? reach : position;
   for (int g = 0; g < kv_heads; g++) {
     for (int t = 0; t < splits; t++) {
       uint32_t lo = (uint32_t)t * SPLIT > first ? (uint32_t)t * SPLIT : first;
-      uint32_t hi = position + 1 < (uint32_t)(t + 1) * SPLIT ? position + 1 : (uint32_t)(t + 1) * SPLIT;
+      uint32_t hi = top + 1 < (uint32_t)(t + 1) * SPLIT ? top + 1 : (uint32_t)(t + 1) * SPLIT;
       int count = hi > lo ? (int)(hi - lo) : 0;
       for (int e = 0; e < group * d; e++) {
         const float *head = q + (size_t)(g * group + e / d) * d;
         qs[e] = rope ? fkref_rope_elem(head, e % d, d, rotated, position, theta) : head[e % d];
       }
-      size_t base = ((size_t)s * kv_heads + g) * length;
       /* A score: four fused multiply-add chains from +0, one a quarter of
        * the dimensions in order, added ((c0 + c1) + (c2 + c3)), then scaled. */
       const int dq = d / 4;
       for (int h = 0; h < group; h++) {
         for (int r = 0; r < count; r++) {
-          size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
+          const uint16_t *kr = row_of(L, (uint16_t *)kc, kp, lo + (uint32_t)r, g);
           float c[4];
           for (int j = 0; j < 4; j++) {
             c[j] = 0.0f;
             for (int i = j * dq; i < (j + 1) * dq; i++)
-              c[j] = fmaf(qs[h * d + i], widen_cache(kc[at + i], cache_bf16), c[j]);
+              c[j] = fmaf(qs[h * d + i], widen_cache(kr[i], cache_bf16), c[j]);
           }
           wt[h * SPLIT + r] = ((c[0] + c[1]) + (c[2] + c[3])) * scale;
         }
@@ -555,8 +610,8 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
             float lc = pairwise_sum(runw, run);
             float ac = 0.0f;
             for (int r = c * run; r < (c + 1) * run && r < count; r++) {
-              size_t at = (base + (lo + (uint32_t)r) % (uint32_t)length) * d;
-              ac = fmaf(wt[h * SPLIT + r], widen_cache(vc[at + i], cache_bf16), ac);
+              const uint16_t *vr = row_of(L, (uint16_t *)vc, vp, lo + (uint32_t)r, g);
+              ac = fmaf(wt[h * SPLIT + r], widen_cache(vr[i], cache_bf16), ac);
             }
             l = l + lc;
             acc = acc + ac;
@@ -571,6 +626,37 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
     }
   }
   return 0;
+}
+
+int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
+                      int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
+                      int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
+                      int cache_bf16) {
+  fkref_rows L = {0, kv_heads, head_dim, length, slot < (uint32_t)slots ? slot : 0, 0, 0, 0, NULL};
+  return attend_rows(&L, q, kc, vc, NULL, NULL, partials, heads, kv_heads, head_dim, splits, split, rope, rotated,
+                     theta, scale, window, position, position, cache_bf16);
+}
+
+/* The ring attention with a reach: positions up to max(position, reach). */
+int fkref_step_attend_reach(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
+                            int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
+                            int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
+                            uint32_t reach, int cache_bf16) {
+  fkref_rows L = {0, kv_heads, head_dim, length, slot < (uint32_t)slots ? slot : 0, 0, 0, 0, NULL};
+  return attend_rows(&L, q, kc, vc, NULL, NULL, partials, heads, kv_heads, head_dim, splits, split, rope, rotated,
+                     theta, scale, window, position, reach, cache_bf16);
+}
+
+/* The attention over a paged pool: the row's block table `table` of
+ * `table_len` blocks, the pool's `blocks` blocks at kp[b] and vp[b]. */
+int fkref_step_attend_paged(const float *q, uint16_t *const *kp, uint16_t *const *vp, float *partials, int heads,
+                            int kv_heads, int head_dim, int block_size, const uint32_t *table, int table_len,
+                            int blocks, int splits, int split, int rope, int rotated, float theta, float scale,
+                            int window, uint32_t position, uint32_t reach, int cache_bf16) {
+  if (block_size <= 0 || table_len <= 0 || blocks <= 0) return -1;
+  fkref_rows L = {1, kv_heads, head_dim, 0, 0, block_size, table_len, blocks, table};
+  return attend_rows(&L, q, NULL, NULL, kp, vp, partials, heads, kv_heads, head_dim, splits, split, rope, rotated,
+                     theta, scale, window, position, reach, cache_bf16);
 }
 
 /* The attention in wide splits (fk_attention.h, attend_wide): a split of S =

@@ -115,6 +115,18 @@ int fkref_step_attend(const float *q, const uint16_t *kc, const uint16_t *vc, fl
                       int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
                       int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
                       int cache_bf16);
+int fkref_step_attend_reach(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,
+                            int kv_heads, int head_dim, int length, int slots, int splits, int split, int rope,
+                            int rotated, float theta, float scale, int window, uint32_t position, uint32_t slot,
+                            uint32_t reach, int cache_bf16);
+int fkref_step_attend_paged(const float *q, uint16_t *const *kp, uint16_t *const *vp, float *partials, int heads,
+                            int kv_heads, int head_dim, int block_size, const uint32_t *table, int table_len,
+                            int blocks, int splits, int split, int rope, int rotated, float theta, float scale,
+                            int window, uint32_t position, uint32_t reach, int cache_bf16);
+int fkref_step_store_paged(const float *x0, const float *x1, uint16_t *const *p0, uint16_t *const *p1,
+                           int n_stores, int rope0, int rope1, int kv_heads, int head_dim, int block_size,
+                           const uint32_t *table, int table_len, int blocks, int rotated, float theta,
+                           uint32_t position, int cache_bf16);
 
 /* The splits combined once, in split order. */
 int fkref_step_attend_wide(const float *q, const uint16_t *kc, const uint16_t *vc, float *partials, int heads,

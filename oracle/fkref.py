@@ -61,6 +61,14 @@ def lib() -> ctypes.CDLL:
             "fkref_step_attend": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
                                        ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32, _i]),
             "fkref_step_combine": (_i, [_vp, _vp, _i, _i, _i]),
+            "fkref_step_attend_reach": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i,
+                                             ctypes.c_float, ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32,
+                                             ctypes.c_uint32, _i]),
+            "fkref_step_attend_paged": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _i, _i, _i,
+                                             ctypes.c_float, ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32,
+                                             _i]),
+            "fkref_step_store_paged": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _i,
+                                            ctypes.c_float, ctypes.c_uint32, _i]),
             "fkref_step_attend_wide": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
                                             ctypes.c_float, _i, ctypes.c_uint32, ctypes.c_uint32, _i]),
             "fkref_argmax": (ctypes.c_uint32, [_vp, _i]),

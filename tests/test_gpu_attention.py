@@ -36,8 +36,8 @@ def test_attention_and_combine_match_the_oracle(device, kernels, case):
     params = K.StepAttendParams(heads, kv, d, x["length"], 1, splits, x["split"], x["rope"], x["rotated"],
                                 x["length"], x["scale"], x["window"], x["bf16"], x["store"],
                                 x["rope"] if x["store"] else 0)
-    kernels.launch("fk_step_attend", kv * splits, 512, {**{k: v.ptr for k, v in b.items()}, "partials": partials.ptr},
-                   params)
+    kernels.launch("fk_step_attend", kv * splits, 512, {**{k: v.ptr for k, v in b.items()}, "partials": partials.ptr,
+                                                       "reach": 0}, params)
     kernels.launch("fk_step_combine", heads, 64, {"partials": partials.ptr, "out": out.ptr},
                    K.StepCombineParams(heads, d, splits))
     device.sync()
@@ -88,9 +88,10 @@ def test_wide_attention_matches_the_oracle(device, kernels, case, split):
                                 x["length"], x["scale"], x["window"], x["bf16"], x["store"],
                                 x["rope"] if x["store"] else 0)
     entry = "fk_step_attend_wide"
-    spans = [(bound[n].ptr, bound[n].size) for n in K.ABIS[entry].buffers]
+    spans = [(bound[n].ptr, bound[n].size) if n in bound else (0, 0) for n in K.ABIS[entry].buffers]
     runtime.launch_check(entry, kv * splits, threads, lds, spans, params)
-    kernels.launch(entry, kv * splits, threads, {k: v.ptr for k, v in bound.items()}, params, lds_bytes=lds)
+    kernels.launch(entry, kv * splits, threads, {**{k: v.ptr for k, v in bound.items()}, "reach": 0}, params,
+                   lds_bytes=lds)
     kernels.launch("fk_step_combine", heads, 64, {"partials": partials.ptr, "out": out.ptr},
                    K.StepCombineParams(heads, d, splits))
     device.sync()
