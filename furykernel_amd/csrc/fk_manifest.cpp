@@ -216,8 +216,26 @@ std::vector<Entry> build() {
       {FK_P(fk_step_argmax_params, n, "u32")}, sizeof(fk_step_argmax_params));
   add("fk_step_act_mul", 0, {buf("a", "read", "f32"), buf("b", "read", "f32"), buf("y", "write", "f32")},
       {FK_P(fk_step_act_mul_params, n, "u32"), FK_P(fk_step_act_mul_params, act, "u32"),
-       FK_P(fk_step_act_mul_params, b_off, "u32")},
+       FK_P(fk_step_act_mul_params, b_off, "u32"), FK_P(fk_step_act_mul_params, half, "u32")},
       sizeof(fk_step_act_mul_params));
+  add("fk_step_route", 64,
+      {buf("x", "read", "f32"), buf("scale", "read", "f32"), buf("ids", "write", "u32"), buf("ws", "write", "f32")},
+      {FK_P(fk_step_route_params, n, "u32"), FK_P(fk_step_route_params, k, "u32"),
+       FK_P(fk_step_route_params, has_scale, "u32")},
+      sizeof(fk_step_route_params));
+  add("fk_step_combine_ranks", 0,
+      {buf("w", "read", "f32"), buf("x", "read", "f32"), buf("res", "read", "f32"), buf("y", "write", "f32")},
+      {FK_P(fk_step_combine_ranks_params, seg, "u32"), FK_P(fk_step_combine_ranks_params, ranks, "u32"),
+       FK_P(fk_step_combine_ranks_params, residual, "u32")},
+      sizeof(fk_step_combine_ranks_params));
+  for (const char *name : {"fk_gemv_routed_f16_r1", "fk_gemv_routed_f16_r2", "fk_gemv_routed_f32_r1"}) {
+    using S = fk_gemv_routed_params;
+    add(name, 0,
+        {buf("table", "read", "u64"), buf("ids", "read", "u32"), buf("x", "read", "f32"), buf("y", "write", "f32")},
+        {FK_P(S, n, "u32"), FK_P(S, k, "u32"), FK_P(S, ranks, "u32"), FK_P(S, shared, "u32"), FK_P(S, entries, "u32"),
+         FK_P(S, groups_per_rank, "u32")},
+        sizeof(S));
+  }
   add("fk_step_advance", 0,
       {buf("next_token", "read", "u32"), buf("token", "write", "u32"), buf("position", "read_write", "u32")},
       {FK_P(fk_step_advance_params, context, "u32"), FK_P(fk_step_advance_params, step, "u32")},
@@ -544,6 +562,44 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({"c1", 0});
     }
     if (p.rope[0] || p.rope[1]) need.push_back({"rope", 0});
+  } else if (std::strcmp(entry, "fk_step_act_mul") == 0) {
+    fk_step_act_mul_params p;
+    std::memcpy(&p, params, sizeof p);
+    if (p.n == 0 || (uint64_t)groups * threads < p.n || (p.half && p.n % p.half))
+      return bad(err, cap, FK_ERR_ARG, "%s: %u elements in segments of %u, %u x %u threads", entry, p.n, p.half,
+                 groups, threads);
+    need = {{"a", (uint64_t)(p.half ? 2 : 1) * p.n * 4}, {"y", (uint64_t)p.n * 4}};
+    if (!p.half) need.push_back({"b", ((uint64_t)p.b_off + p.n) * 4});
+  } else if (std::strcmp(entry, "fk_step_route") == 0) {
+    fk_step_route_params p;
+    std::memcpy(&p, params, sizeof p);
+    if (p.k < 1 || p.k > 8 || p.k > p.n)
+      return bad(err, cap, FK_ERR_ARG, "%s: the %u largest of %u logits (1 to 8)", entry, p.k, p.n);
+    need = {{"x", (uint64_t)p.n * 4}, {"ids", (uint64_t)p.k * 4}, {"ws", (uint64_t)p.k * 4}};
+    if (p.has_scale) need.push_back({"scale", (uint64_t)p.n * 4});
+  } else if (std::strcmp(entry, "fk_step_combine_ranks") == 0) {
+    fk_step_combine_ranks_params p;
+    std::memcpy(&p, params, sizeof p);
+    if (p.ranks < 1 || p.seg == 0 || (uint64_t)groups * threads < p.seg)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u ranks of %u in %u x %u threads", entry, p.ranks, p.seg, groups,
+                 threads);
+    need = {{"w", (uint64_t)p.ranks * 4}, {"x", (uint64_t)p.ranks * p.seg * 4}, {"y", (uint64_t)p.seg * 4}};
+    if (p.residual) need.push_back({"res", (uint64_t)p.seg * 4});
+  } else if (std::strncmp(entry, "fk_gemv_routed_", 15) == 0) {
+    fk_gemv_routed_params p;
+    std::memcpy(&p, params, sizeof p);
+    const bool f32 = std::strncmp(entry + 15, "f32", 3) == 0;
+    const uint32_t pack = f32 ? 4 : 8, r = (uint32_t)(entry[std::strlen(entry) - 1] - '0');
+    if (p.entries == 0 || p.ranks == 0 || p.n == 0 || p.n % r || p.k == 0 || p.k % pack || threads % 64 ||
+        threads > 256 ||
+        p.groups_per_rank == 0 || groups != p.ranks * p.groups_per_rank ||
+        (uint64_t)p.groups_per_rank * (threads / 64) * r < p.n)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u ranks of %u rows at k %u in %u groups of %u", entry, p.ranks, p.n,
+                 p.k, groups, threads);
+    need = {{"table", (uint64_t)p.entries * 8},
+            {"ids", (uint64_t)p.ranks * 4},
+            {"x", (uint64_t)(p.shared ? 1 : p.ranks) * p.k * 4},
+            {"y", (uint64_t)p.ranks * p.n * 4}};
   } else if (std::strcmp(entry, "fk_step_token") == 0) {
     fk_step_token_params p;
     std::memcpy(&p, params, sizeof p);

@@ -291,6 +291,32 @@ __device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, con
       fk::gemv_wave<WT, XT, P, R>(w, x, scale, y, p.n, p.k, row0);                                         \
   }
 
+// LinearRouted: threadgroup (rank, group) of a rank's groups_per_rank takes
+// its W * R rows of the rank's table entry, the id clamped into the table.
+#define FK_GEMV_ROUTED_ENTRY(NAME, WT, P, R, KPL)                                                            \
+  extern "C" __global__ void __launch_bounds__(256)                                                        \
+      NAME(const uint64_t *__restrict__ table, const uint32_t *__restrict__ ids, const float *__restrict__ x, \
+           float *__restrict__ y, fk_gemv_routed_params p) {                                               \
+    const uint32_t rank = blockIdx.x / p.groups_per_rank;                                                  \
+    const uint32_t grp = blockIdx.x % p.groups_per_rank;                                                   \
+    const uint32_t row0 = (grp * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * (R);                  \
+    if (rank >= p.ranks || row0 >= p.n) return;                                                            \
+    const uint32_t e = min(ids[rank], p.entries - 1);                                                      \
+    const WT *w = reinterpret_cast<const WT *>(table[e]);                                                  \
+    const float *xr = x + (p.shared ? (size_t)0 : (size_t)rank * p.k);                                     \
+    float *yr = y + (size_t)rank * p.n;                                                                    \
+    if (p.k / (P) == FK_WAVE * (KPL))                                                                      \
+      fk::gemv_wave_inflight<WT, float, P, R, KPL, true>(w, xr, nullptr, yr, p.n, p.k, row0);             \
+    else if (p.k / (P) < FK_WAVE * (KPL))                                                                  \
+      fk::gemv_wave_inflight<WT, float, P, R, KPL, false>(w, xr, nullptr, yr, p.n, p.k, row0);            \
+    else                                                                                                   \
+      fk::gemv_wave<WT, float, P, R>(w, xr, nullptr, yr, p.n, p.k, row0);                                  \
+  }
+
+FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_f16_r1, _Float16, 8, 1, 8)
+FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_f16_r2, _Float16, 8, 2, 8)
+FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_f32_r1, float, 4, 1, 16)
+
 // Packs a lane holds in flight: rows of 4096 f32, 4096 f16 (by one row or
 // two) and 8192 int8; wider rows take the loop.
 FK_GEMV_ENTRY(fk_gemv_f32_f32_r1, float, float, 4, 1, 16)

@@ -166,7 +166,78 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
     fk_step_act_mul(const float *__restrict__ a, const float *__restrict__ b, float *__restrict__ y,
                     fk_step_act_mul_params p) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < p.n) y[i] = fk::act_mul(a[i], b[p.b_off + i], p.act);
+  if (i >= p.n) return;
+  if (p.half) {
+    const size_t at = (size_t)(i / p.half) * 2 * p.half + i % p.half;
+    y[i] = fk::act_mul(a[at], a[at + p.half], p.act);
+  } else {
+    y[i] = fk::act_mul(a[i], b[p.b_off + i], p.act);
+  }
+}
+
+// Routing: one wavefront, k rounds of the wavefront's largest key among the
+// logits not yet taken (the argmax keys, a NaN's the lowest), then lane 0's
+// weights.
+extern "C" __global__ void __launch_bounds__(FK_WAVE)
+    fk_step_route(const float *__restrict__ x, const float *__restrict__ scale, uint32_t *__restrict__ ids,
+                  float *__restrict__ ws, fk_step_route_params p) {
+  const uint32_t lane = threadIdx.x;
+  uint32_t taken[8];
+  float tv[8];
+#pragma unroll
+  for (int r = 0; r < 8; r++) taken[r] = 0xFFFFFFFFu, tv[r] = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    if ((uint32_t)r < p.k) {
+      uint64_t best = 0;
+      for (uint32_t i = lane; i < p.n; i += FK_WAVE) {
+        bool seen = false;
+#pragma unroll
+        for (int q = 0; q < 8; q++) seen |= q < r && taken[q] == i;
+        const float v = x[i];
+        const uint64_t key = __builtin_isnan(v) ? (uint64_t)(0xFFFFFFFFu - i) : fk::argmax_key(v, i);
+        if (!seen && key > best) best = key;
+      }
+#pragma unroll
+      for (int m = 1; m < FK_WAVE; m <<= 1) {
+        const uint64_t o = __shfl_xor(best, m);
+        best = o > best ? o : best;
+      }
+      taken[r] = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu);
+      tv[r] = x[taken[r]];
+    }
+  }
+  if (lane == 0) {
+    float e[8], total = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      if ((uint32_t)r < p.k) {
+        e[r] = fk::exp_once(tv[r] - tv[0]);
+        total = total + e[r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      if ((uint32_t)r < p.k) {
+        float w = e[r] / total;
+        if (p.has_scale) w = w * scale[taken[r]];
+        ids[r] = taken[r];
+        ws[r] = w;
+      }
+    }
+  }
+}
+
+// CombineRanks, and the residual add after it.
+extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
+    fk_step_combine_ranks(const float *__restrict__ w, const float *__restrict__ x, const float *__restrict__ res,
+                          float *__restrict__ y, fk_step_combine_ranks_params p) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.seg) return;
+  float acc = w[0] * x[i];
+  for (uint32_t r = 1; r < p.ranks; r++) acc = acc + w[r] * x[(size_t)r * p.seg + i];
+  if (p.residual) acc = res[i] + acc;
+  y[i] = acc;
 }
 
 // The next decode step's inputs: its token is this step's greedy token, its

@@ -30,6 +30,12 @@ _STRUCTS = {
     "fk_step_combine": K.StepCombineParams,
     "fk_step_argmax": K.CountParams,
     "fk_step_act_mul": K.ActMulParams,
+    "fk_step_route": K.RouteParams,
+    "fk_rmsnorm_f32": K.RmsNormParams,
+    "fk_step_combine_ranks": K.CombineRanksParams,
+    "fk_gemv_routed_f16_r1": K.GemvRoutedParams,
+    "fk_gemv_routed_f16_r2": K.GemvRoutedParams,
+    "fk_gemv_routed_f32_r1": K.GemvRoutedParams,
     "fk_prefill_softcap": K.PrefillSoftcapParams,
     "fk_step_token": K.StepTokenParams,
     "fk_gemm_f16_store": K.GemmParams,
@@ -231,6 +237,8 @@ class Engine:
         for src, w in weights.items():
             if f"weight:{src}" in self.lowered.buffers:
                 self.write(f"weight:{src}", w)
+            if f"table:{src}" in self.lowered.buffers:  # a table's entries, in order
+                self.write(f"table:{src}", w)
             wide = f"widen:{src}"
             if wide in self.lowered.buffers:
                 self.write(wide, widen(self.lowered.program.source_named(src).kind.type, w))

@@ -129,7 +129,7 @@ class PrefillSoftcapParams(ctypes.Structure):
 
 
 class ActMulParams(ctypes.Structure):
-    _fields_ = [("n", ctypes.c_uint32), ("act", ctypes.c_uint32), ("b_off", ctypes.c_uint32)]
+    _fields_ = [("n", ctypes.c_uint32), ("act", ctypes.c_uint32), ("b_off", ctypes.c_uint32), ("half", ctypes.c_uint32)]
 
 
 class PrefillArgmaxParams(ctypes.Structure):
@@ -197,6 +197,19 @@ class AttendArgs(ctypes.Structure):
                 ("kc", ctypes.c_uint64), ("vc", ctypes.c_uint64), ("position", ctypes.c_uint64),
                 ("slot", ctypes.c_uint64), ("rope", ctypes.c_uint64), ("out", ctypes.c_uint64),
                 ("p", StepAttendParams)]
+
+
+class RouteParams(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_uint32), ("k", ctypes.c_uint32), ("has_scale", ctypes.c_uint32)]
+
+
+class GemvRoutedParams(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_uint32), ("k", ctypes.c_uint32), ("ranks", ctypes.c_uint32),
+                ("shared", ctypes.c_uint32), ("entries", ctypes.c_uint32), ("groups_per_rank", ctypes.c_uint32)]
+
+
+class CombineRanksParams(ctypes.Structure):
+    _fields_ = [("seg", ctypes.c_uint32), ("ranks", ctypes.c_uint32), ("residual", ctypes.c_uint32)]
 
 
 class StepCombineParams(ctypes.Structure):
@@ -302,6 +315,10 @@ ABIS: dict[str, KernelAbi] = {
     "fk_step_combine": KernelAbi("fk_step_combine", ("partials", "out"), StepCombineParams, 64),
     "fk_step_argmax": KernelAbi("fk_step_argmax", ("x", "out"), CountParams),
     "fk_step_act_mul": KernelAbi("fk_step_act_mul", ("a", "b", "y"), ActMulParams),
+    "fk_step_route": KernelAbi("fk_step_route", ("x", "scale", "ids", "ws"), RouteParams, 64),
+    "fk_step_combine_ranks": KernelAbi("fk_step_combine_ranks", ("w", "x", "res", "y"), CombineRanksParams),
+    **{e: KernelAbi(e, ("table", "ids", "x", "y"), GemvRoutedParams)
+       for e in ("fk_gemv_routed_f16_r1", "fk_gemv_routed_f16_r2", "fk_gemv_routed_f32_r1")},
     "fk_step_advance": KernelAbi("fk_step_advance", ("next_token", "token", "position"), AdvanceParams),
     "fk_init_normal": KernelAbi("fk_init_normal", ("dst",), InitNormalParams),
     "fk_noop": KernelAbi("fk_noop", (), NoopParams),
@@ -588,6 +605,12 @@ def launch_reads(entry: str, params: dict) -> set[str]:
         if params.get("has_reach"):
             need.add("reach")
         return need
+    if entry == "fk_step_route":
+        return {"x", "ids", "ws"} | ({"scale"} if params.get("has_scale") else set())
+    if entry == "fk_step_combine_ranks":
+        return {"w", "x", "y"} | ({"res"} if params.get("residual") else set())
+    if entry == "fk_step_act_mul":
+        return {"a", "y"} | (set() if params.get("half") else {"b"})
     if entry == "fk_step_store_paged":
         need = {"x0", "p0", "position", "table"}
         if params.get("n_stores", 1) > 1:

@@ -13,6 +13,7 @@ step's kernels (src/FuryKernel/Backend.hs:29-101).
 
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass, field
 from typing import Callable, Optional
@@ -21,8 +22,9 @@ import numpy as np
 
 from .program.check import CheckedProgram
 from .program.graph import (
-    BF16, CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, Gather, GatedGelu, GeluMul, Input, KvStore,
-    Linear, Paged, Ring, RmsNorm, Rope, ROPE_HALVES, SCache, SInput, Softcap, SRowInts, SWeight)
+    BF16, CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, CombineRanks, Gather, GatedGelu, GeluMul,
+    Input, KvStore, Linear, LinearRouted, Paged, Ring, RmsNorm, Rope, ROPE_HALVES, Route, SCache, SInput, Softcap,
+    SRowInts, STable, SWeight)
 from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
 
 THREADS = 256
@@ -114,7 +116,8 @@ def lower_plan(checked: CheckedProgram, plan: Plan, rows: int = 1, compute_units
     out = Lowered(checked.program, plan, rows)
     low = _StepLowering(out, compute_units, wide, choose)
     for step in plan.steps:
-        out.launches.append(low.step(step))
+        made = low.step(step)
+        out.launches.extend(made if isinstance(made, list) else [made])
     if fuse:
         _fuse_attention(out)
         _fuse_light(out, compute_units, choose)
@@ -338,6 +341,7 @@ class _StepLowering:
         self.compute_units = compute_units
         self.wide = wide
         self.choose = choose
+        self.materialized: set = set()  # values a launch of an earlier part of the step made
         self.p = out.program
         self.producer = {v: n for n in self.p.nodes for v in n.outputs}
 
@@ -411,6 +415,8 @@ class _StepLowering:
         return name
 
     def stored_before(self, step: Step, v: int) -> bool:
+        if v in self.materialized:
+            return True
         prod = self.producer.get(v)
         if prod is not None and isinstance(prod.op, Input):
             return True
@@ -418,11 +424,31 @@ class _StepLowering:
 
     # Steps -----------------------------------------------------------------------
 
-    def step(self, step: Step) -> Launch:
+    def step(self, step: Step):
         kinds = {w.kind for w in step.work}
         if STAGE in kinds or LAND in kinds:
             raise LoweringError(f"{step.name}: staged stores are not lowered yet")
         anchors = [self.p.node(w.node) for w in step.work if w.kind == ANCHOR]
+        if anchors and any(isinstance(a.op, LinearRouted) for a in anchors):
+            return self.routed_step(step, anchors)
+        # An RMSNorm the step recomputes and stores: made once by its own
+        # launch, then read as stored by the rest of the step.
+        pre = []
+        for w in step.work:
+            node = self.p.node(w.node)
+            if w.kind == RECOMPUTE and isinstance(node.op, RmsNorm) and \
+                    any(st.value == node.outputs[0] for st in step.stores) and self.stored_before(step, node.op.x):
+                pre.append(self.norm_launch(step, node))
+        if pre:
+            made = {L.bind["y"] for L in pre}
+            kept = [w for w in step.work if not (w.kind == RECOMPUTE and
+                                                 self.value(self.p.node(w.node).outputs[0]) in made)]
+            step = dataclasses.replace(step, work=kept,
+                                       stores=[st for st in step.stores if self.value(st.value) not in made])
+            for L in pre:
+                self.materialized.add(L.meta["value"])
+            rest = self.step(step)
+            return pre + (rest if isinstance(rest, list) else [rest])
         if anchors and all(isinstance(a.op, Linear) for a in anchors):
             return self.gemv_step(step, anchors)
         if len(anchors) == 1 and isinstance(anchors[0].op, Attend):
@@ -772,7 +798,112 @@ class _StepLowering:
         return Launch(step.name, "fk_step_combine", spec.heads, 64,
                       {"partials": pname, "out": self.value(out)}, params)
 
+    def norm_launch(self, step: Step, node) -> Launch:
+        """An RMSNorm of one stored row as its own launch (fk_rmsnorm_f32, one
+        row in segments, tgReduceSum's order over 256 threads)."""
+        op = node.op
+        shape = self.p.value(op.x).shape
+        seg = shape.segment or shape.width
+        if seg % 4 or shape.width % seg:
+            raise LoweringError(f"{step.name}: an RMSNorm in segments of {seg} of a row of {shape.width}")
+        gamma = None if op.gamma is None else self.gains(op.gamma)
+        out = self.value(node.outputs[0])
+        x = self.value(op.x)
+        return Launch(f"{step.name}:{self.p.value(node.outputs[0]).name}", "fk_rmsnorm_f32", shape.width // seg, 256,
+                      {"x": x, "gamma": gamma, "y": out},
+                      {"rows": 1, "width": shape.width, "seg": seg, "eps": float(np.float32(op.eps)),
+                       "factor": float(np.float32(op.factor)), "has_gamma": int(gamma is not None)},
+                      {"value": node.outputs[0]})
+
+    def table(self, s: int) -> tuple[str, STable]:
+        """A table of weights: its entries in order in ``table:<name>``, their
+        addresses in ``tableaddr:<name>`` (u64, the engine writes them)."""
+        src = self.p.source(s)
+        if not isinstance(src.kind, STable):
+            raise LoweringError(f"{src.name} is not a table")
+        t = src.kind.type
+        if t not in (F16, F32):
+            raise LoweringError(f"table {src.name} of {t}: the routed GEMV takes f16 and f32 entries")
+        size = int(np.prod(src.kind.dims))
+        pool = self.out.buffer(f"table:{src.name}", t, src.kind.entries * size)
+        addr = self.out.buffer(f"tableaddr:{src.name}", "u64", src.kind.entries)
+        self.out.constants[addr] = ("addresses", pool, size * (2 if t == F16 else 4))
+        return addr, src.kind
+
+    def routed_step(self, step: Step, anchors: list) -> list:
+        """A step anchoring LinearRouted (Eval.hs:291-321): its route (if it
+        recomputes it) by fk_step_route into the stored ids and weights, a
+        gated activation of its input (if it recomputes one) by fk_step_act_mul
+        into a row of its own, then the routed GEMV."""
+        if len(anchors) != 1:
+            raise LoweringError(f"{step.name}: {len(anchors)} routed anchors; the routed GEMV takes one")
+        anchor = anchors[0]
+        op = anchor.op
+        launches = []
+        for w in step.work:
+            node = self.p.node(w.node)
+            if w.kind == ANCHOR:
+                continue
+            if w.kind != RECOMPUTE:
+                raise LoweringError(f"{step.name}: {w.kind} work beside a routed anchor")
+            if isinstance(node.op, Route):
+                launches.append(self.route_launch(step, node))
+            elif isinstance(node.op, GatedGelu) and node.outputs[0] == op.x:
+                launches.append(self.gated_launch(step, node))
+            else:
+                raise LoweringError(f"{step.name}: no routed step recomputes {type(node.op).__name__}")
+        for L in launches:
+            self.materialized |= set(L.meta["values"])
+        if not self.stored_before(step, op.ids) or not self.stored_before(step, op.x):
+            raise LoweringError(f"{step.name}: the routed GEMV's ids and input neither stored nor made")
+        addr, tk = self.table(op.table)
+        n, k = tk.dims
+        ranks = self.p.value(op.ids).shape.width
+        width = self.p.value(op.x).shape.width
+        if width not in (k, ranks * k):
+            raise LoweringError(f"{step.name}: an input of {width} for {ranks} ranks of {k}")
+        out = anchor.outputs[0]
+        if [st.value for st in step.stores if st.value not in self.materialized] != [out]:
+            raise LoweringError(f"{step.name}: a routed step storing other than its anchor's rows")
+        r = 2 if tk.type == F16 and n >= 2048 else 1
+        entry = f"fk_gemv_routed_{tk.type}_r{r}"
+        per_group = 4 * r  # 256 threads
+        gpr = -(-n // per_group)
+        params = {"n": n, "k": k, "ranks": ranks, "shared": int(width == k), "entries": tk.entries,
+                  "groups_per_rank": gpr}
+        bind = {"table": addr, "ids": self.value(op.ids), "x": self.value(op.x), "y": self.value(out)}
+        launches.append(Launch(step.name, entry, ranks * gpr, 256, bind, params))
+        return launches
+
+    def route_launch(self, step: Step, node) -> Launch:
+        op = node.op
+        ids, ws = node.outputs
+        n = self.p.value(op.x).shape.width
+        if not self.stored_before(step, op.x):
+            raise LoweringError(f"{step.name}: a route of logits not stored")
+        scale = None if op.spec.expert_scale is None else self.gains(op.spec.expert_scale)
+        x = self.value(op.x)
+        return Launch(f"{step.name}:route", "fk_step_route", 1, 64,
+                      {"x": x, "scale": scale or x, "ids": self.value(ids), "ws": self.value(ws)},
+                      {"n": n, "k": op.spec.k, "has_scale": int(scale is not None)}, {"values": [ids, ws]})
+
+    def gated_launch(self, step: Step, node) -> Launch:
+        op = node.op
+        if op.form not in ACT or not self.stored_before(step, op.x):
+            raise LoweringError(f"{step.name}: a gated activation of a row not stored")
+        shape = self.p.value(op.x).shape
+        half = shape.segment // 2
+        n = shape.width // 2
+        x = self.value(op.x)
+        return Launch(f"{step.name}:{self.p.value(node.outputs[0]).name}", "fk_step_act_mul", -(-n // THREADS),
+                      THREADS, {"a": x, "b": x, "y": self.value(node.outputs[0])},
+                      {"n": n, "act": ACT[op.form], "b_off": 0, "half": half}, {"values": [node.outputs[0]]})
+
     def light_step(self, step: Step) -> Launch:
+        rec = [self.p.node(w.node) for w in step.work if w.kind == RECOMPUTE]
+        comb = [r for r in rec if isinstance(r.op, CombineRanks)]
+        if comb and len(rec) <= 2:
+            return self.combine_ranks_step(step, rec, comb[0])
         rec = [self.p.node(w.node) for w in step.work if w.kind == RECOMPUTE]
         if len(rec) != 1 or len(step.stores) != 1 or step.stores[0].value != rec[0].outputs[0]:
             raise LoweringError(f"{step.name}: a light step other than one stored recompute")
@@ -806,3 +937,28 @@ class _StepLowering:
             return Launch(step.name, "fk_prefill_softcap", max(1, -(-n // 256)), 256,
                           {"x": self.value(op.x), "y": self.value(node.outputs[0])}, {"count": n, "cap": cap})
         raise LoweringError(f"{step.name}: no light kernel recomputes {type(op).__name__}")
+
+    def combine_ranks_step(self, step: Step, rec: list, comb) -> Launch:
+        """CombineRanks of stored weights and rows, and the residual add of it
+        (if the step recomputes one), into the stored value."""
+        op = comb.op
+        if not self.stored_before(step, op.weights) or not self.stored_before(step, op.x):
+            raise LoweringError(f"{step.name}: a combine of ranks not stored")
+        res, out = None, comb.outputs[0]
+        adds = [r for r in rec if r is not comb]
+        if adds:
+            a = adds[0].op
+            if not isinstance(a, Add) or comb.outputs[0] not in (a.a, a.b):
+                raise LoweringError(f"{step.name}: a combine of ranks with {type(a).__name__}")
+            other = a.b if a.a == comb.outputs[0] else a.a
+            if not self.stored_before(step, other):
+                raise LoweringError(f"{step.name}: a residual not stored")
+            res, out = self.value(other), adds[0].outputs[0]
+        if [st.value for st in step.stores] != [out]:
+            raise LoweringError(f"{step.name}: a combine of ranks storing other than its value")
+        seg = self.p.value(op.x).shape.segment
+        ranks = self.p.value(op.weights).shape.width
+        x = self.value(op.x)
+        return Launch(step.name, "fk_step_combine_ranks", -(-seg // THREADS), THREADS,
+                      {"w": self.value(op.weights), "x": x, "res": res or x, "y": self.value(out)},
+                      {"seg": seg, "ranks": ranks, "residual": int(res is not None)})

@@ -171,7 +171,43 @@ typedef struct fk_step_act_mul_params {
   uint32_t n;
   uint32_t act;   /* FK_ACT_* */
   uint32_t b_off; /* elements into b where the second row starts (a gated activation's second half) */
+  uint32_t half;  /* 0: a and b as rows; else segments of 2 half of one row a (b unread): y[s half + i] =
+                     act(a[2 s half + i]) a[2 s half + half + i] (GatedGelu, Eval.hs:356-371) */
 } fk_step_act_mul_params;
+
+/* Routing (Eval.hs:391-404, routeRow :648-655): the k largest of n logits,
+ * ties to the lower index (a NaN ranked below every number), in rank order;
+ * their weights exp(x - best) binary64's rounded once over their sum from
+ * +0 in rank order, each divided by the sum, times its expert's scale if
+ * has_scale. */
+typedef struct fk_step_route_params {
+  uint32_t n;
+  uint32_t k; /* 1 to 8, at most n */
+  uint32_t has_scale;
+} fk_step_route_params;
+
+/* LinearRouted (Eval.hs:291-321): for each of `ranks` ranks, the n rows of
+ * the table entry ids[rank] (its address table[ids[rank]], the id clamped
+ * below `entries`) times the row x (shared) or the rank's slice of k
+ * elements, in the reference GEMV's order; a rank's rows in
+ * groups_per_rank threadgroups. */
+typedef struct fk_gemv_routed_params {
+  uint32_t n;
+  uint32_t k;
+  uint32_t ranks;
+  uint32_t shared;
+  uint32_t entries;
+  uint32_t groups_per_rank;
+} fk_gemv_routed_params;
+
+/* CombineRanks (Eval.hs:405-414): y[i] = ((w0 x0[i] + w1 x1[i]) + ...), x_r
+ * the rank's segment of `seg`; then, with `residual`, res[i] + y[i] (the
+ * residual add the plan recomputes with it). */
+typedef struct fk_step_combine_ranks_params {
+  uint32_t seg;
+  uint32_t ranks;
+  uint32_t residual;
+} fk_step_combine_ranks_params;
 
 typedef struct fk_step_advance_params {
   uint32_t context; /* positions wrap below this */

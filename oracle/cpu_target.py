@@ -187,9 +187,43 @@ class CpuTarget:
             self.buffers[b["out"]][0] = L.fkref_argmax(self._p(b["x"]), p["n"])
             st = 0
         elif e == "fk_step_act_mul":
-            off = p.get("b_off", 0)
-            bb = self.buffers[b["b"]][off:]
-            st = L.fkref_act_mul(self._p(b["a"]), bb.ctypes.data, self._p(b["y"]), p["n"], p.get("act", 0))
+            half = p.get("half", 0)
+            if half:
+                # segments of 2 half of one row: each element's act·mul as the
+                # contiguous form computes it
+                a = self.buffers[b["a"]]
+                i = np.arange(p["n"])
+                at = (i // half) * 2 * half + i % half
+                aa, bb = np.ascontiguousarray(a[at]), np.ascontiguousarray(a[at + half])
+                y = np.zeros(p["n"], np.float32)
+                st = L.fkref_act_mul(aa.ctypes.data, bb.ctypes.data, y.ctypes.data, p["n"], p.get("act", 0))
+                self.buffers[b["y"]][:p["n"]] = y
+            else:
+                off = p.get("b_off", 0)
+                bb = self.buffers[b["b"]][off:]
+                st = L.fkref_act_mul(self._p(b["a"]), bb.ctypes.data, self._p(b["y"]), p["n"], p.get("act", 0))
+        elif e == "fk_rmsnorm_f32":
+            st = L.fkref_rmsnorm(self._p(b["x"]), self._p(b["gamma"]) if p["has_gamma"] else None, self._p(b["y"]),
+                                 p["rows"], p["width"], p["seg"], p["eps"], p["factor"], launch.threads, 64, 4)
+        elif e == "fk_step_route":
+            st = L.fkref_route(self._p(b["x"]), self._p(b["scale"]) if p["has_scale"] else None, self._p(b["ids"]),
+                               self._p(b["ws"]), p["n"], p["k"], p["has_scale"])
+        elif e.startswith("fk_gemv_routed_"):
+            wt = e.split("_")[3]
+            kind, pool, entry_bytes = self.lowered.constants[b["table"]]
+            table, ids = self.buffers[pool], self.buffers[b["ids"]]
+            x, y = self.buffers[b["x"]], self.buffers[b["y"]]
+            n, k = p["n"], p["k"]
+            st = 0
+            for r in range(p["ranks"]):
+                ent = min(int(ids[r]), p["entries"] - 1)
+                w = table.ctypes.data + ent * entry_bytes
+                xr = x.ctypes.data + (0 if p["shared"] else r * k * 4)
+                yr = y.ctypes.data + r * n * 4
+                st = st or L.fkref_gemv(w, TYPE[wt], xr, fkref.F32, yr, None, n, k, 1, 64, 8 if wt == "f16" else 4, 1)
+        elif e == "fk_step_combine_ranks":
+            st = L.fkref_combine_ranks(self._p(b["w"]), self._p(b["x"]), self._p(b["res"]), self._p(b["y"]), p["seg"],
+                                       p["ranks"], p["residual"])
         else:
             raise ValueError(f"the CPU target has no kernel {e}")
         if st:

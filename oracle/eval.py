@@ -22,8 +22,8 @@ import numpy as np
 
 from furykernel_amd.program.check import CheckedProgram
 from furykernel_amd.program.graph import (
-    CACHE_BF16, Add, ArgMax, Attend, Concat, Gather, GatedGelu, GELU_TANH, GeluMul, Input, KvStore, Linear, Ring,
-    RmsNorm, Rope, SCache, ScaleBy, SILU, Softcap)
+    CACHE_BF16, Add, ArgMax, Attend, CombineRanks, Concat, Gather, GatedGelu, GELU_TANH, GeluMul, Input, KvStore,
+    Linear, LinearRouted, Ring, RmsNorm, Rope, Route, SCache, ScaleBy, SILU, Softcap, STable)
 
 from . import fkref
 
@@ -39,6 +39,7 @@ class Bindings:
     weights: dict = field(default_factory=dict)
     row_ints: dict = field(default_factory=dict)
     caches: dict = field(default_factory=dict)
+    tables: dict = field(default_factory=dict)  # name -> [entry's flat values, ...]
 
 
 @dataclass
@@ -340,6 +341,62 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
             env[out] = [sum(tm[t] for t in toks) * op.factor for toks in ints(op.tokens)]
         elif isinstance(op, ArgMax):
             env[out] = [np.array([float(arg_max(list(x)))]) for x in env[op.x]]
+        elif isinstance(op, Route):
+            # Eval.hs:391-404, routeRow :648-655: the k largest logits, ties
+            # to the lower index, in rank order; weights a softmax over them
+            # (exp(x - best) / their sum, the sum a left fold from 0), each
+            # times its expert's scale if there is one.
+            scale = None if op.spec.expert_scale is None else weight(op.spec.expert_scale)
+            ids_rows, w_rows = [], []
+            for x in env[op.x]:
+                order = sorted(range(len(x)), key=lambda i: (-x[i], i))
+                top = order[:op.spec.k]
+                best = x[order[0]]
+                es = [math.exp(x[i] - best) for i in top]
+                total = 0.0
+                for e in es:
+                    total = total + e
+                ids_rows.append(np.array(top, np.float64))
+                w_rows.append(np.array([e / total * (1.0 if scale is None else scale[i]) for i, e in zip(top, es)]))
+            env[n.outputs[0]], env[n.outputs[1]] = ids_rows, w_rows
+        elif isinstance(op, LinearRouted):
+            # Eval.hs:291-321: rank r's segment is its expert's weights times
+            # the row (shared by every rank when the row is one expert's
+            # input wide, else the rank's slice of it).
+            src = sources[op.table]
+            if not isinstance(src.kind, STable):
+                raise EvalError(f"{src.name} is not a table.")
+            entries = b.tables.get(src.name)
+            if entries is None:
+                raise EvalError(f"No table {src.name}.")
+            if len(entries) != src.kind.entries:
+                raise EvalError(f"{src.name} has {len(entries)} entries bound, not {src.kind.entries}.")
+            out_w, k = src.kind.dims
+            mats = [np.asarray(e, np.float64).reshape(out_w, k) for e in entries]
+            shared = values[op.x].shape.width == k
+            res = []
+            for idr, xr in zip(env[op.ids], env[op.x]):
+                parts = []
+                for rank, e in enumerate(idr):
+                    entry = int(round(e))
+                    if not 0 <= entry < len(mats):
+                        raise EvalError(f"{n.name}: expert {entry} is not in the table.")
+                    base = 0 if shared else rank * k
+                    xs = xr[base:base + k]
+                    parts.append(np.array([hsum(mats[entry][j] * xs) for j in range(out_w)]))
+                res.append(np.concatenate(parts))
+            env[out] = res
+        elif isinstance(op, CombineRanks):
+            # Eval.hs:405-414: sum over ranks of weight times the rank's
+            # segment, a left fold from the first rank's product.
+            seg = values[op.x].shape.segment
+            res = []
+            for wr, xr in zip(env[op.weights], env[op.x]):
+                acc = wr[0] * xr[0:seg]
+                for r in range(1, len(wr)):
+                    acc = acc + wr[r] * xr[r * seg:(r + 1) * seg]
+                res.append(acc)
+            env[out] = res
         else:
             raise EvalError(f"{n.name}: {type(op).__name__} is not evaluated here")
     outs = {}

@@ -792,6 +792,54 @@ uint64_t fkref_argmax_key(float v, uint32_t index) {
   return ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - index);
 }
 
+/* Routing (fk_step_route): the k largest logits by their argmax keys (a
+ * NaN's key the lowest, its index's), then exp(x_r - x_0) binary64's rounded
+ * once, their sum from +0 in rank order, each over the sum, times its
+ * expert's scale if given. */
+int fkref_route(const float *x, const float *scale, uint32_t *ids, float *ws, int n, int k, int has_scale) {
+  if (k < 1 || k > 8 || k > n) return -1;
+  uint32_t taken[8];
+  float tv[8], e[8], total = 0.0f;
+  for (int r = 0; r < k; r++) {
+    uint64_t best = 0;
+    for (int i = 0; i < n; i++) {
+      int seen = 0;
+      for (int q = 0; q < r; q++) seen |= taken[q] == (uint32_t)i;
+      uint64_t key = isnan(x[i]) ? (uint64_t)(0xFFFFFFFFu - (uint32_t)i) : fkref_argmax_key(x[i], (uint32_t)i);
+      if (!seen && key > best) best = key;
+    }
+    taken[r] = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu);
+    tv[r] = x[taken[r]];
+  }
+  for (int r = 0; r < k; r++) {
+    e[r] = fkref_exp(tv[r] - tv[0]);
+    total = total + e[r];
+  }
+  for (int r = 0; r < k; r++) {
+    float w = e[r] / total;
+    if (has_scale) w = w * scale[taken[r]];
+    ids[r] = taken[r];
+    ws[r] = w;
+  }
+  return 0;
+}
+
+/* CombineRanks (fk_step_combine_ranks): a left fold from the first rank's
+ * product, each product rounded, then the residual added in front. */
+int fkref_combine_ranks(const float *w, const float *x, const float *res, float *y, int seg, int ranks,
+                        int residual) {
+  if (ranks < 1 || seg < 1) return -1;
+  for (int i = 0; i < seg; i++) {
+    float acc = w[0] * x[i];
+    for (int r = 1; r < ranks; r++) {
+      float t = w[r] * x[(size_t)r * seg + i];
+      acc = acc + t;
+    }
+    y[i] = residual ? res[i] + acc : acc;
+  }
+  return 0;
+}
+
 uint64_t fkref_argmax_keyed(const float *x, int n) {
   uint64_t best = 0;
   for (int i = 0; i < n; i++) {

@@ -143,6 +143,9 @@ uint32_t fkref_argmax(const float *x, int n);
  * key of a row of n (0 for n = 0). */
 uint64_t fkref_argmax_key(float v, uint32_t index);
 uint64_t fkref_argmax_keyed(const float *x, int n);
+int fkref_route(const float *x, const float *scale, uint32_t *ids, float *ws, int n, int k, int has_scale);
+int fkref_combine_ranks(const float *w, const float *x, const float *res, float *y, int seg, int ranks,
+                        int residual);
 
 /* SiLU(a) * b elementwise: a / (1 + exp(-a)) * b, exp binary64's rounded once. */
 int fkref_silu_mul(const float *a, const float *b, float *y, int n);

@@ -75,6 +75,8 @@ def lib() -> ctypes.CDLL:
             "fkref_argmax_key": (ctypes.c_uint64, [ctypes.c_float, ctypes.c_uint32]),
             "fkref_argmax_keyed": (ctypes.c_uint64, [_vp, _i]),
             "fkref_silu_mul": (_i, [_vp, _vp, _vp, _i]),
+            "fkref_route": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+            "fkref_combine_ranks": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)

@@ -124,3 +124,13 @@ def test_a_reach_reads_past_the_rows_position(paged):
     own = run_cpu(low, x, position, **({"table": table, "pool": pool} if paged else {"ring": ring}),
                   reach=position)
     assert rel(own.read("value:o"), ev.outputs["o"][0]) > 1e-3
+
+
+@pytest.mark.parametrize("case", CASES, ids=case_id)
+def test_every_paged_launch_passes_the_launch_checks(case):
+    from test_moe import host_checked
+    from furykernel_amd.lower import lower_plan
+    from furykernel_amd.program.plan import PlanOptions, plan
+    for checked in (paged_program(case), paged_program(case, reach_bound=case[3] * case[5]), ring_program(case)):
+        for fuse in (True, False):
+            host_checked(lower_plan(checked, plan(PlanOptions(), checked), fuse=fuse))
