@@ -60,7 +60,7 @@ def build_runtime() -> Path:
     obj = PACKAGE / ".fk_ops.o"
     _run([HIPCC, "-c", "-fPIC", *KERNEL_FLAGS, f"-I{ROOT / 'include'}", str(CSRC / "fk_ops.hip"), "-o", str(obj)])
     objs.append(obj)
-    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp), "-lhiprtc"])
     for o in objs:
         o.unlink()
     os.replace(tmp, RUNTIME_SO)

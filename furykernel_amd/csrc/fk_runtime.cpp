@@ -10,10 +10,12 @@
 #include "../../include/fkrocm.h"
 
 #include <hip/hip_runtime_api.h>
+#include <hip/hiprtc.h>
 
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <mutex>
@@ -189,6 +191,48 @@ int fk_module_load_file(fk_ctx *ctx, const char *path, fk_module **out) {
   if (image.empty()) return fail(ctx, FK_ERR_ARG, "fk_module_load_file: %s is empty", path);
   return fk_module_load(ctx, image.data(), image.size(), out);
 }
+
+// hipRTC --------------------------------------------------------------------
+
+int fk_rtc_compile(const char *source, const char *name, const char *const *options, int n_options, void **code,
+                   size_t *code_bytes, char **log) {
+  if (!source || !code || !code_bytes || n_options < 0 || (n_options > 0 && !options))
+    return fail(nullptr, FK_ERR_ARG, "fk_rtc_compile: null argument");
+  *code = nullptr;
+  *code_bytes = 0;
+  if (log) *log = nullptr;
+  hiprtcProgram prog;
+  hiprtcResult r = hiprtcCreateProgram(&prog, source, name ? name : "unit.hip", 0, nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS) return fail(nullptr, FK_ERR_COMPILE, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
+  r = hiprtcCompileProgram(prog, n_options, const_cast<const char **>(options));
+  size_t log_bytes = 0;
+  if (log && hiprtcGetProgramLogSize(prog, &log_bytes) == HIPRTC_SUCCESS && log_bytes > 1) {
+    *log = static_cast<char *>(malloc(log_bytes + 1));
+    if (*log) {
+      hiprtcGetProgramLog(prog, *log);
+      (*log)[log_bytes] = '\0';
+    }
+  }
+  if (r != HIPRTC_SUCCESS) {
+    hiprtcDestroyProgram(&prog);
+    return fail(nullptr, FK_ERR_COMPILE, "fk_rtc_compile: %s: %s", name ? name : "unit.hip",
+                hiprtcGetErrorString(r));
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  void *buf = n ? malloc(n) : nullptr;
+  if (!buf) {
+    hiprtcDestroyProgram(&prog);
+    return fail(nullptr, FK_ERR_OOM, "fk_rtc_compile: no host memory for a code object of %zu bytes", n);
+  }
+  hiprtcGetCode(prog, static_cast<char *>(buf));
+  hiprtcDestroyProgram(&prog);
+  *code = buf;
+  *code_bytes = n;
+  return FK_OK;
+}
+
+void fk_rtc_free(void *p) { free(p); }
 
 int fk_module_unload(fk_module *m) {
   if (!m) return fail(nullptr, FK_ERR_ARG, "fk_module_unload: null module");

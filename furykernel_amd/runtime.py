@@ -28,6 +28,7 @@ STATUS_NAMES = {
     -4: "FK_ERR_NOT_FOUND",
     -5: "FK_ERR_STATE",
     -6: "FK_ERR_OOM",
+    -7: "FK_ERR_COMPILE",
 }
 
 # Every entry point of include/fkrocm.h: (name, restype, argtypes).
@@ -136,6 +137,9 @@ ENTRY_POINTS: list[tuple[str, object, list]] = [
     ("fk_table_enqueue", _int, [_vp, _u32, _u32, _vp]),
     ("fk_attend_decode", _int, [_vp, _vp, _vp]),
     ("fk_attend_decode_noalloc", _int, [_vp, _vp, _vp]),
+    ("fk_rtc_compile", _int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), _int, _PP,
+                              ctypes.POINTER(_sz), ctypes.POINTER(ctypes.c_char_p)]),
+    ("fk_rtc_free", None, [_vp]),
 ]
 
 

@@ -43,7 +43,8 @@ enum {
   FK_ERR_RANGE = -3,     /* a copy or launch outside what was allocated or allowed */
   FK_ERR_NOT_FOUND = -4, /* an entry point the module lacks, a missing file */
   FK_ERR_STATE = -5,     /* a call out of order (graph capture not begun, ...) */
-  FK_ERR_OOM = -6        /* device or arena memory exhausted */
+  FK_ERR_OOM = -6,       /* device or arena memory exhausted */
+  FK_ERR_COMPILE = -7    /* hipRTC refused a translation unit (fk_rtc_compile's log says why) */
 };
 
 typedef struct fk_ctx fk_ctx;
@@ -91,6 +92,18 @@ int fk_module_load_file(fk_ctx *ctx, const char *path, fk_module **out);
 int fk_module_unload(fk_module *mod);
 /* The kernel `entry` (a `LoweredKernel`'s `lkEntry`). */
 int fk_function(fk_module *mod, const char *entry, fk_fn **out);
+
+/* hipRTC: a lowered translation unit's HIP source (the `Lowered`'s
+ * `loweredSource`, src/FuryKernel/Backend.hs:37-44, as the IR target of
+ * furykernel_amd/ir/rocm.py emits it) compiled for the device at run time, as
+ * the reference's runtimes compile a backend's source (Backend.hs:4-11).
+ * Needs no device or context.  On success `*code` is a code object of
+ * `*code_bytes` for fk_module_load; on FK_ERR_COMPILE, `*log` (if `log` is
+ * given) holds the compiler's messages.  Both are the caller's to free with
+ * fk_rtc_free.  Failures are reported by fk_last_error(NULL). */
+int fk_rtc_compile(const char *source, const char *name, const char *const *options, int n_options, void **code,
+                   size_t *code_bytes, char **log);
+void fk_rtc_free(void *p);
 
 /* Device memory. -------------------------------------------------------------
  * A buffer is a handle on device memory with its size; its device address is

@@ -848,3 +848,46 @@ uint64_t fkref_argmax_keyed(const float *x, int n) {
   }
   return best;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Element-wise numerics for the IR interpreter                              */
+
+void fkref_widen_f16_n(const uint16_t *h, float *y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = fkref_widen_f16(h[i]);
+}
+
+void fkref_widen_bf16_n(const uint16_t *b, float *y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = fkref_widen_bf16(b[i]);
+}
+
+void fkref_narrow_f16_n(const float *x, uint16_t *y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = fkref_narrow_f16(x[i]);
+}
+
+void fkref_narrow_bf16_n(const float *x, uint16_t *y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = fkref_narrow_bf16(x[i]);
+}
+
+void fkref_narrow_f16_f64_n(const double *x, uint16_t *y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = fkref_narrow_f16_f64(x[i]);
+}
+
+/* IEEE 754's fusedMultiplyAdd: C's fmaf rounds the exact a * b + c once
+ * (Interp.hs:872-891); a NaN result is the quiet NaN with no payload. */
+void fkref_fma_f32_n(const float *a, const float *b, const float *c, float *y, size_t n) {
+  for (size_t i = 0; i < n; i++) {
+    const float r = fmaf(a[i], b[i], c[i]);
+    y[i] = isnan(r) ? float_of(0x7FC00000u) : r;
+  }
+}
+
+void fkref_unary_f64_n(int op, const double *x, double *y, size_t n) {
+  for (size_t i = 0; i < n; i++) {
+    switch (op) {
+      case FKREF_RSQRT: y[i] = 1.0 / sqrt(x[i]); break;
+      case FKREF_EXP: y[i] = exp(x[i]); break;
+      case FKREF_LOG: y[i] = log(x[i]); break;
+      default: y[i] = tanh(x[i]); break;
+    }
+  }
+}

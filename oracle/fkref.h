@@ -156,6 +156,20 @@ float fkref_gelu_tanh(float a);
 float fkref_softcap(float x, float cap);
 int fkref_act_mul(const float *a, const float *b, float *y, int n, int act);
 
+/* Element-wise forms of the numerics, for the IR interpreter (oracle/interp.py):
+ * src/FuryKernel/Numerics.hs's conversions, IEEE 754's fusedMultiplyAdd of
+ * binary32 (C's fmaf, one rounding), and rsqrt, exp, log and tanh of binary64
+ * by the platform's libm, as the reference's interpreter computes them
+ * (src/FuryKernel/Interp.hs:828-854). */
+void fkref_widen_f16_n(const uint16_t *h, float *y, size_t n);
+void fkref_widen_bf16_n(const uint16_t *b, float *y, size_t n);
+void fkref_narrow_f16_n(const float *x, uint16_t *y, size_t n);
+void fkref_narrow_bf16_n(const float *x, uint16_t *y, size_t n);
+void fkref_narrow_f16_f64_n(const double *x, uint16_t *y, size_t n);
+void fkref_fma_f32_n(const float *a, const float *b, const float *c, float *y, size_t n);
+enum { FKREF_RSQRT = 0, FKREF_EXP = 1, FKREF_LOG = 2, FKREF_TANH = 3 };
+void fkref_unary_f64_n(int op, const double *x, double *y, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

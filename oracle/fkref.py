@@ -77,6 +77,13 @@ def lib() -> ctypes.CDLL:
             "fkref_silu_mul": (_i, [_vp, _vp, _vp, _i]),
             "fkref_route": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
             "fkref_combine_ranks": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+            "fkref_widen_f16_n": (None, [_vp, _vp, ctypes.c_size_t]),
+            "fkref_widen_bf16_n": (None, [_vp, _vp, ctypes.c_size_t]),
+            "fkref_narrow_f16_n": (None, [_vp, _vp, ctypes.c_size_t]),
+            "fkref_narrow_bf16_n": (None, [_vp, _vp, ctypes.c_size_t]),
+            "fkref_narrow_f16_f64_n": (None, [_vp, _vp, ctypes.c_size_t]),
+            "fkref_fma_f32_n": (None, [_vp, _vp, _vp, _vp, ctypes.c_size_t]),
+            "fkref_unary_f64_n": (None, [_i, _vp, _vp, ctypes.c_size_t]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
