@@ -512,6 +512,7 @@ def main_kernels(args) -> int:
                                     "frac": round(nbytes / best[1] / 1e3 / HBM_PEAK_GBPS, 4)}
     for b in bufs:
         b.free()
+    table.update(ir_gemv_table(dev, timed, copies_of))
 
     head = table["matvec_f32_4096x4096"]
     line = {
@@ -521,8 +522,9 @@ def main_kernels(args) -> int:
         "data": "synthetic: N(0, 1) matrices, vectors and rows generated on the device; int8 weights a fixed "
                 "byte pattern",
         "config": {"workload": "standalone kernels: f32 matvec 4096 x 4096, RMSNorm and row softmax over 64 x 4096 "
-                               "f32, int8 weight-only matvec 8192 x 8192 (per-row scales, f16 x); each launch on "
-                               "its own copy of the inputs (512 MB of copies)"},
+                               "f32, int8 weight-only matvec 8192 x 8192 (per-row scales, f16 x), and the IR "
+                               "target's bf16 GEMV family (lowered to HIP, compiled by hipRTC) at 8192 x 2048 and "
+                               "2048 x 8192; each launch on its own copy of the inputs (512 MB of copies)"},
         "roofline": {"kernel": head["kernel"], "bound": "hbm", "achieved": head["gbps"], "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": head["frac"], "traffic": None, "avg_launch_us": head["avg_us"],
                      "bytes_per_launch": head["bytes"]},
@@ -531,6 +533,57 @@ def main_kernels(args) -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+# The IR target's bf16 GEMV family at the 1B decode's FFN shapes: a few
+# variants each (rows a SIMD group, threads, pack, split-K).
+IR_GEMV = {(8192, 2048): [(4, 256, 8, 2), (2, 256, 8, 1), (2, 1024, 8, 4), (2, 512, 8, 2)],
+           (2048, 8192): [(2, 1024, 8, 4), (1, 1024, 8, 4), (1, 512, 8, 2), (2, 512, 8, 2)]}
+
+
+def ir_gemv_table(dev, timed, copies_of) -> dict:
+    """The reference's bf16 GEMV family (test/Test/FuryKernel/Gemv.hs) built
+    as IR, lowered by the MI355X backend to HIP and compiled by hipRTC: each
+    shape's best variant, each launch on its own copy of W (bf16 N(0, 1)
+    halves' bits), algorithmic bytes W + x + y."""
+    import numpy as np
+
+    from furykernel_amd.ir import rocm
+    from furykernel_amd.ir.build import ROCM
+    from furykernel_amd.ir.gate import check
+    from furykernel_amd.ir.gemv import GemvShape, GemvVariant, gemv
+    from furykernel_amd.ir.runtime import Unit
+
+    kernels = []
+    for (n, k), vs in IR_GEMV.items():
+        for r, t, p, s in vs:
+            name = f"ir_gemv_bf16_n{n}_k{k}_r{r}_t{t}_p{p}_s{s}"
+            kern, problems = gemv(ROCM, name, GemvShape(n, k, 1), GemvVariant(r, t, p, s))
+            assert not problems, problems
+            kernels.append(((n, k), name, check(kern, ROCM)))
+    unit = Unit(dev, rocm.lower([c for _, _, c in kernels]), "ir_gemv.hip")
+    rng = np.random.default_rng(11)
+    out = {}
+    for (n, k) in IR_GEMV:
+        wbits = (rng.standard_normal(n * k).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        ws = [dev.upload(wbits) for _ in range(copies_of(n * k * 2))]
+        x = dev.upload((rng.standard_normal(k).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+        y = dev.alloc(n * 2)
+        nbytes = n * k * 2 + k * 2 + n * 2
+        best = None
+        for shape, name, _ in kernels:
+            if shape != (n, k):
+                continue
+            us = timed([lambda w=w, name=name: unit.launch(name, {}, {"x": x, "w": w, "y": y}) for w in ws], 20)
+            log(f"{name}: {us:.2f} us a launch, {nbytes / us / 1e3:.1f} GB/s")
+            if best is None or us < best[1]:
+                best = (name, us)
+        out[f"ir_gemv_bf16_{n}x{k}"] = {"kernel": best[0], "avg_us": round(best[1], 3), "bytes": nbytes,
+                                         "gbps": round(nbytes / best[1] / 1e3, 1),
+                                         "frac": round(nbytes / best[1] / 1e3 / HBM_PEAK_GBPS, 4)}
+        for b in ws + [x, y]:
+            b.free()
+    return out
 
 
 def matvec_cpu_baseline(seconds: float) -> dict:

@@ -15,6 +15,11 @@ The pieces, from the bottom:
   one row, and of many rows on the matrix cores).
 * ``engine`` — runs a plan's steps on the GPU, its state resident in HBM;
   ``decode`` and ``prefill`` hold a session over it.
+* ``ir`` — the kernel IR, its builder and gate, and the MI355X backend that
+  lowers checked kernels to HIP compiled at run time by hipRTC (the
+  reference's ``Backend``), with their launcher.
+* ``variant``, ``selection``, ``tuning`` — the GEMV families' variant spaces,
+  the committed selections and the tuner that writes them.
 
 Nothing here computes on the CPU in place of the GPU: without the native
 library or a GPU, the runtime raises.

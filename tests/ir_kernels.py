@@ -119,88 +119,16 @@ def through_blocks(caps, distinct: bool = True, apart: bool = True):
 
 
 # ---------------------------------------------------------------------------
-# test/Test/FuryKernel/Gemv.hs: y = W x, bf16, f32 accumulation, baked shape
+# test/Test/FuryKernel/Gemv.hs: the bf16 GEMV family, furykernel_amd/ir/gemv.py
 
-@dataclass(frozen=True)
-class GemvShape:
-    outputs: int
-    inputs: int
-    batch: int
-
-
-@dataclass(frozen=True)
-class GemvVariant:
-    rows_per_simd: int
-    threads: int
-    pack: int
-    split: int
+from furykernel_amd.ir.gemv import GemvShape, GemvVariant  # noqa: E402
+from furykernel_amd.ir.gemv import gemv as _gemv  # noqa: E402
 
 
 def gemv(caps, name: str, sh: GemvShape, v: GemvVariant):
-    n, kk, m = sh.outputs, sh.inputs, sh.batch
-    r, s = v.rows_per_simd, v.split
-    width = caps.simd_width
-    simds = v.threads // width
-    row_groups = simds // s
-    rows_per_group = row_groups * r
-    per_group = rows_per_group * m
-    packs = kk // v.pack
-    chains = range(v.pack // 4)
-    k = KernelBuilder(name, caps)
-    x = k.buffer("x", R, BF16, m * kk)
-    w = k.buffer("w", R, BF16, n * kk)
-    y = k.buffer("y", W, BF16, m * n)
-    k.threads(v.threads)
-    k.groups(n // rows_per_group)
-    partials = k.tg_array("partials", F32, s * per_group) if s > 1 else None
-    if s == 1:
-        split, row_group, lane = u32(0), simd_group_index, simd_lane
-    else:
-        split = k.let("split", rem(simd_group_index, s))
-        row_group = k.let("row_group", quot(simd_group_index, s))
-        lane = k.let("lane", split * width + simd_lane)
-    row0 = k.let("row0", group_index * rows_per_group + row_group * r)
-    accs = [[[k.var(f"acc{q}_{i}_{c}", f32(0.0)) for c in chains] for i in range(m)] for q in range(r)]
-    with k.for_step("j", lane, packs, s * width) as j:
-        xs = []
-        for i in range(m):
-            xp = k.load_pack(f"x{i}", v.pack, x, j if i == 0 else u32(i * packs) + j)
-            xs.append([k.let(f"xf{i}_{e}", widen(F32, xe)) for e, xe in enumerate(xp)])
-        for q in range(r):
-            wp = k.load_pack(f"w{q}", v.pack, w, (row0 + q) * packs + j)
-            ws = [k.let(f"wf{q}_{e}", widen(F32, we)) for e, we in enumerate(wp)]
-            for xv, accs_i in zip(xs, accs[q]):
-                for c, acc in zip(chains, accs_i):
-                    def prod(o, c=c, xv=xv):
-                        return xv[4 * c + o] * ws[4 * c + o]
-                    k.assign(acc, acc.get + ((prod(0) + prod(1)) + (prod(2) + prod(3))))
-    totals = []
-    for q in range(r):
-        row = []
-        for i in range(m):
-            terms = [a.get for a in accs[q][i]]
-            e = terms[0]
-            for t in terms[1:]:
-                e = e + t
-            row.append(k.simd_sum(f"total{q}_{i}", e))
-        totals.append(row)
-    if partials is None:
-        with k.when_lane(simd_lane.eq(0)):
-            for i in range(m):
-                values = [narrow(BF16, totals[q][i]) for q in range(r)]
-                if r == 1:
-                    k.store(y, u32(i * n) + row0, values[0])
-                else:
-                    k.store_pack(y, u32(i * (n // r)) + group_index * row_groups + row_group, values)
-    else:
-        with k.when_lane(simd_lane.eq(0)):
-            for q in range(r):
-                for i in range(m):
-                    k.tg_store(partials, ((row_group * r + q) * m + i) * s + split, totals[q][i])
-        combine_splits(k, "total", partials, s, per_group,
-                       lambda o, total: k.store(y, rem(o, m) * n + group_index * rows_per_group + quot(o, m),
-                                                narrow(BF16, total)))
-    return built(k)
+    kernel, problems = _gemv(caps, name, sh, v)
+    assert problems == [], problems
+    return kernel
 
 
 # ---------------------------------------------------------------------------
