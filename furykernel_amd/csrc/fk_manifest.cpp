@@ -257,6 +257,7 @@ std::vector<Entry> build() {
     p.push_back(fk_abi_param{"length", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, length))});
     p.push_back(fk_abi_param{"slots", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, slots))});
     p.push_back(fk_abi_param{"cache_bf16", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, cache_bf16))});
+    p.push_back(fk_abi_param{"staged", "u32", (uint32_t)(offsetof(S, r) + offsetof(fk_gemm_rope_params, staged))});
     add("fk_gemm_f16_qkv_rope", 256,
         {buf("a", "read", "f16"), buf("b0", "read", "f16"), buf("b1", "read", "f16"), buf("b2", "read", "f16"),
          buf("c0", "write", "f16"), buf("c1", "read_write", "f16"), buf("c2", "read_write", "f16"),
@@ -287,7 +288,16 @@ std::vector<Entry> build() {
          buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16")},
         {FK_P(S, rows, "u32"), FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"),
          FK_P(S, rotated, "u32"), FK_P(S, rope_rows, "u32"), FK_P(S, length, "u32"), FK_P(S, slots, "u32"),
-         FK_P(S, cache_bf16, "u32")},
+         FK_P(S, cache_bf16, "u32"), FK_P(S, staged, "u32")},
+        sizeof(S));
+  }
+  {
+    using S = fk_prefill_land_params;
+    add("fk_prefill_land", 256,
+        {buf("ks", "read", "f16"), buf("vs", "read", "f16"), buf("position", "read", "u32"),
+         buf("slot", "read", "u32"), buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16")},
+        {FK_P(S, rows, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, head_dim, "u32"), FK_P(S, length, "u32"),
+         FK_P(S, slots, "u32")},
         sizeof(S));
   }
   {
@@ -295,9 +305,11 @@ std::vector<Entry> build() {
     for (int g : {1, 2, 4})
       add("fk_prefill_attend_g" + std::to_string(g), 64 * g,
           {buf("qr", "read", "f16"), buf("kc", "read", "f16"), buf("vc", "read", "f16"),
-           buf("position", "read", "u32"), buf("slot", "read", "u32"), buf("out", "write", "f16")},
+           buf("position", "read", "u32"), buf("slot", "read", "u32"), buf("out", "write", "f16"),
+           buf("ks", "read", "f16"), buf("vs", "read", "f16")},
           {FK_P(S, rows, "u32"), FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, length, "u32"),
-           FK_P(S, slots, "u32"), FK_P(S, window, "u32"), FK_P(S, cache_bf16, "u32"), FK_P(S, scale, "f32")},
+           FK_P(S, slots, "u32"), FK_P(S, window, "u32"), FK_P(S, cache_bf16, "u32"), FK_P(S, scale, "f32"),
+           FK_P(S, staged, "u32"), FK_P(S, run_rows, "u32")},
           sizeof(S));
   }
   add("fk_prefill_softcap", 256, {buf("x", "read", "f32"), buf("y", "write", "f32")},
@@ -623,6 +635,30 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({"slot", 0});
       need.push_back({"rope", 0});
     }
+  } else if (std::strncmp(entry, "fk_prefill_attend_g", 19) == 0) {
+    fk_prefill_attend_params p;
+    std::memcpy(&p, params, sizeof p);
+    const uint64_t kw = (uint64_t)p.kv_heads * 64 * 2;
+    need = {{"qr", (uint64_t)p.rows * p.heads * 64 * 2},
+            {"kc", (uint64_t)p.slots * p.length * kw},
+            {"vc", (uint64_t)p.slots * p.length * kw},
+            {"position", (uint64_t)p.rows * 4},
+            {"slot", (uint64_t)p.rows * 4},
+            {"out", (uint64_t)p.rows * p.heads * 64 * 2}};
+    if (p.staged) {
+      if (p.run_rows == 0 || p.run_rows % 32 || p.rows % p.run_rows)
+        return bad(err, cap, FK_ERR_ARG, "%s: staged runs of %u rows in a step of %u (multiples of 32 that divide it)",
+                   entry, p.run_rows, p.rows);
+      need.push_back({"ks", (uint64_t)p.rows * kw});
+      need.push_back({"vs", (uint64_t)p.rows * kw});
+    }
+  } else if (std::strcmp(entry, "fk_prefill_land") == 0) {
+    fk_prefill_land_params p;
+    std::memcpy(&p, params, sizeof p);
+    const uint64_t kw = (uint64_t)p.kv_heads * p.head_dim * 2;
+    need = {{"ks", (uint64_t)p.rows * kw}, {"vs", (uint64_t)p.rows * kw}, {"position", (uint64_t)p.rows * 4},
+            {"slot", (uint64_t)p.rows * 4}, {"kc", (uint64_t)p.slots * p.length * kw},
+            {"vc", (uint64_t)p.slots * p.length * kw}};
   } else {
     // Every other kernel dereferences each of its buffers (a norm without
     // gains excepted).

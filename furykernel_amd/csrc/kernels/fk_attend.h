@@ -65,6 +65,7 @@ template <uint32_t G>
 __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc,
                                                const uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                                                const uint32_t *__restrict__ slot, uint16_t *__restrict__ out,
+                                               const uint16_t *__restrict__ kst, const uint16_t *__restrict__ vst,
                                                const fk_prefill_attend_params &p) {
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][FK_ATT_KB * 64];
   __shared__ __attribute__((aligned(16))) uint16_t vs[2][FK_ATT_KB * 64];
@@ -105,6 +106,14 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // Blocks with every key visible to every row of the block need no mask.
   const uint32_t win_lo = p.window && last_pos + 1 > p.window ? last_pos + 1 - p.window : 0;
   const size_t cache_base = ((size_t)sl * p.kv_heads + g) * p.length * 64;
+  // Staged stores (Plan.hs:41-50): the step's own rows of this sequence are
+  // not in the ring yet.  Its run of rows starts at row rf (runs of run_rows
+  // rows, consecutive positions of one slot), position start; keys from
+  // there on are read from the staging rows [rows][kv_heads][64], the
+  // earlier ones from the ring.
+  const bool staged = p.staged != 0;
+  const uint32_t rf = staged ? (r0 / p.run_rows) * p.run_rows : 0u;
+  const uint32_t start = staged ? position[rf] : 0xFFFFFFFFu;
 
   // Where lane l's transposed V reads start (see softmax_pv).
   const uint32_t tq = lane & 15;
@@ -117,15 +126,20 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // buffer, bf16 caches converted on the way (a uniform branch, so that f16
   // caches pay nothing for it).
   uint4 kreg[per], vreg[per];
-  auto fetch = [&](uint4 (&reg)[per], const uint16_t *__restrict__ cache, uint32_t kb) {
+  auto fetch = [&](uint4 (&reg)[per], const uint16_t *__restrict__ cache, const uint16_t *__restrict__ stage,
+                   uint32_t kb) {
     const uint32_t ring0 = (kb * FK_ATT_KB) % p.length;
 #pragma unroll
     for (uint32_t e = 0; e < per; e++) {
       const uint32_t u = tid + e * nthreads;
       const uint32_t key = u / 8, c8 = (u % 8) * 8;
-      const bool live = kb * FK_ATT_KB + key <= last_pos;
-      reg[e] = live ? *reinterpret_cast<const uint4 *>(cache + cache_base + (size_t)(ring0 + key) * 64 + c8)
-                    : make_uint4(0, 0, 0, 0);
+      const uint32_t t = kb * FK_ATT_KB + key;
+      const bool live = t <= last_pos;
+      // A staged row's index, clamped into the step's rows.
+      const uint32_t srow = min(rf + (t - min(t, start)), p.rows - 1);
+      const uint16_t *src = staged && t >= start ? stage + ((size_t)srow * p.kv_heads + g) * 64 + c8
+                                                 : cache + cache_base + (size_t)(ring0 + key) * 64 + c8;
+      reg[e] = live ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
     }
   };
   auto stash_k = [&](uint32_t buf) {
@@ -249,16 +263,16 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // registers, and go into the other pair after (every wavefront left it at
   // the last barrier); one barrier a block.
   const uint32_t kb0 = first_pos / FK_ATT_KB, kb_last = last_pos / FK_ATT_KB;
-  fetch(kreg, kc, kb0);
-  fetch(vreg, vc, kb0);
+  fetch(kreg, kc, kst, kb0);
+  fetch(vreg, vc, vst, kb0);
   stash_k(0);
   stash_v(0);
   __syncthreads();
   for (uint32_t kb = kb0; kb <= kb_last; kb++) {
     const uint32_t buf = (kb - kb0) & 1;
     if (kb < kb_last) {
-      fetch(kreg, kc, kb + 1);
-      fetch(vreg, vc, kb + 1);
+      fetch(kreg, kc, kst, kb + 1);
+      fetch(vreg, vc, vst, kb + 1);
     }
     step(kb, buf);
     if (kb < kb_last) {
@@ -287,8 +301,8 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   extern "C" __global__ void __launch_bounds__(64 * G) fk_prefill_attend_g##G(                         \
       const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,       \
       const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot, uint16_t *__restrict__ out,   \
-      fk_prefill_attend_params p) {                                                                             \
-    prefill_attend<G>(qr, kc, vc, position, slot, out, p);                                                      \
+      const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs, fk_prefill_attend_params p) {          \
+    prefill_attend<G>(qr, kc, vc, position, slot, out, ks, vs, p);                                              \
   }
 FK_PREFILL_ATTEND(1)
 FK_PREFILL_ATTEND(2)

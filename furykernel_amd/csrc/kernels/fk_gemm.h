@@ -310,16 +310,17 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
     const bool turn = anchor != 2;
     const uint32_t head0 = (n0 + wn * 128) / 64;
     uint16_t *const dst = reinterpret_cast<uint16_t *>(anchor == 0 ? c0 : (anchor == 1 ? c1 : c2));
-    const size_t hstride = anchor == 0 ? 64 : (size_t)rp.length * 64;  // halves from head to head
+    // halves from head to head: q's rows and staged k, v rows hold a row's heads side by side
+    const size_t hstride = anchor == 0 || rp.staged ? 64 : (size_t)rp.length * 64;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t row = m + 16 * i;
       const uint32_t pos = position[row];
       const uint32_t sl = min(slot[row], rp.slots - 1);
       const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
-      uint16_t *const base = anchor == 0
-                                 ? dst + (size_t)row * p.ldc[0] + head0 * 64
-                                 : dst + (((size_t)sl * rp.kv_heads + head0) * rp.length + pos % rp.length) * 64;
+      uint16_t *const base = anchor == 0 ? dst + (size_t)row * p.ldc[0] + head0 * 64
+                             : rp.staged ? dst + ((size_t)row * rp.kv_heads + head0) * 64
+                                         : dst + (((size_t)sl * rp.kv_heads + head0) * rp.length + pos % rp.length) * 64;
 #pragma unroll
       for (int jp = 0; jp < 2; jp++)
 #pragma unroll

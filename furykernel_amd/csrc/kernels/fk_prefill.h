@@ -5,6 +5,7 @@
 //   fk_prefill_gather      x = embed[token] · factor, f32 rows
 //   fk_prefill_norm_pack   RMSNorm of f32 rows into f16 in the tile layout
 //                          (the GEMM's A)
+//   fk_prefill_land        staged k and v rows landed in the ring
 //   fk_prefill_rope_store  q RoPE'd into f16 rows; k RoPE'd and v stored into
 //                          the caches at each row's position
 //   fk_prefill_softcap     a softcap over rows (the head's, before the argmax)
@@ -171,12 +172,35 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store(
     } else {
       const uint32_t f = e < qw + kw ? e - qw : e - qw - kw;
       const uint32_t h = f / d, i = f % d;
-      const size_t at = (((size_t)sl * p.kv_heads + h) * p.length + pos % p.length) * d + i;
+      const size_t at = p.staged ? ((size_t)row * p.kv_heads + h) * d + i
+                                 : (((size_t)sl * p.kv_heads + h) * p.length + pos % p.length) * d + i;
       if (e < qw + kw)
         kc[at] = fk::narrow_cache(fk::rope_elem(kx + h * d, i, d, p.rotated, cs), bf16);
       else
         vc[at] = fk::narrow_cache(vx[f], bf16);
     }
+  }
+}
+
+// Staged rows landed (Plan.hs:41-50): row r's k and v heads, as the caches
+// hold them, from the staging rows into the ring at (slot, head, position
+// mod length).  One threadgroup a row; a copy of 16-bit elements.
+extern "C" __global__ void __launch_bounds__(256) fk_prefill_land(
+    const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs, const uint32_t *__restrict__ position,
+    const uint32_t *__restrict__ slot, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    fk_prefill_land_params p) {
+  const uint32_t row = blockIdx.x;
+  const uint32_t kw = p.kv_heads * p.head_dim;
+  const uint32_t pos = position[row];
+  const uint32_t sl = min(slot[row], p.slots - 1);
+  for (uint32_t e = threadIdx.x; e < 2 * kw; e += blockDim.x) {
+    const uint32_t f = e < kw ? e : e - kw;
+    const uint32_t h = f / p.head_dim, i = f % p.head_dim;
+    const size_t at = (((size_t)sl * p.kv_heads + h) * p.length + pos % p.length) * p.head_dim + i;
+    if (e < kw)
+      kc[at] = ks[(size_t)row * kw + f];
+    else
+      vc[at] = vs[(size_t)row * kw + f];
   }
 }
 

@@ -50,6 +50,7 @@ _STRUCTS = {
     "fk_prefill_attend_g2": K.PrefillAttendParams,
     "fk_prefill_attend_g4": K.PrefillAttendParams,
     "fk_prefill_argmax": K.PrefillArgmaxParams,
+    "fk_prefill_land": K.PrefillLandParams,
 }
 
 

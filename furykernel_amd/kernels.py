@@ -99,7 +99,7 @@ class GemmQkvParams(ctypes.Structure):
     """fk_gemm_qkv_params: the GEMM's parameters, then the RoPE and caches'."""
     _fields_ = GemmParams._fields_ + [("kv_heads", ctypes.c_uint32), ("rope_rows", ctypes.c_uint32),
                                       ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32),
-                                      ("cache_bf16", ctypes.c_uint32)]
+                                      ("cache_bf16", ctypes.c_uint32), ("staged", ctypes.c_uint32)]
 
 
 class PrefillGatherParams(ctypes.Structure):
@@ -115,13 +115,20 @@ class PrefillNormParams(ctypes.Structure):
 class PrefillRopeParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
                 ("head_dim", ctypes.c_uint32), ("rotated", ctypes.c_uint32), ("rope_rows", ctypes.c_uint32),
-                ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32), ("cache_bf16", ctypes.c_uint32)]
+                ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32), ("cache_bf16", ctypes.c_uint32),
+                ("staged", ctypes.c_uint32)]
 
 
 class PrefillAttendParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
                 ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32), ("window", ctypes.c_uint32),
-                ("cache_bf16", ctypes.c_uint32), ("scale", ctypes.c_float)]
+                ("cache_bf16", ctypes.c_uint32), ("scale", ctypes.c_float), ("staged", ctypes.c_uint32),
+                ("run_rows", ctypes.c_uint32)]
+
+
+class PrefillLandParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+                ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32)]
 
 
 class PrefillSoftcapParams(ctypes.Structure):
@@ -297,8 +304,11 @@ ABIS: dict[str, KernelAbi] = {
     "fk_prefill_rope_store": KernelAbi("fk_prefill_rope_store", ("q", "k", "v", "position", "slot", "rope", "qr",
                                                                  "kc", "vc"), PrefillRopeParams),
     **{f"fk_prefill_attend_g{g}": KernelAbi(f"fk_prefill_attend_g{g}", ("qr", "kc", "vc", "position", "slot",
-                                                                        "out"), PrefillAttendParams, 64 * g)
+                                                                        "out", "ks", "vs"), PrefillAttendParams,
+                                            64 * g)
        for g in (1, 2, 4)},
+    "fk_prefill_land": KernelAbi("fk_prefill_land", ("ks", "vs", "position", "slot", "kc", "vc"),
+                                 PrefillLandParams, 256),
     "fk_prefill_argmax": KernelAbi("fk_prefill_argmax", ("x", "out"), PrefillArgmaxParams, 256),
     "fk_prefill_softcap": KernelAbi("fk_prefill_softcap", ("x", "y"), PrefillSoftcapParams, 256),
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
@@ -485,7 +495,8 @@ class Kernels:
         _need(position, rows * 4, "position", entry)
         _need(slot, rows * 4, "slot", entry)
         _need(out, rows * heads * 64 * 2, "out", entry)
-        bound = {"qr": qr.ptr, "kc": kc.ptr, "vc": vc.ptr, "position": position.ptr, "slot": slot.ptr, "out": out.ptr}
+        bound = {"qr": qr.ptr, "kc": kc.ptr, "vc": vc.ptr, "position": position.ptr, "slot": slot.ptr, "out": out.ptr,
+                 "ks": 0, "vs": 0}
         self.launch(entry, (rows // 32) * kv_heads, 64 * (heads // kv_heads), bound,
                     PrefillAttendParams(rows, heads, kv_heads, length, slots, window, int(cache_bf16), scale), stream)
 
@@ -637,4 +648,6 @@ def launch_reads(entry: str, params: dict) -> set[str]:
         return need
     if entry == "fk_rmsnorm_f32" or entry.startswith("fk_prefill_norm_pack"):
         return set(abi.buffers) - ({"gamma"} if not params.get("has_gamma") else set())
+    if entry.startswith("fk_prefill_attend_g"):
+        return set(abi.buffers) - (set() if params.get("staged") else {"ks", "vs"})
     return set(abi.buffers)

@@ -21,8 +21,16 @@ cores).  Each value is made in the layout its readers take:
   q, k, v are never f32 rows in HBM;
 - the greedy token is ``fk_prefill_argmax`` over each row's logits.
 
-Steps of other shapes (staged KV stores, a gathered Linear input, segments
-narrower than the row) are refused with ``LoweringError``.  Pure host logic:
+Staged KV stores (the ring has no room for a step's rows: Plan.hs:41-50)
+store each row's k and v heads, as the cache holds them, into staging rows
+(``staged:`` buffers, [rows][kv_heads][64]) instead of the ring; the
+attention reads a sequence's positions from its run's first row on from
+there and the rest from the ring; and the step that lands them copies them
+into the ring (``fk_prefill_land``).  A staged step's rows come in runs of
+``run_rows`` rows, each one sequence's consecutive positions.
+
+Steps of other shapes (a gathered Linear input, segments narrower than the
+row) are refused with ``LoweringError``.  Pure host logic:
 the lowering a ``Backend Rocm`` does for a step of many rows
 (src/FuryKernel/Backend.hs:29-101, src/FuryKernel/Program/Plan.hs:270-300 for
 the sequence rows of a step).
@@ -51,14 +59,18 @@ QBLOCK = 32                        # rows an attention threadgroup takes
 HEAD_DIM = 64                      # the attention kernel's head dimension
 
 
-def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int) -> Lowered:
+def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int, run_rows: Optional[int] = None) -> Lowered:
     """The launches of every step of the plan for a step of `rows` rows (a
     multiple of 256: the sequences' rows one after another, each sequence's
-    run a multiple of 32 rows)."""
+    run a multiple of 32 rows; `run_rows` rows each where the plan stages
+    KV stores, the plan's sequence rows)."""
     if rows <= 0 or rows % SLAB:
         raise LoweringError(f"a step of {rows} rows; the prefill kernels take multiples of {SLAB}")
+    run_rows = rows if run_rows is None else run_rows
+    if run_rows <= 0 or run_rows % QBLOCK or rows % run_rows:
+        raise LoweringError(f"runs of {run_rows} rows in a step of {rows}: multiples of {QBLOCK} that divide it")
     out = Lowered(checked.program, plan, rows)
-    _Prefill(out).run()
+    _Prefill(out, run_rows).run()
     _fuse_qkv_rope(out)
     return out
 
@@ -96,7 +108,7 @@ def _fuse_qkv_rope(out: Lowered) -> None:
         bind = dict(gm.bind, c0=rs.bind["qr"], c1=rs.bind["kc"], c2=rs.bind["vc"], position=rs.bind["position"],
                     slot=rs.bind["slot"], rope=rs.bind["rope"])
         params = dict(gm.params, kv_heads=p["kv_heads"], rope_rows=p["rope_rows"], length=p["length"],
-                      slots=p["slots"], cache_bf16=p["cache_bf16"])
+                      slots=p["slots"], cache_bf16=p["cache_bf16"], staged=p["staged"])
         launches[j] = Launch(gm.step, "fk_gemm_f16_qkv_rope", gm.groups, gm.threads, bind, params, {},
                              gm.lds_bytes)
         del launches[i]
@@ -105,8 +117,11 @@ def _fuse_qkv_rope(out: Lowered) -> None:
 
 
 class _Prefill:
-    def __init__(self, out: Lowered):
+    def __init__(self, out: Lowered, run_rows: int):
         self.out = out
+        self.run_rows = run_rows
+        self.staged: set = set()   # KvStore nodes the plan stages
+        self.landing: dict = {}    # KvStore node id -> (staging buffer, ring buffer)
         self.p = out.program
         self.rows = out.rows
         self.producer = {v: n for n in self.p.nodes for v in n.outputs}
@@ -129,6 +144,8 @@ class _Prefill:
             self.step(step)
         if self.pending:
             raise LoweringError(f"KV stores {[n.name for n in self.pending]} with no attention after them")
+        if self.landing:
+            raise LoweringError(f"staged KV stores {sorted(self.landing)} never landed")
         for o in self.p.outputs:
             if o.value not in self.rows_of:
                 raise LoweringError(f"output {o.name} is never made as rows")
@@ -248,9 +265,6 @@ class _Prefill:
 
     def step(self, step: Step) -> None:
         kinds = {w.kind for w in step.work}
-        if STAGE in kinds or LAND in kinds:
-            raise LoweringError(f"{step.name}: staged KV stores (the ring has no room for the step's rows); the "
-                                f"prefill lowering stores in place")
         anchors = [self.p.node(w.node) for w in step.work if w.kind == ANCHOR]
         if anchors and all(isinstance(a.op, Linear) for a in anchors):
             return self.linear_step(step, anchors)
@@ -258,9 +272,9 @@ class _Prefill:
             return self.attend_step(step, anchors[0])
         if anchors:
             raise LoweringError(f"{step.name}: anchors of mixed or unknown kinds")
-        if EFFECT in kinds:
+        if EFFECT in kinds or STAGE in kinds:
             return self.store_step(step)
-        if COMBINE in kinds:
+        if COMBINE in kinds or LAND in kinds:
             return self.combine_step(step)
         return self.light_step(step)
 
@@ -364,10 +378,12 @@ class _Prefill:
     def store_step(self, step: Step) -> None:
         for w in step.work:
             node = self.p.node(w.node)
-            if w.kind == EFFECT:
+            if w.kind in (EFFECT, STAGE):
                 if not isinstance(node.op, KvStore):
                     raise LoweringError(f"{step.name}: an effect other than a KV store")
                 self.pending.append(node)
+                if w.kind == STAGE:
+                    self.staged.add(node.id)
             elif w.kind != RECOMPUTE or not isinstance(node.op, Rope):
                 raise LoweringError(f"{step.name}: {w.kind} {node.name} in a store step")
 
@@ -404,6 +420,10 @@ class _Prefill:
         if set(stores) != {op.to.keys, op.to.values} or len(self.pending) != 2:
             raise LoweringError(f"{step.name}: the attention's key and value stores are not the steps before it")
         self.pending = []
+        staged = {stores[c].id in self.staged for c in stores}
+        if len(staged) != 1:
+            raise LoweringError(f"{step.name}: one of the attention's stores staged, the other not")
+        staged = staged.pop()
         k_raw, k_rope = self.roped(step, stores[op.to.keys].op.x)
         q_raw, q_rope = self.roped(step, op.q)
         v_raw = stores[op.to.values].op.x
@@ -418,28 +438,55 @@ class _Prefill:
             raise LoweringError(f"{step.name}: q, k, v rows of other widths than the heads'")
         pos, seq = self.ints(op.to.positions), self.ints(op.to.sequences)
         qr = self.out.buffer(f"qrot:{self.p.value(op.q).name}", "f16", heads * HEAD_DIM * self.rows)
+        ks = vs = None
+        if staged:
+            elem = "bf16" if kbf else "f16"
+            ks = self.out.buffer(f"staged:{kname[len('cache:'):]}", elem, self.rows * kvh * HEAD_DIM)
+            vs = self.out.buffer(f"staged:{vname[len('cache:'):]}", elem, self.rows * kvh * HEAD_DIM)
+            self.landing[stores[op.to.keys].id] = (ks, kname)
+            self.landing[stores[op.to.values].id] = (vs, vname)
         self.launch(step, "fk_prefill_rope_store", self.rows, 256,
                     {"q": self.rows_value(step, q_raw), "k": self.rows_value(step, k_raw),
                      "v": self.rows_value(step, v_raw), "position": pos, "slot": seq,
-                     "rope": self.rope(rs, HEAD_DIM, klay.length), "qr": qr, "kc": kname, "vc": vname},
+                     "rope": self.rope(rs, HEAD_DIM, klay.length), "qr": qr, "kc": ks or kname, "vc": vs or vname},
                     {"rows": self.rows, "heads": heads, "kv_heads": kvh, "head_dim": HEAD_DIM, "rotated": rs.rotated,
-                     "rope_rows": klay.length, "length": klay.length, "slots": klay.slots, "cache_bf16": int(kbf)})
+                     "rope_rows": klay.length, "length": klay.length, "slots": klay.slots, "cache_bf16": int(kbf),
+                     "staged": int(staged)})
         outv = anchor.outputs[0]
         obuf = self.value_tiled(outv)
         self.tiled_of[outv] = obuf
         g = heads // kvh
         self.launch(step, f"fk_prefill_attend_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
-                    {"qr": qr, "kc": kname, "vc": vname, "position": pos, "slot": seq, "out": obuf},
+                    {"qr": qr, "kc": kname, "vc": vname, "position": pos, "slot": seq, "out": obuf,
+                     "ks": ks, "vs": vs},
                     {"rows": self.rows, "heads": heads, "kv_heads": kvh, "length": klay.length,
                      "slots": klay.slots, "window": spec.window or 0, "cache_bf16": int(kbf),
-                     "scale": float(np.float32(spec.scale))})
+                     "scale": float(np.float32(spec.scale)), "staged": int(staged),
+                     "run_rows": self.run_rows if staged else 0})
 
     def combine_step(self, step: Step) -> None:
-        # The prefill attention finishes its rows in one launch: nothing to combine.
+        # The prefill attention finishes its rows in one launch: nothing to
+        # combine; staged stores land here, after the last attention reading
+        # the ring (Plan.hs:41-50).
+        lands = []
         for w in step.work:
             node = self.p.node(w.node)
-            if w.kind != COMBINE or not isinstance(node.op, Attend) or node.outputs[0] not in self.tiled_of:
+            if w.kind == LAND and isinstance(node.op, KvStore) and node.id in self.landing:
+                lands.append(node)
+            elif w.kind != COMBINE or not isinstance(node.op, Attend) or node.outputs[0] not in self.tiled_of:
                 raise LoweringError(f"{step.name}: {w.kind} {node.name} in a combine step")
+        if not lands:
+            return
+        if len(lands) != 2 or lands[0].op.at.positions != lands[1].op.at.positions or \
+                lands[0].op.at.sequences != lands[1].op.at.sequences:
+            raise LoweringError(f"{step.name}: lands of other than one key and value pair")
+        (ks, kname), (vs, vname) = (self.landing.pop(n.id) for n in lands)
+        _, lay, _ = self.cache(lands[0].op.at.cache)
+        self.launch(step, "fk_prefill_land", self.rows, 256,
+                    {"ks": ks, "vs": vs, "position": self.ints(lands[0].op.at.positions),
+                     "slot": self.ints(lands[0].op.at.sequences), "kc": kname, "vc": vname},
+                    {"rows": self.rows, "kv_heads": lay.kv_heads, "head_dim": lay.head_dim, "length": lay.length,
+                     "slots": lay.slots})
 
     def light_step(self, step: Step) -> None:
         rec = self.recomputes(step)
@@ -490,7 +537,7 @@ class PrefillSession:
     step's (the same names, layout and rounding)."""
 
     def __init__(self, device, kernels, dims, seqs: int, seq_rows: int, layers: Optional[int] = None,
-                 embed: bool = True, rope_rotated: Optional[int] = None):
+                 embed: bool = True, rope_rotated: Optional[int] = None, position_bound: Optional[int] = None):
         from .engine import Engine
         from .program.check import check_program
         from .program.decoder import decoder_step
@@ -501,15 +548,18 @@ class PrefillSession:
         self.device, self.kernels, self.dims = device, kernels, dims
         self.seqs, self.seq_rows, self.rows = seqs, seq_rows, seqs * seq_rows
         self.embed = embed
-        self.program = decoder_step(dims, "prefill", embed, layers, position_bound=seq_rows,
+        # Positions below `position_bound` (the rows' own, seq_rows, by
+        # default): a bound past what the ring holds beyond a step's rows
+        # makes the plan stage the KV stores.
+        self.program = decoder_step(dims, "prefill", embed, layers, position_bound=position_bound or seq_rows,
                                     rope_rotated=rope_rotated)
         self.checked = check_program(self.program)
         self.plan = plan(PlanOptions(sequence_rows=seq_rows), self.checked)
-        self.lowered = lower_prefill(self.checked, self.plan, self.rows)
+        self.lowered = lower_prefill(self.checked, self.plan, self.rows, run_rows=seq_rows)
         self.engine = Engine(device, kernels, self.lowered)
         positions = np.tile(np.arange(seq_rows, dtype=np.uint32), seqs)
         slots = np.repeat(np.arange(seqs, dtype=np.uint32), seq_rows)
-        check_rows(positions, slots)
+        check_rows(positions, slots, seq_rows)
         self.engine.set_ints("position", positions, seq_rows)
         self.engine.set_ints("slot", slots, dims.slots)
 
@@ -544,6 +594,10 @@ class PrefillSession:
 
     def graph(self, stream=None):
         return self.engine.capture(stream=stream)
+
+    @property
+    def staged(self) -> bool:
+        return any(L.entry == "fk_prefill_land" for L in self.lowered.launches)
 
     def logits(self) -> np.ndarray:
         return self.engine.read("value:logits").reshape(self.rows, -1)

@@ -280,6 +280,7 @@ typedef struct fk_gemm_rope_params {
   uint32_t length;    /* ring length */
   uint32_t slots;
   uint32_t cache_bf16;
+  uint32_t staged;    /* k and v rows into staging rows [rows][kv_heads][64] (the plan's staged stores) */
 } fk_gemm_rope_params;
 
 typedef struct fk_gemm_qkv_params {
@@ -313,6 +314,7 @@ typedef struct fk_prefill_rope_params {
   uint32_t length;    /* ring length */
   uint32_t slots;
   uint32_t cache_bf16;
+  uint32_t staged;    /* kc and vc are staging rows [rows][kv_heads][head_dim], the row's own */
 } fk_prefill_rope_params;
 
 typedef struct fk_prefill_attend_params {
@@ -324,7 +326,20 @@ typedef struct fk_prefill_attend_params {
   uint32_t window;   /* 0: none; else a row sees positions > position - window */
   uint32_t cache_bf16;
   float scale;
+  uint32_t staged;   /* a sequence's positions from its run's first row on are read from ks and vs */
+  uint32_t run_rows; /* staged: each sequence's run of rows in the step, a multiple of 32 */
 } fk_prefill_attend_params;
+
+/* The staged rows landed in the ring (src/FuryKernel/Program/Plan.hs:41-50):
+ * row r's kv heads from ks and vs ([rows][kv_heads][head_dim]) into kc and
+ * vc at (slot[r], head, position[r] mod length). */
+typedef struct fk_prefill_land_params {
+  uint32_t rows;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t length;
+  uint32_t slots;
+} fk_prefill_land_params;
 
 typedef struct fk_prefill_softcap_params {
   uint32_t count; /* elements */

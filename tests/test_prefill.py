@@ -93,10 +93,47 @@ def test_prefill_lowering_of_the_1b_decoder():
     assert low.launches[1].entry == "fk_prefill_norm_pack_w2048"   # the one-pass norm of rows of 2048
 
 
+def test_staged_stores_lower_to_staging_rows_reads_and_lands():
+    """Positions up to the ring's length leave no room for a step's rows
+    (Plan.hs:41-50): the plan stages the stores, the QKV epilogue writes the
+    staging rows, the attention reads them, and the combine step lands them."""
+    from furykernel_amd import kernels as K, runtime
+    from furykernel_amd.engine import check_launch, params_struct
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill"))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
+    entries = [l.entry for l in low.launches]
+    assert entries.count("fk_prefill_land") == SMALL_PREFILL.layers
+    qkv = [l for l in low.launches if l.entry == "fk_gemm_f16_qkv_rope"]
+    att = [l for l in low.launches if l.entry.startswith("fk_prefill_attend")]
+    lands = [l for l in low.launches if l.entry == "fk_prefill_land"]
+    for q, a, land in zip(qkv, att, lands):
+        assert q.params["staged"] == 1 and q.bind["c1"].startswith("staged:") and q.bind["c2"].startswith("staged:")
+        assert a.params["staged"] == 1 and a.params["run_rows"] == 128
+        assert (a.bind["ks"], a.bind["vs"]) == (q.bind["c1"], q.bind["c2"])
+        assert (land.bind["ks"], land.bind["vs"], land.bind["kc"], land.bind["vc"]) == \
+            (a.bind["ks"], a.bind["vs"], a.bind["kc"], a.bind["vc"])
+        assert entries.index("fk_prefill_land", entries.index(a.entry)) > entries.index(a.entry)
+    assert low.buffers["staged:l0_k_cache"].count == 256 * SMALL_PREFILL.kv_heads * 64
+    # every launch through the engine's and the launch table's checks on the host
+    at, addr = 1 << 40, {}
+    for name, spec in low.buffers.items():
+        addr[name] = at
+        at += (spec.nbytes + 4095) // 4096 * 4096
+    for L in low.launches:
+        check_launch(L, low.buffers)
+        spans = [(0, 0) if L.bind.get(b) is None else (addr[L.bind[b]], low.buffers[L.bind[b]].nbytes)
+                 for b in K.ABIS[L.entry].buffers]
+        runtime.launch_check(L.entry, L.groups, L.threads, L.lds_bytes, spans, params_struct(L))
+    # in place, nothing is staged
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
+    assert "fk_prefill_land" not in [l.entry for l in low.launches]
+    assert not any(n.startswith("staged:") for n in low.buffers)
+    with pytest.raises(LoweringError, match="runs of 96"):
+        lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=96)
+
+
 def test_prefill_refuses_what_its_kernels_do_not_take():
-    with pytest.raises(LoweringError):   # positions up to the ring's length: no room, staged stores
-        c = check_program(decoder_step(SMALL_PREFILL, name="prefill"))
-        lower_prefill(c, plan(PlanOptions(sequence_rows=256), c), 256)
     with pytest.raises(LoweringError):   # rows not a multiple of 256
         c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128))
         lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 128)
