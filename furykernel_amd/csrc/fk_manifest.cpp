@@ -645,10 +645,11 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
             {"position", (uint64_t)p.rows * 4},
             {"slot", (uint64_t)p.rows * 4},
             {"out", (uint64_t)p.rows * p.heads * 64 * 2}};
+    if ((p.staged && p.run_rows == 0) || (p.run_rows && (p.run_rows % 32 || p.rows % p.run_rows)) || p.rows % 32 ||
+        p.kv_heads == 0)
+      return bad(err, cap, FK_ERR_ARG, "%s: runs of %u rows in a step of %u (multiples of 32 that divide it)", entry,
+                 p.run_rows, p.rows);
     if (p.staged) {
-      if (p.run_rows == 0 || p.run_rows % 32 || p.rows % p.run_rows)
-        return bad(err, cap, FK_ERR_ARG, "%s: staged runs of %u rows in a step of %u (multiples of 32 that divide it)",
-                   entry, p.run_rows, p.rows);
       need.push_back({"ks", (uint64_t)p.rows * kw});
       need.push_back({"vs", (uint64_t)p.rows * kw});
     }

@@ -74,9 +74,17 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & (FK_WAVE - 1);
   const uint32_t wave = tid / FK_WAVE;
+  // Heaviest first: a block's keys grow with its place in its run (a
+  // sequence's consecutive positions), so threadgroup j takes, of every run
+  // and kv head, the run's last block first, then the one before: the
+  // longest blocks start first and the short ones fill in at the end.
   const uint32_t qblocks = p.rows / 32;
-  const uint32_t r0 = (blockIdx.x % qblocks) * 32;   // the block's first row
-  const uint32_t g = blockIdx.x / qblocks;           // kv head
+  const uint32_t per_run = (p.run_rows ? p.run_rows : p.rows) / 32;  // blocks a run
+  const uint32_t runs = qblocks / per_run;
+  const uint32_t t_rank = blockIdx.x / (runs * p.kv_heads);
+  const uint32_t rest = blockIdx.x % (runs * p.kv_heads);
+  const uint32_t r0 = ((rest / p.kv_heads) * per_run + (per_run - 1 - t_rank)) * 32;  // the block's first row
+  const uint32_t g = rest % p.kv_heads;                                               // kv head
   const uint32_t h = g * G + wave;                   // this wavefront's query head
   const uint32_t p0 = position[r0];
   const uint32_t sl = min(slot[r0], p.slots - 1);

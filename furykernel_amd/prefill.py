@@ -462,7 +462,7 @@ class _Prefill:
                     {"rows": self.rows, "heads": heads, "kv_heads": kvh, "length": klay.length,
                      "slots": klay.slots, "window": spec.window or 0, "cache_bf16": int(kbf),
                      "scale": float(np.float32(spec.scale)), "staged": int(staged),
-                     "run_rows": self.run_rows if staged else 0})
+                     "run_rows": self.run_rows})
 
     def combine_step(self, step: Step) -> None:
         # The prefill attention finishes its rows in one launch: nothing to

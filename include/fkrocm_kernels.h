@@ -327,7 +327,8 @@ typedef struct fk_prefill_attend_params {
   uint32_t cache_bf16;
   float scale;
   uint32_t staged;   /* a sequence's positions from its run's first row on are read from ks and vs */
-  uint32_t run_rows; /* staged: each sequence's run of rows in the step, a multiple of 32 */
+  uint32_t run_rows; /* each sequence's run of rows in the step, a multiple of 32 dividing rows (0: one run);
+                       staged runs read their own rows from ks and vs */
 } fk_prefill_attend_params;
 
 /* The staged rows landed in the ring (src/FuryKernel/Program/Plan.hs:41-50):
