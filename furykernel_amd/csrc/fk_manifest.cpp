@@ -249,6 +249,11 @@ std::vector<Entry> build() {
          buf("c0", "write", ct), buf("c1", "write", ct), buf("c2", "write", ct), buf("r0", "read", "f32")},
         gemm_params(), sizeof(fk_gemm_params));
   }
+  add("fk_gemm_f16_store_keys", 256,
+      {buf("a", "read", "f16"), buf("b0", "read", "f16"), buf("b1", "read", "f16"), buf("b2", "read", "f16"),
+       buf("c0", "write", "f32"), buf("c1", "write", "f32"), buf("c2", "write", "f32"), buf("r0", "read", "f32"),
+       buf("keys", "write", "u64")},
+      gemm_params(), sizeof(fk_gemm_params));
   {
     using S = fk_gemm_qkv_params;
     std::vector<fk_abi_param> p = gemm_params();
@@ -318,6 +323,9 @@ std::vector<Entry> build() {
   add("fk_prefill_argmax", 256, {buf("x", "read", "f32"), buf("out", "write", "u32")},
       {FK_P(fk_prefill_argmax_params, rows, "u32"), FK_P(fk_prefill_argmax_params, width, "u32")},
       sizeof(fk_prefill_argmax_params));
+  add("fk_prefill_argmax_keys", 256, {buf("keys", "read", "u64"), buf("out", "write", "u32")},
+      {FK_P(fk_prefill_argmax_keys_params, rows, "u32"), FK_P(fk_prefill_argmax_keys_params, parts, "u32")},
+      sizeof(fk_prefill_argmax_keys_params));
 
   for (Entry &e : out) {
     e.abi.entry = e.entry.c_str();
@@ -630,6 +638,15 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({cn[j], 0});
     }
     if (std::strcmp(entry, "fk_gemm_f16_add") == 0) need.push_back({"r0", 0});
+    if (std::strcmp(entry, "fk_gemm_f16_store_keys") == 0) {
+      // One anchor whose columns start at 0 and fill its rows: the keys
+      // index a row's columns 128 at a time.
+      if (p.n_anchors != 1 || p.first_col[0] != 0 || p.first_col[1] == 0 || p.ldc[0] != p.first_col[1] ||
+          p.first_col[1] % 256 || p.m % 256)
+        return bad(err, cap, FK_ERR_ARG, "%s: %u anchors, columns [%u, %u) in rows of %u", entry, p.n_anchors,
+                   p.first_col[0], p.first_col[1], p.ldc[0]);
+      need.push_back({"keys", (uint64_t)p.m * (p.ldc[0] / 128) * 8});
+    }
     if (std::strcmp(entry, "fk_gemm_f16_qkv_rope") == 0) {
       need.push_back({"position", 0});
       need.push_back({"slot", 0});
@@ -653,6 +670,13 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({"ks", (uint64_t)p.rows * kw});
       need.push_back({"vs", (uint64_t)p.rows * kw});
     }
+  } else if (std::strcmp(entry, "fk_prefill_argmax_keys") == 0) {
+    fk_prefill_argmax_keys_params p;
+    std::memcpy(&p, params, sizeof p);
+    if (p.parts == 0 || (uint64_t)groups * 4 < p.rows || threads != 256)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows of %u keys in %u x %u threads", entry, p.rows, p.parts, groups,
+                 threads);
+    need = {{"keys", (uint64_t)p.rows * p.parts * 8}, {"out", (uint64_t)p.rows * 4}};
   } else if (std::strcmp(entry, "fk_prefill_land") == 0) {
     fk_prefill_land_params p;
     std::memcpy(&p, params, sizeof p);

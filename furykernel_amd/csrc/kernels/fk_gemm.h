@@ -60,7 +60,8 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
                                           const uint32_t *__restrict__ position = nullptr,
                                           const uint32_t *__restrict__ slot = nullptr,
                                           const float *__restrict__ rope = nullptr,
-                                          const fk_gemm_rope_params &rp = fk_gemm_rope_params{}) {
+                                          const fk_gemm_rope_params &rp = fk_gemm_rope_params{},
+                                          uint64_t *__restrict__ keys = nullptr) {
   extern __shared__ uint4 gemm_lds[];
   constexpr uint32_t ROW16 = FK_GEMM_BK * 2 / 16;           // 16-byte units a staged row takes
   constexpr uint32_t TILEB = FK_GEMM_BM * FK_GEMM_BK * 2;    // bytes of one operand's staged tile
@@ -265,37 +266,46 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
   if (MODE == FK_GEMM_SILU_MUL) {
     uint16_t *out = reinterpret_cast<uint16_t *>(c0);
     const uint32_t ncols = p.ldc[0];
+    // silu(g) u = g / (1 + e^-g) · u, or gelu(g) u = 0.5 g (1 + tanh(y)) u
+    // with tanh(y) = 1 - 2 / (1 + e^2y), with the hardware's exp and
+    // reciprocal (a few ulp of binary32), then rounded once to f16 (2^-11):
+    // the f16 rounding bounds the error.  An exponential overflowing gives
+    // the limits (silu 0, tanh 1).  The activation is a branch on the
+    // launch's uniform parameter around the whole epilogue, each side
+    // unrolled, so a tile pays for its own activation's exponentials only.
+    auto act_mul_tiles = [&](auto gelu_tag) {
+      constexpr bool GELU = decltype(gelu_tag)::value;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+      for (int i = 0; i < 8; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        // Blocks 0-3: gate columns wn 64 + 16 j; blocks 4-7 the same up columns.
-        const uint32_t n = n0 + wn * 64 + 16 * j + nq;
-        uint16_t h[4];
+        for (int j = 0; j < 4; j++) {
+          // Blocks 0-3: gate columns wn 64 + 16 j; blocks 4-7 the same up columns.
+          const uint32_t n = n0 + wn * 64 + 16 * j + nq;
+          uint16_t h[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float gt = acc[i][j][r];
-          const float u = acc[i][j + 4][r];
-          // silu(g) u = g / (1 + e^-g) · u, or gelu(g) u = 0.5 g (1 +
-          // tanh(y)) u with tanh(y) = 1 - 2 / (1 + e^2y), with the hardware's
-          // exp and reciprocal (a few ulp of binary32), then rounded once to
-          // f16 (2^-11): the f16 rounding bounds the error.  An exponential
-          // overflowing gives the limits (silu 0, tanh 1).  The choice is a
-          // select, uniform over the launch.
-          const float e = __expf(-gt);
-          const float silu = gt * __builtin_amdgcn_rcpf(1.0f + e);
-          const float y = 0.7978845608028654f * (gt + ((0.044715f * gt) * gt) * gt);
-          const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(2.0f * y));
-          const float gelu = (0.5f * gt) * (1.0f + th);
-          h[r] = fk::to_f16((p.act == FK_ACT_GELU_TANH ? gelu : silu) * u);
+          for (int r = 0; r < 4; r++) {
+            const float gt = acc[i][j][r];
+            const float u = acc[i][j + 4][r];
+            float a;
+            if constexpr (GELU) {
+              const float y = 0.7978845608028654f * (gt + ((0.044715f * gt) * gt) * gt);
+              const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(2.0f * y));
+              a = (0.5f * gt) * (1.0f + th);
+            } else {
+              a = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt));
+            }
+            h[r] = fk::to_f16(a * u);
+          }
+          uint2 w;
+          w.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+          w.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+          // Four consecutive columns of one row: half of one 16-byte unit.
+          *reinterpret_cast<uint2 *>(out + fk::tile_offset(m + 16 * i, n, ncols)) = w;
+          if (j == 3) asm volatile("" ::: "memory");  // one row block at a time
         }
-        uint2 w;
-        w.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-        w.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
-        // Four consecutive columns of one row: half of one 16-byte unit.
-        *reinterpret_cast<uint2 *>(out + fk::tile_offset(m + 16 * i, n, ncols)) = w;
-        if (j == 3) asm volatile("" ::: "memory");  // one row block at a time
-      }
+    };
+    if (p.act == FK_ACT_GELU_TANH) act_mul_tiles(fk_bool_tag<true>{});
+    else act_mul_tiles(fk_bool_tag<false>{});
   } else if (MODE == FK_GEMM_QKV_ROPE) {
     // A 256-column tile is 4 whole heads, a wavefront's 128 columns 2; a
     // lane's blocks 4 jp + jj and 4 jp + jj + 2 hold columns d and d + 32 of
@@ -349,9 +359,18 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
   } else {
     float *out = reinterpret_cast<float *>(anchor == 0 ? c0 : (anchor == 1 ? c1 : c2));
     const uint32_t ld = anchor == 0 ? p.ldc[0] : (anchor == 1 ? p.ldc[1] : p.ldc[2]);
+    // The greedy token's keys (one anchor, its columns from 0): the key of
+    // the largest element of each row's 128 columns of the wavefront, the
+    // row's key part (n0 + wn 128) / 128 of ld / 128.  A lane meets its
+    // columns in increasing order and keeps the first of its largest by the
+    // high word of fk::argmax_key alone (the value's order: NaN 0 but at
+    // column 0, where it is above everything), so the 64-bit key is made
+    // once a row block, from the kept value and column.
+    const uint32_t col0 = n0 + wn * 128 + nq;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const size_t row = (size_t)(m + 16 * i) * ld + n0 + wn * 128 + nq;
+      uint32_t bk = 0, bi = col0;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
         fk_float4v v = acc[i][j];
@@ -365,6 +384,29 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
           for (int r = 0; r < 4; r++) v[r] = __builtin_canonicalizef(v[r]);
         }
         *reinterpret_cast<fk_float4v *>(out + row + 16 * j) = v;
+        if (MODE == FK_GEMM_STORE_KEYS) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const float z = v[r] + 0.0f;  // -0 to +0: the two zeros are one value
+            const uint32_t u = __float_as_uint(z);
+            const uint32_t nan_key = j == 0 && r == 0 && col0 == 0 ? 0xFFFFFFFFu : 0u;
+            const uint32_t key = z != z ? nan_key : u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+            bi = key > bk ? col0 + 16 * j + r : bi;
+            bk = key > bk ? key : bk;
+          }
+        }
+      }
+      if (MODE == FK_GEMM_STORE_KEYS) {
+        uint64_t best = ((uint64_t)bk << 32) | (uint64_t)(0xFFFFFFFFu - bi);
+        // Lanes l, l ^ 16, l ^ 32 and l ^ 48 hold the same row's other
+        // columns of the wavefront's 128.
+#pragma unroll
+        for (int s = 16; s <= 32; s <<= 1) {
+          const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(best >> 32), s) << 32) |
+                                 (uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)best, s);
+          best = other > best ? other : best;
+        }
+        if (lane_e < 16) keys[(size_t)(m + 16 * i) * (ld / 128) + (n0 + wn * 128) / 128] = best;
       }
       // One row block at a time: the compiler may not gather every block's
       // addresses (and loads) ahead, which would crowd the registers the
@@ -387,6 +429,17 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
 FK_GEMM_ENTRY(fk_gemm_f16_store, FK_GEMM_STORE)
 FK_GEMM_ENTRY(fk_gemm_f16_add, FK_GEMM_ADD)
 FK_GEMM_ENTRY(fk_gemm_f16_silu_mul, FK_GEMM_SILU_MUL)
+
+// The plain store with the greedy token folded in: one anchor, its C rows
+// and each row's keys [M][N / 128], which fk_prefill_argmax_keys reduces.
+extern "C" __global__ void __launch_bounds__(FK_GEMM_THREADS)
+    fk_gemm_f16_store_keys(const _Float16 *__restrict__ a, const _Float16 *__restrict__ b0,
+                           const _Float16 *__restrict__ b1, const _Float16 *__restrict__ b2, void *__restrict__ c0,
+                           void *__restrict__ c1, void *__restrict__ c2, const float *r0, uint64_t *__restrict__ keys,
+                           fk_gemm_params p) {
+  gemm_tile<FK_GEMM_STORE_KEYS>(a, b0, b1, b2, c0, c1, c2, r0, p, nullptr, nullptr, nullptr, fk_gemm_rope_params{},
+                                keys);
+}
 
 // The QKV projection with RoPE and the KV store in its epilogue: anchors q,
 // k, v (in that order), C0 the f16 q rows, C1 and C2 the K and V caches

@@ -10,6 +10,7 @@
 //                          the caches at each row's position
 //   fk_prefill_softcap     a softcap over rows (the head's, before the argmax)
 //   fk_prefill_argmax      the greedy token of each row
+//   fk_prefill_argmax_keys the same from the keys the head's GEMM folded in
 //
 // (The causal attention between them, fk_prefill_attend_g*, is fk_attend.h:
 // a code object of its own.)
@@ -204,11 +205,6 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_land(
   }
 }
 
-// The greedy token of each row: the index of its largest logit, the first
-// of equals, by the decode step's 64-bit keys (value order, then the
-// complement of the index; a NaN at index 0 wins, elsewhere loses:
-// src/FuryKernel/Program/Eval.hs:681-685).  One wave a row.
-
 // A softcap over the logits of every row (src/FuryKernel/Program/Eval.hs:
 // 384-390), in place or into another buffer: y = cap tanh(x / cap), as the
 // decode step's epilogue computes it.
@@ -218,6 +214,10 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_softcap(const float
   for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < p.count; i += gridDim.x * 256) y[i] = fk::softcap(x[i], p.cap);
 }
 
+// The greedy token of each row: the index of its largest logit, the first
+// of equals, by the decode step's 64-bit keys (value order, then the
+// complement of the index; a NaN at index 0 wins, elsewhere loses:
+// src/FuryKernel/Program/Eval.hs:681-685).  One wave a row.
 extern "C" __global__ void __launch_bounds__(256) fk_prefill_argmax(const float *__restrict__ x,
                                                                     uint32_t *__restrict__ out,
                                                                     fk_prefill_argmax_params p) {
@@ -230,6 +230,28 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_argmax(const float 
     const uint64_t key = fk::argmax_key(xr[j], j);
     best = key > best ? key : best;
   }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(best >> 32), s) << 32) |
+                           (uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)best, s);
+    best = other > best ? other : best;
+  }
+  if (lane == 0) out[row] = 0xFFFFFFFFu - (uint32_t)best;
+}
+
+// The greedy token of each row from the keys fk_gemm_f16_store_keys left,
+// `parts` a row (the keys of its columns 128 at a time): their maximum is
+// the maximum of every element's key, the fold fk_prefill_argmax makes.  One
+// wave a row.
+extern "C" __global__ void __launch_bounds__(256) fk_prefill_argmax_keys(const uint64_t *__restrict__ keys,
+                                                                         uint32_t *__restrict__ out,
+                                                                         fk_prefill_argmax_keys_params p) {
+  const uint32_t row = blockIdx.x * 4 + threadIdx.x / FK_WAVE;
+  if (row >= p.rows) return;
+  const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
+  const uint64_t *kr = keys + (size_t)row * p.parts;
+  uint64_t best = 0;
+  for (uint32_t j = lane; j < p.parts; j += FK_WAVE) best = kr[j] > best ? kr[j] : best;
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) {
     const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(best >> 32), s) << 32) |

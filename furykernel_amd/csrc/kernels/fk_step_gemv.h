@@ -56,23 +56,6 @@ __device__ __forceinline__ T pick3(uint32_t a, T x0, T x1, T x2) {
   return a == 0 ? x0 : (a == 1 ? x1 : x2);
 }
 
-// The greedy token's fold (src/FuryKernel/Program/Eval.hs:681-685: a later
-// element wins only if strictly larger) as the maximum of one 64-bit key per
-// element: the value's order in the high word (+0 and -0 equal; a NaN at
-// index 0 above everything, since nothing is larger than it and it is never
-// replaced; a NaN elsewhere below everything, since it never wins), and the
-// complement of the index in the low word, so equal values go to the lowest.
-__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
-  uint32_t hi;
-  if (__builtin_isnan(v)) {
-    hi = index == 0 ? 0xFFFFFFFFu : 0u;
-  } else {
-    const uint32_t b = v == 0.0f ? 0u : __float_as_uint(v);
-    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  }
-  return ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - index);
-}
-
 // Where slot q of block b is: its anchor, its row in the anchor, and whether
 // it exists.
 template <int R>

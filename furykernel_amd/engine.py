@@ -39,6 +39,7 @@ _STRUCTS = {
     "fk_prefill_softcap": K.PrefillSoftcapParams,
     "fk_step_token": K.StepTokenParams,
     "fk_gemm_f16_store": K.GemmParams,
+    "fk_gemm_f16_store_keys": K.GemmParams,
     "fk_gemm_f16_add": K.GemmParams,
     "fk_gemm_f16_silu_mul": K.GemmParams,
     "fk_gemm_f16_qkv_rope": K.GemmQkvParams,
@@ -50,6 +51,7 @@ _STRUCTS = {
     "fk_prefill_attend_g2": K.PrefillAttendParams,
     "fk_prefill_attend_g4": K.PrefillAttendParams,
     "fk_prefill_argmax": K.PrefillArgmaxParams,
+    "fk_prefill_argmax_keys": K.PrefillArgmaxKeysParams,
     "fk_prefill_land": K.PrefillLandParams,
 }
 

@@ -143,6 +143,10 @@ class PrefillArgmaxParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("width", ctypes.c_uint32)]
 
 
+class PrefillArgmaxKeysParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("parts", ctypes.c_uint32)]
+
+
 class StepTokenParams(ctypes.Structure):
     _fields_ = [("slots", ctypes.c_uint32), ("context", ctypes.c_uint32), ("step", ctypes.c_uint32),
                 ("advance", ctypes.c_uint32)]
@@ -295,6 +299,8 @@ ABIS: dict[str, KernelAbi] = {
     "fk_step_token": KernelAbi("fk_step_token", ("arg", "out", "token", "position"), StepTokenParams, 64),
     **{f"fk_gemm_f16_{mode}": KernelAbi(f"fk_gemm_f16_{mode}", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0"),
                                         GemmParams, 256) for mode in ("store", "add", "silu_mul")},
+    "fk_gemm_f16_store_keys": KernelAbi("fk_gemm_f16_store_keys", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0",
+                                                                   "keys"), GemmParams, 256),
     "fk_gemm_f16_qkv_rope": KernelAbi("fk_gemm_f16_qkv_rope", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0",
                                                                "position", "slot", "rope"), GemmQkvParams, 256),
     "fk_prefill_gather": KernelAbi("fk_prefill_gather", ("table", "tokens", "x"), PrefillGatherParams, 256),
@@ -310,6 +316,7 @@ ABIS: dict[str, KernelAbi] = {
     "fk_prefill_land": KernelAbi("fk_prefill_land", ("ks", "vs", "position", "slot", "kc", "vc"),
                                  PrefillLandParams, 256),
     "fk_prefill_argmax": KernelAbi("fk_prefill_argmax", ("x", "out"), PrefillArgmaxParams, 256),
+    "fk_prefill_argmax_keys": KernelAbi("fk_prefill_argmax_keys", ("keys", "out"), PrefillArgmaxKeysParams, 256),
     "fk_prefill_softcap": KernelAbi("fk_prefill_softcap", ("x", "y"), PrefillSoftcapParams, 256),
     "fk_step_store": KernelAbi("fk_step_store", ("x0", "x1", "c0", "c1", "position", "slot", "rope"),
                                StepStoreParams),
@@ -402,15 +409,20 @@ class Kernels:
     GEMM_TILE, GEMM_K, GEMM_LDS = 256, 64, 4 * 2 * 256 * 32 * 2
 
     def gemm(self, a: runtime.Buffer, bs: list, cs: list, m: int, k: int, rows: list, mode: str = "store",
-             r: runtime.Buffer | None = None, stream: runtime.Stream | None = None, act: int = 0) -> None:
+             r: runtime.Buffer | None = None, stream: runtime.Stream | None = None, act: int = 0,
+             keys: runtime.Buffer | None = None) -> None:
         """A [m, k] f16 in the tile layout (furykernel_amd.layout) times the
         weights bs[j] ([rows[j], k] f16, tiled: the anchors) into cs[j]
         ([m, rows[j]] f32 rows; "add": plus r, [m, rows[0]] f32, which may be
         cs[0]).  "silu_mul": one weight, the pair of gate and up ([2 rows[0],
-        k], layout.pair), into cs[0] [m, rows[0]] f16 tiled as silu(gate) up."""
+        k], layout.pair), into cs[0] [m, rows[0]] f16 tiled as silu(gate) up.
+        "store_keys": one anchor stored as "store" does, and `keys` [m,
+        rows[0] / 128] u64 the greedy token's keys (prefill_argmax_keys)."""
         entry = f"fk_gemm_f16_{mode}"
         if entry not in ABIS:
             raise LaunchError(f"no GEMM {entry}")
+        if (mode == "store_keys") != (keys is not None) or (keys is not None and len(bs) != 1):
+            raise LaunchError(f"{entry}: keys go with the store_keys mode and one anchor")
         t = self.GEMM_TILE
         if m <= 0 or m % t or k <= 0 or k % self.GEMM_K:
             raise LaunchError(f"{entry}: m = {m} must be a multiple of {t}, k = {k} of {self.GEMM_K}")
@@ -437,12 +449,16 @@ class Kernels:
             groups = (m // t) * (sum(rows) // t)
         if r is not None:
             _need(r, m * rows[0] * 4, "R", entry)
+        if keys is not None:
+            _need(keys, m * (rows[0] // 128) * 8, "keys", entry)
         first = [0]
         for n in rows:
             first.append(first[-1] + n)
         first += [first[-1]] * (4 - len(first))
         ldc = (list(rows) + [0, 0, 0])[:3]
         bufs = {"a": a.ptr, "r0": r.ptr if r is not None else 0}
+        if keys is not None:
+            bufs["keys"] = keys.ptr
         for j in range(3):
             bufs[f"b{j}"] = bs[j].ptr if j < len(bs) else 0
             bufs[f"c{j}"] = cs[j].ptr if j < len(cs) else 0
@@ -466,6 +482,28 @@ class Kernels:
             _need(gamma, width * 4, "gamma", entry)
         self.launch(entry, rows // 4, 256, {"x": x.ptr, "gamma": gamma.ptr if gamma is not None else 0, "y": y.ptr},
                     PrefillNormParams(rows, width, eps, factor, int(gamma is not None)), stream)
+
+    def prefill_argmax(self, x: runtime.Buffer, out: runtime.Buffer, rows: int, width: int,
+                       stream: runtime.Stream | None = None) -> None:
+        """The greedy token of each f32 row [rows, width] into out (u32)."""
+        entry = "fk_prefill_argmax"
+        if rows <= 0 or width <= 0:
+            raise LaunchError(f"{entry}: [{rows}, {width}]")
+        _need(x, rows * width * 4, "x", entry)
+        _need(out, rows * 4, "out", entry)
+        self.launch(entry, (rows + 3) // 4, 256, {"x": x.ptr, "out": out.ptr}, PrefillArgmaxParams(rows, width), stream)
+
+    def prefill_argmax_keys(self, keys: runtime.Buffer, out: runtime.Buffer, rows: int, parts: int,
+                            stream: runtime.Stream | None = None) -> None:
+        """The greedy token of each row from its `parts` keys (u64, [rows,
+        parts], as gemm's store_keys mode leaves them) into out (u32)."""
+        entry = "fk_prefill_argmax_keys"
+        if rows <= 0 or parts <= 0:
+            raise LaunchError(f"{entry}: {rows} rows of {parts} keys")
+        _need(keys, rows * parts * 8, "keys", entry)
+        _need(out, rows * 4, "out", entry)
+        self.launch(entry, (rows + 3) // 4, 256, {"keys": keys.ptr, "out": out.ptr},
+                    PrefillArgmaxKeysParams(rows, parts), stream)
 
     def prefill_attend(self, qr: runtime.Buffer, kc: runtime.Buffer, vc: runtime.Buffer, position: runtime.Buffer,
                        slot: runtime.Buffer, out: runtime.Buffer, rows: int, heads: int, kv_heads: int,
@@ -645,6 +683,8 @@ def launch_reads(entry: str, params: dict) -> set[str]:
             need.add("r0")
         if entry == "fk_gemm_f16_qkv_rope":
             need |= {"position", "slot", "rope"}
+        if entry == "fk_gemm_f16_store_keys":
+            need.add("keys")
         return need
     if entry == "fk_rmsnorm_f32" or entry.startswith("fk_prefill_norm_pack"):
         return set(abi.buffers) - ({"gamma"} if not params.get("has_gamma") else set())

@@ -19,7 +19,9 @@ cores).  Each value is made in the layout its readers take:
   when the three came from one GEMM and every pair of the heads turns, the
   GEMM's epilogue does the RoPE and the stores (``fk_gemm_f16_qkv_rope``) and
   q, k, v are never f32 rows in HBM;
-- the greedy token is ``fk_prefill_argmax`` over each row's logits.
+- the greedy token is ``fk_prefill_argmax`` over each row's logits, or,
+  when the head's GEMM stored them, keys that GEMM leaves (128 columns a
+  key) reduced by ``fk_prefill_argmax_keys``.
 
 Staged KV stores (the ring has no room for a step's rows: Plan.hs:41-50)
 store each row's k and v heads, as the cache holds them, into staging rows
@@ -72,7 +74,37 @@ def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int, run_rows: Opti
     out = Lowered(checked.program, plan, rows)
     _Prefill(out, run_rows).run()
     _fuse_qkv_rope(out)
+    _fuse_argmax(out)
     return out
+
+
+def _fuse_argmax(out: Lowered) -> None:
+    """Folds each ``fk_prefill_argmax`` over rows that a one-anchor
+    ``fk_gemm_f16_store`` made (the head's logits, no softcap between) into
+    that GEMM: ``fk_gemm_f16_store_keys`` stores the same rows and leaves
+    each row's greedy-token keys, 128 columns a key, and
+    ``fk_prefill_argmax_keys`` takes their maximum, the same token as the
+    argmax over the rows.  No launch between the two may touch the rows."""
+    launches = out.launches
+    for i, am in enumerate(launches):
+        if am.entry != "fk_prefill_argmax":
+            continue
+        x = am.bind["x"]
+        j = next((j for j in range(i - 1, -1, -1) if x in launches[j].bind.values()), None)
+        if j is None:
+            continue
+        gm = launches[j]
+        p = gm.params
+        if gm.entry != "fk_gemm_f16_store" or gm.bind["c0"] != x or p["n_anchors"] != 1 or \
+                p["first_col"][0] != 0 or p["ldc"][0] != p["first_col"][1] or p["ldc"][0] != am.params["width"]:
+            continue
+        rows, parts = am.params["rows"], p["ldc"][0] // 128
+        keys = out.buffer(f"keys:{x}", "u64", rows * parts)
+        launches[j] = Launch(gm.step, "fk_gemm_f16_store_keys", gm.groups, gm.threads, dict(gm.bind, keys=keys),
+                             dict(p), {}, gm.lds_bytes)
+        launches[i] = Launch(am.step, "fk_prefill_argmax_keys", am.groups, am.threads,
+                             {"keys": keys, "out": am.bind["out"]}, {"rows": rows, "parts": parts}, {},
+                             am.lds_bytes)
 
 
 def _fuse_qkv_rope(out: Lowered) -> None:

@@ -24,6 +24,8 @@
  *   fk_gemm_f16_<store|add|silu_mul>  a b0 b1 b2 c0 c1 c2 r0   fk_gemm_params
  *   fk_gemm_f16_qkv_rope a b0 b1 b2 c0 c1 c2 r0 position slot rope
  *                                                      fk_gemm_qkv_params
+ *   fk_gemm_f16_store_keys a b0 b1 b2 c0 c1 c2 r0 keys  fk_gemm_params
+ *   fk_prefill_argmax_keys keys out                    fk_prefill_argmax_keys_params
  *   (the manifest lists every entry.)
  */
 #ifndef FKROCM_KERNELS_H
@@ -261,8 +263,10 @@ enum {
   FK_GEMM_STORE = 0,    /* C = A B^T (f32 rows) */
   FK_GEMM_ADD = 1,      /* C = R + A B^T (f32 rows), R [M, ldc]; R may be C */
   FK_GEMM_SILU_MUL = 2, /* C = f16(silu(A G^T) (A U^T)) in the tile layout; B0 the paired gate/up weights */
-  FK_GEMM_QKV_ROPE = 3  /* anchors q, k, v: q RoPE'd into f16 rows (C0), k RoPE'd into the K cache (C1), v into
+  FK_GEMM_QKV_ROPE = 3, /* anchors q, k, v: q RoPE'd into f16 rows (C0), k RoPE'd into the K cache (C1), v into
                            the V cache (C2), at each row's slot and position */
+  FK_GEMM_STORE_KEYS = 4 /* one anchor's C = A B^T (f32 rows), and for each row and 128 columns the greedy token's
+                            64-bit key of their largest element: keys [M][N / 128] */
 };
 
 typedef struct fk_gemm_params {
@@ -351,6 +355,11 @@ typedef struct fk_prefill_argmax_params {
   uint32_t rows;
   uint32_t width;
 } fk_prefill_argmax_params;
+
+typedef struct fk_prefill_argmax_keys_params {
+  uint32_t rows;
+  uint32_t parts; /* keys a row (fk_gemm_f16_store_keys: its columns / 128) */
+} fk_prefill_argmax_keys_params;
 
 #ifdef __cplusplus
 }

@@ -162,3 +162,85 @@ def test_gemm_refuses_shapes_it_does_not_take(device, kernels):
         kernels.gemm(a, [b], [c], 256, 64, [256], "silu_mul")  # the pair is 2 x 256 rows
     for x in (a, b, c):
         x.free()
+
+
+def _tokens_three_ways(device, kernels, a, b):
+    """C = a bᵀ by the store GEMM and by the keys GEMM; the tokens of the
+    keys, of fk_prefill_argmax over the stored rows, and of the oracle's
+    fold over them."""
+    from oracle import fkref
+    L = fkref.lib()
+    m, k = a.shape
+    n = b.shape[0]
+    ba, bb = device.upload(pack(a)), device.upload(pack(b))
+    c0, c1 = device.alloc(m * n * 4), device.alloc(m * n * 4)
+    keys, t0, t1 = device.alloc(m * (n // 128) * 8), device.alloc(m * 4), device.alloc(m * 4)
+    print(f"gemm store_keys m {m} k {k} n {n}", flush=True)
+    kernels.gemm(ba, [bb], [c0], m, k, [n], "store")
+    kernels.gemm(ba, [bb], [c1], m, k, [n], "store_keys", keys=keys)
+    kernels.prefill_argmax(c0, t0, m, n)
+    kernels.prefill_argmax_keys(keys, t1, m, n // 128)
+    device.sync()
+    s0, s1 = c0.read(np.float32, m * n), c1.read(np.float32, m * n)
+    by_keys, by_rows = t1.read(np.uint32, m), t0.read(np.uint32, m)
+    for x in (ba, bb, c0, c1, keys, t0, t1):
+        x.free()
+    rows = s0.reshape(m, n)
+    folded = np.array([L.fkref_argmax(np.ascontiguousarray(r).ctypes.data, n) for r in rows], np.uint32)
+    return s0, s1, by_keys, by_rows, folded
+
+
+def test_the_keys_gemm_stores_the_same_rows_and_leaves_the_greedy_tokens(device, kernels):
+    """Random operands (ties are rare; the fold decides them)."""
+    a, b = f16((512, 128)), f16((1024, 128))
+    s0, s1, by_keys, by_rows, folded = _tokens_three_ways(device, kernels, a, b)
+    assert np.array_equal(s0.view(np.uint32), s1.view(np.uint32))
+    assert np.array_equal(by_keys, folded) and np.array_equal(by_rows, folded)
+
+
+# Rows of logits the fold has rules for, made exactly by one-hot rows of A
+# against weights whose column 0 holds the pattern (every other column 0).
+def _patterns(n=512):
+    rng = np.random.default_rng(11)
+    base = lambda: rng.standard_normal(n).astype(np.float16)  # noqa: E731
+    pats = {}
+    p = np.full(n, 1.5, np.float16)
+    pats["all equal"] = p
+    p = base(); p[5] = p[300] = 9.0
+    pats["tie inside the row"] = p
+    p = base(); p[127] = p[128] = 9.0
+    pats["tie across 128 columns"] = p
+    p = base(); p[16] = p[4] = 9.0
+    pats["tie between lanes"] = p
+    p = base(); p[n - 1] = 9.0
+    pats["largest last"] = p
+    p = base(); p[0] = np.nan; p[9] = 9.0
+    pats["NaN first"] = p
+    p = base(); p[7] = np.nan; p[100] = 9.0
+    pats["NaN elsewhere"] = p
+    p = base(); p[200] = p[300] = np.inf
+    pats["two infinities"] = p
+    pats["all -inf"] = np.full(n, -np.inf, np.float16)
+    pats["all NaN"] = np.full(n, np.nan, np.float16)
+    p = np.zeros(n, np.float16); p[::2] = -0.0
+    pats["signed zeros"] = p
+    p = -np.abs(base()); p[77] = -0.0; p[78] = 0.0
+    pats["zero the largest"] = p
+    return pats
+
+
+@pytest.mark.parametrize("name", list(_patterns()))
+def test_the_keys_gemm_follows_the_folds_rules(device, kernels, name):
+    pat = _patterns()[name]
+    m, k, n = 256, 64, len(pat)
+    a = np.zeros((m, k), np.float16)
+    a[:, 0] = 1.0
+    b = np.zeros((n, k), np.float16)
+    b[:, 0] = pat
+    s0, s1, by_keys, by_rows, folded = _tokens_three_ways(device, kernels, a, b)
+    assert np.array_equal(s0.view(np.uint32), s1.view(np.uint32))
+    assert np.array_equal(by_keys, folded) and np.array_equal(by_rows, folded)
+    want = {"all equal": 0, "tie inside the row": 5, "tie across 128 columns": 127, "tie between lanes": 4,
+            "largest last": n - 1, "NaN first": 0, "NaN elsewhere": 100, "two infinities": 200, "all -inf": 0,
+            "all NaN": 0, "signed zeros": 0, "zero the largest": 77}[name]
+    assert set(folded.tolist()) == {want}

@@ -226,3 +226,34 @@ def test_the_launch_check_refuses_wide_attention_and_combine_prologues_out_of_sh
     spans[i] = (spans[i][0], spans[i][1] - 4)
     with pytest.raises(runtime.FkError):
         _check(o, low.buffers, spans=spans)
+
+
+def test_the_launch_check_takes_the_prefill_heads_keys_and_refuses_them_out_of_shape():
+    from furykernel_amd.engine import params_struct
+    from furykernel_amd.prefill import lower_prefill
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.decoder import SMALL_PREFILL, decoder_step
+    from furykernel_amd.program.plan import PlanOptions, plan
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256)
+    for L in low.launches:
+        _check(L, low.buffers)
+    head, token = low.launches[-2:]
+    assert (head.entry, token.entry) == ("fk_gemm_f16_store_keys", "fk_prefill_argmax_keys")
+    spans = _spans(head, low.buffers)
+    i = list(K.ABIS[head.entry].buffers).index("keys")
+    spans[i] = (spans[i][0], spans[i][1] - 8)  # one key short
+    with pytest.raises(runtime.FkError, match="keys holds"):
+        _check(head, low.buffers, spans=spans)
+    p = params_struct(head)
+    p.ldc[0] = p.first_col[1] + 256  # rows wider than the anchor's columns
+    with pytest.raises(runtime.FkError, match="anchors"):
+        _check(head, low.buffers, params=p)
+    spans = _spans(token, low.buffers)
+    spans[0] = (spans[0][0], spans[0][1] - 8)
+    with pytest.raises(runtime.FkError, match="keys holds"):
+        _check(token, low.buffers, spans=spans)
+    p = params_struct(token)
+    p.rows = 4 * token.groups + 1  # more rows than its waves
+    with pytest.raises(runtime.FkError, match="rows"):
+        _check(token, low.buffers, params=p)

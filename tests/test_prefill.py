@@ -58,7 +58,14 @@ def test_prefill_lowering_of_the_small_decoder():
     # the QKV GEMM RoPEs and stores in its epilogue: no RoPE launch, no f32 q, k, v
     per_layer = [norm, "fk_gemm_f16_qkv_rope", "fk_prefill_attend_g2",
                  "fk_gemm_f16_add", norm, "fk_gemm_f16_silu_mul", "fk_gemm_f16_add"]
-    assert entries == ["fk_prefill_gather"] + per_layer * 2 + [norm, "fk_gemm_f16_store", "fk_prefill_argmax"]
+    # the head's GEMM leaves the greedy token's keys, 128 columns a key
+    assert entries == ["fk_prefill_gather"] + per_layer * 2 + [norm, "fk_gemm_f16_store_keys",
+                                                               "fk_prefill_argmax_keys"]
+    head, token = low.launches[-2:]
+    assert head.bind["keys"] == token.bind["keys"] and head.bind["c0"] == "value:logits"
+    assert token.params == {"rows": 256, "parts": SMALL_PREFILL.vocab // 128}
+    assert low.buffers[head.bind["keys"]].dtype == "u64"
+    assert low.buffers[head.bind["keys"]].count == 256 * SMALL_PREFILL.vocab // 128
     qkv = low.launches[2]
     assert qkv.params["first_col"] == [0, 512, 768, 1024] and qkv.groups == 1 * 4
     att = low.launches[3]
@@ -206,3 +213,33 @@ def test_fast_evaluator_agrees_over_interleaved_sequences_and_windows(window):
     ex, fa = evaluate(checked, b), evaluate_fast(checked, b)
     want = np.array(ex.outputs["o"])
     assert np.max(np.abs(fa.outputs["o"] - want)) <= 1e-12 * np.max(np.abs(want))
+
+
+def prefill_head(cap=None):
+    """A head of many rows: RMSNorm, the logits over f16 weights, an optional
+    softcap, the greedy token."""
+    from furykernel_amd.program.build import program
+    from furykernel_amd.program.graph import F16, F32, whole_row
+
+    def body(b):
+        x = b.input("x", whole_row(256))
+        norm = b.weight("final_norm", [256], F32)
+        embed = b.weight("embed", [512, 256], F16)
+        logits = b.linear("logits", embed, 0, b.rmsnorm("normed", 1e-6, norm, 1, x))
+        out = logits if cap is None else b.softcap("capped", cap, logits)
+        b.output("logits", out)
+        b.output("token", b.argmax("token", out))
+    return check_program(program("prefill_head", body))
+
+
+def test_the_token_folds_into_the_heads_gemm_only_without_a_softcap():
+    plain = prefill_head()
+    low = lower_prefill(plain, plan(PlanOptions(), plain), 512)
+    assert [l.entry for l in low.launches][-2:] == ["fk_gemm_f16_store_keys", "fk_prefill_argmax_keys"]
+    assert low.launches[-1].params == {"rows": 512, "parts": 4}
+    # a softcap between the logits and the token: the token reads the capped
+    # rows, so the plain argmax stays
+    capped = prefill_head(30.0)
+    low = lower_prefill(capped, plan(PlanOptions(), capped), 512)
+    assert [l.entry for l in low.launches][-3:] == ["fk_gemm_f16_store", "fk_prefill_softcap", "fk_prefill_argmax"]
+    assert low.launches[-1].bind["x"] == low.launches[-2].bind["y"]
