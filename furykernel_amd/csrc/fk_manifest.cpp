@@ -632,6 +632,24 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
     fk_gemm_params p;
     std::memcpy(&p, params, sizeof p);
     static const char *bn[3] = {"b0", "b1", "b2"}, *cn[3] = {"c0", "c1", "c2"};
+    // The tiles: 256 rows by 256 columns of the anchors (SiLU·mul: 128 gate
+    // columns and their up columns), one threadgroup each, k in pairs of
+    // steps of 32; the LDS ring of 4 stages.
+    const bool silu = std::strcmp(entry, "fk_gemm_f16_silu_mul") == 0;
+    const uint32_t cols = silu ? p.ldc[0] : (p.n_anchors >= 1 && p.n_anchors <= 3 ? p.first_col[p.n_anchors] : 0);
+    const uint32_t unit = silu ? 128 : 256;
+    bool shape = p.n_anchors >= 1 && p.n_anchors <= (silu ? 1u : 3u) && p.m && p.m % 256 == 0 && p.k &&
+                 p.k % 64 == 0 && cols && cols % unit == 0 && (silu || p.first_col[0] == 0);
+    for (uint32_t j = 0; shape && !silu && j < p.n_anchors; j++)
+      shape = p.first_col[j + 1] > p.first_col[j] && (p.first_col[j + 1] - p.first_col[j]) % 256 == 0 &&
+              p.ldc[j] >= p.first_col[j + 1] - p.first_col[j];
+    if (!shape || (uint64_t)groups != (uint64_t)(p.m / 256) * (cols / unit))
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows, k %u, %u anchors over %u columns in %u threadgroups", entry, p.m,
+                 p.k, p.n_anchors, cols, groups);
+    const uint32_t lds = 4 * (256 + 256) * 32 * 2;
+    if (lds_bytes < lds)
+      return bad(err, cap, FK_ERR_RANGE, "%s: %u bytes of threadgroup memory, its ring takes %u", entry, lds_bytes,
+                 lds);
     need.push_back({"a", 0});
     for (uint32_t j = 0; j < p.n_anchors && j < 3; j++) {
       need.push_back({bn[j], 0});

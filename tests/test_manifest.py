@@ -240,6 +240,16 @@ def test_the_launch_check_takes_the_prefill_heads_keys_and_refuses_them_out_of_s
         _check(L, low.buffers)
     head, token = low.launches[-2:]
     assert (head.entry, token.entry) == ("fk_gemm_f16_store_keys", "fk_prefill_argmax_keys")
+    # a GEMM's grid is its tiles, its LDS the ring
+    for L in [l for l in low.launches if l.entry.startswith("fk_gemm_f16_")]:
+        for bad in (dataclasses.replace(L, groups=L.groups + 1), dataclasses.replace(L, groups=L.groups - 1),
+                    dataclasses.replace(L, lds_bytes=L.lds_bytes - 16)):
+            with pytest.raises(runtime.FkError, match="threadgroup"):
+                _check(bad, low.buffers)
+        p = params_struct(L)
+        p.k += 32   # k in pairs of steps of 32
+        with pytest.raises(runtime.FkError, match="threadgroups"):
+            _check(L, low.buffers, params=p)
     spans = _spans(head, low.buffers)
     i = list(K.ABIS[head.entry].buffers).index("keys")
     spans[i] = (spans[i][0], spans[i][1] - 8)  # one key short
