@@ -29,8 +29,9 @@ def bound(a, b):
     return 2 * (k + 64) * 2.0**-24 * mag + 2.0**-126
 
 
-def run(device, kernels, a, bs, mode="store", r=None):
-    """bs: the weights; for "silu_mul", [gate, up]."""
+def run(device, kernels, a, bs, mode="store", r=None, act=0):
+    """bs: the weights; for "silu_mul", [gate, up] (act: the activation,
+    SiLU 0 or GELU-tanh 1)."""
     m, k = a.shape
     ba = device.upload(pack(a))
     if mode == "silu_mul":
@@ -43,7 +44,7 @@ def run(device, kernels, a, bs, mode="store", r=None):
         cs = [device.alloc(m * n * 4) for n in rows]
     br = device.upload(r) if r is not None else None
     print(f"gemm {mode} m {m} k {k} rows {rows}", flush=True)
-    kernels.gemm(ba, bb, cs, m, k, rows, mode, br)
+    kernels.gemm(ba, bb, cs, m, k, rows, mode, br, act=act)
     device.sync()
     if mode == "silu_mul":
         out = [unpack(cs[0].read(np.float16, m * rows[0]), m, rows[0])]
@@ -110,13 +111,29 @@ def test_gemm_residual_in_place(device, kernels):
         x.free()
 
 
-def test_gemm_silu_mul_epilogue_writes_the_tile_layout(device, kernels):
+def gelu_mul(a, g, u):
+    """0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) u in binary64."""
+    ge = a.astype(np.float64) @ g.astype(np.float64).T
+    ue = a.astype(np.float64) @ u.astype(np.float64).T
+    return 0.5 * ge * (1 + np.tanh(np.sqrt(2 / np.pi) * (ge + 0.044715 * ge ** 3))) * ue
+
+
+@pytest.mark.parametrize("act", [0, 1], ids=["silu", "gelu-tanh"])
+def test_gemm_act_mul_epilogue_writes_the_tile_layout(device, kernels, act):
+    """The gate/up GEMM's epilogue with each activation, within the f16 bar
+    of binary64 (gate values of either sign, out to |g| of about 8, where
+    both activations bend)."""
     a = f16((256, 256), 0.5)
     g, u = f16((384, 256), 0.5), f16((384, 256), 0.5)
-    (c,) = run(device, kernels, a, [g, u], "silu_mul")
-    exact = silu_mul(a, g, u)
+    (c,) = run(device, kernels, a, [g, u], "silu_mul", act=act)
+    exact = (gelu_mul if act else silu_mul)(a, g, u)
+    ge = a.astype(np.float64) @ g.astype(np.float64).T
+    assert np.min(ge) < -4 and np.max(ge) > 4
     err = np.abs(c.astype(np.float64) - exact)
     assert np.max(err) <= 2e-3 * np.max(np.abs(exact))
+    # the two activations differ far beyond the bar: the branch is taken
+    other = (silu_mul if act else gelu_mul)(a, g, u)
+    assert np.max(np.abs(other - exact)) > 4 * 2e-3 * np.max(np.abs(exact))
 
 
 @pytest.mark.parametrize("k,rows,mode", [(2048, [2048, 512, 512], "store"), (2048, [2048], "add"),

@@ -8,8 +8,11 @@ binary64 evaluator (oracle/eval.py, pinned to the exact one).  The GEMM
 operands and the attention's probabilities are f16 on this path; the
 evaluator rounds only the cache stores.  With every pair of the heads turned
 the QKV GEMM RoPEs and stores in its epilogue; with 16 of the 32 the RoPE
-kernel does (both run).
+kernel does (both run); and the same decoder with a GELU-tanh MLP (the gate/up
+GEMM's other activation).
 """
+
+import dataclasses
 
 import numpy as np
 import pytest
@@ -45,21 +48,26 @@ def rel(a, b):
     return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
 
 
-@pytest.fixture(scope="module", params=[None, 16], ids=["rope-all-pairs", "rope-16-pairs"])
+@pytest.fixture(scope="module", params=[(None, "silu"), (16, "silu"), (None, "gelu_tanh")],
+                ids=["rope-all-pairs", "rope-16-pairs", "gelu-tanh"])
 def run(request, device, kernels):
     from furykernel_amd.prefill import PrefillSession
 
-    s = PrefillSession(device, kernels, SMALL_PREFILL, SEQS, SEQ_ROWS, rope_rotated=request.param)
+    rotated, act = request.param
+    dims = dataclasses.replace(SMALL_PREFILL, act=act)
+    s = PrefillSession(device, kernels, dims, SEQS, SEQ_ROWS, rope_rotated=rotated)
     entries = {l.entry for l in s.lowered.launches}
     fused = "fk_gemm_f16_qkv_rope" in entries
-    assert fused == (request.param is None) and fused != ("fk_prefill_rope_store" in entries)
+    assert fused == (rotated is None) and fused != ("fk_prefill_rope_store" in entries)
+    acts = {l.params["act"] for l in s.lowered.launches if l.entry == "fk_gemm_f16_silu_mul"}
+    assert acts == {1 if act == "gelu_tanh" else 0}
     weights, tokens = small_state(s.checked)
     s.write_weights(weights)
     for name in s.lowered.buffers:
         if name.startswith("cache:"):
             s.engine.zero(name)
     s.set_tokens(tokens)
-    print(f"prefill small, rotated {request.param}: {len(s.lowered.launches)} launches", flush=True)
+    print(f"prefill small, rotated {rotated}, {act}: {len(s.lowered.launches)} launches", flush=True)
     s.run()
     device.sync()
     lay = SMALL_PREFILL
