@@ -312,7 +312,27 @@ def evaluate_bounds(checked, b, ev: Evaluation, kept=None) -> Bounds:
     def put(vid, bounds):
         env[vid] = [Approx(x, e) for x, e in zip(exact_of(vid), bounds)]
 
+    recorded: dict = {}   # value id -> its bounds, where downstream reads the stored value exactly
+
+    def anchor(node) -> None:
+        """A value the kernels stored (`kept.values`) must be within its
+        bound of its exact value; what reads it then reads it exactly."""
+        for v in node.outputs:
+            name = values[v].name
+            if kept is None or name not in kept.values or v not in env:
+                continue
+            got = [float(x) for x in np.asarray(kept.values[name][0], np.float64)]
+            for i, (g, a) in enumerate(zip(got, env[v])):
+                if not within(g, a.exact, a.bound):
+                    raise EvalError(f"The kernels stored {g} as {name}[{i}], not within {a.bound} of {a.exact}.")
+            recorded[v] = env[v]
+            env[v] = [exact_a(g) for g in got]
+
+    prev = None
     for n in p.nodes:
+        if prev is not None:
+            anchor(prev)
+        prev = n
         op = n.op
         out = n.outputs[0] if n.outputs else None
         if isinstance(op, Input):
@@ -439,7 +459,10 @@ def evaluate_bounds(checked, b, ev: Evaluation, kept=None) -> Bounds:
             put(out, [0.0 if arg_max_decided(approx(op.x)) else INF])
         else:
             raise EvalError(f"{n.name}: no bounds of {type(op).__name__} here")
-    return Bounds({values[v].name: [np.array([a.bound for a in row])] for v, row in env.items()}, stores)
+    if prev is not None:
+        anchor(prev)
+    return Bounds({values[v].name: [np.array([a.bound for a in recorded.get(v, row)])] for v, row in env.items()},
+                  stores)
 
 
 def evaluate_stored(checked, b, kept):

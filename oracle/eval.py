@@ -46,9 +46,16 @@ class Bindings:
 class Kept:
     """What a step's kernels stored (Eval.hs:174-184): ``caches`` name ->
     {slot: flat values as the step left them}; ``rows`` name -> [rows] of the
-    values the kernels staged for the cache's store, if they staged them."""
+    values the kernels staged for the cache's store, if they staged them.
+
+    ``values`` name -> [rows] of a value the kernels stored: this target's
+    extension of evaluateStored from caches to stored values, so that each
+    launch is checked from what the launches before it stored.  The value is
+    evaluated (and recorded) from its inputs as usual, and what reads it
+    downstream reads the stored rows instead."""
     caches: dict = field(default_factory=dict)
     rows: dict = field(default_factory=dict)
+    values: dict = field(default_factory=dict)
 
 
 @dataclass
@@ -177,7 +184,23 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
     def unit_name(layout) -> str:
         return "slot" if isinstance(layout, Ring) else "block"
 
+    recorded: dict = {}   # value id -> its evaluated rows, where downstream reads the stored ones
+
+    def anchor(node) -> None:
+        for v in node.outputs:
+            name = values[v].name
+            if kept is not None and name in kept.values and v in env:
+                rows = [np.asarray(r, np.float64) for r in kept.values[name]]
+                if len(rows) != len(env[v]) or any(r.shape != e.shape for r, e in zip(rows, env[v])):
+                    raise EvalError(f"The kernels' {name} is not the shape of the value.")
+                recorded[v] = env[v]
+                env[v] = rows
+
+    prev = None
     for n in p.nodes:
+        if prev is not None:
+            anchor(prev)
+        prev = n
         op = n.op
         out = n.outputs[0] if n.outputs else None
         if isinstance(op, Input):
@@ -399,12 +422,14 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
             env[out] = res
         else:
             raise EvalError(f"{n.name}: {type(op).__name__} is not evaluated here")
+    if prev is not None:
+        anchor(prev)
     outs = {}
     for o in p.outputs:
         if o.value not in env:
             raise EvalError(f"The output {o.name} was never made.")
-        outs[o.name] = env[o.value]
-    return Evaluation({values[v].name: rows for v, rows in env.items()}, outs, caches)
+        outs[o.name] = recorded.get(o.value, env[o.value])
+    return Evaluation({values[v].name: recorded.get(v, rows) for v, rows in env.items()}, outs, caches)
 
 
 def evaluate_fast(checked: CheckedProgram, b: Bindings) -> Evaluation:

@@ -241,6 +241,67 @@ def kept_of(cpu, checked):
     return Kept(caches={n: {0: cpu.read(f"cache:{n}").astype(np.float64)} for n in names})
 
 
+def kept_values_of(cpu, checked):
+    """What the launches stored of every value some launch writes, with the
+    caches they left (oracle.eval.Kept)."""
+    kept = kept_of(cpu, checked)
+    stored = written(cpu.lowered)
+    kept.values = {v.name: [cpu.read(f"value:{v.name}").astype(np.float64)]
+                   for v in checked.program.values if f"value:{v.name}" in stored}
+    return kept
+
+
+def check_anchored(cpu, checked, w, c, x, position):
+    """Every stored value within its bound of the exact value of its own
+    launch's stored inputs (EvalError otherwise), every bound finite: each
+    layer is pinned, not only the first.  The bounds, relative to the
+    largest exact element of each value."""
+    from oracle.eval import evaluate
+    kept = kept_values_of(cpu, checked)
+    b = bindings(w, c, x, position)
+    ev = evaluate(checked, b, kept)
+    bd = B.evaluate_bounds(checked, b, ev, kept)
+    rel = {}
+    for name in kept.values:
+        bound = bd.values[name][0]
+        assert np.all(np.isfinite(bound)), name
+        rel[name] = float(np.max(bound) / max(np.max(np.abs(ev.values[name][0])), 1e-300))
+    return ev, bd, rel
+
+
+@pytest.mark.parametrize("width", [64, 32])
+@pytest.mark.parametrize("store_gelus", [False, True])
+def test_tiny_decode_within_bounds_anchored_at_every_stored_value(width, store_gelus):
+    """This target's extension of evaluateStored from caches to stored values
+    (oracle.eval.Kept.values): each launch's outputs checked from what the
+    launches before it stored, so the worst-case bounds no longer compound
+    through the layers' norms; both layers' values are held to about 1e-5
+    of their largest elements."""
+    checked, w, c, x, position = tiny_state(position=31)
+    cpu = run_cpu_target(checked, w, c, x, position, width, PlanOptions(store_gelus=store_gelus))
+    ev, bd, rel = check_anchored(cpu, checked, w, c, x, position)
+    assert any(n.startswith("l1_") for n in rel) and "logits" in rel
+    assert max(v for n, v in rel.items() if n != "token") < 1e-4
+    assert int(cpu.read("value:token")[0]) == int(ev.values["token"][0][0]) or bd.values["token"][0][0] != 0
+
+
+def test_an_anchored_value_moved_past_its_bound_is_refused():
+    """The anchored check has teeth at the last layer: one element of the
+    second layer's residual (planted in what the oracle is given as stored)
+    moved by ten times its bound."""
+    from oracle.eval import EvalError, evaluate
+    checked, w, c, x, position = tiny_state(position=31)
+    cpu = run_cpu_target(checked, w, c, x, position, 64)
+    _, bd, _ = check_anchored(cpu, checked, w, c, x, position)
+    kept = kept_values_of(cpu, checked)
+    row = kept.values["l1_x1"][0].copy()
+    row[7] += 10 * max(float(bd.values["l1_x1"][0][7]), 1e-30)
+    kept.values["l1_x1"] = [row]
+    b = bindings(w, c, x, position)
+    with pytest.raises(EvalError, match="l1_x1"):
+        B.evaluate_bounds(checked, b, evaluate(checked, b, kept), kept)
+
+
 def test_evaluate_stored_reads_what_the_kernels_stored():
     """evaluateStored (Eval.hs:189-198): given the caches the CPU target left,
     the evaluation keeps its stores, checks each against its bound, and the

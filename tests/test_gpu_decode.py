@@ -233,5 +233,11 @@ def test_tiny_decode_on_the_gpu_within_the_element_bounds(device, kernels):
         from test_bounds import kept_of
         ev2, bd2 = B.evaluate_stored(checked, bindings(w, c, x, position), kept_of(Read, checked))
         assert check_tiny(Read, ev2, bd2, checked, c) == []
+        # and anchored at every value the launches stored: each launch from
+        # its stored inputs, both layers held to finite bounds
+        from test_bounds import check_anchored
+        _, _, rel = check_anchored(Read, checked, w, c, x, position)
+        assert any(n.startswith("l1_") for n in rel)
+        assert max(v for n, v in rel.items() if n != "token") < 1e-4
     finally:
         s.close()
