@@ -383,7 +383,13 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
 #pragma unroll
           for (int r = 0; r < 4; r++) v[r] = __builtin_canonicalizef(v[r]);
         }
-        *reinterpret_cast<fk_float4v *>(out + row + 16 * j) = v;
+        if (MODE == FK_GEMM_STORE_KEYS) {
+          // The logits: a gigabyte no later launch of the step reads (the
+          // keys carry the token), streamed past the caches.
+          __builtin_nontemporal_store(v, reinterpret_cast<fk_float4v *>(out + row + 16 * j));
+        } else {
+          *reinterpret_cast<fk_float4v *>(out + row + 16 * j) = v;
+        }
         if (MODE == FK_GEMM_STORE_KEYS) {
 #pragma unroll
           for (int r = 0; r < 4; r++) {
