@@ -513,6 +513,7 @@ def main_kernels(args) -> int:
     for b in bufs:
         b.free()
     table.update(ir_gemv_table(dev, timed, copies_of))
+    table.update(paged_routed_table(dev, ks, args.eager))
 
     head = table["matvec_f32_4096x4096"]
     line = {
@@ -583,6 +584,132 @@ def ir_gemv_table(dev, timed, copies_of) -> dict:
                                          "frac": round(nbytes / best[1] / 1e3 / HBM_PEAK_GBPS, 4)}
         for b in ws + [x, y]:
             b.free()
+    return out
+
+
+def paged_routed_table(dev, ks, eager: bool = False, reps: int = 50) -> dict:
+    """Decode attention at the 1B step's shape (32 heads over 8, d 64, the
+    row at position 4095 of 4096) over a ring and over a paged pool (64
+    blocks of 64 positions through a scrambled block table, pool of 80
+    blocks), and a routed-experts step (hidden 2048, 16 experts of FFN 1024,
+    top 2, expert scales): each planned step lowered, its launches captured
+    as one HIP graph (the step repeated to at least 16 launches) and
+    replayed `reps` times between HIP events (with `eager`, the step's
+    launches queued one by one `reps` times, each a dispatch of its own in a
+    kernel trace).
+    Algorithmic bytes: the K and V rows read (attention), the router and the
+    two routed experts' weights (MoE), plus each step's inputs and outputs."""
+    import math
+
+    import numpy as np
+
+    from furykernel_amd.engine import Engine
+    from furykernel_amd.lower import lower_plan
+    from furykernel_amd.program.build import program
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.graph import CACHE_F16, F16, F32, AttnSpec, Paged, Ring, RopeSpec, Shape, whole_row
+    from furykernel_amd.program.plan import PlanOptions, plan
+
+    heads, kv, d, positions, bs = 32, 8, 64, 4096, 64
+
+    def attention(layout, seq_count, seq_bound):
+        def body(b):
+            q = b.input("q", Shape(heads * d, d), F32)
+            k = b.input("k", Shape(kv * d, d), F32)
+            v = b.input("v", Shape(kv * d, d), F32)
+            pos = b.row_ints("position", 1, positions)
+            sq = b.row_ints("blocks" if isinstance(layout, Paged) else "slot", seq_count, seq_bound)
+            kc, vc = b.cache("kc", layout, CACHE_F16), b.cache("vc", layout, CACHE_F16)
+            spec = RopeSpec(10000.0, d // 2)
+            qr, kr = b.rope("qr", spec, pos, q), b.rope("kr", spec, pos, k)
+            b.kv_store("store_k", kc, pos, sq, kr)
+            b.kv_store("store_v", vc, pos, sq, v)
+            b.output("o", b.attend("o", AttnSpec(heads, kv, d, None, 1.0 / math.sqrt(d), None), qr, kc, vc, pos, sq))
+        return check_program(program("decode_attention", body))
+
+    def moe():
+        hidden, experts, ffn, k = 2048, 16, 1024, 2
+
+        def body(b):
+            x = b.input("x", whole_row(hidden), F32)
+            g = b.weight("moe_norm", [hidden], F32)
+            router = b.weight("router", [experts, hidden], F16)
+            scale = b.weight("expert_scale", [experts], F32)
+            gu = b.table("experts_gate_up", experts, [2 * ffn, hidden], F16)
+            dn = b.table("experts_down", experts, [hidden, ffn], F16)
+            cn = b.rmsnorm("moe_in", 1e-6, g, 1.0, x)
+            ids, ws = b.route("route", k, scale, b.linear("router_logits", router, 0, cn))
+            act = b.gated_gelu("experts_act", b.linear_routed("experts_gate_up_out", gu, ids, cn))
+            s = b.combine_ranks("experts_sum", ws, b.linear_routed("experts_out", dn, ids, act))
+            b.output("y", b.add("y", x, s))
+        nbytes = (experts * hidden + k * 2 * ffn * hidden + k * hidden * ffn) * 2 + 3 * hidden * 4
+        return check_program(program("moe", body)), nbytes
+
+    def timed(eng, low) -> float:
+        # the step repeated to at least 16 launches in its graph, so that the
+        # graph launch's own cost does not dominate a step of a few launches
+        n = len(low.launches)
+        copies = 1 if eager else max(1, -(-16 // n))
+        if eager:
+            run, finish = eng.enqueue, None
+        else:
+            g = eng.capture(only=list(range(n)) * copies)
+            run, finish = g.replay, g.destroy
+        run()
+        dev.sync()
+        start, end = dev.event(), dev.event()
+        start.record()
+        for _ in range(reps):
+            run()
+        end.record()
+        end.synchronize()
+        if finish is not None:
+            finish()
+        return start.elapsed_ms(end) * 1e3 / (reps * copies)
+
+    rng = np.random.default_rng(5)
+    out = {}
+    att_bytes = 2 * positions * kv * d * 2 + (heads + 2 * kv) * d * 4 + heads * d * 4
+    for name, layout, count, bound in (("decode_attention_ring_4096", Ring(1, kv, positions, d), 1, 1),
+                                       ("decode_attention_paged_4096_bs64", Paged(80, bs, kv, d), positions // bs, 80)):
+        checked = attention(layout, count, bound)
+        low = lower_plan(checked, plan(PlanOptions(), checked))
+        eng = Engine(dev, ks, low)
+        try:
+            for v in ("q", "k", "v"):
+                eng.init_normal(f"value:{v}", int(rng.integers(1 << 30)), 0.5)
+            eng.init_normal("cache:kc", 71, 1.0)
+            eng.init_normal("cache:vc", 72, 1.0)
+            eng.set_ints("position", [positions - 1], positions)
+            if isinstance(layout, Paged):
+                eng.set_ints("blocks", rng.permutation(80)[:count], 80)
+            else:
+                eng.set_ints("slot", [0], 1)
+            us = timed(eng, low)
+        finally:
+            eng.close()
+        entries = [l.entry for l in low.launches]
+        log(f"{name}: {entries}, {us:.2f} us a step, {att_bytes / us / 1e3:.1f} GB/s")
+        out[name] = {"launches": entries, "avg_us": round(us, 3), "bytes": att_bytes,
+                     "gbps": round(att_bytes / us / 1e3, 1), "frac": round(att_bytes / us / 1e3 / HBM_PEAK_GBPS, 4)}
+    checked, nbytes = moe()
+    low = lower_plan(checked, plan(PlanOptions(), checked))
+    eng = Engine(dev, ks, low)
+    try:
+        for i, name in enumerate(sorted(n for n in low.buffers if n.startswith(("weight:", "table:")))):
+            if low.buffers[name].dtype == "f32":
+                eng.write(name, np.ones(low.buffers[name].count, np.float32))
+            else:
+                eng.init_normal(name, 300 + i, 0.05)
+        eng.init_normal("value:x", 299, 1.0)
+        us = timed(eng, low)
+    finally:
+        eng.close()
+    entries = [l.entry for l in low.launches]
+    log(f"moe_step_2048_e16_f1024_k2: {entries}, {us:.2f} us a step, {nbytes / us / 1e3:.1f} GB/s")
+    out["moe_step_2048_e16_f1024_k2"] = {"launches": entries, "avg_us": round(us, 3), "bytes": nbytes,
+                                         "gbps": round(nbytes / us / 1e3, 1),
+                                         "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)}
     return out
 
 
