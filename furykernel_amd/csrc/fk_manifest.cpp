@@ -558,6 +558,10 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
   } else if (std::strcmp(entry, "fk_step_combine") == 0) {
     fk_step_combine_params p;
     std::memcpy(&p, params, sizeof p);
+    // one wavefront a head
+    if (p.heads == 0 || groups != p.heads || p.splits == 0 || p.head_dim == 0)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u heads of %u in %u splits, %u threadgroups", entry, p.heads,
+                 p.head_dim, p.splits, groups);
     need = {{"partials", (uint64_t)p.heads * p.splits * (p.head_dim + 2) * 4},
             {"out", (uint64_t)p.heads * p.head_dim * 4}};
   } else if (std::strcmp(entry, "fk_step_store_paged") == 0) {
