@@ -26,6 +26,7 @@ ARCH = "gfx950"
 RUNTIME_SO = PACKAGE / "libfkrocm.so"
 KERNELS_CO = PACKAGE / "fk_kernels.hsaco"
 ATTEND_CO = PACKAGE / "fk_attend.hsaco"
+KERNELS_SO = PACKAGE / "libfkkernels.so"   # the two code objects, as data of a shared library
 
 KERNEL_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -85,8 +86,29 @@ def build_attend() -> Path:
     return ATTEND_CO
 
 
+def build_kernel_library() -> Path:
+    """The hand-written kernels' code objects as read-only data of one
+    shared library (symbols fk_kernels_co .. fk_kernels_co_end and
+    fk_attend_co .. fk_attend_co_end), which the package loads and hands to
+    fk_module_load: the process maps the library that holds the device code
+    it runs."""
+    import tempfile
+    with tempfile.TemporaryDirectory() as tmpdir:
+        asm = Path(tmpdir) / "fk_kernels_blob.S"
+        lines = ['.section .rodata']
+        for sym, co in (("fk_kernels_co", KERNELS_CO), ("fk_attend_co", ATTEND_CO)):
+            lines += [f".global {sym}", f".global {sym}_end", ".balign 4096", f"{sym}:",
+                      f'.incbin "{co}"', f"{sym}_end:"]
+        lines.append('.section .note.GNU-stack,"",@progbits')
+        asm.write_text("\n".join(lines) + "\n")
+        tmp = KERNELS_SO.with_suffix(".so.tmp")
+        _run(["gcc", "-shared", "-fPIC", str(asm), "-o", str(tmp)])
+        os.replace(tmp, KERNELS_SO)
+    return KERNELS_SO
+
+
 def build_all() -> list[Path]:
-    return [build_runtime(), build_kernels(), build_attend()]
+    return [build_runtime(), build_kernels(), build_attend(), build_kernel_library()]
 
 
 if __name__ == "__main__":

@@ -27,6 +27,9 @@ from . import runtime
 PACKAGE = Path(__file__).resolve().parent
 CODE_OBJECT = PACKAGE / "fk_kernels.hsaco"
 ATTEND_OBJECT = PACKAGE / "fk_attend.hsaco"   # the prefill attention, built apart (fk_attend.h)
+# Both code objects as read-only data of one shared library (build.py
+# build_kernel_library): what the device runs is mapped into the process.
+KERNEL_LIBRARY = PACKAGE / "libfkkernels.so"
 WAVE = 64
 
 
@@ -360,13 +363,20 @@ ATTEND_PREFIX = "fk_prefill_attend"
 class Kernels:
     """The code object loaded on a device, and a launcher per kernel family."""
 
-    def __init__(self, device: runtime.Device, path: Path = CODE_OBJECT, attend_path: Path = ATTEND_OBJECT):
-        for p in (path, attend_path):
-            if not Path(p).exists():
-                raise runtime.NativeMissing(f"{p} is not built; run __graft_entry__.build()")
+    def __init__(self, device: runtime.Device, library: Path = KERNEL_LIBRARY):
+        if not Path(library).exists():
+            raise runtime.NativeMissing(f"{library} is not built; run __graft_entry__.build()")
         self.device = device
-        self.module = device.load_module(path)
-        self.attend_module = device.load_module(attend_path)
+        self.library = ctypes.CDLL(str(library))
+        images = []
+        for sym in ("fk_kernels_co", "fk_attend_co"):
+            start = ctypes.addressof(ctypes.c_char.in_dll(self.library, sym))
+            end = ctypes.addressof(ctypes.c_char.in_dll(self.library, sym + "_end"))
+            if end <= start:
+                raise runtime.NativeMissing(f"{library}: {sym} is empty")
+            images.append((start, end - start))
+        self.module = device.load_module_image(*images[0])
+        self.attend_module = device.load_module_image(*images[1])
 
     def fn(self, entry: str) -> runtime.Function:
         module = self.attend_module if entry.startswith(ATTEND_PREFIX) else self.module

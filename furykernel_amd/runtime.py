@@ -449,6 +449,12 @@ class Device:
         _check(self.ctx, library().fk_module_load_file(self.ctx, str(path).encode(), ctypes.byref(h)))
         return Module(self, h.value)
 
+    def load_module_image(self, address: int, nbytes: int) -> Module:
+        """A code object held in host memory at `address` (`nbytes` long)."""
+        h = ctypes.c_void_p()
+        _check(self.ctx, library().fk_module_load(self.ctx, ctypes.c_void_p(address), nbytes, ctypes.byref(h)))
+        return Module(self, h.value)
+
     def event(self) -> Event:
         return Event(self)
 

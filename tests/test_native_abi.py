@@ -42,6 +42,20 @@ def test_code_object_holds_every_kernel_entry():
         assert entry.encode() + b"\0" in where, entry
 
 
+def test_the_kernel_library_holds_the_code_objects_the_package_loads():
+    """libfkkernels.so (what Kernels loads on a device) carries both code
+    objects byte for byte, between its start and end symbols."""
+    import ctypes
+
+    from furykernel_amd import kernels
+
+    lib = ctypes.CDLL(str(kernels.KERNEL_LIBRARY))
+    for sym, path in (("fk_kernels_co", kernels.CODE_OBJECT), ("fk_attend_co", kernels.ATTEND_OBJECT)):
+        start = ctypes.addressof(ctypes.c_char.in_dll(lib, sym))
+        end = ctypes.addressof(ctypes.c_char.in_dll(lib, sym + "_end"))
+        assert ctypes.string_at(start, end - start) == path.read_bytes(), sym
+
+
 def test_kernarg_is_pointers_then_c_layout_params():
     from furykernel_amd import kernels
 
