@@ -183,3 +183,57 @@ def test_prefill_norm_pack_against_f64(device, kernels, width):
     assert np.all(np.abs(got - want) <= np.abs(want) * (2.0**-11 + 2.0**-20) + 2.0**-25)
     for b in (bx, bg, by):
         b.free()
+
+
+@pytest.mark.parametrize("staged", [False, True], ids=["in-place", "staged"])
+def test_prefill_with_bf16_caches_against_the_f64_evaluator(device, kernels, staged):
+    """The small decoder with bf16 KV caches: the QKV epilogue rounds k and v
+    to bf16 (into the ring, or into staging rows that fk_prefill_land copies),
+    the attention widens them to f16 for the matrix cores.  Logits within the
+    f16 bar of the evaluator (which rounds its cache stores to bf16 too); each
+    cache element within the bar plus one bf16 unit in the last place of
+    itself, since an element next to a rounding boundary may round either way
+    from values that agree to the bar; tokens each row's argmax."""
+    from furykernel_amd.prefill import PrefillSession
+    from furykernel_amd.program.graph import CACHE_BF16
+
+    dims = dataclasses.replace(SMALL_PREFILL, cache_elem=CACHE_BF16)
+    s = PrefillSession(device, kernels, dims, SEQS, SEQ_ROWS, position_bound=dims.context if staged else None)
+    try:
+        assert s.staged == staged
+        assert all(l.params.get("cache_bf16") == 1 for l in s.lowered.launches if "cache_bf16" in l.params)
+        weights, tokens = small_state(s.checked)
+        s.write_weights(weights)
+        for name in s.lowered.buffers:
+            if name.startswith("cache:"):
+                s.engine.zero(name)
+        s.set_tokens(tokens)
+        print(f"prefill small, bf16 caches, staged {staged}", flush=True)
+        s.run()
+        device.sync()
+        lay = dims
+        caches = {}
+        for src in s.checked.program.sources:
+            if type(src.kind).__name__ == "SCache":
+                caches[src.name] = {u: np.zeros(lay.kv_heads * lay.context * lay.head_dim) for u in range(lay.slots)}
+        positions = np.tile(np.arange(SEQ_ROWS), SEQS)
+        slots = np.repeat(np.arange(SEQS), SEQ_ROWS)
+        ev = evaluate_fast(s.checked, Bindings(
+            SEQS * SEQ_ROWS, weights={k: np.asarray(v, np.float64) for k, v in weights.items()},
+            row_ints={"tokens": tokens[:, None], "position": positions[:, None], "slot": slots[:, None]},
+            caches=caches))
+        got = s.logits()
+        assert rel(got, ev.outputs["logits"]) <= BAR
+        assert np.array_equal(s.tokens(), np.argmax(got, axis=1))
+        for layer in range(lay.layers):
+            for kv in ("k", "v"):
+                name = f"l{layer}_{kv}_cache"
+                bits = s.engine.read(f"cache:{name}").view(np.uint16).astype(np.uint32)
+                g = (bits << 16).view(np.float32).astype(np.float64).reshape(lay.slots, lay.kv_heads, lay.context,
+                                                                             lay.head_dim)
+                w = np.stack([ev.caches[name][u] for u in range(lay.slots)]).reshape(g.shape)
+                gw, ww = g[:, :, :SEQ_ROWS], w[:, :, :SEQ_ROWS]
+                assert np.all(np.abs(gw - ww) <= BAR * np.max(np.abs(ww)) + 2.0 ** -7 * np.abs(ww)), name
+                assert np.all(g[:, :, SEQ_ROWS:] == 0)
+    finally:
+        s.close()
