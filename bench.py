@@ -147,15 +147,16 @@ def kernel_table(session, reps: int, eager: bool) -> dict:
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "traffic_decode_1b_f16.md"
+PREFILL_TRAFFIC_PROFILE = ROOT / "profiles" / "traffic_prefill_1b_f16.md"
 
 
-def measured_traffic(entry: str):
+def measured_traffic(entry: str, profile: Path = TRAFFIC_PROFILE):
     """HBM bytes a launch of `entry` moves, as the committed rocprofv3 counter
     runs measured them (FETCH_SIZE and WRITE_SIZE, each scaled by what it
     reads for a copy of known size); None if the profile has no row for it."""
-    if not TRAFFIC_PROFILE.exists():
+    if not profile.exists():
         return None
-    for line in TRAFFIC_PROFILE.read_text().splitlines():
+    for line in profile.read_text().splitlines():
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) == 7 and cells[0] == entry:
             return int(cells[4])
@@ -366,7 +367,11 @@ def main_prefill(args) -> int:
         "mfma": {"flops_per_prefill": flops, "achieved_tflops": round(tflops, 1),
                  "frac_of_peak": round(tflops / MFMA_PEAK_TFLOPS, 4), "peak_tflops": MFMA_PEAK_TFLOPS},
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": dom["tflops"], "peak": MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(dom["tflops"] / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(dom["tflops"] / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(dominant, PREFILL_TRAFFIC_PROFILE),
+                     "traffic_source": "read from profiles/traffic_prefill_1b_f16.md (the committed rocprofv3 "
+                                       "FETCH_SIZE and WRITE_SIZE runs of this workload: bytes leaving the L2s, "
+                                       "which the memory-side cache may serve), not measured in this run",
                      "avg_launch_us": dom["avg_us"], "flops_per_launch": dom["flops_per_launch"],
                      "launches_per_step": dom["launches"]},
         "kernels": table,
