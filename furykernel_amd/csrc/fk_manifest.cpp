@@ -269,6 +269,16 @@ std::vector<Entry> build() {
          buf("r0", "read", "f32"), buf("position", "read", "u32"), buf("slot", "read", "u32"),
          buf("rope", "read", "f32")},
         p, sizeof(S));
+    using SP = fk_gemm_qkv_paged_params;
+    p.push_back(fk_abi_param{"block_size", "u32", (uint32_t)(offsetof(SP, pg) + offsetof(fk_paging, block_size))});
+    p.push_back(fk_abi_param{"table_len", "u32", (uint32_t)(offsetof(SP, pg) + offsetof(fk_paging, table_len))});
+    p.push_back(fk_abi_param{"blocks", "u32", (uint32_t)(offsetof(SP, pg) + offsetof(fk_paging, blocks))});
+    add("fk_gemm_f16_qkv_rope_paged", 256,
+        {buf("a", "read", "f16"), buf("b0", "read", "f16"), buf("b1", "read", "f16"), buf("b2", "read", "f16"),
+         buf("c0", "write", "f16"), buf("c1", "read_write", "f16"), buf("c2", "read_write", "f16"),
+         buf("r0", "read", "f32"), buf("position", "read", "u32"), buf("table", "read", "u32"),
+         buf("rope", "read", "f32")},
+        p, sizeof(SP));
   }
   {
     using S = fk_prefill_gather_params;
@@ -315,6 +325,18 @@ std::vector<Entry> build() {
           {FK_P(S, rows, "u32"), FK_P(S, heads, "u32"), FK_P(S, kv_heads, "u32"), FK_P(S, length, "u32"),
            FK_P(S, slots, "u32"), FK_P(S, window, "u32"), FK_P(S, cache_bf16, "u32"), FK_P(S, scale, "f32"),
            FK_P(S, staged, "u32"), FK_P(S, run_rows, "u32")},
+          sizeof(S));
+  }
+  {
+    using S = fk_prefill_attend_paged_params;
+    for (int g : {1, 2, 4})
+      add("fk_prefill_attend_paged_g" + std::to_string(g), 64 * g,
+          {buf("qr", "read", "f16"), buf("kc", "read", "f16"), buf("vc", "read", "f16"),
+           buf("position", "read", "u32"), buf("table", "read", "u32"), buf("out", "write", "f16")},
+          {FK_P(S, a.rows, "u32"), FK_P(S, a.heads, "u32"), FK_P(S, a.kv_heads, "u32"), FK_P(S, a.length, "u32"),
+           FK_P(S, a.slots, "u32"), FK_P(S, a.window, "u32"), FK_P(S, a.cache_bf16, "u32"), FK_P(S, a.scale, "f32"),
+           FK_P(S, a.staged, "u32"), FK_P(S, a.run_rows, "u32"), FK_P(S, g.block_size, "u32"),
+           FK_P(S, g.table_len, "u32"), FK_P(S, g.blocks, "u32")},
           sizeof(S));
   }
   add("fk_prefill_softcap", 256, {buf("x", "read", "f32"), buf("y", "write", "f32")},
@@ -674,6 +696,19 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       need.push_back({"slot", 0});
       need.push_back({"rope", 0});
     }
+    if (std::strcmp(entry, "fk_gemm_f16_qkv_rope_paged") == 0) {
+      fk_gemm_qkv_paged_params q;
+      std::memcpy(&q, params, sizeof q);
+      if (q.pg.block_size == 0 || q.pg.table_len == 0 || q.pg.blocks == 0 || q.r.staged || q.r.kv_heads == 0)
+        return bad(err, cap, FK_ERR_ARG, "%s: blocks of %u positions, tables of %u, a pool of %u, staged %u", entry,
+                   q.pg.block_size, q.pg.table_len, q.pg.blocks, q.r.staged);
+      const uint64_t pool = (uint64_t)q.pg.blocks * q.r.kv_heads * q.pg.block_size * 64 * 2;
+      need.push_back({"position", (uint64_t)p.m * 4});
+      need.push_back({"table", (uint64_t)p.m * q.pg.table_len * 4});
+      need.push_back({"rope", 0});
+      for (Need &n : need)
+        if (std::strcmp(n.name, "c1") == 0 || std::strcmp(n.name, "c2") == 0) n.bytes = pool;
+    }
   } else if (std::strncmp(entry, "fk_prefill_attend_g", 19) == 0) {
     fk_prefill_attend_params p;
     std::memcpy(&p, params, sizeof p);
@@ -699,6 +734,23 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       return bad(err, cap, FK_ERR_ARG, "%s: %u rows of %u keys in %u x %u threads", entry, p.rows, p.parts, groups,
                  threads);
     need = {{"keys", (uint64_t)p.rows * p.parts * 8}, {"out", (uint64_t)p.rows * 4}};
+  } else if (std::strncmp(entry, "fk_prefill_attend_paged_g", 25) == 0) {
+    fk_prefill_attend_paged_params pp;
+    std::memcpy(&pp, params, sizeof pp);
+    const fk_prefill_attend_params &p = pp.a;
+    const uint32_t g = (uint32_t)(entry[std::strlen(entry) - 1] - '0');
+    if (p.rows == 0 || p.rows % 32 || p.kv_heads == 0 || p.heads != g * p.kv_heads || p.staged ||
+        (p.run_rows && (p.run_rows % 32 || p.rows % p.run_rows)) || pp.g.block_size == 0 || pp.g.table_len == 0 ||
+        pp.g.blocks == 0 || groups != (p.rows / 32) * p.kv_heads)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows, %u heads over %u, blocks of %u, tables of %u, %u threadgroups",
+                 entry, p.rows, p.heads, p.kv_heads, pp.g.block_size, pp.g.table_len, groups);
+    const uint64_t pool = (uint64_t)pp.g.blocks * p.kv_heads * pp.g.block_size * 64 * 2;
+    need = {{"qr", (uint64_t)p.rows * p.heads * 64 * 2},
+            {"kc", pool},
+            {"vc", pool},
+            {"position", (uint64_t)p.rows * 4},
+            {"table", (uint64_t)p.rows * pp.g.table_len * 4},
+            {"out", (uint64_t)p.rows * p.heads * 64 * 2}};
   } else if (std::strcmp(entry, "fk_prefill_land") == 0) {
     fk_prefill_land_params p;
     std::memcpy(&p, params, sizeof p);

@@ -61,12 +61,16 @@ typedef short fk_short4 __attribute__((ext_vector_type(4)));
 typedef _Float16 fk_half2 __attribute__((ext_vector_type(2)));
 typedef float fk_float2v __attribute__((ext_vector_type(2)));
 
-template <uint32_t G>
+// PG: the caches are paged pools ([blocks][kv_heads][block_size][64]) and
+// `slot` the rows' block tables ([rows][table_len]); a block of rows reads
+// its first row's table (its rows are one sequence's).
+template <uint32_t G, bool PG = false>
 __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc,
                                                const uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                                                const uint32_t *__restrict__ slot, uint16_t *__restrict__ out,
                                                const uint16_t *__restrict__ kst, const uint16_t *__restrict__ vst,
-                                               const fk_prefill_attend_params &p) {
+                                               const fk_prefill_attend_params &p,
+                                               const fk_paging &pg = fk_paging{}) {
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][FK_ATT_KB * 64];
   __shared__ __attribute__((aligned(16))) uint16_t vs[2][FK_ATT_KB * 64];
   constexpr uint32_t nthreads = G * FK_WAVE;
@@ -87,7 +91,8 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   const uint32_t g = rest % p.kv_heads;                                               // kv head
   const uint32_t h = g * G + wave;                   // this wavefront's query head
   const uint32_t p0 = position[r0];
-  const uint32_t sl = min(slot[r0], p.slots - 1);
+  const uint32_t sl = PG ? 0u : min(slot[r0], p.slots - 1);
+  const uint32_t *const tab = slot + (size_t)r0 * pg.table_len;  // PG: the block's table
   const bool bf16 = p.cache_bf16 != 0;
   const uint32_t qw = p.heads * 64;
   const uint32_t qrow = r0 + lane % 32;
@@ -119,7 +124,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // rows, consecutive positions of one slot), position start; keys from
   // there on are read from the staging rows [rows][kv_heads][64], the
   // earlier ones from the ring.
-  const bool staged = p.staged != 0;
+  const bool staged = !PG && p.staged != 0;
   const uint32_t rf = staged ? (r0 / p.run_rows) * p.run_rows : 0u;
   const uint32_t start = staged ? position[rf] : 0xFFFFFFFFu;
 
@@ -145,8 +150,15 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
       const bool live = t <= last_pos;
       // A staged row's index, clamped into the step's rows.
       const uint32_t srow = min(rf + (t - min(t, start)), p.rows - 1);
-      const uint16_t *src = staged && t >= start ? stage + ((size_t)srow * p.kv_heads + g) * 64 + c8
-                                                 : cache + cache_base + (size_t)(ring0 + key) * 64 + c8;
+      const uint16_t *src;
+      if constexpr (PG) {
+        // position t's block through the table, both clamped into place
+        const uint32_t blk = min(tab[min(t / pg.block_size, pg.table_len - 1)], pg.blocks - 1);
+        src = cache + (((size_t)blk * p.kv_heads + g) * pg.block_size + t % pg.block_size) * 64 + c8;
+      } else {
+        src = staged && t >= start ? stage + ((size_t)srow * p.kv_heads + g) * 64 + c8
+                                   : cache + cache_base + (size_t)(ring0 + key) * 64 + c8;
+      }
       reg[e] = live ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
     }
   };
@@ -315,4 +327,17 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
 FK_PREFILL_ATTEND(1)
 FK_PREFILL_ATTEND(2)
 FK_PREFILL_ATTEND(4)
+
+// The same over paged pools: kc and vc the pools, `table` the rows' block
+// tables; no staged rows.
+#define FK_PREFILL_ATTEND_PAGED(G)                                                                                \
+  extern "C" __global__ void __launch_bounds__(64 * G) fk_prefill_attend_paged_g##G(                             \
+      const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,         \
+      const uint32_t *__restrict__ position, const uint32_t *__restrict__ table, uint16_t *__restrict__ out,     \
+      fk_prefill_attend_paged_params p) {                                                                        \
+    prefill_attend<G, true>(qr, kc, vc, position, table, out, nullptr, nullptr, p.a, p.g);                       \
+  }
+FK_PREFILL_ATTEND_PAGED(1)
+FK_PREFILL_ATTEND_PAGED(2)
+FK_PREFILL_ATTEND_PAGED(4)
 

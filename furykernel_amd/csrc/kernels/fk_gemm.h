@@ -61,7 +61,8 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
                                           const uint32_t *__restrict__ slot = nullptr,
                                           const float *__restrict__ rope = nullptr,
                                           const fk_gemm_rope_params &rp = fk_gemm_rope_params{},
-                                          uint64_t *__restrict__ keys = nullptr) {
+                                          uint64_t *__restrict__ keys = nullptr,
+                                          const fk_paging &pg = fk_paging{}) {
   extern __shared__ uint4 gemm_lds[];
   constexpr uint32_t ROW16 = FK_GEMM_BK * 2 / 16;           // 16-byte units a staged row takes
   constexpr uint32_t TILEB = FK_GEMM_BM * FK_GEMM_BK * 2;    // bytes of one operand's staged tile
@@ -306,7 +307,7 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
     };
     if (p.act == FK_ACT_GELU_TANH) act_mul_tiles(fk_bool_tag<true>{});
     else act_mul_tiles(fk_bool_tag<false>{});
-  } else if (MODE == FK_GEMM_QKV_ROPE) {
+  } else if (MODE == FK_GEMM_QKV_ROPE || MODE == FK_GEMM_QKV_ROPE_PAGED) {
     // A 256-column tile is 4 whole heads, a wavefront's 128 columns 2; a
     // lane's blocks 4 jp + jj and 4 jp + jj + 2 hold columns d and d + 32 of
     // head jp, both elements of each pair RoPE turns (NeoX halves, as
@@ -320,17 +321,26 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
     const bool turn = anchor != 2;
     const uint32_t head0 = (n0 + wn * 128) / 64;
     uint16_t *const dst = reinterpret_cast<uint16_t *>(anchor == 0 ? c0 : (anchor == 1 ? c1 : c2));
-    // halves from head to head: q's rows and staged k, v rows hold a row's heads side by side
-    const size_t hstride = anchor == 0 || rp.staged ? 64 : (size_t)rp.length * 64;
+    // halves from head to head: q's rows and staged k, v rows hold a row's
+    // heads side by side, a ring a head's length positions apart, a paged
+    // pool's block a block's positions apart
+    constexpr bool PAGED = MODE == FK_GEMM_QKV_ROPE_PAGED;
+    const size_t hstride = anchor == 0 || rp.staged ? 64 : (PAGED ? (size_t)pg.block_size : (size_t)rp.length) * 64;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t row = m + 16 * i;
       const uint32_t pos = position[row];
-      const uint32_t sl = min(slot[row], rp.slots - 1);
+      // PAGED: `slot` holds the rows' block tables; position pos's block,
+      // the table index and the block clamped into place
+      const uint32_t sl = PAGED ? min(slot[(size_t)row * pg.table_len + min(pos / pg.block_size, pg.table_len - 1)],
+                                      pg.blocks - 1)
+                                : min(slot[row], rp.slots - 1);
       const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
-      uint16_t *const base = anchor == 0 ? dst + (size_t)row * p.ldc[0] + head0 * 64
-                             : rp.staged ? dst + ((size_t)row * rp.kv_heads + head0) * 64
-                                         : dst + (((size_t)sl * rp.kv_heads + head0) * rp.length + pos % rp.length) * 64;
+      uint16_t *const base =
+          anchor == 0 ? dst + (size_t)row * p.ldc[0] + head0 * 64
+          : rp.staged ? dst + ((size_t)row * rp.kv_heads + head0) * 64
+          : PAGED     ? dst + (((size_t)sl * rp.kv_heads + head0) * pg.block_size + pos % pg.block_size) * 64
+                      : dst + (((size_t)sl * rp.kv_heads + head0) * rp.length + pos % rp.length) * 64;
 #pragma unroll
       for (int jp = 0; jp < 2; jp++)
 #pragma unroll
@@ -458,4 +468,15 @@ extern "C" __global__ void __launch_bounds__(FK_GEMM_THREADS)
                          const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot,
                          const float *__restrict__ rope, fk_gemm_qkv_params p) {
   gemm_tile<FK_GEMM_QKV_ROPE>(a, b0, b1, b2, c0, c1, c2, r0, p.g, position, slot, rope, p.r);
+}
+
+// The same with the K and V caches paged pools ([blocks][kv_heads][block
+// size][64]) and `table` the rows' block tables ([rows][table_len]).
+extern "C" __global__ void __launch_bounds__(FK_GEMM_THREADS)
+    fk_gemm_f16_qkv_rope_paged(const _Float16 *__restrict__ a, const _Float16 *__restrict__ b0,
+                               const _Float16 *__restrict__ b1, const _Float16 *__restrict__ b2, void *__restrict__ c0,
+                               void *__restrict__ c1, void *__restrict__ c2, const float *r0,
+                               const uint32_t *__restrict__ position, const uint32_t *__restrict__ table,
+                               const float *__restrict__ rope, fk_gemm_qkv_paged_params p) {
+  gemm_tile<FK_GEMM_QKV_ROPE_PAGED>(a, b0, b1, b2, c0, c1, c2, r0, p.g, position, table, rope, p.r, nullptr, p.pg);
 }

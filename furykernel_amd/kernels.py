@@ -129,6 +129,18 @@ class PrefillAttendParams(ctypes.Structure):
                 ("run_rows", ctypes.c_uint32)]
 
 
+class GemmQkvPagedParams(ctypes.Structure):
+    """fk_gemm_qkv_paged_params: the QKV GEMM's, then the pools' paging."""
+    _fields_ = GemmQkvParams._fields_ + [("block_size", ctypes.c_uint32), ("table_len", ctypes.c_uint32),
+                                         ("blocks", ctypes.c_uint32)]
+
+
+class PrefillAttendPagedParams(ctypes.Structure):
+    """fk_prefill_attend_paged_params: the attention's, then the pools' paging."""
+    _fields_ = PrefillAttendParams._fields_ + [("block_size", ctypes.c_uint32), ("table_len", ctypes.c_uint32),
+                                               ("blocks", ctypes.c_uint32)]
+
+
 class PrefillLandParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
                 ("length", ctypes.c_uint32), ("slots", ctypes.c_uint32)]
@@ -306,6 +318,9 @@ ABIS: dict[str, KernelAbi] = {
                                                                    "keys"), GemmParams, 256),
     "fk_gemm_f16_qkv_rope": KernelAbi("fk_gemm_f16_qkv_rope", ("a", "b0", "b1", "b2", "c0", "c1", "c2", "r0",
                                                                "position", "slot", "rope"), GemmQkvParams, 256),
+    "fk_gemm_f16_qkv_rope_paged": KernelAbi("fk_gemm_f16_qkv_rope_paged", ("a", "b0", "b1", "b2", "c0", "c1", "c2",
+                                                                           "r0", "position", "table", "rope"),
+                                            GemmQkvPagedParams, 256),
     "fk_prefill_gather": KernelAbi("fk_prefill_gather", ("table", "tokens", "x"), PrefillGatherParams, 256),
     "fk_prefill_norm_pack": KernelAbi("fk_prefill_norm_pack", ("x", "gamma", "y"), PrefillNormParams, 256),
     **{f"fk_prefill_norm_pack_w{w}": KernelAbi(f"fk_prefill_norm_pack_w{w}", ("x", "gamma", "y"), PrefillNormParams,
@@ -315,6 +330,10 @@ ABIS: dict[str, KernelAbi] = {
     **{f"fk_prefill_attend_g{g}": KernelAbi(f"fk_prefill_attend_g{g}", ("qr", "kc", "vc", "position", "slot",
                                                                         "out", "ks", "vs"), PrefillAttendParams,
                                             64 * g)
+       for g in (1, 2, 4)},
+    **{f"fk_prefill_attend_paged_g{g}": KernelAbi(f"fk_prefill_attend_paged_g{g}", ("qr", "kc", "vc", "position",
+                                                                                    "table", "out"),
+                                                  PrefillAttendPagedParams, 64 * g)
        for g in (1, 2, 4)},
     "fk_prefill_land": KernelAbi("fk_prefill_land", ("ks", "vs", "position", "slot", "kc", "vc"),
                                  PrefillLandParams, 256),
@@ -693,6 +712,8 @@ def launch_reads(entry: str, params: dict) -> set[str]:
             need.add("r0")
         if entry == "fk_gemm_f16_qkv_rope":
             need |= {"position", "slot", "rope"}
+        if entry == "fk_gemm_f16_qkv_rope_paged":
+            need |= {"position", "table", "rope"}
         if entry == "fk_gemm_f16_store_keys":
             need.add("keys")
         return need

@@ -50,7 +50,7 @@ from .layout import SLAB, pack, pair
 from .lower import ACT, Launch, Lowered, LoweringError, rope_table
 from .program.check import CheckedProgram
 from .program.graph import (
-    CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, Gather, GeluMul, Input, KvStore, Linear, Ring,
+    CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, Gather, GeluMul, Input, KvStore, Linear, Paged, Ring,
     RmsNorm, Softcap,
     Rope, ROPE_HALVES, SCache, SInput, SRowInts, SWeight, op_values)
 from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
@@ -75,6 +75,10 @@ def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int, run_rows: Opti
     _Prefill(out, run_rows).run()
     _fuse_qkv_rope(out)
     _fuse_argmax(out)
+    for L in out.launches:
+        if L.entry == "fk_prefill_rope_store" and L.meta.get("paging"):
+            raise LoweringError(f"{L.step}: stores into a paged pool are made by the QKV GEMM's epilogue, which "
+                                f"needs q, k and v from one GEMM and RoPE on every pair of the heads of 64")
     return out
 
 
@@ -137,12 +141,13 @@ def _fuse_qkv_rope(out: Lowered) -> None:
             i += 1
             continue
         p = rs.params
+        paging = rs.meta.get("paging")
         bind = dict(gm.bind, c0=rs.bind["qr"], c1=rs.bind["kc"], c2=rs.bind["vc"], position=rs.bind["position"],
-                    slot=rs.bind["slot"], rope=rs.bind["rope"])
+                    rope=rs.bind["rope"], **{"table" if paging else "slot": rs.bind["slot"]})
         params = dict(gm.params, kv_heads=p["kv_heads"], rope_rows=p["rope_rows"], length=p["length"],
-                      slots=p["slots"], cache_bf16=p["cache_bf16"], staged=p["staged"])
-        launches[j] = Launch(gm.step, "fk_gemm_f16_qkv_rope", gm.groups, gm.threads, bind, params, {},
-                             gm.lds_bytes)
+                      slots=p["slots"], cache_bf16=p["cache_bf16"], staged=p["staged"], **(paging or {}))
+        launches[j] = Launch(gm.step, "fk_gemm_f16_qkv_rope_paged" if paging else "fk_gemm_f16_qkv_rope",
+                             gm.groups, gm.threads, bind, params, {}, gm.lds_bytes)
         del launches[i]
         for name in qkv:
             del out.buffers[name]
@@ -224,13 +229,25 @@ class _Prefill:
             raise LoweringError(f"{src.name}: the prefill kernels take one integer a row")
         return self.out.buffer(f"ints:{src.name}", "u32", self.rows)
 
-    def cache(self, s: int) -> tuple[str, Ring, bool]:
+    def tables(self, s: int) -> tuple[str, int]:
+        """The rows' block tables, [rows][table length] u32."""
         src = self.p.source(s)
-        if not isinstance(src.kind, SCache) or not isinstance(src.kind.layout, Ring):
-            raise LoweringError(f"{src.name}: the prefill attention takes ring caches")
+        if not isinstance(src.kind, SRowInts):
+            raise LoweringError(f"{src.name}: block tables are row integers")
+        return self.out.buffer(f"ints:{src.name}", "u32", self.rows * src.kind.count), src.kind.count
+
+    def cache(self, s: int) -> tuple[str, object, bool]:
+        """A ring's or a paged pool's buffer ([slots][kv heads][length][d] or
+        [blocks][kv heads][block size][d]), its layout, whether bf16."""
+        src = self.p.source(s)
+        if not isinstance(src.kind, SCache) or not isinstance(src.kind.layout, (Ring, Paged)):
+            raise LoweringError(f"{src.name}: the prefill attention takes ring caches and paged pools")
         lay = src.kind.layout
         bf16 = src.kind.elem == CACHE_BF16
-        count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
+        if isinstance(lay, Ring):
+            count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
+        else:
+            count = lay.blocks * lay.kv_heads * lay.block_size * lay.head_dim
         return self.out.buffer(f"cache:{src.name}", "bf16" if bf16 else "f16", count), lay, bf16
 
     def rope(self, spec, d: int, rows: int) -> str:
@@ -439,9 +456,16 @@ class _Prefill:
         vname, vlay, vbf = self.cache(op.to.values)
         if klay != vlay or kbf != vbf or klay.kv_heads != spec.kv_heads or klay.head_dim != HEAD_DIM:
             raise LoweringError(f"{step.name}: key and value caches of different layouts")
-        if klay.length % ATTEND_KEYS:
-            raise LoweringError(f"{step.name}: a ring of {klay.length}; the prefill attention reads keys by "
-                                f"blocks of {ATTEND_KEYS} that must not wrap")
+        paged = isinstance(klay, Paged)
+        if paged:
+            table, table_len = self.tables(op.to.sequences)
+            length = table_len * klay.block_size   # the positions a row's table covers
+            paging = {"block_size": klay.block_size, "table_len": table_len, "blocks": klay.blocks}
+        else:
+            length, paging = klay.length, None
+            if klay.length % ATTEND_KEYS:
+                raise LoweringError(f"{step.name}: a ring of {klay.length}; the prefill attention reads keys by "
+                                    f"blocks of {ATTEND_KEYS} that must not wrap")
         stores = {}
         for n in self.pending:
             at = n.op.at
@@ -456,6 +480,8 @@ class _Prefill:
         if len(staged) != 1:
             raise LoweringError(f"{step.name}: one of the attention's stores staged, the other not")
         staged = staged.pop()
+        if staged and paged:
+            raise LoweringError(f"{step.name}: staged stores into paged pools")
         k_raw, k_rope = self.roped(step, stores[op.to.keys].op.x)
         q_raw, q_rope = self.roped(step, op.q)
         v_raw = stores[op.to.values].op.x
@@ -468,7 +494,8 @@ class _Prefill:
         if self.width(q_raw) != heads * HEAD_DIM or self.width(k_raw) != kvh * HEAD_DIM or \
                 self.width(v_raw) != kvh * HEAD_DIM:
             raise LoweringError(f"{step.name}: q, k, v rows of other widths than the heads'")
-        pos, seq = self.ints(op.to.positions), self.ints(op.to.sequences)
+        pos = self.ints(op.to.positions)
+        seq = table if paged else self.ints(op.to.sequences)
         qr = self.out.buffer(f"qrot:{self.p.value(op.q).name}", "f16", heads * HEAD_DIM * self.rows)
         ks = vs = None
         if staged:
@@ -477,24 +504,31 @@ class _Prefill:
             vs = self.out.buffer(f"staged:{vname[len('cache:'):]}", elem, self.rows * kvh * HEAD_DIM)
             self.landing[stores[op.to.keys].id] = (ks, kname)
             self.landing[stores[op.to.values].id] = (vs, vname)
-        self.launch(step, "fk_prefill_rope_store", self.rows, 256,
-                    {"q": self.rows_value(step, q_raw), "k": self.rows_value(step, k_raw),
-                     "v": self.rows_value(step, v_raw), "position": pos, "slot": seq,
-                     "rope": self.rope(rs, HEAD_DIM, klay.length), "qr": qr, "kc": ks or kname, "vc": vs or vname},
-                    {"rows": self.rows, "heads": heads, "kv_heads": kvh, "head_dim": HEAD_DIM, "rotated": rs.rotated,
-                     "rope_rows": klay.length, "length": klay.length, "slots": klay.slots, "cache_bf16": int(kbf),
-                     "staged": int(staged)})
+        # (into a paged pool only through the QKV GEMM's epilogue: a RoPE
+        # launch left over after the fold is refused, with its paging in meta)
+        self.out.launches.append(Launch(
+            step.name, "fk_prefill_rope_store", self.rows, 256,
+            {"q": self.rows_value(step, q_raw), "k": self.rows_value(step, k_raw),
+             "v": self.rows_value(step, v_raw), "position": pos, "slot": seq,
+             "rope": self.rope(rs, HEAD_DIM, length), "qr": qr, "kc": ks or kname, "vc": vs or vname},
+            {"rows": self.rows, "heads": heads, "kv_heads": kvh, "head_dim": HEAD_DIM, "rotated": rs.rotated,
+             "rope_rows": length, "length": length, "slots": 0 if paged else klay.slots, "cache_bf16": int(kbf),
+             "staged": int(staged)}, {"paging": paging} if paged else {}, 0))
         outv = anchor.outputs[0]
         obuf = self.value_tiled(outv)
         self.tiled_of[outv] = obuf
         g = heads // kvh
-        self.launch(step, f"fk_prefill_attend_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
-                    {"qr": qr, "kc": kname, "vc": vname, "position": pos, "slot": seq, "out": obuf,
-                     "ks": ks, "vs": vs},
-                    {"rows": self.rows, "heads": heads, "kv_heads": kvh, "length": klay.length,
-                     "slots": klay.slots, "window": spec.window or 0, "cache_bf16": int(kbf),
-                     "scale": float(np.float32(spec.scale)), "staged": int(staged),
-                     "run_rows": self.run_rows})
+        params = {"rows": self.rows, "heads": heads, "kv_heads": kvh, "length": length,
+                  "slots": 0 if paged else klay.slots, "window": spec.window or 0, "cache_bf16": int(kbf),
+                  "scale": float(np.float32(spec.scale)), "staged": int(staged), "run_rows": self.run_rows}
+        if paged:
+            self.launch(step, f"fk_prefill_attend_paged_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
+                        {"qr": qr, "kc": kname, "vc": vname, "position": pos, "table": seq, "out": obuf},
+                        dict(params, **paging))
+        else:
+            self.launch(step, f"fk_prefill_attend_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
+                        {"qr": qr, "kc": kname, "vc": vname, "position": pos, "slot": seq, "out": obuf,
+                         "ks": ks, "vs": vs}, params)
 
     def combine_step(self, step: Step) -> None:
         # The prefill attention finishes its rows in one launch: nothing to
@@ -569,7 +603,8 @@ class PrefillSession:
     step's (the same names, layout and rounding)."""
 
     def __init__(self, device, kernels, dims, seqs: int, seq_rows: int, layers: Optional[int] = None,
-                 embed: bool = True, rope_rotated: Optional[int] = None, position_bound: Optional[int] = None):
+                 embed: bool = True, rope_rotated: Optional[int] = None, position_bound: Optional[int] = None,
+                 paging: Optional[tuple] = None, tables: Optional[np.ndarray] = None):
         from .engine import Engine
         from .program.check import check_program
         from .program.decoder import decoder_step
@@ -584,7 +619,7 @@ class PrefillSession:
         # default): a bound past what the ring holds beyond a step's rows
         # makes the plan stage the KV stores.
         self.program = decoder_step(dims, "prefill", embed, layers, position_bound=position_bound or seq_rows,
-                                    rope_rotated=rope_rotated)
+                                    rope_rotated=rope_rotated, paging=paging)
         self.checked = check_program(self.program)
         self.plan = plan(PlanOptions(sequence_rows=seq_rows), self.checked)
         self.lowered = lower_prefill(self.checked, self.plan, self.rows, run_rows=seq_rows)
@@ -593,7 +628,21 @@ class PrefillSession:
         slots = np.repeat(np.arange(seqs, dtype=np.uint32), seq_rows)
         check_rows(positions, slots, seq_rows)
         self.engine.set_ints("position", positions, seq_rows)
-        self.engine.set_ints("slot", slots, dims.slots)
+        if paging is None:
+            self.engine.set_ints("slot", slots, dims.slots)
+        else:
+            # Paged pools (paging = (block size, pool blocks)): sequence i's
+            # block table is row i of `tables` (default: distinct blocks in a
+            # scrambled order), every row of the sequence carrying it.
+            block_size, pool_blocks = paging
+            table_len = dims.context // block_size
+            if tables is None:
+                if seqs * table_len > pool_blocks:
+                    raise LoweringError(f"{seqs} tables of {table_len} blocks in a pool of {pool_blocks}")
+                perm = np.random.default_rng(0).permutation(pool_blocks)[:seqs * table_len]
+                tables = perm.reshape(seqs, table_len)
+            self.tables = np.asarray(tables, np.uint32).reshape(seqs, table_len)
+            self.engine.set_ints("blocks", np.repeat(self.tables, seq_rows, axis=0), pool_blocks)
 
     def weight_buffers(self):
         return [name for name in self.lowered.layouts]

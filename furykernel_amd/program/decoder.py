@@ -15,7 +15,7 @@ from dataclasses import dataclass
 from typing import Optional
 
 from .build import ProgramBuilder, program
-from .graph import BF16, CACHE_F16, F16, F32, GELU_TANH, SILU, AttnSpec, Program, Ring, RopeSpec, whole_row
+from .graph import BF16, CACHE_F16, F16, F32, GELU_TANH, SILU, AttnSpec, Paged, Program, Ring, RopeSpec, whole_row
 
 
 @dataclass(frozen=True)
@@ -75,20 +75,29 @@ SMALL_PREFILL = DecoderDims(d_model=256, layers=2, heads=8, kv_heads=4, head_dim
 
 def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
                  layers: Optional[int] = None, position_bound: Optional[int] = None,
-                 rope_rotated: Optional[int] = None) -> Program:
+                 rope_rotated: Optional[int] = None, paging: Optional[tuple] = None) -> Program:
     """One step of the decoder over the rows it is given (one a decode step,
     a sequence's run of rows a prefill): ``embed`` gathers each token's row
     of ``embed`` (else the rows ``x`` are an input); outputs ``logits`` and
     the greedy ``token`` of every row.  Positions are declared below
     ``position_bound`` (default: the context), which decides whether a
     step's KV stores fit the ring in place (Plan.hs:276-281).  RoPE turns
-    ``rope_rotated`` pairs of each head (default: all, head_dim / 2)."""
+    ``rope_rotated`` pairs of each head (default: all, head_dim / 2).
+    ``paging`` = (block size, pool blocks): the caches are paged pools
+    (Graph.hs:144-152) and each row carries its block table (``blocks``, the
+    context's positions in blocks) in place of its ring slot."""
     L = dims.layers if layers is None else layers
     wt = dims.weight_type
 
     def body(b: ProgramBuilder):
         pos = b.row_ints("position", 1, dims.context if position_bound is None else position_bound)
-        slot = b.row_ints("slot", 1, dims.slots)
+        if paging is None:
+            slot = b.row_ints("slot", 1, dims.slots)
+            layout = Ring(dims.slots, dims.kv_heads, dims.context, dims.head_dim)
+        else:
+            block_size, pool_blocks = paging
+            slot = b.row_ints("blocks", dims.context // block_size, pool_blocks)
+            layout = Paged(pool_blocks, block_size, dims.kv_heads, dims.head_dim)
         if embed:
             tokens = b.row_ints("tokens", 1, dims.vocab)
             table = b.weight("embed", [dims.vocab, dims.d_model], wt)
@@ -108,8 +117,8 @@ def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
             wg = b.weight(p + "gate_proj", [dims.ffn, dims.d_model], wt)
             wu = b.weight(p + "up_proj", [dims.ffn, dims.d_model], wt)
             wd = b.weight(p + "down_proj", [dims.d_model, dims.ffn], wt)
-            kc = b.cache(p + "k_cache", Ring(dims.slots, dims.kv_heads, dims.context, dims.head_dim), dims.cache_elem)
-            vc = b.cache(p + "v_cache", Ring(dims.slots, dims.kv_heads, dims.context, dims.head_dim), dims.cache_elem)
+            kc = b.cache(p + "k_cache", layout, dims.cache_elem)
+            vc = b.cache(p + "v_cache", layout, dims.cache_elem)
             a = b.rmsnorm(p + "attn_in", dims.eps, g_attn, 1.0, x)
             q = b.linear(p + "q", wq, dims.head_dim, a)
             k = b.linear(p + "k", wk, dims.head_dim, a)

@@ -25,6 +25,10 @@
  *   fk_gemm_f16_qkv_rope a b0 b1 b2 c0 c1 c2 r0 position slot rope
  *                                                      fk_gemm_qkv_params
  *   fk_gemm_f16_store_keys a b0 b1 b2 c0 c1 c2 r0 keys  fk_gemm_params
+ *   fk_gemm_f16_qkv_rope_paged a b0 b1 b2 c0 c1 c2 r0 position table rope
+ *                                                      fk_gemm_qkv_paged_params
+ *   fk_prefill_attend_paged_g<1|2|4> qr kc vc position table out
+ *                                                      fk_prefill_attend_paged_params
  *   fk_prefill_argmax_keys keys out                    fk_prefill_argmax_keys_params
  *   (the manifest lists every entry.)
  */
@@ -265,8 +269,9 @@ enum {
   FK_GEMM_SILU_MUL = 2, /* C = f16(silu(A G^T) (A U^T)) in the tile layout; B0 the paired gate/up weights */
   FK_GEMM_QKV_ROPE = 3, /* anchors q, k, v: q RoPE'd into f16 rows (C0), k RoPE'd into the K cache (C1), v into
                            the V cache (C2), at each row's slot and position */
-  FK_GEMM_STORE_KEYS = 4 /* one anchor's C = A B^T (f32 rows), and for each row and 128 columns the greedy token's
-                            64-bit key of their largest element: keys [M][N / 128] */
+  FK_GEMM_STORE_KEYS = 4, /* one anchor's C = A B^T (f32 rows), and for each row and 128 columns the greedy
+                             token's 64-bit key of their largest element: keys [M][N / 128] */
+  FK_GEMM_QKV_ROPE_PAGED = 5 /* FK_GEMM_QKV_ROPE with the caches paged pools, through each row's block table */
 };
 
 typedef struct fk_gemm_params {
@@ -291,6 +296,13 @@ typedef struct fk_gemm_qkv_params {
   fk_gemm_params g;
   fk_gemm_rope_params r;
 } fk_gemm_qkv_params;
+
+/* fk_gemm_f16_qkv_rope_paged: `r.length` and `r.slots` unused, no staged rows. */
+typedef struct fk_gemm_qkv_paged_params {
+  fk_gemm_params g;
+  fk_gemm_rope_params r;
+  fk_paging pg;
+} fk_gemm_qkv_paged_params;
 
 typedef struct fk_prefill_gather_params {
   uint32_t rows;
@@ -334,6 +346,14 @@ typedef struct fk_prefill_attend_params {
   uint32_t run_rows; /* each sequence's run of rows in the step, a multiple of 32 dividing rows (0: one run);
                        staged runs read their own rows from ks and vs */
 } fk_prefill_attend_params;
+
+/* fk_prefill_attend_paged_g*: the attention over paged pools; `a.slots`,
+ * `a.staged` and `a.run_rows` unused, `a.length` the positions a table covers
+ * (table_len block_size). */
+typedef struct fk_prefill_attend_paged_params {
+  fk_prefill_attend_params a;
+  fk_paging g;
+} fk_prefill_attend_paged_params;
 
 /* The staged rows landed in the ring (src/FuryKernel/Program/Plan.hs:41-50):
  * row r's kv heads from ks and vs ([rows][kv_heads][head_dim]) into kc and

@@ -139,3 +139,49 @@ def test_staged_1b_prefill_is_the_in_place_one(device, kernels):
             assert np.array_equal(ca[n], b.engine.read(n))
     finally:
         b.close()
+
+
+def _pool_as_rings(pool, tables, kv_heads, block_size, d):
+    """A pool [blocks][kv_heads][block_size][d] read through each sequence's
+    table as rings [sequences][kv_heads][table_len block_size][d]."""
+    p = pool.reshape(-1, kv_heads, block_size, d)
+    return np.stack([np.concatenate([p[b] for b in t], axis=1) for t in tables])
+
+
+@pytest.mark.parametrize("dims,seqs,rows,layers,paging", [
+    (SMALL_PREFILL, SEQS, SEQ_ROWS, None, (64, 11)),
+    (ONE_B_PREFILL, 4, 2048, 2, (64, 300)),
+], ids=["small", "1b-two-layers"])
+def test_paged_prefill_is_the_ring_prefill_bit_for_bit(device, kernels, dims, seqs, rows, layers, paging):
+    """The caches as paged pools, each sequence's rows through a scrambled
+    block table: logits and tokens are the ring prefill's bit for bit, and
+    the pool read through the tables holds the ring's rows."""
+    from furykernel_amd.prefill import PrefillSession
+    tokens = np.random.default_rng(33).integers(0, dims.vocab, seqs * rows)
+    out = {}
+    for paged in (False, True):
+        s = PrefillSession(device, kernels, dims, seqs, rows, layers=layers, paging=paging if paged else None)
+        try:
+            entries = {l.entry for l in s.lowered.launches}
+            assert ("fk_gemm_f16_qkv_rope_paged" in entries) == paged
+            for name in s.lowered.buffers:
+                if name.startswith("cache:"):
+                    s.engine.zero(name)
+            s.init_synthetic(seed=41)
+            s.set_tokens(tokens)
+            print(f"prefill {dims.d_model} x {seqs * rows} rows, paged {paged}", flush=True)
+            s.run()
+            device.sync()
+            pick = np.arange(0, seqs * rows, 37)
+            caches = {n: s.engine.read(n).copy() for n in s.lowered.buffers if n.startswith("cache:")}
+            out[paged] = (s.logits()[pick].copy(), s.tokens().copy(), caches,
+                          s.tables if paged else None)
+        finally:
+            s.close()
+    (la, ta, ca, _), (lb, tb, cb, tables) = out[False], out[True]
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)) and np.array_equal(ta, tb)
+    bs = paging[0]
+    for name, ring in ca.items():
+        ring = ring.reshape(dims.slots, dims.kv_heads, dims.context, dims.head_dim)[:seqs]
+        got = _pool_as_rings(cb[name], tables, dims.kv_heads, bs, dims.head_dim)
+        assert np.array_equal(got.view(np.uint16), ring.view(np.uint16)), name

@@ -243,3 +243,32 @@ def test_the_token_folds_into_the_heads_gemm_only_without_a_softcap():
     low = lower_prefill(capped, plan(PlanOptions(), capped), 512)
     assert [l.entry for l in low.launches][-3:] == ["fk_gemm_f16_store", "fk_prefill_softcap", "fk_prefill_argmax"]
     assert low.launches[-1].bind["x"] == low.launches[-2].bind["y"]
+
+
+def test_paged_pools_lower_to_the_paged_qkv_epilogue_and_attention():
+    """Caches as paged pools (Graph.hs:144-152): the QKV GEMM's epilogue
+    stores through each row's block table, the attention reads through it."""
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128, paging=(64, 8)))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
+    entries = [l.entry for l in low.launches]
+    assert entries.count("fk_gemm_f16_qkv_rope_paged") == entries.count("fk_prefill_attend_paged_g2") == 2
+    assert "fk_prefill_rope_store" not in entries and "fk_prefill_attend_g2" not in entries
+    qkv, att = low.launches[2], low.launches[3]
+    assert qkv.bind["table"] == att.bind["table"] == "ints:blocks"
+    assert low.buffers["ints:blocks"].count == 256 * 4
+    assert (qkv.bind["c1"], qkv.bind["c2"]) == (att.bind["kc"], att.bind["vc"])
+    assert low.buffers[att.bind["kc"]].count == 8 * 4 * 64 * 64
+    for L in (qkv, att):
+        assert (L.params["block_size"], L.params["table_len"], L.params["blocks"], L.params["length"]) == (64, 4, 8, 256)
+
+
+def test_paged_pools_are_refused_where_the_kernels_do_not_reach():
+    # RoPE on some pairs: the stores would fall to the RoPE kernel, which takes rings
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128, paging=(64, 8), rope_rotated=16))
+    with pytest.raises(LoweringError, match="paged pool"):
+        lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
+    # a pool has room for any step's rows (Plan.hs:276-281 stages only ring
+    # stores): positions up to the table's reach store in place
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", paging=(64, 8)))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
+    assert not any(l.entry == "fk_prefill_land" for l in low.launches)
