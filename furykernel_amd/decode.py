@@ -35,9 +35,10 @@ class DecodeSession:
     layers: Optional[int] = None
     fuse: bool = True
     tuned: bool = False  # shape the GEMV steps as the committed selections pick
+    paging: Optional[tuple] = None  # (block size, pool blocks): the caches as paged pools
 
     def __post_init__(self):
-        self.program = decoder_step(self.dims, embed=self.embed, layers=self.layers)
+        self.program = decoder_step(self.dims, embed=self.embed, layers=self.layers, paging=self.paging)
         self.checked = check_program(self.program)
         self.plan = plan(self.options, self.checked)
         choose = None
@@ -69,9 +70,18 @@ class DecodeSession:
                 self.engine.init_normal(f"value:{src.name}", cache_seed + 104729 * i, std)
         self.device.sync()
 
-    def set_position(self, position: int, slot: int = 0, token: Optional[int] = None) -> None:
+    def set_position(self, position: int, slot: int = 0, token: Optional[int] = None,
+                     table: Optional[np.ndarray] = None) -> None:
+        """The row's position and ring slot, or with paged pools its block
+        table (the context's positions in blocks)."""
         self.engine.set_ints("position", [position], self.dims.context)
-        self.engine.set_ints("slot", [slot], self.dims.slots)
+        if self.paging is None:
+            self.engine.set_ints("slot", [slot], self.dims.slots)
+        else:
+            block_size, pool_blocks = self.paging
+            if table is None or len(table) != self.dims.context // block_size:
+                raise ValueError(f"a block table of {self.dims.context // block_size} blocks")
+            self.engine.set_ints("blocks", table, pool_blocks)
         if self.embed and token is not None:
             self.engine.set_ints("tokens", [token], self.dims.vocab)
 

@@ -241,3 +241,44 @@ def test_tiny_decode_on_the_gpu_within_the_element_bounds(device, kernels):
         assert max(v for n, v in rel.items() if n != "token") < 1e-4
     finally:
         s.close()
+
+
+def test_paged_decode_step_is_the_ring_step_bit_for_bit(device, kernels):
+    """Two layers of the 1B-shape step at position 4095 with the caches as
+    paged pools (blocks of 64 positions in a pool of 80, a scrambled table):
+    the pools hold the ring's rows through the table, and the step's logits,
+    token and the row it stores are the ring step's bit for bit."""
+    import dataclasses
+
+    from furykernel_amd.program.decoder import ONE_B
+    dims = dataclasses.replace(ONE_B)
+    bs, pool = 64, 80
+    table = np.random.default_rng(4).permutation(pool)[:dims.context // bs].astype(np.uint32)
+    ring = DecodeSession(device, kernels, dims, PlanOptions(store_gelus=True), embed=True, layers=2)
+    paged = DecodeSession(device, kernels, dims, PlanOptions(store_gelus=True), embed=True, layers=2,
+                          paging=(bs, pool))
+    try:
+        assert any(l.entry == "fk_step_attend_paged" for l in paged.lowered.launches)
+        ring.init_synthetic()
+        paged.init_synthetic()
+        names = [n for n in ring.lowered.buffers if n.startswith("cache:")]
+        for n in names:   # the ring's rows scattered into the pool's blocks by the table
+            r = ring.engine.read(n).reshape(dims.kv_heads, dims.context // bs, bs, dims.head_dim)
+            p = np.zeros((pool, dims.kv_heads, bs, dims.head_dim), r.dtype)
+            p[table] = r.transpose(1, 0, 2, 3)
+            paged.engine.write(n, p.reshape(-1))
+        ring.set_position(4095, token=7)
+        paged.set_position(4095, token=7, table=table)
+        print("1B shapes, two layers: ring and paged decode steps at position 4095", flush=True)
+        ring.step()
+        paged.step()
+        device.sync()
+        assert np.array_equal(ring.logits().view(np.uint32), paged.logits().view(np.uint32))
+        assert ring.token() == paged.token()
+        for n in names:
+            r = ring.engine.read(n).reshape(dims.kv_heads, dims.context // bs, bs, dims.head_dim)
+            p = paged.engine.read(n).reshape(pool, dims.kv_heads, bs, dims.head_dim)
+            assert np.array_equal(p[table].transpose(1, 0, 2, 3).view(np.uint16), r.view(np.uint16)), n
+    finally:
+        ring.close()
+        paged.close()
