@@ -1,7 +1,7 @@
 """The host side of the C ABI in ``include/fkrocm.h``, through ctypes.
 
 This is the binding a ``FuryKernel.Rocm`` target makes with ``foreign import
-ccall`` (INTEGRATION.md has that stub), in the host language this repository
+ccall``, one declaration an entry point, in the host language this repository
 can run.  It loads ``libfkrocm.so`` from the package and nothing else: if the
 library is missing, or no GPU is present, every entry point raises.  There is
 no fallback of any kind.
