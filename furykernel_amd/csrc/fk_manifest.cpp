@@ -307,6 +307,18 @@ std::vector<Entry> build() {
         sizeof(S));
   }
   {
+    using S = fk_prefill_rope_paged_params;
+    add("fk_prefill_rope_store_paged", 0,
+        {buf("q", "read", "f32"), buf("k", "read", "f32"), buf("v", "read", "f32"), buf("position", "read", "u32"),
+         buf("table", "read", "u32"), buf("rope", "read", "f32"), buf("qr", "write", "f16"),
+         buf("kc", "read_write", "f16"), buf("vc", "read_write", "f16")},
+        {FK_P(S, r.rows, "u32"), FK_P(S, r.heads, "u32"), FK_P(S, r.kv_heads, "u32"), FK_P(S, r.head_dim, "u32"),
+         FK_P(S, r.rotated, "u32"), FK_P(S, r.rope_rows, "u32"), FK_P(S, r.length, "u32"), FK_P(S, r.slots, "u32"),
+         FK_P(S, r.cache_bf16, "u32"), FK_P(S, r.staged, "u32"), FK_P(S, g.block_size, "u32"),
+         FK_P(S, g.table_len, "u32"), FK_P(S, g.blocks, "u32")},
+        sizeof(S));
+  }
+  {
     using S = fk_prefill_land_params;
     add("fk_prefill_land", 256,
         {buf("ks", "read", "f16"), buf("vs", "read", "f16"), buf("position", "read", "u32"),
@@ -734,6 +746,20 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       return bad(err, cap, FK_ERR_ARG, "%s: %u rows of %u keys in %u x %u threads", entry, p.rows, p.parts, groups,
                  threads);
     need = {{"keys", (uint64_t)p.rows * p.parts * 8}, {"out", (uint64_t)p.rows * 4}};
+  } else if (std::strcmp(entry, "fk_prefill_rope_store_paged") == 0) {
+    fk_prefill_rope_paged_params pp;
+    std::memcpy(&pp, params, sizeof pp);
+    const fk_prefill_rope_params &p = pp.r;
+    if (p.rows == 0 || groups != p.rows || p.staged || p.head_dim == 0 || p.kv_heads == 0 ||
+        2 * p.rotated > p.head_dim || pp.g.block_size == 0 || pp.g.table_len == 0 || pp.g.blocks == 0)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows in %u threadgroups, blocks of %u, tables of %u, staged %u", entry,
+                 p.rows, groups, pp.g.block_size, pp.g.table_len, p.staged);
+    const uint64_t kw = (uint64_t)p.kv_heads * p.head_dim;
+    const uint64_t pool = (uint64_t)pp.g.blocks * p.kv_heads * pp.g.block_size * p.head_dim * 2;
+    need = {{"q", (uint64_t)p.rows * p.heads * p.head_dim * 4}, {"k", (uint64_t)p.rows * kw * 4},
+            {"v", (uint64_t)p.rows * kw * 4}, {"position", (uint64_t)p.rows * 4},
+            {"table", (uint64_t)p.rows * pp.g.table_len * 4}, {"rope", (uint64_t)p.rope_rows * p.rotated * 8},
+            {"qr", (uint64_t)p.rows * p.heads * p.head_dim * 2}, {"kc", pool}, {"vc", pool}};
   } else if (std::strncmp(entry, "fk_prefill_attend_paged_g", 25) == 0) {
     fk_prefill_attend_paged_params pp;
     std::memcpy(&pp, params, sizeof pp);

@@ -153,14 +153,23 @@ FK_NORM_PACK_HELD(4096, 8)
 // length).  One threadgroup a row.  The cache stores round as the decode
 // step's stores do (narrowF16 / narrowBF16).
 
-extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store(
-    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-    const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot, const float *__restrict__ rope,
-    uint16_t *__restrict__ qr, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, fk_prefill_rope_params p) {
+// PG: kc and vc are paged pools ([blocks][kv_heads][block_size][d]) and
+// `slot` the rows' block tables ([rows][table_len]).
+template <bool PG>
+__device__ __forceinline__ void prefill_rope_store(const float *__restrict__ q, const float *__restrict__ k,
+                                                   const float *__restrict__ v, const uint32_t *__restrict__ position,
+                                                   const uint32_t *__restrict__ slot, const float *__restrict__ rope,
+                                                   uint16_t *__restrict__ qr, uint16_t *__restrict__ kc,
+                                                   uint16_t *__restrict__ vc, const fk_prefill_rope_params &p,
+                                                   const fk_paging &pg = fk_paging{}) {
   const uint32_t row = blockIdx.x;
   const uint32_t d = p.head_dim;
   const uint32_t pos = position[row];
-  const uint32_t sl = min(slot[row], p.slots - 1);
+  // the row's ring slot, or its position's block through its table (both
+  // clamped into place)
+  const uint32_t sl = PG ? min(slot[(size_t)row * pg.table_len + min(pos / pg.block_size, pg.table_len - 1)],
+                               pg.blocks - 1)
+                         : min(slot[row], p.slots - 1);
   const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
   const uint32_t qw = p.heads * d, kw = p.kv_heads * d;
   const float *qx = q + (size_t)row * qw;
@@ -173,14 +182,31 @@ extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store(
     } else {
       const uint32_t f = e < qw + kw ? e - qw : e - qw - kw;
       const uint32_t h = f / d, i = f % d;
-      const size_t at = p.staged ? ((size_t)row * p.kv_heads + h) * d + i
-                                 : (((size_t)sl * p.kv_heads + h) * p.length + pos % p.length) * d + i;
+      const size_t at = PG        ? (((size_t)sl * p.kv_heads + h) * pg.block_size + pos % pg.block_size) * d + i
+                        : p.staged ? ((size_t)row * p.kv_heads + h) * d + i
+                                   : (((size_t)sl * p.kv_heads + h) * p.length + pos % p.length) * d + i;
       if (e < qw + kw)
         kc[at] = fk::narrow_cache(fk::rope_elem(kx + h * d, i, d, p.rotated, cs), bf16);
       else
         vc[at] = fk::narrow_cache(vx[f], bf16);
     }
   }
+}
+
+extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot, const float *__restrict__ rope,
+    uint16_t *__restrict__ qr, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, fk_prefill_rope_params p) {
+  prefill_rope_store<false>(q, k, v, position, slot, rope, qr, kc, vc, p);
+}
+
+// The same storing k and v into paged pools through the rows' block tables.
+extern "C" __global__ void __launch_bounds__(256) fk_prefill_rope_store_paged(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const uint32_t *__restrict__ position, const uint32_t *__restrict__ table, const float *__restrict__ rope,
+    uint16_t *__restrict__ qr, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    fk_prefill_rope_paged_params p) {
+  prefill_rope_store<true>(q, k, v, position, table, rope, qr, kc, vc, p.r, p.g);
 }
 
 // Staged rows landed (Plan.hs:41-50): row r's k and v heads, as the caches

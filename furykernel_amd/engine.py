@@ -49,6 +49,7 @@ _STRUCTS = {
     "fk_prefill_norm_pack": K.PrefillNormParams,
     **{f"fk_prefill_norm_pack_w{w}": K.PrefillNormParams for w in K.NORM_PACK_HELD},
     "fk_prefill_rope_store": K.PrefillRopeParams,
+    "fk_prefill_rope_store_paged": K.PrefillRopePagedParams,
     "fk_prefill_attend_g1": K.PrefillAttendParams,
     "fk_prefill_attend_g2": K.PrefillAttendParams,
     "fk_prefill_attend_g4": K.PrefillAttendParams,

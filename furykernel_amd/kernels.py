@@ -135,6 +135,12 @@ class GemmQkvPagedParams(ctypes.Structure):
                                          ("blocks", ctypes.c_uint32)]
 
 
+class PrefillRopePagedParams(ctypes.Structure):
+    """fk_prefill_rope_paged_params: the RoPE store's, then the pools' paging."""
+    _fields_ = PrefillRopeParams._fields_ + [("block_size", ctypes.c_uint32), ("table_len", ctypes.c_uint32),
+                                             ("blocks", ctypes.c_uint32)]
+
+
 class PrefillAttendPagedParams(ctypes.Structure):
     """fk_prefill_attend_paged_params: the attention's, then the pools' paging."""
     _fields_ = PrefillAttendParams._fields_ + [("block_size", ctypes.c_uint32), ("table_len", ctypes.c_uint32),
@@ -325,6 +331,9 @@ ABIS: dict[str, KernelAbi] = {
     "fk_prefill_norm_pack": KernelAbi("fk_prefill_norm_pack", ("x", "gamma", "y"), PrefillNormParams, 256),
     **{f"fk_prefill_norm_pack_w{w}": KernelAbi(f"fk_prefill_norm_pack_w{w}", ("x", "gamma", "y"), PrefillNormParams,
                                                256) for w in NORM_PACK_HELD},
+    "fk_prefill_rope_store_paged": KernelAbi("fk_prefill_rope_store_paged", ("q", "k", "v", "position", "table",
+                                                                             "rope", "qr", "kc", "vc"),
+                                             PrefillRopePagedParams),
     "fk_prefill_rope_store": KernelAbi("fk_prefill_rope_store", ("q", "k", "v", "position", "slot", "rope", "qr",
                                                                  "kc", "vc"), PrefillRopeParams),
     **{f"fk_prefill_attend_g{g}": KernelAbi(f"fk_prefill_attend_g{g}", ("qr", "kc", "vc", "position", "slot",

@@ -75,10 +75,6 @@ def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int, run_rows: Opti
     _Prefill(out, run_rows).run()
     _fuse_qkv_rope(out)
     _fuse_argmax(out)
-    for L in out.launches:
-        if L.entry == "fk_prefill_rope_store" and L.meta.get("paging"):
-            raise LoweringError(f"{L.step}: stores into a paged pool are made by the QKV GEMM's epilogue, which "
-                                f"needs q, k and v from one GEMM and RoPE on every pair of the heads of 64")
     return out
 
 
@@ -122,8 +118,8 @@ def _fuse_qkv_rope(out: Lowered) -> None:
     i = 0
     while i < len(launches):
         rs = launches[i]
-        if rs.entry != "fk_prefill_rope_store" or rs.params["rotated"] != HEAD_DIM // 2 or \
-                rs.params["head_dim"] != HEAD_DIM:
+        if rs.entry not in ("fk_prefill_rope_store", "fk_prefill_rope_store_paged") or \
+                rs.params["rotated"] != HEAD_DIM // 2 or rs.params["head_dim"] != HEAD_DIM:
             i += 1
             continue
         qkv = (rs.bind["q"], rs.bind["k"], rs.bind["v"])
@@ -141,9 +137,9 @@ def _fuse_qkv_rope(out: Lowered) -> None:
             i += 1
             continue
         p = rs.params
-        paging = rs.meta.get("paging")
+        paging = {f: p[f] for f in ("block_size", "table_len", "blocks")} if rs.entry.endswith("_paged") else None
         bind = dict(gm.bind, c0=rs.bind["qr"], c1=rs.bind["kc"], c2=rs.bind["vc"], position=rs.bind["position"],
-                    rope=rs.bind["rope"], **{"table" if paging else "slot": rs.bind["slot"]})
+                    rope=rs.bind["rope"], **({"table": rs.bind["table"]} if paging else {"slot": rs.bind["slot"]}))
         params = dict(gm.params, kv_heads=p["kv_heads"], rope_rows=p["rope_rows"], length=p["length"],
                       slots=p["slots"], cache_bf16=p["cache_bf16"], staged=p["staged"], **(paging or {}))
         launches[j] = Launch(gm.step, "fk_gemm_f16_qkv_rope_paged" if paging else "fk_gemm_f16_qkv_rope",
@@ -504,16 +500,14 @@ class _Prefill:
             vs = self.out.buffer(f"staged:{vname[len('cache:'):]}", elem, self.rows * kvh * HEAD_DIM)
             self.landing[stores[op.to.keys].id] = (ks, kname)
             self.landing[stores[op.to.values].id] = (vs, vname)
-        # (into a paged pool only through the QKV GEMM's epilogue: a RoPE
-        # launch left over after the fold is refused, with its paging in meta)
-        self.out.launches.append(Launch(
-            step.name, "fk_prefill_rope_store", self.rows, 256,
-            {"q": self.rows_value(step, q_raw), "k": self.rows_value(step, k_raw),
-             "v": self.rows_value(step, v_raw), "position": pos, "slot": seq,
-             "rope": self.rope(rs, HEAD_DIM, length), "qr": qr, "kc": ks or kname, "vc": vs or vname},
-            {"rows": self.rows, "heads": heads, "kv_heads": kvh, "head_dim": HEAD_DIM, "rotated": rs.rotated,
-             "rope_rows": length, "length": length, "slots": 0 if paged else klay.slots, "cache_bf16": int(kbf),
-             "staged": int(staged)}, {"paging": paging} if paged else {}, 0))
+        self.launch(step, "fk_prefill_rope_store_paged" if paged else "fk_prefill_rope_store", self.rows, 256,
+                    {"q": self.rows_value(step, q_raw), "k": self.rows_value(step, k_raw),
+                     "v": self.rows_value(step, v_raw), "position": pos, "table" if paged else "slot": seq,
+                     "rope": self.rope(rs, HEAD_DIM, length), "qr": qr, "kc": ks or kname, "vc": vs or vname},
+                    dict({"rows": self.rows, "heads": heads, "kv_heads": kvh, "head_dim": HEAD_DIM,
+                          "rotated": rs.rotated, "rope_rows": length, "length": length,
+                          "slots": 0 if paged else klay.slots, "cache_bf16": int(kbf), "staged": int(staged)},
+                         **(paging or {})))
         outv = anchor.outputs[0]
         obuf = self.value_tiled(outv)
         self.tiled_of[outv] = obuf

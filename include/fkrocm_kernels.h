@@ -333,6 +333,12 @@ typedef struct fk_prefill_rope_params {
   uint32_t staged;    /* kc and vc are staging rows [rows][kv_heads][head_dim], the row's own */
 } fk_prefill_rope_params;
 
+/* fk_prefill_rope_store_paged: `r.length`, `r.slots` and `r.staged` unused. */
+typedef struct fk_prefill_rope_paged_params {
+  fk_prefill_rope_params r;
+  fk_paging g;
+} fk_prefill_rope_paged_params;
+
 typedef struct fk_prefill_attend_params {
   uint32_t rows;     /* a multiple of 32 */
   uint32_t heads;

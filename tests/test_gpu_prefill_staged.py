@@ -148,22 +148,27 @@ def _pool_as_rings(pool, tables, kv_heads, block_size, d):
     return np.stack([np.concatenate([p[b] for b in t], axis=1) for t in tables])
 
 
-@pytest.mark.parametrize("dims,seqs,rows,layers,paging", [
-    (SMALL_PREFILL, SEQS, SEQ_ROWS, None, (64, 11)),
-    (ONE_B_PREFILL, 4, 2048, 2, (64, 300)),
-], ids=["small", "1b-two-layers"])
-def test_paged_prefill_is_the_ring_prefill_bit_for_bit(device, kernels, dims, seqs, rows, layers, paging):
+@pytest.mark.parametrize("dims,seqs,rows,layers,paging,rotated", [
+    (SMALL_PREFILL, SEQS, SEQ_ROWS, None, (64, 11), None),
+    (SMALL_PREFILL, SEQS, SEQ_ROWS, None, (32, 20), 16),
+    (ONE_B_PREFILL, 4, 2048, 2, (64, 300), None),
+], ids=["small", "small-rope-kernel", "1b-two-layers"])
+def test_paged_prefill_is_the_ring_prefill_bit_for_bit(device, kernels, dims, seqs, rows, layers, paging, rotated):
     """The caches as paged pools, each sequence's rows through a scrambled
     block table: logits and tokens are the ring prefill's bit for bit, and
-    the pool read through the tables holds the ring's rows."""
+    the pool read through the tables holds the ring's rows.  With every pair
+    turned the QKV GEMM's epilogue stores into the pools; with 16 of 32 the
+    RoPE kernel does."""
     from furykernel_amd.prefill import PrefillSession
     tokens = np.random.default_rng(33).integers(0, dims.vocab, seqs * rows)
     out = {}
     for paged in (False, True):
-        s = PrefillSession(device, kernels, dims, seqs, rows, layers=layers, paging=paging if paged else None)
+        s = PrefillSession(device, kernels, dims, seqs, rows, layers=layers, paging=paging if paged else None,
+                           rope_rotated=rotated)
         try:
             entries = {l.entry for l in s.lowered.launches}
-            assert ("fk_gemm_f16_qkv_rope_paged" in entries) == paged
+            store = "fk_prefill_rope_store_paged" if rotated else "fk_gemm_f16_qkv_rope_paged"
+            assert (store in entries) == paged
             for name in s.lowered.buffers:
                 if name.startswith("cache:"):
                     s.engine.zero(name)

@@ -262,13 +262,19 @@ def test_paged_pools_lower_to_the_paged_qkv_epilogue_and_attention():
         assert (L.params["block_size"], L.params["table_len"], L.params["blocks"], L.params["length"]) == (64, 4, 8, 256)
 
 
-def test_paged_pools_are_refused_where_the_kernels_do_not_reach():
-    # RoPE on some pairs: the stores would fall to the RoPE kernel, which takes rings
+def test_paged_pools_with_rope_on_some_pairs_store_through_the_rope_kernel():
     c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128, paging=(64, 8), rope_rotated=16))
-    with pytest.raises(LoweringError, match="paged pool"):
-        lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
-    # a pool has room for any step's rows (Plan.hs:276-281 stages only ring
-    # stores): positions up to the table's reach store in place
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
+    entries = [l.entry for l in low.launches]
+    assert entries.count("fk_prefill_rope_store_paged") == 2 and "fk_gemm_f16_qkv_rope_paged" not in entries
+    rs = low.launches[entries.index("fk_prefill_rope_store_paged")]
+    assert rs.bind["table"] == "ints:blocks" and rs.params["rotated"] == 16
+    assert (rs.params["block_size"], rs.params["table_len"], rs.params["blocks"]) == (64, 4, 8)
+
+
+def test_a_pool_has_room_for_any_steps_rows():
+    # Plan.hs:276-281 stages only ring stores: positions up to the table's
+    # reach store in place
     c = check_program(decoder_step(SMALL_PREFILL, name="prefill", paging=(64, 8)))
     low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
     assert not any(l.entry == "fk_prefill_land" for l in low.launches)
