@@ -61,6 +61,9 @@ def parse():
                     help="queue each step's launches on the stream instead of replaying a HIP graph")
     ap.add_argument("--workload", choices=("decode", "prefill", "kernels"), default="decode",
                     help="decode (the headline metric) or the 1B prefill of 4 x 2048 rows")
+    ap.add_argument("--paged", action="store_true",
+                    help="prefill workload: the KV caches as paged pools (blocks of 64 positions, each sequence's "
+                         "rows through a scrambled block table) instead of rings")
     ap.add_argument("--calibrate", action="store_true",
                     help="only read and write 1 GiB with the streaming kernels (the known sizes that scale the "
                          "HBM counters FETCH_SIZE and WRITE_SIZE)")
@@ -297,7 +300,8 @@ def main_prefill(args) -> int:
 
     dev = runtime.Device(0)
     ks = kernels.Kernels(dev)
-    s = PrefillSession(dev, ks, D, PREFILL_SEQS, PREFILL_ROWS)
+    paging = (64, PREFILL_SEQS * D.context // 64) if args.paged else None
+    s = PrefillSession(dev, ks, D, PREFILL_SEQS, PREFILL_ROWS, paging=paging)
     rows = s.rows
     s.init_synthetic()
     s.set_tokens(np.random.default_rng(3).integers(0, D.vocab, rows))
@@ -360,7 +364,9 @@ def main_prefill(args) -> int:
         "dtype": "f16",
         "data": "synthetic: weights N(0, 0.02) (norm gains 1) generated on the device, random tokens",
         "config": {"workload": "1B-class f16 prefill via the planner: 4 sequences x 2048 rows (positions 0..2047) "
-                               "into 4 ring slots of 4096, logits and greedy token for every row",
+                               + ("into a paged pool of 256 blocks of 64 positions through scrambled block tables"
+                                  if args.paged else "into 4 ring slots of 4096")
+                               + ", logits and greedy token for every row",
                    "d_model": D.d_model, "layers": D.layers, "heads": D.heads, "kv_heads": D.kv_heads,
                    "head_dim": D.head_dim, "ffn": D.ffn, "vocab": D.vocab, "kv_length": D.context,
                    "rows": rows, "launches": len(low.launches), "launch": "one HIP graph per prefill"},
