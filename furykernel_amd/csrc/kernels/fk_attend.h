@@ -139,6 +139,19 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // buffer, bf16 caches converted on the way (a uniform branch, so that f16
   // caches pay nothing for it).
   uint4 kreg[per], vreg[per];
+  // PG: where each of the thread's units of block kb lies in a pool (the
+  // keys' and the values' pools alike), looked up once for both.
+  size_t poff[per];
+  auto locate = [&](uint32_t kb) {
+#pragma unroll
+    for (uint32_t e = 0; e < per; e++) {
+      const uint32_t u = tid + e * nthreads;
+      const uint32_t t = kb * FK_ATT_KB + u / 8;
+      // position t's block through the table, both clamped into place
+      const uint32_t blk = min(tab[min(t / pg.block_size, pg.table_len - 1)], pg.blocks - 1);
+      poff[e] = (((size_t)blk * p.kv_heads + g) * pg.block_size + t % pg.block_size) * 64 + (u % 8) * 8;
+    }
+  };
   auto fetch = [&](uint4 (&reg)[per], const uint16_t *__restrict__ cache, const uint16_t *__restrict__ stage,
                    uint32_t kb) {
     const uint32_t ring0 = (kb * FK_ATT_KB) % p.length;
@@ -152,9 +165,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
       const uint32_t srow = min(rf + (t - min(t, start)), p.rows - 1);
       const uint16_t *src;
       if constexpr (PG) {
-        // position t's block through the table, both clamped into place
-        const uint32_t blk = min(tab[min(t / pg.block_size, pg.table_len - 1)], pg.blocks - 1);
-        src = cache + (((size_t)blk * p.kv_heads + g) * pg.block_size + t % pg.block_size) * 64 + c8;
+        src = cache + poff[e];
       } else {
         src = staged && t >= start ? stage + ((size_t)srow * p.kv_heads + g) * 64 + c8
                                    : cache + cache_base + (size_t)(ring0 + key) * 64 + c8;
@@ -283,6 +294,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // registers, and go into the other pair after (every wavefront left it at
   // the last barrier); one barrier a block.
   const uint32_t kb0 = first_pos / FK_ATT_KB, kb_last = last_pos / FK_ATT_KB;
+  if constexpr (PG) locate(kb0);
   fetch(kreg, kc, kst, kb0);
   fetch(vreg, vc, vst, kb0);
   stash_k(0);
@@ -291,6 +303,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   for (uint32_t kb = kb0; kb <= kb_last; kb++) {
     const uint32_t buf = (kb - kb0) & 1;
     if (kb < kb_last) {
+      if constexpr (PG) locate(kb + 1);
       fetch(kreg, kc, kst, kb + 1);
       fetch(vreg, vc, vst, kb + 1);
     }
