@@ -775,6 +775,16 @@ def main() -> int:
     session = DecodeSession(dev, ks, ONE_B, PLAN, embed=True, tuned=not args.untuned)
     from furykernel_amd import tuning
     tuned = {f: p for f, p in tuning.validated(dev.info.compute_units).items() if f.startswith("step_gemv")}
+
+    def selection_label(used: dict):
+        """The step GEMV picks the lowering used, each family's as class ->
+        point, and the committed families it refused (stale or invalid)."""
+        out: dict = {f: {c: "_".join(f"{a}{v}" for a, v in pt) for c, pt in p.items()} for f, p in used.items()}
+        for f, problems in tuning.chooser_problems.items():
+            if f.startswith("step_gemv"):
+                out[f] = f"refused: {problems[0]}" + (f" (+{len(problems) - 1} more)" if len(problems) > 1 else "")
+        return out or "none committed"
+
     log(f"GEMV step selections used: {sorted(tuned) or 'none'}"
         + (f"; refused: {tuning.chooser_problems}" if tuning.chooser_problems else ""))
     session.init_synthetic()
@@ -835,9 +845,7 @@ def main() -> int:
                    "kv_heads": ONE_B.kv_heads, "head_dim": ONE_B.head_dim, "ffn": ONE_B.ffn, "vocab": ONE_B.vocab,
                    "kv_length": ONE_B.context, "position": POSITION, "launches": len(session.lowered.launches),
                    "launch": "eager launches per token" if args.eager else "one HIP graph per token",
-                   "gemv_selection": "untuned" if args.untuned else
-                   ({f: {c: "_".join(f"{a}{v}" for a, v in pt) for c, pt in p.items()} for f, p in tuned.items()}
-                    or "none committed")},
+                   "gemv_selection": "untuned" if args.untuned else selection_label(tuned)},
         "hbm": {"step_bytes": nbytes, "achieved_gbps": round(nbytes * tok_s / 1e9, 1),
                 "frac_of_peak": round(nbytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4), "peak_gbps": HBM_PEAK_GBPS,
                 "ms_per_step_events": round(event_ms / args.steps, 4)},

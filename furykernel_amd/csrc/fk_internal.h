@@ -28,6 +28,7 @@ struct fk_ctx {
   // no-alloc entry's static scratch on this context's device.
   void *workspace = nullptr;
   size_t workspace_bytes = 0;
+  std::mutex workspace_mu;  // held across a call's grow and launch, so no thread frees it under another's launch
   void *scratch = nullptr;
 };
 

@@ -731,10 +731,18 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
             {"position", (uint64_t)p.rows * 4},
             {"slot", (uint64_t)p.rows * 4},
             {"out", (uint64_t)p.rows * p.heads * 64 * 2}};
+    const uint32_t g = (uint32_t)(entry[std::strlen(entry) - 1] - '0');
     if ((p.staged && p.run_rows == 0) || (p.run_rows && (p.run_rows % 32 || p.rows % p.run_rows)) || p.rows % 32 ||
-        p.kv_heads == 0)
+        p.rows == 0 || p.kv_heads == 0)
       return bad(err, cap, FK_ERR_ARG, "%s: runs of %u rows in a step of %u (multiples of 32 that divide it)", entry,
                  p.run_rows, p.rows);
+    // The grid is every (query block, kv head), heaviest first: a larger
+    // grid would index blocks past their run; the heads are the group's
+    // wavefronts; keys go by blocks of 64 positions.
+    if (p.heads != g * p.kv_heads || p.length == 0 || p.length % 64 || p.slots == 0 ||
+        (uint64_t)groups != (uint64_t)(p.rows / 32) * p.kv_heads || threads != g * 64)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u heads over %u, a ring of %u, %u threadgroups of %u threads", entry,
+                 p.heads, p.kv_heads, p.length, groups, threads);
     if (p.staged) {
       need.push_back({"ks", (uint64_t)p.rows * kw});
       need.push_back({"vs", (uint64_t)p.rows * kw});
@@ -777,9 +785,27 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
             {"position", (uint64_t)p.rows * 4},
             {"table", (uint64_t)p.rows * pp.g.table_len * 4},
             {"out", (uint64_t)p.rows * p.heads * 64 * 2}};
+  } else if (std::strcmp(entry, "fk_prefill_rope_store") == 0) {
+    fk_prefill_rope_params p;
+    std::memcpy(&p, params, sizeof p);
+    // One threadgroup a row.
+    if (p.rows == 0 || groups != p.rows || p.head_dim == 0 || p.kv_heads == 0 || 2 * p.rotated > p.head_dim ||
+        p.rope_rows == 0 || (!p.staged && (p.length == 0 || p.slots == 0)))
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows in %u threadgroups, heads of %u turning %u pairs, a ring of %u",
+                 entry, p.rows, groups, p.head_dim, p.rotated, p.length);
+    const uint64_t kw = (uint64_t)p.kv_heads * p.head_dim;
+    const uint64_t cache = p.staged ? (uint64_t)p.rows * kw * 2 : (uint64_t)p.slots * p.length * kw * 2;
+    need = {{"q", (uint64_t)p.rows * p.heads * p.head_dim * 4}, {"k", (uint64_t)p.rows * kw * 4},
+            {"v", (uint64_t)p.rows * kw * 4}, {"position", (uint64_t)p.rows * 4},
+            {"slot", (uint64_t)p.rows * 4}, {"rope", (uint64_t)p.rope_rows * p.rotated * 8},
+            {"qr", (uint64_t)p.rows * p.heads * p.head_dim * 2}, {"kc", cache}, {"vc", cache}};
   } else if (std::strcmp(entry, "fk_prefill_land") == 0) {
     fk_prefill_land_params p;
     std::memcpy(&p, params, sizeof p);
+    // One threadgroup a row.
+    if (p.rows == 0 || groups != p.rows || p.kv_heads == 0 || p.head_dim == 0 || p.length == 0 || p.slots == 0)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows in %u threadgroups, %u heads of %u, a ring of %u in %u slots",
+                 entry, p.rows, groups, p.kv_heads, p.head_dim, p.length, p.slots);
     const uint64_t kw = (uint64_t)p.kv_heads * p.head_dim * 2;
     need = {{"ks", (uint64_t)p.rows * kw}, {"vs", (uint64_t)p.rows * kw}, {"position", (uint64_t)p.rows * 4},
             {"slot", (uint64_t)p.rows * 4}, {"kc", (uint64_t)p.slots * p.length * kw},

@@ -121,6 +121,7 @@ extern "C" int fk_attend_decode(fk_ctx *ctx, const fk_attend_args *a, fk_stream 
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return fk_fail(ctx, FK_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
   hipStream_t s = stream ? stream->stream : ctx->stream;
+  std::lock_guard<std::mutex> lock(ctx->workspace_mu);
   if (bytes > ctx->workspace_bytes) {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     e = hipStreamIsCapturing(s, &cap);

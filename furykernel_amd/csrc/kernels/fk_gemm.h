@@ -331,10 +331,13 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
       const uint32_t row = m + 16 * i;
       const uint32_t pos = position[row];
       // PAGED: `slot` holds the rows' block tables; position pos's block,
-      // the table index and the block clamped into place
+      // the table index and the block clamped into place.  A position past
+      // its table stores no k or v (as the decode step's paged store skips
+      // it); its q row is still written.
       const uint32_t sl = PAGED ? min(slot[(size_t)row * pg.table_len + min(pos / pg.block_size, pg.table_len - 1)],
                                       pg.blocks - 1)
                                 : min(slot[row], rp.slots - 1);
+      const bool keep = !PAGED || anchor == 0 || pos / pg.block_size < pg.table_len;
       const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
       uint16_t *const base =
           anchor == 0 ? dst + (size_t)row * p.ldc[0] + head0 * 64
@@ -360,9 +363,12 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
             hi[r] = bf16 && anchor != 0 ? fk::narrow_bf16(yr) : fk::to_f16(yr);
           }
           uint16_t *const at = base + jp * hstride + d;
-          *reinterpret_cast<uint2 *>(at) = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
-          *reinterpret_cast<uint2 *>(at + 32) =
-              make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+          if (keep) {
+            *reinterpret_cast<uint2 *>(at) =
+                make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+            *reinterpret_cast<uint2 *>(at + 32) =
+                make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+          }
         }
       asm volatile("" ::: "memory");  // one row block at a time
     }

@@ -166,17 +166,19 @@ __device__ __forceinline__ void prefill_rope_store(const float *__restrict__ q, 
   const uint32_t d = p.head_dim;
   const uint32_t pos = position[row];
   // the row's ring slot, or its position's block through its table (both
-  // clamped into place)
+  // clamped into place); a position past its table stores no k or v, as
+  // the decode step's paged store skips it
   const uint32_t sl = PG ? min(slot[(size_t)row * pg.table_len + min(pos / pg.block_size, pg.table_len - 1)],
                                pg.blocks - 1)
                          : min(slot[row], p.slots - 1);
   const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
   const uint32_t qw = p.heads * d, kw = p.kv_heads * d;
+  const uint32_t stored = !PG || pos / pg.block_size < pg.table_len ? qw + 2 * kw : qw;
   const float *qx = q + (size_t)row * qw;
   const float *kx = k + (size_t)row * kw;
   const float *vx = v + (size_t)row * kw;
   const bool bf16 = p.cache_bf16 != 0;
-  for (uint32_t e = threadIdx.x; e < qw + 2 * kw; e += blockDim.x) {
+  for (uint32_t e = threadIdx.x; e < stored; e += blockDim.x) {
     if (e < qw) {
       qr[(size_t)row * qw + e] = fk::to_f16(fk::rope_elem(qx + (e / d) * d, e % d, d, p.rotated, cs));
     } else {

@@ -136,6 +136,42 @@ def source_hash(unit: str) -> int:
     return lib.fk_fnv1a64(text, len(text))
 
 
+# The header that defines each tuned family's entries.
+_DEFINED_IN = (("fk_step_gemv_", "fk_step_gemv.h"), ("fk_gemv_", "fk_gemv.h"))
+
+
+def _include_closure(header: str) -> list:
+    """The header and the kernels-directory headers it includes, transitively,
+    in name order (the parameter structs' header excepted: an entry's
+    parameter layout is its ABI hash)."""
+    seen, todo = set(), [header]
+    while todo:
+        h = todo.pop()
+        if h in seen:
+            continue
+        seen.add(h)
+        for line in (KERNELS_DIR / h).read_text().splitlines():
+            t = line.strip()
+            if t.startswith('#include "') and "/" not in t:
+                todo.append(t.split('"')[1])
+    return sorted(seen)
+
+
+def entry_source_hash(entry: str) -> int:
+    """FNV-1a 64 over what an entry's code is made of: the text of the header
+    that defines it and of the kernels headers that header includes, then the
+    entry's ABI hash (its bindings and parameter layout).  A change to another
+    kernel's header leaves it as it is.  Entries of no tuned family take their
+    whole translation unit's source hash."""
+    lib = runtime.library()
+    for prefix, header in _DEFINED_IN:
+        if entry.startswith(prefix):
+            text = b"".join((KERNELS_DIR / h).read_bytes() for h in _include_closure(header))
+            text += f" {runtime.abi_of(entry).abi_hash:016x}".encode()
+            return lib.fk_fnv1a64(text, len(text))
+    return source_hash("fk_attend.hip" if entry.startswith("fk_prefill_attend") else "fk_kernels.hip")
+
+
 def manifest_of(entry: str, tg_memory: int = 0) -> JObject:
     """The manifest of one kernel of the code objects."""
     abi = runtime.abi_of(entry)

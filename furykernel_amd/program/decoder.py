@@ -34,6 +34,7 @@ class DecoderDims:
     cache_elem: str = CACHE_F16
     slots: int = 1        # sequences the caches hold
     act: str = SILU       # the gated MLP's activation: SILU or GELU_TANH
+    embed_factor: float = 1.0  # the gathered embedding row's scale (Gather's factor, Eval.hs:528-535)
 
     @property
     def q_width(self) -> int:
@@ -66,6 +67,10 @@ ONE_B = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, 
 # The 1B prefill: four sequences of 2048 rows into a ring of 4096 positions.
 ONE_B_PREFILL = DecoderDims(d_model=2048, layers=16, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000,
                             context=4096, slots=4)
+# The tiny decode with its embedding row scaled as the reference's embedding
+# program scales it (ProgramTest.hs:785-789: factor 5.65625), the ring of 32.
+TINY_EMBED = DecoderDims(d_model=64, layers=2, heads=4, kv_heads=4, head_dim=16, ffn=256, vocab=256, context=32,
+                         weight_type=F32, embed_factor=5.65625)
 # A small f16 decoder the prefill kernels take whole (anchors of 256 rows,
 # heads of 64, two kv heads to a group), for checking prefill against the
 # f64 evaluator.
@@ -101,7 +106,7 @@ def decoder_step(dims: DecoderDims, name: str = "decode", embed: bool = True,
         if embed:
             tokens = b.row_ints("tokens", 1, dims.vocab)
             table = b.weight("embed", [dims.vocab, dims.d_model], wt)
-            x = b.gather("x0", table, tokens, 1.0)
+            x = b.gather("x0", table, tokens, dims.embed_factor)
         else:
             x = b.input("x", whole_row(dims.d_model), F32)
         rope = RopeSpec(dims.rope_theta, dims.head_dim // 2 if rope_rotated is None else rope_rotated)

@@ -311,11 +311,11 @@ def variants(profile: Profile, space: Space, shape: Shape) -> list:
 
 def launch_hash(launch: Launch) -> int:
     """What stands for the reference's IR hash of a variant's kernel: 64-bit
-    FNV-1a over the source hash of the entry's code object and the launch
-    (entry, threadgroups, threads, LDS, parameter bytes), so that a pick is
-    stale when the kernel's source or its launch changes."""
-    from .manifest import source_hash
-    unit = "fk_attend.hip" if launch.entry.startswith("fk_prefill_attend") else "fk_kernels.hip"
-    text = (f"{source_hash(unit):016x} {launch.entry} {launch.groups} {launch.threads} {launch.lds_bytes} "
-            f"{launch.params.hex()}").encode()
+    FNV-1a over the source hash of the entry's own code (its defining header
+    and what that includes, and its ABI hash) and the launch (entry,
+    threadgroups, threads, LDS, parameter bytes), so that a pick is stale when
+    its kernel's source or its launch changes, and only then."""
+    from .manifest import entry_source_hash
+    text = (f"{entry_source_hash(launch.entry):016x} {launch.entry} {launch.groups} {launch.threads} "
+            f"{launch.lds_bytes} {launch.params.hex()}").encode()
     return runtime.library().fk_fnv1a64(text, len(text))

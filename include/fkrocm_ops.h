@@ -36,7 +36,12 @@ typedef struct fk_attend_args {
 
 /* The attention step; its splits' partial results go to a workspace the
  * context allocates (hipMalloc) on first use and grows when a call needs
- * more, which it refuses (FK_ERR_STATE) on a stream being captured.
+ * more, which it refuses (FK_ERR_STATE) on a stream being captured.  The
+ * context has one workspace: calls from several threads are serialized
+ * while they grow it and queue their launches, but calls on one context
+ * whose work overlaps on the GPU (two fk_streams, or a stream's work still
+ * running when another's is queued) race on the same partials; such callers
+ * order their streams, or take one context each.
  * Source: src/FuryKernel/Program/Eval.hs:474-527 (Attend), Plan.hs:174-181
  * (Partials + Combine). */
 int fk_attend_decode(fk_ctx *ctx, const fk_attend_args *args, fk_stream *stream);

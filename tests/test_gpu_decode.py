@@ -282,3 +282,35 @@ def test_paged_decode_step_is_the_ring_step_bit_for_bit(device, kernels):
     finally:
         ring.close()
         paged.close()
+
+
+def test_tiny_embed_decode_on_the_gpu_within_1e4_of_the_f64_evaluator(device, kernels):
+    """The tiny decode with the token's embedding row gathered and scaled by
+    5.65625 (the reference's embedding program, ProgramTest.hs:785-789) on
+    the GPU: every buffer the step stores (the layer-0 QKV step's gathered
+    prologue, the gathered residual, caches, logits, token) bit for bit the
+    CPU target's, and the logits within 1e-4 of the f64 evaluator."""
+    from furykernel_amd.program.decoder import TINY_EMBED
+    from test_embed_decode import POSITION, TOKEN, embed_state, rel, run_cpu, run_eval
+
+    checked, w, c = embed_state()
+    s = DecodeSession(device, kernels, TINY_EMBED, PlanOptions(), embed=True)
+    try:
+        for name, v in w.items():
+            if f"weight:{name}" in s.lowered.buffers:
+                s.engine.write(f"weight:{name}", v)
+        for name, v in c.items():
+            s.engine.write(f"cache:{name}", v)
+        s.set_position(POSITION, token=TOKEN)
+        cpu = mirror(s)
+        print(f"tiny decode, embedding row scaled by 5.65625, token {TOKEN} at position {POSITION}", flush=True)
+        s.step()
+        device.sync()
+        cpu.run()
+        assert compare_all(s, cpu, [n for n in s.lowered.buffers if not n.startswith("weight:")]) == []
+        # the mirrored state is the CPU tests' state
+        assert np.array_equal(bits(s.logits()), bits(run_cpu(checked, w, c).read("value:logits")))
+        ev = run_eval(checked, w, c)
+        assert rel(s.logits(), ev.outputs["logits"][0]) <= 1e-4
+    finally:
+        s.close()

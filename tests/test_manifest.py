@@ -267,3 +267,52 @@ def test_the_launch_check_takes_the_prefill_heads_keys_and_refuses_them_out_of_s
     p.rows = 4 * token.groups + 1  # more rows than its waves
     with pytest.raises(runtime.FkError, match="rows"):
         _check(token, low.buffers, params=p)
+
+
+def test_the_launch_check_refuses_prefill_attention_stores_and_lands_out_of_shape():
+    """The ring prefill attention's grid is every (query block, kv head),
+    its heads G to a kv head, its ring in blocks of 64 positions; the RoPE
+    store and the landing of staged rows are one threadgroup a row.  Each
+    is taken as lowered and refused with a grid, a group or a ring that
+    would index past its buffers."""
+    from furykernel_amd.engine import params_struct
+    from furykernel_amd.prefill import lower_prefill
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.decoder import SMALL_PREFILL, decoder_step
+    from furykernel_amd.program.plan import PlanOptions, plan
+    # RoPE on some pairs (the separate store), positions up to the whole
+    # ring (staged stores, landed after the attention)
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", rope_rotated=16))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256)
+    by = {}
+    for L in low.launches:
+        _check(L, low.buffers)
+        by.setdefault(L.entry, L)
+    att, rope, land = by["fk_prefill_attend_g2"], by["fk_prefill_rope_store"], by["fk_prefill_land"]
+    for L in (att, rope, land):
+        for g in (L.groups + 1, L.groups - 1):
+            with pytest.raises(runtime.FkError, match="threadgroups"):
+                _check(dataclasses.replace(L, groups=g), low.buffers)
+    p = params_struct(att)
+    p.heads = p.heads + p.kv_heads   # a group of 3 launched as 2
+    with pytest.raises(runtime.FkError, match="heads"):
+        _check(att, low.buffers, params=p)
+    p = params_struct(att)
+    p.length = p.length - 32
+    with pytest.raises(runtime.FkError, match="ring"):
+        _check(att, low.buffers, params=p)
+    with pytest.raises(runtime.FkError, match="threads"):
+        _check(dataclasses.replace(att, threads=att.threads * 2), low.buffers)
+    p = params_struct(rope)
+    p.rotated = p.head_dim // 2 + 1
+    with pytest.raises(runtime.FkError, match="pairs"):
+        _check(rope, low.buffers, params=p)
+    spans = _spans(rope, low.buffers)
+    i = list(K.ABIS[rope.entry].buffers).index("qr")
+    spans[i] = (spans[i][0], spans[i][1] - 2)
+    with pytest.raises(runtime.FkError, match="qr holds"):
+        _check(rope, low.buffers, spans=spans)
+    p = params_struct(land)
+    p.slots = 0
+    with pytest.raises(runtime.FkError, match="slots"):
+        _check(land, low.buffers, params=p)
