@@ -240,11 +240,38 @@ def test_the_step_family_keeps_the_classes_that_fill_the_gpu():
 
 def test_committed_selections_validate():
     """Every selection committed under furykernel_amd/selections/ parses and
-    validates against its family's space on this target's 256 CUs (a stale
-    one, whose kernels changed after tuning, is refused and not used)."""
-    T.validated(256)
-    for family, problems in T.chooser_problems.items():
-        assert all("was picked as the kernel of IR hash" in p for p in problems), (family, problems)
+    validates against its family's space on this target's 256 CUs, every
+    pick still the launch it was timed as: a stale pick (its kernel's code
+    or its launch changed after tuning) fails here, so the committed picks
+    are the ones the lowering and the bench use."""
+    picks = T.validated(256)
+    assert T.chooser_problems == {}
+    assert sorted(picks) == sorted(s.family for s in T.spaces(256))
+
+
+def test_a_pick_goes_stale_only_with_its_own_kernel(tmp_path):
+    """A pick's hash covers its entry's defining header and what that
+    includes: another kernel's header (the prefill's) leaves the step GEMV's
+    hash as it is; its own header changes it."""
+    from furykernel_amd import manifest as M
+    entry = "fk_step_gemv_f16_k2048_r1_p0_e0"
+    before = M.entry_source_hash(entry)
+    assert "fk_prefill.h" not in M._include_closure("fk_step_gemv.h")
+    assert "fk_step_gemv.h" in M._include_closure("fk_step_gemv.h")
+    saved = M.KERNELS_DIR
+    fake = tmp_path / "kernels"
+    fake.mkdir()
+    for f in saved.iterdir():
+        if f.is_file():
+            (fake / f.name).write_bytes(f.read_bytes())
+    try:
+        M.KERNELS_DIR = fake
+        (fake / "fk_prefill.h").write_text((fake / "fk_prefill.h").read_text() + "\n// another kernel's change\n")
+        assert M.entry_source_hash(entry) == before
+        (fake / "fk_step_gemv.h").write_text((fake / "fk_step_gemv.h").read_text() + "\n// its own change\n")
+        assert M.entry_source_hash(entry) != before
+    finally:
+        M.KERNELS_DIR = saved
 
 
 # The lowering's use of a pick -------------------------------------------------
