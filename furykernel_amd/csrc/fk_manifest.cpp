@@ -143,11 +143,11 @@ std::vector<Entry> build() {
     const char *name, *wt;
     bool pairs;
   };
-  const Shape shapes[] = {{"fk_step_gemv_f16_k2048_r1", "f16", false}, {"fk_step_gemv_f16_k2048_r2", "f16", true},
-                          {"fk_step_gemv_f16_k8192_r1", "f16", false}, {"fk_step_gemv_bf16_k2048_r1", "bf16", false},
+  const Shape shapes[] = {{"fk_step_gemv_f16_k2048_r1", "f16", true}, {"fk_step_gemv_f16_k2048_r2", "f16", true},
+                          {"fk_step_gemv_f16_k8192_r1", "f16", false}, {"fk_step_gemv_bf16_k2048_r1", "bf16", true},
                           {"fk_step_gemv_bf16_k2048_r2", "bf16", true}, {"fk_step_gemv_bf16_k8192_r1", "bf16", false},
-                          {"fk_step_gemv_f32_k256_r1", "f32", false},
-                          {"fk_step_gemv_f32_k256_r2", "f32", true},   {"fk_step_gemv_f32_k1024_r1", "f32", false},
+                          {"fk_step_gemv_f32_k256_r1", "f32", true},
+                          {"fk_step_gemv_f32_k256_r2", "f32", true},   {"fk_step_gemv_f32_k1024_r1", "f32", true},
                           {"fk_step_gemv_f32_k1024_r2", "f32", true}};
   for (const Shape &s : shapes) {
     const char *wt = keep(s.wt);
@@ -506,8 +506,13 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       return bad(err, cap, FK_ERR_RANGE, "%s: %u anchors, k = %u (at most %d)", entry, p.n_anchors, p.k, kmax);
     uint64_t widest = 0;
     for (uint32_t j = 0; j < p.n_anchors; j++) widest = p.rows[j] > widest ? p.rows[j] : widest;
-    if (epi == FK_EPI_SILU_MUL && (p.n_anchors != 2 || p.rows[0] != p.rows[1] || r < 2))
-      return bad(err, cap, FK_ERR_ARG, "%s: the SiLU·mul epilogue on %u anchors, blocks of %d", entry, p.n_anchors, r);
+    // The SiLU·mul epilogue: two anchors of as many rows, in blocks of row
+    // pairs (r 2) or of one row of each anchor in turn (r 1: blocks twice
+    // the rows, so that a wavefront's partner is the next).
+    if (epi == FK_EPI_SILU_MUL &&
+        (p.n_anchors != 2 || p.rows[0] != p.rows[1] || (r == 1 && (uint64_t)p.blocks != 2ull * p.rows[0])))
+      return bad(err, cap, FK_ERR_ARG, "%s: the SiLU·mul epilogue on %u anchors, %u blocks of %d", entry, p.n_anchors,
+                 p.blocks, r);
     if (epi == FK_EPI_SOFTCAP && (p.n_anchors != 1 || !(p.cap > 0.0f && p.cap < __builtin_inff())))
       return bad(err, cap, FK_ERR_ARG, "%s: a softcap of %g on %u anchors", entry, (double)p.cap, p.n_anchors);
     if ((p.act != FK_ACT_SILU && p.act != FK_ACT_GELU_TANH) || p.src2_off % 4)

@@ -69,7 +69,13 @@ struct Block {
     const uint32_t total = p.first_row[p.n_anchors];
 #pragma unroll
     for (int q = 0; q < R; q++) {
-      if (paired) {
+      if (paired && R == 1) {
+        // One row a block: blocks 2j and 2j + 1 are row j of the first
+        // anchor and of the second, held by a wavefront and the next.
+        anchor[q] = b & 1u;
+        row[q] = b >> 1;
+        live[q] = b < p.blocks && row[q] < p.rows[0];
+      } else if (paired) {
         constexpr uint32_t H = R / 2 > 0 ? R / 2 : 1;
         anchor[q] = (uint32_t)q < H ? 0u : 1u;
         row[q] = b * H + ((uint32_t)q % H);
@@ -133,7 +139,11 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
                                           float *__restrict__ epi_out, unsigned long long *__restrict__ arg,
                                           const fk_step_gemv_params &p) {
   static_assert(P * sizeof(WT) == 16, "a pack is one 16-byte load");
-  static_assert(EPI != FK_EPI_SILU_MUL || R % 2 == 0, "the SiLU·mul epilogue pairs rows");
+  static_assert(EPI != FK_EPI_SILU_MUL || R % 2 == 0 || R == 1, "the SiLU·mul epilogue pairs rows");
+  // The SiLU·mul epilogue at one row a block: a wavefront's row and its
+  // neighbour's meet in LDS (each threadgroup's wavefronts run the same
+  // number of blocks, one barrier a block).
+  constexpr bool PAIR1 = EPI == FK_EPI_SILU_MUL && R == 1;
   constexpr int C = P / 4;
   // The prologue's packs of 4 a thread holds, at most, with the 512 threads
   // every launch of these kernels has.
@@ -153,6 +163,7 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
   extern __shared__ float4 lds4[];  // xt[XT]
   __shared__ float slots[16];
   __shared__ unsigned long long bests[16];
+  __shared__ float pairv[PAIR1 ? 2 : 1][PAIR1 ? 16 : 1];  // PAIR1: each wavefront's row, by block parity
   float4 *xt = lds4;
   const uint32_t k = p.k;
   const uint32_t tid = threadIdx.x;
@@ -317,6 +328,7 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
   // Chunk c of lane l's pack it of the anchors' input row.
   auto xin4 = [&](int it, int c) -> float4 { return xt[(it * C + c) * FK_WAVE + lane]; };
   uint64_t best = 0;
+  uint32_t turn = 0;  // PAIR1: the blocks run so far
   // Block `blk`'s rows from the weights `w`: the residuals loaded first (lane q
   // holds slot q's), then (with DB) the next block's weights issued into `wn`,
   // then the block computed, reduced and its epilogue run.
@@ -381,6 +393,20 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
     }
     fk::wave_sums<R>(t);
 
+    if constexpr (PAIR1) {
+      // Row j of the first anchor (even wavefront) and of the second (the
+      // odd one next to it): both tiles stored, then act(first) · second
+      // by the even wavefront, from its partner's value in LDS.
+      const uint32_t a = blk.anchor[0], r = blk.row[0];
+      if (lane == 0) {
+        if (blk.live[0] && p.store_tile) fk::pick3(a, y0, y1, y2)[r] = t[0];
+        pairv[turn & 1][wave] = t[0];
+      }
+      __syncthreads();
+      if (lane == 0 && blk.live[0] && a == 0) epi_out[r] = fk::act_mul(t[0], pairv[turn & 1][wave + 1], p.act);
+      turn++;
+      return;
+    }
     // Epilogue: slot q's stores by lane q.
 #pragma unroll
     for (int q = 0; q < R; q++) {
@@ -416,6 +442,19 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
       if (b >= blocks) break;
       run(bb, wb, ba, wa, b + total_waves);
       b += total_waves;
+    }
+  } else if constexpr (PAIR1) {
+    // Every wavefront of the threadgroup runs as many blocks as its first
+    // (a barrier a block): a block past the last is run dead, its loads
+    // clamped into the weights.
+    uint32_t b0 = blockIdx.x * waves;
+    while (b0 < blocks) {
+      run(ba, wa, bb, wa, 0);
+      b += total_waves;
+      b0 += total_waves;
+      if (b0 >= blocks) break;
+      ba.locate(b, p);
+      fk::issue_block<WT, P, R, KPL>(wa, ba, w0, w1, w2, k, packs, lane, p);
     }
   } else {
     while (b < blocks) {
@@ -483,17 +522,17 @@ __device__ __forceinline__ void step_gemv(const WT *__restrict__ w0, const WT *_
 // 8192 (16 packs a lane), one row a block.  A block's loads are issued when the
 // block before it is done: the memory's parallelism comes from the resident
 // wavefronts, each with one block in flight.
-FK_STEP_GEMV_SHAPE(fk_step_gemv_f16_k2048_r1, _Float16, 8, 1, 4, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f16_k2048_r1, _Float16, 8, 1, 4, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f16_k2048_r2, _Float16, 8, 2, 4, false)
 FK_STEP_GEMV_SHAPE(fk_step_gemv_f16_k8192_r1, _Float16, 8, 1, 16, false)
 // bf16 weights (the reference builder's): the f16 shapes.
-FK_STEP_GEMV_SHAPE(fk_step_gemv_bf16_k2048_r1, fk::bf16_t, 8, 1, 4, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_bf16_k2048_r1, fk::bf16_t, 8, 1, 4, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_bf16_k2048_r2, fk::bf16_t, 8, 2, 4, false)
 FK_STEP_GEMV_SHAPE(fk_step_gemv_bf16_k8192_r1, fk::bf16_t, 8, 1, 16, false)
 // f32 weights: k up to 256 and 1024.
-FK_STEP_GEMV_SHAPE(fk_step_gemv_f32_k256_r1, float, 4, 1, 1, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k256_r1, float, 4, 1, 1, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k256_r2, float, 4, 2, 1, false)
-FK_STEP_GEMV_SHAPE(fk_step_gemv_f32_k1024_r1, float, 4, 1, 4, false)
+FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k1024_r1, float, 4, 1, 4, false)
 FK_STEP_GEMV_SHAPE_PAIRS(fk_step_gemv_f32_k1024_r2, float, 4, 2, 4, false)
 
 // The greedy token from the folded argmax: the largest of the threadgroups'

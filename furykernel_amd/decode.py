@@ -11,7 +11,7 @@ token costs one graph replay.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Optional
+from typing import Callable, Optional
 
 import numpy as np
 
@@ -36,17 +36,18 @@ class DecodeSession:
     fuse: bool = True
     tuned: bool = False  # shape the GEMV steps as the committed selections pick
     paging: Optional[tuple] = None  # (block size, pool blocks): the caches as paged pools
+    choose: Optional[Callable] = None  # the GEMV steps' (rows a block, threadgroups a CU), as lower_plan takes
 
     def __post_init__(self):
         self.program = decoder_step(self.dims, embed=self.embed, layers=self.layers, paging=self.paging)
         self.checked = check_program(self.program)
         self.plan = plan(self.options, self.checked)
-        choose = None
-        if self.tuned:
+        choose = self.choose
+        if self.tuned and choose is None:
             from .tuning import committed_chooser
             choose = committed_chooser(self.device.info.compute_units)
         self.lowered = lower_plan(self.checked, self.plan, fuse=self.fuse,
-                                  compute_units=self.device.info.compute_units if self.tuned else 256,
+                                  compute_units=self.device.info.compute_units if choose else 256,
                                   choose=choose)
         self.engine = Engine(self.device, self.kernels, self.lowered)
 

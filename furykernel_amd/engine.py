@@ -156,8 +156,9 @@ def check_launch(launch: Launch, specs: dict) -> None:
                                 f"{p.get('pro_mode')} and {p.get('epi_mode')}")
         if p["k"] > kmax or not 1 <= p["n_anchors"] <= 3:
             raise K.LaunchError(f"{e}: k = {p['k']} past {kmax}, or {p['n_anchors']} anchors")
-        if epi == K.EPI_SILU_MUL and (p["n_anchors"] != 2 or p["rows"][0] != p["rows"][1] or r < 2):
-            raise K.LaunchError(f"{e}: the SiLU·mul epilogue on anchors {p['rows']}, blocks of {r}")
+        if epi == K.EPI_SILU_MUL and (p["n_anchors"] != 2 or p["rows"][0] != p["rows"][1]
+                                      or (r == 1 and p["blocks"] != 2 * p["rows"][0])):
+            raise K.LaunchError(f"{e}: the SiLU·mul epilogue on anchors {p['rows']}, {p['blocks']} blocks of {r}")
         if epi == K.EPI_SOFTCAP and (p["n_anchors"] != 1 or not 0 < p.get("cap", 0) < float("inf")):
             raise K.LaunchError(f"{e}: a softcap of {p.get('cap')} on {p['n_anchors']} anchors")
         if pro == K.PRO_COMBINE and (not 1 <= p.get("splits", 0) <= K.COMBINE_SPLITS or not p.get("head_dim")

@@ -292,12 +292,13 @@ def _gemv_abis() -> dict[str, KernelAbi]:
 
 # The GEMV step kernels (fk_step_gemv.h): <shape>_p<prologue>_e<epilogue>, a
 # shape being the weight type, the largest input width it takes and its rows a
-# block; the SiLU·mul epilogue (3) only on shapes of row pairs.
-STEP_GEMV_SHAPES = {"fk_step_gemv_f16_k2048_r1": False, "fk_step_gemv_f16_k2048_r2": True,
-                    "fk_step_gemv_f16_k8192_r1": False, "fk_step_gemv_bf16_k2048_r1": False,
+# block; the SiLU·mul epilogue (3) on every shape but the widest inputs' (at
+# one row a block, a wavefront's row meets its neighbour's in LDS).
+STEP_GEMV_SHAPES = {"fk_step_gemv_f16_k2048_r1": True, "fk_step_gemv_f16_k2048_r2": True,
+                    "fk_step_gemv_f16_k8192_r1": False, "fk_step_gemv_bf16_k2048_r1": True,
                     "fk_step_gemv_bf16_k2048_r2": True, "fk_step_gemv_bf16_k8192_r1": False,
-                    "fk_step_gemv_f32_k256_r1": False,
-                    "fk_step_gemv_f32_k256_r2": True, "fk_step_gemv_f32_k1024_r1": False,
+                    "fk_step_gemv_f32_k256_r1": True,
+                    "fk_step_gemv_f32_k256_r2": True, "fk_step_gemv_f32_k1024_r1": True,
                     "fk_step_gemv_f32_k1024_r2": True}
 STEP_GEMV_ENTRIES = tuple(f"{shape}_p{pro}_e{epi}" for shape, pairs in STEP_GEMV_SHAPES.items() for pro in range(6)
                           for epi in ((0, 1, 2, 3, 4, 5) if pairs else (0, 1, 2, 4, 5)))

@@ -304,9 +304,11 @@ def _shape_gemv(launch: Launch, compute_units: int, rows: Optional[int] = None, 
         raise LoweringError(f"{launch.step}: weights of {wt}")
     entry = f"{entry}_p{p['pro_mode']}_e{p['epi_mode']}"
     if p["epi_mode"] == EPI_SILU_MUL:
-        if r < 2:
-            raise LoweringError(f"{launch.step}: the SiLU·mul epilogue needs blocks of row pairs")
-        blocks = -(-p["rows"][0] // (r // 2))
+        if r == 1 and k > 2048 and wt in (F16, BF16):
+            raise LoweringError(f"{launch.step}: no SiLU·mul epilogue at an input row of {k}")
+        # r 2: row j of both anchors a block; r 1: row j of the first anchor,
+        # then of the second, in blocks 2j and 2j + 1.
+        blocks = 2 * p["rows"][0] if r == 1 else -(-p["rows"][0] // (r // 2))
     else:
         blocks = -(-total // r)
     p["blocks"] = blocks

@@ -129,12 +129,21 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
     # issues its first block's loads (clamped) even when gw is past the blocks.
     total_waves = groups * (THREADS // WAVE)
     issued = np.unique(np.concatenate([np.arange(total_waves), np.arange(blocks)]))
+    if epi == EPI_SILU_MUL and R == 1:
+        # every wavefront of a threadgroup runs as many blocks as its first:
+        # blocks up to the next multiple of the threadgroup's wavefronts
+        waves = THREADS // WAVE
+        issued = np.unique(np.concatenate([issued, np.arange(-(-blocks // waves) * waves)]))
 
     lanes = np.arange(WAVE)
     jl = np.minimum(lanes[:, None] + WAVE * np.arange(KPL)[None, :], packs - 1).ravel()
     for q in range(R):
         b = issued
-        if epi == EPI_SILU_MUL:
+        if epi == EPI_SILU_MUL and R == 1:
+            a = b & 1
+            row = b >> 1
+            live = (b < blocks) & (row < rows[0])
+        elif epi == EPI_SILU_MUL:
             H = max(R // 2, 1)
             a = np.where(q < H, 0, 1)
             a = np.full(b.shape, a)
@@ -176,5 +185,5 @@ def check_launch(launch, buffers: dict, groups: int | None = None) -> None:
         slots = prm["arg_slots"]
         if slots > elems("arg"):
             raise Bad(f"{launch.entry}: {slots} argmax slots in a buffer of {elems('arg')}")
-    if epi == EPI_SILU_MUL and (n_anchors != 2 or rows[0] != rows[1] or R < 2):
-        raise Bad(f"{launch.entry}: the SiLU·mul epilogue on anchors {rows[:n_anchors]}, blocks of {R}")
+    if epi == EPI_SILU_MUL and (n_anchors != 2 or rows[0] != rows[1] or (R == 1 and blocks != 2 * rows[0])):
+        raise Bad(f"{launch.entry}: the SiLU·mul epilogue on anchors {rows[:n_anchors]}, {blocks} blocks of {R}")

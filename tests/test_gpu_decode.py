@@ -105,6 +105,47 @@ def test_1b_decode_step_bit_exact(device, kernels, store_gelus, tuned):
         s.close()
 
 
+@pytest.mark.parametrize("pick", [(1, 3), (1, 4), (2, 3)])
+def test_1b_decode_step_bit_exact_in_every_block_shape(device, kernels, pick):
+    """Two layers of the 1B step with every GEMV step shaped as the pick
+    says (rows a block, threadgroups a CU) where it can be: at one row a
+    block the gate/up step's SiLU·mul meets each row of gate and of up
+    across two wavefronts; every stored buffer the CPU target's."""
+    s = DecodeSession(device, kernels, ONE_B, PlanOptions(store_gelus=True), embed=True, layers=2,
+                      choose=lambda L: pick)
+    try:
+        gu = [L for L in s.lowered.launches if L.params.get("epi_mode") == 3]
+        assert gu and all(f"_r{pick[0]}_" in L.entry for L in gu)
+        s.init_synthetic()
+        s.set_position(4095, token=31999)
+        cpu = mirror(s)
+        print(f"1B decode (2 layers) with GEMV blocks {pick}: {len(s.lowered.launches)} launches", flush=True)
+        s.step()
+        device.sync()
+        cpu.run()
+        assert compare_all(s, cpu, [n for n in s.lowered.buffers if not n.startswith("weight:")]) == []
+    finally:
+        s.close()
+
+
+def test_tiny_decode_bit_exact_at_one_row_a_block(device, kernels):
+    """The tiny f32 step (SiLU·mul folded into gate/up) with every GEMV step
+    at one row a block, two threadgroups a CU: bit for bit the CPU target's."""
+    s = DecodeSession(device, kernels, TINY32, PlanOptions(store_gelus=True), embed=False, choose=lambda L: (1, 2))
+    try:
+        assert any(L.params.get("epi_mode") == 3 and "_r1_" in L.entry for L in s.lowered.launches)
+        s.init_synthetic()
+        s.set_position(20)
+        cpu = mirror(s)
+        print("tiny decode, one row a block", flush=True)
+        s.step()
+        device.sync()
+        cpu.run()
+        assert compare_all(s, cpu) == []
+    finally:
+        s.close()
+
+
 def test_1b_full_decode_greedy_tokens_via_graph(device, kernels):
     """All 16 layers, planned as the benchmark plans them: three greedy tokens by
     graph replay, each step's token the CPU target's for the same state."""

@@ -293,11 +293,21 @@ def test_a_pick_reshapes_the_launch_and_changes_no_bit():
     assert len(gu) == 16
     for i in gu:
         assert picked.launches[i].groups == 768 and base.launches[i].groups == 512
-        assert picked.launches[i].entry == base.launches[i].entry  # the SiLU pair epilogue keeps 2 rows a block
-    # a pick a launch cannot take (1 row a block under the pair epilogue) is passed over
-    odd = lower_plan(c, pl, choose=lambda L: (1, 4))
+        assert picked.launches[i].entry == base.launches[i].entry  # the SiLU pair epilogue at 2 rows a block
+    # one row a block under the pair epilogue: each row of gate, then of up,
+    # a block of its own (twice the rows in blocks)
+    one = lower_plan(c, pl, choose=lambda L: (1, 4))
     for i in gu:
-        assert odd.launches[i].entry == base.launches[i].entry and odd.launches[i].groups == base.launches[i].groups
+        L = one.launches[i]
+        assert L.entry == base.launches[i].entry.replace("_r2_", "_r1_") and L.params["blocks"] == 2 * 8192
+        assert L.groups == 1024
+    # a pick a launch cannot take (two rows a block at an input row of 8192,
+    # the down projection's) is passed over
+    down = [i for i, L in enumerate(base.launches) if "_k8192_" in L.entry]
+    assert len(down) == 16
+    two = lower_plan(c, pl, choose=lambda L: (2, 2))
+    for i in down:
+        assert two.launches[i].entry == base.launches[i].entry and two.launches[i].groups == base.launches[i].groups
 
     # the tiny step under every launch's (1, 4) and (2, 1) against the default: the same bits
     tiny = check_program(decoder_step(dataclasses.replace(TINY, context=32), embed=False))
