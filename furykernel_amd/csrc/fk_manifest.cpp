@@ -18,6 +18,7 @@
 #include <cstring>
 #include <deque>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/fkrocm.h"
@@ -228,7 +229,22 @@ std::vector<Entry> build() {
       {FK_P(fk_step_combine_ranks_params, seg, "u32"), FK_P(fk_step_combine_ranks_params, ranks, "u32"),
        FK_P(fk_step_combine_ranks_params, residual, "u32")},
       sizeof(fk_step_combine_ranks_params));
-  for (const char *name : {"fk_gemv_routed_f16_r1", "fk_gemv_routed_f16_r2", "fk_gemv_routed_f32_r1"}) {
+  add("fk_step_elementwise", 0,
+      {buf("a", "read", "f32"), buf("b", "read", "f32"), buf("c", "read", "f32"), buf("y", "write", "f32")},
+      {FK_P(fk_step_elementwise_params, n, "u32"), FK_P(fk_step_elementwise_params, op, "u32"),
+       FK_P(fk_step_elementwise_params, width, "u32"), FK_P(fk_step_elementwise_params, width_b, "u32"),
+       FK_P(fk_step_elementwise_params, factor, "f32")},
+      sizeof(fk_step_elementwise_params));
+  for (const auto &g : {std::pair<const char *, const char *>{"fk_step_gather_f32", "f32"},
+                        {"fk_step_gather_f16", "f16"}, {"fk_step_gather_bf16", "bf16"}}) {
+    using S = fk_step_gather_params;
+    add(g.first, 0, {buf("table", "read", g.second), buf("tokens", "read", "u32"), buf("y", "write", "f32")},
+        {FK_P(S, rows, "u32"), FK_P(S, width, "u32"), FK_P(S, count, "u32"), FK_P(S, table_rows, "u32"),
+         FK_P(S, factor, "f32")},
+        sizeof(S));
+  }
+  for (const char *name : {"fk_gemv_routed_f16_r1", "fk_gemv_routed_f16_r2", "fk_gemv_routed_f32_r1",
+                           "fk_gemv_routed_bf16_r1", "fk_gemv_routed_bf16_r2"}) {
     using S = fk_gemv_routed_params;
     add(name, 0,
         {buf("table", "read", "u64"), buf("ids", "read", "u32"), buf("x", "read", "f32"), buf("y", "write", "f32")},
@@ -648,6 +664,36 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
                  threads);
     need = {{"w", (uint64_t)p.ranks * 4}, {"x", (uint64_t)p.ranks * p.seg * 4}, {"y", (uint64_t)p.seg * 4}};
     if (p.residual) need.push_back({"res", (uint64_t)p.seg * 4});
+  } else if (std::strcmp(entry, "fk_step_elementwise") == 0) {
+    fk_step_elementwise_params p;
+    std::memcpy(&p, params, sizeof p);
+    const uint64_t n = p.n;
+    if (n == 0 || (uint64_t)groups * threads < n || p.op > FK_ELT_CONCAT || p.width == 0 ||
+        (p.op == FK_ELT_STANDARDIZE && n % p.width) ||
+        (p.op == FK_ELT_CONCAT && (p.width_b == 0 || n % (p.width + p.width_b))))
+      return bad(err, cap, FK_ERR_ARG, "%s: operation %u over %u elements in rows of %u (+%u), %u x %u threads",
+                 entry, p.op, p.n, p.width, p.width_b, groups, threads);
+    need = {{"a", n * 4}, {"y", n * 4}};
+    if (p.op == FK_ELT_ADD) need.push_back({"b", n * 4});
+    if (p.op == FK_ELT_SCALE) need.push_back({"b", 4});
+    if (p.op == FK_ELT_STANDARDIZE) {
+      need.push_back({"b", (uint64_t)p.width * 4});
+      need.push_back({"c", (uint64_t)p.width * 4});
+    }
+    if (p.op == FK_ELT_CONCAT) {
+      const uint64_t rows = n / (p.width + p.width_b);
+      need = {{"a", rows * p.width * 4}, {"b", rows * p.width_b * 4}, {"y", n * 4}};
+    }
+  } else if (std::strncmp(entry, "fk_step_gather_", 15) == 0) {
+    fk_step_gather_params p;
+    std::memcpy(&p, params, sizeof p);
+    const uint64_t eb = std::strcmp(entry + 15, "f32") == 0 ? 4 : 2;
+    const uint64_t n = (uint64_t)p.rows * p.width;
+    if (n == 0 || p.count == 0 || p.table_rows == 0 || (uint64_t)groups * threads < n)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows of %u, %u tokens a row of a table of %u, %u x %u threads", entry,
+                 p.rows, p.width, p.count, p.table_rows, groups, threads);
+    need = {{"table", (uint64_t)p.table_rows * p.width * eb}, {"tokens", (uint64_t)p.rows * p.count * 4},
+            {"y", n * 4}};
   } else if (std::strncmp(entry, "fk_gemv_routed_", 15) == 0) {
     fk_gemv_routed_params p;
     std::memcpy(&p, params, sizeof p);

@@ -64,6 +64,21 @@ __device__ __forceinline__ void load_pack(const _Float16 *__restrict__ p, float 
 }
 
 template <int P, bool NT = false>
+__device__ __forceinline__ void load_pack(const bf16_t *__restrict__ p, float (&out)[P]) {
+  static_assert(P % 8 == 0, "bf16 packs are 16-byte loads");
+#pragma unroll
+  for (int i = 0; i < P / 8; i++) {
+    uint4 v = load16<NT>(p + 8 * i);
+    uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      out[8 * i + 2 * h] = __uint_as_float(words[h] << 16);
+      out[8 * i + 2 * h + 1] = __uint_as_float(words[h] & 0xFFFF0000u);
+    }
+  }
+}
+
+template <int P, bool NT = false>
 __device__ __forceinline__ void load_pack(const int8_t *__restrict__ p, float (&out)[P]) {
   static_assert(P % 16 == 0, "i8 packs are 16-byte loads");
 #pragma unroll
@@ -130,6 +145,17 @@ __device__ __forceinline__ void unpack_w(const uint4 &u, float (&out)[P], _Float
   for (int h = 0; h < 4; h++) {
     out[2 * h] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] & 0xFFFFu));
     out[2 * h + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[h] >> 16));
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void unpack_w(const uint4 &u, float (&out)[P], bf16_t) {
+  static_assert(P == 8, "eight bf16 a word");
+  const uint32_t words[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int h = 0; h < 4; h++) {
+    out[2 * h] = __uint_as_float(words[h] << 16);
+    out[2 * h + 1] = __uint_as_float(words[h] & 0xFFFF0000u);
   }
 }
 
@@ -316,6 +342,9 @@ __device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, con
 FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_f16_r1, _Float16, 8, 1, 8)
 FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_f16_r2, _Float16, 8, 2, 8)
 FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_f32_r1, float, 4, 1, 16)
+// bf16 tables (the reference builder's `table`, Program/Build.hs:185-186).
+FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_bf16_r1, fk::bf16_t, 8, 1, 8)
+FK_GEMV_ROUTED_ENTRY(fk_gemv_routed_bf16_r2, fk::bf16_t, 8, 2, 8)
 
 // Packs a lane holds in flight: rows of 4096 f32, 4096 f16 (by one row or
 // two) and 8192 int8; wider rows take the loop.

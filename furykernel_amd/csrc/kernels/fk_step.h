@@ -10,6 +10,8 @@
 //   fk_step_combine  attention's combine of its splits
 //   fk_step_argmax   the greedy token of a stored row
 //   fk_step_act_mul  a stored act·mul, SiLU or GELU-tanh (the light step `store_gelus` plans)
+//   fk_step_elementwise, fk_step_gather_*  a light step's Add, ScaleBy,
+//                    Standardize, Concat, Gather of stored rows
 //   fk_step_advance  the next decode step's token and position, on the device
 //
 // Arithmetic follows the evaluator's contract (src/FuryKernel/Program/Eval.hs:
@@ -239,6 +241,55 @@ extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
   if (p.residual) acc = res[i] + acc;
   y[i] = acc;
 }
+
+// A light step's elementwise value of stored rows (Add, ScaleBy,
+// Standardize, Concat); binary32 operations in the evaluator's order.
+extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)
+    fk_step_elementwise(const float *__restrict__ a, const float *__restrict__ b, const float *__restrict__ c,
+                        float *__restrict__ y, fk_step_elementwise_params p) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.n) return;
+  switch (p.op) {
+    case FK_ELT_ADD: y[i] = a[i] + b[i]; break;
+    case FK_ELT_SCALE: y[i] = a[i] * b[0]; break;
+    case FK_ELT_STANDARDIZE: {
+      const uint32_t j = i % p.width;
+      y[i] = (p.factor * a[i] - b[j]) * c[j];
+      break;
+    }
+    default: {  // FK_ELT_CONCAT
+      const uint32_t w = p.width + p.width_b;
+      const uint32_t r = i / w, j = i % w;
+      y[i] = j < p.width ? a[(size_t)r * p.width + j] : b[(size_t)r * p.width_b + (j - p.width)];
+    }
+  }
+}
+
+// Gather: each row's tokens' table rows summed from +0 in order, then
+// scaled.
+template <typename WT>
+__device__ __forceinline__ void step_gather(const WT *__restrict__ table, const uint32_t *__restrict__ tokens,
+                                            float *__restrict__ y, const fk_step_gather_params &p) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.rows * p.width) return;
+  const uint32_t r = i / p.width, j = i % p.width;
+  float s = 0.0f;
+  for (uint32_t t = 0; t < p.count; t++) {
+    const uint32_t tok = min(tokens[(size_t)r * p.count + t], p.table_rows - 1);
+    s = s + fk::to_float(table[(size_t)tok * p.width + j]);
+  }
+  y[i] = s * p.factor;
+}
+
+#define FK_STEP_GATHER(NAME, WT)                                                                            \
+  extern "C" __global__ void __launch_bounds__(FK_STEP_THREADS)                                           \
+      NAME(const WT *__restrict__ table, const uint32_t *__restrict__ tokens, float *__restrict__ y,      \
+           fk_step_gather_params p) {                                                                      \
+    step_gather<WT>(table, tokens, y, p);                                                                  \
+  }
+FK_STEP_GATHER(fk_step_gather_f32, float)
+FK_STEP_GATHER(fk_step_gather_f16, _Float16)
+FK_STEP_GATHER(fk_step_gather_bf16, fk::bf16_t)
 
 // The next decode step's inputs: its token is this step's greedy token, its
 // position `step` more.

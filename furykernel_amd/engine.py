@@ -36,6 +36,12 @@ _STRUCTS = {
     "fk_gemv_routed_f16_r1": K.GemvRoutedParams,
     "fk_gemv_routed_f16_r2": K.GemvRoutedParams,
     "fk_gemv_routed_f32_r1": K.GemvRoutedParams,
+    "fk_gemv_routed_bf16_r1": K.GemvRoutedParams,
+    "fk_gemv_routed_bf16_r2": K.GemvRoutedParams,
+    "fk_step_elementwise": K.ElementwiseParams,
+    "fk_step_gather_f32": K.GatherParams,
+    "fk_step_gather_f16": K.GatherParams,
+    "fk_step_gather_bf16": K.GatherParams,
     "fk_prefill_softcap": K.PrefillSoftcapParams,
     "fk_step_token": K.StepTokenParams,
     "fk_gemm_f16_store": K.GemmParams,

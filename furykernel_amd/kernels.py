@@ -160,6 +160,20 @@ class ActMulParams(ctypes.Structure):
     _fields_ = [("n", ctypes.c_uint32), ("act", ctypes.c_uint32), ("b_off", ctypes.c_uint32), ("half", ctypes.c_uint32)]
 
 
+class ElementwiseParams(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_uint32), ("op", ctypes.c_uint32), ("width", ctypes.c_uint32),
+                ("width_b", ctypes.c_uint32), ("factor", ctypes.c_float)]
+
+
+class GatherParams(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_uint32), ("width", ctypes.c_uint32), ("count", ctypes.c_uint32),
+                ("table_rows", ctypes.c_uint32), ("factor", ctypes.c_float)]
+
+
+# fk_step_elementwise's operations.
+ELT_ADD, ELT_SCALE, ELT_STANDARDIZE, ELT_CONCAT = range(4)
+
+
 class PrefillArgmaxParams(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_uint32), ("width", ctypes.c_uint32)]
 
@@ -367,7 +381,11 @@ ABIS: dict[str, KernelAbi] = {
     "fk_step_route": KernelAbi("fk_step_route", ("x", "scale", "ids", "ws"), RouteParams, 64),
     "fk_step_combine_ranks": KernelAbi("fk_step_combine_ranks", ("w", "x", "res", "y"), CombineRanksParams),
     **{e: KernelAbi(e, ("table", "ids", "x", "y"), GemvRoutedParams)
-       for e in ("fk_gemv_routed_f16_r1", "fk_gemv_routed_f16_r2", "fk_gemv_routed_f32_r1")},
+       for e in ("fk_gemv_routed_f16_r1", "fk_gemv_routed_f16_r2", "fk_gemv_routed_f32_r1",
+                 "fk_gemv_routed_bf16_r1", "fk_gemv_routed_bf16_r2")},
+    "fk_step_elementwise": KernelAbi("fk_step_elementwise", ("a", "b", "c", "y"), ElementwiseParams),
+    **{f"fk_step_gather_{t}": KernelAbi(f"fk_step_gather_{t}", ("table", "tokens", "y"), GatherParams)
+       for t in ("f32", "f16", "bf16")},
     "fk_step_advance": KernelAbi("fk_step_advance", ("next_token", "token", "position"), AdvanceParams),
     "fk_init_normal": KernelAbi("fk_init_normal", ("dst",), InitNormalParams),
     "fk_noop": KernelAbi("fk_noop", (), NoopParams),
@@ -699,6 +717,9 @@ def launch_reads(entry: str, params: dict) -> set[str]:
         return {"w", "x", "y"} | ({"res"} if params.get("residual") else set())
     if entry == "fk_step_act_mul":
         return {"a", "y"} | (set() if params.get("half") else {"b"})
+    if entry == "fk_step_elementwise":
+        op = params.get("op", ELT_ADD)
+        return {"a", "y"} | ({"b", "c"} if op == ELT_STANDARDIZE else {"b"})
     if entry == "fk_step_store_paged":
         need = {"x0", "p0", "position", "table"}
         if params.get("n_stores", 1) > 1:

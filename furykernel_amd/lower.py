@@ -22,10 +22,10 @@ import numpy as np
 
 from .program.check import CheckedProgram
 from .program.graph import (
-    BF16, CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, CombineRanks, Gather, GatedGelu, GeluMul,
-    Input, KvStore, Linear, LinearRouted, Paged, Ring, RmsNorm, Rope, ROPE_HALVES, Route, SCache, SInput, Softcap,
-    SRowInts, STable, SWeight)
-from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step
+    BF16, CACHE_BF16, F16, F32, GELU_TANH, SILU, U32, Add, ArgMax, Attend, CombineRanks, Concat, Gather, GatedGelu,
+    GeluMul, Input, KvStore, Linear, LinearRouted, Paged, Ring, RmsNorm, Rope, ROPE_HALVES, Route, ScaleBy, SCache,
+    SInput, Softcap, SRowInts, Standardize, STable, SWeight, op_values as _inputs_of)
+from .program.plan import ANCHOR, COMBINE, EFFECT, EPILOGUE, LAND, RECOMPUTE, STAGE, Plan, Step, Stored, Work
 
 THREADS = 256
 ATTN_SPLIT = 128      # positions a split of the narrow attention covers (64 or 128)
@@ -46,6 +46,8 @@ PRO_STORED, PRO_RMSNORM, PRO_GATHER, PRO_GATHER_RMSNORM, PRO_SILU_MUL, PRO_COMBI
 EPI_NONE, EPI_ADD_STORED, EPI_ADD_GATHER, EPI_SILU_MUL, EPI_ARGMAX, EPI_SOFTCAP = 0, 1, 2, 3, 4, 5
 # Activations of an act·mul (the SiLU form this target adds, GELU-tanh the reference's).
 ACT = {SILU: 0, GELU_TANH: 1}
+# fk_step_elementwise's operations.
+ELT_ADD, ELT_SCALE, ELT_STANDARDIZE, ELT_CONCAT = range(4)
 
 
 class LoweringError(ValueError):
@@ -427,10 +429,52 @@ class _StepLowering:
     # Steps -----------------------------------------------------------------------
 
     def step(self, step: Step):
+        """The step's launches: one fused kernel where the step's work fits
+        one (its recomputes in the kernel's prologue), else the fewest of its
+        recomputes, in plan order, made first by launches of their own
+        (``light_launch``) and read as stored by the rest."""
         kinds = {w.kind for w in step.work}
         if STAGE in kinds or LAND in kinds:
             raise LoweringError(f"{step.name}: staged stores are not lowered yet")
+        try:
+            return self.fused_step(step)
+        except LoweringError as first:
+            last = first
+            recs = [w for w in step.work if w.kind == RECOMPUTE]
+            for k in range(1, len(recs) + 1):
+                saved = (set(self.materialized), dict(self.out.buffers), dict(self.out.constants),
+                         dict(self.out.layouts))
+                try:
+                    made = []
+                    for w in recs[:k]:
+                        L = self.light_launch(step, self.p.node(w.node))
+                        made.append(L)
+                        self.materialized |= set(L.meta["values"])
+                    done = {v for L in made for v in L.meta["values"]}
+                    rest = dataclasses.replace(step, work=[w for w in step.work if w not in recs[:k]],
+                                               stores=[st for st in step.stores if st.value not in done])
+                    if not rest.work:
+                        return made
+                    more = self.fused_step(rest)
+                    return made + (more if isinstance(more, list) else [more])
+                except LoweringError as e:
+                    last = e
+                    self.materialized, bufs, consts, lays = saved
+                    for d, old in ((self.out.buffers, bufs), (self.out.constants, consts), (self.out.layouts, lays)):
+                        d.clear()
+                        d.update(old)
+            raise last if recs else first
+
+    def fused_step(self, step: Step):
+        kinds = {w.kind for w in step.work}
         anchors = [self.p.node(w.node) for w in step.work if w.kind == ANCHOR]
+        groups = self.anchor_groups(anchors)
+        if len(groups) > 1:
+            out = []
+            for g in groups:
+                made = self.fused_step(self.sub_step(step, g))
+                out += made if isinstance(made, list) else [made]
+            return out
         if anchors and any(isinstance(a.op, LinearRouted) for a in anchors):
             return self.routed_step(step, anchors)
         # An RMSNorm the step recomputes and stores: made once by its own
@@ -462,6 +506,97 @@ class _StepLowering:
         if COMBINE in kinds:
             return self.combine_step(step)
         return self.light_step(step)
+
+    def anchor_groups(self, anchors: list) -> list:
+        """Anchors one kernel cannot take together, apart: linear layers by
+        their input row, routed ones each alone."""
+        groups: dict = {}
+        for a in anchors:
+            key = ("routed", a.id) if isinstance(a.op, LinearRouted) else \
+                ("linear", a.op.x) if isinstance(a.op, Linear) else ("other", a.id)
+            groups.setdefault(key, []).append(a)
+        return list(groups.values())
+
+    def sub_step(self, step: Step, anchors: list) -> Step:
+        """The part of a step that makes these anchors: the recomputes their
+        inputs come from, the epilogues on their tiles, the stores of what
+        they and those make."""
+        recs = {self.p.node(w.node).outputs[0]: w for w in step.work if w.kind == RECOMPUTE}
+        ids = {a.id for a in anchors}
+        need, todo = set(), [v for a in anchors for v in _inputs_of(a.op)]
+        while todo:
+            v = todo.pop()
+            if v in recs and v not in need:
+                need.add(v)
+                todo += _inputs_of(self.p.node(recs[v].node).op)
+        tiles = {v for a in anchors for v in a.outputs}
+        work = []
+        for w in step.work:
+            node = self.p.node(w.node)
+            if (w.kind == ANCHOR and w.node in ids) or (w.kind == RECOMPUTE and node.outputs[0] in need) or \
+                    (w.kind == EPILOGUE and tiles & set(_inputs_of(node.op))):
+                work.append(w)
+        made = {v for w in work for v in self.p.node(w.node).outputs}
+        return dataclasses.replace(step, work=work, stores=[st for st in step.stores if st.value in made])
+
+    def light_launch(self, step: Step, node) -> Launch:
+        """One recomputed value made by a launch of its own, from stored (or
+        already made) values, into its value buffer: the step's fused kernel
+        then reads it as stored.  ``meta["values"]`` names what it makes."""
+        op = node.op
+        out = node.outputs[0]
+        name = f"{step.name}:{self.p.value(out).name}"
+        for v in _inputs_of(op):
+            if not self.stored_before(step, v):
+                raise LoweringError(f"{step.name}: {self.p.value(out).name} of a value neither stored nor made")
+        width = self.p.value(out).shape.width
+        grid = max(1, -(-width // THREADS))
+
+        def elementwise(eop, a, b=None, c=None, w=None, wb=0, factor=1.0):
+            params = {"n": width, "op": eop, "width": w or width, "width_b": wb, "factor": float(np.float32(factor))}
+            bind = {"a": a, "b": b or a, "c": c or a, "y": self.value(out)}
+            return Launch(name, "fk_step_elementwise", grid, THREADS, bind, params, {"values": [out]})
+
+        if isinstance(op, Add):
+            return elementwise(ELT_ADD, self.value(op.a), self.value(op.b))
+        if isinstance(op, ScaleBy):
+            return elementwise(ELT_SCALE, self.value(op.x), self.gains(op.weight))
+        if isinstance(op, Standardize):
+            seg = self.p.value(op.x).shape.width
+            bias, scale = self.gains(op.bias), self.gains(op.scale)
+            if int(np.prod(self.p.source(op.bias).kind.dims)) < seg or \
+                    int(np.prod(self.p.source(op.scale).kind.dims)) < seg:
+                raise LoweringError(f"{step.name}: a standardize of rows of {seg} by a narrower bias or scale")
+            return elementwise(ELT_STANDARDIZE, self.value(op.x), bias, scale, w=seg, factor=op.factor)
+        if isinstance(op, Concat):
+            wa, wb = self.p.value(op.a).shape.width, self.p.value(op.b).shape.width
+            return elementwise(ELT_CONCAT, self.value(op.a), self.value(op.b), w=wa, wb=wb)
+        if isinstance(op, Gather):
+            tname, ttype = self.weight(op.table)
+            tsrc = self.p.source(op.tokens)
+            rows_ = self.p.source(op.table).kind.dims[0]
+            params = {"rows": 1, "width": width, "count": tsrc.kind.count, "table_rows": rows_,
+                      "factor": float(np.float32(op.factor))}
+            return Launch(name, f"fk_step_gather_{ttype}", grid, THREADS,
+                          {"table": tname, "tokens": self.ints(op.tokens), "y": self.value(out)}, params,
+                          {"values": [out]})
+        if isinstance(op, RmsNorm):
+            L = self.norm_launch(step, node)
+            L.meta["values"] = [out]
+            return L
+        if isinstance(op, Route):
+            return self.route_launch(step, node)
+        if isinstance(op, (GeluMul, GatedGelu, Softcap, ArgMax, CombineRanks)):
+            shape = self.p.value(op.x if not isinstance(op, GeluMul) else op.a).shape
+            if isinstance(op, GatedGelu) and shape.segment != shape.width:
+                L = self.gated_launch(step, node)
+                return L
+            one = dataclasses.replace(step, work=[Work(RECOMPUTE, node.id)], stores=[Stored(out, ("elements", F32))])
+            L = self.light_step(one)
+            L.step = name
+            L.meta = dict(L.meta or {}, values=[out])
+            return L
+        raise LoweringError(f"{step.name}: no launch of its own makes {type(op).__name__}")
 
     def recomputes(self, step: Step) -> dict:
         return {self.p.node(w.node).outputs[0]: self.p.node(w.node) for w in step.work if w.kind == RECOMPUTE}
@@ -824,12 +959,12 @@ class _StepLowering:
         if not isinstance(src.kind, STable):
             raise LoweringError(f"{src.name} is not a table")
         t = src.kind.type
-        if t not in (F16, F32):
-            raise LoweringError(f"table {src.name} of {t}: the routed GEMV takes f16 and f32 entries")
+        if t not in (F16, BF16, F32):
+            raise LoweringError(f"table {src.name} of {t}: the routed GEMV takes f16, bf16 and f32 entries")
         size = int(np.prod(src.kind.dims))
         pool = self.out.buffer(f"table:{src.name}", t, src.kind.entries * size)
         addr = self.out.buffer(f"tableaddr:{src.name}", "u64", src.kind.entries)
-        self.out.constants[addr] = ("addresses", pool, size * (2 if t == F16 else 4))
+        self.out.constants[addr] = ("addresses", pool, size * (4 if t == F32 else 2))
         return addr, src.kind
 
     def routed_step(self, step: Step, anchors: list) -> list:
@@ -867,7 +1002,7 @@ class _StepLowering:
         out = anchor.outputs[0]
         if [st.value for st in step.stores if st.value not in self.materialized] != [out]:
             raise LoweringError(f"{step.name}: a routed step storing other than its anchor's rows")
-        r = 2 if tk.type == F16 and n >= 2048 else 1
+        r = 2 if tk.type in (F16, BF16) and n >= 2048 else 1
         entry = f"fk_gemv_routed_{tk.type}_r{r}"
         per_group = 4 * r  # 256 threads
         gpr = -(-n // per_group)

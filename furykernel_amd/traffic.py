@@ -93,6 +93,15 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
         return p["n"] * 4 + 4
     if e == "fk_step_act_mul":
         return p["n"] * 4 * 3
+    if e == "fk_step_elementwise":
+        if p["op"] == 2:      # standardize: the row, bias and scale in, the row out
+            return p["n"] * 8 + p["width"] * 8
+        if p["op"] == 1:      # scale: the row and the factor in, the row out
+            return p["n"] * 8 + 4
+        return p["n"] * 12 if p["op"] == 0 else p["n"] * 8
+    if e.startswith("fk_step_gather_"):
+        eb = 4 if e.endswith("f32") else 2
+        return p["rows"] * p["width"] * (p["count"] * eb + 4) + p["rows"] * p["count"] * 4
     if e == "fk_prefill_softcap":
         return p["count"] * 4 * 2
     raise ValueError(f"no byte count for {e}")

@@ -215,6 +215,33 @@ typedef struct fk_step_combine_ranks_params {
   uint32_t residual;
 } fk_step_combine_ranks_params;
 
+/* A light step's elementwise value of stored rows, one thread an element of
+ * the n = rows * width elements (Eval.hs:336-355, 536-544):
+ *   FK_ELT_ADD          y = a + b                      (Add)
+ *   FK_ELT_SCALE        y = a * b[0]                   (ScaleBy; b the weight widened to f32)
+ *   FK_ELT_STANDARDIZE  y[j] = (factor a[j] - b[j]) c[j], j the element's place in its row
+ *                       (Standardize; b the bias, c the scale, each of `width` f32)
+ *   FK_ELT_CONCAT       rows of width of a, then width_b of b (Concat; n the output's elements) */
+enum { FK_ELT_ADD = 0, FK_ELT_SCALE = 1, FK_ELT_STANDARDIZE = 2, FK_ELT_CONCAT = 3 };
+typedef struct fk_step_elementwise_params {
+  uint32_t n;
+  uint32_t op;      /* FK_ELT_* */
+  uint32_t width;   /* a row's elements (of a, for FK_ELT_CONCAT) */
+  uint32_t width_b; /* FK_ELT_CONCAT: a row's elements of b */
+  float factor;     /* FK_ELT_STANDARDIZE */
+} fk_step_elementwise_params;
+
+/* Gather (Eval.hs:528-535): row r of y is the sum, from +0 in order, of the
+ * table rows of its `count` tokens (each clamped below table_rows), times
+ * factor: y[r][j] = (Σ_t table[tok(r, t)][j]) f.  One thread an element. */
+typedef struct fk_step_gather_params {
+  uint32_t rows;
+  uint32_t width;
+  uint32_t count;      /* tokens a row */
+  uint32_t table_rows;
+  float factor;
+} fk_step_gather_params;
+
 typedef struct fk_step_advance_params {
   uint32_t context; /* positions wrap below this */
   uint32_t step;    /* positions advance by this (0 holds the position) */

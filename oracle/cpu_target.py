@@ -220,7 +220,42 @@ class CpuTarget:
                 w = table.ctypes.data + ent * entry_bytes
                 xr = x.ctypes.data + (0 if p["shared"] else r * k * 4)
                 yr = y.ctypes.data + r * n * 4
-                st = st or L.fkref_gemv(w, TYPE[wt], xr, fkref.F32, yr, None, n, k, 1, 64, 8 if wt == "f16" else 4, 1)
+                st = st or L.fkref_gemv(w, TYPE[wt], xr, fkref.F32, yr, None, n, k, 1, 64, 4 if wt == "f32" else 8, 1)
+        elif e == "fk_step_elementwise":
+            # fk_step.h's elementwise operations, each a binary32 operation
+            # in the evaluator's order (Eval.hs:336-355, 536-544)
+            n, op = p["n"], p["op"]
+            a = self.buffers[b["a"]]
+            y = self.buffers[b["y"]]
+            if op == 0:
+                y[:n] = a[:n] + self.buffers[b["b"]][:n]
+            elif op == 1:
+                y[:n] = a[:n] * self.buffers[b["b"]][0]
+            elif op == 2:
+                w = p["width"]
+                bias, scale = self.buffers[b["b"]][:w], self.buffers[b["c"]][:w]
+                f = np.float32(p["factor"])
+                y[:n] = ((f * a[:n].reshape(-1, w) - bias) * scale).reshape(-1)
+            else:
+                wa, wb = p["width"], p["width_b"]
+                rows = n // (wa + wb)
+                y[:n] = np.concatenate([a[:rows * wa].reshape(rows, wa),
+                                        self.buffers[b["b"]][:rows * wb].reshape(rows, wb)], axis=1).reshape(-1)
+            st = 0
+        elif e.startswith("fk_step_gather_"):
+            # each row's tokens' table rows summed from +0 in order, then
+            # times the factor, in binary32
+            wt = e[len("fk_step_gather_"):]
+            t = self.buffers[b["table"]]
+            table = (t.astype(np.uint32) << 16).view(np.float32) if wt == "bf16" else t.astype(np.float32)
+            rows, width, count = p["rows"], p["width"], p["count"]
+            table = table[:p["table_rows"] * width].reshape(p["table_rows"], width)
+            toks = np.minimum(self.buffers[b["tokens"]][:rows * count].reshape(rows, count), p["table_rows"] - 1)
+            acc = np.zeros((rows, width), np.float32)
+            for c in range(count):
+                acc = acc + table[toks[:, c]]
+            self.buffers[b["y"]][:rows * width] = (acc * np.float32(p["factor"])).reshape(-1)
+            st = 0
         elif e == "fk_step_combine_ranks":
             st = L.fkref_combine_ranks(self._p(b["w"]), self._p(b["x"]), self._p(b["res"]), self._p(b["y"]), p["seg"],
                                        p["ranks"], p["residual"])

@@ -173,14 +173,17 @@ def _residual_gather_program(table_type):
     return program("residual_gather", body)
 
 
-def test_a_residual_gathered_from_a_table_of_another_type_is_refused():
+def test_a_residual_gathered_from_a_table_of_another_type_is_gathered_apart():
     """The GEMV step's epilogue reads the gathered residual's table as the
-    weights' element type: an f32 table under f16 weights is refused, the
-    same table in f16 lowers to the gathered-residual epilogue."""
+    weights' element type: the same table in f16 lowers to the
+    gathered-residual epilogue; an f32 table under f16 weights is refused
+    there, so its gather is a launch of its own and the epilogue adds the
+    stored row."""
     from furykernel_amd.program.graph import F16, F32
     ok = check_program(_residual_gather_program(F16))
     low = lower_plan(ok, plan(PlanOptions(), ok))
     assert [L.entry for L in low.launches] == ["fk_step_gemv_f16_k2048_r1_p0_e2"]
-    bad = check_program(_residual_gather_program(F32))
-    with pytest.raises(LoweringError, match="table of f32 under weights of f16"):
-        lower_plan(bad, plan(PlanOptions(), bad))
+    apart = check_program(_residual_gather_program(F32))
+    low = lower_plan(apart, plan(PlanOptions(), apart))
+    assert [L.entry for L in low.launches] == ["fk_step_gather_f32", "fk_step_gemv_f16_k2048_r1_p0_e1"]
+    assert low.launches[1].bind["res"] == low.launches[0].bind["y"]
