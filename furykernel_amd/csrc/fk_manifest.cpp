@@ -115,6 +115,9 @@ std::vector<Entry> build() {
       add(std::string("fk_gemv_") + wt + "_f32_r" + std::to_string(r), 0,
           {buf("w", "read", wt), buf("x", "read", "f32"), buf("y", "write", "f32")},
           {FK_P(fk_gemv_params, n, "u32"), FK_P(fk_gemv_params, k, "u32")}, sizeof(fk_gemv_params));
+  for (const char *wt : {"f32", "f16", "bf16"})
+    add(std::string("fk_gemv_p4_") + wt, 0, {buf("w", "read", wt), buf("x", "read", "f32"), buf("y", "write", "f32")},
+        {FK_P(fk_gemv_params, n, "u32"), FK_P(fk_gemv_params, k, "u32")}, sizeof(fk_gemv_params));
   for (int r : {1, 2, 4})
     add("fk_gemv_i8_f16_r" + std::to_string(r), 0,
         {buf("w", "read", "i8"), buf("scale", "read", "f32"), buf("x", "read", "f16"), buf("y", "write", "f32")},
@@ -664,6 +667,16 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
                  threads);
     need = {{"w", (uint64_t)p.ranks * 4}, {"x", (uint64_t)p.ranks * p.seg * 4}, {"y", (uint64_t)p.seg * 4}};
     if (p.residual) need.push_back({"res", (uint64_t)p.seg * 4});
+  } else if (std::strncmp(entry, "fk_gemv_p4_", 11) == 0) {
+    fk_gemv_params p;
+    std::memcpy(&p, params, sizeof p);
+    const uint64_t eb = std::strcmp(entry + 11, "f32") == 0 ? 4 : 2;
+    // a wavefront a row, packs of 4 elements
+    if (p.n == 0 || p.k == 0 || p.k % 4 || threads % 64 || threads > 256 ||
+        (uint64_t)groups * (threads / 64) < p.n)
+      return bad(err, cap, FK_ERR_ARG, "%s: %u rows of %u in %u groups of %u threads", entry, p.n, p.k, groups,
+                 threads);
+    need = {{"w", (uint64_t)p.n * p.k * eb}, {"x", (uint64_t)p.k * 4}, {"y", (uint64_t)p.n * 4}};
   } else if (std::strcmp(entry, "fk_step_elementwise") == 0) {
     fk_step_elementwise_params p;
     std::memcpy(&p, params, sizeof p);

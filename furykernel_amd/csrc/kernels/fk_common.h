@@ -41,6 +41,7 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
 
 // Four 32-bit words in registers: a 16-byte load or store.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 
 template <int CTRL>

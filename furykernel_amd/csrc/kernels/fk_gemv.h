@@ -48,9 +48,28 @@ __device__ __forceinline__ void load_pack(const float *__restrict__ p, float (&o
   }
 }
 
+// A pack of 4 half elements: one 8-byte load.
+template <bool NT>
+__device__ __forceinline__ uint2 load8(const void *p) {
+  if constexpr (NT) {
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+    return uint2{v[0], v[1]};
+  } else {
+    return *reinterpret_cast<const uint2 *>(p);
+  }
+}
+
 template <int P, bool NT = false>
 __device__ __forceinline__ void load_pack(const _Float16 *__restrict__ p, float (&out)[P]) {
-  static_assert(P % 8 == 0, "f16 packs are 16-byte loads");
+  if constexpr (P == 4) {
+    const uint2 v = load8<NT>(p);
+    out[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v.x & 0xFFFFu));
+    out[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v.x >> 16));
+    out[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v.y & 0xFFFFu));
+    out[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v.y >> 16));
+    return;
+  }
+  static_assert(P == 4 || P % 8 == 0, "f16 packs are 8- or 16-byte loads");
 #pragma unroll
   for (int i = 0; i < P / 8; i++) {
     uint4 v = load16<NT>(p + 8 * i);
@@ -65,7 +84,15 @@ __device__ __forceinline__ void load_pack(const _Float16 *__restrict__ p, float 
 
 template <int P, bool NT = false>
 __device__ __forceinline__ void load_pack(const bf16_t *__restrict__ p, float (&out)[P]) {
-  static_assert(P % 8 == 0, "bf16 packs are 16-byte loads");
+  if constexpr (P == 4) {
+    const uint2 v = load8<NT>(p);
+    out[0] = __uint_as_float(v.x << 16);
+    out[1] = __uint_as_float(v.x & 0xFFFF0000u);
+    out[2] = __uint_as_float(v.y << 16);
+    out[3] = __uint_as_float(v.y & 0xFFFF0000u);
+    return;
+  }
+  static_assert(P == 4 || P % 8 == 0, "bf16 packs are 8- or 16-byte loads");
 #pragma unroll
   for (int i = 0; i < P / 8; i++) {
     uint4 v = load16<NT>(p + 8 * i);
@@ -316,6 +343,19 @@ __device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, con
     else                                                                                                   \
       fk::gemv_wave<WT, XT, P, R>(w, x, scale, y, p.n, p.k, row0);                                         \
   }
+
+// Rows whose width is a multiple of 4 but not of a 16-byte pack (the small
+// programs' linear layers): packs of 4 elements, the loop form.
+#define FK_GEMV_P4_ENTRY(NAME, WT)                                                                            \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const WT *__restrict__ w, const float *__restrict__ x, \
+                                                         float *__restrict__ y, fk_gemv_params p) {           \
+    const uint32_t row0 = blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE;                       \
+    if (row0 >= p.n) return;                                                                                   \
+    fk::gemv_wave<WT, float, 4, 1>(w, x, nullptr, y, p.n, p.k, row0);                                          \
+  }
+FK_GEMV_P4_ENTRY(fk_gemv_p4_f32, float)
+FK_GEMV_P4_ENTRY(fk_gemv_p4_f16, _Float16)
+FK_GEMV_P4_ENTRY(fk_gemv_p4_bf16, fk::bf16_t)
 
 // LinearRouted: threadgroup (rank, group) of a rank's groups_per_rank takes
 // its W * R rows of the rank's table entry, the id clamped into the table.

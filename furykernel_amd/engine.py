@@ -39,6 +39,9 @@ _STRUCTS = {
     "fk_gemv_routed_bf16_r1": K.GemvRoutedParams,
     "fk_gemv_routed_bf16_r2": K.GemvRoutedParams,
     "fk_step_elementwise": K.ElementwiseParams,
+    "fk_gemv_p4_f32": K.GemvParams,
+    "fk_gemv_p4_f16": K.GemvParams,
+    "fk_gemv_p4_bf16": K.GemvParams,
     "fk_step_gather_f32": K.GatherParams,
     "fk_step_gather_f16": K.GatherParams,
     "fk_step_gather_bf16": K.GatherParams,

@@ -301,6 +301,9 @@ def _gemv_abis() -> dict[str, KernelAbi]:
     for r in (1, 2, 4):
         e = f"fk_gemv_i8_f16_r{r}"
         out[e] = KernelAbi(e, ("w", "scale", "x", "y"), GemvParams)
+    for wt in ("f32", "f16", "bf16"):
+        e = f"fk_gemv_p4_{wt}"
+        out[e] = KernelAbi(e, ("w", "x", "y"), GemvParams)
     return out
 
 

@@ -609,6 +609,9 @@ class _StepLowering:
             raise LoweringError(f"{step.name}: anchors of different inputs")
         x = xs.pop()
         rec = self.recomputes(step)
+        k = self.p.value(x).shape.width
+        if k % 8 and k % 4 == 0:
+            return self.small_gemv_step(step, anchors, x)
         used: set = set()
         bind: dict = {k: None for k in ("w0", "w1", "w2", "y0", "y1", "y2", "src", "src2", "gamma", "table", "token",
                                         "res", "res_table", "res_token", "epi_out", "arg")}
@@ -775,6 +778,26 @@ class _StepLowering:
         launch = Launch(step.name, "", 0, GEMV_THREADS, bind, params, {"wtype": wt})
         _shape_gemv(launch, self.compute_units, choose=self.choose)
         return launch
+
+    def small_gemv_step(self, step: Step, anchors: list, x: int) -> list:
+        """Linear anchors over a row of a multiple of 4 elements but not of a
+        16-byte pack: a launch each (fk_gemv_p4_*, a wavefront a row, packs of
+        4), from the stored row, their tiles stored."""
+        if any(w.kind not in (ANCHOR,) for w in step.work) or not self.stored_before(step, x):
+            raise LoweringError(f"{step.name}: a linear layer over a row of {self.p.value(x).shape.width} with "
+                                f"other work, or of a row not stored")
+        outs = {a.outputs[0] for a in anchors}
+        if {st.value for st in step.stores} != outs:
+            raise LoweringError(f"{step.name}: a linear layer over a short row whose tiles are not all stored")
+        k = self.p.value(x).shape.width
+        launches = []
+        for a in anchors:
+            wname, wt = self.weight(a.op.weight)
+            n = self.p.value(a.outputs[0]).shape.width
+            launches.append(Launch(step.name, f"fk_gemv_p4_{wt}", -(-n // 4), THREADS,
+                                   {"w": wname, "x": self.value(x), "y": self.value(a.outputs[0])},
+                                   {"n": n, "k": k}))
+        return launches
 
     def rope_of(self, step: Step, node, rec: dict) -> Optional[int]:
         if not isinstance(node.op, Rope):

@@ -93,6 +93,9 @@ def launch_bytes(lowered: Lowered, launch: Launch, position: int) -> int:
         return p["n"] * 4 + 4
     if e == "fk_step_act_mul":
         return p["n"] * 4 * 3
+    if e.startswith("fk_gemv_p4_"):
+        eb = 4 if e.endswith("f32") else 2
+        return p["n"] * p["k"] * eb + p["k"] * 4 + p["n"] * 4
     if e == "fk_step_elementwise":
         if p["op"] == 2:      # standardize: the row, bias and scale in, the row out
             return p["n"] * 8 + p["width"] * 8

@@ -221,6 +221,12 @@ class CpuTarget:
                 xr = x.ctypes.data + (0 if p["shared"] else r * k * 4)
                 yr = y.ctypes.data + r * n * 4
                 st = st or L.fkref_gemv(w, TYPE[wt], xr, fkref.F32, yr, None, n, k, 1, 64, 4 if wt == "f32" else 8, 1)
+        elif e.startswith("fk_gemv_p4_"):
+            # a wavefront a row, packs of 4: the reference GEMV's order at
+            # width 64, pack 4, split 1
+            wt = e[len("fk_gemv_p4_"):]
+            st = L.fkref_gemv(self._p(b["w"]), TYPE[wt], self._p(b["x"]), fkref.F32, self._p(b["y"]), None, p["n"],
+                              p["k"], 1, self.width, 4, 1)
         elif e == "fk_step_elementwise":
             # fk_step.h's elementwise operations, each a binary32 operation
             # in the evaluator's order (Eval.hs:336-355, 536-544)

@@ -2,8 +2,8 @@
 ABI (tests/test_reference_programs.py runs them on the CPU target): every
 buffer a launch writes bit for bit the oracle's CPU target's from the same
 device state, and every output within 1e-4 of the f64 evaluator.  layer
-and its k = v form, two_tiles, embed (gather scaled by 5.65625), and
-predicting, ungated and gated (bf16 expert tables)."""
+and its k = v form, two_tiles, embed (gather scaled by 5.65625), pooled
+(three rows summed, a linear layer over rows of 4), and predicting, ungated and gated (bf16 expert tables)."""
 
 import numpy as np
 import pytest

@@ -12,6 +12,9 @@ token an argmax the evaluator decides the same.
   closing chain of norms, adds and a ScaleBy;
 - ``two_tiles`` (:655-663): an Add of two anchors as its own step;
 - ``embed`` (:785-789): a gather scaled by 5.65625, stored;
+- ``pooled`` (:1614-1621): three rows of a table summed and divided by 3
+  (a repeated row among them), then a linear layer over rows of 4 (packs of
+  4 elements, a wavefront a row);
 - ``predicting`` (:769-784), planned ungated and gated (``optGated``,
   Plan.hs:246-251: the route's ids a stored step before the routed anchor).
 
@@ -31,6 +34,7 @@ CASES = {
     "layer_kv": (lambda: P.layer(True), {"position": [30], "slot": [0]}),
     "two_tiles": (P.two_tiles, {}),
     "embed": (P.embed_program, {"tokens": [37]}),
+    "pooled": (P.pooled, {"rows": [5, 0, 5]}),
     "predicting": (P.predicting, {}),
 }
 
