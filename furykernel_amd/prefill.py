@@ -61,18 +61,23 @@ QBLOCK = 32                        # rows an attention threadgroup takes
 HEAD_DIM = 64                      # the attention kernel's head dimension
 
 
-def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int, run_rows: Optional[int] = None) -> Lowered:
+def lower_prefill(checked: CheckedProgram, plan: Plan, rows: int, run_rows: Optional[int] = None,
+                  scratch_slot: bool = False) -> Lowered:
     """The launches of every step of the plan for a step of `rows` rows (a
     multiple of 256: the sequences' rows one after another, each sequence's
     run a multiple of 32 rows; `run_rows` rows each where the plan stages
-    KV stores, the plan's sequence rows)."""
+    KV stores, the plan's sequence rows).  With `scratch_slot`, each ring
+    holds one slot more (and each paged pool one block more) past the
+    program's: rows that only fill a step out to its tiles store there, so
+    that a step's real rows may be any number (``PrefillSession``,
+    ``DecodeRows``)."""
     if rows <= 0 or rows % SLAB:
         raise LoweringError(f"a step of {rows} rows; the prefill kernels take multiples of {SLAB}")
     run_rows = rows if run_rows is None else run_rows
     if run_rows <= 0 or run_rows % QBLOCK or rows % run_rows:
         raise LoweringError(f"runs of {run_rows} rows in a step of {rows}: multiples of {QBLOCK} that divide it")
     out = Lowered(checked.program, plan, rows)
-    _Prefill(out, run_rows).run()
+    _Prefill(out, run_rows, scratch_slot).run()
     _fuse_qkv_rope(out)
     _fuse_argmax(out)
     return out
@@ -150,9 +155,10 @@ def _fuse_qkv_rope(out: Lowered) -> None:
 
 
 class _Prefill:
-    def __init__(self, out: Lowered, run_rows: int):
+    def __init__(self, out: Lowered, run_rows: int, scratch: bool = False):
         self.out = out
         self.run_rows = run_rows
+        self.scratch = int(scratch)  # a ring's slots (a pool's blocks) one past the program's
         self.staged: set = set()   # KvStore nodes the plan stages
         self.landing: dict = {}    # KvStore node id -> (staging buffer, ring buffer)
         self.p = out.program
@@ -241,9 +247,9 @@ class _Prefill:
         lay = src.kind.layout
         bf16 = src.kind.elem == CACHE_BF16
         if isinstance(lay, Ring):
-            count = lay.slots * lay.kv_heads * lay.length * lay.head_dim
+            count = (lay.slots + self.scratch) * lay.kv_heads * lay.length * lay.head_dim
         else:
-            count = lay.blocks * lay.kv_heads * lay.block_size * lay.head_dim
+            count = (lay.blocks + self.scratch) * lay.kv_heads * lay.block_size * lay.head_dim
         return self.out.buffer(f"cache:{src.name}", "bf16" if bf16 else "f16", count), lay, bf16
 
     def rope(self, spec, d: int, rows: int) -> str:
@@ -456,7 +462,7 @@ class _Prefill:
         if paged:
             table, table_len = self.tables(op.to.sequences)
             length = table_len * klay.block_size   # the positions a row's table covers
-            paging = {"block_size": klay.block_size, "table_len": table_len, "blocks": klay.blocks}
+            paging = {"block_size": klay.block_size, "table_len": table_len, "blocks": klay.blocks + self.scratch}
         else:
             length, paging = klay.length, None
             if klay.length % ATTEND_KEYS:
@@ -506,14 +512,16 @@ class _Prefill:
                      "rope": self.rope(rs, HEAD_DIM, length), "qr": qr, "kc": ks or kname, "vc": vs or vname},
                     dict({"rows": self.rows, "heads": heads, "kv_heads": kvh, "head_dim": HEAD_DIM,
                           "rotated": rs.rotated, "rope_rows": length, "length": length,
-                          "slots": 0 if paged else klay.slots, "cache_bf16": int(kbf), "staged": int(staged)},
+                          "slots": 0 if paged else klay.slots + self.scratch, "cache_bf16": int(kbf),
+                          "staged": int(staged)},
                          **(paging or {})))
         outv = anchor.outputs[0]
         obuf = self.value_tiled(outv)
         self.tiled_of[outv] = obuf
         g = heads // kvh
         params = {"rows": self.rows, "heads": heads, "kv_heads": kvh, "length": length,
-                  "slots": 0 if paged else klay.slots, "window": spec.window or 0, "cache_bf16": int(kbf),
+                  "slots": 0 if paged else klay.slots + self.scratch, "window": spec.window or 0,
+                  "cache_bf16": int(kbf),
                   "scale": float(np.float32(spec.scale)), "staged": int(staged), "run_rows": self.run_rows}
         if paged:
             self.launch(step, f"fk_prefill_attend_paged_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
@@ -546,7 +554,7 @@ class _Prefill:
                     {"ks": ks, "vs": vs, "position": self.ints(lands[0].op.at.positions),
                      "slot": self.ints(lands[0].op.at.sequences), "kc": kname, "vc": vname},
                     {"rows": self.rows, "kv_heads": lay.kv_heads, "head_dim": lay.head_dim, "length": lay.length,
-                     "slots": lay.slots})
+                     "slots": lay.slots + self.scratch})
 
     def light_step(self, step: Step) -> None:
         rec = self.recomputes(step)
@@ -577,66 +585,78 @@ def weight_image(lowered: Lowered, name: str, weights: dict) -> np.ndarray:
     return pack(pair(mats[0], mats[1]))
 
 
-def check_rows(positions, slots, qblock: int = QBLOCK) -> None:
+def check_rows(positions, slots, qblock: int = QBLOCK, first_rows: bool = False) -> None:
     """The attention's contract on a step's rows: every block of `qblock`
-    rows is one sequence's (one slot) at consecutive positions."""
+    rows is one sequence's (one slot) at consecutive positions.  With
+    `first_rows`, rows of slot -1 are rows that fill the step out: a block's
+    real rows come first, and its filling rows continue their positions."""
     pos = np.asarray(positions, np.int64).reshape(-1)
     sl = np.asarray(slots, np.int64).reshape(-1)
     if pos.size != sl.size or pos.size % qblock:
         raise LoweringError(f"{pos.size} rows: the prefill attention takes blocks of {qblock}")
     pb, sb = pos.reshape(-1, qblock), sl.reshape(-1, qblock)
-    if np.any(sb != sb[:, :1]) or np.any(pb - pb[:, :1] != np.arange(qblock)):
+    if first_rows:
+        fill = sb < 0
+        if np.any(fill[:, :-1] & ~fill[:, 1:]) or np.any(np.where(fill, sb[:, :1], sb) != sb[:, :1]):
+            raise LoweringError(f"a block of {qblock} rows whose real rows are not first, or of two sequences")
+    elif np.any(sb != sb[:, :1]):
+        raise LoweringError(f"rows of a block of {qblock} are not one sequence's")
+    if np.any(pb - pb[:, :1] != np.arange(qblock)):
         raise LoweringError(f"rows of a block of {qblock} are not one sequence's consecutive positions")
 
 
-class PrefillSession:
-    """The prefill of `seqs` sequences of `seq_rows` rows each (positions 0 ..
-    seq_rows - 1, sequence i in ring slot i) through one decoder program:
-    gated, planned with steps of the sequence's rows, lowered to the prefill
-    kernels and resident on one GPU.  The KV caches it fills are the decode
-    step's (the same names, layout and rounding)."""
+def run_of(seq_rows: int) -> int:
+    """The rows a sequence's run takes in a step: its rows rounded up to
+    whole query blocks, so that a step's tiles are whole runs (32, 64, 128
+    or 256 rows, or a multiple of 256)."""
+    if seq_rows < 1:
+        raise LoweringError(f"a run of {seq_rows} rows")
+    if seq_rows > SLAB:
+        return -(-seq_rows // SLAB) * SLAB
+    run = QBLOCK
+    while run < seq_rows:
+        run *= 2
+    return run
 
-    def __init__(self, device, kernels, dims, seqs: int, seq_rows: int, layers: Optional[int] = None,
-                 embed: bool = True, rope_rotated: Optional[int] = None, position_bound: Optional[int] = None,
-                 paging: Optional[tuple] = None, tables: Optional[np.ndarray] = None):
+
+class _RowsSession:
+    """A step of many rows through the prefill kernels, its rows placed:
+    ``place`` gives each row of the step (padded out to whole tiles) its
+    position and slot; rows that only fill the step out store into the
+    caches' scratch slot, one past the program's, and their outputs are
+    never read.  The KV caches are the decode step's (the same names,
+    layout and rounding), with that slot after them."""
+
+    def _setup(self, device, kernels, dims, program, sequence_rows: int, rows: int, run_rows: int,
+               positions, slots, real, scratch: bool, paging=None, tables=None) -> None:
         from .engine import Engine
         from .program.check import check_program
-        from .program.decoder import decoder_step
         from .program.plan import PlanOptions, plan
 
-        if seqs < 1 or seqs > dims.slots:
-            raise LoweringError(f"{seqs} sequences for caches of {dims.slots} slots")
         self.device, self.kernels, self.dims = device, kernels, dims
-        self.seqs, self.seq_rows, self.rows = seqs, seq_rows, seqs * seq_rows
-        self.embed = embed
-        # Positions below `position_bound` (the rows' own, seq_rows, by
-        # default): a bound past what the ring holds beyond a step's rows
-        # makes the plan stage the KV stores.
-        self.program = decoder_step(dims, "prefill", embed, layers, position_bound=position_bound or seq_rows,
-                                    rope_rotated=rope_rotated, paging=paging)
+        self.program = program
         self.checked = check_program(self.program)
-        self.plan = plan(PlanOptions(sequence_rows=seq_rows), self.checked)
-        self.lowered = lower_prefill(self.checked, self.plan, self.rows, run_rows=seq_rows)
+        self.plan = plan(PlanOptions(sequence_rows=sequence_rows), self.checked)
+        self.lowered = lower_prefill(self.checked, self.plan, rows, run_rows=run_rows, scratch_slot=scratch)
         self.engine = Engine(device, kernels, self.lowered)
-        positions = np.tile(np.arange(seq_rows, dtype=np.uint32), seqs)
-        slots = np.repeat(np.arange(seqs, dtype=np.uint32), seq_rows)
-        check_rows(positions, slots, seq_rows)
-        self.engine.set_ints("position", positions, seq_rows)
+        self.rows, self.run_rows = rows, run_rows
+        self.real = np.asarray(real, np.int64)
+        self.positions = np.asarray(positions, np.uint32)
+        self.slots = np.asarray(slots, np.uint32)
+        marks = np.where(np.isin(np.arange(rows), self.real), self.slots.astype(np.int64), -1)
+        check_rows(self.positions, marks, QBLOCK, first_rows=True)
+        # the real rows' positions and slots within their bounds; the
+        # filling rows' positions continue their block's, past the bound
+        bound = self.checked.program.source_named("position").kind.bound
+        if np.any(self.positions[self.real] >= bound):
+            raise LoweringError(f"positions {self.positions[self.real].tolist()} not below their bound {bound}")
+        self.engine.write("ints:position", self.positions)
         if paging is None:
-            self.engine.set_ints("slot", slots, dims.slots)
+            self.engine.set_ints("slot", self.slots, dims.slots + int(scratch))
         else:
-            # Paged pools (paging = (block size, pool blocks)): sequence i's
-            # block table is row i of `tables` (default: distinct blocks in a
-            # scrambled order), every row of the sequence carrying it.
             block_size, pool_blocks = paging
-            table_len = dims.context // block_size
-            if tables is None:
-                if seqs * table_len > pool_blocks:
-                    raise LoweringError(f"{seqs} tables of {table_len} blocks in a pool of {pool_blocks}")
-                perm = np.random.default_rng(0).permutation(pool_blocks)[:seqs * table_len]
-                tables = perm.reshape(seqs, table_len)
-            self.tables = np.asarray(tables, np.uint32).reshape(seqs, table_len)
-            self.engine.set_ints("blocks", np.repeat(self.tables, seq_rows, axis=0), pool_blocks)
+            self.tables = np.asarray(tables, np.uint32)
+            self.engine.set_ints("blocks", self.tables, pool_blocks + int(scratch))
 
     def weight_buffers(self):
         return [name for name in self.lowered.layouts]
@@ -659,10 +679,17 @@ class PrefillSession:
         self.device.sync()
 
     def set_tokens(self, tokens) -> None:
-        self.engine.set_ints("tokens", np.asarray(tokens, np.uint32).reshape(-1), self.dims.vocab)
+        """The real rows' tokens, in order (the filling rows take token 0)."""
+        t = np.zeros(self.rows, np.uint32)
+        t[self.real] = np.asarray(tokens, np.uint32).reshape(-1)
+        self.engine.set_ints("tokens", t, self.dims.vocab)
 
     def set_rows(self, x: np.ndarray) -> None:
-        self.engine.write("value:x", np.asarray(x, np.float32).reshape(-1))
+        """The real rows' inputs, in order (the filling rows zero)."""
+        x = np.asarray(x, np.float32).reshape(len(self.real), -1)
+        full = np.zeros((self.rows, x.shape[1]), np.float32)
+        full[self.real] = x
+        self.engine.write("value:x", full.reshape(-1))
 
     def run(self, stream=None) -> None:
         self.engine.enqueue(stream)
@@ -675,13 +702,117 @@ class PrefillSession:
         return any(L.entry == "fk_prefill_land" for L in self.lowered.launches)
 
     def logits(self) -> np.ndarray:
-        return self.engine.read("value:logits").reshape(self.rows, -1)
+        """The real rows' logits, in order."""
+        return self.engine.read("value:logits").reshape(self.rows, -1)[self.real]
 
     def tokens(self) -> np.ndarray:
-        return self.engine.read("value:token")
+        return self.engine.read("value:token")[self.real]
 
     def cache(self, name: str) -> np.ndarray:
         return self.engine.read(f"cache:{name}")
 
     def close(self) -> None:
         self.engine.close()
+
+
+class PrefillSession(_RowsSession):
+    """The prefill of `seqs` sequences of `seq_rows` rows each (positions 0 ..
+    seq_rows - 1, sequence i in ring slot i) through one decoder program:
+    gated, planned with steps of the sequence's rows, lowered to the prefill
+    kernels and resident on one GPU.  The KV caches it fills are the decode
+    step's (the same names, layout and rounding)."""
+
+    def __init__(self, device, kernels, dims, seqs: int, seq_rows: int, layers: Optional[int] = None,
+                 embed: bool = True, rope_rotated: Optional[int] = None, position_bound: Optional[int] = None,
+                 paging: Optional[tuple] = None, tables: Optional[np.ndarray] = None):
+        from .program.decoder import decoder_step
+
+        if seqs < 1 or seqs > dims.slots:
+            raise LoweringError(f"{seqs} sequences for caches of {dims.slots} slots")
+        self.seqs, self.seq_rows = seqs, seq_rows
+        self.embed = embed
+        # Each sequence's rows take a run of whole query blocks, and the step
+        # whole tiles of runs: rows past a sequence's (and whole runs past
+        # the sequences) fill them out, in the scratch slot.
+        rows, run, positions, slots, real = prefill_placement(seqs, seq_rows, dims.slots)
+        pad = rows != seqs * seq_rows
+        rows_tables = None
+        if paging is not None:
+            # Paged pools (paging = (block size, pool blocks)): sequence i's
+            # block table is row i of `tables` (default: distinct blocks in a
+            # scrambled order), every row of the sequence carrying it; the
+            # filling rows' tables hold the scratch block.
+            block_size, pool_blocks = paging
+            table_len = dims.context // block_size
+            if tables is None:
+                if seqs * table_len > pool_blocks:
+                    raise LoweringError(f"{seqs} tables of {table_len} blocks in a pool of {pool_blocks}")
+                perm = np.random.default_rng(0).permutation(pool_blocks)[:seqs * table_len]
+                tables = perm.reshape(seqs, table_len)
+            tables = np.asarray(tables, np.uint32).reshape(seqs, table_len)
+            rows_tables = np.full((rows, table_len), pool_blocks, np.uint32)
+            for i in range(seqs):
+                rows_tables[i * run:i * run + seq_rows] = tables[i]
+        # Positions below `position_bound` (the rows' own, seq_rows, by
+        # default): a bound past what the ring holds beyond a step's rows
+        # makes the plan stage the KV stores.
+        program = decoder_step(dims, "prefill", embed, layers, position_bound=position_bound or seq_rows,
+                               rope_rotated=rope_rotated, paging=paging)
+        self._setup(device, kernels, dims, program, seq_rows, rows, run, positions, slots, real, pad, paging,
+                    rows_tables)
+        if paging is not None:
+            self.tables = tables
+
+
+
+class DecodeRows(_RowsSession):
+    """A decode step of several rows (Eval.hs:126-140: each row a sequence
+    at its own position and slot) through the prefill kernels: row i is the
+    first row of query block i, whose other 31 rows continue its positions
+    in the scratch slot (their outputs unread), the step filled out to whole
+    tiles likewise.  The program is the decode step's (``decoder_step``,
+    positions below the context), planned one row a sequence."""
+
+    def __init__(self, device, kernels, dims, positions, slots, layers: Optional[int] = None, embed: bool = True):
+        from .program.decoder import decoder_step
+
+        self.embed = embed
+        rows, pos, sl, real = decode_placement(positions, slots, dims.slots)
+        program = decoder_step(dims, "decode", embed, layers, position_bound=dims.context)
+        self._setup(device, kernels, dims, program, 1, rows, QBLOCK, pos, sl, real, True)
+
+
+def decode_placement(positions, slots, n_slots: int) -> tuple:
+    """A decode step's rows in a step of whole tiles: (rows, each row's
+    position, its slot, the real rows).  Row i is the first row of query
+    block i; the rest of each block continues its positions in the scratch
+    slot (`n_slots`), and blocks past the rows fill the tiles out there."""
+    positions = np.asarray(positions, np.uint32).reshape(-1)
+    slots = np.asarray(slots, np.uint32).reshape(-1)
+    m = positions.size
+    if m < 1 or slots.size != m or np.any(slots >= n_slots):
+        raise LoweringError(f"{m} rows in slots {slots.tolist()} of {n_slots}")
+    rows = -(-m * QBLOCK // SLAB) * SLAB
+    pos = np.zeros(rows, np.uint32)
+    sl = np.full(rows, n_slots, np.uint32)
+    for b in range(rows // QBLOCK):
+        pos[b * QBLOCK:(b + 1) * QBLOCK] = (positions[b] if b < m else 0) + np.arange(QBLOCK, dtype=np.uint32)
+    real = np.arange(m) * QBLOCK
+    sl[real] = slots
+    return rows, pos, sl, real
+
+
+def prefill_placement(seqs: int, seq_rows: int, n_slots: int) -> tuple:
+    """A prefill's rows in a step of whole tiles: (rows, the run of each
+    sequence, each row's position, its slot, the real rows).  Sequence i's
+    rows (positions 0 .. seq_rows - 1, slot i) start run i; the run's rest,
+    and runs past the sequences, continue positions in the scratch slot
+    (`n_slots`)."""
+    run = run_of(seq_rows)
+    rows = -(-seqs * run // SLAB) * SLAB
+    positions = np.tile(np.arange(run, dtype=np.uint32), rows // run)
+    slots = np.full(rows, n_slots, np.uint32)
+    real = np.concatenate([np.arange(i * run, i * run + seq_rows) for i in range(seqs)])
+    for i in range(seqs):
+        slots[i * run:i * run + seq_rows] = i
+    return rows, run, positions, slots, real

@@ -134,3 +134,22 @@ def test_every_paged_launch_passes_the_launch_checks(case):
     for checked in (paged_program(case), paged_program(case, reach_bound=case[3] * case[5]), ring_program(case)):
         for fuse in (True, False):
             host_checked(lower_plan(checked, plan(PlanOptions(), checked), fuse=fuse))
+
+
+def test_the_planner_stages_ring_stores_only():
+    """Plan.hs:335-345 stages a store only into a ring (``SCache (Ring ..)``)
+    whose room is short of a step's rows; a paged pool's store is never
+    staged, whatever the rows: the same prefill program over a ring of 256
+    positions with positions bound by the whole ring stages its stores, and
+    over a paged pool of the same positions does not (so no lowering of a
+    staged store into a pool is asked for)."""
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.decoder import SMALL_PREFILL, decoder_step
+    from furykernel_amd.program.plan import LAND, STAGE, PlanOptions, plan
+
+    def kinds(paging):
+        c = check_program(decoder_step(SMALL_PREFILL, name="prefill", layers=1, paging=paging))
+        return {w.kind for s in plan(PlanOptions(sequence_rows=128), c).steps for w in s.work}
+
+    assert {STAGE, LAND} <= kinds(None)
+    assert not {STAGE, LAND} & kinds((64, 16))
