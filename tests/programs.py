@@ -12,7 +12,7 @@ from furykernel_amd.program.graph import (
 
 
 def layer(k_eq_v: bool = False):
-    """ProgramTest.hs:412-485: hidden 32, four query heads of 8 over two KV
+    """ProgramTest.hs:488-557: hidden 32, four query heads of 8 over two KV
     heads, 8 experts of 16 of which a row takes 2."""
     hidden, eps = 32, 1e-6
 
