@@ -80,6 +80,27 @@ def test_gemv_i8_8192(device, kernels):
     assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 32, 16, 2, row_scale=s)))
 
 
+@pytest.mark.parametrize("r,k", [(1, 8192), (2, 8192), (4, 8192), (1, 1040), (2, 4096), (4, 2064)])
+def test_gemv_i8_edge_values_bit_exact(device, kernels, r, k):
+    """The reference chain's order bit for bit on the whole int8 range (-128
+    and 0 included) against x with f16 subnormals, signed zeros, its
+    largest values and cancelling pairs, full and ragged rows, every load in
+    flight and the loop form of the widest rows."""
+    n = 512
+    rng = np.random.default_rng(17 + r)
+    w = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    w[:, ::7] = 0
+    pick = rng.integers(0, 6, k)
+    x = np.select([pick == 0, pick == 1, pick == 2, pick == 3, pick == 4],
+                  [rng.integers(1, 1024, k) * 2.0 ** -24, np.where(rng.integers(0, 2, k) == 1, -0.0, 0.0),
+                   rng.choice([-65504.0, 65504.0], k), rng.normal(0, 1, k) * 2.0 ** 10, rng.normal(0, 1, k)],
+                  rng.normal(0, 1e-3, k)).astype(np.float16)
+    x[1::2][:100] = -x[0::2][:100]  # pairs that cancel
+    s = np.ones(n, np.float32)
+    got = run_gemv(device, kernels, w, x, "i8", r, scale=s)
+    assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 64, 16, 1, row_scale=s)))
+
+
 def test_gemv_i8_integer_closed_form(device, kernels):
     n, k = 256, 8192
     w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
