@@ -549,8 +549,11 @@ def main_kernels(args) -> int:
 
 # The IR target's bf16 GEMV family at the 1B decode's FFN shapes: a few
 # variants each (rows a SIMD group, threads, pack, split-K).
-IR_GEMV = {(8192, 2048): [(4, 256, 8, 2), (2, 256, 8, 1), (2, 1024, 8, 4), (2, 512, 8, 2)],
-           (2048, 8192): [(2, 1024, 8, 4), (1, 1024, 8, 4), (1, 512, 8, 2), (2, 512, 8, 2)]}
+# The variants of the IR GEMV family timed a shape: the fastest of a sweep of
+# rows a SIMD group 1-8, threads 256-1024 and splits 1-16 on the MI355X, and
+# their neighbours.
+IR_GEMV = {(8192, 2048): [(2, 256, 8, 4), (4, 256, 8, 4), (2, 512, 8, 4), (2, 1024, 8, 4)],
+           (2048, 8192): [(4, 1024, 8, 16), (2, 1024, 8, 16), (2, 1024, 8, 4), (2, 256, 8, 4)]}
 
 
 def ir_gemv_table(dev, timed, copies_of) -> dict:
