@@ -326,31 +326,16 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
     // pool's block a block's positions apart
     constexpr bool PAGED = MODE == FK_GEMM_QKV_ROPE_PAGED;
     const size_t hstride = anchor == 0 || rp.staged ? 64 : (PAGED ? (size_t)pg.block_size : (size_t)rp.length) * 64;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t row = m + 16 * i;
-      const uint32_t pos = position[row];
-      // PAGED: `slot` holds the rows' block tables; position pos's block,
-      // the table index and the block clamped into place.  A position past
-      // its table stores no k or v (as the decode step's paged store skips
-      // it); its q row is still written.
-      const uint32_t sl = PAGED ? min(slot[(size_t)row * pg.table_len + min(pos / pg.block_size, pg.table_len - 1)],
-                                      pg.blocks - 1)
-                                : min(slot[row], rp.slots - 1);
-      const bool keep = !PAGED || anchor == 0 || pos / pg.block_size < pg.table_len;
-      const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
-      uint16_t *const base =
-          anchor == 0 ? dst + (size_t)row * p.ldc[0] + head0 * 64
-          : rp.staged ? dst + ((size_t)row * rp.kv_heads + head0) * 64
-          : PAGED     ? dst + (((size_t)sl * rp.kv_heads + head0) * pg.block_size + pos % pg.block_size) * 64
-                      : dst + (((size_t)sl * rp.kv_heads + head0) * rp.length + pos % rp.length) * 64;
+    // Row block i's RoPE and stores: `base` its row's first head, `unit(u)`
+    // the u-th 16 bytes (pairs 2 u, 2 u + 1) of its position's table row.
+    auto emit = [&](int i, uint16_t *const base, bool keep, auto unit) {
 #pragma unroll
       for (int jp = 0; jp < 2; jp++)
 #pragma unroll
         for (int jj = 0; jj < 2; jj++) {
           const uint32_t d = 16 * jj + nq;  // the low half's first of four columns; their partners d + 32 ..
-          const float4 t01 = *reinterpret_cast<const float4 *>(cs + 2 * d);      // (cos, sin) of pairs d, d + 1
-          const float4 t23 = *reinterpret_cast<const float4 *>(cs + 2 * d + 4);  // pairs d + 2, d + 3
+          const float4 t01 = unit(d / 2);      // (cos, sin) of pairs d, d + 1
+          const float4 t23 = unit(d / 2 + 1);  // pairs d + 2, d + 3
           const float cc[4] = {t01.x, t01.z, t23.x, t23.z};
           const float sn[4] = {t01.y, t01.w, t23.y, t23.w};
           uint16_t lo[4], hi[4];
@@ -371,6 +356,76 @@ __device__ __forceinline__ void gemm_tile(const _Float16 *__restrict__ a, const 
           }
         }
       asm volatile("" ::: "memory");  // one row block at a time
+    };
+    if constexpr (PAGED) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t row = m + 16 * i;
+        const uint32_t pos = position[row];
+        // `slot` holds the rows' block tables; position pos's block, the
+        // table index and the block clamped into place.  A position past its
+        // table stores no k or v (as the decode step's paged store skips
+        // it); its q row is still written.
+        const uint32_t sl =
+            min(slot[(size_t)row * pg.table_len + min(pos / pg.block_size, pg.table_len - 1)], pg.blocks - 1);
+        const bool keep = anchor == 0 || pos / pg.block_size < pg.table_len;
+        const float *cs = rope + (size_t)min(pos, rp.rope_rows - 1) * 64;
+        uint16_t *const base =
+            anchor == 0 ? dst + (size_t)row * p.ldc[0] + head0 * 64
+                        : dst + (((size_t)sl * rp.kv_heads + head0) * pg.block_size + pos % pg.block_size) * 64;
+        emit(i, base, keep, [&](uint32_t u) { return *reinterpret_cast<const float4 *>(cs + 4 * u); });
+      }
+    } else {
+      // A ring's tile: its 256 rows' RoPE table entries and ring places go
+      // into LDS first (the K loop's ring is free once every wavefront is
+      // past its last step), and the row blocks read them there: read from
+      // HBM at each row block's turn, every row block would wait for its
+      // loads behind the stores of the row block before it (the vector
+      // memory counter counts loads and stores together).  Thread t takes row
+      // t's position and place (the offset of its first head's row in the
+      // ring); then each wavefront loads 64 rows' entries straight into LDS,
+      // 4 rows (1 KB) a load, lane L taking 16-byte unit (L mod 16) ^ (r mod
+      // 16) of row r = 4 q + L div 16 into place L mod 16 of the row, so that
+      // the 16 rows of a row block's reads meet 16 different places.
+      float *const lrope = reinterpret_cast<float *>(gemm_lds);  // [256 rows][64]
+      uint32_t *const lpos = reinterpret_cast<uint32_t *>(lrope + 256 * 64);
+      uint64_t *const lrow = reinterpret_cast<uint64_t *>(lpos + 256);
+      __syncthreads();
+      {
+        const uint32_t row = m0 + tid;
+        const uint32_t pos = position[row];
+        lpos[tid] = min(pos, rp.rope_rows - 1);
+        // (The ring length is taken anew through an asm statement, so that
+        // its reciprocal is not computed before the K loop and held across
+        // it.)
+        uint32_t length = rp.length;
+        asm volatile("" : "+s"(length));
+        lrow[tid] = ((uint64_t)min(slot[row], rp.slots - 1) * rp.kv_heads * length + pos % length) * 64;
+      }
+      __syncthreads();
+      {
+        const auto rsrc = fk::buffer(rope, (size_t)rp.rope_rows * 64 * 4);
+        FK_LDS char *const lbase = (FK_LDS char *)gemm_lds + wave_s * 64 * 256;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+          const uint32_t r = wave * 64 + 4 * q + lane / 16;
+          const uint32_t unit = (lane % 16) ^ (r % 16);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lbase + q * 1024, 16, (lpos[r] * 64 + unit * 4) * 4, 0, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t rt = wm * 128 + lane_e % 16 + 16 * i;  // the row in the tile
+        const uint32_t row = m0 + rt;
+        const float *cs = lrope + rt * 64;
+        uint16_t *const base = anchor == 0 ? dst + (size_t)row * p.ldc[0] + head0 * 64
+                               : rp.staged ? dst + ((size_t)row * rp.kv_heads + head0) * 64
+                                           : dst + lrow[rt] + head0 * hstride;
+        emit(i, base, true,
+             [&](uint32_t u) { return *reinterpret_cast<const float4 *>(cs + 4 * (u ^ (rt % 16))); });
+      }
     }
   } else {
     float *out = reinterpret_cast<float *>(anchor == 0 ? c0 : (anchor == 1 ? c1 : c2));
