@@ -348,8 +348,9 @@ std::vector<Entry> build() {
   }
   {
     using S = fk_prefill_attend_params;
+    for (const char *form : {"fk_prefill_attend_g", "fk_prefill_attend_f16_g"})
     for (int g : {1, 2, 4})
-      add("fk_prefill_attend_g" + std::to_string(g), 64 * g,
+      add(form + std::to_string(g), 64 * g,
           {buf("qr", "read", "f16"), buf("kc", "read", "f16"), buf("vc", "read", "f16"),
            buf("position", "read", "u32"), buf("slot", "read", "u32"), buf("out", "write", "f16"),
            buf("ks", "read", "f16"), buf("vs", "read", "f16")},
@@ -785,9 +786,14 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
       for (Need &n : need)
         if (std::strcmp(n.name, "c1") == 0 || std::strcmp(n.name, "c2") == 0) n.bytes = pool;
     }
-  } else if (std::strncmp(entry, "fk_prefill_attend_g", 19) == 0) {
+  } else if (std::strncmp(entry, "fk_prefill_attend_g", 19) == 0 ||
+             std::strncmp(entry, "fk_prefill_attend_f16_g", 23) == 0) {
     fk_prefill_attend_params p;
     std::memcpy(&p, params, sizeof p);
+    // The f16 form loads f16 ring rows straight into LDS: no bf16 rows to
+    // convert, no staged rows.
+    if (entry[18] == 'f' && (p.cache_bf16 || p.staged))
+      return bad(err, cap, FK_ERR_ARG, "%s: bf16 caches %u or staged rows %u", entry, p.cache_bf16, p.staged);
     const uint64_t kw = (uint64_t)p.kv_heads * 64 * 2;
     need = {{"qr", (uint64_t)p.rows * p.heads * 64 * 2},
             {"kc", (uint64_t)p.slots * p.length * kw},

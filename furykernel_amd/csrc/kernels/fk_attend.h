@@ -64,7 +64,13 @@ typedef float fk_float2v __attribute__((ext_vector_type(2)));
 // PG: the caches are paged pools ([blocks][kv_heads][block_size][64]) and
 // `slot` the rows' block tables ([rows][table_len]); a block of rows reads
 // its first row's table (its rows are one sequence's).
-template <uint32_t G, bool PG = false>
+// DIRECT: f16 rings and no staged rows; each block's K and V rows go
+// straight from the ring into LDS (direct loads, no registers between), a
+// row's units placed by the loads' source addresses as the staging writes
+// would place them; keys past the block's last query read that query's own
+// row (its score is masked and its probability 0, so a finite row is all
+// it needs).
+template <uint32_t G, bool PG = false, bool DIRECT = false>
 __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc,
                                                const uint16_t *__restrict__ vc, const uint32_t *__restrict__ position,
                                                const uint32_t *__restrict__ slot, uint16_t *__restrict__ out,
@@ -294,6 +300,40 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // registers, and go into the other pair after (every wavefront left it at
   // the last barrier); one barrier a block.
   const uint32_t kb0 = first_pos / FK_ATT_KB, kb_last = last_pos / FK_ATT_KB;
+  if constexpr (DIRECT) {
+    // Block kb's rows into buffer buf: wavefront w's q-th load fills keys
+    // 8 (w NQ + q) .. + 7 (1 KB), lane L unit L mod 8 of key L div 8's row.
+    constexpr uint32_t NQ = 8 / G;
+    const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
+    const auto krs = fk::buffer(kc + cache_base, (size_t)p.length * 128);
+    const auto vrs = fk::buffer(vc + cache_base, (size_t)p.length * 128);
+    const uint32_t last_row = last_pos % p.length;
+    auto fetch_direct = [&](uint32_t kb, uint32_t buf) {
+      const uint32_t ring0 = (kb * FK_ATT_KB) % p.length;
+#pragma unroll
+      for (uint32_t q = 0; q < NQ; q++) {
+        const uint32_t key = (wave * NQ + q) * 8 + lane / 8, slot_u = lane % 8;
+        const uint32_t row = kb * FK_ATT_KB + key <= last_pos ? ring0 + key : last_row;
+        const uint32_t ku = slot_u ^ ((key >> 1) & 7u);         // K: unit u at place u ^ ((key >> 1) mod 8)
+        const uint32_t vu = slot_u ^ (((key >> 1) & 1u) << 2);  // V: the row's halves swapped when key bit 1 is set
+        const uint32_t at = (wave_s * NQ + q) * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (FK_ATT_LDS char *)&ks[buf][0] + at, 16, (row * 64 + ku * 8) * 2,
+                                                 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (FK_ATT_LDS char *)&vs[buf][0] + at, 16, (row * 64 + vu * 8) * 2,
+                                                 0, 0, 0);
+      }
+    };
+    fetch_direct(kb0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (uint32_t kb = kb0; kb <= kb_last; kb++) {
+      const uint32_t buf = (kb - kb0) & 1;
+      if (kb < kb_last) fetch_direct(kb + 1, buf ^ 1);
+      step(kb, buf);
+      __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of block kb + 1 landed
+      __syncthreads();
+    }
+  } else {
   if constexpr (PG) locate(kb0);
   fetch(kreg, kc, kst, kb0);
   fetch(vreg, vc, vst, kb0);
@@ -313,6 +353,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
       stash_v(buf ^ 1);
     }
     __syncthreads();
+  }
   }
 
   // O = Oᵀ / sum into the tile layout: lane l's query row, d = 32 db + 8 gg +
@@ -340,6 +381,19 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
 FK_PREFILL_ATTEND(1)
 FK_PREFILL_ATTEND(2)
 FK_PREFILL_ATTEND(4)
+
+// The same over f16 rings with no staged rows, each block's rows loaded
+// straight into LDS (the same bindings; ks and vs unused).
+#define FK_PREFILL_ATTEND_F16(G)                                                                                \
+  extern "C" __global__ void __launch_bounds__(64 * G) fk_prefill_attend_f16_g##G(                     \
+      const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,       \
+      const uint32_t *__restrict__ position, const uint32_t *__restrict__ slot, uint16_t *__restrict__ out,   \
+      const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs, fk_prefill_attend_params p) {          \
+    prefill_attend<G, false, true>(qr, kc, vc, position, slot, out, nullptr, nullptr, p);                      \
+  }
+FK_PREFILL_ATTEND_F16(1)
+FK_PREFILL_ATTEND_F16(2)
+FK_PREFILL_ATTEND_F16(4)
 
 // The same over paged pools: kc and vc the pools, `table` the rows' block
 // tables; no staged rows.

@@ -59,9 +59,8 @@ _STRUCTS = {
     **{f"fk_prefill_norm_pack_w{w}": K.PrefillNormParams for w in K.NORM_PACK_HELD},
     "fk_prefill_rope_store": K.PrefillRopeParams,
     "fk_prefill_rope_store_paged": K.PrefillRopePagedParams,
-    "fk_prefill_attend_g1": K.PrefillAttendParams,
-    "fk_prefill_attend_g2": K.PrefillAttendParams,
-    "fk_prefill_attend_g4": K.PrefillAttendParams,
+    **{f"{form}{g}": K.PrefillAttendParams for form in ("fk_prefill_attend_g", "fk_prefill_attend_f16_g")
+       for g in (1, 2, 4)},
     "fk_prefill_argmax": K.PrefillArgmaxParams,
     "fk_prefill_argmax_keys": K.PrefillArgmaxKeysParams,
     "fk_prefill_land": K.PrefillLandParams,

@@ -354,10 +354,9 @@ ABIS: dict[str, KernelAbi] = {
                                              PrefillRopePagedParams),
     "fk_prefill_rope_store": KernelAbi("fk_prefill_rope_store", ("q", "k", "v", "position", "slot", "rope", "qr",
                                                                  "kc", "vc"), PrefillRopeParams),
-    **{f"fk_prefill_attend_g{g}": KernelAbi(f"fk_prefill_attend_g{g}", ("qr", "kc", "vc", "position", "slot",
-                                                                        "out", "ks", "vs"), PrefillAttendParams,
-                                            64 * g)
-       for g in (1, 2, 4)},
+    **{f"{form}{g}": KernelAbi(f"{form}{g}", ("qr", "kc", "vc", "position", "slot", "out", "ks", "vs"),
+                               PrefillAttendParams, 64 * g)
+       for form in ("fk_prefill_attend_g", "fk_prefill_attend_f16_g") for g in (1, 2, 4)},
     **{f"fk_prefill_attend_paged_g{g}": KernelAbi(f"fk_prefill_attend_paged_g{g}", ("qr", "kc", "vc", "position",
                                                                                     "table", "out"),
                                                   PrefillAttendPagedParams, 64 * g)
@@ -577,7 +576,8 @@ class Kernels:
         f16): an element beyond f16's range (|x| > 65504) becomes infinite and
         one below 2^-24 flushes to zero, so bf16 caches are for values inside
         f16's range, as the prefill's own stores of f16-range rows are."""
-        entry = f"fk_prefill_attend_g{heads // kv_heads if kv_heads and heads % kv_heads == 0 else 0}"
+        g = heads // kv_heads if kv_heads and heads % kv_heads == 0 else 0
+        entry = f"fk_prefill_attend_{'g' if cache_bf16 else 'f16_g'}{g}"
         if rows <= 0 or rows % 256 or kv_heads <= 0 or heads % kv_heads or heads // kv_heads not in (1, 2, 4):
             raise LaunchError(f"{entry}: {rows} rows, {heads} heads over {kv_heads}")
         if length <= 0 or length % ATTEND_KEYS:
@@ -753,6 +753,6 @@ def launch_reads(entry: str, params: dict) -> set[str]:
         return need
     if entry == "fk_rmsnorm_f32" or entry.startswith("fk_prefill_norm_pack"):
         return set(abi.buffers) - ({"gamma"} if not params.get("has_gamma") else set())
-    if entry.startswith("fk_prefill_attend_g"):
+    if entry.startswith(("fk_prefill_attend_g", "fk_prefill_attend_f16_g")):
         return set(abi.buffers) - (set() if params.get("staged") else {"ks", "vs"})
     return set(abi.buffers)

@@ -528,7 +528,9 @@ class _Prefill:
                         {"qr": qr, "kc": kname, "vc": vname, "position": pos, "table": seq, "out": obuf},
                         dict(params, **paging))
         else:
-            self.launch(step, f"fk_prefill_attend_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
+            # f16 rings without staged rows: each block's rows straight into LDS
+            form = "fk_prefill_attend_g" if kbf or staged else "fk_prefill_attend_f16_g"
+            self.launch(step, f"{form}{g}", (self.rows // QBLOCK) * kvh, 64 * g,
                         {"qr": qr, "kc": kname, "vc": vname, "position": pos, "slot": seq, "out": obuf,
                          "ks": ks, "vs": vs}, params)
 

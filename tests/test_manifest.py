@@ -269,6 +269,32 @@ def test_the_launch_check_takes_the_prefill_heads_keys_and_refuses_them_out_of_s
         _check(token, low.buffers, params=p)
 
 
+def test_the_launch_check_takes_the_f16_prefill_attention_only_without_bf16_or_staged_rows():
+    """The f16 form loads f16 ring rows straight into LDS: a launch of it
+    with bf16 caches or staged rows is refused; the lowering gives those the
+    staging form."""
+    from furykernel_amd.engine import params_struct
+    from furykernel_amd.prefill import lower_prefill
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.decoder import SMALL_PREFILL, decoder_step
+    from furykernel_amd.program.plan import PlanOptions, plan
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256)
+    att = next(L for L in low.launches if L.entry.startswith("fk_prefill_attend"))
+    assert att.entry == "fk_prefill_attend_f16_g2"
+    _check(att, low.buffers)
+    for field in ("cache_bf16", "staged"):
+        p = params_struct(att)
+        setattr(p, field, 1)
+        if field == "staged":
+            p.run_rows = 128
+        with pytest.raises(runtime.FkError, match="bf16 caches"):
+            _check(att, low.buffers, params=p)
+    staged = check_program(decoder_step(SMALL_PREFILL, name="prefill"))
+    low = lower_prefill(staged, plan(PlanOptions(sequence_rows=128), staged), 256, run_rows=128)
+    assert {L.entry for L in low.launches if L.entry.startswith("fk_prefill_attend")} == {"fk_prefill_attend_g2"}
+
+
 def test_the_launch_check_refuses_prefill_attention_stores_and_lands_out_of_shape():
     """The ring prefill attention's grid is every (query block, kv head),
     its heads G to a kv head, its ring in blocks of 64 positions; the RoPE

@@ -56,7 +56,8 @@ def test_prefill_lowering_of_the_small_decoder():
     entries = [l.entry for l in low.launches]
     norm = "fk_prefill_norm_pack"     # rows of 256: the two-pass kernel
     # the QKV GEMM RoPEs and stores in its epilogue: no RoPE launch, no f32 q, k, v
-    per_layer = [norm, "fk_gemm_f16_qkv_rope", "fk_prefill_attend_g2",
+    # f16 rings, no staged rows: the attention loads its blocks straight into LDS
+    per_layer = [norm, "fk_gemm_f16_qkv_rope", "fk_prefill_attend_f16_g2",
                  "fk_gemm_f16_add", norm, "fk_gemm_f16_silu_mul", "fk_gemm_f16_add"]
     # the head's GEMM leaves the greedy token's keys, 128 columns a key
     assert entries == ["fk_prefill_gather"] + per_layer * 2 + [norm, "fk_gemm_f16_store_keys",
@@ -69,7 +70,7 @@ def test_prefill_lowering_of_the_small_decoder():
     qkv = low.launches[2]
     assert qkv.params["first_col"] == [0, 512, 768, 1024] and qkv.groups == 1 * 4
     att = low.launches[3]
-    assert att.entry == "fk_prefill_attend_g2" and att.threads == 128 and att.groups == (256 // 32) * 4
+    assert att.entry == "fk_prefill_attend_f16_g2" and att.threads == 128 and att.groups == (256 // 32) * 4
     assert (qkv.bind["c0"], qkv.bind["c1"], qkv.bind["c2"]) == (att.bind["qr"], att.bind["kc"], att.bind["vc"])
     assert (qkv.params["kv_heads"], qkv.params["length"], qkv.params["slots"]) == (4, 256, 2)
     assert not any(b.startswith(("value:l0_q", "value:l0_k", "value:l0_v")) for b in low.buffers)
@@ -95,7 +96,7 @@ def test_prefill_lowering_of_the_1b_decoder():
     gu = [l for l in low.launches if l.entry == "fk_gemm_f16_silu_mul"][0]
     assert gu.groups == 32 * (8192 // 128)
     att = [l for l in low.launches if l.entry.startswith("fk_prefill_attend")][0]
-    assert att.entry == "fk_prefill_attend_g4" and att.threads == 256 and att.groups == 256 * 8
+    assert att.entry == "fk_prefill_attend_f16_g4" and att.threads == 256 and att.groups == 256 * 8
     assert low.buffers["cache:l0_k_cache"].count == 4 * 8 * 4096 * 64
     assert low.launches[1].entry == "fk_prefill_norm_pack_w2048"   # the one-pass norm of rows of 2048
 
