@@ -27,6 +27,11 @@
  *   fk_gemm_f16_store_keys a b0 b1 b2 c0 c1 c2 r0 keys  fk_gemm_params
  *   fk_gemm_f16_qkv_rope_paged a b0 b1 b2 c0 c1 c2 r0 position table rope
  *                                                      fk_gemm_qkv_paged_params
+ *   fk_prefill_attend_g<1|2|4>, fk_prefill_attend_f16_g<1|2|4>
+ *                        qr kc vc position slot out ks vs
+ *                                                      fk_prefill_attend_params
+ *     (the f16 form: f16 rings and no staged rows, each key block loaded
+ *     straight into LDS; ks and vs unused)
  *   fk_prefill_attend_paged_g<1|2|4> qr kc vc position table out
  *                                                      fk_prefill_attend_paged_params
  *   fk_prefill_argmax_keys keys out                    fk_prefill_argmax_keys_params
