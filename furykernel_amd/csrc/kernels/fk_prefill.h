@@ -105,11 +105,22 @@ __device__ __forceinline__ void norm_pack_held(const float *__restrict__ x, cons
   const uint32_t lane = threadIdx.x & (FK_WAVE - 1);
   constexpr uint32_t width = 512 * U;
   const float *xr = x + (size_t)row * width;
-  float4 a[U], b[U];
+  // The row and the gains are loaded together, so that the gains' round
+  // trip is not added after the row's sum.
+  float4 a[U], b[U], ga[U], gb[U];
 #pragma unroll
   for (int t = 0; t < U; t++) {
     a[t] = *reinterpret_cast<const float4 *>(xr + 8 * (lane + 64 * t));
     b[t] = *reinterpret_cast<const float4 *>(xr + 8 * (lane + 64 * t) + 4);
+  }
+#pragma unroll
+  for (int t = 0; t < U; t++) {
+    ga[t] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    gb[t] = ga[t];
+    if (p.has_gamma) {
+      ga[t] = *reinterpret_cast<const float4 *>(gamma + 8 * (lane + 64 * t));
+      gb[t] = *reinterpret_cast<const float4 *>(gamma + 8 * (lane + 64 * t) + 4);
+    }
   }
   float ss = 0.0f;
 #pragma unroll
@@ -121,12 +132,7 @@ __device__ __forceinline__ void norm_pack_held(const float *__restrict__ x, cons
 #pragma unroll
   for (int t = 0; t < U; t++) {
     const uint32_t u = lane + 64 * t;
-    float g[8] = {1, 1, 1, 1, 1, 1, 1, 1};
-    if (p.has_gamma) {
-      const float4 ga = *reinterpret_cast<const float4 *>(gamma + 8 * u);
-      const float4 gb = *reinterpret_cast<const float4 *>(gamma + 8 * u + 4);
-      g[0] = ga.x; g[1] = ga.y; g[2] = ga.z; g[3] = ga.w; g[4] = gb.x; g[5] = gb.y; g[6] = gb.z; g[7] = gb.w;
-    }
+    const float g[8] = {ga[t].x, ga[t].y, ga[t].z, ga[t].w, gb[t].x, gb[t].y, gb[t].z, gb[t].w};
     const float v[8] = {a[t].x, a[t].y, a[t].z, a[t].w, b[t].x, b[t].y, b[t].z, b[t].w};
     uint32_t h[4];
 #pragma unroll
