@@ -9,7 +9,7 @@ TEST INFRASTRUCTURE: imported only by tests/, as the checker of the target's
 binary32 results against the evaluator's exact ones.
 
 `evaluate_bounds` follows Eval.hs's node cases for the operations the decode
-programs use (Input, Linear, RmsNorm, Add, Concat, ScaleBy, GatedGelu,
+programs use (Input, Linear, RmsNorm, Add, Concat, ScaleBy, Standardize, GatedGelu,
 GeluMul, Rope, Softcap, KvStore, Attend, Gather, ArgMax) on one row a step,
 given the exact values `oracle.eval.evaluate` made.  The SiLU form of GeluMul
 is this target's addition: silu(a) = a / (1 + e^-a), bounded as that
@@ -25,7 +25,7 @@ import numpy as np
 
 from furykernel_amd.program.graph import (
     Add, ArgMax, Attend, Concat, GatedGelu, GELU_TANH, GeluMul, Gather, Input, KvStore, Linear, Ring, RmsNorm, Rope,
-    SCache, ScaleBy, SILU, Softcap)
+    SCache, ScaleBy, SILU, Softcap, Standardize)
 
 from .eval import EvalError, Evaluation, round_cache
 
@@ -378,12 +378,19 @@ def evaluate_bounds(checked, b, ev: Evaluation, kept=None) -> Bounds:
         elif isinstance(op, Rope):
             spec = op.spec
             d = values[op.x].shape.segment
-            pos = float(row_int(op.positions)[0])
+            part = d // spec.axes
+            pos = row_int(op.positions)
             xs = approx(op.x)
             bs = []
             for c in range(0, len(xs), d):
-                bs += rotation_bounds(float(spec.theta), spec.rotated, d, pos, xs[c:c + d])
+                for a in range(spec.axes):
+                    bs += rotation_bounds(float(spec.theta), spec.rotated, part, float(pos[a]),
+                                          xs[c + a * part:c + (a + 1) * part])
             put(out, bs)
+        elif isinstance(op, Standardize):
+            bias, scale = weight(op.bias), weight(op.scale)
+            put(out, [product_a([sum_a([product_a([const_a(op.factor), u]), neg_a(exact_a(float(bias[j])))]),
+                                 exact_a(float(scale[j]))]).bound for j, u in enumerate(approx(op.x))])
         elif isinstance(op, Softcap):
             put(out, [product_a([const_a(op.cap), monotone_a(5, math.tanh, product_a([u, const_a(1 / op.cap)]))]).bound
                       for u in approx(op.x)])

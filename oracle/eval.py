@@ -23,7 +23,7 @@ import numpy as np
 from furykernel_amd.program.check import CheckedProgram
 from furykernel_amd.program.graph import (
     CACHE_BF16, Add, ArgMax, Attend, CombineRanks, Concat, Gather, GatedGelu, GELU_TANH, GeluMul, Input, KvStore,
-    Linear, LinearRouted, Ring, RmsNorm, Rope, Route, SCache, ScaleBy, SILU, Softcap, STable)
+    Linear, LinearRouted, Ring, RmsNorm, Rope, Route, SCache, ScaleBy, SILU, Softcap, Standardize, STable)
 
 from . import fkref
 
@@ -249,16 +249,21 @@ def evaluate(checked: CheckedProgram, b: Bindings, kept: Kept | None = None) -> 
         elif isinstance(op, GeluMul):
             env[out] = [np.array([gelu(op.form, u) * v for u, v in zip(x, y)]) for x, y in zip(env[op.a], env[op.b])]
         elif isinstance(op, Rope):
+            # Eval.hs:372-383: a head of d is `axes` parts of d / axes, part a
+            # turned by the row's a-th position as a head of its own width.
             spec = op.spec
-            if spec.axes != 1:
-                raise EvalError("RoPE of several axes is not evaluated here")
             d = values[op.x].shape.segment
+            part = d // spec.axes
             ps = ints(op.positions)
             res = []
             for pos, x in zip(ps, env[op.x]):
-                res.append(np.concatenate([rotate(spec.theta, spec.rotated, d, float(pos[0]), x[c:c + d])
-                                           for c in range(0, len(x), d)]))
+                res.append(np.concatenate([rotate(spec.theta, spec.rotated, part, float(pos[a]), x[c + a * part:c + (a + 1) * part])
+                                           for c in range(0, len(x), d) for a in range(spec.axes)]))
             env[out] = res
+        elif isinstance(op, Standardize):
+            # Eval.hs:536-543: (f x_j - bias_j) scale_j.
+            bias, scale = weight(op.bias), weight(op.scale)
+            env[out] = [np.array([(op.factor * v - bias[j]) * scale[j] for j, v in enumerate(x)]) for x in env[op.x]]
         elif isinstance(op, Softcap):
             env[out] = [np.array([op.cap * math.tanh(v / op.cap) for v in x]) for x in env[op.x]]
         elif isinstance(op, KvStore):
@@ -498,16 +503,22 @@ def evaluate_fast(checked: CheckedProgram, b: Bindings) -> Evaluation:
             env[out] = op.cap * np.tanh(env[op.x] / op.cap)
         elif isinstance(op, Rope):
             spec = op.spec
-            d = values[op.x].shape.segment
+            d = values[op.x].shape.segment // spec.axes        # the width each axis turns
             half = d // 2
-            pos = ints(op.positions)[:, 0].astype(np.float64)
+            pos = ints(op.positions).astype(np.float64)          # [m, axes]
             i = np.arange(half)
             freq = np.array([math.pow(spec.theta, -(2 * j) / d) if j < spec.rotated else 0.0 for j in i])
-            t = pos[:, None] * freq[None, :]                       # [m, half]
-            c, s_ = np.cos(t)[:, None, :], np.sin(t)[:, None, :]
-            x = env[op.x].reshape(m, -1, d)
+            t = pos[:, None, :, None] * freq[None, None, None, :]   # [m, 1, axes, half]
+            c, s_ = np.cos(t), np.sin(t)
+            x = env[op.x].reshape(m, -1, spec.axes, d)
             lo, hi = x[..., :half], x[..., half:]
             env[out] = np.concatenate([lo * c - hi * s_, hi * c + lo * s_], axis=-1).reshape(m, -1)
+        elif isinstance(op, Standardize):
+            env[out] = (op.factor * env[op.x] - weight(op.bias)[None, :]) * weight(op.scale)[None, :]
+        elif isinstance(op, Concat):
+            env[out] = np.concatenate([env[op.a], env[op.b]], axis=1)
+        elif isinstance(op, ScaleBy):
+            env[out] = env[op.x] * weight(op.weight)[0]
         elif isinstance(op, KvStore):
             src = sources[op.at.cache]
             lay, elem = src.kind.layout, src.kind.elem
