@@ -361,8 +361,9 @@ std::vector<Entry> build() {
   }
   {
     using S = fk_prefill_attend_paged_params;
+    for (const char *form : {"fk_prefill_attend_paged_g", "fk_prefill_attend_paged_f16_g"})
     for (int g : {1, 2, 4})
-      add("fk_prefill_attend_paged_g" + std::to_string(g), 64 * g,
+      add(form + std::to_string(g), 64 * g,
           {buf("qr", "read", "f16"), buf("kc", "read", "f16"), buf("vc", "read", "f16"),
            buf("position", "read", "u32"), buf("table", "read", "u32"), buf("out", "write", "f16")},
           {FK_P(S, a.rows, "u32"), FK_P(S, a.heads, "u32"), FK_P(S, a.kv_heads, "u32"), FK_P(S, a.length, "u32"),
@@ -838,11 +839,19 @@ int fk_launch_check(const char *entry, uint32_t groups, uint32_t threads, uint32
             {"v", (uint64_t)p.rows * kw * 4}, {"position", (uint64_t)p.rows * 4},
             {"table", (uint64_t)p.rows * pp.g.table_len * 4}, {"rope", (uint64_t)p.rope_rows * p.rotated * 8},
             {"qr", (uint64_t)p.rows * p.heads * p.head_dim * 2}, {"kc", pool}, {"vc", pool}};
-  } else if (std::strncmp(entry, "fk_prefill_attend_paged_g", 25) == 0) {
+  } else if (std::strncmp(entry, "fk_prefill_attend_paged_g", 25) == 0 ||
+             std::strncmp(entry, "fk_prefill_attend_paged_f16_g", 29) == 0) {
     fk_prefill_attend_paged_params pp;
     std::memcpy(&pp, params, sizeof pp);
     const fk_prefill_attend_params &p = pp.a;
     const uint32_t g = (uint32_t)(entry[std::strlen(entry) - 1] - '0');
+    // The f16 form loads f16 pool rows straight into LDS, at 32-bit offsets
+    // into the pool, through a block table it holds in LDS (256 entries).
+    if (entry[24] == 'f' &&
+        (p.cache_bf16 || pp.g.table_len > 256 ||
+         (uint64_t)pp.g.blocks * p.kv_heads * pp.g.block_size * 128 > 0xFFFFFFFFull))
+      return bad(err, cap, FK_ERR_ARG, "%s: bf16 caches %u, tables of %u, a pool of %u blocks", entry, p.cache_bf16,
+                 pp.g.table_len, pp.g.blocks);
     if (p.rows == 0 || p.rows % 32 || p.kv_heads == 0 || p.heads != g * p.kv_heads || p.staged ||
         (p.run_rows && (p.run_rows % 32 || p.rows % p.run_rows)) || pp.g.block_size == 0 || pp.g.table_len == 0 ||
         pp.g.blocks == 0 || groups != (p.rows / 32) * p.kv_heads)

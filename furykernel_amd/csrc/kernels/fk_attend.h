@@ -31,6 +31,7 @@
 // layout of [rows, heads · 64], the output projection's A.
 
 #define FK_ATT_KB 64     // keys a block
+#define FK_ATT_TABLE 256 // a block table's entries the direct paged form holds in LDS
 // Staged rows are 64 halves (128 bytes), swizzled rather than padded.  K: a
 // row's 16-byte unit u sits at u ^ ((key >> 1) mod 8), so that the fragment
 // reads (16 lanes: 16 keys, one unit) meet 16 different bank groups and the
@@ -303,17 +304,33 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   if constexpr (DIRECT) {
     // Block kb's rows into buffer buf: wavefront w's q-th load fills keys
     // 8 (w NQ + q) .. + 7 (1 KB), lane L unit L mod 8 of key L div 8's row.
+    // A ring's rows are read relative to the (slot, kv head) ring; a pool's
+    // relative to the pool (under 4 GiB), through the threadgroup's block
+    // table, which goes into LDS first (its blocks clamped into the pool).
     constexpr uint32_t NQ = 8 / G;
     const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
-    const auto krs = fk::buffer(kc + cache_base, (size_t)p.length * 128);
-    const auto vrs = fk::buffer(vc + cache_base, (size_t)p.length * 128);
-    const uint32_t last_row = last_pos % p.length;
+    const size_t span = PG ? (size_t)pg.blocks * p.kv_heads * pg.block_size * 128 : (size_t)p.length * 128;
+    const auto krs = fk::buffer(PG ? kc : kc + cache_base, span);
+    const auto vrs = fk::buffer(PG ? vc : vc + cache_base, span);
+    const uint32_t last_row = PG ? 0u : last_pos % p.length;
+    __shared__ uint32_t ltab[PG ? FK_ATT_TABLE : 1];
+    if constexpr (PG) {
+      const uint32_t used = min(last_pos / pg.block_size + 1, pg.table_len);
+      for (uint32_t i = tid; i < used; i += nthreads) ltab[i] = min(tab[i], pg.blocks - 1);
+      __syncthreads();
+    }
     auto fetch_direct = [&](uint32_t kb, uint32_t buf) {
-      const uint32_t ring0 = (kb * FK_ATT_KB) % p.length;
+      const uint32_t ring0 = PG ? 0u : (kb * FK_ATT_KB) % p.length;
 #pragma unroll
       for (uint32_t q = 0; q < NQ; q++) {
         const uint32_t key = (wave * NQ + q) * 8 + lane / 8, slot_u = lane % 8;
-        const uint32_t row = kb * FK_ATT_KB + key <= last_pos ? ring0 + key : last_row;
+        uint32_t row;  // the key's row (of 64 halves) in the ring or the pool
+        if constexpr (PG) {
+          const uint32_t t = min(kb * FK_ATT_KB + key, last_pos);
+          row = (ltab[min(t / pg.block_size, pg.table_len - 1)] * p.kv_heads + g) * pg.block_size + t % pg.block_size;
+        } else {
+          row = kb * FK_ATT_KB + key <= last_pos ? ring0 + key : last_row;
+        }
         const uint32_t ku = slot_u ^ ((key >> 1) & 7u);         // K: unit u at place u ^ ((key >> 1) mod 8)
         const uint32_t vu = slot_u ^ (((key >> 1) & 1u) << 2);  // V: the row's halves swapped when key bit 1 is set
         const uint32_t at = (wave_s * NQ + q) * 1024;
@@ -407,4 +424,17 @@ FK_PREFILL_ATTEND_F16(4)
 FK_PREFILL_ATTEND_PAGED(1)
 FK_PREFILL_ATTEND_PAGED(2)
 FK_PREFILL_ATTEND_PAGED(4)
+
+// The same over f16 pools (under 4 GiB, tables of at most FK_ATT_TABLE
+// blocks), each block's rows loaded straight into LDS.
+#define FK_PREFILL_ATTEND_PAGED_F16(G)                                                                            \
+  extern "C" __global__ void __launch_bounds__(64 * G) fk_prefill_attend_paged_f16_g##G(                         \
+      const uint16_t *__restrict__ qr, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,         \
+      const uint32_t *__restrict__ position, const uint32_t *__restrict__ table, uint16_t *__restrict__ out,     \
+      fk_prefill_attend_paged_params p) {                                                                        \
+    prefill_attend<G, true, true>(qr, kc, vc, position, table, out, nullptr, nullptr, p.a, p.g);                 \
+  }
+FK_PREFILL_ATTEND_PAGED_F16(1)
+FK_PREFILL_ATTEND_PAGED_F16(2)
+FK_PREFILL_ATTEND_PAGED_F16(4)
 

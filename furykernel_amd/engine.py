@@ -53,7 +53,8 @@ _STRUCTS = {
     "fk_gemm_f16_silu_mul": K.GemmParams,
     "fk_gemm_f16_qkv_rope": K.GemmQkvParams,
     "fk_gemm_f16_qkv_rope_paged": K.GemmQkvPagedParams,
-    **{f"fk_prefill_attend_paged_g{g}": K.PrefillAttendPagedParams for g in (1, 2, 4)},
+    **{f"{form}{g}": K.PrefillAttendPagedParams for form in ("fk_prefill_attend_paged_g", "fk_prefill_attend_paged_f16_g")
+       for g in (1, 2, 4)},
     "fk_prefill_gather": K.PrefillGatherParams,
     "fk_prefill_norm_pack": K.PrefillNormParams,
     **{f"fk_prefill_norm_pack_w{w}": K.PrefillNormParams for w in K.NORM_PACK_HELD},

@@ -357,10 +357,9 @@ ABIS: dict[str, KernelAbi] = {
     **{f"{form}{g}": KernelAbi(f"{form}{g}", ("qr", "kc", "vc", "position", "slot", "out", "ks", "vs"),
                                PrefillAttendParams, 64 * g)
        for form in ("fk_prefill_attend_g", "fk_prefill_attend_f16_g") for g in (1, 2, 4)},
-    **{f"fk_prefill_attend_paged_g{g}": KernelAbi(f"fk_prefill_attend_paged_g{g}", ("qr", "kc", "vc", "position",
-                                                                                    "table", "out"),
-                                                  PrefillAttendPagedParams, 64 * g)
-       for g in (1, 2, 4)},
+    **{f"{form}{g}": KernelAbi(f"{form}{g}", ("qr", "kc", "vc", "position", "table", "out"),
+                               PrefillAttendPagedParams, 64 * g)
+       for form in ("fk_prefill_attend_paged_g", "fk_prefill_attend_paged_f16_g") for g in (1, 2, 4)},
     "fk_prefill_land": KernelAbi("fk_prefill_land", ("ks", "vs", "position", "slot", "kc", "vc"),
                                  PrefillLandParams, 256),
     "fk_prefill_argmax": KernelAbi("fk_prefill_argmax", ("x", "out"), PrefillArgmaxParams, 256),

@@ -524,7 +524,12 @@ class _Prefill:
                   "cache_bf16": int(kbf),
                   "scale": float(np.float32(spec.scale)), "staged": int(staged), "run_rows": self.run_rows}
         if paged:
-            self.launch(step, f"fk_prefill_attend_paged_g{g}", (self.rows // QBLOCK) * kvh, 64 * g,
+            # f16 pools under 4 GiB with tables of at most 256 blocks: each
+            # block's rows straight into LDS
+            pool_bytes = paging["blocks"] * kvh * paging["block_size"] * HEAD_DIM * 2
+            direct = not kbf and paging["table_len"] <= 256 and pool_bytes < 1 << 32
+            form = "fk_prefill_attend_paged_f16_g" if direct else "fk_prefill_attend_paged_g"
+            self.launch(step, f"{form}{g}", (self.rows // QBLOCK) * kvh, 64 * g,
                         {"qr": qr, "kc": kname, "vc": vname, "position": pos, "table": seq, "out": obuf},
                         dict(params, **paging))
         else:

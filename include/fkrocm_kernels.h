@@ -32,8 +32,10 @@
  *                                                      fk_prefill_attend_params
  *     (the f16 form: f16 rings and no staged rows, each key block loaded
  *     straight into LDS; ks and vs unused)
- *   fk_prefill_attend_paged_g<1|2|4> qr kc vc position table out
- *                                                      fk_prefill_attend_paged_params
+ *   fk_prefill_attend_paged_g<1|2|4>, fk_prefill_attend_paged_f16_g<1|2|4>
+ *                        qr kc vc position table out   fk_prefill_attend_paged_params
+ *     (the f16 form: f16 pools under 4 GiB, tables of at most 256 blocks,
+ *     each key block loaded straight into LDS)
  *   fk_prefill_argmax_keys keys out                    fk_prefill_argmax_keys_params
  *   (the manifest lists every entry.)
  */

@@ -295,6 +295,27 @@ def test_the_launch_check_takes_the_f16_prefill_attention_only_without_bf16_or_s
     assert {L.entry for L in low.launches if L.entry.startswith("fk_prefill_attend")} == {"fk_prefill_attend_g2"}
 
 
+def test_the_launch_check_takes_the_paged_f16_attention_only_within_its_table_and_offsets():
+    """The paged f16 form holds a block table of at most 256 entries in LDS and
+    reads the pool at 32-bit offsets: larger tables, pools of 4 GiB or more,
+    and bf16 pools are refused (the lowering gives those the other form)."""
+    from furykernel_amd.engine import params_struct
+    from furykernel_amd.prefill import lower_prefill
+    from furykernel_amd.program.check import check_program
+    from furykernel_amd.program.decoder import SMALL_PREFILL, decoder_step
+    from furykernel_amd.program.plan import PlanOptions, plan
+    c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128, paging=(64, 8)))
+    low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
+    att = next(L for L in low.launches if L.entry.startswith("fk_prefill_attend"))
+    assert att.entry == "fk_prefill_attend_paged_f16_g2"
+    _check(att, low.buffers)
+    for field, value in (("cache_bf16", 1), ("table_len", 257), ("blocks", 1 << 20)):
+        p = params_struct(att)
+        setattr(p, field, value)
+        with pytest.raises(runtime.FkError, match="bf16 caches|threadgroups"):
+            _check(att, low.buffers, params=p)
+
+
 def test_the_launch_check_refuses_prefill_attention_stores_and_lands_out_of_shape():
     """The ring prefill attention's grid is every (query block, kv head),
     its heads G to a kv head, its ring in blocks of 64 positions; the RoPE

@@ -252,7 +252,8 @@ def test_paged_pools_lower_to_the_paged_qkv_epilogue_and_attention():
     c = check_program(decoder_step(SMALL_PREFILL, name="prefill", position_bound=128, paging=(64, 8)))
     low = lower_prefill(c, plan(PlanOptions(sequence_rows=128), c), 256, run_rows=128)
     entries = [l.entry for l in low.launches]
-    assert entries.count("fk_gemm_f16_qkv_rope_paged") == entries.count("fk_prefill_attend_paged_g2") == 2
+    # f16 pools: the attention's blocks straight into LDS
+    assert entries.count("fk_gemm_f16_qkv_rope_paged") == entries.count("fk_prefill_attend_paged_f16_g2") == 2
     assert "fk_prefill_rope_store" not in entries and "fk_prefill_attend_g2" not in entries
     qkv, att = low.launches[2], low.launches[3]
     assert qkv.bind["table"] == att.bind["table"] == "ints:blocks"
