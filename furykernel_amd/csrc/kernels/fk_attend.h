@@ -78,8 +78,9 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
                                                const uint16_t *__restrict__ kst, const uint16_t *__restrict__ vst,
                                                const fk_prefill_attend_params &p,
                                                const fk_paging &pg = fk_paging{}) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][FK_ATT_KB * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][FK_ATT_KB * 64];
+  // The two buffers of K and of V: four objects (see the direct loop for why).
+  __shared__ __attribute__((aligned(16))) uint16_t ks0[FK_ATT_KB * 64], ks1[FK_ATT_KB * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t vs0[FK_ATT_KB * 64], vs1[FK_ATT_KB * 64];
   constexpr uint32_t nthreads = G * FK_WAVE;
   constexpr uint32_t per = FK_ATT_KB * 8 / nthreads;   // 16-byte units of K (and of V) a thread stages
   const uint32_t tid = threadIdx.x;
@@ -188,7 +189,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
 #pragma unroll
     for (uint32_t e = 0; e < per; e++) {
       const uint32_t u = tid + e * nthreads;
-      *reinterpret_cast<uint4 *>(&ks[buf][fk_att_kplace(u / 8, (u % 8) * 8)]) = kreg[e];
+      *reinterpret_cast<uint4 *>(&(buf ? ks1 : ks0)[fk_att_kplace(u / 8, (u % 8) * 8)]) = kreg[e];
     }
   };
   auto stash_v = [&](uint32_t buf) {
@@ -199,7 +200,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
 #pragma unroll
     for (uint32_t e = 0; e < per; e++) {
       const uint32_t u = tid + e * nthreads;
-      *reinterpret_cast<uint4 *>(&vs[buf][fk_att_vplace(u / 8, (u % 8) * 8)]) = vreg[e];
+      *reinterpret_cast<uint4 *>(&(buf ? vs1 : vs0)[fk_att_vplace(u / 8, (u % 8) * 8)]) = vreg[e];
     }
   };
 
@@ -211,7 +212,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
   // full relative precision, and O / sum does not depend on the reference.
   // A row that has seen no key yet keeps nothing: its reference and every
   // score are -inf, and with mc = 0 each exp2 is exp2(-inf) = 0.
-  auto step = [&](uint32_t kb, uint32_t buf) {
+  auto step = [&](uint32_t kb, const uint16_t *kbuf, const uint16_t *vbuf) {
     // Sᵀ = K Qᵀ: two halves of 32 keys, 4 chunks of 16 d each.  A = K: lane
     // l holds K[key 32 sb + l mod 32][16 c + 8 (l div 32) .. + 7].
     fk_float16v sc[2];
@@ -222,7 +223,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
 #pragma unroll
       for (int k4 = 0; k4 < 4; k4++) {
         fk::Half8 kf;
-        kf.u = *reinterpret_cast<const uint4 *>(&ks[buf][fk_att_kplace(32 * sb + lane % 32, 16 * k4 + 8 * (lane / 32))]);
+        kf.u = *reinterpret_cast<const uint4 *>(&kbuf[fk_att_kplace(32 * sb + lane % 32, 16 * k4 + 8 * (lane / 32))]);
         sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf.h, qf[k4].h, sc[sb], 0, 0, 0);
       }
     }
@@ -286,9 +287,9 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
       for (int q = 0; q < 4; q++) {
         const uint32_t key0 = 32 * (q / 2) + 16 * (q % 2) + tr_key;
         const fk_short4 t0 =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((FK_ATT_LDS fk_short4 *)&vs[buf][fk_att_vplace(key0, 32 * db + tr_d)]);
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((FK_ATT_LDS fk_short4 *)&vbuf[fk_att_vplace(key0, 32 * db + tr_d)]);
         const fk_short4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (FK_ATT_LDS fk_short4 *)&vs[buf][fk_att_vplace(key0 + 8, 32 * db + tr_d)]);
+            (FK_ATT_LDS fk_short4 *)&vbuf[fk_att_vplace(key0 + 8, 32 * db + tr_d)]);
         const uint2 w0 = __builtin_bit_cast(uint2, t0), w1 = __builtin_bit_cast(uint2, t1);
         fk::Half8 vf;
         vf.u = make_uint4(w0.x, w0.y, w1.x, w1.y);
@@ -319,7 +320,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
       for (uint32_t i = tid; i < used; i += nthreads) ltab[i] = min(tab[i], pg.blocks - 1);
       __syncthreads();
     }
-    auto fetch_direct = [&](uint32_t kb, uint32_t buf) {
+    auto fetch_direct = [&](uint32_t kb, uint16_t *kdst, uint16_t *vdst) {
       const uint32_t ring0 = PG ? 0u : (kb * FK_ATT_KB) % p.length;
 #pragma unroll
       for (uint32_t q = 0; q < NQ; q++) {
@@ -334,19 +335,29 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
         const uint32_t ku = slot_u ^ ((key >> 1) & 7u);         // K: unit u at place u ^ ((key >> 1) mod 8)
         const uint32_t vu = slot_u ^ (((key >> 1) & 1u) << 2);  // V: the row's halves swapped when key bit 1 is set
         const uint32_t at = (wave_s * NQ + q) * 1024;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (FK_ATT_LDS char *)&ks[buf][0] + at, 16, (row * 64 + ku * 8) * 2,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (FK_ATT_LDS char *)kdst + at, 16, (row * 64 + ku * 8) * 2,
                                                  0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (FK_ATT_LDS char *)&vs[buf][0] + at, 16, (row * 64 + vu * 8) * 2,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (FK_ATT_LDS char *)vdst + at, 16, (row * 64 + vu * 8) * 2,
                                                  0, 0, 0);
       }
     };
-    fetch_direct(kb0, 0);
+    // A block: block kb + 1's loads into one pair of buffers, then block kb
+    // multiplied from the other.  The compiler makes a read of LDS wait for
+    // every direct load into LDS that it cannot tell apart from the read, so
+    // that without the restrict-qualified buffers each block's reads waited
+    // for the next block's loads to land, and the loads' latency was paid a
+    // block; with them the loads fly during the block.
+    auto blk = [&](uint32_t kb, const uint16_t *__restrict__ kbuf, const uint16_t *__restrict__ vbuf,
+                   uint16_t *__restrict__ kdst, uint16_t *__restrict__ vdst) {
+      if (kb < kb_last) fetch_direct(kb + 1, kdst, vdst);
+      step(kb, kbuf, vbuf);
+    };
+    fetch_direct(kb0, ks0, vs0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (uint32_t kb = kb0; kb <= kb_last; kb++) {
-      const uint32_t buf = (kb - kb0) & 1;
-      if (kb < kb_last) fetch_direct(kb + 1, buf ^ 1);
-      step(kb, buf);
+      const bool odd = (kb - kb0) & 1;
+      blk(kb, odd ? ks1 : ks0, odd ? vs1 : vs0, odd ? ks0 : ks1, odd ? vs0 : vs1);
       __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of block kb + 1 landed
       __syncthreads();
     }
@@ -364,7 +375,7 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
       fetch(kreg, kc, kst, kb + 1);
       fetch(vreg, vc, vst, kb + 1);
     }
-    step(kb, buf);
+    step(kb, buf ? ks1 : ks0, buf ? vs1 : vs0);
     if (kb < kb_last) {
       stash_k(buf ^ 1);
       stash_v(buf ^ 1);
