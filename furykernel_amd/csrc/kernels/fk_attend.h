@@ -244,7 +244,13 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
 #pragma unroll
     for (int r = 1; r < 16; r++)
       mblk = __builtin_fmaxf(__builtin_fmaxf(mblk, sc[1][r]), r + 1 < 16 ? sc[0][r + 1] : sc[1][r]);
-    mblk = __builtin_fmaxf(mblk, __shfl_xor(mblk, 32)) * c;
+    // The two halves of the wavefront hold the other 32 keys of each query:
+    // v_permlane32_swap gives each lane the other half's value (an exchange
+    // in the vector ALU, where a shuffle would go through LDS).
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mblk), __float_as_uint(mblk), false, false);
+      mblk = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+    }
     const bool passed = mblk > mrun + 8.0f;
     if (__any(passed)) {
       const float mnew = passed ? mblk : mrun;
@@ -275,7 +281,10 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
         reinterpret_cast<fk_half2 *>(&pf[2 * sb + r / 8])[(r % 8) / 2] = pair;
         psum = __builtin_amdgcn_fdot2(pair, ones, psum, false);
       }
-    lrun += psum + __shfl_xor(psum, 32);
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
+      lrun += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
     // Oᵀ += Vᵀ Pᵀ, chunk by chunk.  Transposed V reads: within each 16
     // lanes, lane 4 k + q reads key K0 + k, d D0 + 4 q .. + 3 and receives
     // keys K0 .. K0 + 3 of d D0 + (its index in the 16); for chunk (sb, k2)
