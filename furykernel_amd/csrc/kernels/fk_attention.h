@@ -30,6 +30,21 @@ struct AttendLds {
   alignas(16) float pl[FK_ATTN_WAVES * FK_ATTN_MAX_GROUP];     // [run][head]: the runs' weight sums
 };
 
+// A lane's value and its partner's in the other row of its pair of rows
+// (lane l ^ 16) or in the other half of the wavefront (lane l ^ 32),
+// exchanged in the vector ALU rather than through LDS: of the two words
+// v_permlane16_swap / v_permlane32_swap return, one is the lane's own and
+// the other its partner's (which is which depends on the row), so only
+// order-free uses (a maximum, the sum of two) take them.
+__device__ __forceinline__ uint2 rows_pair(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return make_uint2(r[0], r[1]);
+}
+__device__ __forceinline__ uint2 halves_pair(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return make_uint2(r[0], r[1]);
+}
+
 // Head h's largest of the wavefronts' maxima pm[h][wave] (maximumNumber,
 // exact whatever the order), on max_key's integers so that no branch
 // separates the reads.
@@ -276,8 +291,10 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
         int k = max_key(v);
         k = max(k, dpp_i<0x124>(k));  // row_ror:4, the next position of this head
         k = max(k, dpp_i<0x128>(k));  // row_ror:8
-        k = max(k, __shfl_xor(k, 16));
-        k = max(k, __shfl_xor(k, 32));
+        uint2 o = rows_pair((uint32_t)k);
+        k = max((int)o.x, (int)o.y);
+        o = halves_pair((uint32_t)k);
+        k = max((int)o.x, (int)o.y);
         if (lane < 4 && a * 4 + lane < group) sh.pm[(a * 4 + lane) * FK_ATTN_WAVES + wave] = from_max_key(k);
       }
     }
@@ -286,8 +303,11 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
   // The weights exp(score - max), the head's maximum the largest of the
   // wavefronts': thread (r, j) makes heads j and j + 4 (zero past the
   // positions the split holds), then each run's pairwise sum over its
-  // positions by shuffles (lane 4p + j's partner at level m holds position
-  // p ^ m, same head).
+  // positions: at level m (1, 2, 4, 8) lane 4p + j adds the level's sum of
+  // position p + m (same head), by row rotations for m = 1, 2 and the row
+  // and half exchanges for m = 4, 8, so that lanes with p a multiple of 2m
+  // hold the pairwise sum of positions p .. p + 2m - 1 (the run's first
+  // lanes, which store it, hold the run's).
   {
     const uint32_t rl = split / FK_ATTN_WAVES;  // a run's positions: 16 or 8
 #pragma unroll
@@ -300,8 +320,17 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
         if (h < group && r < split) sh.wt[r * FK_ATTN_MAX_GROUP + h] = w;
         float t = w;
 #pragma unroll
-        for (uint32_t m2 = 1; m2 < FK_ATTN_MAX_SPLIT / FK_ATTN_WAVES; m2 <<= 1)
-          if (m2 < rl) t = t + __shfl_xor(t, 4 * m2);
+        for (uint32_t m2 = 1; m2 < FK_ATTN_MAX_SPLIT / FK_ATTN_WAVES; m2 <<= 1) {
+          if (m2 >= rl) continue;
+          if (m2 == 1) {
+            t = t + dpp_f<0x12C>(t);  // row_ror:12: lane l + 4 of the row, position p + 1
+          } else if (m2 == 2) {
+            t = t + dpp_f<0x128>(t);  // row_ror:8: lane l + 8 of the row, position p + 2
+          } else {
+            const uint2 o = m2 == 4 ? rows_pair(__float_as_uint(t)) : halves_pair(__float_as_uint(t));
+            t = __uint_as_float(o.x) + __uint_as_float(o.y);
+          }
+        }
         if (h < group && r < split && r % rl == 0) sh.pl[(r / rl) * FK_ATTN_MAX_GROUP + h] = t;
       }
     }
