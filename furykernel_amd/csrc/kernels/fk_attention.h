@@ -396,6 +396,221 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
   }
 }
 
+// The 1B decode's shape over a ring (groups of 4 query heads, heads of 64,
+// splits of 128 positions, f16 caches): attend_split's arithmetic in the
+// same order, with each wavefront's 16 positions (its run) kept in its
+// registers from the loads to the weighted values.  Thread (p, j) of
+// wavefront w loads quarter j of position 16 w + p's key (32 bytes) and makes
+// that position's scores; lane i loads dimension i of the run's 16 value rows
+// (one 128-byte row a load) and weighs them by the run's weights, read from
+// the lanes that made them.  Two barriers before the weighted values (the
+// queries and the new rows; the heads' maxima) and one before the runs'
+// sums, where attend_split stages keys, weights and values in LDS between
+// four.
+__device__ __forceinline__ void attend_runs(AttendLds &sh, const float *__restrict__ q,
+                                            const float *__restrict__ knew, const float *__restrict__ vnew,
+                                            uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+                                            const uint32_t *__restrict__ position,
+                                            const uint32_t *__restrict__ slot, const float *__restrict__ rope,
+                                            float *__restrict__ partials, const uint32_t *__restrict__ reach,
+                                            const fk_step_attend_params &p) {
+  constexpr uint32_t G = 4, D = 64, S = 128, HALF = D / 2, RUN = S / FK_ATTN_WAVES;
+  static_assert(RUN == 16 && FK_ATTN_WAVES * FK_WAVE == FK_ATTN_THREADS, "a wavefront's 16 positions are its run");
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (FK_WAVE - 1);
+  const uint32_t wave = tid / FK_WAVE;
+  const uint32_t g = blockIdx.x / p.splits;
+  const uint32_t t = blockIdx.x % p.splits;
+  const uint32_t pos = position[0];
+  const uint32_t sraw = slot[0];
+  const uint32_t s = sraw < p.slots ? sraw : 0;
+  const uint32_t first = (p.window && pos + 1 > p.window) ? pos + 1 - p.window : 0;
+  const uint32_t top = p.has_reach ? max(pos, reach[0]) : pos;
+  const uint32_t lo = max(first, t * S);
+  const uint32_t hi = min(top + 1, (t + 1) * S);
+  const uint32_t n = hi > lo ? hi - lo : 0;
+  const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
+  const bool stores = p.store && sraw < p.slots && lo <= pos && pos < hi;
+  const uint32_t srow = stores ? pos - lo : 0xFFFFFFFFu;  // the split's row the new key and value replace
+  const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
+  const uint32_t ring0 = lo % p.length;
+  // Ring row of split row r, a row past the split's reading its last (or
+  // row lo) and replaced by zeros.
+  auto ring_row = [&](uint32_t r) {
+    uint32_t ring = ring0 + min(r, n > 0 ? n - 1 : 0u);
+    ring = ring >= p.length ? ring - p.length : ring;
+    return base + ring;
+  };
+  const uint32_t r = tid / 4;   // this thread's position of the split (its score's)
+  const uint32_t jq = tid % 4;  // its quarter of the key, its head of the weights
+  const uint32_t u0 = wave * RUN;
+
+  // Loads, in the order their results are needed: the query rows with their
+  // RoPE partners and cosines, the new rows, the key quarter, the values.
+  float qx = 0.0f, qp = 0.0f, qc = 1.0f, qn = 0.0f;
+  if (tid < G * D) {
+    const float *head = q + (size_t)(g * G + tid / D) * D;
+    const uint32_t j = tid % D;
+    const uint32_t i = j < HALF ? j : j - HALF;
+    qx = head[j];
+    if (p.rope && i < p.rotated) {
+      qp = head[j < HALF ? j + HALF : j - HALF];
+      qc = cs[2 * i];
+      qn = cs[2 * i + 1];
+    }
+  }
+  float kx = 0.0f, kp = 0.0f, kcs = 1.0f, ksn = 0.0f, vx = 0.0f;
+  if (stores && tid < D) {
+    const float *head = knew + (size_t)g * D;
+    const uint32_t j = tid;
+    const uint32_t i = j < HALF ? j : j - HALF;
+    kx = head[j];
+    if (p.krope && i < p.rotated) {
+      kp = head[j < HALF ? j + HALF : j - HALF];
+      kcs = cs[2 * i];
+      ksn = cs[2 * i + 1];
+    }
+    vx = vnew[(size_t)g * D + j];
+  }
+  const bool live = r < n;
+  const u32x4 *krow = reinterpret_cast<const u32x4 *>(kc + ring_row(r) * D + 16 * jq);
+  u32x4 kr[2];
+  kr[0] = __builtin_nontemporal_load(krow);
+  kr[1] = __builtin_nontemporal_load(krow + 1);
+  uint16_t vr[RUN];
+#pragma unroll
+  for (uint32_t u = 0; u < RUN; u++) vr[u] = __builtin_nontemporal_load(vc + ring_row(u0 + u) * D + lane);
+
+  // The query rows RoPE'd into LDS; the new key row RoPE'd and the new value
+  // row rounded into the cache and into LDS (after the values' slots: the
+  // keys' and values' LDS is otherwise unused here).
+  uint16_t *const knew_sh = reinterpret_cast<uint16_t *>(sh.vs);
+  uint16_t *const vnew_sh = knew_sh + D;
+  if (tid < G * D) {
+    const uint32_t j = tid % D;
+    const uint32_t i = j < HALF ? j : j - HALF;
+    float v = qx;
+    if (p.rope && i < p.rotated) v = j < HALF ? qx * qc - qp * qn : qx * qc + qp * qn;
+    sh.qs[tid] = v;
+  }
+  if (stores && tid < D) {
+    const uint32_t j = tid;
+    const uint32_t i = j < HALF ? j : j - HALF;
+    float k = kx;
+    if (p.krope && i < p.rotated) k = j < HALF ? kx * kcs - kp * ksn : kx * kcs + kp * ksn;
+    const uint16_t kh = narrow_cache(k, false);
+    const uint16_t vh = narrow_cache(vx, false);
+    const size_t at = (base + pos % p.length) * D + j;
+    kc[at] = kh;
+    vc[at] = vh;
+    knew_sh[j] = kh;
+    vnew_sh[j] = vh;
+  }
+  __syncthreads();
+
+  // Scores: quarter jq of position r's key against every head's quarter,
+  // the quad's chains added by DPP ((c0 + c1) + (c2 + c3)); lane 4 p + j
+  // keeps head j's, and the wavefront's 16 positions give each head's
+  // maximum into pm[head][wave].
+  float hs;
+  {
+    uint32_t kw[8];
+    if (r == srow) {
+      const uint32_t *kn = reinterpret_cast<const uint32_t *>(knew_sh) + 8 * jq;
+#pragma unroll
+      for (int e = 0; e < 8; e++) kw[e] = kn[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        kw[e] = live ? kr[0][e] : 0u;
+        kw[4 + e] = live ? kr[1][e] : 0u;
+      }
+    }
+    float kf[16];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      kf[2 * e] = widen_cache((uint16_t)(kw[e] & 0xFFFFu), false);
+      kf[2 * e + 1] = widen_cache((uint16_t)(kw[e] >> 16), false);
+    }
+    float sc[G];
+#pragma unroll
+    for (uint32_t h = 0; h < G; h++) {
+      const float *qh = sh.qs + h * D + jq * 16;
+      float c = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) c = __builtin_fmaf(qh[i], kf[i], c);
+      c = c + dpp_f<0xB1>(c);  // quad_perm [1, 0, 3, 2]: c0 + c1, c2 + c3
+      c = c + dpp_f<0x4E>(c);  // quad_perm [2, 3, 0, 1]: (c0 + c1) + (c2 + c3)
+      sc[h] = live ? c * p.scale : -__builtin_inff();
+    }
+    hs = sc[0];
+#pragma unroll
+    for (uint32_t h = 1; h < G; h++) hs = jq == h ? sc[h] : hs;
+    int k = max_key(hs);
+    k = max(k, dpp_i<0x124>(k));  // row_ror:4
+    k = max(k, dpp_i<0x128>(k));  // row_ror:8
+    uint2 o = rows_pair((uint32_t)k);
+    k = max((int)o.x, (int)o.y);
+    o = halves_pair((uint32_t)k);
+    k = max((int)o.x, (int)o.y);
+    if (lane < G) sh.pm[lane * FK_ATTN_WAVES + wave] = from_max_key(k);
+  }
+  __syncthreads();
+
+  // The weights exp(score - max) (zero past the split's positions) and the
+  // run's pairwise sum of each head's (the tree of attend_split: lanes 0-3
+  // hold the run's sums); then lane i's weighted values of the run, every
+  // head at once, in order of position from +0, each weight read from the
+  // lane that made it.
+  const float w = live ? exp_once(hs - waves_max(sh.pm, jq)) : 0.0f;
+  float tsum = w;
+  tsum = tsum + dpp_f<0x12C>(tsum);  // row_ror:12: position p + 1
+  tsum = tsum + dpp_f<0x128>(tsum);  // row_ror:8: position p + 2
+  {
+    uint2 o = rows_pair(__float_as_uint(tsum));
+    tsum = __uint_as_float(o.x) + __uint_as_float(o.y);
+    o = halves_pair(__float_as_uint(tsum));
+    tsum = __uint_as_float(o.x) + __uint_as_float(o.y);
+  }
+  float acc[G];
+#pragma unroll
+  for (uint32_t h = 0; h < G; h++) acc[h] = 0.0f;
+#pragma unroll
+  for (uint32_t u = 0; u < RUN; u++) {
+    const uint32_t ru = u0 + u;
+    const uint16_t vh = ru == srow ? vnew_sh[lane] : (ru < n ? vr[u] : (uint16_t)0);
+    const float v = widen_cache(vh, false);
+#pragma unroll
+    for (uint32_t h = 0; h < G; h++) {
+      const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 4 * u + h));
+      acc[h] = __builtin_fmaf(wu, v, acc[h]);
+    }
+  }
+  float *pacc = reinterpret_cast<float *>(sh.ks);  // [wave][head][dim]
+#pragma unroll
+  for (uint32_t h = 0; h < G; h++) pacc[(wave * FK_ATTN_MAX_GROUP + h) * FK_ATTN_MAX_DIM + lane] = acc[h];
+  if (lane < G) sh.pl[wave * FK_ATTN_MAX_GROUP + lane] = tsum;
+  __syncthreads();
+  if (tid < G * D) {
+    const uint32_t h = tid / D;
+    const uint32_t i = tid % D;
+    float lt = 0.0f;
+    float at = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < FK_ATTN_WAVES; w2++) {
+      lt = lt + sh.pl[w2 * FK_ATTN_MAX_GROUP + h];
+      at = at + pacc[(w2 * FK_ATTN_MAX_GROUP + h) * FK_ATTN_MAX_DIM + i];
+    }
+    const size_t ht = (size_t)(g * G + h) * p.splits + t;
+    if (i == 0) {
+      float *o = partials + (size_t)p.heads * p.splits * D + 2 * ht;
+      o[0] = waves_max(sh.pm, h);
+      o[1] = lt;
+    }
+    partials[ht * D + i] = at;
+  }
+}
+
 }  // namespace fk
 
 namespace fk {
@@ -411,7 +626,7 @@ __device__ __forceinline__ void step_attend(const float *__restrict__ q, const f
   const CacheRows cr{kc, vc, nullptr, nullptr, {1u, 1u, 1u}};
   const uint32_t group = p.heads / p.kv_heads;
   if (group == 4 && p.head_dim == 64 && p.split == 128 && !p.cache_bf16)
-    attend_split<4, 64, 128, 0>(sh, q, knew, vnew, cr, position, slot, rope, partials, reach, p);
+    attend_runs(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, reach, p);
   else if (group == 4 && p.head_dim == 64 && p.split == 64 && !p.cache_bf16)
     attend_split<4, 64, 64, 0>(sh, q, knew, vnew, cr, position, slot, rope, partials, reach, p);
   else

@@ -30,6 +30,14 @@ CASES = [
     # groups of 8 (two heads a lane); position 2048: split 16 holds one
     # position, splits 17-31 none
     (16, 2, 64, 128, 4096, 2048, 0, 1, 1, 1),
+    # the 1B decode's shape (groups of 4, heads of 64, splits of 128, f16)
+    # short of full splits: the new rows mid-split, the last wavefronts'
+    # runs partly or wholly past the split's positions
+    (16, 4, 64, 128, 1024, 1000, 0, 0, 1, 1),
+    # ... a window starting mid-split, no RoPE, nothing stored
+    (8, 2, 64, 128, 512, 300, 100, 0, 0, 0),
+    # ... position 130: split 1 holds three positions, splits 2-31 none
+    (32, 8, 64, 128, 4096, 130, 0, 0, 1, 1),
 ]
 
 

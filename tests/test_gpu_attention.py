@@ -3,7 +3,8 @@ against the oracle's restatement bit for bit, over shapes the planned models
 do not reach: groups of 1 to 8 query heads a kv head (two heads a lane at 8),
 head widths 8 to 64, splits of 64 and 128 positions, f16 and bf16 caches, a
 window, the new key and value rows stored first (the key RoPE'd or not), a
-position just past a split's start, and the 1B shape with every split full.
+position just past a split's start, and the 1B shape with every split full
+and short of full.
 Compared: both caches after the store, the partials, the combined rows."""
 
 import numpy as np
