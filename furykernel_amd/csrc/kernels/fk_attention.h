@@ -396,33 +396,35 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
   }
 }
 
-// The 1B decode's shape over a ring (groups of 4 query heads, heads of 64,
-// splits of 128 positions, f16 caches): attend_split's arithmetic in the
-// same order, with each wavefront's 16 positions (its run) kept in its
-// registers from the loads to the weighted values.  Thread (p, j) of
-// wavefront w loads quarter j of position 16 w + p's key (32 bytes) and makes
-// that position's scores; lane i loads dimension i of the run's 16 value rows
-// (one 128-byte row a load) and weighs them by the run's weights, read from
-// the lanes that made them.  Two barriers before the weighted values (the
-// queries and the new rows; the heads' maxima) and one before the runs'
-// sums, where attend_split stages keys, weights and values in LDS between
-// four.
+// The 1B decode's shape (groups of 4 query heads, heads of 64, splits of 128
+// positions, f16 caches; a ring, or with PG paged pools): attend_split's arithmetic in the
+// same order, with each wavefront's 16 positions (its run) in its registers
+// from the keys' loads to the weighted values.  Thread (p, j) of wavefront w
+// loads quarter j of position 16 w + p's key (32 bytes) and makes that
+// position's scores; the values go into LDS as attend_split's do (while the
+// scores are made), and lane i weighs dimension i of the run's rows by the
+// run's weights, read from the lanes that made them.  Two barriers before the
+// weighted values (the queries and the new rows; the heads' maxima and the
+// values) and one before the runs' sums, where attend_split stages keys,
+// weights and values in LDS between four.
+template <bool PG>
 __device__ __forceinline__ void attend_runs(AttendLds &sh, const float *__restrict__ q,
                                             const float *__restrict__ knew, const float *__restrict__ vnew,
-                                            uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
-                                            const uint32_t *__restrict__ position,
+                                            const CacheRows &cr, const uint32_t *__restrict__ position,
                                             const uint32_t *__restrict__ slot, const float *__restrict__ rope,
                                             float *__restrict__ partials, const uint32_t *__restrict__ reach,
                                             const fk_step_attend_params &p) {
   constexpr uint32_t G = 4, D = 64, S = 128, HALF = D / 2, RUN = S / FK_ATTN_WAVES;
   static_assert(RUN == 16 && FK_ATTN_WAVES * FK_WAVE == FK_ATTN_THREADS, "a wavefront's 16 positions are its run");
+  uint16_t *__restrict__ kc = cr.kc;
+  uint16_t *__restrict__ vc = cr.vc;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & (FK_WAVE - 1);
   const uint32_t wave = tid / FK_WAVE;
   const uint32_t g = blockIdx.x / p.splits;
   const uint32_t t = blockIdx.x % p.splits;
   const uint32_t pos = position[0];
-  const uint32_t sraw = slot[0];
+  const uint32_t sraw = PG ? 0u : slot[0];
   const uint32_t s = sraw < p.slots ? sraw : 0;
   const uint32_t first = (p.window && pos + 1 > p.window) ? pos + 1 - p.window : 0;
   const uint32_t top = p.has_reach ? max(pos, reach[0]) : pos;
@@ -430,16 +432,25 @@ __device__ __forceinline__ void attend_runs(AttendLds &sh, const float *__restri
   const uint32_t hi = min(top + 1, (t + 1) * S);
   const uint32_t n = hi > lo ? hi - lo : 0;
   const float *cs = rope + (size_t)min(pos, p.rope_rows - 1) * 2 * p.rotated;
-  const bool stores = p.store && sraw < p.slots && lo <= pos && pos < hi;
+  // A store needs its row's slot (a ring's) or block (a pool's) to exist.
+  const bool held = PG ? (pos / cr.g.block_size < cr.g.table_len && slot[pos / cr.g.block_size] < cr.g.blocks)
+                       : sraw < p.slots;
+  const bool stores = p.store && held && lo <= pos && pos < hi;
   const uint32_t srow = stores ? pos - lo : 0xFFFFFFFFu;  // the split's row the new key and value replace
   const size_t base = ((size_t)s * p.kv_heads + g) * p.length;
-  const uint32_t ring0 = lo % p.length;
-  // Ring row of split row r, a row past the split's reading its last (or
-  // row lo) and replaced by zeros.
-  auto ring_row = [&](uint32_t r) {
-    uint32_t ring = ring0 + min(r, n > 0 ? n - 1 : 0u);
-    ring = ring >= p.length ? ring - p.length : ring;
-    return base + ring;
+  const uint32_t ring0 = PG ? 0u : lo % p.length;
+  // Split row r's key and value rows (ring index (lo + r) mod length, or
+  // position lo + r through the block table), a row past the split's
+  // reading its last (or row lo) and replaced by zeros.
+  auto row_of = [&](const uint16_t *c, const uint64_t *pool, uint32_t r) -> const uint16_t * {
+    const uint32_t rr = min(r, n > 0 ? n - 1 : 0u);
+    if constexpr (PG) {
+      return paged_row(pool, slot, cr.g, lo + rr, g, D);
+    } else {
+      uint32_t ring = ring0 + rr;
+      ring = ring >= p.length ? ring - p.length : ring;
+      return c + (base + ring) * D;
+    }
   };
   const uint32_t r = tid / 4;   // this thread's position of the split (its score's)
   const uint32_t jq = tid % 4;  // its quarter of the key, its head of the weights
@@ -473,19 +484,24 @@ __device__ __forceinline__ void attend_runs(AttendLds &sh, const float *__restri
     vx = vnew[(size_t)g * D + j];
   }
   const bool live = r < n;
-  const u32x4 *krow = reinterpret_cast<const u32x4 *>(kc + ring_row(r) * D + 16 * jq);
+  const u32x4 *krow = reinterpret_cast<const u32x4 *>(row_of(kc, cr.kpool, r) + 16 * jq);
   u32x4 kr[2];
   kr[0] = __builtin_nontemporal_load(krow);
   kr[1] = __builtin_nontemporal_load(krow + 1);
-  uint16_t vr[RUN];
+  // The values, 16 bytes a load: thread e's units e and e + 512 (row e / 8
+  // and 64 rows on, unit e mod 8).
+  u32x4 vr[2];
 #pragma unroll
-  for (uint32_t u = 0; u < RUN; u++) vr[u] = __builtin_nontemporal_load(vc + ring_row(u0 + u) * D + lane);
+  for (int m = 0; m < 2; m++) {
+    const uint32_t e = tid + m * FK_ATTN_THREADS;
+    vr[m] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row_of(vc, cr.vpool, e / 8) + 8 * (e % 8)));
+  }
 
   // The query rows RoPE'd into LDS; the new key row RoPE'd and the new value
-  // row rounded into the cache and into LDS (after the values' slots: the
-  // keys' and values' LDS is otherwise unused here).
-  uint16_t *const knew_sh = reinterpret_cast<uint16_t *>(sh.vs);
-  uint16_t *const vnew_sh = knew_sh + D;
+  // row rounded into the cache, the key into LDS (the weights' LDS, unused
+  // here) and the value into its row of the values' LDS.
+  uint16_t *const knew_sh = reinterpret_cast<uint16_t *>(sh.wt);
+  uint16_t *const vsh = reinterpret_cast<uint16_t *>(sh.vs);
   if (tid < G * D) {
     const uint32_t j = tid % D;
     const uint32_t i = j < HALF ? j : j - HALF;
@@ -500,11 +516,16 @@ __device__ __forceinline__ void attend_runs(AttendLds &sh, const float *__restri
     if (p.krope && i < p.rotated) k = j < HALF ? kx * kcs - kp * ksn : kx * kcs + kp * ksn;
     const uint16_t kh = narrow_cache(k, false);
     const uint16_t vh = narrow_cache(vx, false);
-    const size_t at = (base + pos % p.length) * D + j;
-    kc[at] = kh;
-    vc[at] = vh;
+    if constexpr (PG) {
+      paged_row(cr.kpool, slot, cr.g, pos, g, D)[j] = kh;
+      paged_row(cr.vpool, slot, cr.g, pos, g, D)[j] = vh;
+    } else {
+      const size_t at = (base + pos % p.length) * D + j;
+      kc[at] = kh;
+      vc[at] = vh;
+    }
     knew_sh[j] = kh;
-    vnew_sh[j] = vh;
+    vsh[srow * D + j] = vh;
   }
   __syncthreads();
 
@@ -555,6 +576,13 @@ __device__ __forceinline__ void attend_runs(AttendLds &sh, const float *__restri
     k = max((int)o.x, (int)o.y);
     if (lane < G) sh.pm[lane * FK_ATTN_WAVES + wave] = from_max_key(k);
   }
+  // The values into LDS (rows past the split's positions zero, the new row
+  // already in its place).
+#pragma unroll
+  for (int m = 0; m < 2; m++) {
+    const uint32_t e = tid + m * FK_ATTN_THREADS;
+    if (e / 8 != srow) sh.vs[e] = e / 8 < n ? vr[m] : u32x4{0u, 0u, 0u, 0u};
+  }
   __syncthreads();
 
   // The weights exp(score - max) (zero past the split's positions) and the
@@ -577,9 +605,7 @@ __device__ __forceinline__ void attend_runs(AttendLds &sh, const float *__restri
   for (uint32_t h = 0; h < G; h++) acc[h] = 0.0f;
 #pragma unroll
   for (uint32_t u = 0; u < RUN; u++) {
-    const uint32_t ru = u0 + u;
-    const uint16_t vh = ru == srow ? vnew_sh[lane] : (ru < n ? vr[u] : (uint16_t)0);
-    const float v = widen_cache(vh, false);
+    const float v = widen_cache(vsh[(u0 + u) * D + lane], false);
 #pragma unroll
     for (uint32_t h = 0; h < G; h++) {
       const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 4 * u + h));
@@ -626,7 +652,7 @@ __device__ __forceinline__ void step_attend(const float *__restrict__ q, const f
   const CacheRows cr{kc, vc, nullptr, nullptr, {1u, 1u, 1u}};
   const uint32_t group = p.heads / p.kv_heads;
   if (group == 4 && p.head_dim == 64 && p.split == 128 && !p.cache_bf16)
-    attend_runs(sh, q, knew, vnew, kc, vc, position, slot, rope, partials, reach, p);
+    attend_runs<false>(sh, q, knew, vnew, cr, position, slot, rope, partials, reach, p);
   else if (group == 4 && p.head_dim == 64 && p.split == 64 && !p.cache_bf16)
     attend_split<4, 64, 64, 0>(sh, q, knew, vnew, cr, position, slot, rope, partials, reach, p);
   else
@@ -647,7 +673,7 @@ __device__ __forceinline__ void step_attend_paged(const float *__restrict__ q, c
   const fk_step_attend_params &p = pp.a;
   const uint32_t group = p.heads / p.kv_heads;
   if (group == 4 && p.head_dim == 64 && p.split == 128 && !p.cache_bf16)
-    attend_split<4, 64, 128, 0, true>(sh, q, knew, vnew, cr, position, table, rope, partials, reach, p);
+    attend_runs<true>(sh, q, knew, vnew, cr, position, table, rope, partials, reach, p);
   else
     attend_split<0, 0, 0, -1, true>(sh, q, knew, vnew, cr, position, table, rope, partials, reach, p);
 }
