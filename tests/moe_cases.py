@@ -1,5 +1,5 @@
 """A routed-experts decode step (the reference's MoE half of its layer,
-test/Test/FuryKernel/ProgramTest.hs:412-485, on its own): the row normed,
+test/Test/FuryKernel/ProgramTest.hs:533-547 of `layer`, :488-557, on its own): the row normed,
 the router's logits, the k experts routed, their gate/up rows from a table,
 the gated GELU of each rank's rows, their down rows, the ranks combined by
 the route's weights and added to the row.  Seeded state, and the step's runs
