@@ -311,6 +311,82 @@ __device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, con
   }
 }
 
+// The int8 weights' full rows (k = 64 KPL 16) with x (f16) staged once a
+// threadgroup of T threads in LDS, where every wavefront would otherwise read
+// the whole 16 KB x row from memory beside its own 8 KB of weights: the x
+// loads first (T into 16-byte chunks), then the rows' weights, then the
+// chunks into LDS transposed (chunk u of lane l's pack it at (2 it + u) 64 +
+// l, so a wavefront's reads meet distinct banks) and one barrier.  The same
+// sums as gemv_wave_inflight: each product of an int8 and an f16 is exact in
+// binary32, so a pair's sum p0 + p1 is one fused multiply-add of the second
+// product onto the first (one rounding either way), the chain of four
+// (p0 + p1) + (p2 + p3).  Every wavefront reaches the barrier: rows past n
+// read row n - 1 and store nothing.
+template <int T, int R, int KPL>
+__device__ __forceinline__ void gemv_i8_xlds(const int8_t *__restrict__ w, const _Float16 *__restrict__ x,
+                                             const float *__restrict__ scale, float *__restrict__ y, uint32_t n,
+                                             uint32_t row0) {
+  constexpr int P = 16, C = 4;
+  constexpr uint32_t K = 64 * KPL * P;
+  constexpr uint32_t CH = K * 2 / 16;  // x's 16-byte chunks
+  constexpr int PER = CH / T;
+  static_assert(CH % T == 0, "x's chunks divide among the threads");
+  __shared__ uint4 xs[CH];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (FK_WAVE - 1);
+  uint4 xc[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) xc[i] = reinterpret_cast<const uint4 *>(x)[tid + i * T];
+  uint4 wv[R][KPL];
+#pragma unroll
+  for (int q = 0; q < R; q++) {
+    const int8_t *wr = w + (size_t)min(row0 + q, n - 1) * K;
+#pragma unroll
+    for (int it = 0; it < KPL; it++) wv[q][it] = load16<true>(wr + (size_t)(lane + FK_WAVE * it) * P);
+  }
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const uint32_t j = tid + i * T, pack = j / 2;
+    xs[((pack / FK_WAVE) * 2 + j % 2) * FK_WAVE + pack % FK_WAVE] = xc[i];
+  }
+  __syncthreads();
+  float acc[R][C];
+#pragma unroll
+  for (int q = 0; q < R; q++)
+#pragma unroll
+    for (int c = 0; c < C; c++) acc[q][c] = 0.0f;
+#pragma unroll
+  for (int it = 0; it < KPL; it++) {
+    const uint4 xu[2] = {xs[(2 * it) * FK_WAVE + lane], xs[(2 * it + 1) * FK_WAVE + lane]};
+    float xf[P];
+    unpack<P>(xu, xf, _Float16{});
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      float wf[P];
+      unpack_w<P>(wv[q][it], wf, int8_t{});
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const float s01 = __builtin_fmaf(xf[4 * c + 1], wf[4 * c + 1], xf[4 * c] * wf[4 * c]);
+        const float s23 = __builtin_fmaf(xf[4 * c + 3], wf[4 * c + 3], xf[4 * c + 2] * wf[4 * c + 2]);
+        acc[q][c] = acc[q][c] + (s01 + s23);
+      }
+    }
+  }
+  float t[R];
+#pragma unroll
+  for (int q = 0; q < R; q++) {
+    t[q] = acc[q][0];
+#pragma unroll
+    for (int c = 1; c < C; c++) t[q] = t[q] + acc[q][c];
+  }
+  wave_sums<R>(t);
+#pragma unroll
+  for (int q = 0; q < R; q++) {
+    const uint32_t row = row0 + q;
+    if (lane == 0 && row < n) y[row] = scale ? t[q] * scale[row] : t[q];
+  }
+}
+
 }  // namespace fk
 
 // Entry points: a threadgroup of W wavefronts takes W * R consecutive rows;
@@ -330,18 +406,21 @@ __device__ __forceinline__ void gemv_wave_inflight(const WT *__restrict__ w, con
       fk::gemv_wave<WT, XT, P, R>(w, x, nullptr, y, p.n, p.k, row0);                                         \
   }
 
+// The int8 entries: full rows of 64 KPL packs in threadgroups of 256 with x
+// staged in LDS (gemv_i8_xlds); other widths and threadgroups by the loop
+// form (which keeps the kernel's registers to what the staged form needs,
+// so that as many wavefronts as its LDS allows are resident).
 #define FK_GEMV_SCALED_ENTRY(NAME, WT, XT, P, R, KPL)                                                      \
   extern "C" __global__ void __launch_bounds__(256)                                                        \
       NAME(const WT *__restrict__ w, const float *__restrict__ scale, const XT *__restrict__ x,            \
            float *__restrict__ y, fk_gemv_params p) {                                                      \
     const uint32_t row0 = (blockIdx.x * (blockDim.x / FK_WAVE) + threadIdx.x / FK_WAVE) * (R);           \
+    if (p.k / (P) == FK_WAVE * (KPL) && blockDim.x == 256) {                                               \
+      fk::gemv_i8_xlds<256, R, KPL>(w, x, scale, y, p.n, row0);                                            \
+      return;                                                                                              \
+    }                                                                                                      \
     if (row0 >= p.n) return;                                                                               \
-    if (p.k / (P) == FK_WAVE * (KPL))                                                                      \
-      fk::gemv_wave_inflight<WT, XT, P, R, KPL, true>(w, x, scale, y, p.n, p.k, row0);                    \
-    else if (p.k / (P) < FK_WAVE * (KPL))                                                                  \
-      fk::gemv_wave_inflight<WT, XT, P, R, KPL, false>(w, x, scale, y, p.n, p.k, row0);                   \
-    else                                                                                                   \
-      fk::gemv_wave<WT, XT, P, R>(w, x, scale, y, p.n, p.k, row0);                                         \
+    fk::gemv_wave<WT, XT, P, R>(w, x, scale, y, p.n, p.k, row0);                                           \
   }
 
 // Rows whose width is a multiple of 4 but not of a 16-byte pack (the small
