@@ -101,6 +101,32 @@ def test_gemv_i8_edge_values_bit_exact(device, kernels, r, k):
     assert np.array_equal(bits(got), bits(fkref.gemv(w, x, 64, 16, 1, row_scale=s)))
 
 
+@pytest.mark.parametrize("n,r,threads", [(37, 1, 256), (9, 2, 256), (5, 1, 128), (70, 2, 64)])
+def test_gemv_i8_ragged_rows_full_width(device, kernels, n, r, threads):
+    """Full rows of 8192 with fewer rows than the last threadgroup holds: in
+    256-thread groups x goes through LDS and every wavefront reaches its
+    barrier (rows past n read row n - 1 and store nothing); smaller groups
+    take the loop form.  Bit for bit against the oracle, and y past n left
+    as it was."""
+    k = 8192
+    rng = np.random.default_rng(n * 10 + r)
+    w = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    x = rng.normal(0, 1, k).astype(np.float16)
+    s = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    rows_per_group = threads // 64 * r
+    pad = -(-n // rows_per_group) * rows_per_group
+    bw, bx, bs = device.upload(w), device.upload(x), device.upload(s)
+    by = device.upload(np.full(pad, 7.0, np.float32))
+    print(f"gemv i8 {n}x{k} r{r} {threads} threads", flush=True)
+    kernels.gemv(bw, bx, by, n, k, wtype="i8", rows_per_wave=r, threads=threads, scale=bs)
+    device.sync()
+    out = by.read(np.float32, pad)
+    for b in (bw, bx, by, bs):
+        b.free()
+    assert np.array_equal(bits(out[:n]), bits(fkref.gemv(w, x, 64, 16, 1, row_scale=s)))
+    assert np.all(out[n:] == 7.0)
+
+
 def test_gemv_i8_integer_closed_form(device, kernels):
     n, k = 256, 8192
     w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
