@@ -397,8 +397,8 @@ __device__ __forceinline__ void attend_split(AttendLds &sh, const float *__restr
 }
 
 // The 1B decode's shape (groups of 4 query heads, heads of 64, splits of 128
-// positions, f16 caches; a ring, or with PG paged pools): attend_split's arithmetic in the
-// same order, with each wavefront's 16 positions (its run) in its registers
+// positions, f16 caches; a ring, or with PG paged pools): attend_split's
+// arithmetic in the same order, with each wavefront's 16 positions (its run) in its registers
 // from the keys' loads to the weighted values.  Thread (p, j) of wavefront w
 // loads quarter j of position 16 w + p's key (32 bytes) and makes that
 // position's scores; the values go into LDS as attend_split's do (while the
