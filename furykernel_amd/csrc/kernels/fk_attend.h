@@ -329,8 +329,30 @@ __device__ __forceinline__ void prefill_attend(const uint16_t *__restrict__ qr, 
       for (uint32_t i = tid; i < used; i += nthreads) ltab[i] = min(tab[i], pg.blocks - 1);
       __syncthreads();
     }
+    // A ring block whose keys all come before the block's last query reads
+    // rows ring0 .. ring0 + 63 as they lie: each load's lane part of the
+    // address (the key's row and unit) is the same every block and the
+    // block's part a scalar offset, so such blocks spend no vector
+    // operations on addresses.
+    uint32_t kvo[NQ], vvo[NQ];
+#pragma unroll
+    for (uint32_t q = 0; q < NQ; q++) {
+      const uint32_t key = (wave * NQ + q) * 8 + lane / 8, slot_u = lane % 8;
+      kvo[q] = key * 128 + (slot_u ^ ((key >> 1) & 7u)) * 16;
+      vvo[q] = key * 128 + (slot_u ^ (((key >> 1) & 1u) << 2)) * 16;
+    }
     auto fetch_direct = [&](uint32_t kb, uint16_t *kdst, uint16_t *vdst) {
       const uint32_t ring0 = PG ? 0u : (kb * FK_ATT_KB) % p.length;
+      if (!PG && kb * FK_ATT_KB + FK_ATT_KB - 1 <= last_pos) {
+        const uint32_t so = ring0 * 128;
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; q++) {
+          const uint32_t at = (wave_s * NQ + q) * 1024;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (FK_ATT_LDS char *)kdst + at, 16, kvo[q], so, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (FK_ATT_LDS char *)vdst + at, 16, vvo[q], so, 0, 0);
+        }
+        return;
+      }
 #pragma unroll
       for (uint32_t q = 0; q < NQ; q++) {
         const uint32_t key = (wave * NQ + q) * 8 + lane / 8, slot_u = lane % 8;
